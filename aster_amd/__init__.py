@@ -1,0 +1,17 @@
+"""aster_amd -- MI355X-native (gfx950) INT8 paged-KV decode hot path.
+
+The path of sutiankang/aster that this package replaces: quantize-and-append of
+new K/V tokens into an INT8 paged cache and ragged paged attention over it,
+behind the reference's names (KVQuantization, QuantizedKV, quantize_kv,
+KernelWork, UnsupportedAttentionBackend) and a C-ABI library of hand-written
+HIP kernels (include/aster_kv.h).
+"""
+
+from .attention_backend import BACKEND, AttentionWork, KernelWork, UnsupportedAttentionBackend
+from .kv_quantization import KVQuantization, QuantizedKV, quantize_kv
+from .paged_kv import DEFAULT_PARTITION_TOKENS, PagedKVCache
+
+__all__ = [
+    "BACKEND", "AttentionWork", "KernelWork", "UnsupportedAttentionBackend",
+    "KVQuantization", "QuantizedKV", "quantize_kv", "DEFAULT_PARTITION_TOKENS", "PagedKVCache",
+]

@@ -1,0 +1,150 @@
+// Fused quantize-and-append of new K/V token rows into the paged INT8 arena.
+//
+// Arithmetic follows quantize_kv (src/aster/optimization/kv_quantization.py:82-94)
+// bit for bit: fp32 source, amax over the row, scale = amax==0 ? 1 :
+// max(amax/127, FLT_MIN) with an IEEE-correct division, codes =
+// rint(clamp(x/scale, -127, 127)) again with IEEE division (never x*(1/scale)),
+// round-half-to-even via v_rndne. The library is built with
+// -fhip-fp32-correctly-rounded-divide-sqrt and without denormal flushing.
+//
+// Two launches per call: a finiteness scan that sets ASTR_FLAG_NONFINITE_INPUT,
+// then the quantize/scatter kernel that does nothing when that bit is set, so a
+// bad suffix mutates no slot (kv_quantization.py:77-81, state.py:292 runs the
+// check before any copy).
+#include <cfloat>
+
+#include "common.h"
+
+namespace astr {
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // one wave per (token, head, K|V) row
+constexpr int kMaxPerLane = 8;    // head_dim <= 512
+
+struct AppendArgs {
+  const void* key;
+  const void* value;
+  int64_t key_token_stride, key_head_stride, value_token_stride, value_head_stride;
+  int64_t num_tokens;
+  const int64_t* slot_mapping;
+  astr_paged_kv cache;
+  int32_t* err_flag;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void finite_scan_kernel(AppendArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t rows = a.num_tokens * a.cache.num_kv_heads;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= (a.value ? 2 : 1) * rows) return;
+  const bool is_v = row >= rows;
+  const int64_t r = is_v ? row - rows : row;
+  const int64_t t = r / a.cache.num_kv_heads, h = r % a.cache.num_kv_heads;
+  const T* src = static_cast<const T*>(is_v ? a.value : a.key) +
+                 t * (is_v ? a.value_token_stride : a.key_token_stride) +
+                 h * (is_v ? a.value_head_stride : a.key_head_stride);
+  bool bad = false;
+  for (int d = lane; d < a.cache.head_dim; d += kWave) {
+    const float x = to_float<T>(src[d]);
+    bad |= !__builtin_isfinite(x);
+  }
+  if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_INPUT);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void quantize_append_kernel(AppendArgs a) {
+  // All-or-nothing: the finite scan of this call (or an unacknowledged earlier
+  // one) flagged the input, so leave every slot untouched.
+  if (__atomic_load_n(a.err_flag, __ATOMIC_RELAXED) & ASTR_FLAG_NONFINITE_INPUT) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t rows = a.num_tokens * a.cache.num_kv_heads;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= (a.value ? 2 : 1) * rows) return;
+  const bool is_v = row >= rows;
+  const int64_t r = is_v ? row - rows : row;
+  const int64_t t = r / a.cache.num_kv_heads, h = r % a.cache.num_kv_heads;
+  const int64_t slot = a.slot_mapping[t];
+  if (slot < 0) return;  // padding token: no slot
+  const int64_t block = slot / a.cache.block_size, offset = slot % a.cache.block_size;
+  if (block >= a.cache.num_blocks) {
+    if (lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+    return;
+  }
+  const int D = a.cache.head_dim;
+  const T* src = static_cast<const T*>(is_v ? a.value : a.key) +
+                 t * (is_v ? a.value_token_stride : a.key_token_stride) +
+                 h * (is_v ? a.value_head_stride : a.key_head_stride);
+  float x[kMaxPerLane];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxPerLane; ++i) {
+    const int d = lane + i * kWave;
+    x[i] = d < D ? to_float<T>(src[d]) : 0.f;
+    amax = fmaxf(amax, fabsf(x[i]));
+  }
+  amax = wave_max(amax);
+  // kv_quantization.py:86-90 -- true division, then the FLT_MIN clamp.
+  const float scale = amax == 0.f ? 1.f : fmaxf(amax / 127.f, FLT_MIN);
+  int8_t* codes = (is_v ? a.cache.v_codes : a.cache.k_codes) + block * a.cache.code_block_stride +
+                  h * a.cache.code_head_stride + offset * D;
+#pragma unroll
+  for (int i = 0; i < kMaxPerLane; ++i) {
+    const int d = lane + i * kWave;
+    if (d < D) {
+      // kv_quantization.py:91-93 -- divide, clamp, round half to even.
+      const float n = fminf(fmaxf(x[i] / scale, -127.f), 127.f);
+      codes[d] = (int8_t)__builtin_rintf(n);
+    }
+  }
+  if (lane == 0) {
+    float* scales = (is_v ? a.cache.v_scales : a.cache.k_scales) +
+                    block * a.cache.scale_block_stride + h * a.cache.scale_head_stride + offset;
+    *scales = scale;
+  }
+}
+
+template <typename T>
+int launch_append(const AppendArgs& a, hipStream_t stream) {
+  const int64_t rows = (a.value ? 2 : 1) * a.num_tokens * a.cache.num_kv_heads;
+  const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  if (blocks > INT32_MAX) return fail(ASTR_EINVAL, "too many rows for one append launch");
+  hipLaunchKernelGGL(finite_scan_kernel<T>, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(quantize_append_kernel<T>, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "quantize_append launch");
+}
+
+}  // namespace
+}  // namespace astr
+
+extern "C" int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void* key,
+                                          const void* value, int32_t in_dtype, int64_t num_tokens,
+                                          int64_t key_token_stride, int64_t key_head_stride,
+                                          int64_t value_token_stride, int64_t value_head_stride,
+                                          const int64_t* slot_mapping, int32_t* err_flag,
+                                          void* stream) {
+  using namespace astr;
+  if (cache == nullptr || err_flag == nullptr)
+    return fail(ASTR_EINVAL, "cache descriptor and err_flag are required");
+  if (num_tokens < 0) return fail(ASTR_EINVAL, "num_tokens must be >= 0");
+  if (num_tokens == 0) return 0;
+  if (key == nullptr || slot_mapping == nullptr)
+    return fail(ASTR_EINVAL, "key and slot_mapping are required");
+  if (cache->k_codes == nullptr || cache->k_scales == nullptr ||
+      (value != nullptr && (cache->v_codes == nullptr || cache->v_scales == nullptr)))
+    return fail(ASTR_EINVAL, "cache code/scale pointers are required");
+  if (cache->head_dim < 1 || cache->head_dim > kWave * kMaxPerLane)
+    return fail(ASTR_EUNSUPPORTED, "head_dim %d outside 1..%d", cache->head_dim,
+                kWave * kMaxPerLane);
+  if (cache->num_kv_heads < 1 || cache->block_size < 1 || cache->num_blocks < 1)
+    return fail(ASTR_EINVAL, "cache sizes must be positive");
+  AppendArgs a{key, value, key_token_stride, key_head_stride, value_token_stride,
+               value_head_stride, num_tokens, slot_mapping, *cache, err_flag};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (in_dtype) {
+    case ASTR_F32: return launch_append<float>(a, s);
+    case ASTR_F16: return launch_append<_Float16>(a, s);
+    case ASTR_BF16: return launch_append<bf16_t>(a, s);
+    default: return fail(ASTR_EUNSUPPORTED, "input dtype %d is not f32/f16/bf16", in_dtype);
+  }
+}

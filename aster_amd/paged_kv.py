@@ -1,0 +1,206 @@
+"""Device arena of the paged INT8 KV cache and the two hot-path calls on it.
+
+Arena layout (one allocation per model, block-major so a physical page of all
+layers is contiguous for copy-on-write and host swap):
+
+    codes  int8  [num_blocks, num_layers, 2 (K, V), num_kv_heads, block_size, head_dim]
+    scales fp32  [num_blocks, num_layers, 2 (K, V), num_kv_heads, block_size]
+
+Block ``b`` is the reference's ``PageRef.index`` (src/aster/inference/state.py:131-134):
+the reference keeps per page and layer a ``QuantizedKV`` of codes ``[1, Hkv, bs, D]``
+and scales ``[1, Hkv, bs, 1]`` (state.py:319-327, kv_quantization.py:97-110);
+here those are ``codes[b, layer, 0|1]`` / ``scales[b, layer, 0|1]`` of one arena.
+
+``append`` replaces quantize_kv + the per-token copy_kv loop of
+``PagedStatePool._append_leaves`` (state.py:292, 339-344): token ``t`` goes to
+slot ``slot_mapping[t] = page * block_size + offset``. ``paged_attention``
+replaces the per-row ``online_attention`` calls of
+``PagedAttentionRunner.forward_batch`` (src/aster/inference/paged_attention.py:168-215)
+with one launch over all rows.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _native
+from .attention_backend import BACKEND, KernelWork, UnsupportedAttentionBackend
+from .kv_quantization import KVQuantization, QuantizedKV, _DTYPE_CODES, require_int8
+
+DEFAULT_PARTITION_TOKENS = 512
+
+
+class PagedKVCache:
+    """Caller-owned device arena for ``num_layers`` layers of INT8 paged K/V."""
+
+    def __init__(self, *, num_blocks, num_layers, num_kv_heads, head_dim, block_size=16,
+                 device="cuda", quantization=None):
+        quantization = KVQuantization("int8") if quantization is None else quantization
+        require_int8(quantization)
+        if min(num_blocks, num_layers, num_kv_heads, head_dim, block_size) < 1:
+            raise ValueError("Cache capacities must be positive")
+        if block_size != 16:
+            raise UnsupportedAttentionBackend("hip_int8_paged kernels use 16-token blocks")
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise UnsupportedAttentionBackend("hip_int8_paged arenas live in HIP device memory")
+        self.quantization = quantization
+        self.num_blocks, self.num_layers = num_blocks, num_layers
+        self.num_kv_heads, self.head_dim, self.block_size = num_kv_heads, head_dim, block_size
+        self.device = device
+        self.codes = torch.zeros((num_blocks, num_layers, 2, num_kv_heads, block_size, head_dim),
+                                 dtype=torch.int8, device=device)
+        self.scales = torch.ones((num_blocks, num_layers, 2, num_kv_heads, block_size),
+                                 dtype=torch.float32, device=device)
+        self.err_flag = torch.zeros(1, dtype=torch.int32, device=device)
+        self._descs = [self._make_desc(layer) for layer in range(num_layers)]
+
+    # ---- descriptors --------------------------------------------------------
+    def _make_desc(self, layer):
+        c, s = self.codes, self.scales
+        return _native.PagedKVDesc(
+            k_codes=c[0, layer, 0].data_ptr(), v_codes=c[0, layer, 1].data_ptr(),
+            k_scales=s[0, layer, 0].data_ptr(), v_scales=s[0, layer, 1].data_ptr(),
+            code_block_stride=c.stride(0), code_head_stride=c.stride(3),
+            scale_block_stride=s.stride(0), scale_head_stride=s.stride(3),
+            num_blocks=self.num_blocks, block_size=self.block_size,
+            num_kv_heads=self.num_kv_heads, head_dim=self.head_dim)
+
+    def layer_desc(self, layer):
+        return self._descs[layer]
+
+    @property
+    def nbytes(self):
+        return self.codes.numel() + self.scales.numel() * 4
+
+    def page(self, block, layer):
+        """Zero-copy ``QuantizedKV`` views ``[1, Hkv, bs, D]`` of one page
+        (the reference's ``PageView.payload[2*layer : 2*layer+2]``, state.py:158-163)."""
+        k = QuantizedKV(self.codes[block, layer, 0][None], self.scales[block, layer, 0][None, ..., None],
+                        torch.float32)
+        v = QuantizedKV(self.codes[block, layer, 1][None], self.scales[block, layer, 1][None, ..., None],
+                        torch.float32)
+        return k, v
+
+    # ---- error flag ---------------------------------------------------------
+    def pending_errors(self):
+        """Read (synchronising) and clear the sticky device error flag."""
+        flags = int(self.err_flag.item())
+        if flags:
+            self.err_flag.zero_()
+        return flags
+
+    def raise_errors(self):
+        """Raise the reference's ValueError for any flagged device error."""
+        flags = self.pending_errors()
+        if flags & _native.FLAG_NONFINITE_INPUT:
+            raise ValueError("Quantized KV requires finite floating input")
+        if flags & _native.FLAG_NONFINITE_SCORE:
+            raise ValueError(
+                "Attention score overflow; cannot repair an infinite dot product with softmax")
+        if flags & _native.FLAG_BAD_INDEX:
+            raise ValueError("Slot, block table or context length outside the KV arena")
+
+    # ---- hot path -----------------------------------------------------------
+    def append(self, layer, key, value, slot_mapping, *, check=False):
+        """Quantize ``key``/``value`` ``[T, Hkv, D]`` (fp32/fp16/bf16, device) into
+        the slots ``slot_mapping`` (int64 ``[T]``; negative = skip). With
+        ``check=True`` synchronise and raise ``ValueError`` on non-finite input, as
+        quantize_kv does (kv_quantization.py:77-81); otherwise the error stays in
+        the sticky flag (and blocks further appends) until ``raise_errors``."""
+        _check_rows(key, "key", self.num_kv_heads, self.head_dim, self.device)
+        _check_rows(value, "value", self.num_kv_heads, self.head_dim, self.device)
+        if key.shape != value.shape or key.dtype != value.dtype:
+            raise ValueError("key and value must share shape and dtype")
+        if (slot_mapping.dtype != torch.int64 or slot_mapping.shape != (key.shape[0],)
+                or slot_mapping.device != self.device or not slot_mapping.is_contiguous()):
+            raise ValueError("slot_mapping must be a contiguous int64 device vector [T]")
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _native.check(
+            _native.lib().astr_kv_quantize_append_i8(
+                self._descs[layer], key.data_ptr(), value.data_ptr(), _DTYPE_CODES[key.dtype],
+                key.shape[0], key.stride(0), key.stride(1), value.stride(0), value.stride(1),
+                slot_mapping.data_ptr(), self.err_flag.data_ptr(), stream),
+            "quantize_append")
+        if check:
+            self.raise_errors()
+
+    def workspace_bytes(self, num_seqs, num_q_heads, max_context_len,
+                        partition_tokens=DEFAULT_PARTITION_TOKENS):
+        return int(_native.lib().astr_paged_attention_i8_workspace_bytes(
+            num_seqs, num_q_heads, self.head_dim, max_context_len, partition_tokens))
+
+    def paged_attention(self, layer, query, block_tables, context_lens, *, max_context_len,
+                        scale=None, window=None, partition_tokens=DEFAULT_PARTITION_TOKENS,
+                        out=None, workspace=None, work=None, check=False):
+        """Decode attention of one query token per sequence over this layer.
+
+        ``query`` ``[S, Hq, D]`` fp32/fp16/bf16; ``block_tables`` int32 ``[S, max_blocks]``;
+        ``context_lens`` int32 ``[S]`` (committed length including the new token,
+        which sits at position ``ctx - 1``); ``max_context_len`` host upper bound of
+        ``context_lens``. ``scale`` defaults to ``head_dim ** -0.5``
+        (nn/attention.py:130); ``window`` keeps keys ``pos > ctx - 1 - window``
+        (online_attention.py:183-184). Returns ``[S, Hq, D]`` in the query dtype
+        (online_attention.py:219)."""
+        if query.ndim != 3 or query.shape[-1] != self.head_dim or query.device != self.device:
+            raise ValueError("query must be [num_seqs, num_q_heads, head_dim] on the cache device")
+        if query.dtype not in _DTYPE_CODES:
+            raise UnsupportedAttentionBackend(f"query dtype {query.dtype} is not fp32/fp16/bf16")
+        if query.stride(-1) != 1:
+            raise ValueError("query rows must be contiguous")
+        num_seqs, num_q_heads = query.shape[0], query.shape[1]
+        if num_q_heads % self.num_kv_heads:
+            raise ValueError("Query heads must divide into KV groups")
+        _check_index(block_tables, "block_tables", 2, self.device)
+        _check_index(context_lens, "context_lens", 1, self.device)
+        if block_tables.shape[0] != num_seqs or context_lens.shape[0] != num_seqs:
+            raise ValueError("block_tables/context_lens must have one row per sequence")
+        if max_context_len > block_tables.shape[1] * self.block_size:
+            raise ValueError("max_context_len exceeds the block table capacity")
+        scale = self.head_dim ** -0.5 if scale is None else float(scale)
+        if not math.isfinite(scale) or scale <= 0:
+            raise ValueError("Attention scale must be finite and positive")
+        if window is not None and (type(window) is not int or window < 1):
+            raise ValueError("Invalid causal/window semantics")
+        if out is None:
+            out = torch.empty_like(query)
+        need = self.workspace_bytes(num_seqs, num_q_heads, max_context_len, partition_tokens)
+        if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+            workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _native.check(
+            _native.lib().astr_paged_attention_i8(
+                self._descs[layer], query.data_ptr(), _DTYPE_CODES[query.dtype], query.stride(0),
+                query.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
+                block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(),
+                num_seqs, num_q_heads, max_context_len, scale, window or 0, partition_tokens,
+                workspace.data_ptr() if need else None, need, self.err_flag.data_ptr(), stream),
+            "paged_attention")
+        if work is not None:
+            work.backend, work.fallback_reason = BACKEND, None
+            work.page_launches += 2 if need else 1
+            work.query_tiles += 1
+            work.max_query_tile = max(work.max_query_tile, 1)
+            work.max_key_tile = max(work.max_key_tile, self.block_size)
+            work.compiler_version = _native.lib().astr_version().decode()
+        if check:
+            self.raise_errors()
+        return out
+
+
+def _check_rows(tensor, name, heads, width, device):
+    if (not isinstance(tensor, torch.Tensor) or tensor.ndim != 3 or tensor.shape[1] != heads
+            or tensor.shape[2] != width or tensor.device != device or tensor.stride(-1) != 1):
+        raise ValueError(f"{name} must be a [T, num_kv_heads, head_dim] device tensor with "
+                         "contiguous rows")
+    if tensor.dtype not in _DTYPE_CODES:
+        raise ValueError("Quantized KV requires finite floating input")
+
+
+def _check_index(tensor, name, ndim, device):
+    if (not isinstance(tensor, torch.Tensor) or tensor.dtype != torch.int32 or tensor.ndim != ndim
+            or tensor.device != device or tensor.stride(-1) != 1):
+        raise ValueError(f"{name} must be an int32 device tensor of rank {ndim} with "
+                         "contiguous rows")

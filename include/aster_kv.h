@@ -1,0 +1,141 @@
+/*
+ * aster_kv.h -- C ABI of the MI355X (gfx950) INT8 paged-KV decode path.
+ *
+ * Plain pointers and sizes only: every pointer except `cache` and the
+ * `astr_*_workspace_bytes` arguments is a DEVICE pointer owned by the caller
+ * (the torch allocator in the Python host layer); the library never allocates
+ * or frees device memory. `stream` is a hipStream_t passed as void*; work is
+ * stream-ordered and the calls return without synchronising.
+ *
+ * Return codes (all entry points):
+ *    0  success (launched)
+ *   -1  ASTR_EINVAL       invalid argument (Python raises ValueError)
+ *   -2  ASTR_EUNSUPPORTED configuration this build has no kernel for
+ *                         (Python raises UnsupportedAttentionBackend)
+ *   >0  hipError_t from the launch
+ * astr_last_error() returns a thread-local message for the last failure.
+ *
+ * Device error flag (int32, caller-zeroed, sticky until the caller clears it):
+ *   bit 0 ASTR_FLAG_NONFINITE_INPUT  a K/V input value was NaN/Inf: the
+ *                                    append wrote NO slot (all-or-nothing)
+ *   bit 1 ASTR_FLAG_NONFINITE_SCORE  an attention score was NaN/Inf
+ *   bit 2 ASTR_FLAG_BAD_INDEX        a slot / block-table entry / context
+ *                                    length pointed outside the arena or
+ *                                    the block table (the access was skipped)
+ */
+#ifndef ASTER_KV_H
+#define ASTER_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ASTR_EINVAL (-1)
+#define ASTR_EUNSUPPORTED (-2)
+
+#define ASTR_FLAG_NONFINITE_INPUT 1
+#define ASTR_FLAG_NONFINITE_SCORE 2
+#define ASTR_FLAG_BAD_INDEX 4
+
+/* Element types of queries, outputs and K/V inputs. */
+enum astr_dtype { ASTR_F32 = 0, ASTR_F16 = 1, ASTR_BF16 = 2 };
+
+/*
+ * One layer of the paged INT8 KV arena (device memory, caller-owned).
+ * Codes: a block holds num_kv_heads x block_size token rows of head_dim int8
+ * codes; a token row is contiguous (token stride = head_dim bytes).
+ * Scales: one fp32 per (block, head, token); token stride = 1 float.
+ * Physical block b, kv head h, token slot s lives at
+ *   k_codes + b*code_block_stride + h*code_head_stride + s*head_dim
+ *   k_scales + b*scale_block_stride + h*scale_head_stride + s
+ * (same for v_*). This is the reference's per-page [1,Hkv,bs,D] codes and
+ * [1,Hkv,bs,1] scales (kv_quantization.py:97-110, state.py:319-327) stacked
+ * into one arena indexed by PageRef.index.
+ */
+typedef struct astr_paged_kv {
+  int8_t* k_codes;
+  int8_t* v_codes;
+  float* k_scales;
+  float* v_scales;
+  int64_t code_block_stride;  /* bytes  */
+  int64_t code_head_stride;   /* bytes  */
+  int64_t scale_block_stride; /* floats */
+  int64_t scale_head_stride;  /* floats */
+  int32_t num_blocks;
+  int32_t block_size;   /* must be 16 */
+  int32_t num_kv_heads;
+  int32_t head_dim;     /* 64, 128 or 256 for attention; any 1..512 for append */
+} astr_paged_kv;
+
+/*
+ * Quantize new K and V token rows to INT8 + fp32 per-(token, head) scales and
+ * write them into their cache slots.
+ * Replaces quantize_kv (src/aster/optimization/kv_quantization.py:71-94) as
+ * called from PagedStatePool._append_leaves (src/aster/inference/state.py:292)
+ * plus its per-token raw copy_kv into page slot divmod(offset, block_size)
+ * (state.py:339-344, kv_quantization.py:113-127).
+ *   key/value: [num_tokens, num_kv_heads, head_dim] elements of `in_dtype`,
+ *              strides in elements (last dim contiguous). value may be NULL
+ *              to quantize key rows only (into k_codes/k_scales).
+ *   slot_mapping: int64 [num_tokens], slot = block*block_size + offset;
+ *              slot < 0 skips the token (padding).
+ * Bit-exact with the reference: scale = amax==0 ? 1 : max(amax/127, FLT_MIN),
+ * code = rint(clamp(x/scale, -127, 127)) with IEEE fp32 division.
+ * All-or-nothing: a NaN/Inf anywhere in key/value sets
+ * ASTR_FLAG_NONFINITE_INPUT and no slot is written (kv_quantization.py:77-81).
+ * A set input-flag bit also suppresses later appends until cleared.
+ */
+int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void* key, const void* value,
+                               int32_t in_dtype, int64_t num_tokens, int64_t key_token_stride,
+                               int64_t key_head_stride, int64_t value_token_stride,
+                               int64_t value_head_stride, const int64_t* slot_mapping,
+                               int32_t* err_flag, void* stream);
+
+/*
+ * Ragged paged attention over the INT8 arena, one query token per sequence
+ * (decode). Replaces the per-row online_attention call of
+ * PagedAttentionRunner.forward_batch (src/aster/inference/paged_attention.py:168-215),
+ * i.e. online_attention_statistics (src/aster/optimization/online_attention.py:74-214),
+ * merge_softmax (:42-63) and SoftmaxState.output (:35-39), for all rows in one launch.
+ *   query/out: [num_seqs, num_q_heads, head_dim] of q_dtype (out has the query
+ *              dtype, online_attention.py:219); strides in elements.
+ *   block_tables: int32 [num_seqs, block_table_stride] physical block ids.
+ *   context_lens: int32 [num_seqs]; the query sits at position ctx-1 and sees
+ *              keys 0..ctx-1 (ctx-window..ctx-1 when window > 0).
+ *   GQA: query head h reads kv head h / (num_q_heads / num_kv_heads).
+ *   max_context_len: host-side upper bound of context_lens (sizes the split-K grid).
+ *   partition_tokens: split-K partition (multiple of 16*4); 0 selects 512.
+ *   workspace: >= astr_paged_attention_i8_workspace_bytes(...) bytes.
+ * Output rows with ctx == 0 are zero (fully-masked rows, online_attention.py:37).
+ */
+int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query, int32_t q_dtype,
+                            int64_t q_token_stride, int64_t q_head_stride, void* out,
+                            int64_t out_token_stride, int64_t out_head_stride,
+                            const int32_t* block_tables, int32_t block_table_stride,
+                            const int32_t* context_lens, int32_t num_seqs, int32_t num_q_heads,
+                            int32_t max_context_len, float scale, int32_t window,
+                            int32_t partition_tokens, void* workspace, size_t workspace_bytes,
+                            int32_t* err_flag, void* stream);
+
+/*
+ * Workspace bytes astr_paged_attention_i8 needs for its split-K partials.
+ * Analogue of KernelSpec.workspace_bytes (src/aster/core/contracts.py:102-134).
+ */
+size_t astr_paged_attention_i8_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                               int32_t head_dim, int32_t max_context_len,
+                                               int32_t partition_tokens);
+
+/* Thread-local description of the last non-zero return code. */
+const char* astr_last_error(void);
+
+/* Library version string ("aster_kv <semver> gfx950"). */
+const char* astr_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ASTER_KV_H */

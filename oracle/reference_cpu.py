@@ -1,0 +1,321 @@
+"""numpy restatement of the reference's INT8 paged-decode arithmetic.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``): the product never imports
+this module. Every function cites the reference file:line it restates, relative
+to the sutiankang/aster source tree (``src/aster/...``).
+
+Parity status of each function (how it is pinned, in ``tests/test_oracle.py``):
+  quantize_kv_int8          pinned: reference known-answer test (seed-76 tensor,
+                            test_hot_kv.py:22-42), exact ties, zero row,
+                            FLT_MIN clamp, true-division vs reciprocal cases,
+                            error bound and |code|max == 127 invariants.
+  dequantize                pinned: closed form fp32(code)*scale (atol 0).
+  merge_softmax / output    pinned: partition merge == whole, -inf partitions.
+  online_attention_statistics
+                            pinned: fp64 brute-force dense softmax (dense.py),
+                            page order invariance, fully-masked rows == 0,
+                            single-key and equal-score closed forms.
+  paged_attention           pinned through online_attention_statistics plus
+                            block-table permutation invariance.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+import math
+
+import numpy as np
+
+FLT_TINY = np.float32(np.finfo(np.float32).tiny)
+DBL_TINY = np.float64(np.finfo(np.float64).tiny)
+INT8_MAXIMUM = 127.0  # kv_quantization.py:23-25 (KVQuantization("int8").maximum)
+
+
+# ----------------------------------------------------------------------------
+# quantization (src/aster/optimization/kv_quantization.py)
+# ----------------------------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class QuantizedKV:
+    """codes int8 [..., T, D] and scales [..., T, 1] (kv_quantization.py:28-68)."""
+
+    values: np.ndarray
+    scales: np.ndarray
+
+    @property
+    def shape(self):
+        return self.values.shape
+
+    def narrow(self, start, count):
+        """Token-axis slice (kv_quantization.py:57-64)."""
+        return QuantizedKV(
+            self.values[..., start : start + count, :], self.scales[..., start : start + count, :]
+        )
+
+    def dequantize(self, dtype=None):
+        """``values.to(scales.dtype) * scales`` then cast (kv_quantization.py:66-68)."""
+        out = self.values.astype(self.scales.dtype) * self.scales
+        return out if dtype is None else out.astype(dtype)
+
+
+def quantize_kv_int8(x):
+    """Per-(token, head) symmetric INT8 codes + scales (kv_quantization.py:71-94).
+
+    ``x`` is a float16/float32/float64 array ``[..., T, D]`` (bf16 data is passed
+    as the float32 array holding the same values, which is what ``.to(float32)``
+    at :82-83 produces). Accumulation is float64 only for float64 input (:82).
+    Steps: amax over the last dim (:84); scale = 1 where amax == 0 else
+    max(amax / 127, tiny) with true division (:86-90); codes =
+    round_half_even(clamp(x / scale, -127, 127)) (:91-93).
+    """
+    x = np.asarray(x)
+    if x.ndim < 3 or x.shape[-1] < 1:
+        raise ValueError("Quantized KV needs explicit layout [...,tokens,width] and format")
+    if x.dtype not in (np.float16, np.float32, np.float64) or not np.isfinite(x).all():
+        raise ValueError("Quantized KV requires finite floating input")
+    acc = np.float64 if x.dtype == np.float64 else np.float32
+    tiny = DBL_TINY if acc == np.float64 else FLT_TINY
+    source = x.astype(acc)
+    maximum = np.abs(source).max(axis=-1, keepdims=True)
+    divided = np.divide(maximum, acc(INT8_MAXIMUM), dtype=acc)
+    scales = np.where(maximum == 0, acc(1.0), np.maximum(divided, tiny)).astype(acc)
+    normalized = np.clip(np.divide(source, scales, dtype=acc), -INT8_MAXIMUM, INT8_MAXIMUM)
+    codes = np.rint(normalized).astype(np.int8)
+    return QuantizedKV(codes, scales)
+
+
+# ----------------------------------------------------------------------------
+# online softmax (src/aster/optimization/online_attention.py)
+# ----------------------------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class AttentionBlock:
+    """One KV page: key/value ``[B, Hkv, T, D]`` float arrays or QuantizedKV,
+    absolute token offset and optional key padding ``[B, T]`` (online_attention.py:10-15)."""
+
+    key: object
+    value: object
+    offset: int
+    padding: np.ndarray | None = None
+
+
+@dataclass(frozen=True)
+class SoftmaxState:
+    """(maximum, mass, weighted) over ``[B, Hkv, G, Q]`` (online_attention.py:29-39)."""
+
+    maximum: np.ndarray
+    mass: np.ndarray
+    weighted: np.ndarray
+
+    def output(self):
+        """``weighted / max(mass, tiny)`` reshaped to ``[B, Hq, Q, Dv]`` (:35-39)."""
+        tiny = DBL_TINY if self.mass.dtype == np.float64 else FLT_TINY
+        value = self.weighted / np.maximum(self.mass, tiny)[..., None]
+        b, h, g, q, w = value.shape
+        return value.reshape(b, h * g, q, w)
+
+
+def _exp_where_finite(m, safe):
+    out = np.zeros_like(m)
+    finite = np.isfinite(m)
+    out[finite] = np.exp(m[finite] - safe[finite])
+    return out
+
+
+def merge_softmax(left, right):
+    """LSE merge of disjoint partitions; non-finite maxima weigh 0 (online_attention.py:42-63)."""
+    if left.maximum.shape != right.maximum.shape or left.weighted.shape != right.weighted.shape:
+        raise ValueError("Attention partitions must describe the same queries and accumulator layout")
+    maximum = np.maximum(left.maximum, right.maximum)
+    safe = np.where(np.isfinite(maximum), maximum, 0).astype(maximum.dtype)
+    a = _exp_where_finite(left.maximum, safe)
+    b = _exp_where_finite(right.maximum, safe)
+    return SoftmaxState(
+        maximum,
+        left.mass * a + right.mass * b,
+        left.weighted * a[..., None] + right.weighted * b[..., None],
+    )
+
+
+def _tile(value, start, count, dtype):
+    """kv_tile (kv_quantization.py:130-132): dequantize a token slice."""
+    if isinstance(value, QuantizedKV):
+        return value.narrow(start, count).dequantize(dtype)
+    return value[..., start : start + count, :].astype(dtype)
+
+
+def _length(value):
+    return value.values.shape[-2] if isinstance(value, QuantizedKV) else value.shape[-2]
+
+
+def online_attention_statistics(
+    query,
+    blocks,
+    *,
+    query_positions,
+    causal=True,
+    window=None,
+    query_padding=None,
+    scale=None,
+    query_block_size=32,
+    key_block_size=64,
+):
+    """Blockwise online softmax over a list of pages (online_attention.py:74-214).
+
+    ``query`` ``[B, Hq, Q, D]``; GQA maps query head ``h`` to kv head ``h // G``
+    through the ``[B, Hkv, G, Q, D]`` reshape (:157-161). Visibility per tile
+    (:175-188): causal ``kpos <= qpos``, window ``kpos > qpos - window``, key and
+    query padding. Fully-invisible tiles are skipped (:189-190); non-finite
+    scores raise (:193-196); each tile's (max, sum, P@V) is merged into the
+    running state with ``merge_softmax`` (:197-206).
+    """
+    blocks = tuple(blocks)
+    query = np.asarray(query)
+    if query.ndim != 4 or min(query.shape) < 1 or not blocks:
+        raise ValueError("Need nonempty query/pages and positive integer tile sizes")
+    if not np.isfinite(query).all():
+        raise ValueError("Query must be finite")
+    acc = np.float64 if query.dtype == np.float64 else np.float32
+    batch, query_heads, queries, width = query.shape
+    heads = blocks[0].key.shape[1]
+    value_width = blocks[0].value.shape[-1]
+    if heads < 1 or query_heads % heads:
+        raise ValueError("Query heads must divide into KV groups")
+    intervals = sorted((b.offset, b.offset + _length(b.key)) for b in blocks)
+    if any(l[1] > r[0] for l, r in zip(intervals, intervals[1:])):
+        raise ValueError("Overlapping KV blocks would count the same key twice")
+    scale = width**-0.5 if scale is None else scale
+    if not math.isfinite(scale) or scale <= 0:
+        raise ValueError("Attention scale must be finite and positive")
+    scale = acc(scale)
+    groups = query_heads // heads
+    positions_all = np.asarray(query_positions)
+    maxima, masses, numerators = [], [], []
+    for begin in range(0, queries, query_block_size):
+        end = min(queries, begin + query_block_size)
+        q = query[:, :, begin:end, :].astype(acc).reshape(batch, heads, groups, end - begin, width)
+        positions = positions_all[:, begin:end]
+        shape = (batch, heads, groups, end - begin)
+        state = SoftmaxState(
+            np.full(shape, -np.inf, dtype=acc),
+            np.zeros(shape, dtype=acc),
+            np.zeros(shape + (value_width,), dtype=acc),
+        )
+        for block in blocks:
+            length = _length(block.key)
+            for start in range(0, length, key_block_size):
+                stop = min(length, start + key_block_size)
+                keys = _tile(block.key, start, stop - start, acc)
+                values = _tile(block.value, start, stop - start, acc)
+                key_positions = np.arange(block.offset + start, block.offset + stop)
+                visible = np.ones((batch, end - begin, stop - start), dtype=bool)
+                if causal:
+                    visible &= key_positions[None, None, :] <= positions[:, :, None]
+                if window is not None:
+                    visible &= key_positions[None, None, :] > positions[:, :, None] - window
+                if block.padding is not None:
+                    visible &= np.asarray(block.padding, dtype=bool)[:, None, start:stop]
+                if query_padding is not None:
+                    visible &= np.asarray(query_padding, dtype=bool)[:, begin:end, None]
+                if not visible.any():
+                    continue
+                scores = np.einsum("bhgqd,bhkd->bhgqk", q, keys) * scale
+                if not np.isfinite(scores).all():
+                    raise ValueError(
+                        "Attention score overflow; cannot repair an infinite dot product with softmax"
+                    )
+                scores = np.where(visible[:, None, None], scores, -np.inf).astype(acc)
+                maximum = scores.max(-1)
+                safe = np.where(np.isfinite(maximum), maximum, 0).astype(acc)
+                probability = np.exp(scores - safe[..., None])
+                local = SoftmaxState(
+                    maximum,
+                    probability.sum(-1),
+                    np.einsum("bhgqk,bhkd->bhgqd", probability, values),
+                )
+                state = merge_softmax(state, local)
+        maxima.append(state.maximum)
+        masses.append(state.mass)
+        numerators.append(state.weighted)
+    return SoftmaxState(
+        np.concatenate(maxima, -1), np.concatenate(masses, -1), np.concatenate(numerators, -2)
+    )
+
+
+def online_attention(query, blocks, **kwargs):
+    """``online_attention_statistics(...).output()`` (online_attention.py:217-219),
+    returned in the accumulator dtype (the cast to the query dtype is left to the
+    caller so parity can be checked before the final rounding)."""
+    return online_attention_statistics(query, blocks, **kwargs).output()
+
+
+# ----------------------------------------------------------------------------
+# paged runner assembly (src/aster/inference/paged_attention.py, state.py)
+# ----------------------------------------------------------------------------
+
+
+def page_blocks(k_codes, k_scales, v_codes, v_scales, block_table, length, block_size,
+                padding=None):
+    """One AttentionBlock per page, narrowed to its valid tokens, at absolute
+    offset ``index * block_size`` (state.py:358-390 read_pages;
+    paged_attention.py:170-183). Arena layout: codes ``[blocks, Hkv, bs, D]``,
+    scales ``[blocks, Hkv, bs]``; ``padding`` optional ``[blocks, bs]`` bool."""
+    blocks = []
+    for index in range(math.ceil(length / block_size)):
+        page = int(block_table[index])
+        count = min(block_size, length - index * block_size)
+        key = QuantizedKV(k_codes[page][None, :, :count], k_scales[page][None, :, :count, None])
+        value = QuantizedKV(v_codes[page][None, :, :count], v_scales[page][None, :, :count, None])
+        pad = None if padding is None else padding[page][None, :count]
+        blocks.append(AttentionBlock(key, value, index * block_size, pad))
+    return blocks
+
+
+def paged_attention(query, k_codes, k_scales, v_codes, v_scales, block_tables, context_lens,
+                    *, block_size, scale, query_lens=None, causal=True, window=None,
+                    query_block_size=32, key_block_size=64, padding=None):
+    """Ragged paged attention over a committed arena, row by row, as
+    ``PagedAttentionRunner.forward_batch`` does (paged_attention.py:168-215).
+
+    ``query`` ``[total_q, Hq, D]`` packed by ``query_lens`` (default: one query
+    token per sequence). Row ``b``'s ``n_b`` queries sit at absolute positions
+    ``context_lens[b] - n_b .. context_lens[b] - 1`` (the chunk has already been
+    appended, so ``context_lens`` counts it). Returns ``[total_q, Hq, Dv]`` in the
+    accumulator dtype.
+    """
+    query = np.asarray(query)
+    n = len(context_lens)
+    query_lens = [1] * n if query_lens is None else [int(x) for x in query_lens]
+    outputs = []
+    cursor = 0
+    for b in range(n):
+        ctx, qn = int(context_lens[b]), query_lens[b]
+        q = query[cursor : cursor + qn].transpose(1, 0, 2)[None]
+        cursor += qn
+        blocks = page_blocks(k_codes, k_scales, v_codes, v_scales, block_tables[b], ctx,
+                             block_size, padding)
+        positions = np.arange(ctx - qn, ctx)[None]
+        out = online_attention(q, blocks, query_positions=positions, causal=causal, window=window,
+                               scale=scale, query_block_size=query_block_size,
+                               key_block_size=key_block_size)
+        outputs.append(out[0].transpose(1, 0, 2))
+    return np.concatenate(outputs, 0)
+
+
+def quantize_append(k, v, slot_mapping, k_codes, k_scales, v_codes, v_scales, block_size):
+    """Quantize new tokens and copy raw codes/scales into ``slot // bs, slot % bs``
+    (state.py:292 quantize, :339-344 per-token copy_kv). ``k``/``v`` ``[T, Hkv, D]``;
+    slots < 0 are skipped. Mutates the arena arrays in place."""
+    qk = quantize_kv_int8(np.asarray(k).transpose(1, 0, 2)[None])
+    qv = quantize_kv_int8(np.asarray(v).transpose(1, 0, 2)[None])
+    for t, slot in enumerate(np.asarray(slot_mapping).tolist()):
+        if slot < 0:
+            continue
+        page, offset = divmod(int(slot), block_size)
+        k_codes[page, :, offset] = qk.values[0, :, t]
+        k_scales[page, :, offset] = qk.scales[0, :, t, 0]
+        v_codes[page, :, offset] = qv.values[0, :, t]
+        v_scales[page, :, offset] = qv.scales[0, :, t, 0]
+    return qk, qv

@@ -1,0 +1,35 @@
+"""Helpers shared by the GPU parity tests: move a PagedKVCache layer to numpy in the
+oracle's arena layout and run the oracle on it."""
+
+import numpy as np
+import torch
+
+from oracle import reference_cpu as ref
+
+# north_star tolerance for attention outputs vs the reference's dequantize-then-attend path
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def arena_numpy(cache, layer=0):
+    """(k_codes, k_scales, v_codes, v_scales) as numpy [blocks, Hkv, bs, D] / [blocks, Hkv, bs]."""
+    codes = cache.codes[:, layer].cpu().numpy()
+    scales = cache.scales[:, layer].cpu().numpy()
+    return codes[:, 0], scales[:, 0], codes[:, 1], scales[:, 1]
+
+
+def oracle_decode(workload_or_tables, cache, query, layer=0, context_lens=None, scale=None,
+                  window=None):
+    if context_lens is None:
+        tables, lens = workload_or_tables.block_tables, workload_or_tables.context_lens
+        scale = workload_or_tables.scale if scale is None else scale
+    else:
+        tables, lens = workload_or_tables, context_lens
+    q = query.float().cpu().numpy()
+    return ref.paged_attention(q, *arena_numpy(cache, layer), tables, lens, block_size=16,
+                               scale=scale, window=window)
+
+
+def assert_attention_close(actual, expected, atol=ATOL, rtol=RTOL):
+    """|a - b| <= atol + rtol * |b| elementwise (torch.testing.assert_close semantics)."""
+    a = actual.float().cpu().numpy() if isinstance(actual, torch.Tensor) else actual
+    np.testing.assert_allclose(a, expected, atol=atol, rtol=rtol)

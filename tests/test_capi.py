@@ -1,0 +1,109 @@
+"""C-ABI library checks that need no GPU: it loads, exports every symbol the header
+declares, sizes workspaces, and rejects bad arguments before touching a device."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from aster_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "aster_kv.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(astr_\w+)\s*\(", text,
+                                 flags=re.M)))
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == sorted(_native.EXPORTED_SYMBOLS)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _native.lib()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.astr_version().decode().endswith("gfx950")
+
+
+def test_workspace_bytes():
+    lib = _native.lib()
+    ws = lib.astr_paged_attention_i8_workspace_bytes
+    # one partition: no split-K partials
+    assert ws(64, 32, 128, 512, 512) == 0
+    assert ws(64, 32, 128, 4096, 512) == 64 * 32 * 8 * (128 + 2) * 4
+    assert ws(16, 64, 128, 32768, 512) == 16 * 64 * 64 * 130 * 4
+    assert ws(4, 4, 64, 300, 64) == 4 * 4 * 5 * 66 * 4
+    assert ws(4, 4, 64, 300, 0) == 0          # 0 selects 512-token partitions
+    assert ws(4, 4, 64, 300, 100) == 0        # not a multiple of 64 -> invalid -> 0
+
+
+def _desc(**kw):
+    base = dict(k_codes=16, v_codes=16, k_scales=16, v_scales=16, code_block_stride=2048,
+                code_head_stride=2048, scale_block_stride=16, scale_head_stride=16,
+                num_blocks=4, block_size=16, num_kv_heads=1, head_dim=128)
+    base.update(kw)
+    return _native.PagedKVDesc(**base)
+
+
+def _attn(desc, **kw):
+    args = dict(query=16, q_dtype=2, q_tok=128, q_head=128, out=16, o_tok=128, o_head=128,
+                tables=16, bt_stride=4, lens=16, num_seqs=1, hq=1, max_ctx=64, scale=0.1,
+                window=0, part=512, ws=None, ws_bytes=0, flag=16)
+    args.update(kw)
+    return _native.lib().astr_paged_attention_i8(
+        ctypes.byref(desc) if desc is not None else None, *args.values(), None)
+
+
+def test_attention_argument_errors_need_no_device():
+    lib = _native.lib()
+    assert _attn(None) == _native.ASTR_EINVAL
+    assert "err_flag" in _native.last_error()
+    assert _attn(_desc(), flag=None) == _native.ASTR_EINVAL
+    assert _attn(_desc(block_size=8)) == _native.ASTR_EUNSUPPORTED
+    assert _attn(_desc(num_kv_heads=2), hq=3) == _native.ASTR_EINVAL
+    assert _attn(_desc(), scale=float("nan")) == _native.ASTR_EINVAL
+    assert _attn(_desc(), scale=0.0) == _native.ASTR_EINVAL
+    assert _attn(_desc(), window=-1) == _native.ASTR_EINVAL
+    assert _attn(_desc(), max_ctx=65, bt_stride=4) == _native.ASTR_EINVAL
+    assert _attn(_desc(), part=100) == _native.ASTR_EINVAL
+    assert _attn(_desc(), q_dtype=7) == _native.ASTR_EUNSUPPORTED
+    assert _attn(_desc(), query=17) == _native.ASTR_EINVAL  # misaligned rows
+    assert _attn(_desc(head_dim=96, code_block_stride=1536, code_head_stride=1536),
+                 q_tok=96, q_head=96, o_tok=96, o_head=96) == _native.ASTR_EUNSUPPORTED
+    assert _attn(_desc(), max_ctx=1024, bt_stride=64, part=64) == _native.ASTR_EINVAL  # no workspace
+    assert "workspace" in _native.last_error()
+    assert _attn(_desc(), num_seqs=0) == 0  # empty batch: nothing to launch
+    del lib
+
+
+def test_append_argument_errors_need_no_device():
+    lib = _native.lib()
+    f = lib.astr_kv_quantize_append_i8
+    d = _desc()
+    assert f(None, 16, 16, 0, 1, 128, 128, 128, 128, 16, 16, None) == _native.ASTR_EINVAL
+    assert f(ctypes.byref(d), 16, 16, 0, -1, 128, 128, 128, 128, 16, 16, None) == _native.ASTR_EINVAL
+    assert f(ctypes.byref(d), 16, 16, 0, 0, 128, 128, 128, 128, 16, 16, None) == 0  # no tokens
+    assert f(ctypes.byref(d), 16, 16, 9, 1, 128, 128, 128, 128, 16, 16, None) == \
+        _native.ASTR_EUNSUPPORTED
+    big = _desc(head_dim=1024)
+    assert f(ctypes.byref(big), 16, 16, 0, 1, 1024, 1024, 1024, 1024, 16, 16, None) == \
+        _native.ASTR_EUNSUPPORTED
+    assert f(ctypes.byref(d), None, 16, 0, 1, 128, 128, 128, 128, 16, 16, None) == _native.ASTR_EINVAL
+
+
+def test_check_maps_codes_to_reference_exceptions():
+    from aster_amd import UnsupportedAttentionBackend
+
+    _attn(None)
+    with pytest.raises(ValueError):
+        _native.check(_native.ASTR_EINVAL, "x")
+    with pytest.raises(UnsupportedAttentionBackend):
+        _native.check(_native.ASTR_EUNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _native.check(98, "x")
+    _native.check(0, "x")

@@ -1,0 +1,190 @@
+"""GPU parity of the paged decode attention kernel against the oracle's page-by-page
+online softmax (online_attention.py:74-219 via paged_attention.py:168-215), within
+the north_star tolerance |a-b| <= 2e-3 + 1e-2|b|, plus size-independent
+properties at the full BASELINE sizes."""
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from aster_amd import KernelWork, PagedKVCache, UnsupportedAttentionBackend
+from aster_amd import workloads as wl
+from tests.gpu_util import arena_numpy, assert_attention_close, oracle_decode
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _build(w, device, layers=1):
+    cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=layers, num_kv_heads=w.num_kv_heads,
+                         head_dim=w.head_dim, device=device)
+    wl.materialize(w, cache, device=device)
+    tables, lens = wl.device_tables(w, device)
+    return cache, tables, lens
+
+
+def test_config1_matches_golden_output(device):
+    g = np.load(os.path.join(GOLDEN, "config1.npz"))
+    cache = PagedKVCache(num_blocks=64, num_layers=1, num_kv_heads=4, head_dim=64, device=device)
+    cache.append(0, torch.from_numpy(g["k"]).to(device), torch.from_numpy(g["v"]).to(device),
+                 torch.from_numpy(g["slots"]).to(device), check=True)
+    q = torch.from_numpy(g["q"]).to(device)
+    tables = torch.from_numpy(g["block_tables"]).to(device)
+    lens = torch.from_numpy(g["context_lens"]).to(device)
+    work = KernelWork()
+    for part in (512, 64):
+        out = cache.paged_attention(0, q, tables, lens, max_context_len=300, scale=64 ** -0.5,
+                                    partition_tokens=part, work=work, check=True)
+        assert out.dtype == torch.float32 and out.shape == (4, 4, 64)
+        assert_attention_close(out, g["out"])
+        # fp32 queries: far tighter than the north_star bound in practice
+        assert_attention_close(out, g["out"], atol=2e-5, rtol=2e-5)
+    assert work.backend == "hip_int8_paged" and work.fallback_reason is None
+
+
+@pytest.mark.parametrize("builder,rows,max_len", [
+    (wl.config2, 12, None),
+    (wl.config4, 6, None),
+    (wl.config5, 2, 3000),
+])
+@pytest.mark.parametrize("part", [512, 64])
+def test_scaled_configs_match_oracle(device, builder, rows, max_len, part):
+    w = wl.scaled(builder(), num_seqs=rows, max_len=max_len)
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    out = cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                                scale=w.scale, partition_tokens=part, check=True)
+    assert out.dtype == w.q_dtype
+    assert_attention_close(out, oracle_decode(w, cache, q))
+
+
+@pytest.mark.parametrize("dim,hq,hkv", [(64, 8, 8), (128, 16, 8), (128, 32, 8), (128, 64, 8),
+                                        (256, 8, 2), (64, 16, 2)])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_head_dims_groups_dtypes(device, dim, hq, hkv, qdtype):
+    lens = np.array([1, 15, 16, 17, 255, 256, 257, 600], np.int32)
+    rng = np.random.default_rng(dim + hq)
+    tables, pool = wl._tables_from_lengths(lens, rng, spare_blocks=3)
+    w = wl.DecodeWorkload("edge", hq, hkv, dim, lens, tables, pool, qdtype, 7, dim ** -0.5)
+    cache, t, l = _build(w, device)
+    q = wl.queries(w, device)
+    out = cache.paged_attention(0, q, t, l, max_context_len=600, partition_tokens=128, check=True)
+    assert_attention_close(out, oracle_decode(w, cache, q))
+
+
+@pytest.mark.parametrize("window", [1, 7, 16, 100, 1000])
+def test_sliding_window(device, window):
+    w = wl.scaled(wl.config2(), num_seqs=6, max_len=700)
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    out = cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                                window=window, partition_tokens=128, check=True)
+    assert_attention_close(out, oracle_decode(w, cache, q, window=window))
+
+
+def test_empty_rows_are_zero_and_ctx_one_returns_value(device):
+    lens = np.array([0, 1, 40, 0], np.int32)
+    tables = np.array([[0, 0, 0], [1, 0, 0], [2, 3, 4], [0, 0, 0]], np.int32)
+    w = wl.DecodeWorkload("empty", 8, 2, 128, lens, tables, 5, torch.bfloat16, 3, 128 ** -0.5)
+    cache = PagedKVCache(num_blocks=5, num_layers=1, num_kv_heads=2, head_dim=128, device=device)
+    wl.materialize(w, cache, device=device)
+    t, l = wl.device_tables(w, device)
+    q = wl.queries(w, device)
+    out = cache.paged_attention(0, q, t, l, max_context_len=40, check=True)
+    assert (out[0] == 0).all() and (out[3] == 0).all()
+    # one visible key: the output is that dequantized value row (per kv head)
+    kc, ks, vc, vs = arena_numpy(cache)
+    vrow = vc[1, :, 0].astype(np.float32) * vs[1, :, 0, None]
+    np.testing.assert_allclose(out[1].float().cpu().numpy(), np.repeat(vrow, 4, 0),
+                               rtol=1e-2, atol=1e-6)
+
+
+def test_full_config2_split_invariance_and_permutation(device):
+    """Full BASELINE config 2: split-K partition size does not change the result
+    beyond tolerance, and relabelling physical blocks (permuting the arena and the
+    block tables together) gives bit-identical output."""
+    w = wl.config2()
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    ref_out = cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                                    partition_tokens=4096, check=True)
+    for part in (512, 256, 64):
+        out = cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                                    partition_tokens=part, check=True)
+        assert_attention_close(out, ref_out.float().cpu().numpy())
+    perm = torch.randperm(w.num_blocks, generator=torch.Generator().manual_seed(5))
+    inverse = torch.argsort(perm).to(torch.int32)
+    other = PagedKVCache(num_blocks=w.num_blocks, num_layers=1, num_kv_heads=8, head_dim=128,
+                         device=device)
+    other.codes.copy_(cache.codes[perm.to(device)])
+    other.scales.copy_(cache.scales[perm.to(device)])
+    tables2 = inverse.to(device)[tables.long()].to(torch.int32).contiguous()
+    out2 = other.paged_attention(0, q, tables2, lens, max_context_len=w.max_context_len,
+                                 check=True)
+    out1 = cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                                 check=True)
+    assert torch.equal(out1, out2)
+    # a few full-length rows against the oracle
+    sub = [int(i) for i in np.argsort(w.context_lens)[-2:]]
+    ora = oracle_decode(w.block_tables[sub], cache, q[sub], context_lens=w.context_lens[sub],
+                        scale=w.scale)
+    assert_attention_close(out1[sub], ora)
+
+
+def test_full_config5_long_context_rows_match_oracle(device):
+    """32768-token rows with 10% x8 K outliers, 64 split-K partitions per row."""
+    w = wl.config5()
+    w = wl.DecodeWorkload(w.name, w.num_q_heads, w.num_kv_heads, w.head_dim, w.context_lens[:2],
+                          w.block_tables[:2], w.num_blocks, w.q_dtype, w.seed, w.scale,
+                          w.k_outlier_fraction)
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    out = cache.paged_attention(0, q, tables, lens, max_context_len=32768, check=True)
+    assert_attention_close(out, oracle_decode(w, cache, q))
+
+
+def test_duplicate_rows_and_prefix_sharing(device):
+    """Rows aliasing the same blocks give identical outputs for identical queries."""
+    w = wl.scaled(wl.config4(), num_seqs=4)
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    t2 = tables.clone()
+    t2[1] = t2[0]
+    l2 = lens.clone()
+    l2[1] = l2[0]
+    q2 = q.clone()
+    q2[1] = q2[0]
+    out = cache.paged_attention(0, q2, t2, l2, max_context_len=w.max_context_len, check=True)
+    assert torch.equal(out[0], out[1])
+
+
+def test_errors(device):
+    w = wl.scaled(wl.config2(), num_seqs=2, max_len=64)
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    bad = tables.clone()
+    bad[0, 0] = w.num_blocks + 7
+    with pytest.raises(ValueError, match="outside"):
+        cache.paged_attention(0, q, bad, lens, max_context_len=w.max_context_len, check=True)
+    long_lens = lens.clone()
+    long_lens[1] = tables.shape[1] * 16 + 5  # beyond the block table: clamped and flagged
+    with pytest.raises(ValueError, match="outside"):
+        cache.paged_attention(0, q, tables, long_lens, max_context_len=w.max_context_len,
+                              check=True)
+    with pytest.raises(ValueError):
+        cache.paged_attention(0, q, tables, lens, max_context_len=10 ** 6)
+    with pytest.raises(ValueError):
+        cache.paged_attention(0, q, tables.long(), lens, max_context_len=64)
+    with pytest.raises(UnsupportedAttentionBackend):
+        cache.paged_attention(0, q.double(), tables, lens, max_context_len=64)
+    with pytest.raises(ValueError, match="divide"):
+        cache.paged_attention(0, torch.zeros(2, 12, 128, device=device, dtype=torch.bfloat16),
+                              tables, lens, max_context_len=64)
+    with pytest.raises(UnsupportedAttentionBackend):  # GQA group of 16 has no kernel
+        cache.paged_attention(0, torch.zeros(2, 128, 128, device=device, dtype=torch.bfloat16),
+                              tables, lens, max_context_len=64)
+    assert math.isfinite(float(cache.paged_attention(0, q, tables, lens, max_context_len=64,
+                                                     check=True).float().abs().max()))
