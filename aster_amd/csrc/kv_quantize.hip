@@ -31,87 +31,158 @@ struct AppendArgs {
   int32_t* err_flag;
 };
 
-template <typename T>
-__global__ __launch_bounds__(256) void finite_scan_kernel(AppendArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t rows = a.num_tokens * a.cache.num_kv_heads;
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= (a.value ? 2 : 1) * rows) return;
-  const bool is_v = row >= rows;
-  const int64_t r = is_v ? row - rows : row;
-  const int64_t t = r / a.cache.num_kv_heads, h = r % a.cache.num_kv_heads;
-  const T* src = static_cast<const T*>(is_v ? a.value : a.key) +
-                 t * (is_v ? a.value_token_stride : a.key_token_stride) +
-                 h * (is_v ? a.value_head_stride : a.key_head_stride);
-  bool bad = false;
-  for (int d = lane; d < a.cache.head_dim; d += kWave) {
-    const float x = to_float<T>(src[d]);
-    bad |= !__builtin_isfinite(x);
-  }
-  if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_INPUT);
+// Row (token t, head h, K or V) handled by this wave; false past the last row.
+struct RowRef {
+  int t, h;
+  bool is_v;
+};
+
+__device__ __forceinline__ bool row_of(const AppendArgs& a, RowRef& rr) {
+  const int heads = a.cache.num_kv_heads;
+  const int rows = (int)a.num_tokens * heads;  // host checks rows * 2 < 2^31
+  const int row = blockIdx.x * kRowsPerBlock + (int)(threadIdx.x >> 6);
+  if (row >= (a.value ? 2 : 1) * rows) return false;
+  rr.is_v = row >= rows;
+  const int r = rr.is_v ? row - rows : row;
+  rr.t = r / heads;
+  rr.h = r - rr.t * heads;
+  return true;
 }
 
 template <typename T>
+__device__ __forceinline__ const T* row_src(const AppendArgs& a, const RowRef& rr) {
+  return static_cast<const T*>(rr.is_v ? a.value : a.key) +
+         rr.t * (rr.is_v ? a.value_token_stride : a.key_token_stride) +
+         rr.h * (rr.is_v ? a.value_head_stride : a.key_head_stride);
+}
+
+// Load the row into registers: VEC consecutive elements per lane when
+// head_dim == 64*VEC (one vector load), otherwise a strided fallback whose
+// loads are clamped in bounds so they all issue before the first use.
+template <typename T, int VEC>
+__device__ __forceinline__ void load_row(const T* src, int D, int lane, float (&x)[kMaxPerLane]) {
+  if constexpr (VEC > 0) {
+    struct alignas(sizeof(T) * VEC) Pack {
+      T e[VEC];
+    };
+    const Pack w = *reinterpret_cast<const Pack*>(src + lane * VEC);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) x[i] = to_float<T>(w.e[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+      const int d = lane + i * kWave;
+      const float v = to_float<T>(src[d < D ? d : D - 1]);
+      x[i] = d < D ? v : 0.f;
+    }
+  }
+}
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void finite_scan_kernel(AppendArgs a) {
+  RowRef rr;
+  if (!row_of(a, rr)) return;
+  const int lane = threadIdx.x & 63;
+  float x[kMaxPerLane];
+  load_row<T, VEC>(row_src<T>(a, rr), a.cache.head_dim, lane, x);
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < (VEC > 0 ? VEC : kMaxPerLane); ++i) bad |= !__builtin_isfinite(x[i]);
+  if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_INPUT);
+}
+
+template <typename T, int VEC>
 __global__ __launch_bounds__(256) void quantize_append_kernel(AppendArgs a) {
   // All-or-nothing: the finite scan of this call (or an unacknowledged earlier
-  // one) flagged the input, so leave every slot untouched.
-  if (__atomic_load_n(a.err_flag, __ATOMIC_RELAXED) & ASTR_FLAG_NONFINITE_INPUT) return;
+  // one) flagged the input, so leave every slot untouched. The flag, slot and
+  // row loads are independent and issue together.
+  RowRef rr;
+  if (!row_of(a, rr)) return;
   const int lane = threadIdx.x & 63;
-  const int64_t rows = a.num_tokens * a.cache.num_kv_heads;
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= (a.value ? 2 : 1) * rows) return;
-  const bool is_v = row >= rows;
-  const int64_t r = is_v ? row - rows : row;
-  const int64_t t = r / a.cache.num_kv_heads, h = r % a.cache.num_kv_heads;
-  const int64_t slot = a.slot_mapping[t];
+  const int flag = __atomic_load_n(a.err_flag, __ATOMIC_RELAXED);
+  const int64_t slot = a.slot_mapping[rr.t];
+  const int D = a.cache.head_dim;
+  float x[kMaxPerLane];
+  load_row<T, VEC>(row_src<T>(a, rr), D, lane, x);
+  if (flag & ASTR_FLAG_NONFINITE_INPUT) return;
   if (slot < 0) return;  // padding token: no slot
-  const int64_t block = slot / a.cache.block_size, offset = slot % a.cache.block_size;
+  const int64_t block = slot / a.cache.block_size, offset = slot - block * a.cache.block_size;
   if (block >= a.cache.num_blocks) {
     if (lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
     return;
   }
-  const int D = a.cache.head_dim;
-  const T* src = static_cast<const T*>(is_v ? a.value : a.key) +
-                 t * (is_v ? a.value_token_stride : a.key_token_stride) +
-                 h * (is_v ? a.value_head_stride : a.key_head_stride);
-  float x[kMaxPerLane];
+  constexpr int N = VEC > 0 ? VEC : kMaxPerLane;
   float amax = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
-    const int d = lane + i * kWave;
-    x[i] = d < D ? to_float<T>(src[d]) : 0.f;
-    amax = fmaxf(amax, fabsf(x[i]));
-  }
+  for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(x[i]));
   amax = wave_max(amax);
   // kv_quantization.py:86-90 -- true division, then the FLT_MIN clamp.
   const float scale = amax == 0.f ? 1.f : fmaxf(amax / 127.f, FLT_MIN);
-  int8_t* codes = (is_v ? a.cache.v_codes : a.cache.k_codes) + block * a.cache.code_block_stride +
-                  h * a.cache.code_head_stride + offset * D;
+  int8_t* codes = (rr.is_v ? a.cache.v_codes : a.cache.k_codes) +
+                  block * a.cache.code_block_stride + rr.h * a.cache.code_head_stride + offset * D;
+  int8_t q[N];
 #pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
-    const int d = lane + i * kWave;
-    if (d < D) {
-      // kv_quantization.py:91-93 -- divide, clamp, round half to even.
-      const float n = fminf(fmaxf(x[i] / scale, -127.f), 127.f);
-      codes[d] = (int8_t)__builtin_rintf(n);
+  for (int i = 0; i < N; ++i) {
+    // kv_quantization.py:91-93 -- divide, clamp, round half to even.
+    const float n = fminf(fmaxf(x[i] / scale, -127.f), 127.f);
+    q[i] = (int8_t)__builtin_rintf(n);
+  }
+  if constexpr (VEC > 0) {
+    struct alignas(VEC) Pack {
+      int8_t e[VEC];
+    };
+    Pack w;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) w.e[i] = q[i];
+    *reinterpret_cast<Pack*>(codes + lane * VEC) = w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+      const int d = lane + i * kWave;
+      if (d < D) codes[d] = q[i];
     }
   }
   if (lane == 0) {
-    float* scales = (is_v ? a.cache.v_scales : a.cache.k_scales) +
-                    block * a.cache.scale_block_stride + h * a.cache.scale_head_stride + offset;
+    float* scales = (rr.is_v ? a.cache.v_scales : a.cache.k_scales) +
+                    block * a.cache.scale_block_stride + rr.h * a.cache.scale_head_stride + offset;
     *scales = scale;
   }
 }
 
-template <typename T>
+template <typename T, int VEC>
 int launch_append(const AppendArgs& a, hipStream_t stream) {
   const int64_t rows = (a.value ? 2 : 1) * a.num_tokens * a.cache.num_kv_heads;
   const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  if (blocks > INT32_MAX) return fail(ASTR_EINVAL, "too many rows for one append launch");
-  hipLaunchKernelGGL(finite_scan_kernel<T>, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
-  hipLaunchKernelGGL(quantize_append_kernel<T>, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((finite_scan_kernel<T, VEC>), dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((quantize_append_kernel<T, VEC>), dim3((uint32_t)blocks), dim3(256), 0,
+                     stream, a);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "quantize_append launch");
+}
+
+template <typename T>
+int launch_append_dim(const AppendArgs& a, hipStream_t stream) {
+  const int D = a.cache.head_dim;
+  // The vector path needs every row start aligned to a whole vector.
+  const int64_t vec = D >= 64 ? D / 64 : 1;
+  auto aligned = [&](const void* p, int64_t tok, int64_t head) {
+    return p == nullptr || (reinterpret_cast<uintptr_t>(p) % (sizeof(T) * vec) == 0 &&
+                            tok % vec == 0 && head % vec == 0);
+  };
+  const bool codes_ok = a.cache.code_block_stride % vec == 0 && a.cache.code_head_stride % vec == 0 &&
+                        reinterpret_cast<uintptr_t>(a.cache.k_codes) % vec == 0 &&
+                        (a.value == nullptr || reinterpret_cast<uintptr_t>(a.cache.v_codes) % vec == 0);
+  if (aligned(a.key, a.key_token_stride, a.key_head_stride) &&
+      aligned(a.value, a.value_token_stride, a.value_head_stride) && codes_ok) {
+    switch (D) {
+      case 64: return launch_append<T, 1>(a, stream);
+      case 128: return launch_append<T, 2>(a, stream);
+      case 256: return launch_append<T, 4>(a, stream);
+      case 512: return launch_append<T, 8>(a, stream);
+      default: break;
+    }
+  }
+  return launch_append<T, 0>(a, stream);
 }
 
 }  // namespace
@@ -138,13 +209,15 @@ extern "C" int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void
                 kWave * kMaxPerLane);
   if (cache->num_kv_heads < 1 || cache->block_size < 1 || cache->num_blocks < 1)
     return fail(ASTR_EINVAL, "cache sizes must be positive");
+  if ((value ? 2 : 1) * num_tokens * (int64_t)cache->num_kv_heads >= INT32_MAX)
+    return fail(ASTR_EINVAL, "too many rows for one append launch");
   AppendArgs a{key, value, key_token_stride, key_head_stride, value_token_stride,
                value_head_stride, num_tokens, slot_mapping, *cache, err_flag};
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (in_dtype) {
-    case ASTR_F32: return launch_append<float>(a, s);
-    case ASTR_F16: return launch_append<_Float16>(a, s);
-    case ASTR_BF16: return launch_append<bf16_t>(a, s);
+    case ASTR_F32: return launch_append_dim<float>(a, s);
+    case ASTR_F16: return launch_append_dim<_Float16>(a, s);
+    case ASTR_BF16: return launch_append_dim<bf16_t>(a, s);
     default: return fail(ASTR_EUNSUPPORTED, "input dtype %d is not f32/f16/bf16", in_dtype);
   }
 }

@@ -1,26 +1,39 @@
 // Ragged paged decode attention over the INT8 KV arena (gfx950).
 //
-// One workgroup (4 waves) per (sequence, kv head, split-K partition). Every
-// wave owns whole 16-token blocks of the partition and serves ALL G query heads
-// of the GQA group from the same registers, so each K/V byte is read from HBM
-// once per (sequence, kv head). Inside a wave, a 16-token block of one kv head
-// (16*D int8 codes, contiguous) is read with 16-byte-per-lane coalesced loads;
-// lane l holds the 16 codes [16*(l % LPT), +16) of token rows l / LPT (+ TPL*j),
-// dequantization is folded into the score (q . (c*s) == s * (q . c)) and into
-// the probability (p * s_v), so codes are converted int8 -> fp32 in registers
-// and never materialised as a tile.
+// Work decomposition: one workgroup (4 waves) per (sequence, kv head, split-K
+// partition). Every wave owns whole 16-token blocks of the partition
+// (blocks w, w+4, ...) and serves all G query heads of the GQA group, so each
+// K/V byte is read from HBM once per (sequence, kv head). The physical block ids
+// of a wave are read once into a register and picked per block with readlane,
+// so the loop issues no dependent vector loads and the next block's K/V loads
+// stay in flight while the current block is processed.
 //
-// Online softmax in base 2 with a lazily-raised reference maximum: a block only
-// rescales the running (l, acc) when one of its scores exceeds the reference by
-// more than kRescaleSlack (a wave-uniform branch, taken on the first block and
-// rarely after), so the common path has no cross-lane max at all. The final
-// state (m, l, acc) is the reference's SoftmaxState (online_attention.py:29-39)
-// up to the exp -> exp2 change of base, which cancels in acc / l.
+// bf16/fp16 queries -> decode_mfma_kernel. Per 16-token block:
+//   S^T[t][g] = K[t][:] . Q[g][:]  on 16x16x32 f16 MFMAs (A = K rows, B = Q^T),
+//   O^T[d][g] += V^T[d][t] P^T[t][g] on 16x16x16 f16 MFMAs (A = V^T, B = P^T).
+// INT8 codes are exact in f16: a byte permute builds 0x64xx halves (1024+u),
+// the XOR with 0x80 makes u = c+128 and a packed f16 subtract of 1152 leaves c
+// exactly. The MFMA output layout of S^T (lane l holds tokens 4*(l/16)+j of head
+// l%16) is exactly the B-operand layout P^T needs, so softmax runs in registers
+// with no transpose. Queries are rounded to f16 after an exact power-of-two
+// rescale that keeps max|q| below 2^15 (the factor is folded into the score
+// scale); probabilities (times the V scale) are rounded to f16 for PV.
 //
-// Partitions of more than one per (sequence, kv head) write (m, l, acc)
-// partials that merge_kernel combines with the merge_softmax rule
-// (online_attention.py:42-63): non-finite maxima weigh 0, output =
-// acc / max(l, FLT_MIN) (:35-39).
+// fp32 queries -> decode_valu_kernel: the same schedule in exact fp32 VALU
+// arithmetic (int8 -> fp32 in registers, 16-wide dot products per lane reduced
+// with DPP), used where f16 operands would lose query precision.
+//
+// Both fold dequantization into the score (q.(c*s) = s*(q.c)) and into the
+// probability (p*s_v), and run the online softmax in base 2 with a lazily
+// raised reference maximum: a block rescales the running (l, acc) only when one
+// of its scores exceeds the reference by more than kRescaleSlack. The final
+// state is the reference's SoftmaxState (online_attention.py:29-39) up to the
+// exp -> exp2 change of base, which cancels in acc / l.
+//
+// Split-K: partitions of one (sequence, kv head) write (m, l, acc) partials;
+// the last workgroup to finish (device-scope atomic counter in the workspace)
+// merges them with the merge_softmax rule (online_attention.py:42-63):
+// non-finite maxima weigh 0, output = acc / max(l, FLT_MIN) (:35-39).
 #include <cfloat>
 #include <cmath>
 
@@ -31,7 +44,13 @@ namespace {
 
 constexpr int kBlockTokens = 16;
 constexpr int kWaves = 4;
+constexpr int kMaxBlocksPerWave = 64;  // partition <= 4096 tokens
 constexpr float kRescaleSlack = 8.0f;  // p = exp2(s - m) <= 2^8 between rescales
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
 
 struct DecodeArgs {
   const void* q;
@@ -47,8 +66,9 @@ struct DecodeArgs {
   int32_t window;
   int32_t part_blocks;  // blocks per split-K partition
   int32_t max_parts;
-  float* ws_ml;  // [num_seqs][num_q_heads][max_parts][2]  (m, l)
-  float* ws_o;   // [num_seqs][num_q_heads][max_parts][D]  unnormalised acc
+  float* ws_o;          // [num_seqs][num_q_heads][max_parts][D]  unnormalised acc
+  float* ws_ml;         // [num_seqs][num_q_heads][max_parts][2]  (m, l)
+  int32_t* ws_count;    // [num_seqs][num_kv_heads] finished-partition counters (kept zero)
   int32_t* err_flag;
 };
 
@@ -79,201 +99,34 @@ __device__ __forceinline__ RowPlan plan_row(const DecodeArgs& a, int seq, bool r
   return r;
 }
 
-template <int NL>
-struct Tile {
-  uint4 k[NL];
-  uint4 v[NL];
-  float ks[NL];
-  float vs[NL];
+// Per-workgroup shared state: the 4 waves' (m, l, acc) and the last-finisher flag.
+template <int G, int D>
+struct Shared {
+  float m[kWaves][G];
+  float l[kWaves][G];
+  float o[kWaves][G][D];
+  int last;
 };
 
-template <typename QT, int D, int G>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
-  constexpr int LPT = D / 16;               // lanes per token row
-  constexpr int TPL = kWave / LPT;          // token rows per load instruction
-  constexpr int NL = kBlockTokens / TPL;    // load instructions per block
-  constexpr int kLoadBytes = kWave * 16;    // bytes per load instruction
-  static_assert(NL >= 1 && NL * TPL == kBlockTokens, "unsupported head_dim");
-
-  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const RowPlan row = plan_row(a, seq, part == 0 && kvh == 0 && threadIdx.x == 0);
-  if (part >= row.num_parts) return;
-  const int pb0 = row.first_blk + part * a.part_blocks;
-  const int pb1 = min(row.last_blk, pb0 + a.part_blocks);
-
-  const int lrow = lane / LPT;
-  const int d0 = (lane % LPT) * 16;
-
-  // Query slice [d0, d0+16) of the G heads kvh*G .. kvh*G+G-1, in fp32.
-  float qf[G][16];
-  {
-    const QT* qp = static_cast<const QT*>(a.q) + seq * a.q_tok + (int64_t)kvh * G * a.q_head + d0;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      constexpr int kVec = 16 / sizeof(QT);
-      const uint4* src = reinterpret_cast<const uint4*>(qp + g * a.q_head);
-#pragma unroll
-      for (int c = 0; c < 16 / kVec; ++c) {
-        uint4 w = src[c];
-        const QT* e = reinterpret_cast<const QT*>(&w);
-#pragma unroll
-        for (int i = 0; i < kVec; ++i) qf[g][c * kVec + i] = to_float<QT>(e[i]);
-      }
-    }
-  }
-
-  float m[G], l[G], acc[G][16];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[g][i] = 0.f;
-  }
-
-  const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
-  const int8_t* kbase = a.cache.k_codes + (int64_t)kvh * a.cache.code_head_stride;
-  const int8_t* vbase = a.cache.v_codes + (int64_t)kvh * a.cache.code_head_stride;
-  const float* ksbase = a.cache.k_scales + (int64_t)kvh * a.cache.scale_head_stride;
-  const float* vsbase = a.cache.v_scales + (int64_t)kvh * a.cache.scale_head_stride;
-
-  auto load_tile = [&](int blk, Tile<NL>& t) -> bool {
-    const int phys = bt[blk];
-    if ((unsigned)phys >= (unsigned)a.cache.num_blocks) return false;
-    const int8_t* kp = kbase + (int64_t)phys * a.cache.code_block_stride + lane * 16;
-    const int8_t* vp = vbase + (int64_t)phys * a.cache.code_block_stride + lane * 16;
-    const float* ksp = ksbase + (int64_t)phys * a.cache.scale_block_stride + lrow;
-    const float* vsp = vsbase + (int64_t)phys * a.cache.scale_block_stride + lrow;
-#pragma unroll
-    for (int j = 0; j < NL; ++j) {
-      t.k[j] = *reinterpret_cast<const uint4*>(kp + j * kLoadBytes);
-      t.v[j] = *reinterpret_cast<const uint4*>(vp + j * kLoadBytes);
-      t.ks[j] = ksp[j * TPL];
-      t.vs[j] = vsp[j * TPL];
-    }
-    return true;
-  };
-
-  int blk = pb0 + wave;
-  Tile<NL> cur;
-  bool cur_ok = blk < pb1 ? load_tile(blk, cur) : false;
-  bool bad_index = false, bad_score = false;
-  for (; blk < pb1; blk += kWaves) {
-    Tile<NL> nxt;
-    const int nblk = blk + kWaves;
-    const bool nxt_ok = nblk < pb1 ? load_tile(nblk, nxt) : false;
-    if (!cur_ok) {
-      bad_index = true;
-    } else {
-      // ---- scores s[j][g] = (q_g . k_t) * scale_k(t) * softmax_scale * log2e
-      float s[NL][G];
-#pragma unroll
-      for (int j = 0; j < NL; ++j) {
-        const uint32_t w[4] = {cur.k[j].x, cur.k[j].y, cur.k[j].z, cur.k[j].w};
-        float kf[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) kf[i] = i8_to_f(w[i / 4], i % 4);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float dot = 0.f;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) dot = fmaf(qf[g][i], kf[i], dot);
-          s[j][g] = group_sum<LPT>(dot);
-        }
-      }
-      bool need = false, nonfinite = false;
-#pragma unroll
-      for (int j = 0; j < NL; ++j) {
-        const int tok = blk * kBlockTokens + j * TPL + lrow;
-        const bool valid = tok >= row.kv_begin && tok < row.ctx;
-        const float f = cur.ks[j] * a.qk_scale_log2;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float v = s[j][g] * f;
-          nonfinite |= valid && !__builtin_isfinite(v);
-          s[j][g] = valid ? v : -INFINITY;
-          need |= s[j][g] > m[g] + kRescaleSlack;
-        }
-      }
-      if (__ballot(nonfinite) != 0) bad_score = true;
-      if (__ballot(need) != 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float tmax = s[0][g];
-#pragma unroll
-          for (int j = 1; j < NL; ++j) tmax = fmaxf(tmax, s[j][g]);
-          tmax = strided_max<LPT>(tmax);
-          const float mn = fmaxf(m[g], tmax);
-          const float alpha = m[g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[g] - mn);
-          l[g] *= alpha;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[g][i] *= alpha;
-          m[g] = mn;
-        }
-      }
-      // ---- P . V with the value scale folded into p
-#pragma unroll
-      for (int j = 0; j < NL; ++j) {
-        const uint32_t w[4] = {cur.v[j].x, cur.v[j].y, cur.v[j].z, cur.v[j].w};
-        float vf[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) vf[i] = i8_to_f(w[i / 4], i % 4);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float p = __builtin_amdgcn_exp2f(s[j][g] - m[g]);
-          l[g] += p;
-          const float pv = p * cur.vs[j];
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[g][i] = fmaf(pv, vf[i], acc[g][i]);
-        }
-      }
-    }
-    cur = nxt;
-    cur_ok = nxt_ok;
-  }
-  if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
-  if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
-
-  // ---- reduce the wave's token rows (lanes of one d-chunk hold other tokens)
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    l[g] = strided_sum<LPT>(l[g]);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[g][i] = strided_sum<LPT>(acc[g][i]);
-  }
-
-  // ---- merge the 4 waves through LDS
-  __shared__ float s_m[kWaves][G], s_l[kWaves][G];
-  __shared__ float s_o[kWaves][G][D];
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      s_m[wave][g] = m[g];
-      s_l[wave][g] = l[g];
-    }
-  }
-  if (lrow == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s_o[wave][g][d0 + i] = acc[g][i];
-  }
-  __syncthreads();
-
+// Combine the 4 waves of the workgroup (already in `sh`) and either write the
+// normalised output (single partition) or this partition's partial; the last
+// partition to finish merges all partials of the (sequence, kv head).
+template <typename QT, int G, int D>
+__device__ void finish_partition(const DecodeArgs& a, Shared<G, D>& sh, const RowPlan& row,
+                                 int seq, int kvh, int part) {
   const bool split = row.num_parts > 1;
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int g = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][g]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sh.m[w][g]);
     float L = 0.f, O = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float mw = s_m[w][g];
+      const float mw = sh.m[w][g];
       const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-      L = fmaf(s_l[w][g], f, L);
-      O = fmaf(s_o[w][g][d], f, O);
+      L = fmaf(sh.l[w][g], f, L);
+      O = fmaf(sh.o[w][g][d], f, O);
     }
     const int h = kvh * G + g;
     if (!split) {
@@ -288,18 +141,25 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
       }
     }
   }
-}
-
-// Split-K combine: merge_softmax over the partitions of each (sequence, q head).
-template <typename QT, int D>
-__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
-  const int h = blockIdx.x, seq = blockIdx.y;
-  const RowPlan row = plan_row(a, seq, false);
-  if (row.num_parts <= 1) return;
-  const int64_t base = ((int64_t)seq * a.num_q_heads + h) * a.max_parts;
-  float M = -INFINITY;
-  for (int p = 0; p < row.num_parts; ++p) M = fmaxf(M, a.ws_ml[(base + p) * 2]);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+  if (!split) return;
+  // Release this partition's partial, then count it; the last one merges.
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t* counter = a.ws_count + (int64_t)seq * a.cache.num_kv_heads + kvh;
+    const int done = atomicAdd(counter, 1);
+    sh.last = done == row.num_parts - 1;
+    if (sh.last) atomicExch(counter, 0);  // every partition has counted: reset for the next call
+  }
+  __syncthreads();
+  if (!sh.last) return;
+  __threadfence();  // acquire the other partitions' partials
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int g = idx / D, d = idx % D;
+    const int h = kvh * G + g;
+    const int64_t base = ((int64_t)seq * a.num_q_heads + h) * a.max_parts;
+    float M = -INFINITY;
+    for (int p = 0; p < row.num_parts; ++p) M = fmaxf(M, a.ws_ml[(base + p) * 2]);
     float L = 0.f, O = 0.f;
     for (int p = 0; p < row.num_parts; ++p) {
       const float mp = a.ws_ml[(base + p) * 2];
@@ -312,13 +172,441 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
   }
 }
 
+// Physical block ids of this wave's blocks (pb0 + wave + 4*i), one per lane.
+__device__ __forceinline__ int wave_block_ids(const DecodeArgs& a, int seq, int first, int nbw,
+                                              int lane) {
+  const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
+  return lane < nbw ? bt[first + kWaves * lane] : 0;
+}
+
+// ================================ MFMA kernel (bf16 / fp16 queries)
+
+template <int D>
+struct MfmaTile {
+  static constexpr int KCH = D / 64;  // 16-byte K chunks per lane
+  static constexpr int VB = D / 16;   // V bytes per lane per token row
+  uint4 k[KCH];
+  uint32_t v[4][VB / 4];
+  float4_t ks, vs;
+};
+
+template <int D>
+__device__ __forceinline__ void load_mfma_tile(const DecodeArgs& a, int phys, int kvh, int r,
+                                               int qg, MfmaTile<D>& t) {
+  constexpr int KCH = MfmaTile<D>::KCH, VB = MfmaTile<D>::VB;
+  const int64_t blk = (int64_t)phys * a.cache.code_block_stride +
+                      (int64_t)kvh * a.cache.code_head_stride;
+  const int8_t* kp = a.cache.k_codes + blk + r * D + 16 * qg;
+#pragma unroll
+  for (int h = 0; h < KCH; ++h) t.k[h] = *reinterpret_cast<const uint4*>(kp + 64 * h);
+  const int8_t* vp = a.cache.v_codes + blk + (4 * qg) * D + r * VB;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int8_t* row = vp + j * D;
+    if constexpr (VB == 4) {
+      t.v[j][0] = *reinterpret_cast<const uint32_t*>(row);
+    } else if constexpr (VB == 8) {
+      const uint2 w = *reinterpret_cast<const uint2*>(row);
+      t.v[j][0] = w.x;
+      t.v[j][1] = w.y;
+    } else {
+      const uint4 w = *reinterpret_cast<const uint4*>(row);
+      t.v[j][0] = w.x;
+      t.v[j][1] = w.y;
+      t.v[j][2] = w.z;
+      t.v[j][3] = w.w;
+    }
+  }
+  const int64_t sb = (int64_t)phys * a.cache.scale_block_stride +
+                     (int64_t)kvh * a.cache.scale_head_stride + 4 * qg;
+  t.ks = *reinterpret_cast<const float4_t*>(a.cache.k_scales + sb);
+  t.vs = *reinterpret_cast<const float4_t*>(a.cache.v_scales + sb);
+}
+
+// 4 int8 codes -> two f16 pairs holding exactly the codes.
+__device__ __forceinline__ void codes_to_f16(uint32_t w, half2_t& lo, half2_t& hi) {
+  const uint32_t u = w ^ 0x80808080u;                       // bytes c + 128
+  const uint32_t l = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // 1024 + u0, 1024 + u1
+  const uint32_t h = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // 1024 + u2, 1024 + u3
+  const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  lo = __builtin_bit_cast(half2_t, l) - bias;
+  hi = __builtin_bit_cast(half2_t, h) - bias;
+}
+
+// Byte k of rows r0/r1 -> f16 pair (code[r0][k], code[r1][k]).
+template <int K>
+__device__ __forceinline__ half2_t column_pair(uint32_t r0, uint32_t r1) {
+  constexpr uint32_t sel = 0x0C000C00u | ((4u + K) << 16) | K;
+  const uint32_t p = __builtin_amdgcn_perm(r1, r0, sel) ^ 0x64806480u;  // 1152 + c
+  const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  return __builtin_bit_cast(half2_t, p) - bias;
+}
+
+template <typename QT, int D, int G>
+__global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
+  static_assert(D == 64 || D == 128 || D == 256, "head_dim");
+  static_assert(G >= 1 && G <= 16, "GQA group");
+  constexpr int KCH = MfmaTile<D>::KCH, VB = MfmaTile<D>::VB;
+  constexpr int NQK = D / 32;  // 16x16x32 MFMAs per block for S^T
+  constexpr int NPV = D / 16;  // 16x16x16 MFMAs per block for O^T
+
+  __shared__ Shared<G, D> sh;
+  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int r = lane & 15, qg = lane >> 4;
+  const RowPlan row = plan_row(a, seq, part == 0 && kvh == 0 && threadIdx.x == 0);
+  if (part >= row.num_parts) return;
+  const int pb0 = row.first_blk + part * a.part_blocks;
+  const int pb1 = min(row.last_blk, pb0 + a.part_blocks);
+  const int first = pb0 + wave;
+  const int nbw = first < pb1 ? (pb1 - first + kWaves - 1) / kWaves : 0;
+  const bool gvalid = r < G;
+
+  // ---- query operand: lane holds Q[g = r][d] for d in 16*qg + 64*h + [0, 16)
+  half8_t qop[NQK];
+  float cf;  // score factor: softmax scale * log2(e) * 2^e
+  {
+    float qv[KCH][16];
+    const QT* qp = static_cast<const QT*>(a.q) + seq * a.q_tok +
+                   (int64_t)(kvh * G + (gvalid ? r : 0)) * a.q_head + 16 * qg;
+    float mx = 0.f;
+#pragma unroll
+    for (int h = 0; h < KCH; ++h) {
+      const uint4* src = reinterpret_cast<const uint4*>(qp + 64 * h);
+      const uint4 w0 = src[0], w1 = src[1];
+      const QT* e0 = reinterpret_cast<const QT*>(&w0);
+      const QT* e1 = reinterpret_cast<const QT*>(&w1);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        qv[h][i] = gvalid ? to_float<QT>(e0[i]) : 0.f;
+        qv[h][8 + i] = gvalid ? to_float<QT>(e1[i]) : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(qv[h][i]));
+    }
+    mx = fmaxf(mx, shfl_xor(mx, 16));
+    mx = fmaxf(mx, shfl_xor(mx, 32));
+    int ex = 0;
+    if (mx >= 32768.f) {
+      frexpf(mx, &ex);
+      ex -= 15;  // mx * 2^-ex < 2^15
+    }
+    const float down = ldexpf(1.f, -ex);
+#pragma unroll
+    for (int kk = 0; kk < NQK; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qop[kk][e] = (_Float16)(qv[kk / 2][(kk % 2) * 8 + e] * down);
+    cf = a.qk_scale_log2 * ldexpf(1.f, ex);
+  }
+
+  float4_t acc[NPV];
+#pragma unroll
+  for (int n = 0; n < NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m = gvalid ? -INFINITY : 0.f;  // invalid head columns never contribute
+  float l = 0.f;
+
+  const int ids = wave_block_ids(a, seq, first, nbw, lane);
+  bool bad_index = false, bad_score = false;
+  // fetch block i of this wave into t; false (and nothing loaded) for a bad id
+  auto fetch = [&](int i, MfmaTile<D>& t) -> bool {
+    const int phys = __builtin_amdgcn_readlane(ids, i);
+    const bool ok = (unsigned)phys < (unsigned)a.cache.num_blocks;
+    if (ok) load_mfma_tile<D>(a, phys, kvh, r, qg, t);
+    return ok;
+  };
+  auto process = [&](int i, const MfmaTile<D>& cur) {
+    // ---- S^T = K . Q^T
+    float4_t s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < NQK; ++kk) {
+      const uint4 c = cur.k[kk / 2];
+      const uint32_t w0 = (kk % 2) ? c.z : c.x, w1 = (kk % 2) ? c.w : c.y;
+      half2_t p0, p1, p2, p3;
+      codes_to_f16(w0, p0, p1);
+      codes_to_f16(w1, p2, p3);
+      const half8_t kop = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+      s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[kk], s4, 0, 0, 0);
+    }
+    // ---- scores of tokens 4*qg + j for head g = r (base-2, dequantised)
+    const int blk = first + kWaves * i;
+    const int tok0 = blk * kBlockTokens + 4 * qg;
+    const bool edge = blk * kBlockTokens < row.kv_begin || (blk + 1) * kBlockTokens > row.ctx;
+    float sc[4];
+    bool need = false, nonfinite = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = s4[j] * (cur.ks[j] * cf);
+      bool valid = gvalid;
+      if (edge) valid = valid && tok0 + j >= row.kv_begin && tok0 + j < row.ctx;
+      nonfinite |= valid && !__builtin_isfinite(v);
+      v = valid ? v : -INFINITY;
+      need |= v > m + kRescaleSlack;
+      sc[j] = v;
+    }
+    if (__ballot(nonfinite) != 0) bad_score = true;
+    if (__ballot(need) != 0) {
+      float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      tmax = fmaxf(tmax, shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, shfl_xor(tmax, 32));
+      const float mn = fmaxf(m, tmax);
+      const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+      l *= alpha;
+#pragma unroll
+      for (int n = 0; n < NPV; ++n) acc[n] *= alpha;
+      m = mn;
+    }
+    half4_t pop;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = __builtin_amdgcn_exp2f(sc[j] - m);
+      l += p;
+      pop[j] = (_Float16)(p * cur.vs[j]);
+    }
+    // ---- O^T += V^T . P^T (row m of MFMA n is d = VB*m + n)
+#pragma unroll
+    for (int n = 0; n < NPV; ++n) {
+      half2_t a01, a23;
+      switch (n % 4) {
+        case 0:
+          a01 = column_pair<0>(cur.v[0][n / 4], cur.v[1][n / 4]);
+          a23 = column_pair<0>(cur.v[2][n / 4], cur.v[3][n / 4]);
+          break;
+        case 1:
+          a01 = column_pair<1>(cur.v[0][n / 4], cur.v[1][n / 4]);
+          a23 = column_pair<1>(cur.v[2][n / 4], cur.v[3][n / 4]);
+          break;
+        case 2:
+          a01 = column_pair<2>(cur.v[0][n / 4], cur.v[1][n / 4]);
+          a23 = column_pair<2>(cur.v[2][n / 4], cur.v[3][n / 4]);
+          break;
+        default:
+          a01 = column_pair<3>(cur.v[0][n / 4], cur.v[1][n / 4]);
+          a23 = column_pair<3>(cur.v[2][n / 4], cur.v[3][n / 4]);
+          break;
+      }
+      const half4_t vop = {a01[0], a01[1], a23[0], a23[1]};
+      acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop, pop, acc[n], 0, 0, 0);
+    }
+  };
+  // Two tiles in fixed registers (ping-pong): block i+1 loads while block i runs.
+  MfmaTile<D> t0, t1;
+  bool ok0 = nbw > 0 ? fetch(0, t0) : false, ok1 = false;
+  for (int i = 0; i < nbw; i += 2) {
+    if (i + 1 < nbw) ok1 = fetch(i + 1, t1);
+    if (ok0) process(i, t0); else bad_index = true;
+    if (i + 1 >= nbw) break;
+    if (i + 2 < nbw) ok0 = fetch(i + 2, t0);
+    if (ok1) process(i + 1, t1); else bad_index = true;
+  }
+  if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+  if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
+
+  // ---- per-wave state to LDS: lane (qg, r<G) holds O[g=r][d = VB*(4*qg + j) + n]
+  l += shfl_xor(l, 16);
+  l += shfl_xor(l, 32);
+  if (gvalid) {
+    if (qg == 0) {
+      sh.m[wave][r] = m;
+      sh.l[wave][r] = l;
+    }
+#pragma unroll
+    for (int n = 0; n < NPV; ++n)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sh.o[wave][r][VB * (4 * qg + j) + n] = acc[n][j];
+  }
+  __syncthreads();
+  finish_partition<QT, G, D>(a, sh, row, seq, kvh, part);
+}
+
+// ================================ exact fp32 VALU kernel (fp32 queries)
+
+template <int NL>
+struct ValuTile {
+  uint4 k[NL];
+  uint4 v[NL];
+  float ks[NL];
+  float vs[NL];
+};
+
+template <typename QT, int D, int G>
+__global__ __launch_bounds__(256) void decode_valu_kernel(DecodeArgs a) {
+  constexpr int LPT = D / 16;             // lanes per token row
+  constexpr int TPL = kWave / LPT;        // token rows per load instruction
+  constexpr int NL = kBlockTokens / TPL;  // load instructions per block
+  constexpr int kLoadBytes = kWave * 16;
+  static_assert(NL >= 1 && NL * TPL == kBlockTokens, "unsupported head_dim");
+
+  __shared__ Shared<G, D> sh;
+  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const RowPlan row = plan_row(a, seq, part == 0 && kvh == 0 && threadIdx.x == 0);
+  if (part >= row.num_parts) return;
+  const int pb0 = row.first_blk + part * a.part_blocks;
+  const int pb1 = min(row.last_blk, pb0 + a.part_blocks);
+  const int first = pb0 + wave;
+  const int nbw = first < pb1 ? (pb1 - first + kWaves - 1) / kWaves : 0;
+  const int lrow = lane / LPT;
+  const int d0 = (lane % LPT) * 16;
+
+  float qf[G][16];
+  {
+    const QT* qp = static_cast<const QT*>(a.q) + seq * a.q_tok + (int64_t)kvh * G * a.q_head + d0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      constexpr int kVec = 16 / sizeof(QT);
+      const uint4* src = reinterpret_cast<const uint4*>(qp + g * a.q_head);
+#pragma unroll
+      for (int c = 0; c < 16 / kVec; ++c) {
+        const uint4 w = src[c];
+        const QT* e = reinterpret_cast<const QT*>(&w);
+#pragma unroll
+        for (int i = 0; i < kVec; ++i) qf[g][c * kVec + i] = to_float<QT>(e[i]);
+      }
+    }
+  }
+  float m[G], l[G], acc[G][16];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[g][i] = 0.f;
+  }
+  const int8_t* kbase = a.cache.k_codes + (int64_t)kvh * a.cache.code_head_stride + lane * 16;
+  const int8_t* vbase = a.cache.v_codes + (int64_t)kvh * a.cache.code_head_stride + lane * 16;
+  const float* ksbase = a.cache.k_scales + (int64_t)kvh * a.cache.scale_head_stride + lrow;
+  const float* vsbase = a.cache.v_scales + (int64_t)kvh * a.cache.scale_head_stride + lrow;
+  auto load = [&](int phys, ValuTile<NL>& t) {
+    const int8_t* kp = kbase + (int64_t)phys * a.cache.code_block_stride;
+    const int8_t* vp = vbase + (int64_t)phys * a.cache.code_block_stride;
+    const float* ksp = ksbase + (int64_t)phys * a.cache.scale_block_stride;
+    const float* vsp = vsbase + (int64_t)phys * a.cache.scale_block_stride;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      t.k[j] = *reinterpret_cast<const uint4*>(kp + j * kLoadBytes);
+      t.v[j] = *reinterpret_cast<const uint4*>(vp + j * kLoadBytes);
+      t.ks[j] = ksp[j * TPL];
+      t.vs[j] = vsp[j * TPL];
+    }
+  };
+
+  const int ids = wave_block_ids(a, seq, first, nbw, lane);
+  bool bad_index = false, bad_score = false;
+  auto fetch = [&](int i, ValuTile<NL>& t) -> bool {
+    const int phys = __builtin_amdgcn_readlane(ids, i);
+    const bool ok = (unsigned)phys < (unsigned)a.cache.num_blocks;
+    if (ok) load(phys, t);
+    return ok;
+  };
+  auto process = [&](int i, const ValuTile<NL>& cur) {
+    const int blk = first + kWaves * i;
+    float s[NL][G];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const uint32_t w[4] = {cur.k[j].x, cur.k[j].y, cur.k[j].z, cur.k[j].w};
+      float kf[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) kf[e] = i8_to_f(w[e / 4], e % 4);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dot = fmaf(qf[g][e], kf[e], dot);
+        s[j][g] = group_sum<LPT>(dot);
+      }
+    }
+    bool need = false, nonfinite = false;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int tok = blk * kBlockTokens + j * TPL + lrow;
+      const bool valid = tok >= row.kv_begin && tok < row.ctx;
+      const float f = cur.ks[j] * a.qk_scale_log2;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float v = s[j][g] * f;
+        nonfinite |= valid && !__builtin_isfinite(v);
+        s[j][g] = valid ? v : -INFINITY;
+        need |= s[j][g] > m[g] + kRescaleSlack;
+      }
+    }
+    if (__ballot(nonfinite) != 0) bad_score = true;
+    if (__ballot(need) != 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float tmax = s[0][g];
+#pragma unroll
+        for (int j = 1; j < NL; ++j) tmax = fmaxf(tmax, s[j][g]);
+        tmax = strided_max<LPT>(tmax);
+        const float mn = fmaxf(m[g], tmax);
+        const float alpha = m[g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[g] - mn);
+        l[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[g][e] *= alpha;
+        m[g] = mn;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const uint32_t w[4] = {cur.v[j].x, cur.v[j].y, cur.v[j].z, cur.v[j].w};
+      float vf[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) vf[e] = i8_to_f(w[e / 4], e % 4);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float p = __builtin_amdgcn_exp2f(s[j][g] - m[g]);
+        l[g] += p;
+        const float pv = p * cur.vs[j];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[g][e] = fmaf(pv, vf[e], acc[g][e]);
+      }
+    }
+  };
+  ValuTile<NL> t0, t1;
+  bool ok0 = nbw > 0 ? fetch(0, t0) : false, ok1 = false;
+  for (int i = 0; i < nbw; i += 2) {
+    if (i + 1 < nbw) ok1 = fetch(i + 1, t1);
+    if (ok0) process(i, t0); else bad_index = true;
+    if (i + 1 >= nbw) break;
+    if (i + 2 < nbw) ok0 = fetch(i + 2, t0);
+    if (ok1) process(i + 1, t1); else bad_index = true;
+  }
+  if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+  if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
+
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    l[g] = strided_sum<LPT>(l[g]);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[g][e] = strided_sum<LPT>(acc[g][e]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      sh.m[wave][g] = m[g];
+      sh.l[wave][g] = l[g];
+    }
+  }
+  if (lrow == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sh.o[wave][g][d0 + e] = acc[g][e];
+  }
+  __syncthreads();
+  finish_partition<QT, G, D>(a, sh, row, seq, kvh, part);
+}
+
+// ================================ launch / dispatch
+
 template <typename QT, int D, int G>
 int launch_decode(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid((uint32_t)a.max_parts, (uint32_t)a.cache.num_kv_heads, (uint32_t)a.num_seqs);
-  hipLaunchKernelGGL((decode_kernel<QT, D, G>), grid, dim3(kWaves * kWave), 0, stream, a);
-  if (a.max_parts > 1) {
-    hipLaunchKernelGGL((merge_kernel<QT, D>), dim3((uint32_t)a.num_q_heads, (uint32_t)a.num_seqs),
-                       dim3(D < 256 ? D : 256), 0, stream, a);
+  if constexpr (sizeof(QT) == 4) {
+    hipLaunchKernelGGL((decode_valu_kernel<QT, D, G>), grid, dim3(kWaves * kWave), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((decode_mfma_kernel<QT, D, G>), grid, dim3(kWaves * kWave), 0, stream, a);
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "paged_attention launch");
@@ -331,7 +619,11 @@ int dispatch_group(const DecodeArgs& a, int G, hipStream_t s) {
     case 2: return launch_decode<QT, D, 2>(a, s);
     case 4: return launch_decode<QT, D, 4>(a, s);
     case 8: return launch_decode<QT, D, 8>(a, s);
-    default: return fail(ASTR_EUNSUPPORTED, "GQA group size %d not in {1,2,4,8}", G);
+    case 16:
+      if constexpr (sizeof(QT) == 2 && D <= 128) return launch_decode<QT, D, 16>(a, s);
+      [[fallthrough]];
+    default:
+      return fail(ASTR_EUNSUPPORTED, "GQA group size %d not supported for this query dtype", G);
   }
 }
 
@@ -351,11 +643,36 @@ int resolve_partition(int32_t partition_tokens) {
   return partition_tokens == 0 ? kDefaultPartitionTokens : partition_tokens;
 }
 
+bool valid_partition(int pt) {
+  return pt > 0 && pt % (kBlockTokens * kWaves) == 0 &&
+         pt <= kBlockTokens * kWaves * kMaxBlocksPerWave;
+}
+
 int64_t max_parts_for(int32_t max_context_len, int32_t partition_tokens) {
   const int64_t blocks = ((int64_t)max_context_len + kBlockTokens - 1) / kBlockTokens;
   const int64_t pb = partition_tokens / kBlockTokens;
   const int64_t parts = (blocks + pb - 1) / pb;
   return parts < 1 ? 1 : parts;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// [completion counters][partial acc][partial (m, l)]: the counters come first
+// so a caller can keep that prefix zero across calls of different shapes.
+struct WorkspaceLayout {
+  size_t count_bytes, o_bytes, ml_bytes;
+  size_t total() const { return count_bytes + o_bytes + ml_bytes; }
+};
+
+WorkspaceLayout workspace_layout(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, int64_t parts) {
+  WorkspaceLayout w{0, 0, 0};
+  if (parts <= 1) return w;
+  const size_t rows = (size_t)num_seqs * num_q_heads * parts;
+  w.count_bytes = align256((size_t)num_seqs * num_kv_heads * sizeof(int32_t));
+  w.o_bytes = align256(rows * head_dim * sizeof(float));
+  w.ml_bytes = align256(rows * 2 * sizeof(float));
+  return w;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -364,16 +681,17 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 }  // namespace astr
 
 extern "C" size_t astr_paged_attention_i8_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
-                                                          int32_t head_dim,
+                                                          int32_t num_kv_heads, int32_t head_dim,
                                                           int32_t max_context_len,
                                                           int32_t partition_tokens) {
   using namespace astr;
-  if (num_seqs < 0 || num_q_heads < 0 || head_dim < 0 || max_context_len < 0) return 0;
+  if (num_seqs < 0 || num_q_heads < 0 || num_kv_heads < 0 || head_dim < 0 || max_context_len < 0)
+    return 0;
   const int pt = resolve_partition(partition_tokens);
-  if (pt <= 0 || pt % (kBlockTokens * kWaves) != 0) return 0;
-  const int64_t parts = max_parts_for(max_context_len, pt);
-  if (parts <= 1) return 0;
-  return (size_t)num_seqs * num_q_heads * parts * (head_dim + 2) * sizeof(float);
+  if (!valid_partition(pt)) return 0;
+  return workspace_layout(num_seqs, num_q_heads, num_kv_heads, head_dim,
+                          max_parts_for(max_context_len, pt))
+      .total();
 }
 
 extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query,
@@ -392,6 +710,7 @@ extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* q
     return fail(ASTR_EINVAL, "num_seqs/max_context_len/block_table_stride must be >= 0 and "
                              "num_q_heads >= 1");
   if (num_seqs == 0) return 0;
+  if (num_seqs > 65535) return fail(ASTR_EUNSUPPORTED, "more than 65535 sequences per launch");
   if (query == nullptr || out == nullptr || block_tables == nullptr || context_lens == nullptr)
     return fail(ASTR_EINVAL, "query, out, block_tables and context_lens are required");
   if (!(scale > 0.f) || !std::isfinite(scale))
@@ -404,9 +723,9 @@ extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* q
                 cache->num_kv_heads);
   if (cache->num_blocks < 1) return fail(ASTR_EINVAL, "cache has no blocks");
   const int pt = resolve_partition(partition_tokens);
-  if (pt <= 0 || pt % (kBlockTokens * kWaves) != 0)
-    return fail(ASTR_EINVAL, "partition_tokens %d must be a positive multiple of %d", pt,
-                kBlockTokens * kWaves);
+  if (!valid_partition(pt))
+    return fail(ASTR_EINVAL, "partition_tokens %d must be a positive multiple of %d up to %d", pt,
+                kBlockTokens * kWaves, kBlockTokens * kWaves * kMaxBlocksPerWave);
   if ((int64_t)max_context_len > (int64_t)block_table_stride * kBlockTokens)
     return fail(ASTR_EINVAL, "max_context_len %d exceeds block table capacity %lld",
                 max_context_len, (long long)block_table_stride * kBlockTokens);
@@ -418,15 +737,19 @@ extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* q
       (out_head_stride * esize) % 16)
     return fail(ASTR_EINVAL, "query/out rows must be 16-byte aligned");
   if (!aligned16(cache->k_codes) || !aligned16(cache->v_codes) ||
-      cache->code_block_stride % 16 || cache->code_head_stride % 16)
-    return fail(ASTR_EINVAL, "cache code blocks must be 16-byte aligned");
+      cache->code_block_stride % 16 || cache->code_head_stride % 16 ||
+      !aligned16(cache->k_scales) || !aligned16(cache->v_scales) ||
+      cache->scale_block_stride % 4 || cache->scale_head_stride % 4)
+    return fail(ASTR_EINVAL, "cache code and scale blocks must be 16-byte aligned");
   const int64_t parts = max_parts_for(max_context_len, pt);
-  if (parts > 65535) return fail(ASTR_EUNSUPPORTED, "too many split-K partitions (%lld)",
-                                 (long long)parts);
-  const size_t need = astr_paged_attention_i8_workspace_bytes(
-      num_seqs, num_q_heads, cache->head_dim, max_context_len, partition_tokens);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-    return fail(ASTR_EINVAL, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+  if (parts > 65535)
+    return fail(ASTR_EUNSUPPORTED, "too many split-K partitions (%lld)", (long long)parts);
+  const WorkspaceLayout ws = workspace_layout(num_seqs, num_q_heads, cache->num_kv_heads,
+                                              cache->head_dim, parts);
+  if (ws.total() > 0 && (workspace == nullptr || workspace_bytes < ws.total() ||
+                         (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0))
+    return fail(ASTR_EINVAL, "a 256-byte aligned workspace of %zu bytes is required (%zu given)",
+                ws.total(), workspace_bytes);
 
   DecodeArgs a{};
   a.q = query;
@@ -445,8 +768,12 @@ extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* q
   a.window = window;
   a.part_blocks = pt / kBlockTokens;
   a.max_parts = (int32_t)parts;
-  a.ws_o = static_cast<float*>(workspace);
-  a.ws_ml = need > 0 ? a.ws_o + (size_t)num_seqs * num_q_heads * parts * cache->head_dim : nullptr;
+  if (ws.total() > 0) {
+    char* base = static_cast<char*>(workspace);
+    a.ws_count = reinterpret_cast<int32_t*>(base);
+    a.ws_o = reinterpret_cast<float*>(base + ws.count_bytes);
+    a.ws_ml = reinterpret_cast<float*>(base + ws.count_bytes + ws.o_bytes);
+  }
   a.err_flag = err_flag;
   const int G = num_q_heads / cache->num_kv_heads;
   hipStream_t s = static_cast<hipStream_t>(stream);

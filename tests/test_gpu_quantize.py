@@ -71,7 +71,8 @@ def _edge_rows(dim, rng):
         r[:n] = ties[:n] * np.float32(2.0**e)
         rows.append(r)
     rows.append(rng.standard_normal(dim).astype(np.float32) * 8)
-    rows.append((rng.standard_normal(dim) * 10.0 ** rng.uniform(-6, 6, dim)).astype(np.float32))
+    # mixed magnitudes that stay finite in fp16 (max 65504)
+    rows.append((rng.standard_normal(dim) * 10.0 ** rng.uniform(-6, 4, dim)).astype(np.float32))
     rows.append(np.full(dim, -3.25, np.float32))
     for _ in range(20):
         rows.append(rng.standard_normal(dim).astype(np.float32))
