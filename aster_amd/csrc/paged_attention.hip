@@ -30,10 +30,12 @@
 // state is the reference's SoftmaxState (online_attention.py:29-39) up to the
 // exp -> exp2 change of base, which cancels in acc / l.
 //
-// Split-K: partitions of one (sequence, kv head) write (m, l, acc) partials;
-// the last workgroup to finish (device-scope atomic counter in the workspace)
-// merges them with the merge_softmax rule (online_attention.py:42-63):
-// non-finite maxima weigh 0, output = acc / max(l, FLT_MIN) (:35-39).
+// Split-K: partitions of one (sequence, kv head) write (m, l, acc) partials and
+// merge_kernel, launched next on the same stream, combines them with the
+// merge_softmax rule (online_attention.py:42-63): non-finite maxima weigh 0,
+// output = acc / max(l, FLT_MIN) (:35-39). (An in-kernel last-finisher merge
+// needs agent-scope fences, which on gfx950 write back and invalidate the
+// whole L2 of the XCD per workgroup; the kernel boundary is far cheaper.)
 #include <cfloat>
 #include <cmath>
 
@@ -68,7 +70,6 @@ struct DecodeArgs {
   int32_t max_parts;
   float* ws_o;          // [num_seqs][num_q_heads][max_parts][D]  unnormalised acc
   float* ws_ml;         // [num_seqs][num_q_heads][max_parts][2]  (m, l)
-  int32_t* ws_count;    // [num_seqs][num_kv_heads] finished-partition counters (kept zero)
   int32_t* err_flag;
 };
 
@@ -99,18 +100,16 @@ __device__ __forceinline__ RowPlan plan_row(const DecodeArgs& a, int seq, bool r
   return r;
 }
 
-// Per-workgroup shared state: the 4 waves' (m, l, acc) and the last-finisher flag.
+// Per-workgroup shared state: the 4 waves' (m, l, acc).
 template <int G, int D>
 struct Shared {
   float m[kWaves][G];
   float l[kWaves][G];
   float o[kWaves][G][D];
-  int last;
 };
 
-// Combine the 4 waves of the workgroup (already in `sh`) and either write the
-// normalised output (single partition) or this partition's partial; the last
-// partition to finish merges all partials of the (sequence, kv head).
+// Combine the 4 waves of the workgroup (already in `sh`) and write either the
+// normalised output (single partition) or this partition's partial.
 template <typename QT, int G, int D>
 __device__ void finish_partition(const DecodeArgs& a, Shared<G, D>& sh, const RowPlan& row,
                                  int seq, int kvh, int part) {
@@ -140,35 +139,6 @@ __device__ void finish_partition(const DecodeArgs& a, Shared<G, D>& sh, const Ro
         a.ws_ml[base * 2 + 1] = L;
       }
     }
-  }
-  if (!split) return;
-  // Release this partition's partial, then count it; the last one merges.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int32_t* counter = a.ws_count + (int64_t)seq * a.cache.num_kv_heads + kvh;
-    const int done = atomicAdd(counter, 1);
-    sh.last = done == row.num_parts - 1;
-    if (sh.last) atomicExch(counter, 0);  // every partition has counted: reset for the next call
-  }
-  __syncthreads();
-  if (!sh.last) return;
-  __threadfence();  // acquire the other partitions' partials
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-    const int g = idx / D, d = idx % D;
-    const int h = kvh * G + g;
-    const int64_t base = ((int64_t)seq * a.num_q_heads + h) * a.max_parts;
-    float M = -INFINITY;
-    for (int p = 0; p < row.num_parts; ++p) M = fmaxf(M, a.ws_ml[(base + p) * 2]);
-    float L = 0.f, O = 0.f;
-    for (int p = 0; p < row.num_parts; ++p) {
-      const float mp = a.ws_ml[(base + p) * 2];
-      const float f = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
-      L = fmaf(a.ws_ml[(base + p) * 2 + 1], f, L);
-      O = fmaf(a.ws_o[(base + p) * D + d], f, O);
-    }
-    QT* op = static_cast<QT*>(a.out) + seq * a.o_tok + (int64_t)h * a.o_head;
-    op[d] = from_float<QT>(O / fmaxf(L, FLT_MIN));
   }
 }
 
@@ -598,6 +568,63 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeArgs a) {
   finish_partition<QT, G, D>(a, sh, row, seq, kvh, part);
 }
 
+// ================================ split-K merge
+
+// One wave per (sequence, q head) with more than one partition: lanes load the
+// partitions' (m, l) in parallel, take the wave max, and every lane then sums
+// its d-slice over the partitions with the merge_softmax weights exp2(m_p - M).
+template <typename QT, int D>
+__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
+  constexpr int kPerLane = (D + kWave - 1) / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int unit = blockIdx.x * kWaves + threadIdx.x / kWave;  // seq * Hq + h
+  if (unit >= a.num_seqs * a.num_q_heads) return;
+  const int seq = unit / a.num_q_heads, h = unit % a.num_q_heads;
+  const RowPlan row = plan_row(a, seq, false);
+  if (row.num_parts <= 1) return;
+  const int64_t base = (int64_t)unit * a.max_parts;
+  float M = -INFINITY;
+  for (int p = lane; p < row.num_parts; p += kWave) M = fmaxf(M, a.ws_ml[(base + p) * 2]);
+  M = wave_max(M);
+  float L = 0.f, O[kPerLane];
+#pragma unroll
+  for (int e = 0; e < kPerLane; ++e) O[e] = 0.f;
+  for (int p0 = 0; p0 < row.num_parts; p0 += kWave) {
+    const int p = p0 + lane;
+    float w = 0.f, lw = 0.f;
+    if (p < row.num_parts) {
+      const float mp = a.ws_ml[(base + p) * 2];
+      w = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
+      lw = a.ws_ml[(base + p) * 2 + 1] * w;
+    }
+    // L = sum over partitions (every lane gets the total)
+    lw += shfl_xor(lw, 1);
+    lw += shfl_xor(lw, 2);
+    lw += shfl_xor(lw, 4);
+    lw += shfl_xor(lw, 8);
+    lw += shfl_xor(lw, 16);
+    lw += shfl_xor(lw, 32);
+    L += lw;
+    const int np = min(kWave, row.num_parts - p0);
+    for (int q = 0; q < np; ++q) {
+      const float wq = __shfl(w, q, kWave);
+      const float* op = a.ws_o + (base + p0 + q) * D;
+#pragma unroll
+      for (int e = 0; e < kPerLane; ++e) {
+        const int d = lane + e * kWave;
+        if (d < D) O[e] = fmaf(op[d], wq, O[e]);
+      }
+    }
+  }
+  QT* out = static_cast<QT*>(a.out) + seq * a.o_tok + (int64_t)h * a.o_head;
+  const float inv_l = 1.f / fmaxf(L, FLT_MIN);
+#pragma unroll
+  for (int e = 0; e < kPerLane; ++e) {
+    const int d = lane + e * kWave;
+    if (d < D) out[d] = from_float<QT>(O[e] * inv_l);
+  }
+}
+
 // ================================ launch / dispatch
 
 template <typename QT, int D, int G>
@@ -607,6 +634,11 @@ int launch_decode(const DecodeArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((decode_valu_kernel<QT, D, G>), grid, dim3(kWaves * kWave), 0, stream, a);
   } else {
     hipLaunchKernelGGL((decode_mfma_kernel<QT, D, G>), grid, dim3(kWaves * kWave), 0, stream, a);
+  }
+  if (a.max_parts > 1) {
+    const int units = a.num_seqs * a.num_q_heads;
+    hipLaunchKernelGGL((merge_kernel<QT, D>), dim3((units + kWaves - 1) / kWaves),
+                       dim3(kWaves * kWave), 0, stream, a);
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "paged_attention launch");
@@ -657,19 +689,17 @@ int64_t max_parts_for(int32_t max_context_len, int32_t partition_tokens) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// [completion counters][partial acc][partial (m, l)]: the counters come first
-// so a caller can keep that prefix zero across calls of different shapes.
+// [partial acc][partial (m, l)]
 struct WorkspaceLayout {
-  size_t count_bytes, o_bytes, ml_bytes;
-  size_t total() const { return count_bytes + o_bytes + ml_bytes; }
+  size_t o_bytes, ml_bytes;
+  size_t total() const { return o_bytes + ml_bytes; }
 };
 
-WorkspaceLayout workspace_layout(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
-                                 int32_t head_dim, int64_t parts) {
-  WorkspaceLayout w{0, 0, 0};
+WorkspaceLayout workspace_layout(int32_t num_seqs, int32_t num_q_heads, int32_t head_dim,
+                                 int64_t parts) {
+  WorkspaceLayout w{0, 0};
   if (parts <= 1) return w;
   const size_t rows = (size_t)num_seqs * num_q_heads * parts;
-  w.count_bytes = align256((size_t)num_seqs * num_kv_heads * sizeof(int32_t));
   w.o_bytes = align256(rows * head_dim * sizeof(float));
   w.ml_bytes = align256(rows * 2 * sizeof(float));
   return w;
@@ -681,16 +711,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 }  // namespace astr
 
 extern "C" size_t astr_paged_attention_i8_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
-                                                          int32_t num_kv_heads, int32_t head_dim,
+                                                          int32_t head_dim,
                                                           int32_t max_context_len,
                                                           int32_t partition_tokens) {
   using namespace astr;
-  if (num_seqs < 0 || num_q_heads < 0 || num_kv_heads < 0 || head_dim < 0 || max_context_len < 0)
-    return 0;
+  if (num_seqs < 0 || num_q_heads < 0 || head_dim < 0 || max_context_len < 0) return 0;
   const int pt = resolve_partition(partition_tokens);
   if (!valid_partition(pt)) return 0;
-  return workspace_layout(num_seqs, num_q_heads, num_kv_heads, head_dim,
-                          max_parts_for(max_context_len, pt))
+  return workspace_layout(num_seqs, num_q_heads, head_dim, max_parts_for(max_context_len, pt))
       .total();
 }
 
@@ -744,8 +772,7 @@ extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* q
   const int64_t parts = max_parts_for(max_context_len, pt);
   if (parts > 65535)
     return fail(ASTR_EUNSUPPORTED, "too many split-K partitions (%lld)", (long long)parts);
-  const WorkspaceLayout ws = workspace_layout(num_seqs, num_q_heads, cache->num_kv_heads,
-                                              cache->head_dim, parts);
+  const WorkspaceLayout ws = workspace_layout(num_seqs, num_q_heads, cache->head_dim, parts);
   if (ws.total() > 0 && (workspace == nullptr || workspace_bytes < ws.total() ||
                          (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0))
     return fail(ASTR_EINVAL, "a 256-byte aligned workspace of %zu bytes is required (%zu given)",
@@ -770,9 +797,8 @@ extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* q
   a.max_parts = (int32_t)parts;
   if (ws.total() > 0) {
     char* base = static_cast<char*>(workspace);
-    a.ws_count = reinterpret_cast<int32_t*>(base);
-    a.ws_o = reinterpret_cast<float*>(base + ws.count_bytes);
-    a.ws_ml = reinterpret_cast<float*>(base + ws.count_bytes + ws.o_bytes);
+    a.ws_o = reinterpret_cast<float*>(base);
+    a.ws_ml = reinterpret_cast<float*>(base + ws.o_bytes);
   }
   a.err_flag = err_flag;
   const int G = num_q_heads / cache->num_kv_heads;

@@ -56,7 +56,6 @@ class PagedKVCache:
                                  dtype=torch.float32, device=device)
         self.err_flag = torch.zeros(1, dtype=torch.int32, device=device)
         self._workspace = None
-        self._zero_prefix = 0
         self._descs = [self._make_desc(layer) for layer in range(num_layers)]
 
     # ---- descriptors --------------------------------------------------------
@@ -132,24 +131,16 @@ class PagedKVCache:
     def workspace_bytes(self, num_seqs, num_q_heads, max_context_len,
                         partition_tokens=DEFAULT_PARTITION_TOKENS):
         return int(_native.lib().astr_paged_attention_i8_workspace_bytes(
-            num_seqs, num_q_heads, self.num_kv_heads, self.head_dim, max_context_len,
-            partition_tokens))
+            num_seqs, num_q_heads, self.head_dim, max_context_len, partition_tokens))
 
     def workspace(self, num_seqs, num_q_heads, max_context_len,
                   partition_tokens=DEFAULT_PARTITION_TOKENS):
-        """Split-K workspace owned by this cache, grown on demand. It starts with
-        per-(sequence, kv head) completion counters that must be zero when a call
-        starts; each call leaves its counter prefix zero and uses the rest as
-        scratch, so only a counter prefix longer than the last one needs zeroing."""
+        """Split-K scratch owned by this cache, grown on demand (None when unneeded)."""
         need = self.workspace_bytes(num_seqs, num_q_heads, max_context_len, partition_tokens)
         if not need:
             return None
-        counters = _align256(num_seqs * self.num_kv_heads * 4)
         if self._workspace is None or self._workspace.numel() < need:
-            self._workspace = torch.zeros(need, dtype=torch.uint8, device=self.device)
-        elif counters > self._zero_prefix:
-            self._workspace[self._zero_prefix:counters].zero_()
-        self._zero_prefix = counters
+            self._workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
         return self._workspace
 
     def paged_attention(self, layer, query, block_tables, context_lens, *, max_context_len,
@@ -202,7 +193,7 @@ class PagedKVCache:
             "paged_attention")
         if work is not None:
             work.backend, work.fallback_reason = BACKEND, None
-            work.page_launches += 1
+            work.page_launches += 2 if need else 1
             work.query_tiles += 1
             work.max_query_tile = max(work.max_query_tile, 1)
             work.max_key_tile = max(work.max_key_tile, self.block_size)
@@ -210,10 +201,6 @@ class PagedKVCache:
         if check:
             self.raise_errors()
         return out
-
-
-def _align256(x):
-    return (x + 255) // 256 * 256
 
 
 def _check_rows(tensor, name, heads, width, device):

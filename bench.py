@@ -8,8 +8,8 @@ slot_mapping, then ragged paged attention of the 64 bf16 query rows (32 q heads,
 K/V from HBM, not from the 256 MB MALL, as a real multi-layer decode does.
 
 value = attended KV-tokens/s = sum(context_lens) / step time. The ``roofline``
-object is for the attention call (one decode_mfma_kernel launch with its split-K
-merge fused in), timed with HIP events on the launch stream; ``cpu_baseline`` times the numpy restatement of the
+object is for the attention call (decode_mfma_kernel plus the split-K
+merge_kernel), timed with HIP events on the launch stream; ``cpu_baseline`` times the numpy restatement of the
 reference's CPU path (oracle/) on a bounded sample on this host.
 """
 
@@ -95,8 +95,7 @@ def main():
     out = torch.empty_like(q)
     k_new, v_new, slots = step_batch
     ws_bytes = cache.workspace_bytes(w.num_seqs, w.num_q_heads, w.max_context_len, args.partition)
-    # zero-filled: the split-K completion counters must start at zero (calls keep them zero)
-    workspace = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=device)
+    workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=device)
 
     def attend(layer):
         cache.paged_attention(layer, q, tables, lens, max_context_len=w.max_context_len,
@@ -167,7 +166,7 @@ def main():
         },
         "hbm_fraction_of_step": alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "roofline": {
-            "kernel": "decode_mfma_kernel (one paged_attention call, split-K merge fused)",
+            "kernel": "decode_mfma_kernel + merge_kernel (one paged_attention call)",
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
             "algorithmic_bytes_per_launch": alg_bytes,

@@ -109,12 +109,12 @@ int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void* key, cons
  *   max_context_len: host-side upper bound of context_lens (sizes the split-K grid).
  *   partition_tokens: split-K partition (multiple of 64, at most 4096); 0
  *              selects 512.
- *   workspace: >= astr_paged_attention_i8_workspace_bytes(...) bytes, 256-byte
- *              aligned (NULL allowed when that size is 0). Its first
- *              align256(num_seqs * num_kv_heads * 4) bytes are completion
- *              counters that must be zero when the call starts; the call
- *              leaves them zero (the rest is scratch). Calls sharing one
- *              workspace must be stream-ordered (concurrent calls race).
+ *   workspace: >= astr_paged_attention_i8_workspace_bytes(...) bytes of
+ *              scratch for split-K partials, 256-byte aligned (NULL allowed
+ *              when that size is 0); no initialisation needed. Calls sharing
+ *              one workspace must be stream-ordered (concurrent calls race).
+ * Launches the decode kernel and, when any row can span more than one
+ * partition, the split-K merge kernel after it on the same stream.
  * Output rows with ctx == 0 are zero (fully-masked rows, online_attention.py:37).
  */
 int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query, int32_t q_dtype,
@@ -127,13 +127,12 @@ int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query, int32
                             int32_t* err_flag, void* stream);
 
 /*
- * Workspace bytes astr_paged_attention_i8 needs for its split-K partials and
- * per-(sequence, kv head) completion counters (0 when no row can split).
+ * Workspace bytes astr_paged_attention_i8 needs for its split-K partials
+ * (0 when no row can span more than one partition).
  * Analogue of KernelSpec.workspace_bytes (src/aster/core/contracts.py:102-134).
  */
 size_t astr_paged_attention_i8_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
-                                               int32_t num_kv_heads, int32_t head_dim,
-                                               int32_t max_context_len,
+                                               int32_t head_dim, int32_t max_context_len,
                                                int32_t partition_tokens);
 
 /* Thread-local description of the last non-zero return code. */

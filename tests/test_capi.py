@@ -34,17 +34,17 @@ def test_workspace_bytes():
     lib = _native.lib()
     ws = lib.astr_paged_attention_i8_workspace_bytes
     # one partition: no split-K partials
-    def expect(s, hq, hkv, d, parts):
+    def expect(s, hq, d, parts):
         a = lambda x: (x + 255) // 256 * 256
-        return a(s * hkv * 4) + a(s * hq * parts * d * 4) + a(s * hq * parts * 8)
+        return a(s * hq * parts * d * 4) + a(s * hq * parts * 8)
 
-    assert ws(64, 32, 8, 128, 512, 512) == 0
-    assert ws(64, 32, 8, 128, 4096, 512) == expect(64, 32, 8, 128, 8)
-    assert ws(16, 64, 8, 128, 32768, 512) == expect(16, 64, 8, 128, 64)
-    assert ws(4, 4, 4, 64, 300, 64) == expect(4, 4, 4, 64, 5)
-    assert ws(4, 4, 4, 64, 300, 0) == 0          # 0 selects 512-token partitions
-    assert ws(4, 4, 4, 64, 300, 100) == 0        # not a multiple of 64 -> invalid -> 0
-    assert ws(4, 4, 4, 64, 9000, 8192) == 0      # partitions above 4096 tokens are invalid
+    assert ws(64, 32, 128, 512, 512) == 0
+    assert ws(64, 32, 128, 4096, 512) == expect(64, 32, 128, 8)
+    assert ws(16, 64, 128, 32768, 512) == expect(16, 64, 128, 64)
+    assert ws(4, 4, 64, 300, 64) == expect(4, 4, 64, 5)
+    assert ws(4, 4, 64, 300, 0) == 0          # 0 selects 512-token partitions
+    assert ws(4, 4, 64, 300, 100) == 0        # not a multiple of 64 -> invalid -> 0
+    assert ws(4, 4, 64, 9000, 8192) == 0      # partitions above 4096 tokens are invalid
 
 
 def _desc(**kw):

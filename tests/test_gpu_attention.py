@@ -183,8 +183,8 @@ def test_errors(device):
     with pytest.raises(ValueError, match="divide"):
         cache.paged_attention(0, torch.zeros(2, 12, 128, device=device, dtype=torch.bfloat16),
                               tables, lens, max_context_len=64)
-    with pytest.raises(UnsupportedAttentionBackend):  # GQA group of 16 has no kernel
-        cache.paged_attention(0, torch.zeros(2, 128, 128, device=device, dtype=torch.bfloat16),
+    with pytest.raises(UnsupportedAttentionBackend):  # GQA group of 32 has no kernel
+        cache.paged_attention(0, torch.zeros(2, 256, 128, device=device, dtype=torch.bfloat16),
                               tables, lens, max_context_len=64)
     assert math.isfinite(float(cache.paged_attention(0, q, tables, lens, max_context_len=64,
                                                      check=True).float().abs().max()))
