@@ -47,6 +47,7 @@ namespace {
 constexpr int kBlockTokens = 16;
 constexpr int kWaves = 4;
 constexpr int kMaxBlocksPerWave = 64;  // partition <= 4096 tokens
+constexpr int kStages = 2;             // LDS stages per wave in the MFMA kernel
 constexpr float kRescaleSlack = 8.0f;  // p = exp2(s - m) <= 2^8 between rescales
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -151,46 +152,74 @@ __device__ __forceinline__ int wave_block_ids(const DecodeArgs& a, int seq, int 
 
 // ================================ MFMA kernel (bf16 / fp16 queries)
 
+// One LDS stage holds a 16-token block of one kv head exactly as it sits in
+// HBM: K codes (16 rows x D bytes), V codes, then 16 K and 16 V fp32 scales.
+// Stages are filled with direct global->LDS loads (global_load_lds_dwordx4),
+// so staging costs no VGPRs and a wave can keep NS blocks in flight.
 template <int D>
-struct MfmaTile {
-  static constexpr int KCH = D / 64;  // 16-byte K chunks per lane
-  static constexpr int VB = D / 16;   // V bytes per lane per token row
-  uint4 k[KCH];
-  uint32_t v[4][VB / 4];
-  float4_t ks, vs;
+struct Stage {
+  static constexpr int kK = 0;
+  static constexpr int kV = 16 * D;
+  static constexpr int kS = 32 * D;
+  static constexpr int kBytes = 32 * D + 128;
+  static constexpr int kCodeLoads = 16 * D / 1024;   // 1 KiB wave-loads per K (and per V) tile
+  static constexpr int kLoads = 2 * kCodeLoads + 1;  // VMEM instructions per stage
 };
 
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+// Byte address of an LDS location, as M0 expects it.
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return (uint32_t)(uintptr_t)(const lds_char_t*)p;
+}
+
+// Direct global -> LDS loads. Each lane's 16 (or 4) bytes land at
+// M0 + lane * 16 (or 4). Issued as inline asm so the compiler does not add its
+// conservative "wait for every LDS DMA" before unrelated LDS reads; the stage
+// pipeline waits for exactly the loads it needs with wait_vmcnt.
+__device__ __forceinline__ void lds_dma_x4(const void* gptr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(gptr)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ void lds_dma_x1(const void* gptr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(lds), "v"(gptr)
+               : "memory", "m0");
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// Issue the direct-to-LDS loads of block `phys` (kv head kvh) into stage `st`:
+// exactly Stage<D>::kLoads vector-memory instructions (waves are always full,
+// so the 32-lane scale load always issues).
 template <int D>
-__device__ __forceinline__ void load_mfma_tile(const DecodeArgs& a, int phys, int kvh, int r,
-                                               int qg, MfmaTile<D>& t) {
-  constexpr int KCH = MfmaTile<D>::KCH, VB = MfmaTile<D>::VB;
-  const int64_t blk = (int64_t)phys * a.cache.code_block_stride +
-                      (int64_t)kvh * a.cache.code_head_stride;
-  const int8_t* kp = a.cache.k_codes + blk + r * D + 16 * qg;
+__device__ __forceinline__ void stage_block(const DecodeArgs& a, int phys, int kvh, int lane,
+                                            char* st) {
+  using S = Stage<D>;
+  const int64_t off = (int64_t)phys * a.cache.code_block_stride +
+                      (int64_t)kvh * a.cache.code_head_stride + lane * 16;
+  const uint32_t base = lds_addr(st);
 #pragma unroll
-  for (int h = 0; h < KCH; ++h) t.k[h] = *reinterpret_cast<const uint4*>(kp + 64 * h);
-  const int8_t* vp = a.cache.v_codes + blk + (4 * qg) * D + r * VB;
+  for (int j = 0; j < S::kCodeLoads; ++j)
+    lds_dma_x4(a.cache.k_codes + off + j * 1024, base + S::kK + j * 1024);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int8_t* row = vp + j * D;
-    if constexpr (VB == 4) {
-      t.v[j][0] = *reinterpret_cast<const uint32_t*>(row);
-    } else if constexpr (VB == 8) {
-      const uint2 w = *reinterpret_cast<const uint2*>(row);
-      t.v[j][0] = w.x;
-      t.v[j][1] = w.y;
-    } else {
-      const uint4 w = *reinterpret_cast<const uint4*>(row);
-      t.v[j][0] = w.x;
-      t.v[j][1] = w.y;
-      t.v[j][2] = w.z;
-      t.v[j][3] = w.w;
-    }
+  for (int j = 0; j < S::kCodeLoads; ++j)
+    lds_dma_x4(a.cache.v_codes + off + j * 1024, base + S::kV + j * 1024);
+  const int64_t so = (int64_t)phys * a.cache.scale_block_stride +
+                     (int64_t)kvh * a.cache.scale_head_stride;
+  if (lane < 32) {
+    const float* src = lane < 16 ? a.cache.k_scales + so + lane : a.cache.v_scales + so + lane - 16;
+    lds_dma_x1(src, base + S::kS);
   }
-  const int64_t sb = (int64_t)phys * a.cache.scale_block_stride +
-                     (int64_t)kvh * a.cache.scale_head_stride + 4 * qg;
-  t.ks = *reinterpret_cast<const float4_t*>(a.cache.k_scales + sb);
-  t.vs = *reinterpret_cast<const float4_t*>(a.cache.v_scales + sb);
 }
 
 // 4 int8 codes -> two f16 pairs holding exactly the codes.
@@ -212,41 +241,89 @@ __device__ __forceinline__ half2_t column_pair(uint32_t r0, uint32_t r1) {
   return __builtin_bit_cast(half2_t, p) - bias;
 }
 
-template <typename QT, int D, int G>
+template <int K>
+__device__ __forceinline__ half4_t v_operand(const uint32_t (&v)[4]) {
+  const half2_t a01 = column_pair<K>(v[0], v[1]);
+  const half2_t a23 = column_pair<K>(v[2], v[3]);
+  return half4_t{a01[0], a01[1], a23[0], a23[1]};
+}
+
+template <int D, int G>
+constexpr int stage0_bytes() {
+  constexpr int staging = kWaves * Stage<D>::kBytes;
+  constexpr int merge = (int)sizeof(Shared<G, D>);
+  return staging > merge ? staging : merge;
+}
+
+template <typename QT, int D, int G, int NS>
 __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   static_assert(G >= 1 && G <= 16, "GQA group");
-  constexpr int KCH = MfmaTile<D>::KCH, VB = MfmaTile<D>::VB;
+  static_assert(NS == 2 || NS == 3, "stages");
+  using S = Stage<D>;
+  constexpr int KCH = D / 64;  // 16-byte K chunks per lane per block
+  constexpr int VB = D / 16;   // V bytes per lane per token row
   constexpr int NQK = D / 32;  // 16x16x32 MFMAs per block for S^T
   constexpr int NPV = D / 16;  // 16x16x16 MFMAs per block for O^T
 
-  __shared__ Shared<G, D> sh;
+  // One __shared__ object per stage: the compiler tracks outstanding LDS-DMA
+  // writes per object, so reading stage s waits only for stage s's loads.
+  __shared__ __attribute__((aligned(16))) char lds0[stage0_bytes<D, G>()];
+  __shared__ __attribute__((aligned(16))) char lds1[kWaves * S::kBytes];
+  __shared__ __attribute__((aligned(16))) char lds2[NS == 3 ? kWaves * S::kBytes : 16];
   const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   const int r = lane & 15, qg = lane >> 4;
+  const bool gvalid = r < G;
+
+  // ---- prologue: query rows and (for window == 0) this wave's block ids do not
+  // depend on the context length, so their loads issue together with it.
+  uint4 qraw[KCH][2];
+  {
+    const QT* qp = static_cast<const QT*>(a.q) + seq * a.q_tok +
+                   (int64_t)(kvh * G + (gvalid ? r : 0)) * a.q_head + 16 * qg;
+#pragma unroll
+    for (int h = 0; h < KCH; ++h) {
+      const uint4* src = reinterpret_cast<const uint4*>(qp + 64 * h);
+      qraw[h][0] = src[0];
+      qraw[h][1] = src[1];
+    }
+  }
+  const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
+  const int per_wave = (a.part_blocks + kWaves - 1) / kWaves;
+  int spec = part * a.part_blocks + wave + kWaves * lane;  // block index if kv_begin == 0
+  int ids = (a.window == 0 && lane < per_wave && spec < a.bt_stride) ? bt[spec] : 0;
   const RowPlan row = plan_row(a, seq, part == 0 && kvh == 0 && threadIdx.x == 0);
   if (part >= row.num_parts) return;
   const int pb0 = row.first_blk + part * a.part_blocks;
   const int pb1 = min(row.last_blk, pb0 + a.part_blocks);
   const int first = pb0 + wave;
   const int nbw = first < pb1 ? (pb1 - first + kWaves - 1) / kWaves : 0;
-  const bool gvalid = r < G;
+  if (row.first_blk != 0) ids = lane < nbw ? bt[first + kWaves * lane] : 0;
+  // One bad block id poisons the partition: flag it and stage nothing, so the
+  // stage/wait bookkeeping below never sees a skipped load.
+  const bool bad_index = __ballot(lane < nbw && (unsigned)ids >= (unsigned)a.cache.num_blocks) != 0;
+  const int nblk = bad_index ? 0 : nbw;
 
-  // ---- query operand: lane holds Q[g = r][d] for d in 16*qg + 64*h + [0, 16)
+  char* const st0 = lds0 + wave * S::kBytes;
+  char* const st1 = lds1 + wave * S::kBytes;
+  char* const st2 = lds2 + (NS == 3 ? wave * S::kBytes : 0);
+  if (0 < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, 0), kvh, lane, st0);
+  if (1 < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, 1), kvh, lane, st1);
+  if (NS == 3 && 2 < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, 2), kvh, lane, st2);
+
+  // ---- query operand: lane holds Q[g = r][d] for d in 16*qg + 64*h + [0, 16), as
+  // f16 after an exact 2^-e rescale keeping max|q| < 2^15 (e folded into cf)
   half8_t qop[NQK];
-  float cf;  // score factor: softmax scale * log2(e) * 2^e
+  float cf;
   {
     float qv[KCH][16];
-    const QT* qp = static_cast<const QT*>(a.q) + seq * a.q_tok +
-                   (int64_t)(kvh * G + (gvalid ? r : 0)) * a.q_head + 16 * qg;
     float mx = 0.f;
 #pragma unroll
     for (int h = 0; h < KCH; ++h) {
-      const uint4* src = reinterpret_cast<const uint4*>(qp + 64 * h);
-      const uint4 w0 = src[0], w1 = src[1];
-      const QT* e0 = reinterpret_cast<const QT*>(&w0);
-      const QT* e1 = reinterpret_cast<const QT*>(&w1);
+      const QT* e0 = reinterpret_cast<const QT*>(&qraw[h][0]);
+      const QT* e1 = reinterpret_cast<const QT*>(&qraw[h][1]);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         qv[h][i] = gvalid ? to_float<QT>(e0[i]) : 0.f;
@@ -275,29 +352,51 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
   for (int n = 0; n < NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
   float m = gvalid ? -INFINITY : 0.f;  // invalid head columns never contribute
   float l = 0.f;
+  bool bad_score = false;
 
-  const int ids = wave_block_ids(a, seq, first, nbw, lane);
-  bool bad_index = false, bad_score = false;
-  // fetch block i of this wave into t; false (and nothing loaded) for a bad id
-  auto fetch = [&](int i, MfmaTile<D>& t) -> bool {
-    const int phys = __builtin_amdgcn_readlane(ids, i);
-    const bool ok = (unsigned)phys < (unsigned)a.cache.num_blocks;
-    if (ok) load_mfma_tile<D>(a, phys, kvh, r, qg, t);
-    return ok;
-  };
-  auto process = [&](int i, const MfmaTile<D>& cur) {
-    // ---- S^T = K . Q^T
+  auto step = [&](int i, char* st) {
+    // wait until block i has landed: later stages (up to NS-1) may stay in flight
+    const int later = min(NS - 1, nblk - 1 - i);
+    if (later >= 3) wait_vmcnt<3 * S::kLoads>();
+    else if (later == 2) wait_vmcnt<2 * S::kLoads>();
+    else if (later == 1) wait_vmcnt<S::kLoads>();
+    else wait_vmcnt<0>();
+
+    // ---- S^T = K . Q^T (A = K rows from LDS)
     float4_t s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < NQK; ++kk) {
-      const uint4 c = cur.k[kk / 2];
-      const uint32_t w0 = (kk % 2) ? c.z : c.x, w1 = (kk % 2) ? c.w : c.y;
-      half2_t p0, p1, p2, p3;
-      codes_to_f16(w0, p0, p1);
-      codes_to_f16(w1, p2, p3);
-      const half8_t kop = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-      s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[kk], s4, 0, 0, 0);
+    for (int h = 0; h < KCH; ++h) {
+      const uint4 c = *reinterpret_cast<const uint4*>(st + S::kK + r * D + 16 * qg + 64 * h);
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        half2_t p0, p1, p2, p3;
+        codes_to_f16(sub ? c.z : c.x, p0, p1);
+        codes_to_f16(sub ? c.w : c.y, p2, p3);
+        const half8_t kop = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+        s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[2 * h + sub], s4, 0, 0, 0);
+      }
     }
+    const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
+    const float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg);
+    uint32_t vw[4][VB / 4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const char* rowp = st + S::kV + (4 * qg + j) * D + r * VB;
+      if constexpr (VB == 4) {
+        vw[j][0] = *reinterpret_cast<const uint32_t*>(rowp);
+      } else if constexpr (VB == 8) {
+        const uint2 w = *reinterpret_cast<const uint2*>(rowp);
+        vw[j][0] = w.x;
+        vw[j][1] = w.y;
+      } else {
+        const uint4 w = *reinterpret_cast<const uint4*>(rowp);
+        vw[j][0] = w.x;
+        vw[j][1] = w.y;
+        vw[j][2] = w.z;
+        vw[j][3] = w.w;
+      }
+    }
+
     // ---- scores of tokens 4*qg + j for head g = r (base-2, dequantised)
     const int blk = first + kWaves * i;
     const int tok0 = blk * kBlockTokens + 4 * qg;
@@ -306,7 +405,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     bool need = false, nonfinite = false;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float v = s4[j] * (cur.ks[j] * cf);
+      float v = s4[j] * (ks[j] * cf);
       bool valid = gvalid;
       if (edge) valid = valid && tok0 + j >= row.kv_begin && tok0 + j < row.ctx;
       nonfinite |= valid && !__builtin_isfinite(v);
@@ -331,50 +430,42 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     for (int j = 0; j < 4; ++j) {
       const float p = __builtin_amdgcn_exp2f(sc[j] - m);
       l += p;
-      pop[j] = (_Float16)(p * cur.vs[j]);
+      pop[j] = (_Float16)(p * vs[j]);
     }
     // ---- O^T += V^T . P^T (row m of MFMA n is d = VB*m + n)
 #pragma unroll
     for (int n = 0; n < NPV; ++n) {
-      half2_t a01, a23;
+      const uint32_t col[4] = {vw[0][n / 4], vw[1][n / 4], vw[2][n / 4], vw[3][n / 4]};
+      half4_t vop;
       switch (n % 4) {
-        case 0:
-          a01 = column_pair<0>(cur.v[0][n / 4], cur.v[1][n / 4]);
-          a23 = column_pair<0>(cur.v[2][n / 4], cur.v[3][n / 4]);
-          break;
-        case 1:
-          a01 = column_pair<1>(cur.v[0][n / 4], cur.v[1][n / 4]);
-          a23 = column_pair<1>(cur.v[2][n / 4], cur.v[3][n / 4]);
-          break;
-        case 2:
-          a01 = column_pair<2>(cur.v[0][n / 4], cur.v[1][n / 4]);
-          a23 = column_pair<2>(cur.v[2][n / 4], cur.v[3][n / 4]);
-          break;
-        default:
-          a01 = column_pair<3>(cur.v[0][n / 4], cur.v[1][n / 4]);
-          a23 = column_pair<3>(cur.v[2][n / 4], cur.v[3][n / 4]);
-          break;
+        case 0: vop = v_operand<0>(col); break;
+        case 1: vop = v_operand<1>(col); break;
+        case 2: vop = v_operand<2>(col); break;
+        default: vop = v_operand<3>(col); break;
       }
-      const half4_t vop = {a01[0], a01[1], a23[0], a23[1]};
       acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop, pop, acc[n], 0, 0, 0);
     }
+    // refill this stage with block i + NS (its LDS reads above have completed:
+    // their values fed the MFMAs)
+    if (i + NS < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, i + NS), kvh, lane, st);
   };
-  // Two tiles in fixed registers (ping-pong): block i+1 loads while block i runs.
-  MfmaTile<D> t0, t1;
-  bool ok0 = nbw > 0 ? fetch(0, t0) : false, ok1 = false;
-  for (int i = 0; i < nbw; i += 2) {
-    if (i + 1 < nbw) ok1 = fetch(i + 1, t1);
-    if (ok0) process(i, t0); else bad_index = true;
-    if (i + 1 >= nbw) break;
-    if (i + 2 < nbw) ok0 = fetch(i + 2, t0);
-    if (ok1) process(i + 1, t1); else bad_index = true;
+  for (int i = 0; i < nblk; i += NS) {
+    step(i, st0);
+    if (i + 1 >= nblk) break;
+    step(i + 1, st1);
+    if constexpr (NS == 3) {
+      if (i + 2 >= nblk) break;
+      step(i + 2, st2);
+    }
   }
   if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
   if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
 
-  // ---- per-wave state to LDS: lane (qg, r<G) holds O[g=r][d = VB*(4*qg + j) + n]
+  // ---- per-wave state to LDS (aliases the stages: wait for every wave first)
   l += shfl_xor(l, 16);
   l += shfl_xor(l, 32);
+  __syncthreads();
+  Shared<G, D>& sh = *reinterpret_cast<Shared<G, D>*>(lds0);
   if (gvalid) {
     if (qg == 0) {
       sh.m[wave][r] = m;
@@ -633,7 +724,8 @@ int launch_decode(const DecodeArgs& a, hipStream_t stream) {
   if constexpr (sizeof(QT) == 4) {
     hipLaunchKernelGGL((decode_valu_kernel<QT, D, G>), grid, dim3(kWaves * kWave), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((decode_mfma_kernel<QT, D, G>), grid, dim3(kWaves * kWave), 0, stream, a);
+    hipLaunchKernelGGL((decode_mfma_kernel<QT, D, G, kStages>), grid, dim3(kWaves * kWave), 0,
+                       stream, a);
   }
   if (a.max_parts > 1) {
     const int units = a.num_seqs * a.num_q_heads;
