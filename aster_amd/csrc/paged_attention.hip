@@ -300,7 +300,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
   const int pb1 = min(row.last_blk, pb0 + a.part_blocks);
   const int first = pb0 + wave;
   const int nbw = first < pb1 ? (pb1 - first + kWaves - 1) / kWaves : 0;
-  if (row.first_blk != 0) ids = lane < nbw ? bt[first + kWaves * lane] : 0;
+  if (a.window != 0) ids = lane < nbw ? bt[first + kWaves * lane] : 0;
   // One bad block id poisons the partition: flag it and stage nothing, so the
   // stage/wait bookkeeping below never sees a skipped load.
   const bool bad_index = __ballot(lane < nbw && (unsigned)ids >= (unsigned)a.cache.num_blocks) != 0;
@@ -697,14 +697,24 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
     lw += shfl_xor(lw, 32);
     L += lw;
     const int np = min(kWave, row.num_parts - p0);
-    for (int q = 0; q < np; ++q) {
-      const float wq = __shfl(w, q, kWave);
-      const float* op = a.ws_o + (base + p0 + q) * D;
+    // 8 partitions per round: all their loads issue before the first use
+    for (int q0 = 0; q0 < np; q0 += 8) {
+      float v[8][kPerLane], wq[8];
 #pragma unroll
-      for (int e = 0; e < kPerLane; ++e) {
-        const int d = lane + e * kWave;
-        if (d < D) O[e] = fmaf(op[d], wq, O[e]);
+      for (int u = 0; u < 8; ++u) {
+        const int q = min(q0 + u, np - 1);
+        wq[u] = q0 + u < np ? __shfl(w, q, kWave) : 0.f;
+        const float* op = a.ws_o + (base + p0 + q) * D;
+#pragma unroll
+        for (int e = 0; e < kPerLane; ++e) {
+          const int d = lane + e * kWave;
+          v[u][e] = d < D ? op[d] : 0.f;
+        }
       }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int e = 0; e < kPerLane; ++e) O[e] = fmaf(v[u][e], wq[u], O[e]);
     }
   }
   QT* out = static_cast<QT*>(a.out) + seq * a.o_tok + (int64_t)h * a.o_head;

@@ -34,7 +34,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--config", default="config2", choices=["config2", "config4", "config5"])
     p.add_argument("--layers", type=int, default=4)
-    p.add_argument("--partition", type=int, default=512)
+    p.add_argument("--partition", type=int, default=1024)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
