@@ -85,7 +85,7 @@ def lib():
             c_i32, c_i32, ctypes.c_float, c_i32, c_i32, c_vp, c_sz, c_vp, c_vp,
         ]
         handle.astr_paged_attention_i8.restype = ctypes.c_int
-        handle.astr_paged_attention_i8_workspace_bytes.argtypes = [c_i32] * 5
+        handle.astr_paged_attention_i8_workspace_bytes.argtypes = [c_i32] * 6
         handle.astr_paged_attention_i8_workspace_bytes.restype = c_sz
         handle.astr_last_error.argtypes = []
         handle.astr_last_error.restype = ctypes.c_char_p

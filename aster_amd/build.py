@@ -17,7 +17,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_lib")
 OUT = os.path.join(OUT_DIR, "libaster_kv.so")
-SOURCES = ("errors.hip", "kv_quantize.hip", "paged_attention.hip")
+SOURCES = ("errors.hip", "kv_quantize.hip", "paged_attention.hip", "decode_partition.hip",
+           "decode_streamk.hip")
 ARCH = "gfx950"
 
 FLAGS = [

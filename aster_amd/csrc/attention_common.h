@@ -1,0 +1,336 @@
+// Building blocks shared by the paged decode attention kernels (gfx950):
+// launch arguments, the LDS block stage filled by direct global->LDS loads,
+// exact int8 -> f16 operand conversion, the query operand and the per-block
+// MFMA step (scores, online softmax, P.V).
+#pragma once
+
+#include <cfloat>
+#include <cmath>
+
+#include "common.h"
+
+namespace astr {
+namespace attn {
+
+constexpr int kBlockTokens = 16;
+constexpr int kWaves = 4;              // waves per workgroup
+constexpr int kMaxBlocksPerWave = 64;  // block ids one wave keeps in a register
+constexpr float kRescaleSlack = 8.0f;  // p = exp2(s - m) <= 2^8 between rescales
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+struct DecodeArgs {
+  const void* q;
+  int64_t q_tok, q_head;
+  void* out;
+  int64_t o_tok, o_head;
+  astr_paged_kv cache;
+  const int32_t* block_tables;
+  int32_t bt_stride;
+  const int32_t* context_lens;
+  int32_t num_seqs, num_q_heads;
+  float qk_scale_log2;  // softmax scale * log2(e)
+  int32_t window;
+  // fixed-size split-K partitions
+  int32_t part_blocks;  // blocks per partition
+  int32_t max_parts;
+  // stream-K: equal contiguous block ranges per wave. The entry point passes the
+  // workspace capacity in total_waves and the minimum in min_waves; the launcher
+  // settles total_waves from the kernel's occupancy.
+  int32_t total_waves;
+  int32_t min_waves;
+  float* ws_o;          // partial acc (layout depends on the split mode)
+  float* ws_ml;         // partial (m, l)
+  int32_t* ws_seq;      // stream-K: per-sequence block prefix [num_seqs + 1]
+  int32_t* err_flag;
+};
+
+// Visible key range of a decode row: tokens [kv_begin, ctx), blocks [first, last).
+struct RowSpan {
+  int ctx, kv_begin, first_blk, last_blk;
+};
+
+__device__ __forceinline__ int clamp_ctx(const DecodeArgs& a, int ctx, bool report) {
+  const int cap = a.bt_stride * kBlockTokens;
+  if (ctx < 0 || ctx > cap) {
+    if (report) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+    ctx = ctx < 0 ? 0 : cap;
+  }
+  return ctx;
+}
+
+__device__ __forceinline__ RowSpan row_span(const DecodeArgs& a, int ctx) {
+  RowSpan r;
+  r.ctx = ctx;
+  r.kv_begin = (a.window > 0 && ctx > a.window) ? ctx - a.window : 0;
+  r.first_blk = r.kv_begin / kBlockTokens;
+  r.last_blk = (ctx + kBlockTokens - 1) / kBlockTokens;
+  return r;
+}
+
+// ---- LDS stage of one 16-token block of one kv head, as it sits in HBM:
+// K codes (16 rows x D bytes), V codes, then 16 K and 16 V fp32 scales.
+template <int D>
+struct Stage {
+  static constexpr int kK = 0;
+  static constexpr int kV = 16 * D;
+  static constexpr int kS = 32 * D;
+  static constexpr int kBytes = 32 * D + 128;
+  static constexpr int kCodeLoads = 16 * D / 1024;   // 1 KiB wave-loads per K (and per V) tile
+  static constexpr int kLoads = 2 * kCodeLoads + 1;  // vector-memory instructions per stage
+};
+
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+// Byte address of an LDS location, as M0 expects it.
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return (uint32_t)(uintptr_t)(const lds_char_t*)p;
+}
+
+// Direct global -> LDS loads. Each lane's 16 (or 4) bytes land at
+// M0 + lane * 16 (or 4). Issued as inline asm so the compiler does not add its
+// conservative "wait for every LDS DMA" before unrelated LDS reads; the stage
+// pipelines wait for exactly the loads they need with wait_vmcnt. M0 is a
+// reserved register the compiler sets right before each of its own uses (these
+// kernels have none besides this), so it is not listed as clobbered.
+__device__ __forceinline__ void lds_dma_x4(const void* gptr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(gptr)
+               : "memory");
+}
+
+__device__ __forceinline__ void lds_dma_x1(const void* gptr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(lds), "v"(gptr)
+               : "memory");
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// Issue the direct-to-LDS loads of block `phys` (kv head kvh) into stage `st`:
+// exactly Stage<D>::kLoads vector-memory instructions (waves are always full,
+// so the 32-lane scale load always issues).
+template <int D>
+__device__ __forceinline__ void stage_block(const DecodeArgs& a, int phys, int kvh, int lane,
+                                            char* st) {
+  using S = Stage<D>;
+  const int64_t off = (int64_t)phys * a.cache.code_block_stride +
+                      (int64_t)kvh * a.cache.code_head_stride + lane * 16;
+  const uint32_t base = lds_addr(st);
+#pragma unroll
+  for (int j = 0; j < S::kCodeLoads; ++j)
+    lds_dma_x4(a.cache.k_codes + off + j * 1024, base + S::kK + j * 1024);
+#pragma unroll
+  for (int j = 0; j < S::kCodeLoads; ++j)
+    lds_dma_x4(a.cache.v_codes + off + j * 1024, base + S::kV + j * 1024);
+  const int64_t so = (int64_t)phys * a.cache.scale_block_stride +
+                     (int64_t)kvh * a.cache.scale_head_stride;
+  if (lane < 32) {
+    const float* src = lane < 16 ? a.cache.k_scales + so + lane : a.cache.v_scales + so + lane - 16;
+    lds_dma_x1(src, base + S::kS);
+  }
+}
+
+// ---- exact int8 -> f16 operands
+
+// 4 int8 codes -> two f16 pairs holding exactly the codes: a byte permute builds
+// 0x64xx halves (1024 + u) with u = c + 128, then 1152 is subtracted.
+__device__ __forceinline__ void codes_to_f16(uint32_t w, half2_t& lo, half2_t& hi) {
+  const uint32_t u = w ^ 0x80808080u;                                      // bytes c + 128
+  const uint32_t l = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // 1024 + u0, 1024 + u1
+  const uint32_t h = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // 1024 + u2, 1024 + u3
+  const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  lo = __builtin_bit_cast(half2_t, l) - bias;
+  hi = __builtin_bit_cast(half2_t, h) - bias;
+}
+
+// Byte k of rows r0/r1 -> f16 pair (code[r0][k], code[r1][k]).
+template <int K>
+__device__ __forceinline__ half2_t column_pair(uint32_t r0, uint32_t r1) {
+  constexpr uint32_t sel = 0x0C000C00u | ((4u + K) << 16) | K;
+  const uint32_t p = __builtin_amdgcn_perm(r1, r0, sel) ^ 0x64806480u;  // 1152 + c
+  const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  return __builtin_bit_cast(half2_t, p) - bias;
+}
+
+template <int K>
+__device__ __forceinline__ half4_t v_operand(const uint32_t (&v)[4]) {
+  const half2_t a01 = column_pair<K>(v[0], v[1]);
+  const half2_t a23 = column_pair<K>(v[2], v[3]);
+  return half4_t{a01[0], a01[1], a23[0], a23[1]};
+}
+
+// ---- query operand: lane (qg = lane/16, r = lane%16) holds Q[g = r][d] for
+// d in 16*qg + 64*h + [0, 16), h < D/64 (rows r >= G are zero).
+
+template <int D>
+struct QueryRaw {
+  uint4 w[D / 64][2];
+};
+
+template <typename QT, int D, int G>
+__device__ __forceinline__ void load_query(const DecodeArgs& a, int seq, int kvh, int r, int qg,
+                                           QueryRaw<D>& q) {
+  const QT* qp = static_cast<const QT*>(a.q) + seq * a.q_tok +
+                 (int64_t)(kvh * G + (r < G ? r : 0)) * a.q_head + 16 * qg;
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h) {
+    const uint4* src = reinterpret_cast<const uint4*>(qp + 64 * h);
+    q.w[h][0] = src[0];
+    q.w[h][1] = src[1];
+  }
+}
+
+// f16 B-operands of the QK MFMAs after an exact 2^-e rescale keeping max|q| below
+// 2^15 (e folded into the returned score factor). Cross-lane: call in uniform
+// control flow.
+template <typename QT, int D>
+__device__ __forceinline__ float query_operand(const QueryRaw<D>& q, bool gvalid,
+                                               float qk_scale_log2, half8_t (&qop)[D / 32]) {
+  // two passes over the raw words (max, then convert) keep the live set small
+  float mx = 0.f;
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const QT* e = reinterpret_cast<const QT*>(&q.w[h][c]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(to_float<QT>(e[i])));
+    }
+  mx = gvalid ? mx : 0.f;
+  mx = fmaxf(mx, shfl_xor(mx, 16));
+  mx = fmaxf(mx, shfl_xor(mx, 32));
+  int ex = 0;
+  if (mx >= 32768.f) {
+    frexpf(mx, &ex);
+    ex -= 15;  // mx * 2^-ex < 2^15
+  }
+  const float down = ldexpf(1.f, -ex);
+#pragma unroll
+  for (int kk = 0; kk < D / 32; ++kk) {
+    const QT* e = reinterpret_cast<const QT*>(&q.w[kk / 2][kk % 2]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      qop[kk][i] = gvalid ? (_Float16)(to_float<QT>(e[i]) * down) : (_Float16)0.f;
+  }
+  return qk_scale_log2 * ldexpf(1.f, ex);
+}
+
+// ---- one staged 16-token block through the MFMAs
+//   S^T[t][g] = K[t][:] . Q[g][:]     4 (D/32) x v_mfma_f32_16x16x32_f16
+//   O^T[d][g] += V^T[d][t] P^T[t][g]  8 (D/16) x v_mfma_f32_16x16x16_f16
+// The S^T output layout (lane l: tokens 4*(l/16)+j of head l%16) is the B-operand
+// layout P^T needs, so the online softmax stays in registers. Tokens outside
+// [kv_begin, ctx) are masked; `tok_base` is the block's first token position.
+// Cross-lane (ballots, shuffles): call in uniform control flow.
+template <int D, int G>
+__device__ __forceinline__ void mfma_block(const char* st, const half8_t (&qop)[D / 32], float cf,
+                                           int tok_base, int kv_begin, int ctx, int r, int qg,
+                                           float4_t (&acc)[D / 16], float& m, float& l,
+                                           bool& bad_score) {
+  using S = Stage<D>;
+  constexpr int KCH = D / 64;
+  constexpr int VB = D / 16;
+  constexpr int NPV = D / 16;
+  const bool gvalid = r < G;
+  float4_t s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < KCH; ++h) {
+    const uint4 c = *reinterpret_cast<const uint4*>(st + S::kK + r * D + 16 * qg + 64 * h);
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      half2_t p0, p1, p2, p3;
+      codes_to_f16(sub ? c.z : c.x, p0, p1);
+      codes_to_f16(sub ? c.w : c.y, p2, p3);
+      const half8_t kop = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+      s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[2 * h + sub], s4, 0, 0, 0);
+    }
+  }
+  const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
+  const float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg);
+  uint32_t vw[4][VB / 4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const char* rowp = st + S::kV + (4 * qg + j) * D + r * VB;
+    if constexpr (VB == 4) {
+      vw[j][0] = *reinterpret_cast<const uint32_t*>(rowp);
+    } else if constexpr (VB == 8) {
+      const uint2 w = *reinterpret_cast<const uint2*>(rowp);
+      vw[j][0] = w.x;
+      vw[j][1] = w.y;
+    } else {
+      const uint4 w = *reinterpret_cast<const uint4*>(rowp);
+      vw[j][0] = w.x;
+      vw[j][1] = w.y;
+      vw[j][2] = w.z;
+      vw[j][3] = w.w;
+    }
+  }
+  // scores of tokens 4*qg + j for head g = r (base 2, dequantised)
+  const int tok0 = tok_base + 4 * qg;
+  const bool edge = tok_base < kv_begin || tok_base + kBlockTokens > ctx;
+  float sc[4];
+  bool need = false, nonfinite = false;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float v = s4[j] * (ks[j] * cf);
+    bool valid = gvalid;
+    if (edge) valid = valid && tok0 + j >= kv_begin && tok0 + j < ctx;
+    nonfinite |= valid && !__builtin_isfinite(v);
+    v = valid ? v : -INFINITY;
+    need |= v > m + kRescaleSlack;
+    sc[j] = v;
+  }
+  if (__ballot(nonfinite) != 0) bad_score = true;
+  if (__ballot(need) != 0) {
+    float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    tmax = fmaxf(tmax, shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, shfl_xor(tmax, 32));
+    const float mn = fmaxf(m, tmax);
+    const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+    l *= alpha;
+#pragma unroll
+    for (int n = 0; n < NPV; ++n) acc[n] *= alpha;
+    m = mn;
+  }
+  half4_t pop;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float p = __builtin_amdgcn_exp2f(sc[j] - m);
+    l += p;
+    pop[j] = (_Float16)(p * vs[j]);
+  }
+  // O^T += V^T . P^T (row m of MFMA n is d = VB*m + n)
+#pragma unroll
+  for (int n = 0; n < NPV; ++n) {
+    const uint32_t col[4] = {vw[0][n / 4], vw[1][n / 4], vw[2][n / 4], vw[3][n / 4]};
+    half4_t vop;
+    switch (n % 4) {
+      case 0: vop = v_operand<0>(col); break;
+      case 1: vop = v_operand<1>(col); break;
+      case 2: vop = v_operand<2>(col); break;
+      default: vop = v_operand<3>(col); break;
+    }
+    acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop, pop, acc[n], 0, 0, 0);
+  }
+}
+
+// Kernel entry points (one per translation unit), dispatched on query dtype,
+// head dim and GQA group inside.
+int launch_partitioned(const DecodeArgs& a, int32_t q_dtype, hipStream_t stream);
+int launch_streamk(const DecodeArgs& a, int32_t q_dtype, hipStream_t stream);
+// Largest batch the stream-K kernel takes (its per-sequence table lives in LDS).
+int stream_k_max_seqs();
+
+}  // namespace attn
+}  // namespace astr

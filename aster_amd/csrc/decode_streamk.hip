@@ -1,0 +1,369 @@
+// Stream-K paged decode attention (gfx950, bf16/fp16 queries).
+//
+// The visible 16-token blocks of all (kv head, sequence) rows are laid end to
+// end (kv-head major, then sequence, then block) and cut into equal contiguous
+// ranges, one per wave of a grid sized to the GPU's resident waves. Every wave
+// therefore streams the same number of blocks (no partially filled last round,
+// whatever the context lengths), through a per-wave LDS ring of blocks filled
+// by direct global->LDS loads and the MFMA step of attention_common.h. Where a
+// range begins or ends inside a row, the wave writes a partial (m, l, acc) for
+// that piece; rows a single wave covers entirely are normalised and written
+// directly. A wave owns at most two partial slots (its first and its last
+// piece), and merge_streamk_kernel combines the pieces of every split row with
+// the merge_softmax rule (online_attention.py:42-63).
+#include "attention_common.h"
+
+namespace astr {
+namespace attn {
+namespace {
+
+constexpr int kStagesSK = 2;
+constexpr int kMaxSeqsSK = 512;  // per-sequence table lives in LDS
+
+// Wave owning flat block b when wave w owns [floor(B*w/W), floor(B*(w+1)/W)).
+__device__ __forceinline__ int64_t wave_of(int64_t b, int64_t B, int64_t W) {
+  return ((b + 1) * W - 1) / B;
+}
+
+template <typename QT>
+__device__ __forceinline__ void store_row_zero(const DecodeArgs& a, int seq, int D) {
+  QT* orow = static_cast<QT*>(a.out) + seq * a.o_tok;
+  for (int idx = threadIdx.x; idx < a.num_q_heads * D; idx += blockDim.x)
+    orow[(int64_t)(idx / D) * a.o_head + idx % D] = from_float<QT>(0.f);
+}
+
+template <typename QT, int D, int G, int NS>
+__global__ __launch_bounds__(256) void decode_streamk_kernel(DecodeArgs a) {
+  static_assert(D == 64 || D == 128 || D == 256, "head_dim");
+  static_assert(G >= 1 && G <= 16, "GQA group");
+  static_assert(NS == 2 || NS == 3, "stages");
+  using S = Stage<D>;
+  constexpr int NPV = D / 16;
+  constexpr int VB = D / 16;
+
+  __shared__ __attribute__((aligned(16))) char lds0[kWaves * S::kBytes];
+  __shared__ __attribute__((aligned(16))) char lds1[kWaves * S::kBytes];
+  __shared__ __attribute__((aligned(16))) char lds2[NS == 3 ? kWaves * S::kBytes : 16];
+  __shared__ int s_ctx[kMaxSeqsSK];
+  __shared__ int s_cu[kMaxSeqsSK + 1];
+  __shared__ int s_wsum[kWaves];
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int r = lane & 15, qg = lane >> 4;
+  const bool gvalid = r < G;
+  const int nseq = a.num_seqs;
+  const int hkv = a.cache.num_kv_heads;
+
+  // ---- 1. visible blocks per sequence -> exclusive prefix s_cu (thread t owns 2t, 2t+1)
+  int nb[2] = {0, 0};
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int s = 2 * threadIdx.x + k;
+    if (s < nseq) {
+      const int ctx = clamp_ctx(a, a.context_lens[s], blockIdx.x == 0);
+      s_ctx[s] = ctx;
+      const RowSpan sp = row_span(a, ctx);
+      nb[k] = sp.last_blk - sp.first_blk;
+    }
+  }
+  const int local = nb[0] + nb[1];
+  int incl = local;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int v = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += v;
+  }
+  if (lane == kWave - 1) s_wsum[wave] = incl;
+  __syncthreads();
+  int wbase = 0;
+  for (int w = 0; w < wave; ++w) wbase += s_wsum[w];
+  const int excl = wbase + incl - local;
+  if (2 * (int)threadIdx.x < nseq) s_cu[2 * threadIdx.x] = excl;
+  if (2 * (int)threadIdx.x + 1 < nseq) s_cu[2 * threadIdx.x + 1] = excl + nb[0];
+  const int bseq = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+  if (threadIdx.x == 0) s_cu[nseq] = bseq;
+  __syncthreads();
+  if (blockIdx.x == 0)
+    for (int s = threadIdx.x; s <= nseq; s += blockDim.x) a.ws_seq[s] = s_cu[s];
+  // rows with nothing visible (ctx == 0) are zero (online_attention.py:37)
+  for (int s = blockIdx.x; s < nseq; s += gridDim.x)
+    if (s_cu[s + 1] == s_cu[s]) store_row_zero<QT>(a, s, D);
+
+  // ---- 2. this wave's block range and its block ids / rows (lane j <-> block b0 + j)
+  const int64_t B = (int64_t)bseq * hkv;
+  const int64_t W = a.total_waves;
+  const int64_t gw = (int64_t)blockIdx.x * kWaves + wave;
+  const int64_t b0 = B * gw / W;
+  int n = (int)(B * (gw + 1) / W - b0);
+  const bool too_long = n > kMaxBlocksPerWave;  // contexts beyond the declared maximum
+  if (too_long) n = kMaxBlocksPerWave;
+  int row_id = 0, ids = 0;  // row id = kv_head * nseq + seq
+  if (lane < n) {
+    const int64_t b = b0 + lane;
+    const int kv = (int)(b / bseq);
+    const int rem = (int)(b - (int64_t)kv * bseq);
+    int lo = 0, hi = nseq;  // s_cu[lo] <= rem < s_cu[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_cu[mid] <= rem) lo = mid;
+      else hi = mid;
+    }
+    const RowSpan sp = row_span(a, s_ctx[lo]);
+    ids = a.block_tables[(int64_t)lo * a.bt_stride + sp.first_blk + rem - s_cu[lo]];
+    row_id = kv * nseq + lo;
+  }
+  // first row's query: issued with the block ids, converted before any staging
+  QueryRaw<D> qr;
+  const int row0 = __builtin_amdgcn_readfirstlane(row_id);
+  if (n > 0) load_query<QT, D, G>(a, row0 % nseq, row0 / nseq, r, qg, qr);
+  const bool bad_index =
+      too_long || __ballot(lane < n && (unsigned)ids >= (unsigned)a.cache.num_blocks) != 0;
+  const int nblk = bad_index ? 0 : n;
+
+  half8_t qop[D / 32];
+  float cf = 0.f;
+  if (nblk > 0) cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop);
+
+  char* const st0 = lds0 + wave * S::kBytes;
+  char* const st1 = lds1 + wave * S::kBytes;
+  char* const st2 = lds2 + (NS == 3 ? wave * S::kBytes : 0);
+  auto issue = [&](int j, char* st) {
+    stage_block<D>(a, __builtin_amdgcn_readlane(ids, j),
+                   __builtin_amdgcn_readlane(row_id, j) / nseq, lane, st);
+  };
+  if (0 < nblk) issue(0, st0);
+  if (1 < nblk) issue(1, st1);
+  if (NS == 3 && 2 < nblk) issue(2, st2);
+
+  // ---- 3. stream the blocks, one piece (row) at a time
+  float4_t acc[NPV];
+#pragma unroll
+  for (int k = 0; k < NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m = gvalid ? -INFINITY : 0.f, l = 0.f;
+  bool bad_score = false;
+  int cur = row0, pstart = 0;
+  int pseq = row0 % nseq, pkvh = row0 / nseq;
+  RowSpan psp = row_span(a, nblk > 0 ? s_ctx[pseq] : 0);
+  int64_t pfb = (int64_t)pkvh * bseq + (nblk > 0 ? s_cu[pseq] : 0);  // flat first block of the row
+
+  auto flush = [&](int iend) {
+    float lt = l + shfl_xor(l, 16);
+    lt += shfl_xor(lt, 32);
+    const int64_t pfe = pfb + (s_cu[pseq + 1] - s_cu[pseq]) - 1;
+    if (b0 + pstart == pfb && b0 + iend == pfe) {
+      // the whole row is in this wave: final output
+      if (gvalid) {
+        const float inv = 1.f / fmaxf(lt, FLT_MIN);
+        QT* op = static_cast<QT*>(a.out) + pseq * a.o_tok + (int64_t)(pkvh * G + r) * a.o_head;
+#pragma unroll
+        for (int k = 0; k < NPV; ++k)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) op[VB * (4 * qg + j) + k] = from_float<QT>(acc[k][j] * inv);
+      }
+    } else if (gvalid) {
+      const int64_t slot = (gw * 2 + (pstart == 0 ? 0 : 1)) * G + r;
+      float* o = a.ws_o + slot * D;
+#pragma unroll
+      for (int k = 0; k < NPV; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[VB * (4 * qg + j) + k] = acc[k][j];
+      if (qg == 0) {
+        a.ws_ml[slot * 2] = m;
+        a.ws_ml[slot * 2 + 1] = lt;
+      }
+    }
+  };
+
+  auto step = [&](int i, char* st) {
+    const int rid = __builtin_amdgcn_readlane(row_id, i);
+    if (rid != cur) {  // a new row starts inside this wave's range
+      flush(i - 1);
+      cur = rid;
+      pseq = rid % nseq;
+      pkvh = rid / nseq;
+      pstart = i;
+      psp = row_span(a, s_ctx[pseq]);
+      pfb = (int64_t)pkvh * bseq + s_cu[pseq];
+      load_query<QT, D, G>(a, pseq, pkvh, r, qg, qr);
+      cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop);
+#pragma unroll
+      for (int k = 0; k < NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+      m = gvalid ? -INFINITY : 0.f;
+      l = 0.f;
+    }
+    const int later = min(NS - 1, nblk - 1 - i);
+    if (later >= 2) wait_vmcnt<2 * S::kLoads>();
+    else if (later == 1) wait_vmcnt<S::kLoads>();
+    else wait_vmcnt<0>();
+    const int blk = psp.first_blk + (int)(b0 + i - pfb);
+    mfma_block<D, G>(st, qop, cf, blk * kBlockTokens, psp.kv_begin, psp.ctx, r, qg, acc, m, l,
+                     bad_score);
+    if (i + NS < nblk) issue(i + NS, st);
+  };
+  for (int i = 0; i < nblk; i += NS) {
+    step(i, st0);
+    if (i + 1 >= nblk) break;
+    step(i + 1, st1);
+    if constexpr (NS == 3) {
+      if (i + 2 >= nblk) break;
+      step(i + 2, st2);
+    }
+  }
+  if (nblk > 0) flush(nblk - 1);
+  if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+  if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
+}
+
+// One wave per (sequence, q head): merge the pieces of rows split across waves.
+template <typename QT, int D>
+__global__ __launch_bounds__(256) void merge_streamk_kernel(DecodeArgs a) {
+  constexpr int kPerLane = (D + kWave - 1) / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int unit = blockIdx.x * kWaves + threadIdx.x / kWave;  // seq * Hq + h
+  if (unit >= a.num_seqs * a.num_q_heads) return;
+  const int seq = unit / a.num_q_heads, h = unit % a.num_q_heads;
+  const int G = a.num_q_heads / a.cache.num_kv_heads;
+  const int kvh = h / G, g = h % G;
+  const int cu0 = a.ws_seq[seq], cu1 = a.ws_seq[seq + 1], bseq = a.ws_seq[a.num_seqs];
+  if (cu1 == cu0) return;  // empty row: zeros written by the decode kernel
+  const int64_t B = (int64_t)bseq * a.cache.num_kv_heads, W = a.total_waves;
+  const int64_t fb = (int64_t)kvh * bseq + cu0, fe = fb + (cu1 - cu0) - 1;
+  const int64_t w0 = wave_of(fb, B, W), w1 = wave_of(fe, B, W);
+  if (w0 == w1) return;  // written whole by one wave
+  const int pieces = (int)(w1 - w0 + 1);
+  const bool first_is_tail = B * w0 / W < fb;  // the row is w0's last piece (slot 1)
+  auto slot_of = [&](int p) -> int64_t {
+    const int64_t w = w0 + p;
+    return (w * 2 + (p == 0 && first_is_tail ? 1 : 0)) * G + g;
+  };
+  float M = -INFINITY;
+  for (int p = lane; p < pieces; p += kWave) M = fmaxf(M, a.ws_ml[slot_of(p) * 2]);
+  M = wave_max(M);
+  float L = 0.f, O[kPerLane];
+#pragma unroll
+  for (int e = 0; e < kPerLane; ++e) O[e] = 0.f;
+  for (int p0 = 0; p0 < pieces; p0 += kWave) {
+    const int p = p0 + lane;
+    float w = 0.f, lw = 0.f;
+    if (p < pieces) {
+      const float mp = a.ws_ml[slot_of(p) * 2];
+      w = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
+      lw = a.ws_ml[slot_of(p) * 2 + 1] * w;
+    }
+    lw += shfl_xor(lw, 1);
+    lw += shfl_xor(lw, 2);
+    lw += shfl_xor(lw, 4);
+    lw += shfl_xor(lw, 8);
+    lw += shfl_xor(lw, 16);
+    lw += shfl_xor(lw, 32);
+    L += lw;
+    const int np = min(kWave, pieces - p0);
+    for (int q0 = 0; q0 < np; q0 += 8) {
+      float v[8][kPerLane], wq[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int q = min(q0 + u, np - 1);
+        wq[u] = q0 + u < np ? __shfl(w, q, kWave) : 0.f;
+        const float* op = a.ws_o + slot_of(p0 + q) * D;
+#pragma unroll
+        for (int e = 0; e < kPerLane; ++e) {
+          const int d = lane + e * kWave;
+          v[u][e] = d < D ? op[d] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int e = 0; e < kPerLane; ++e) O[e] = fmaf(v[u][e], wq[u], O[e]);
+    }
+  }
+  QT* out = static_cast<QT*>(a.out) + seq * a.o_tok + (int64_t)h * a.o_head;
+  const float inv_l = 1.f / fmaxf(L, FLT_MIN);
+#pragma unroll
+  for (int e = 0; e < kPerLane; ++e) {
+    const int d = lane + e * kWave;
+    if (d < D) out[d] = from_float<QT>(O[e] * inv_l);
+  }
+}
+
+// Workgroups of `kernel` one CU holds at once (queried once per kernel).
+template <typename Kernel>
+int resident_per_cu(Kernel kernel) {
+  static int cached = 0;
+  if (cached == 0) {
+    int n = 0;
+    cached = (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kWaves * kWave, 0) ==
+                  hipSuccess && n > 0)
+                 ? n
+                 : 1;
+  }
+  return cached;
+}
+
+int device_cus() {
+  int dev = 0, v = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+    return v;
+  return 256;
+}
+
+template <typename QT, int D, int G>
+int launch(DecodeArgs a, hipStream_t stream) {
+  auto kernel = decode_streamk_kernel<QT, D, G, kStagesSK>;
+  // one wave per resident slot (whole workgroups), at least min_waves, at most the
+  // workspace capacity passed in total_waves
+  int64_t waves = (int64_t)device_cus() * resident_per_cu(kernel) * kWaves;
+  if (waves < a.min_waves) waves = (a.min_waves + kWaves - 1) / kWaves * kWaves;
+  if (waves > a.total_waves) waves = a.total_waves / kWaves * kWaves;
+  a.total_waves = (int32_t)waves;
+  const int wgs = (int)(waves / kWaves);
+  hipLaunchKernelGGL(kernel, dim3(wgs), dim3(kWaves * kWave), 0, stream, a);
+  const int units = a.num_seqs * a.num_q_heads;
+  hipLaunchKernelGGL((merge_streamk_kernel<QT, D>), dim3((units + kWaves - 1) / kWaves),
+                     dim3(kWaves * kWave), 0, stream, a);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "paged_attention (stream-K) launch");
+}
+
+template <typename QT, int D>
+int dispatch_group(const DecodeArgs& a, int G, hipStream_t s) {
+  switch (G) {
+    case 1: return launch<QT, D, 1>(a, s);
+    case 2: return launch<QT, D, 2>(a, s);
+    case 4: return launch<QT, D, 4>(a, s);
+    case 8: return launch<QT, D, 8>(a, s);
+    case 16:
+      if constexpr (D <= 128) return launch<QT, D, 16>(a, s);
+      [[fallthrough]];
+    default:
+      return fail(ASTR_EUNSUPPORTED, "GQA group size %d not supported", G);
+  }
+}
+
+template <typename QT>
+int dispatch_dim(const DecodeArgs& a, int G, hipStream_t s) {
+  switch (a.cache.head_dim) {
+    case 64: return dispatch_group<QT, 64>(a, G, s);
+    case 128: return dispatch_group<QT, 128>(a, G, s);
+    case 256: return dispatch_group<QT, 256>(a, G, s);
+    default: return fail(ASTR_EUNSUPPORTED, "head_dim %d not in {64,128,256}", a.cache.head_dim);
+  }
+}
+
+}  // namespace
+
+int launch_streamk(const DecodeArgs& a, int32_t q_dtype, hipStream_t stream) {
+  if (a.min_waves > a.total_waves)
+    return fail(ASTR_EINVAL, "stream-K workspace too small for this launch");
+  const int G = a.num_q_heads / a.cache.num_kv_heads;
+  if (q_dtype == ASTR_F16) return dispatch_dim<_Float16>(a, G, stream);
+  if (q_dtype == ASTR_BF16) return dispatch_dim<bf16_t>(a, G, stream);
+  return fail(ASTR_EUNSUPPORTED, "stream-K decode takes bf16/fp16 queries");
+}
+
+int stream_k_max_seqs() { return kMaxSeqsSK; }
+
+}  // namespace attn
+}  // namespace astr

@@ -29,7 +29,7 @@ from . import _native
 from .attention_backend import BACKEND, KernelWork, UnsupportedAttentionBackend
 from .kv_quantization import KVQuantization, QuantizedKV, _DTYPE_CODES, require_int8
 
-DEFAULT_PARTITION_TOKENS = 512
+DEFAULT_PARTITION_TOKENS = 0  # automatic: stream-K for bf16/fp16, else 512-token partitions
 
 
 class PagedKVCache:
@@ -131,7 +131,8 @@ class PagedKVCache:
     def workspace_bytes(self, num_seqs, num_q_heads, max_context_len,
                         partition_tokens=DEFAULT_PARTITION_TOKENS):
         return int(_native.lib().astr_paged_attention_i8_workspace_bytes(
-            num_seqs, num_q_heads, self.head_dim, max_context_len, partition_tokens))
+            num_seqs, num_q_heads, self.num_kv_heads, self.head_dim, max_context_len,
+            partition_tokens))
 
     def workspace(self, num_seqs, num_q_heads, max_context_len,
                   partition_tokens=DEFAULT_PARTITION_TOKENS):

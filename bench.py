@@ -34,7 +34,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--config", default="config2", choices=["config2", "config4", "config5"])
     p.add_argument("--layers", type=int, default=4)
-    p.add_argument("--partition", type=int, default=1024)
+    p.add_argument("--partition", type=int, default=0,
+                   help="0 = automatic (stream-K); >0 = fixed split-K partition tokens")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
@@ -166,7 +167,8 @@ def main():
         },
         "hbm_fraction_of_step": alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "roofline": {
-            "kernel": "decode_mfma_kernel + merge_kernel (one paged_attention call)",
+            "kernel": ("decode_streamk_kernel + merge_streamk_kernel" if args.partition == 0 else
+                       "decode_mfma_kernel + merge_kernel") + " (one paged_attention call)",
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
             "algorithmic_bytes_per_launch": alg_bytes,

@@ -107,8 +107,11 @@ int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void* key, cons
  *              keys 0..ctx-1 (ctx-window..ctx-1 when window > 0).
  *   GQA: query head h reads kv head h / (num_q_heads / num_kv_heads).
  *   max_context_len: host-side upper bound of context_lens (sizes the split-K grid).
- *   partition_tokens: split-K partition (multiple of 64, at most 4096); 0
- *              selects 512.
+ *   partition_tokens: 0 = automatic: bf16/fp16 queries with at most 512
+ *              sequences use stream-K (equal block ranges per wave across
+ *              rows, partials merged afterwards), everything else 512-token
+ *              split-K partitions; > 0 forces fixed partitions of that many
+ *              tokens (a multiple of 64, at most 4096).
  *   workspace: >= astr_paged_attention_i8_workspace_bytes(...) bytes of
  *              scratch for split-K partials, 256-byte aligned (NULL allowed
  *              when that size is 0); no initialisation needed. Calls sharing
@@ -127,12 +130,13 @@ int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query, int32
                             int32_t* err_flag, void* stream);
 
 /*
- * Workspace bytes astr_paged_attention_i8 needs for its split-K partials
- * (0 when no row can span more than one partition).
+ * Workspace bytes astr_paged_attention_i8 needs for its split-K partials on
+ * the current device (0 when no row can span more than one partition).
  * Analogue of KernelSpec.workspace_bytes (src/aster/core/contracts.py:102-134).
  */
 size_t astr_paged_attention_i8_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
-                                               int32_t head_dim, int32_t max_context_len,
+                                               int32_t num_kv_heads, int32_t head_dim,
+                                               int32_t max_context_len,
                                                int32_t partition_tokens);
 
 /* Thread-local description of the last non-zero return code. */

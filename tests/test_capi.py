@@ -33,18 +33,33 @@ def test_library_loads_and_exports_every_declared_symbol():
 def test_workspace_bytes():
     lib = _native.lib()
     ws = lib.astr_paged_attention_i8_workspace_bytes
-    # one partition: no split-K partials
-    def expect(s, hq, d, parts):
-        a = lambda x: (x + 255) // 256 * 256
+    a = lambda x: (x + 255) // 256 * 256
+
+    def partitioned(s, hq, d, parts):
         return a(s * hq * parts * d * 4) + a(s * hq * parts * 8)
 
-    assert ws(64, 32, 128, 512, 512) == 0
-    assert ws(64, 32, 128, 4096, 512) == expect(64, 32, 128, 8)
-    assert ws(16, 64, 128, 32768, 512) == expect(16, 64, 128, 64)
-    assert ws(4, 4, 64, 300, 64) == expect(4, 4, 64, 5)
-    assert ws(4, 4, 64, 300, 0) == 0          # 0 selects 512-token partitions
-    assert ws(4, 4, 64, 300, 100) == 0        # not a multiple of 64 -> invalid -> 0
-    assert ws(4, 4, 64, 9000, 8192) == 0      # partitions above 4096 tokens are invalid
+    def streamk(s, hq, hkv, d, max_ctx, cus=256):
+        need = -(-(hkv * s * -(-max_ctx // 16)) // 64)
+        cap = max(cus * 32, need)
+        cap = -(-cap // 4) * 4
+        g = hq // hkv
+        return a((s + 1) * 4) + a(cap * 2 * g * d * 4) + a(cap * 2 * g * 2 * 4)
+
+    # fixed partitions (S, Hq, Hkv, D, max_ctx, partition_tokens)
+    assert ws(64, 32, 8, 128, 512, 512) == 0
+    assert ws(64, 32, 8, 128, 4096, 512) == partitioned(64, 32, 128, 8)
+    assert ws(16, 64, 8, 128, 32768, 512) == partitioned(16, 64, 128, 64)
+    assert ws(4, 4, 4, 64, 300, 64) == partitioned(4, 4, 64, 5)
+    assert ws(4, 4, 4, 64, 300, 100) == 0        # not a multiple of 64 -> invalid -> 0
+    assert ws(4, 4, 4, 64, 9000, 8192) == 0      # partitions above 4096 tokens are invalid
+    assert ws(4, 6, 4, 64, 300, 64) == 0         # q heads not a multiple of kv heads
+    # automatic mode: room for stream-K (no GPU here: 256 CUs assumed) and the fallback
+    assert ws(64, 32, 8, 128, 4096, 0) == max(streamk(64, 32, 8, 128, 4096),
+                                              partitioned(64, 32, 128, 8))
+    assert ws(16, 64, 8, 128, 32768, 0) == max(streamk(16, 64, 8, 128, 32768),
+                                               partitioned(16, 64, 128, 64))
+    # more than 512 sequences: partitioned only
+    assert ws(600, 32, 8, 128, 4096, 0) == partitioned(600, 32, 128, 8)
 
 
 def _desc(**kw):
