@@ -91,11 +91,18 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(DecodeArgs a) {
     if (s_cu[s + 1] == s_cu[s]) store_row_zero<QT>(a, s, D);
 
   // ---- 2. this wave's block range and its block ids / rows (lane j <-> block b0 + j)
+  // At most one wave per block: every wave below W then owns at least one block, so a
+  // row whose blocks span waves w0..w1 has exactly one piece in each of them (the merge
+  // relies on it). Waves from W on have nothing to do.
   const int64_t B = (int64_t)bseq * hkv;
-  const int64_t W = a.total_waves;
+  const int64_t W = min((int64_t)a.total_waves, B);
   const int64_t gw = (int64_t)blockIdx.x * kWaves + wave;
-  const int64_t b0 = B * gw / W;
-  int n = (int)(B * (gw + 1) / W - b0);
+  int64_t b0 = 0;
+  int n = 0;
+  if (gw < W) {
+    b0 = B * gw / W;
+    n = (int)(B * (gw + 1) / W - b0);
+  }
   const bool too_long = n > kMaxBlocksPerWave;  // contexts beyond the declared maximum
   if (too_long) n = kMaxBlocksPerWave;
   int row_id = 0, ids = 0;  // row id = kv_head * nseq + seq
@@ -227,7 +234,9 @@ __global__ __launch_bounds__(256) void merge_streamk_kernel(DecodeArgs a) {
   const int kvh = h / G, g = h % G;
   const int cu0 = a.ws_seq[seq], cu1 = a.ws_seq[seq + 1], bseq = a.ws_seq[a.num_seqs];
   if (cu1 == cu0) return;  // empty row: zeros written by the decode kernel
-  const int64_t B = (int64_t)bseq * a.cache.num_kv_heads, W = a.total_waves;
+  // the decode kernel's wave count: one wave per block at most
+  const int64_t B = (int64_t)bseq * a.cache.num_kv_heads;
+  const int64_t W = min((int64_t)a.total_waves, B);
   const int64_t fb = (int64_t)kvh * bseq + cu0, fe = fb + (cu1 - cu0) - 1;
   const int64_t w0 = wave_of(fb, B, W), w1 = wave_of(fe, B, W);
   if (w0 == w1) return;  // written whole by one wave

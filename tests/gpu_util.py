@@ -31,5 +31,6 @@ def oracle_decode(workload_or_tables, cache, query, layer=0, context_lens=None, 
 
 def assert_attention_close(actual, expected, atol=ATOL, rtol=RTOL):
     """|a - b| <= atol + rtol * |b| elementwise (torch.testing.assert_close semantics)."""
-    a = actual.float().cpu().numpy() if isinstance(actual, torch.Tensor) else actual
-    np.testing.assert_allclose(a, expected, atol=atol, rtol=rtol)
+    def host(x):
+        return x.float().cpu().numpy() if isinstance(x, torch.Tensor) else x
+    np.testing.assert_allclose(host(actual), host(expected), atol=atol, rtol=rtol)

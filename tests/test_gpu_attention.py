@@ -163,8 +163,16 @@ def test_duplicate_rows_and_prefix_sharing(device):
     l2[1] = l2[0]
     q2 = q.clone()
     q2[1] = q2[0]
-    out = cache.paged_attention(0, q2, t2, l2, max_context_len=w.max_context_len, check=True)
+    # fixed partitions split both rows at the same token offsets: bit-identical
+    out = cache.paged_attention(0, q2, t2, l2, max_context_len=w.max_context_len,
+                                partition_tokens=512, check=True)
     assert torch.equal(out[0], out[1])
+    # stream-K cuts the flattened block list into equal ranges, so the two copies are
+    # split at different offsets: equal up to the merge's rounding
+    sk = cache.paged_attention(0, q2, t2, l2, max_context_len=w.max_context_len,
+                               partition_tokens=0, check=True)
+    assert_attention_close(sk[1], sk[0])
+    assert_attention_close(sk, out)
 
 
 def test_errors(device):
