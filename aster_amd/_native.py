@@ -29,6 +29,7 @@ ASTR_F32, ASTR_F16, ASTR_BF16 = 0, 1, 2
 EXPORTED_SYMBOLS = (
     "astr_kv_quantize_append_i8",
     "astr_paged_attention_i8",
+    "astr_paged_attention_varlen_i8",
     "astr_paged_attention_i8_workspace_bytes",
     "astr_last_error",
     "astr_version",
@@ -85,6 +86,12 @@ def lib():
             c_i32, c_i32, ctypes.c_float, c_i32, c_i32, c_vp, c_sz, c_vp, c_vp,
         ]
         handle.astr_paged_attention_i8.restype = ctypes.c_int
+        handle.astr_paged_attention_varlen_i8.argtypes = [
+            desc_p, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i32, c_i32, c_i32,
+            c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, ctypes.c_float, c_i32, c_i32, c_vp, c_sz,
+            c_vp, c_vp,
+        ]
+        handle.astr_paged_attention_varlen_i8.restype = ctypes.c_int
         handle.astr_paged_attention_i8_workspace_bytes.argtypes = [c_i32] * 6
         handle.astr_paged_attention_i8_workspace_bytes.restype = c_sz
         handle.astr_last_error.argtypes = []

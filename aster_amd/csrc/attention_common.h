@@ -22,7 +22,7 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-struct DecodeArgs {
+struct AttnArgs {
   const void* q;
   int64_t q_tok, q_head;
   void* out;
@@ -31,6 +31,11 @@ struct DecodeArgs {
   const int32_t* block_tables;
   int32_t bt_stride;
   const int32_t* context_lens;
+  // Packed queries: sequence s owns query/output token rows [q_start[s], q_start[s+1]).
+  // nullptr: one query token per sequence, at row s.
+  const int32_t* q_start;
+  int32_t num_q_tokens;  // rows of query/out (upper bound of q_start[num_seqs])
+  int32_t causal;        // multi-token rows: key k is visible to query position p iff k <= p
   int32_t num_seqs, num_q_heads;
   float qk_scale_log2;  // softmax scale * log2(e)
   int32_t window;
@@ -48,12 +53,39 @@ struct DecodeArgs {
   int32_t* err_flag;
 };
 
+// Query/output token rows [begin, begin + count) of sequence `seq` (count is
+// returned). A q_start entry that is negative, decreasing or beyond num_q_tokens
+// gives count 0 and raises the index flag, so no kernel indexes outside query/out.
+//
+// decode_token: the token row of `seq` when it carries exactly one query token
+// (a decode row), else -1: sequences with several query tokens belong to the
+// prefill kernel and sequences with none produce no output.
+__device__ __forceinline__ int seq_queries(const AttnArgs& a, int seq, int& begin) {
+  if (a.q_start == nullptr) {
+    begin = seq;
+    return 1;
+  }
+  const int b = a.q_start[seq], e = a.q_start[seq + 1];
+  if (b < 0 || e < b || e > a.num_q_tokens) {  // not a valid offset table: no rows, flagged
+    atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+    begin = 0;
+    return 0;
+  }
+  begin = b;
+  return e - b;
+}
+
+__device__ __forceinline__ int decode_token(const AttnArgs& a, int seq) {
+  int begin;
+  return seq_queries(a, seq, begin) == 1 ? begin : -1;
+}
+
 // Visible key range of a decode row: tokens [kv_begin, ctx), blocks [first, last).
 struct RowSpan {
   int ctx, kv_begin, first_blk, last_blk;
 };
 
-__device__ __forceinline__ int clamp_ctx(const DecodeArgs& a, int ctx, bool report) {
+__device__ __forceinline__ int clamp_ctx(const AttnArgs& a, int ctx, bool report) {
   const int cap = a.bt_stride * kBlockTokens;
   if (ctx < 0 || ctx > cap) {
     if (report) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
@@ -62,7 +94,7 @@ __device__ __forceinline__ int clamp_ctx(const DecodeArgs& a, int ctx, bool repo
   return ctx;
 }
 
-__device__ __forceinline__ RowSpan row_span(const DecodeArgs& a, int ctx) {
+__device__ __forceinline__ RowSpan row_span(const AttnArgs& a, int ctx) {
   RowSpan r;
   r.ctx = ctx;
   r.kv_begin = (a.window > 0 && ctx > a.window) ? ctx - a.window : 0;
@@ -121,7 +153,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // exactly Stage<D>::kLoads vector-memory instructions (waves are always full,
 // so the 32-lane scale load always issues).
 template <int D>
-__device__ __forceinline__ void stage_block(const DecodeArgs& a, int phys, int kvh, int lane,
+__device__ __forceinline__ void stage_block(const AttnArgs& a, int phys, int kvh, int lane,
                                             char* st) {
   using S = Stage<D>;
   const int64_t off = (int64_t)phys * a.cache.code_block_stride +
@@ -179,9 +211,9 @@ struct QueryRaw {
 };
 
 template <typename QT, int D, int G>
-__device__ __forceinline__ void load_query(const DecodeArgs& a, int seq, int kvh, int r, int qg,
+__device__ __forceinline__ void load_query(const AttnArgs& a, int tok, int kvh, int r, int qg,
                                            QueryRaw<D>& q) {
-  const QT* qp = static_cast<const QT*>(a.q) + seq * a.q_tok +
+  const QT* qp = static_cast<const QT*>(a.q) + (int64_t)tok * a.q_tok +
                  (int64_t)(kvh * G + (r < G ? r : 0)) * a.q_head + 16 * qg;
 #pragma unroll
   for (int h = 0; h < D / 64; ++h) {
@@ -327,8 +359,11 @@ __device__ __forceinline__ void mfma_block(const char* st, const half8_t (&qop)[
 
 // Kernel entry points (one per translation unit), dispatched on query dtype,
 // head dim and GQA group inside.
-int launch_partitioned(const DecodeArgs& a, int32_t q_dtype, hipStream_t stream);
-int launch_streamk(const DecodeArgs& a, int32_t q_dtype, hipStream_t stream);
+int launch_partitioned(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
+int launch_streamk(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
+// Rows with more than one query token (chunked prefill), one workgroup per
+// (kv head, sequence, tile of query tokens); needs q_start.
+int launch_prefill(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
 // Largest batch the stream-K kernel takes (its per-sequence table lives in LDS).
 int stream_k_max_seqs();
 

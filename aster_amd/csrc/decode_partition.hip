@@ -39,7 +39,7 @@ struct RowPlan : RowSpan {
   int num_parts;
 };
 
-__device__ __forceinline__ RowPlan plan_row(const DecodeArgs& a, int seq, bool report) {
+__device__ __forceinline__ RowPlan plan_row(const AttnArgs& a, int seq, bool report) {
   RowPlan r;
   static_cast<RowSpan&>(r) = row_span(a, clamp_ctx(a, a.context_lens[seq], report));
   int parts = (r.last_blk - r.first_blk + a.part_blocks - 1) / a.part_blocks;
@@ -63,8 +63,8 @@ struct Shared {
 // Combine the 4 waves of the workgroup (already in `sh`) and write either the
 // normalised output (single partition) or this partition's partial.
 template <typename QT, int G, int D>
-__device__ void finish_partition(const DecodeArgs& a, Shared<G, D>& sh, const RowPlan& row,
-                                 int seq, int kvh, int part) {
+__device__ void finish_partition(const AttnArgs& a, Shared<G, D>& sh, const RowPlan& row,
+                                 int seq, int tok, int kvh, int part) {
   const bool split = row.num_parts > 1;
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int g = idx / D, d = idx % D;
@@ -81,7 +81,7 @@ __device__ void finish_partition(const DecodeArgs& a, Shared<G, D>& sh, const Ro
     }
     const int h = kvh * G + g;
     if (!split) {
-      QT* op = static_cast<QT*>(a.out) + seq * a.o_tok + (int64_t)h * a.o_head;
+      QT* op = static_cast<QT*>(a.out) + (int64_t)tok * a.o_tok + (int64_t)h * a.o_head;
       op[d] = from_float<QT>(O / fmaxf(L, FLT_MIN));
     } else {
       const int64_t base = ((int64_t)seq * a.num_q_heads + h) * a.max_parts + part;
@@ -95,7 +95,7 @@ __device__ void finish_partition(const DecodeArgs& a, Shared<G, D>& sh, const Ro
 }
 
 // Physical block ids of this wave's blocks (first + 4*i), one per lane.
-__device__ __forceinline__ int wave_block_ids(const DecodeArgs& a, int seq, int first, int nbw,
+__device__ __forceinline__ int wave_block_ids(const AttnArgs& a, int seq, int first, int nbw,
                                               int lane) {
   const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
   return lane < nbw ? bt[first + kWaves * lane] : 0;
@@ -111,7 +111,7 @@ constexpr int stage0_bytes() {
 // ================================ MFMA kernel (bf16 / fp16 queries)
 
 template <typename QT, int D, int G, int NS>
-__global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   static_assert(G >= 1 && G <= 16, "GQA group");
   static_assert(NS == 2 || NS == 3, "stages");
@@ -128,11 +128,13 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
   const int lane = threadIdx.x % kWave;
   const int r = lane & 15, qg = lane >> 4;
   const bool gvalid = r < G;
+  const int tok = decode_token(a, seq);
+  if (tok < 0) return;  // not a decode row
 
   // ---- prologue: the query and (for window == 0) this wave's block ids do not
   // depend on the context length, so their loads issue together with it.
   QueryRaw<D> qraw;
-  load_query<QT, D, G>(a, seq, kvh, r, qg, qraw);
+  load_query<QT, D, G>(a, tok, kvh, r, qg, qraw);
   const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
   const int per_wave = (a.part_blocks + kWaves - 1) / kWaves;
   const int spec = part * a.part_blocks + wave + kWaves * lane;  // block index if kv_begin == 0
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
       for (int j = 0; j < 4; ++j) sh.o[wave][r][VB * (4 * qg + j) + n] = acc[n][j];
   }
   __syncthreads();
-  finish_partition<QT, G, D>(a, sh, row, seq, kvh, part);
+  finish_partition<QT, G, D>(a, sh, row, seq, tok, kvh, part);
 }
 
 // ================================ exact fp32 VALU kernel (fp32 queries)
@@ -218,7 +220,7 @@ struct ValuTile {
 };
 
 template <typename QT, int D, int G>
-__global__ __launch_bounds__(256) void decode_valu_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
   constexpr int LPT = D / 16;             // lanes per token row
   constexpr int TPL = kWave / LPT;        // token rows per load instruction
   constexpr int NL = kBlockTokens / TPL;  // load instructions per block
@@ -229,6 +231,8 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeArgs a) {
   const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
+  const int tok = decode_token(a, seq);
+  if (tok < 0) return;  // not a decode row
   const RowPlan row = plan_row(a, seq, part == 0 && kvh == 0 && threadIdx.x == 0);
   if (part >= row.num_parts) return;
   const int pb0 = row.first_blk + part * a.part_blocks;
@@ -240,7 +244,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeArgs a) {
 
   float qf[G][16];
   {
-    const QT* qp = static_cast<const QT*>(a.q) + seq * a.q_tok + (int64_t)kvh * G * a.q_head + d0;
+    const QT* qp = static_cast<const QT*>(a.q) + (int64_t)tok * a.q_tok + (int64_t)kvh * G * a.q_head + d0;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       constexpr int kVec = 16 / sizeof(QT);
@@ -383,7 +387,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeArgs a) {
       for (int e = 0; e < 16; ++e) sh.o[wave][g][d0 + e] = acc[g][e];
   }
   __syncthreads();
-  finish_partition<QT, G, D>(a, sh, row, seq, kvh, part);
+  finish_partition<QT, G, D>(a, sh, row, seq, tok, kvh, part);
 }
 
 
@@ -393,12 +397,14 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeArgs a) {
 // partitions' (m, l) in parallel, take the wave max, and every lane then sums
 // its d-slice over the partitions with the merge_softmax weights exp2(m_p - M).
 template <typename QT, int D>
-__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) void merge_kernel(AttnArgs a) {
   constexpr int kPerLane = (D + kWave - 1) / kWave;
   const int lane = threadIdx.x % kWave;
   const int unit = blockIdx.x * kWaves + threadIdx.x / kWave;  // seq * Hq + h
   if (unit >= a.num_seqs * a.num_q_heads) return;
   const int seq = unit / a.num_q_heads, h = unit % a.num_q_heads;
+  const int tok = decode_token(a, seq);
+  if (tok < 0) return;
   const RowPlan row = plan_row(a, seq, false);
   if (row.num_parts <= 1) return;
   const int64_t base = (int64_t)unit * a.max_parts;
@@ -445,7 +451,7 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
         for (int e = 0; e < kPerLane; ++e) O[e] = fmaf(v[u][e], wq[u], O[e]);
     }
   }
-  QT* out = static_cast<QT*>(a.out) + seq * a.o_tok + (int64_t)h * a.o_head;
+  QT* out = static_cast<QT*>(a.out) + (int64_t)tok * a.o_tok + (int64_t)h * a.o_head;
   const float inv_l = 1.f / fmaxf(L, FLT_MIN);
 #pragma unroll
   for (int e = 0; e < kPerLane; ++e) {
@@ -457,7 +463,7 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
 // ================================ launch / dispatch
 
 template <typename QT, int D, int G>
-int launch(const DecodeArgs& a, hipStream_t stream) {
+int launch(const AttnArgs& a, hipStream_t stream) {
   const dim3 grid((uint32_t)a.max_parts, (uint32_t)a.cache.num_kv_heads, (uint32_t)a.num_seqs);
   if constexpr (sizeof(QT) == 4) {
     hipLaunchKernelGGL((decode_valu_kernel<QT, D, G>), grid, dim3(kWaves * kWave), 0, stream, a);
@@ -475,7 +481,7 @@ int launch(const DecodeArgs& a, hipStream_t stream) {
 }
 
 template <typename QT, int D>
-int dispatch_group(const DecodeArgs& a, int G, hipStream_t s) {
+int dispatch_group(const AttnArgs& a, int G, hipStream_t s) {
   switch (G) {
     case 1: return launch<QT, D, 1>(a, s);
     case 2: return launch<QT, D, 2>(a, s);
@@ -490,7 +496,7 @@ int dispatch_group(const DecodeArgs& a, int G, hipStream_t s) {
 }
 
 template <typename QT>
-int dispatch_dim(const DecodeArgs& a, int G, hipStream_t s) {
+int dispatch_dim(const AttnArgs& a, int G, hipStream_t s) {
   switch (a.cache.head_dim) {
     case 64: return dispatch_group<QT, 64>(a, G, s);
     case 128: return dispatch_group<QT, 128>(a, G, s);
@@ -501,7 +507,7 @@ int dispatch_dim(const DecodeArgs& a, int G, hipStream_t s) {
 
 }  // namespace
 
-int launch_partitioned(const DecodeArgs& a, int32_t q_dtype, hipStream_t stream) {
+int launch_partitioned(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
   const int G = a.num_q_heads / a.cache.num_kv_heads;
   switch (q_dtype) {
     case ASTR_F32: return dispatch_dim<float>(a, G, stream);

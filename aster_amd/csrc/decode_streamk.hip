@@ -26,14 +26,14 @@ __device__ __forceinline__ int64_t wave_of(int64_t b, int64_t B, int64_t W) {
 }
 
 template <typename QT>
-__device__ __forceinline__ void store_row_zero(const DecodeArgs& a, int seq, int D) {
-  QT* orow = static_cast<QT*>(a.out) + seq * a.o_tok;
+__device__ __forceinline__ void store_row_zero(const AttnArgs& a, int tok, int D) {
+  QT* orow = static_cast<QT*>(a.out) + (int64_t)tok * a.o_tok;
   for (int idx = threadIdx.x; idx < a.num_q_heads * D; idx += blockDim.x)
     orow[(int64_t)(idx / D) * a.o_head + idx % D] = from_float<QT>(0.f);
 }
 
 template <typename QT, int D, int G, int NS>
-__global__ __launch_bounds__(256) void decode_streamk_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) void decode_streamk_kernel(AttnArgs a) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   static_assert(G >= 1 && G <= 16, "GQA group");
   static_assert(NS == 2 || NS == 3, "stages");
@@ -44,7 +44,8 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char lds0[kWaves * S::kBytes];
   __shared__ __attribute__((aligned(16))) char lds1[kWaves * S::kBytes];
   __shared__ __attribute__((aligned(16))) char lds2[NS == 3 ? kWaves * S::kBytes : 16];
-  __shared__ int s_ctx[kMaxSeqsSK];
+  __shared__ int s_ctx[kMaxSeqsSK];  // -1: not a decode row
+  __shared__ int s_tok[kMaxSeqsSK];  // query/output token row
   __shared__ int s_cu[kMaxSeqsSK + 1];
   __shared__ int s_wsum[kWaves];
 
@@ -55,16 +56,23 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(DecodeArgs a) {
   const int nseq = a.num_seqs;
   const int hkv = a.cache.num_kv_heads;
 
-  // ---- 1. visible blocks per sequence -> exclusive prefix s_cu (thread t owns 2t, 2t+1)
+  // ---- 1. visible blocks per sequence -> exclusive prefix s_cu (thread t owns 2t, 2t+1);
+  // sequences without exactly one query token take no blocks
   int nb[2] = {0, 0};
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int s = 2 * threadIdx.x + k;
     if (s < nseq) {
-      const int ctx = clamp_ctx(a, a.context_lens[s], blockIdx.x == 0);
-      s_ctx[s] = ctx;
-      const RowSpan sp = row_span(a, ctx);
-      nb[k] = sp.last_blk - sp.first_blk;
+      const int tok = decode_token(a, s);
+      s_tok[s] = tok;
+      if (tok >= 0) {
+        const int ctx = clamp_ctx(a, a.context_lens[s], blockIdx.x == 0);
+        s_ctx[s] = ctx;
+        const RowSpan sp = row_span(a, ctx);
+        nb[k] = sp.last_blk - sp.first_blk;
+      } else {
+        s_ctx[s] = -1;
+      }
     }
   }
   const int local = nb[0] + nb[1];
@@ -88,7 +96,7 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(DecodeArgs a) {
     for (int s = threadIdx.x; s <= nseq; s += blockDim.x) a.ws_seq[s] = s_cu[s];
   // rows with nothing visible (ctx == 0) are zero (online_attention.py:37)
   for (int s = blockIdx.x; s < nseq; s += gridDim.x)
-    if (s_cu[s + 1] == s_cu[s]) store_row_zero<QT>(a, s, D);
+    if (s_cu[s + 1] == s_cu[s] && s_ctx[s] >= 0) store_row_zero<QT>(a, s_tok[s], D);
 
   // ---- 2. this wave's block range and its block ids / rows (lane j <-> block b0 + j)
   // At most one wave per block: every wave below W then owns at least one block, so a
@@ -123,7 +131,7 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(DecodeArgs a) {
   // first row's query: issued with the block ids, converted before any staging
   QueryRaw<D> qr;
   const int row0 = __builtin_amdgcn_readfirstlane(row_id);
-  if (n > 0) load_query<QT, D, G>(a, row0 % nseq, row0 / nseq, r, qg, qr);
+  if (n > 0) load_query<QT, D, G>(a, s_tok[row0 % nseq], row0 / nseq, r, qg, qr);
   const bool bad_index =
       too_long || __ballot(lane < n && (unsigned)ids >= (unsigned)a.cache.num_blocks) != 0;
   const int nblk = bad_index ? 0 : n;
@@ -162,7 +170,8 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(DecodeArgs a) {
       // the whole row is in this wave: final output
       if (gvalid) {
         const float inv = 1.f / fmaxf(lt, FLT_MIN);
-        QT* op = static_cast<QT*>(a.out) + pseq * a.o_tok + (int64_t)(pkvh * G + r) * a.o_head;
+        QT* op = static_cast<QT*>(a.out) + (int64_t)s_tok[pseq] * a.o_tok +
+                 (int64_t)(pkvh * G + r) * a.o_head;
 #pragma unroll
         for (int k = 0; k < NPV; ++k)
 #pragma unroll
@@ -192,7 +201,7 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(DecodeArgs a) {
       pstart = i;
       psp = row_span(a, s_ctx[pseq]);
       pfb = (int64_t)pkvh * bseq + s_cu[pseq];
-      load_query<QT, D, G>(a, pseq, pkvh, r, qg, qr);
+      load_query<QT, D, G>(a, s_tok[pseq], pkvh, r, qg, qr);
       cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop);
 #pragma unroll
       for (int k = 0; k < NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -224,7 +233,7 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(DecodeArgs a) {
 
 // One wave per (sequence, q head): merge the pieces of rows split across waves.
 template <typename QT, int D>
-__global__ __launch_bounds__(256) void merge_streamk_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) void merge_streamk_kernel(AttnArgs a) {
   constexpr int kPerLane = (D + kWave - 1) / kWave;
   const int lane = threadIdx.x % kWave;
   const int unit = blockIdx.x * kWaves + threadIdx.x / kWave;  // seq * Hq + h
@@ -233,7 +242,7 @@ __global__ __launch_bounds__(256) void merge_streamk_kernel(DecodeArgs a) {
   const int G = a.num_q_heads / a.cache.num_kv_heads;
   const int kvh = h / G, g = h % G;
   const int cu0 = a.ws_seq[seq], cu1 = a.ws_seq[seq + 1], bseq = a.ws_seq[a.num_seqs];
-  if (cu1 == cu0) return;  // empty row: zeros written by the decode kernel
+  if (cu1 == cu0) return;  // empty or not a decode row: nothing to merge
   // the decode kernel's wave count: one wave per block at most
   const int64_t B = (int64_t)bseq * a.cache.num_kv_heads;
   const int64_t W = min((int64_t)a.total_waves, B);
@@ -287,7 +296,8 @@ __global__ __launch_bounds__(256) void merge_streamk_kernel(DecodeArgs a) {
         for (int e = 0; e < kPerLane; ++e) O[e] = fmaf(v[u][e], wq[u], O[e]);
     }
   }
-  QT* out = static_cast<QT*>(a.out) + seq * a.o_tok + (int64_t)h * a.o_head;
+  QT* out = static_cast<QT*>(a.out) + (int64_t)decode_token(a, seq) * a.o_tok +
+            (int64_t)h * a.o_head;
   const float inv_l = 1.f / fmaxf(L, FLT_MIN);
 #pragma unroll
   for (int e = 0; e < kPerLane; ++e) {
@@ -319,7 +329,7 @@ int device_cus() {
 }
 
 template <typename QT, int D, int G>
-int launch(DecodeArgs a, hipStream_t stream) {
+int launch(AttnArgs a, hipStream_t stream) {
   auto kernel = decode_streamk_kernel<QT, D, G, kStagesSK>;
   // one wave per resident slot (whole workgroups), at least min_waves, at most the
   // workspace capacity passed in total_waves
@@ -337,7 +347,7 @@ int launch(DecodeArgs a, hipStream_t stream) {
 }
 
 template <typename QT, int D>
-int dispatch_group(const DecodeArgs& a, int G, hipStream_t s) {
+int dispatch_group(const AttnArgs& a, int G, hipStream_t s) {
   switch (G) {
     case 1: return launch<QT, D, 1>(a, s);
     case 2: return launch<QT, D, 2>(a, s);
@@ -352,7 +362,7 @@ int dispatch_group(const DecodeArgs& a, int G, hipStream_t s) {
 }
 
 template <typename QT>
-int dispatch_dim(const DecodeArgs& a, int G, hipStream_t s) {
+int dispatch_dim(const AttnArgs& a, int G, hipStream_t s) {
   switch (a.cache.head_dim) {
     case 64: return dispatch_group<QT, 64>(a, G, s);
     case 128: return dispatch_group<QT, 128>(a, G, s);
@@ -363,7 +373,7 @@ int dispatch_dim(const DecodeArgs& a, int G, hipStream_t s) {
 
 }  // namespace
 
-int launch_streamk(const DecodeArgs& a, int32_t q_dtype, hipStream_t stream) {
+int launch_streamk(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
   if (a.min_waves > a.total_waves)
     return fail(ASTR_EINVAL, "stream-K workspace too small for this launch");
   const int G = a.num_q_heads / a.cache.num_kv_heads;

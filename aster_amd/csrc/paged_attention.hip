@@ -1,7 +1,9 @@
-// C ABI of the paged decode attention: argument checks, workspace layout and
-// the choice between the stream-K kernel (bf16/fp16 queries, partition_tokens
-// == 0, up to 512 sequences) and fixed-size split-K partitions (every other
-// case). Kernels: decode_streamk.hip, decode_partition.hip.
+// C ABI of the paged attention: argument checks, workspace layout and kernel
+// choice. Decode rows (one query token) run the stream-K kernel (bf16/fp16
+// queries, partition_tokens == 0, up to 512 sequences) or fixed-size split-K
+// partitions (every other case); rows with several query tokens (chunked
+// prefill, varlen entry point only) run the prefill kernel after them on the same
+// stream. Kernels: decode_streamk.hip, decode_partition.hip, prefill.hip.
 #include <mutex>
 
 #include "attention_common.h"
@@ -130,15 +132,17 @@ extern "C" size_t astr_paged_attention_i8_workspace_bytes(int32_t num_seqs, int3
       .total();
 }
 
-extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query,
-                                       int32_t q_dtype, int64_t q_token_stride,
-                                       int64_t q_head_stride, void* out, int64_t out_token_stride,
-                                       int64_t out_head_stride, const int32_t* block_tables,
-                                       int32_t block_table_stride, const int32_t* context_lens,
-                                       int32_t num_seqs, int32_t num_q_heads,
-                                       int32_t max_context_len, float scale, int32_t window,
-                                       int32_t partition_tokens, void* workspace,
-                                       size_t workspace_bytes, int32_t* err_flag, void* stream) {
+namespace {
+
+int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dtype,
+                    int64_t q_token_stride, int64_t q_head_stride, void* out,
+                    int64_t out_token_stride, int64_t out_head_stride,
+                    const int32_t* query_start_loc, int32_t num_query_tokens,
+                    int32_t max_query_len, int32_t causal, const int32_t* block_tables,
+                    int32_t block_table_stride, const int32_t* context_lens, int32_t num_seqs,
+                    int32_t num_q_heads, int32_t max_context_len, float scale, int32_t window,
+                    int32_t partition_tokens, void* workspace, size_t workspace_bytes,
+                    int32_t* err_flag, void* stream) {
   using namespace astr;
   using namespace astr::attn;
   if (cache == nullptr || err_flag == nullptr)
@@ -148,6 +152,9 @@ extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* q
                              "num_q_heads >= 1");
   if (num_seqs == 0) return 0;
   if (num_seqs > 65535) return fail(ASTR_EUNSUPPORTED, "more than 65535 sequences per launch");
+  if (query_start_loc != nullptr && (num_query_tokens < 0 || max_query_len < 0))
+    return fail(ASTR_EINVAL, "num_query_tokens and max_query_len must be >= 0");
+  if (query_start_loc != nullptr && num_query_tokens == 0) return 0;
   if (query == nullptr || out == nullptr || block_tables == nullptr || context_lens == nullptr)
     return fail(ASTR_EINVAL, "query, out, block_tables and context_lens are required");
   if (!(scale > 0.f) || !std::isfinite(scale))
@@ -194,7 +201,10 @@ extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* q
                                              cache->head_dim, max_context_len, 0, 0)
                             : partitioned_layout(num_seqs, num_q_heads, cache->head_dim, parts);
 
-  DecodeArgs a{};
+  AttnArgs a{};
+  a.q_start = query_start_loc;
+  a.num_q_tokens = query_start_loc != nullptr ? num_query_tokens : num_seqs;
+  a.causal = causal != 0;
   a.q = query;
   a.q_tok = q_token_stride;
   a.q_head = q_head_stride;
@@ -222,5 +232,42 @@ extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* q
   }
   a.err_flag = err_flag;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return streamk ? launch_streamk(a, q_dtype, s) : launch_partitioned(a, q_dtype, s);
+  const int rc = streamk ? launch_streamk(a, q_dtype, s) : launch_partitioned(a, q_dtype, s);
+  if (rc != 0 || query_start_loc == nullptr || max_query_len < 2) return rc;
+  return launch_prefill(a, q_dtype, s);
+}
+
+}  // namespace
+
+extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query,
+                                       int32_t q_dtype, int64_t q_token_stride,
+                                       int64_t q_head_stride, void* out, int64_t out_token_stride,
+                                       int64_t out_head_stride, const int32_t* block_tables,
+                                       int32_t block_table_stride, const int32_t* context_lens,
+                                       int32_t num_seqs, int32_t num_q_heads,
+                                       int32_t max_context_len, float scale, int32_t window,
+                                       int32_t partition_tokens, void* workspace,
+                                       size_t workspace_bytes, int32_t* err_flag, void* stream) {
+  return paged_attention(cache, query, q_dtype, q_token_stride, q_head_stride, out,
+                         out_token_stride, out_head_stride, nullptr, num_seqs, 1, 1, block_tables,
+                         block_table_stride, context_lens, num_seqs, num_q_heads, max_context_len,
+                         scale, window, partition_tokens, workspace, workspace_bytes, err_flag,
+                         stream);
+}
+
+extern "C" int astr_paged_attention_varlen_i8(
+    const astr_paged_kv* cache, const void* query, int32_t q_dtype, int64_t q_token_stride,
+    int64_t q_head_stride, void* out, int64_t out_token_stride, int64_t out_head_stride,
+    const int32_t* query_start_loc, int32_t num_query_tokens, int32_t max_query_len,
+    int32_t causal, const int32_t* block_tables, int32_t block_table_stride,
+    const int32_t* context_lens, int32_t num_seqs, int32_t num_q_heads, int32_t max_context_len,
+    float scale, int32_t window, int32_t partition_tokens, void* workspace, size_t workspace_bytes,
+    int32_t* err_flag, void* stream) {
+  if (query_start_loc == nullptr)
+    return astr::fail(ASTR_EINVAL, "query_start_loc is required (int32 [num_seqs + 1])");
+  return paged_attention(cache, query, q_dtype, q_token_stride, q_head_stride, out,
+                         out_token_stride, out_head_stride, query_start_loc, num_query_tokens,
+                         max_query_len, causal, block_tables, block_table_stride, context_lens,
+                         num_seqs, num_q_heads, max_context_len, scale, window, partition_tokens,
+                         workspace, workspace_bytes, err_flag, stream);
 }

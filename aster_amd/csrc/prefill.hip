@@ -1,0 +1,446 @@
+// Chunked-prefill paged attention over the INT8 arena (gfx950): the sequences of
+// a step that carry more than one query token (a prompt chunk in
+// PagedAttentionRunner.forward_batch, paged_attention.py:168-215), with the
+// visibility rules of online_attention_statistics (online_attention.py:178-188):
+// query token i of a sequence with n query tokens and context ctx (the chunk
+// already appended) sits at position p = ctx - n + i and sees key k iff
+//   k <= p (causal; else k < ctx)  and  k > p - window (window > 0).
+//
+// Work unit: (kv head, sequence, tile of TQ query tokens), TQ * G = 64 * NT
+// (token, head) columns of one kv head, 16 * NT columns per wave. The unit's
+// visible key range is streamed in steps of four 16-token blocks; each wave
+// stages one block of the step into LDS with direct global->LDS loads and then
+// all four waves run all four blocks through the MFMAs:
+//   S^T[t][c]  = K[t][:] . Q[c][:]     v_mfma_f32_16x16x32_f16 (int8 codes are exact in f16)
+//   O^T[d][c] += V^T[d][t] . P^T[t][c]  v_mfma_f32_16x16x16f16 (P^T carries V's scales)
+// so every K/V byte of the unit's range is read once per query tile and shared by
+// the G heads and TQ tokens of the tile. Softmax statistics are per column, in
+// base 2, with the lazy rescale of the decode kernels.
+//
+// Units of one (kv head, sequence) are consecutive, longest (latest) tile first,
+// and the linear workgroup id is remapped so that each XCD (workgroups are dealt
+// to the 8 XCDs round robin) runs one contiguous range of units: the tiles
+// sharing a sequence's K/V then share that XCD's L2.
+#include <climits>
+
+#include "attention_common.h"
+
+namespace astr {
+namespace attn {
+namespace {
+
+constexpr int kXcds = 8;
+
+template <int D>
+struct PrefillShape {
+  static constexpr int NT = D == 256 ? 1 : 2;     // 16-column MFMA tiles per wave
+  static constexpr int kCols = kWaves * 16 * NT;  // (token, head) columns per workgroup
+};
+
+__device__ __forceinline__ int query_tiles(const AttnArgs& a, int s, int tq) {
+  int begin;
+  const int n = seq_queries(a, s, begin);
+  return n > 1 ? (n + tq - 1) / tq : 0;
+}
+
+// Workgroup-wide scan of the query-tile counts of all sequences. Returns the
+// total; when `unit` >= 0, the sequence holding that unit and the unit's index
+// within the sequence land in found[0], found[1]. Every thread calls it.
+__device__ int scan_tiles(const AttnArgs& a, int tq, int unit, int* s_wsum, int* found) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  int base = 0;
+  for (int c0 = 0; c0 < a.num_seqs; c0 += kWaves * kWave) {
+    const int s = c0 + (int)threadIdx.x;
+    const int t = s < a.num_seqs ? query_tiles(a, s, tq) : 0;
+    int incl = t;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int v = __shfl_up(incl, off, kWave);
+      if (lane >= off) incl += v;
+    }
+    if (lane == kWave - 1) s_wsum[wave] = incl;
+    __syncthreads();
+    int wb = base;
+    for (int w = 0; w < wave; ++w) wb += s_wsum[w];
+    incl += wb;
+    if (unit >= incl - t && unit < incl) {
+      found[0] = s;
+      found[1] = unit - (incl - t);
+    }
+    base += s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+    __syncthreads();
+  }
+  return base;
+}
+
+// f16 B-operand of one query column (lane r of its 16-lane group qg holds
+// d = 16*qg + 64*h + [0, 16)), after an exact 2^-e rescale keeping max|q| below
+// 2^15; returns the score factor with e folded in. Cross-lane: uniform control flow.
+template <typename QT, int D>
+__device__ __forceinline__ float query_column(const QT* qp, bool valid, float qk_scale_log2,
+                                              half8_t (&qop)[D / 32]) {
+  constexpr int kVec = 16 / (int)sizeof(QT);  // elements per 16-byte load
+  float x[D / 64][16];
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h) {
+    const uint4* src = reinterpret_cast<const uint4*>(qp + 64 * h);
+#pragma unroll
+    for (int c = 0; c < 16 / kVec; ++c) {
+      const uint4 w = src[c];
+      const QT* e = reinterpret_cast<const QT*>(&w);
+#pragma unroll
+      for (int i = 0; i < kVec; ++i) x[h][c * kVec + i] = valid ? to_float<QT>(e[i]) : 0.f;
+    }
+  }
+  float mx = 0.f;
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(x[h][i]));
+  mx = fmaxf(mx, shfl_xor(mx, 16));
+  mx = fmaxf(mx, shfl_xor(mx, 32));
+  int ex = 0;
+  if (mx >= 32768.f) {
+    frexpf(mx, &ex);
+    ex -= 15;
+  }
+  const float down = ldexpf(1.f, -ex);
+#pragma unroll
+  for (int kk = 0; kk < D / 32; ++kk)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qop[kk][i] = (_Float16)(x[kk / 2][(kk % 2) * 8 + i] * down);
+  return qk_scale_log2 * ldexpf(1.f, ex);
+}
+
+// One staged 16-token block (first key position kb) through the MFMAs for the
+// wave's NT column tiles. `masked`: apply the per-column [lo, hi] key bounds
+// (blocks inside every column's range skip the compares).
+template <int D, int NT>
+__device__ __forceinline__ void prefill_block(const char* st, const half8_t (&qop)[NT][D / 32],
+                                              const float (&cf)[NT], int kb, const int (&lo)[NT],
+                                              const int (&hi)[NT], bool masked, int r, int qg,
+                                              float4_t (&acc)[NT][D / 16], float (&m)[NT],
+                                              float (&l)[NT], bool& bad_score) {
+  using S = Stage<D>;
+  constexpr int KCH = D / 64;
+  constexpr int VB = D / 16;
+  constexpr int NPV = D / 16;
+  float4_t s4[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) s4[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < KCH; ++h) {
+    const uint4 c = *reinterpret_cast<const uint4*>(st + S::kK + r * D + 16 * qg + 64 * h);
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      half2_t p0, p1, p2, p3;
+      codes_to_f16(sub ? c.z : c.x, p0, p1);
+      codes_to_f16(sub ? c.w : c.y, p2, p3);
+      const half8_t kop = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        s4[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[t][2 * h + sub], s4[t], 0, 0, 0);
+    }
+  }
+  const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
+  const float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg);
+  uint32_t vw[4][VB / 4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const char* rowp = st + S::kV + (4 * qg + j) * D + r * VB;
+    if constexpr (VB == 4) {
+      vw[j][0] = *reinterpret_cast<const uint32_t*>(rowp);
+    } else if constexpr (VB == 8) {
+      const uint2 w = *reinterpret_cast<const uint2*>(rowp);
+      vw[j][0] = w.x;
+      vw[j][1] = w.y;
+    } else {
+      const uint4 w = *reinterpret_cast<const uint4*>(rowp);
+      vw[j][0] = w.x;
+      vw[j][1] = w.y;
+      vw[j][2] = w.z;
+      vw[j][3] = w.w;
+    }
+  }
+  const int k0 = kb + 4 * qg;  // keys k0 + j of column r
+  float sc[NT][4];
+  bool need = false, nonfinite = false;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = s4[t][j] * (ks[j] * cf[t]);
+      bool vis = true;
+      if (masked) vis = k0 + j >= lo[t] && k0 + j <= hi[t];
+      nonfinite |= vis && !__builtin_isfinite(v);
+      v = vis ? v : -INFINITY;
+      need |= v > m[t] + kRescaleSlack;
+      sc[t][j] = v;
+    }
+  if (__ballot(nonfinite) != 0) bad_score = true;
+  if (__ballot(need) != 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float tmax = fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3]));
+      tmax = fmaxf(tmax, shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, shfl_xor(tmax, 32));
+      const float mn = fmaxf(m[t], tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m[t] - mn);
+      l[t] *= alpha;
+#pragma unroll
+      for (int n = 0; n < NPV; ++n) acc[t][n] *= alpha;
+      m[t] = mn;
+    }
+  }
+  half4_t pop[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = __builtin_amdgcn_exp2f(sc[t][j] - m[t]);
+      l[t] += p;
+      pop[t][j] = (_Float16)(p * vs[j]);
+    }
+#pragma unroll
+  for (int n = 0; n < NPV; ++n) {
+    const uint32_t col[4] = {vw[0][n / 4], vw[1][n / 4], vw[2][n / 4], vw[3][n / 4]};
+    half4_t vop;
+    switch (n % 4) {
+      case 0: vop = v_operand<0>(col); break;
+      case 1: vop = v_operand<1>(col); break;
+      case 2: vop = v_operand<2>(col); break;
+      default: vop = v_operand<3>(col); break;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop, pop[t], acc[t][n], 0, 0, 0);
+  }
+}
+
+// N consecutive outputs from fp32, with 16-byte (or 8-byte) stores.
+template <typename QT, int N>
+__device__ __forceinline__ void store_run(QT* dst, const float (&v)[N]) {
+  constexpr int kVec = 16 / (int)sizeof(QT);
+  if constexpr (N % kVec == 0) {
+#pragma unroll
+    for (int c = 0; c < N / kVec; ++c) {
+      uint4 w;
+      QT* e = reinterpret_cast<QT*>(&w);
+#pragma unroll
+      for (int i = 0; i < kVec; ++i) e[i] = from_float<QT>(v[c * kVec + i]);
+      reinterpret_cast<uint4*>(dst)[c] = w;
+    }
+  } else if constexpr (N * (int)sizeof(QT) == 8) {
+    uint2 w;
+    QT* e = reinterpret_cast<QT*>(&w);
+#pragma unroll
+    for (int i = 0; i < N; ++i) e[i] = from_float<QT>(v[i]);
+    *reinterpret_cast<uint2*>(dst) = w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) dst[i] = from_float<QT>(v[i]);
+  }
+}
+
+template <typename QT, int D, int G>
+__global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
+  static_assert(D == 64 || D == 128 || D == 256, "head_dim");
+  using S = Stage<D>;
+  constexpr int NT = PrefillShape<D>::NT;
+  constexpr int TQ = PrefillShape<D>::kCols / G;
+  constexpr int NPV = D / 16;
+  constexpr int VB = D / 16;
+  static_assert(PrefillShape<D>::kCols % G == 0, "GQA group must divide the column tile");
+
+  __shared__ __attribute__((aligned(16))) char lds0[kWaves * S::kBytes];
+  __shared__ __attribute__((aligned(16))) char lds1[kWaves * S::kBytes];
+  __shared__ int s_wsum[kWaves];
+  __shared__ int s_found[2];
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int r = lane & 15, qg = lane >> 4;
+  const int hkv = a.cache.num_kv_heads;
+
+  // ---- 1. this workgroup's unit (uniform over the workgroup)
+  const int per_kv = scan_tiles(a, TQ, -1, s_wsum, s_found);
+  const int64_t units = (int64_t)per_kv * hkv;
+  const int64_t per_xcd = (units + kXcds - 1) / kXcds;
+  const int64_t slot = blockIdx.x / kXcds;
+  const int64_t logical = (int64_t)(blockIdx.x % kXcds) * per_xcd + slot;
+  if (slot >= per_xcd || logical >= units) return;
+  const int kvh = (int)(logical / per_kv);
+  if (threadIdx.x == 0) s_found[0] = -1;  // ordered before the scan's writes by its barriers
+  scan_tiles(a, TQ, (int)(logical % per_kv), s_wsum, s_found);
+  const int seq = s_found[0];
+  if (seq < 0) return;  // unreachable for unit < per_kv; keeps every index below in range
+  int q0;
+  const int n = seq_queries(a, seq, q0);
+  const int ntq = (n + TQ - 1) / TQ;
+  const int tile = ntq - 1 - s_found[1];  // latest (longest) tiles first
+  const bool reporter = kvh == 0 && tile == ntq - 1 && threadIdx.x == 0;
+  const int ctx = clamp_ctx(a, a.context_lens[seq], reporter);
+  if (ctx < n && reporter) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);  // chunk longer than the context
+
+  const int pos0 = ctx - n;  // position of the sequence's first query token
+  const int t0 = tile * TQ, t1 = min(n, t0 + TQ);
+  const int lo_wg = a.window > 0 ? max(0, pos0 + t0 - a.window + 1) : 0;
+  const int hi_wg = a.causal ? min(pos0 + t1 - 1, ctx - 1) : ctx - 1;
+  const int b_lo = lo_wg / kBlockTokens;
+  const int b_hi = hi_wg >= lo_wg ? hi_wg / kBlockTokens + 1 : b_lo;  // exclusive
+  const int nsteps = (b_hi - b_lo + kWaves - 1) / kWaves;
+
+  // ---- 2. this wave's columns: flat column f -> token t0 + f / G, head kvh * G + f % G
+  half8_t qop[NT][D / 32];
+  float cf[NT];
+  int lo[NT], hi[NT], ctok[NT], chead[NT];
+  bool cvalid[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int f = (wave * NT + t) * 16 + r;
+    ctok[t] = t0 + f / G;
+    chead[t] = kvh * G + f % G;
+    cvalid[t] = ctok[t] < t1;
+    const int p = pos0 + ctok[t];
+    lo[t] = cvalid[t] ? (a.window > 0 ? max(0, p - a.window + 1) : 0) : INT_MAX;
+    hi[t] = cvalid[t] ? (a.causal ? p : ctx - 1) : -1;
+    const QT* qp = static_cast<const QT*>(a.q) + (int64_t)(q0 + (cvalid[t] ? ctok[t] : t0)) * a.q_tok +
+                   (int64_t)chead[t] * a.q_head + 16 * qg;
+    cf[t] = query_column<QT, D>(qp, cvalid[t], a.qk_scale_log2, qop[t]);
+  }
+  // key bounds over the wave's valid columns (positions grow with f)
+  const int tk_lo = t0 + (wave * NT * 16) / G;
+  const int tk_hi = min(t1 - 1, t0 + ((wave + 1) * NT * 16 - 1) / G);
+  const bool wave_any = tk_lo < t1;
+  const int w_hi_max = a.causal ? pos0 + tk_hi : ctx - 1;
+  const int w_hi_min = a.causal ? pos0 + tk_lo : ctx - 1;
+  const int w_lo_min = a.window > 0 ? max(0, pos0 + tk_lo - a.window + 1) : 0;
+  const int w_lo_max = a.window > 0 ? max(0, pos0 + tk_hi - a.window + 1) : 0;
+
+  float4_t acc[NT][NPV];
+  float m[NT], l[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int k = 0; k < NPV; ++k) acc[t][k] = float4_t{0.f, 0.f, 0.f, 0.f};
+    m[t] = -FLT_MAX;  // finite start: fully masked blocks give exp2(-inf) = 0
+    l[t] = 0.f;
+  }
+  bool bad_index = false, bad_score = false;
+
+  // ---- 3. key steps: block b_lo + 4*step + w is staged by wave w. Lane i of `ids`
+  // holds the id for step (i + 64*k); reloaded every 64 steps.
+  const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
+  int ids = 0;
+  auto load_ids = [&](int s0) {
+    const int blk = b_lo + (s0 + lane) * kWaves + wave;
+    ids = (s0 + lane < nsteps && blk < b_hi) ? bt[blk] : 0;
+  };
+  auto issue = [&](int step, char* buf) -> bool {
+    if (b_lo + step * kWaves + wave >= b_hi) return false;
+    const int id = __builtin_amdgcn_readlane(ids, step % kWave);
+    if ((unsigned)id >= (unsigned)a.cache.num_blocks) {
+      bad_index = true;
+      return false;
+    }
+    stage_block<D>(a, id, kvh, lane, buf + wave * S::kBytes);
+    return true;
+  };
+  if (nsteps > 0) load_ids(0);
+  bool nxt = nsteps > 0 ? issue(0, lds0) : false;
+  for (int i = 0; i < nsteps; ++i) {
+    char* const cur = (i & 1) ? lds1 : lds0;
+    char* const oth = (i & 1) ? lds0 : lds1;
+    nxt = false;
+    if (i + 1 < nsteps) {
+      if ((i + 1) % kWave == 0) load_ids(i + 1);
+      nxt = issue(i + 1, oth);  // `oth` was last read in step i - 1 (barrier below)
+    }
+    if (nxt) wait_vmcnt<S::kLoads>();
+    else wait_vmcnt<0>();
+    __syncthreads();  // every wave's block of step i has landed
+#pragma unroll
+    for (int bw = 0; bw < kWaves; ++bw) {
+      const int kb = (b_lo + i * kWaves + bw) * kBlockTokens;
+      if (kb >= b_hi * kBlockTokens) break;
+      if (!wave_any || kb > w_hi_max || kb + kBlockTokens - 1 < w_lo_min) continue;
+      const bool masked = !(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min);
+      prefill_block<D, NT>(cur + bw * S::kBytes, qop, cf, kb, lo, hi, masked, r, qg, acc, m, l,
+                           bad_score);
+    }
+    __syncthreads();  // step i's stage may be refilled
+  }
+  if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+  if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
+
+  // ---- 4. normalise and store (fully masked columns: l = 0, acc = 0 -> 0)
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    float lt = l[t] + shfl_xor(l[t], 16);
+    lt += shfl_xor(lt, 32);
+    if (!cvalid[t]) continue;
+    const float inv = 1.f / fmaxf(lt, FLT_MIN);
+    QT* op = static_cast<QT*>(a.out) + (int64_t)(q0 + ctok[t]) * a.o_tok +
+             (int64_t)chead[t] * a.o_head;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v[VB];
+#pragma unroll
+      for (int k = 0; k < NPV; ++k) v[k] = acc[t][k][j] * inv;
+      store_run<QT, VB>(op + VB * (4 * qg + j), v);
+    }
+  }
+}
+
+template <typename QT, int D, int G>
+int launch(const AttnArgs& a, hipStream_t stream) {
+  constexpr int TQ = PrefillShape<D>::kCols / G;
+  // Sum over sequences of ceil(n/TQ) for n >= 2 is at most tokens/TQ + sequences
+  // (and at most tokens/2 sequences have n >= 2).
+  const int64_t seqs = a.num_seqs < a.num_q_tokens / 2 ? a.num_seqs : a.num_q_tokens / 2;
+  const int64_t max_units = ((int64_t)a.num_q_tokens + TQ - 1) / TQ + seqs;
+  const int64_t total = max_units * a.cache.num_kv_heads;
+  const int64_t grid = (total + kXcds - 1) / kXcds * kXcds;
+  if (grid == 0) return 0;
+  if (grid > INT32_MAX) return fail(ASTR_EUNSUPPORTED, "prefill grid too large");
+  hipLaunchKernelGGL((prefill_mfma_kernel<QT, D, G>), dim3((uint32_t)grid), dim3(kWaves * kWave),
+                     0, stream, a);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "paged_attention (prefill) launch");
+}
+
+template <typename QT, int D>
+int dispatch_group(const AttnArgs& a, int G, hipStream_t s) {
+  switch (G) {
+    case 1: return launch<QT, D, 1>(a, s);
+    case 2: return launch<QT, D, 2>(a, s);
+    case 4: return launch<QT, D, 4>(a, s);
+    case 8: return launch<QT, D, 8>(a, s);
+    case 16: return launch<QT, D, 16>(a, s);
+    default: return fail(ASTR_EUNSUPPORTED, "GQA group size %d not supported", G);
+  }
+}
+
+template <typename QT>
+int dispatch_dim(const AttnArgs& a, int G, hipStream_t s) {
+  switch (a.cache.head_dim) {
+    case 64: return dispatch_group<QT, 64>(a, G, s);
+    case 128: return dispatch_group<QT, 128>(a, G, s);
+    case 256: return dispatch_group<QT, 256>(a, G, s);
+    default: return fail(ASTR_EUNSUPPORTED, "head_dim %d not in {64,128,256}", a.cache.head_dim);
+  }
+}
+
+}  // namespace
+
+int launch_prefill(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
+  const int G = a.num_q_heads / a.cache.num_kv_heads;
+  switch (q_dtype) {
+    case ASTR_F32: return dispatch_dim<float>(a, G, stream);
+    case ASTR_F16: return dispatch_dim<_Float16>(a, G, stream);
+    default: return dispatch_dim<bf16_t>(a, G, stream);
+  }
+}
+
+}  // namespace attn
+}  // namespace astr

@@ -146,29 +146,53 @@ class PagedKVCache:
 
     def paged_attention(self, layer, query, block_tables, context_lens, *, max_context_len,
                         scale=None, window=None, partition_tokens=DEFAULT_PARTITION_TOKENS,
+                        query_start_loc=None, max_query_len=None, causal=True,
                         out=None, workspace=None, work=None, check=False):
-        """Decode attention of one query token per sequence over this layer.
+        """Paged attention of this layer's arena for every row of a step.
 
-        ``query`` ``[S, Hq, D]`` fp32/fp16/bf16; ``block_tables`` int32 ``[S, max_blocks]``;
-        ``context_lens`` int32 ``[S]`` (committed length including the new token,
-        which sits at position ``ctx - 1``); ``max_context_len`` host upper bound of
-        ``context_lens``. ``scale`` defaults to ``head_dim ** -0.5``
-        (nn/attention.py:130); ``window`` keeps keys ``pos > ctx - 1 - window``
-        (online_attention.py:183-184). Returns ``[S, Hq, D]`` in the query dtype
-        (online_attention.py:219)."""
+        Decode (``query_start_loc=None``): one query token per sequence, ``query``
+        ``[S, Hq, D]``; the token sits at position ``ctx - 1``.
+
+        Mixed step (chunked prefill + decode): ``query`` ``[T, Hq, D]`` packed by
+        sequence, ``query_start_loc`` int32 ``[S + 1]`` device offsets (sequence
+        ``s`` owns rows ``[qsl[s], qsl[s+1])``), ``max_query_len`` the host-side
+        bound of the per-sequence query count (computed with a device sync when
+        omitted). Query ``i`` of a sequence with ``n`` queries sits at position
+        ``ctx - n + i`` (the chunk is already appended, paged_attention.py:185-192)
+        and sees keys ``<= position`` when ``causal`` (online_attention.py:181-182).
+
+        ``block_tables`` int32 ``[S, max_blocks]``; ``context_lens`` int32 ``[S]``
+        (committed length including the step's tokens); ``max_context_len`` host
+        upper bound of ``context_lens``. ``scale`` defaults to ``head_dim ** -0.5``
+        (nn/attention.py:130); ``window`` keeps keys ``k > position - window``
+        (online_attention.py:183-184). Returns the query's shape in the query
+        dtype (online_attention.py:219)."""
         if query.ndim != 3 or query.shape[-1] != self.head_dim or query.device != self.device:
-            raise ValueError("query must be [num_seqs, num_q_heads, head_dim] on the cache device")
+            raise ValueError("query must be [tokens, num_q_heads, head_dim] on the cache device")
         if query.dtype not in _DTYPE_CODES:
             raise UnsupportedAttentionBackend(f"query dtype {query.dtype} is not fp32/fp16/bf16")
         if query.stride(-1) != 1:
             raise ValueError("query rows must be contiguous")
-        num_seqs, num_q_heads = query.shape[0], query.shape[1]
+        num_tokens, num_q_heads = query.shape[0], query.shape[1]
         if num_q_heads % self.num_kv_heads:
             raise ValueError("Query heads must divide into KV groups")
         _check_index(block_tables, "block_tables", 2, self.device)
         _check_index(context_lens, "context_lens", 1, self.device)
-        if block_tables.shape[0] != num_seqs or context_lens.shape[0] != num_seqs:
+        num_seqs = block_tables.shape[0]
+        if context_lens.shape[0] != num_seqs:
             raise ValueError("block_tables/context_lens must have one row per sequence")
+        if query_start_loc is None:
+            if num_tokens != num_seqs:
+                raise ValueError("decode attention takes one query row per sequence")
+        else:
+            _check_index(query_start_loc, "query_start_loc", 1, self.device)
+            if query_start_loc.shape[0] != num_seqs + 1:
+                raise ValueError("query_start_loc must have num_seqs + 1 entries")
+            if max_query_len is None:
+                lens = query_start_loc[1:] - query_start_loc[:-1]
+                max_query_len = int(lens.max().item()) if num_seqs else 0
+            if type(max_query_len) is not int or max_query_len < 0:
+                raise ValueError("max_query_len must be a non-negative int")
         if max_context_len > block_tables.shape[1] * self.block_size:
             raise ValueError("max_context_len exceeds the block table capacity")
         scale = self.head_dim ** -0.5 if scale is None else float(scale)
@@ -184,21 +208,32 @@ class PagedKVCache:
         elif need and workspace.numel() * workspace.element_size() < need:
             raise ValueError(f"workspace of {need} bytes required")
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        _native.check(
-            _native.lib().astr_paged_attention_i8(
+        ws = workspace.data_ptr() if need else None
+        lib = _native.lib()
+        if query_start_loc is None:
+            rc = lib.astr_paged_attention_i8(
                 self._descs[layer], query.data_ptr(), _DTYPE_CODES[query.dtype], query.stride(0),
                 query.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
                 block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(),
                 num_seqs, num_q_heads, max_context_len, scale, window or 0, partition_tokens,
-                workspace.data_ptr() if need else None, need, self.err_flag.data_ptr(), stream),
-            "paged_attention")
+                ws, need, self.err_flag.data_ptr(), stream)
+        else:
+            rc = lib.astr_paged_attention_varlen_i8(
+                self._descs[layer], query.data_ptr(), _DTYPE_CODES[query.dtype], query.stride(0),
+                query.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
+                query_start_loc.data_ptr(), num_tokens, max_query_len, 1 if causal else 0,
+                block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(),
+                num_seqs, num_q_heads, max_context_len, scale, window or 0, partition_tokens,
+                ws, need, self.err_flag.data_ptr(), stream)
+        _native.check(rc, "paged_attention")
         if work is not None:
+            prefill = query_start_loc is not None and max_query_len > 1
             work.backend, work.fallback_reason = BACKEND, None
-            work.page_launches += 2 if need else 1
+            work.page_launches += (2 if need else 1) + (1 if prefill else 0)
             work.query_tiles += 1
-            work.max_query_tile = max(work.max_query_tile, 1)
+            work.max_query_tile = max(work.max_query_tile, max_query_len if prefill else 1)
             work.max_key_tile = max(work.max_key_tile, self.block_size)
-            work.compiler_version = _native.lib().astr_version().decode()
+            work.compiler_version = lib.astr_version().decode()
         if check:
             self.raise_errors()
         return out

@@ -10,6 +10,9 @@ seeded N(0,1) K/V and draws the queries. Nothing here reads files.
   config2  Llama-3-8B-shaped GQA decode: 64 seqs, 32q/8kv, D 128, ctx U[128,4096],
            bf16 Q, shuffled pool sized to the total context; the step appends one
            new token per sequence (64 tokens) before attending.
+  config3  continuous-batching mixed step: 8 prefill chunks of 512 query tokens
+           (prior context U[0,2048]) packed with 120 decode rows (ctx U[256,4096]);
+           32q/8kv, D 128, bf16 Q, causal within chunks.
   config4  prefix-shared decode: 256 seqs aliasing one 2048-token prefix (128
            blocks) + private suffixes U[64,512]; 32q/8kv, D 128, bf16 Q.
   config5  long context: 16 x 32768, 64q/8kv, D 128, bf16 Q, 10% of K rows x8.
@@ -40,11 +43,39 @@ class DecodeWorkload:
     scale: float
     k_outlier_fraction: float = 0.0   # fraction of K rows multiplied by 8
     shared_prefix_blocks: int = 0     # leading blocks aliased by every row
+    query_lens: np.ndarray = None     # int32 [S] query tokens per row (None: 1 each)
     meta: dict = field(default_factory=dict)
 
     @property
     def num_seqs(self):
         return int(self.context_lens.shape[0])
+
+    @property
+    def q_lens(self):
+        if self.query_lens is None:
+            return np.ones(self.num_seqs, dtype=np.int32)
+        return self.query_lens
+
+    @property
+    def num_query_tokens(self):
+        return int(self.q_lens.sum())
+
+    @property
+    def max_query_len(self):
+        return int(self.q_lens.max()) if self.num_seqs else 0
+
+    def query_start_loc(self):
+        return np.concatenate([[0], np.cumsum(self.q_lens)]).astype(np.int32)
+
+    def prefill_flops(self):
+        """QK^T + PV flops of the rows with more than one query token under the
+        causal mask: 4*Hq*D per visible (query, key) pair."""
+        pairs = 0
+        for n, ctx in zip(self.q_lens.tolist(), self.context_lens.tolist()):
+            if n > 1:
+                prior = ctx - n
+                pairs += n * prior + n * (n + 1) // 2
+        return 4 * self.num_q_heads * self.head_dim * pairs
 
     @property
     def max_context_len(self):
@@ -59,7 +90,7 @@ class DecodeWorkload:
         every attended token, Q in, O out, block-table entries and lengths."""
         q_bytes = torch.tensor([], dtype=self.q_dtype).element_size()
         kv = self.attended_tokens * self.num_kv_heads * (2 * self.head_dim + 8)
-        qo = self.num_seqs * self.num_q_heads * self.head_dim * 2 * q_bytes
+        qo = self.num_query_tokens * self.num_q_heads * self.head_dim * 2 * q_bytes
         tables = 4 * int(np.ceil(self.context_lens / BLOCK).sum()) + 4 * self.num_seqs
         return kv + qo + tables
 
@@ -105,6 +136,20 @@ def config2(seed=2):
     tables, pool = _tables_from_lengths(lengths, rng, spare_blocks=64)
     return DecodeWorkload("config2_llama3_8b_decode", 32, 8, 128, lengths, tables, pool,
                           torch.bfloat16, seed, 128 ** -0.5)
+
+
+def config3(seed=3, num_prefill=8, chunk=512, max_prior=2048, num_decode=120,
+            decode_range=(256, 4096)):
+    """Prefill rows first (chunk tokens on top of a prior context), then decode rows;
+    context lengths count the step's own tokens."""
+    rng = np.random.default_rng(seed)
+    prior = rng.integers(0, max_prior, size=num_prefill, endpoint=True)
+    dec = rng.integers(decode_range[0], decode_range[1], size=num_decode, endpoint=True)
+    lengths = np.concatenate([prior + chunk, dec]).astype(np.int32)
+    qlens = np.concatenate([np.full(num_prefill, chunk), np.ones(num_decode)]).astype(np.int32)
+    tables, pool = _tables_from_lengths(lengths, rng, spare_blocks=16)
+    return DecodeWorkload("config3_mixed_prefill_decode", 32, 8, 128, lengths, tables, pool,
+                          torch.bfloat16, seed, 128 ** -0.5, query_lens=qlens)
 
 
 def config4(seed=4):
@@ -156,9 +201,13 @@ def scaled(workload, num_seqs=None, max_len=None, seed=None):
     else:
         pb = 0
         tables, pool = _tables_from_lengths(lengths, rng)
+    qlens = None
+    if workload.query_lens is not None:
+        qlens = np.minimum(workload.query_lens[: len(lengths)], lengths).astype(np.int32)
     return DecodeWorkload(workload.name + "_scaled", workload.num_q_heads, workload.num_kv_heads,
                           workload.head_dim, lengths, tables, pool, workload.q_dtype,
-                          workload.seed, workload.scale, workload.k_outlier_fraction, pb)
+                          workload.seed, workload.scale, workload.k_outlier_fraction, pb,
+                          query_lens=qlens)
 
 
 # ---- device materialisation ---------------------------------------------------------
@@ -191,22 +240,30 @@ def device_tables(workload, device):
             torch.from_numpy(workload.context_lens).to(device))
 
 
+def device_query_start(workload, device):
+    return torch.from_numpy(workload.query_start_loc()).to(device)
+
+
 def materialize(workload, cache, layer=0, device="cuda", keep_sources=False, hold_last=False):
     """Fill ``cache`` layer ``layer`` with every committed token of every row via the
-    HIP quantize-and-append kernel. With ``hold_last`` the last token of each row is
-    left out and returned as the step's append batch ``(k [S,Hkv,D], v, slots)``.
+    HIP quantize-and-append kernel. With ``hold_last`` the step's own tokens (the
+    last ``q_lens[row]`` of each row) are left out and returned as the step's append
+    batch ``(k [T,Hkv,D], v, slots)`` packed like the queries.
     Returns ``(sources, step)``: per-row fp32/bf16 K/V sources when
     ``keep_sources`` (else None) and the held-back batch (or None)."""
     gen = torch.Generator(device=device)
     gen.manual_seed(workload.seed)
     sources = [] if keep_sources else None
     last_k, last_v, last_slots = [], [], []
+    qlens = workload.q_lens
     for row in range(workload.num_seqs):
         k, v = kv_source(workload, row, gen, device)
         slots = torch.from_numpy(token_slots(workload, row)).to(device)
         if hold_last:
-            last_k.append(k[-1:]), last_v.append(v[-1:]), last_slots.append(slots[-1:])
-            k, v, slots = k[:-1], v[:-1], slots[:-1]
+            n = int(min(qlens[row], k.shape[0]))
+            cut = k.shape[0] - n
+            last_k.append(k[cut:]), last_v.append(v[cut:]), last_slots.append(slots[cut:])
+            k, v, slots = k[:cut], v[:cut], slots[:cut]
         if k.shape[0]:
             cache.append(layer, k, v, slots)
         if keep_sources:
@@ -222,6 +279,6 @@ def materialize(workload, cache, layer=0, device="cuda", keep_sources=False, hol
 def queries(workload, device="cuda", seed_offset=1000):
     gen = torch.Generator(device=device)
     gen.manual_seed(workload.seed + seed_offset)
-    q = torch.randn((workload.num_seqs, workload.num_q_heads, workload.head_dim), generator=gen,
-                    device=device, dtype=torch.float32)
+    q = torch.randn((workload.num_query_tokens, workload.num_q_heads, workload.head_dim),
+                    generator=gen, device=device, dtype=torch.float32)
     return q.to(workload.q_dtype)

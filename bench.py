@@ -140,10 +140,13 @@ def main():
     attn_avg_ms = sum(attn_ms) / n
     alg_bytes = w.algorithmic_bytes()
     achieved = alg_bytes / (attn_avg_ms * 1e-3) / 1e9
+    # HBM bytes per call measured by rocprofv3 (FETCH_SIZE/WRITE_SIZE, calibrated
+    # against a copy of known size) for this workload and split mode
     traffic = None
     if os.path.exists(args.traffic):
+        mode = "streamk" if args.partition == 0 else f"partition_{args.partition}"
         with open(args.traffic) as f:
-            traffic = json.load(f).get(w.name, {}).get("bytes_per_launch")
+            traffic = json.load(f).get(w.name, {}).get(mode, {}).get("bytes_per_launch")
 
     result = {
         "metric": "attended KV-tokens/s and % of HBM peak, INT8 paged decode, 1xMI355X",

@@ -130,6 +130,45 @@ int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query, int32
                             int32_t* err_flag, void* stream);
 
 /*
+ * Ragged paged attention for a continuous-batching step that mixes prompt
+ * chunks (several query tokens per sequence, chunked prefill) with decode rows.
+ * Replaces the same per-row online_attention calls of
+ * PagedAttentionRunner.forward_batch (paged_attention.py:168-215) for chunks of
+ * any length, with the visibility rules of online_attention_statistics
+ * (online_attention.py:178-188).
+ *   query/out: [num_query_tokens, num_q_heads, head_dim] packed by sequence.
+ *   query_start_loc: int32 [num_seqs + 1] device offsets (cu_seqlens):
+ *              sequence s owns token rows [qsl[s], qsl[s+1]); an entry that is
+ *              negative, decreasing or beyond num_query_tokens raises
+ *              ASTR_FLAG_BAD_INDEX and that sequence produces nothing.
+ *   max_query_len: host-side upper bound of qsl[s+1]-qsl[s]; <= 1 launches the
+ *              decode kernels only.
+ *   context_lens: int32 [num_seqs], counting the step's own tokens (the chunk
+ *              is appended before attention). Query token i of a sequence with
+ *              n query tokens sits at position ctx-n+i and sees key k iff
+ *              k <= position (causal != 0; else k < ctx) and, when window > 0,
+ *              k > position - window. ctx < n raises ASTR_FLAG_BAD_INDEX.
+ *   Other arguments as astr_paged_attention_i8 (workspace sized by
+ *   astr_paged_attention_i8_workspace_bytes for num_seqs rows; chunk rows need none).
+ * Sequences with one query token take the decode kernels (the query sees every
+ * key, as for astr_paged_attention_i8), longer ones the MFMA prefill kernel
+ * (bf16/fp16/fp32 queries; fp32 queries enter the f16 MFMAs after an exact
+ * power-of-two rescale, i.e. rounded to 11 significant bits), launched after
+ * the decode kernels on the same stream.
+ */
+int astr_paged_attention_varlen_i8(const astr_paged_kv* cache, const void* query,
+                                   int32_t q_dtype, int64_t q_token_stride,
+                                   int64_t q_head_stride, void* out, int64_t out_token_stride,
+                                   int64_t out_head_stride, const int32_t* query_start_loc,
+                                   int32_t num_query_tokens, int32_t max_query_len,
+                                   int32_t causal, const int32_t* block_tables,
+                                   int32_t block_table_stride, const int32_t* context_lens,
+                                   int32_t num_seqs, int32_t num_q_heads, int32_t max_context_len,
+                                   float scale, int32_t window, int32_t partition_tokens,
+                                   void* workspace, size_t workspace_bytes, int32_t* err_flag,
+                                   void* stream);
+
+/*
  * Workspace bytes astr_paged_attention_i8 needs for its split-K partials on
  * the current device (0 when no row can span more than one partition).
  * Analogue of KernelSpec.workspace_bytes (src/aster/core/contracts.py:102-134).

@@ -294,6 +294,8 @@ def paged_attention(query, k_codes, k_scales, v_codes, v_scales, block_tables, c
         ctx, qn = int(context_lens[b]), query_lens[b]
         q = query[cursor : cursor + qn].transpose(1, 0, 2)[None]
         cursor += qn
+        if qn == 0:  # a sequence with no query token this step produces no rows
+            continue
         if ctx == 0:  # no visible key: the fully-masked row is zero (online_attention.py:37)
             width = v_codes.shape[-1]
             acc = np.float64 if query.dtype == np.float64 else np.float32

@@ -18,15 +18,20 @@ def arena_numpy(cache, layer=0):
 
 
 def oracle_decode(workload_or_tables, cache, query, layer=0, context_lens=None, scale=None,
-                  window=None):
+                  window=None, query_lens=None, causal=True):
+    """The oracle's row-by-row paged attention (paged_attention.py:168-215) over this
+    cache layer; a workload supplies tables, lengths, scale and query counts."""
     if context_lens is None:
-        tables, lens = workload_or_tables.block_tables, workload_or_tables.context_lens
-        scale = workload_or_tables.scale if scale is None else scale
+        w = workload_or_tables
+        tables, lens = w.block_tables, w.context_lens
+        scale = w.scale if scale is None else scale
+        if query_lens is None and w.query_lens is not None:
+            query_lens = w.query_lens
     else:
         tables, lens = workload_or_tables, context_lens
     q = query.float().cpu().numpy()
     return ref.paged_attention(q, *arena_numpy(cache, layer), tables, lens, block_size=16,
-                               scale=scale, window=window)
+                               scale=scale, window=window, query_lens=query_lens, causal=causal)
 
 
 def assert_attention_close(actual, expected, atol=ATOL, rtol=RTOL):
