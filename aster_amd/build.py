@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import concurrent.futures
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -31,6 +32,10 @@ FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 NOISE = "is not a recognized feature for this target"
+# Every kernel must run without scratch memory: a lambda or array the compiler
+# cannot keep in registers lands in per-lane scratch and costs several times the
+# kernel's HBM time, so the build rejects it.
+RESOURCE_REMARKS = "-Rpass-analysis=kernel-resource-usage"
 
 
 def hipcc():
@@ -40,13 +45,31 @@ def hipcc():
     return path
 
 
+def _scratch_kernels(remarks):
+    """Kernels whose resource-usage remark reports a non-zero scratch size."""
+    bad, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            bad.append(f"{name} ({m.group(1)} bytes/lane)")
+    return bad
+
+
 def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
-    err = "\n".join(l for l in proc.stderr.splitlines() if NOISE not in l)
+    lines = [l for l in proc.stderr.splitlines() if NOISE not in l]
+    err = "\n".join(l for l in lines if "kernel-resource-usage" not in l)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
+    bad = _scratch_kernels("\n".join(lines))
+    if bad:
+        raise RuntimeError("kernels using scratch memory:\n  " + "\n  ".join(bad))
     if verbose and err.strip():
         print(err, file=sys.stderr)
 
@@ -56,7 +79,7 @@ def build(verbose=False, jobs=None):
     obj_dir = os.path.join(OUT_DIR, "obj")
     os.makedirs(obj_dir, exist_ok=True)
     objs = [os.path.join(obj_dir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
-    compiles = [[hipcc(), *FLAGS, "-I", os.path.join(ROOT, "include"), "-c",
+    compiles = [[hipcc(), *FLAGS, RESOURCE_REMARKS, "-I", os.path.join(ROOT, "include"), "-c",
                  os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
     jobs = jobs or min(len(compiles), os.cpu_count() or 1, 8)
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:

@@ -47,6 +47,7 @@ struct AttnArgs {
   // settles total_waves from the kernel's occupancy.
   int32_t total_waves;
   int32_t min_waves;
+  int32_t pref_waves;  // stream-K: waves the GPU holds at once (set by the launcher)
   float* ws_o;          // partial acc (layout depends on the split mode)
   float* ws_ml;         // partial (m, l)
   int32_t* ws_seq;      // stream-K: per-sequence block prefix [num_seqs + 1]

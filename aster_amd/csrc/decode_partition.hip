@@ -60,11 +60,12 @@ struct Shared {
   float o[kWaves][G][D];
 };
 
-// Combine the 4 waves of the workgroup (already in `sh`) and write either the
-// normalised output (single partition) or this partition's partial.
+// Combine the 4 waves of the workgroup (already in `sh`, heads head0 .. head0+G-1)
+// and write either the normalised output (single partition) or this partition's
+// partial.
 template <typename QT, int G, int D>
 __device__ void finish_partition(const AttnArgs& a, Shared<G, D>& sh, const RowPlan& row,
-                                 int seq, int tok, int kvh, int part) {
+                                 int seq, int tok, int head0, int part) {
   const bool split = row.num_parts > 1;
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int g = idx / D, d = idx % D;
@@ -79,7 +80,7 @@ __device__ void finish_partition(const AttnArgs& a, Shared<G, D>& sh, const RowP
       L = fmaf(sh.l[w][g], f, L);
       O = fmaf(sh.o[w][g][d], f, O);
     }
-    const int h = kvh * G + g;
+    const int h = head0 + g;
     if (!split) {
       QT* op = static_cast<QT*>(a.out) + (int64_t)tok * a.o_tok + (int64_t)h * a.o_head;
       op[d] = from_float<QT>(O / fmaxf(L, FLT_MIN));
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   float l = 0.f;
   bool bad_score = false;
 
-  auto step = [&](int i, char* st) {
+  auto step = [&](int i, char* st) __attribute__((always_inline)) {
     // wait until block i has landed: later stages (up to NS-1) may stay in flight
     const int later = min(NS - 1, nblk - 1 - i);
     if (later >= 2) wait_vmcnt<2 * S::kLoads>();
@@ -206,7 +207,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
       for (int j = 0; j < 4; ++j) sh.o[wave][r][VB * (4 * qg + j) + n] = acc[n][j];
   }
   __syncthreads();
-  finish_partition<QT, G, D>(a, sh, row, seq, tok, kvh, part);
+  finish_partition<QT, G, D>(a, sh, row, seq, tok, kvh * G, part);
 }
 
 // ================================ exact fp32 VALU kernel (fp32 queries)
@@ -219,8 +220,16 @@ struct ValuTile {
   float vs[NL];
 };
 
-template <typename QT, int D, int G>
+// Heads of a GQA group one VALU workgroup serves: a lane keeps 16 query values and
+// 16 accumulators per head in registers, so large groups at D >= 128 are served
+// in passes of 4 heads (each pass re-reads the group's K/V) instead of spilling.
+constexpr int valu_heads(int D, int group) { return (D >= 128 && group > 4) ? 4 : group; }
+
+// GROUP: the GQA group size; G: the heads of it this workgroup serves
+// (blockIdx.y = kv head * GROUP/G + pass).
+template <typename QT, int D, int GROUP, int G>
 __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
+  static_assert(GROUP % G == 0, "passes must tile the group");
   constexpr int LPT = D / 16;             // lanes per token row
   constexpr int TPL = kWave / LPT;        // token rows per load instruction
   constexpr int NL = kBlockTokens / TPL;  // load instructions per block
@@ -228,7 +237,9 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
   static_assert(NL >= 1 && NL * TPL == kBlockTokens, "unsupported head_dim");
 
   __shared__ Shared<G, D> sh;
-  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int part = blockIdx.x, seq = blockIdx.z;
+  const int kvh = blockIdx.y / (GROUP / G);
+  const int head0 = kvh * GROUP + (blockIdx.y % (GROUP / G)) * G;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   const int tok = decode_token(a, seq);
@@ -244,7 +255,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
 
   float qf[G][16];
   {
-    const QT* qp = static_cast<const QT*>(a.q) + (int64_t)tok * a.q_tok + (int64_t)kvh * G * a.q_head + d0;
+    const QT* qp = static_cast<const QT*>(a.q) + (int64_t)tok * a.q_tok + (int64_t)head0 * a.q_head + d0;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       constexpr int kVec = 16 / sizeof(QT);
@@ -270,7 +281,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
   const int8_t* vbase = a.cache.v_codes + (int64_t)kvh * a.cache.code_head_stride + lane * 16;
   const float* ksbase = a.cache.k_scales + (int64_t)kvh * a.cache.scale_head_stride + lrow;
   const float* vsbase = a.cache.v_scales + (int64_t)kvh * a.cache.scale_head_stride + lrow;
-  auto load = [&](int phys, ValuTile<NL>& t) {
+  auto load = [&](int phys, ValuTile<NL>& t) __attribute__((always_inline)) {
     const int8_t* kp = kbase + (int64_t)phys * a.cache.code_block_stride;
     const int8_t* vp = vbase + (int64_t)phys * a.cache.code_block_stride;
     const float* ksp = ksbase + (int64_t)phys * a.cache.scale_block_stride;
@@ -286,13 +297,13 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
 
   const int ids = wave_block_ids(a, seq, first, nbw, lane);
   bool bad_index = false, bad_score = false;
-  auto fetch = [&](int i, ValuTile<NL>& t) -> bool {
+  auto fetch = [&](int i, ValuTile<NL>& t) -> bool __attribute__((always_inline)) {
     const int phys = __builtin_amdgcn_readlane(ids, i);
     const bool ok = (unsigned)phys < (unsigned)a.cache.num_blocks;
     if (ok) load(phys, t);
     return ok;
   };
-  auto process = [&](int i, const ValuTile<NL>& cur) {
+  auto process = [&](int i, const ValuTile<NL>& cur) __attribute__((always_inline)) {
     const int blk = first + kWaves * i;
     float s[NL][G];
 #pragma unroll
@@ -387,7 +398,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
       for (int e = 0; e < 16; ++e) sh.o[wave][g][d0 + e] = acc[g][e];
   }
   __syncthreads();
-  finish_partition<QT, G, D>(a, sh, row, seq, tok, kvh, part);
+  finish_partition<QT, G, D>(a, sh, row, seq, tok, head0, part);
 }
 
 
@@ -466,7 +477,10 @@ template <typename QT, int D, int G>
 int launch(const AttnArgs& a, hipStream_t stream) {
   const dim3 grid((uint32_t)a.max_parts, (uint32_t)a.cache.num_kv_heads, (uint32_t)a.num_seqs);
   if constexpr (sizeof(QT) == 4) {
-    hipLaunchKernelGGL((decode_valu_kernel<QT, D, G>), grid, dim3(kWaves * kWave), 0, stream, a);
+    constexpr int GS = valu_heads(D, G);
+    const dim3 vgrid(grid.x, grid.y * (G / GS), grid.z);
+    hipLaunchKernelGGL((decode_valu_kernel<QT, D, G, GS>), vgrid, dim3(kWaves * kWave), 0, stream,
+                       a);
   } else {
     hipLaunchKernelGGL((decode_mfma_kernel<QT, D, G, kStages>), grid, dim3(kWaves * kWave), 0,
                        stream, a);

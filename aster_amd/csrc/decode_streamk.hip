@@ -20,6 +20,19 @@ namespace {
 constexpr int kStagesSK = 2;
 constexpr int kMaxSeqsSK = 512;  // per-sequence table lives in LDS
 
+// Waves that share the B visible blocks of a launch: the resident waves (one
+// round, no tail), more only where that would put over kMaxBlocksPerWave blocks on
+// a wave, never more than launched, and at most one wave per block (so every wave
+// below W owns at least one block and a row split over waves w0..w1 has exactly
+// one piece in each of them; the merge relies on it). The decode and the merge
+// kernel both derive W from B with this function.
+__device__ __forceinline__ int64_t streamk_waves(const AttnArgs& a, int64_t B) {
+  int64_t w = (B + kMaxBlocksPerWave - 1) / kMaxBlocksPerWave;
+  if (w < a.pref_waves) w = a.pref_waves;
+  if (w > a.total_waves) w = a.total_waves;
+  return w < B ? w : B;
+}
+
 // Wave owning flat block b when wave w owns [floor(B*w/W), floor(B*(w+1)/W)).
 __device__ __forceinline__ int64_t wave_of(int64_t b, int64_t B, int64_t W) {
   return ((b + 1) * W - 1) / B;
@@ -99,11 +112,9 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(AttnArgs a) {
     if (s_cu[s + 1] == s_cu[s] && s_ctx[s] >= 0) store_row_zero<QT>(a, s_tok[s], D);
 
   // ---- 2. this wave's block range and its block ids / rows (lane j <-> block b0 + j)
-  // At most one wave per block: every wave below W then owns at least one block, so a
-  // row whose blocks span waves w0..w1 has exactly one piece in each of them (the merge
-  // relies on it). Waves from W on have nothing to do.
+  // Waves from W on have nothing to do.
   const int64_t B = (int64_t)bseq * hkv;
-  const int64_t W = min((int64_t)a.total_waves, B);
+  const int64_t W = streamk_waves(a, B);
   const int64_t gw = (int64_t)blockIdx.x * kWaves + wave;
   int64_t b0 = 0;
   int n = 0;
@@ -143,7 +154,7 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(AttnArgs a) {
   char* const st0 = lds0 + wave * S::kBytes;
   char* const st1 = lds1 + wave * S::kBytes;
   char* const st2 = lds2 + (NS == 3 ? wave * S::kBytes : 0);
-  auto issue = [&](int j, char* st) {
+  auto issue = [&](int j, char* st) __attribute__((always_inline)) {
     stage_block<D>(a, __builtin_amdgcn_readlane(ids, j),
                    __builtin_amdgcn_readlane(row_id, j) / nseq, lane, st);
   };
@@ -162,7 +173,7 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(AttnArgs a) {
   RowSpan psp = row_span(a, nblk > 0 ? s_ctx[pseq] : 0);
   int64_t pfb = (int64_t)pkvh * bseq + (nblk > 0 ? s_cu[pseq] : 0);  // flat first block of the row
 
-  auto flush = [&](int iend) {
+  auto flush = [&](int iend) __attribute__((always_inline)) {
     float lt = l + shfl_xor(l, 16);
     lt += shfl_xor(lt, 32);
     const int64_t pfe = pfb + (s_cu[pseq + 1] - s_cu[pseq]) - 1;
@@ -191,7 +202,7 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(AttnArgs a) {
     }
   };
 
-  auto step = [&](int i, char* st) {
+  auto step = [&](int i, char* st) __attribute__((always_inline)) {
     const int rid = __builtin_amdgcn_readlane(row_id, i);
     if (rid != cur) {  // a new row starts inside this wave's range
       flush(i - 1);
@@ -243,15 +254,14 @@ __global__ __launch_bounds__(256) void merge_streamk_kernel(AttnArgs a) {
   const int kvh = h / G, g = h % G;
   const int cu0 = a.ws_seq[seq], cu1 = a.ws_seq[seq + 1], bseq = a.ws_seq[a.num_seqs];
   if (cu1 == cu0) return;  // empty or not a decode row: nothing to merge
-  // the decode kernel's wave count: one wave per block at most
   const int64_t B = (int64_t)bseq * a.cache.num_kv_heads;
-  const int64_t W = min((int64_t)a.total_waves, B);
+  const int64_t W = streamk_waves(a, B);
   const int64_t fb = (int64_t)kvh * bseq + cu0, fe = fb + (cu1 - cu0) - 1;
   const int64_t w0 = wave_of(fb, B, W), w1 = wave_of(fe, B, W);
   if (w0 == w1) return;  // written whole by one wave
   const int pieces = (int)(w1 - w0 + 1);
   const bool first_is_tail = B * w0 / W < fb;  // the row is w0's last piece (slot 1)
-  auto slot_of = [&](int p) -> int64_t {
+  auto slot_of = [&](int p) -> int64_t __attribute__((always_inline)) {
     const int64_t w = w0 + p;
     return (w * 2 + (p == 0 && first_is_tail ? 1 : 0)) * G + g;
   };
@@ -331,12 +341,15 @@ int device_cus() {
 template <typename QT, int D, int G>
 int launch(AttnArgs a, hipStream_t stream) {
   auto kernel = decode_streamk_kernel<QT, D, G, kStagesSK>;
-  // one wave per resident slot (whole workgroups), at least min_waves, at most the
-  // workspace capacity passed in total_waves
-  int64_t waves = (int64_t)device_cus() * resident_per_cu(kernel) * kWaves;
+  // launch one wave per resident slot (whole workgroups) and at least min_waves (the
+  // host-side bound), at most the workspace capacity passed in total_waves; the
+  // kernels settle the waves they use from the actual block count
+  const int64_t resident = (int64_t)device_cus() * resident_per_cu(kernel) * kWaves;
+  int64_t waves = resident;
   if (waves < a.min_waves) waves = (a.min_waves + kWaves - 1) / kWaves * kWaves;
   if (waves > a.total_waves) waves = a.total_waves / kWaves * kWaves;
   a.total_waves = (int32_t)waves;
+  a.pref_waves = (int32_t)(resident < waves ? resident : waves);
   const int wgs = (int)(waves / kWaves);
   hipLaunchKernelGGL(kernel, dim3(wgs), dim3(kWaves * kWave), 0, stream, a);
   const int units = a.num_seqs * a.num_q_heads;

@@ -332,11 +332,11 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   // holds the id for step (i + 64*k); reloaded every 64 steps.
   const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
   int ids = 0;
-  auto load_ids = [&](int s0) {
+  auto load_ids = [&](int s0) __attribute__((always_inline)) {
     const int blk = b_lo + (s0 + lane) * kWaves + wave;
     ids = (s0 + lane < nsteps && blk < b_hi) ? bt[blk] : 0;
   };
-  auto issue = [&](int step, char* buf) -> bool {
+  auto issue = [&](int step, char* buf) -> bool __attribute__((always_inline)) {
     if (b_lo + step * kWaves + wave >= b_hi) return false;
     const int id = __builtin_amdgcn_readlane(ids, step % kWave);
     if ((unsigned)id >= (unsigned)a.cache.num_blocks) {

@@ -25,6 +25,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16 MFMA, MI355X
 
 
 def parse():
@@ -32,7 +33,9 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--config", default="config2", choices=["config2", "config4", "config5"])
+    p.add_argument("--config", default="config2",
+                   choices=["config2", "config3", "config4", "config5"],
+                   help="config2 is the headline workload; the others are extra measurements")
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--partition", type=int, default=0,
                    help="0 = automatic (stream-K); >0 = fixed split-K partition tokens")
@@ -71,6 +74,54 @@ def cpu_baseline(w, cache, step_batch, q, budget_s):
                       f"{w.attended_tokens} KV-tokens) in {elapsed:.1f}s, numpy oracle, 1 thread"}
 
 
+def prefill_measurement(w, cache, q, L, args, device):
+    """The rows with more than one query token alone (one varlen call over them):
+    MFMA flops of the causal chunks / call time. The call also launches the decode
+    kernels, which find no decode row, so the rate is a lower bound for the prefill
+    kernel itself (rocprofv3 gives the kernel's own time)."""
+    import numpy as np
+    import torch
+
+    from aster_amd import workloads as wl
+
+    rows = np.nonzero(w.q_lens > 1)[0]
+    sub = wl.DecodeWorkload(w.name + "_prefill_rows", w.num_q_heads, w.num_kv_heads,
+                            w.head_dim, w.context_lens[rows], w.block_tables[rows],
+                            w.num_blocks, w.q_dtype, w.seed, w.scale, query_lens=w.q_lens[rows])
+    qsl_h = w.query_start_loc()
+    take = torch.as_tensor(np.concatenate([np.arange(qsl_h[r], qsl_h[r + 1]) for r in rows]),
+                           device=device).long()
+    qp = q[take].contiguous()
+    tables, lens = wl.device_tables(sub, device)
+    qsl = wl.device_query_start(sub, device)
+    out = torch.empty_like(qp)
+    ws = cache.workspace(sub.num_seqs, sub.num_q_heads, sub.max_context_len, args.partition)
+
+    def call(layer):
+        cache.paged_attention(layer, qp, tables, lens, max_context_len=sub.max_context_len,
+                              scale=sub.scale, partition_tokens=args.partition, out=out,
+                              workspace=ws, query_start_loc=qsl, max_query_len=sub.max_query_len)
+
+    for i in range(5):
+        call(i % L)
+    n = max(args.steps // 4, 20)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n)]
+    torch.cuda.synchronize()
+    for i in range(n):
+        evs[i][0].record()
+        call(i % L)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    cache.raise_errors()
+    avg_ms = sum(a.elapsed_time(b) for a, b in evs) / n
+    flops = sub.prefill_flops()
+    tflops = flops / (avg_ms * 1e-3) / 1e12
+    return {"rows": int(len(rows)), "query_tokens": sub.num_query_tokens, "flops": flops,
+            "call_us": avg_ms * 1e3, "achieved_tflops": tflops, "bound": "mfma",
+            "peak_tflops": MFMA_F16_PEAK_TFLOPS, "frac": tflops / MFMA_F16_PEAK_TFLOPS}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -92,6 +143,8 @@ def main():
         cache.codes[:, layer].copy_(cache.codes[:, 0])
         cache.scales[:, layer].copy_(cache.scales[:, 0])
     tables, lens = wl.device_tables(w, device)
+    varlen = w.query_lens is not None
+    qsl = wl.device_query_start(w, device) if varlen else None
     q = wl.queries(w, device)
     out = torch.empty_like(q)
     k_new, v_new, slots = step_batch
@@ -101,7 +154,8 @@ def main():
     def attend(layer):
         cache.paged_attention(layer, q, tables, lens, max_context_len=w.max_context_len,
                               scale=w.scale, partition_tokens=args.partition, out=out,
-                              workspace=workspace)
+                              workspace=workspace, query_start_loc=qsl,
+                              max_query_len=w.max_query_len if varlen else None)
 
     def step(i):
         layer = i % L
@@ -166,7 +220,8 @@ def main():
             "num_kv_heads": w.num_kv_heads, "head_dim": w.head_dim, "block_size": 16,
             "attended_kv_tokens": w.attended_tokens, "max_context_len": w.max_context_len,
             "append_tokens": int(k_new.shape[0]), "partition_tokens": args.partition,
-            "layer_arenas": L, "step": "quantize_append(64 tok) + paged_attention",
+            "layer_arenas": L,
+            "step": f"quantize_append({int(k_new.shape[0])} tok) + paged_attention",
         },
         "hbm_fraction_of_step": alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "roofline": {
@@ -179,6 +234,10 @@ def main():
         },
         "wall_s_timed_region": wall,
     }
+    if varlen:
+        result["config"]["query_tokens"] = w.num_query_tokens
+        result["config"]["max_query_len"] = w.max_query_len
+        result["prefill"] = prefill_measurement(w, cache, q, L, args, device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, cache, step_batch, q, args.cpu_seconds)
     print(json.dumps(result), flush=True)
