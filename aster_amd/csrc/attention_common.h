@@ -224,6 +224,39 @@ __device__ __forceinline__ void load_query(const AttnArgs& a, int tok, int kvh, 
   }
 }
 
+// The G query rows of kv head kvh, token row tok, by direct-to-LDS loads into
+// `dst` as [G][D] elements of QT (16 bytes per lane, D*sizeof(QT)/16 lanes per
+// head): ceil(G*D*sizeof(QT)/1024) vector-memory instructions.
+template <typename QT, int D, int G>
+__device__ __forceinline__ void stage_query(const AttnArgs& a, int tok, int kvh, int lane,
+                                            char* dst) {
+  constexpr int kLanesPerHead = D * (int)sizeof(QT) / 16;
+  constexpr int kHeadsPerLoad = kWave / kLanesPerHead;
+  constexpr int kLoads = (G + kHeadsPerLoad - 1) / kHeadsPerLoad;
+  const QT* q0 = static_cast<const QT*>(a.q) + (int64_t)tok * a.q_tok;
+#pragma unroll
+  for (int k = 0; k < kLoads; ++k) {
+    const int g = k * kHeadsPerLoad + lane / kLanesPerHead;
+    if (g < G) {
+      const char* src = reinterpret_cast<const char*>(q0 + (int64_t)(kvh * G + g) * a.q_head) +
+                        (lane % kLanesPerHead) * 16;
+      lds_dma_x4(src, lds_addr(dst) + k * 1024);
+    }
+  }
+}
+
+// Query row g of a stage_query buffer in the QueryRaw lane layout.
+template <typename QT, int D>
+__device__ __forceinline__ void lds_query(const char* buf, int g, int qg, QueryRaw<D>& q) {
+  static_assert(sizeof(QT) == 2, "16-bit queries");
+  const char* row = buf + (g * D + 16 * qg) * (int)sizeof(QT);
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h) {
+    q.w[h][0] = *reinterpret_cast<const uint4*>(row + 64 * h * (int)sizeof(QT));
+    q.w[h][1] = *reinterpret_cast<const uint4*>(row + 64 * h * (int)sizeof(QT) + 16);
+  }
+}
+
 // f16 B-operands of the QK MFMAs after an exact 2^-e rescale keeping max|q| below
 // 2^15 (e folded into the returned score factor). Cross-lane: call in uniform
 // control flow.

@@ -104,6 +104,19 @@ __device__ __forceinline__ float wave_max(float x) {
   return x;
 }
 
+// Sum over the 64 lanes (every lane gets it): after the xor-1/xor-2 butterflies a
+// lane holds its quad's sum, and each mirror step adds the mirrored (disjoint)
+// group of the same size.
+__device__ __forceinline__ float wave_sum(float x) {
+  x += dpp<kDppXor1>(x);
+  x += dpp<kDppXor2>(x);
+  x += dpp<kDppHalfMirror>(x);
+  x += dpp<kDppMirror>(x);
+  x += shfl_xor(x, 16);
+  x += shfl_xor(x, 32);
+  return x;
+}
+
 // int8 byte `b` of a packed dword, as float (exact).
 __device__ __forceinline__ float i8_to_f(uint32_t w, int b) {
   return (float)(int8_t)(w >> (8 * b));

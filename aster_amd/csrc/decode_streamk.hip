@@ -1,16 +1,17 @@
 // Stream-K paged decode attention (gfx950, bf16/fp16 queries).
 //
-// The visible 16-token blocks of all (kv head, sequence) rows are laid end to
-// end (kv-head major, then sequence, then block) and cut into equal contiguous
-// ranges, one per wave of a grid sized to the GPU's resident waves. Every wave
-// therefore streams the same number of blocks (no partially filled last round,
-// whatever the context lengths), through a per-wave LDS ring of blocks filled
-// by direct global->LDS loads and the MFMA step of attention_common.h. Where a
-// range begins or ends inside a row, the wave writes a partial (m, l, acc) for
-// that piece; rows a single wave covers entirely are normalised and written
-// directly. A wave owns at most two partial slots (its first and its last
-// piece), and merge_streamk_kernel combines the pieces of every split row with
-// the merge_softmax rule (online_attention.py:42-63).
+// The visible 16-token blocks of all sequences are laid end to end (sequence,
+// then block) and cut into Wr equal contiguous ranges; wave gw streams range
+// gw / Hkv for kv head gw % Hkv, so the Hkv waves working on a range at the same
+// time read the same blocks for different heads (all heads of a block sit in one
+// contiguous stretch of the arena) and every wave streams the same number of
+// blocks whatever the context lengths. Blocks go through a per-wave LDS ring
+// filled by direct global->LDS loads and the MFMA step of attention_common.h.
+// Where a range begins or ends inside a row (kv head, sequence), the wave writes
+// a partial (m, l, acc) for that piece; rows a single wave covers entirely are
+// normalised and written directly. A wave owns at most two partial slots (its
+// first and its last piece), and merge_streamk_kernel combines the pieces of
+// every split row with the merge_softmax rule (online_attention.py:42-63).
 #include "attention_common.h"
 
 namespace astr {
@@ -19,23 +20,24 @@ namespace {
 
 constexpr int kStagesSK = 2;
 constexpr int kMaxSeqsSK = 512;  // per-sequence table lives in LDS
+constexpr int kFastPieces = 16;  // merge: rows split into at most this many pieces load at once
 
-// Waves that share the B visible blocks of a launch: the resident waves (one
-// round, no tail), more only where that would put over kMaxBlocksPerWave blocks on
-// a wave, never more than launched, and at most one wave per block (so every wave
-// below W owns at least one block and a row split over waves w0..w1 has exactly
-// one piece in each of them; the merge relies on it). The decode and the merge
-// kernel both derive W from B with this function.
-__device__ __forceinline__ int64_t streamk_waves(const AttnArgs& a, int64_t B) {
-  int64_t w = (B + kMaxBlocksPerWave - 1) / kMaxBlocksPerWave;
-  if (w < a.pref_waves) w = a.pref_waves;
-  if (w > a.total_waves) w = a.total_waves;
-  return w < B ? w : B;
+// Ranges per kv head over the Bh visible blocks of one head: the resident waves
+// (one round, no tail), more only where that would put over kMaxBlocksPerWave
+// blocks on a wave, never more than launched, and at most one range per block (so
+// every range owns at least one block and a row split over ranges r0..r1 has
+// exactly one piece in each of them; the merge relies on it). The decode and the
+// merge kernel both derive Wr from Bh with this function.
+__device__ __forceinline__ int64_t streamk_ranges(const AttnArgs& a, int64_t Bh, int hkv) {
+  int64_t w = (Bh + kMaxBlocksPerWave - 1) / kMaxBlocksPerWave;
+  if (w < a.pref_waves / hkv) w = a.pref_waves / hkv;
+  if (w > a.total_waves / hkv) w = a.total_waves / hkv;
+  return w < Bh ? w : Bh;
 }
 
-// Wave owning flat block b when wave w owns [floor(B*w/W), floor(B*(w+1)/W)).
-__device__ __forceinline__ int64_t wave_of(int64_t b, int64_t B, int64_t W) {
-  return ((b + 1) * W - 1) / B;
+// Range owning block b when range r owns [floor(Bh*r/Wr), floor(Bh*(r+1)/Wr)).
+__device__ __forceinline__ int64_t range_of(int64_t b, int64_t Bh, int64_t Wr) {
+  return ((b + 1) * Wr - 1) / Bh;
 }
 
 template <typename QT>
@@ -46,17 +48,16 @@ __device__ __forceinline__ void store_row_zero(const AttnArgs& a, int tok, int D
 }
 
 template <typename QT, int D, int G, int NS>
-__global__ __launch_bounds__(256) void decode_streamk_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void decode_streamk_kernel(AttnArgs a) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   static_assert(G >= 1 && G <= 16, "GQA group");
-  static_assert(NS == 2 || NS == 3, "stages");
+  static_assert(NS == 2, "stream-K runs two LDS stages per wave");
   using S = Stage<D>;
   constexpr int NPV = D / 16;
   constexpr int VB = D / 16;
 
   __shared__ __attribute__((aligned(16))) char lds0[kWaves * S::kBytes];
   __shared__ __attribute__((aligned(16))) char lds1[kWaves * S::kBytes];
-  __shared__ __attribute__((aligned(16))) char lds2[NS == 3 ? kWaves * S::kBytes : 16];
   __shared__ int s_ctx[kMaxSeqsSK];  // -1: not a decode row
   __shared__ int s_tok[kMaxSeqsSK];  // query/output token row
   __shared__ int s_cu[kMaxSeqsSK + 1];
@@ -111,24 +112,23 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(AttnArgs a) {
   for (int s = blockIdx.x; s < nseq; s += gridDim.x)
     if (s_cu[s + 1] == s_cu[s] && s_ctx[s] >= 0) store_row_zero<QT>(a, s_tok[s], D);
 
-  // ---- 2. this wave's block range and its block ids / rows (lane j <-> block b0 + j)
-  // Waves from W on have nothing to do.
-  const int64_t B = (int64_t)bseq * hkv;
-  const int64_t W = streamk_waves(a, B);
+  // ---- 2. this wave's head, block range and block ids / rows (lane j <-> block b0 + j);
+  // waves from Wr * Hkv on have nothing to do
+  const int64_t Wr = streamk_ranges(a, bseq, hkv);
   const int64_t gw = (int64_t)blockIdx.x * kWaves + wave;
+  const int kv = (int)(gw % hkv);
+  const int64_t rg = gw / hkv;
   int64_t b0 = 0;
   int n = 0;
-  if (gw < W) {
-    b0 = B * gw / W;
-    n = (int)(B * (gw + 1) / W - b0);
+  if (rg < Wr) {
+    b0 = (int64_t)bseq * rg / Wr;
+    n = (int)((int64_t)bseq * (rg + 1) / Wr - b0);
   }
   const bool too_long = n > kMaxBlocksPerWave;  // contexts beyond the declared maximum
   if (too_long) n = kMaxBlocksPerWave;
   int row_id = 0, ids = 0;  // row id = kv_head * nseq + seq
   if (lane < n) {
-    const int64_t b = b0 + lane;
-    const int kv = (int)(b / bseq);
-    const int rem = (int)(b - (int64_t)kv * bseq);
+    const int rem = (int)(b0 + lane);
     int lo = 0, hi = nseq;  // s_cu[lo] <= rem < s_cu[hi]
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
@@ -139,46 +139,70 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(AttnArgs a) {
     ids = a.block_tables[(int64_t)lo * a.bt_stride + sp.first_blk + rem - s_cu[lo]];
     row_id = kv * nseq + lo;
   }
-  // first row's query: issued with the block ids, converted before any staging
-  QueryRaw<D> qr;
   const int row0 = __builtin_amdgcn_readfirstlane(row_id);
-  if (n > 0) load_query<QT, D, G>(a, s_tok[row0 % nseq], row0 / nseq, r, qg, qr);
   const bool bad_index =
       too_long || __ballot(lane < n && (unsigned)ids >= (unsigned)a.cache.num_blocks) != 0;
   const int nblk = bad_index ? 0 : n;
 
-  half8_t qop[D / 32];
-  float cf = 0.f;
-  if (nblk > 0) cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop);
-
   char* const st0 = lds0 + wave * S::kBytes;
   char* const st1 = lds1 + wave * S::kBytes;
-  char* const st2 = lds2 + (NS == 3 ? wave * S::kBytes : 0);
   auto issue = [&](int j, char* st) __attribute__((always_inline)) {
     stage_block<D>(a, __builtin_amdgcn_readlane(ids, j),
                    __builtin_amdgcn_readlane(row_id, j) / nseq, lane, st);
   };
-  if (0 < nblk) issue(0, st0);
-  if (1 < nblk) issue(1, st1);
-  if (NS == 3 && 2 < nblk) issue(2, st2);
+  // First row's query: its G head rows go by direct-to-LDS loads into stage 1
+  // together with block 0, so the block stream starts without waiting for it;
+  // block 1 takes stage 1 once the query has been read out.
+  QueryRaw<D> qr;
+  half8_t qop[D / 32];
+  float cf = 0.f;
+  if (nblk > 0) {
+    stage_query<QT, D, G>(a, s_tok[row0 % nseq], row0 / nseq, lane, st1);
+    issue(0, st0);
+    wait_vmcnt<S::kLoads>();  // the query has landed; block 0 may still be in flight
+    lds_query<QT, D>(st1, gvalid ? r : 0, qg, qr);
+    cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop);
+    if (1 < nblk) issue(1, st1);  // after the query reads above (their values are consumed)
+  }
 
-  // ---- 3. stream the blocks, one piece (row) at a time
+  // ---- 3. stream the blocks, one piece (the run of one row's blocks) at a time;
+  // block i sits in stage i % 2 and block i + 2 is issued into it once consumed
   float4_t acc[NPV];
-#pragma unroll
-  for (int k = 0; k < NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m = gvalid ? -INFINITY : 0.f, l = 0.f;
+  float m = 0.f, l = 0.f;
   bool bad_score = false;
-  int cur = row0, pstart = 0;
-  int pseq = row0 % nseq, pkvh = row0 / nseq;
-  RowSpan psp = row_span(a, nblk > 0 ? s_ctx[pseq] : 0);
-  int64_t pfb = (int64_t)pkvh * bseq + (nblk > 0 ? s_cu[pseq] : 0);  // flat first block of the row
-
-  auto flush = [&](int iend) __attribute__((always_inline)) {
+  int i = 0;
+  while (i < nblk) {
+    const int rid = __builtin_amdgcn_readlane(row_id, i);
+    // row ids grow with the lane: the piece ends at the first lane holding a larger id
+    const uint64_t beyond = __ballot(lane < nblk && row_id > rid);
+    const int iend = beyond ? (int)__builtin_ctzll(beyond) : nblk;
+    const int pstart = i;
+    const int pseq = rid % nseq, pkvh = rid / nseq;
+    const RowSpan psp = row_span(a, s_ctx[pseq]);
+    const int64_t pfb = s_cu[pseq];  // first block of the row in the per-head order
+    if (i > 0) {  // a new row starts inside this wave's range
+      load_query<QT, D, G>(a, s_tok[pseq], pkvh, r, qg, qr);
+      cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop);
+    }
+#pragma unroll
+    for (int k = 0; k < NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+    m = gvalid ? -INFINITY : 0.f;  // invalid head columns never contribute
+    l = 0.f;
+    const int blk0 = psp.first_blk + (int)(b0 + i - pfb);
+    for (; i < iend; ++i) {
+      char* const st = (i & 1) ? st1 : st0;
+      if (i + 1 < nblk) wait_vmcnt<S::kLoads>();  // block i + 1 may stay in flight
+      else wait_vmcnt<0>();
+      mfma_block<D, G>(st, qop, cf, (blk0 + i - pstart) * kBlockTokens, psp.kv_begin, psp.ctx, r,
+                       qg, acc, m, l, bad_score);
+      if (i + 2 < nblk) issue(i + 2, st);
+    }
+    // write the piece: the final output when the whole row is in this wave, else a
+    // partial in slot 0 (the piece starts the wave's range) or 1 (it ends it)
     float lt = l + shfl_xor(l, 16);
     lt += shfl_xor(lt, 32);
     const int64_t pfe = pfb + (s_cu[pseq + 1] - s_cu[pseq]) - 1;
-    if (b0 + pstart == pfb && b0 + iend == pfe) {
-      // the whole row is in this wave: final output
+    if (b0 + pstart == pfb && b0 + iend - 1 == pfe) {
       if (gvalid) {
         const float inv = 1.f / fmaxf(lt, FLT_MIN);
         QT* op = static_cast<QT*>(a.out) + (int64_t)s_tok[pseq] * a.o_tok +
@@ -200,44 +224,7 @@ __global__ __launch_bounds__(256) void decode_streamk_kernel(AttnArgs a) {
         a.ws_ml[slot * 2 + 1] = lt;
       }
     }
-  };
-
-  auto step = [&](int i, char* st) __attribute__((always_inline)) {
-    const int rid = __builtin_amdgcn_readlane(row_id, i);
-    if (rid != cur) {  // a new row starts inside this wave's range
-      flush(i - 1);
-      cur = rid;
-      pseq = rid % nseq;
-      pkvh = rid / nseq;
-      pstart = i;
-      psp = row_span(a, s_ctx[pseq]);
-      pfb = (int64_t)pkvh * bseq + s_cu[pseq];
-      load_query<QT, D, G>(a, s_tok[pseq], pkvh, r, qg, qr);
-      cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop);
-#pragma unroll
-      for (int k = 0; k < NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
-      m = gvalid ? -INFINITY : 0.f;
-      l = 0.f;
-    }
-    const int later = min(NS - 1, nblk - 1 - i);
-    if (later >= 2) wait_vmcnt<2 * S::kLoads>();
-    else if (later == 1) wait_vmcnt<S::kLoads>();
-    else wait_vmcnt<0>();
-    const int blk = psp.first_blk + (int)(b0 + i - pfb);
-    mfma_block<D, G>(st, qop, cf, blk * kBlockTokens, psp.kv_begin, psp.ctx, r, qg, acc, m, l,
-                     bad_score);
-    if (i + NS < nblk) issue(i + NS, st);
-  };
-  for (int i = 0; i < nblk; i += NS) {
-    step(i, st0);
-    if (i + 1 >= nblk) break;
-    step(i + 1, st1);
-    if constexpr (NS == 3) {
-      if (i + 2 >= nblk) break;
-      step(i + 2, st2);
-    }
   }
-  if (nblk > 0) flush(nblk - 1);
   if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
   if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
 }
@@ -254,56 +241,78 @@ __global__ __launch_bounds__(256) void merge_streamk_kernel(AttnArgs a) {
   const int kvh = h / G, g = h % G;
   const int cu0 = a.ws_seq[seq], cu1 = a.ws_seq[seq + 1], bseq = a.ws_seq[a.num_seqs];
   if (cu1 == cu0) return;  // empty or not a decode row: nothing to merge
-  const int64_t B = (int64_t)bseq * a.cache.num_kv_heads;
-  const int64_t W = streamk_waves(a, B);
-  const int64_t fb = (int64_t)kvh * bseq + cu0, fe = fb + (cu1 - cu0) - 1;
-  const int64_t w0 = wave_of(fb, B, W), w1 = wave_of(fe, B, W);
-  if (w0 == w1) return;  // written whole by one wave
-  const int pieces = (int)(w1 - w0 + 1);
-  const bool first_is_tail = B * w0 / W < fb;  // the row is w0's last piece (slot 1)
+  const int hkv = a.cache.num_kv_heads;
+  const int64_t Wr = streamk_ranges(a, bseq, hkv);
+  const int64_t fb = cu0, fe = cu1 - 1;  // the row's blocks in the per-head order
+  const int64_t r0 = range_of(fb, bseq, Wr), r1 = range_of(fe, bseq, Wr);
+  if (r0 == r1) return;  // written whole by one wave
+  const int pieces = (int)(r1 - r0 + 1);
+  const bool first_is_tail = (int64_t)bseq * r0 / Wr < fb;  // the row is r0's last piece (slot 1)
   auto slot_of = [&](int p) -> int64_t __attribute__((always_inline)) {
-    const int64_t w = w0 + p;
+    const int64_t w = (r0 + p) * hkv + kvh;  // the wave that streamed range r0 + p for this head
     return (w * 2 + (p == 0 && first_is_tail ? 1 : 0)) * G + g;
   };
-  float M = -INFINITY;
-  for (int p = lane; p < pieces; p += kWave) M = fmaxf(M, a.ws_ml[slot_of(p) * 2]);
-  M = wave_max(M);
   float L = 0.f, O[kPerLane];
 #pragma unroll
   for (int e = 0; e < kPerLane; ++e) O[e] = 0.f;
-  for (int p0 = 0; p0 < pieces; p0 += kWave) {
-    const int p = p0 + lane;
-    float w = 0.f, lw = 0.f;
-    if (p < pieces) {
-      const float mp = a.ws_ml[slot_of(p) * 2];
-      w = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
-      lw = a.ws_ml[slot_of(p) * 2 + 1] * w;
+  if (pieces <= kFastPieces) {
+    // common case: every load (statistics and partial rows) issues before the first use
+    float mp = -INFINITY, lp = 0.f;
+    if (lane < pieces) {
+      mp = a.ws_ml[slot_of(lane) * 2];
+      lp = a.ws_ml[slot_of(lane) * 2 + 1];
     }
-    lw += shfl_xor(lw, 1);
-    lw += shfl_xor(lw, 2);
-    lw += shfl_xor(lw, 4);
-    lw += shfl_xor(lw, 8);
-    lw += shfl_xor(lw, 16);
-    lw += shfl_xor(lw, 32);
-    L += lw;
-    const int np = min(kWave, pieces - p0);
-    for (int q0 = 0; q0 < np; q0 += 8) {
-      float v[8][kPerLane], wq[8];
+    float v[kFastPieces][kPerLane];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int q = min(q0 + u, np - 1);
-        wq[u] = q0 + u < np ? __shfl(w, q, kWave) : 0.f;
-        const float* op = a.ws_o + slot_of(p0 + q) * D;
+    for (int u = 0; u < kFastPieces; ++u) {
+      const float* op = a.ws_o + slot_of(u < pieces ? u : 0) * D;
 #pragma unroll
-        for (int e = 0; e < kPerLane; ++e) {
-          const int d = lane + e * kWave;
-          v[u][e] = d < D ? op[d] : 0.f;
-        }
+      for (int e = 0; e < kPerLane; ++e) {
+        const int d = lane + e * kWave;
+        v[u][e] = (u < pieces && d < D) ? op[d] : 0.f;
       }
+    }
+    const float M = wave_max(mp);
+    const float w = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
+    L = wave_sum(lp * w);
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kFastPieces; ++u) {
+      const float wq = __shfl(w, u, kWave);
 #pragma unroll
-        for (int e = 0; e < kPerLane; ++e) O[e] = fmaf(v[u][e], wq[u], O[e]);
+      for (int e = 0; e < kPerLane; ++e) O[e] = fmaf(v[u][e], wq, O[e]);
+    }
+  } else {
+    float M = -INFINITY;
+    for (int p = lane; p < pieces; p += kWave) M = fmaxf(M, a.ws_ml[slot_of(p) * 2]);
+    M = wave_max(M);
+    for (int p0 = 0; p0 < pieces; p0 += kWave) {
+      const int p = p0 + lane;
+      float w = 0.f, lw = 0.f;
+      if (p < pieces) {
+        const float mp = a.ws_ml[slot_of(p) * 2];
+        w = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
+        lw = a.ws_ml[slot_of(p) * 2 + 1] * w;
+      }
+      L += wave_sum(lw);
+      const int np = min(kWave, pieces - p0);
+      for (int q0 = 0; q0 < np; q0 += 8) {
+        float v[8][kPerLane], wq[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int q = min(q0 + u, np - 1);
+          wq[u] = q0 + u < np ? __shfl(w, q, kWave) : 0.f;
+          const float* op = a.ws_o + slot_of(p0 + q) * D;
+#pragma unroll
+          for (int e = 0; e < kPerLane; ++e) {
+            const int d = lane + e * kWave;
+            v[u][e] = d < D ? op[d] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int e = 0; e < kPerLane; ++e) O[e] = fmaf(v[u][e], wq[u], O[e]);
+      }
     }
   }
   QT* out = static_cast<QT*>(a.out) + (int64_t)decode_token(a, seq) * a.o_tok +
