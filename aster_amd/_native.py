@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "astr_paged_attention_i8",
     "astr_paged_attention_varlen_i8",
     "astr_paged_attention_i8_workspace_bytes",
+    "astr_kv_copy_blocks",
     "astr_last_error",
     "astr_version",
 )
@@ -92,6 +93,10 @@ def lib():
             c_vp, c_vp,
         ]
         handle.astr_paged_attention_varlen_i8.restype = ctypes.c_int
+        handle.astr_kv_copy_blocks.argtypes = [
+            c_vp, c_i64, c_vp, c_i32, c_vp, c_i64, c_vp, c_i32, c_i64, c_i32, c_vp, c_vp,
+        ]
+        handle.astr_kv_copy_blocks.restype = ctypes.c_int
         handle.astr_paged_attention_i8_workspace_bytes.argtypes = [c_i32] * 6
         handle.astr_paged_attention_i8_workspace_bytes.restype = c_sz
         handle.astr_last_error.argtypes = []

@@ -20,7 +20,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_lib")
 OUT = os.path.join(OUT_DIR, "libaster_kv.so")
 SOURCES = ("errors.hip", "kv_quantize.hip", "paged_attention.hip", "decode_partition.hip",
-           "decode_streamk.hip", "prefill.hip")
+           "decode_streamk.hip", "prefill.hip", "kv_copy.hip")
 ARCH = "gfx950"
 
 FLAGS = [

@@ -128,6 +128,86 @@ class PagedKVCache:
         if check:
             self.raise_errors()
 
+    # ---- whole-block moves (copy-on-write, host swap) ------------------------
+    @property
+    def block_code_bytes(self):
+        """Bytes of one block's codes, all layers (one contiguous arena stretch)."""
+        return self.codes[0].numel()
+
+    @property
+    def block_scale_bytes(self):
+        return self.scales[0].numel() * self.scales.element_size()
+
+    def _copy(self, src, src_stride, src_index, src_blocks, dst, dst_stride, dst_index,
+              dst_blocks, block_bytes, count, stream):
+        _native.check(
+            _native.lib().astr_kv_copy_blocks(
+                src, src_stride, src_index, src_blocks, dst, dst_stride, dst_index, dst_blocks,
+                block_bytes, count, self.err_flag.data_ptr(), stream),
+            "copy_blocks")
+
+    def _index(self, blocks):
+        return torch.as_tensor(list(blocks), dtype=torch.int32).to(self.device, non_blocking=True)
+
+    def copy_blocks(self, src_blocks, dst_blocks, *, stream=None):
+        """Copy whole blocks (codes and scales of every layer) ``src[i] -> dst[i]``
+        inside the arena, bit-exact (copy-on-write of a shared tail page,
+        state.py:330-337). One launch per array for any number of blocks."""
+        if len(src_blocks) != len(dst_blocks):
+            raise ValueError("src_blocks and dst_blocks differ in length")
+        if not len(src_blocks):
+            return
+        stream = stream or torch.cuda.current_stream(self.device)
+        with torch.cuda.stream(stream):
+            src, dst = self._index(src_blocks), self._index(dst_blocks)
+        cb, sb = self.block_code_bytes, self.block_scale_bytes
+        for base, nbytes in ((self.codes.data_ptr(), cb), (self.scales.data_ptr(), sb)):
+            self._copy(base, nbytes, src.data_ptr(), self.num_blocks, base, nbytes, dst.data_ptr(),
+                       self.num_blocks, nbytes, len(src_blocks), stream.cuda_stream)
+        src.record_stream(stream), dst.record_stream(stream)
+
+    def gather_blocks(self, blocks, *, stream=None):
+        """Blocks ``blocks`` packed into new device tensors ``codes [P, L, 2, Hkv, bs, D]``
+        and ``scales [P, L, 2, Hkv, bs]`` (the gather half of host swap), enqueued on
+        ``stream``."""
+        stream = stream or torch.cuda.current_stream(self.device)
+        count = len(blocks)
+        with torch.cuda.stream(stream):
+            codes = torch.empty((count,) + tuple(self.codes.shape[1:]), dtype=self.codes.dtype,
+                                device=self.device)
+            scales = torch.empty((count,) + tuple(self.scales.shape[1:]), dtype=self.scales.dtype,
+                                 device=self.device)
+            if count:
+                index = self._index(blocks)
+                cb, sb = self.block_code_bytes, self.block_scale_bytes
+                self._copy(self.codes.data_ptr(), cb, index.data_ptr(), self.num_blocks,
+                           codes.data_ptr(), cb, None, count, cb, count, stream.cuda_stream)
+                self._copy(self.scales.data_ptr(), sb, index.data_ptr(), self.num_blocks,
+                           scales.data_ptr(), sb, None, count, sb, count, stream.cuda_stream)
+        return codes, scales
+
+    def scatter_blocks(self, blocks, codes, scales, *, stream=None):
+        """Write packed device blocks (``gather_blocks`` layout) into arena blocks
+        ``blocks`` (the scatter half of host swap), enqueued on ``stream``."""
+        count = len(blocks)
+        if codes.shape != (count,) + tuple(self.codes.shape[1:]) or codes.dtype != self.codes.dtype \
+                or scales.shape != (count,) + tuple(self.scales.shape[1:]) \
+                or scales.dtype != self.scales.dtype or not codes.is_contiguous() \
+                or not scales.is_contiguous() or codes.device != self.device \
+                or scales.device != self.device:
+            raise ValueError("packed blocks do not match the arena layout")
+        if not count:
+            return
+        stream = stream or torch.cuda.current_stream(self.device)
+        with torch.cuda.stream(stream):
+            index = self._index(blocks)
+        cb, sb = self.block_code_bytes, self.block_scale_bytes
+        self._copy(codes.data_ptr(), cb, None, count, self.codes.data_ptr(), cb, index.data_ptr(),
+                   self.num_blocks, cb, count, stream.cuda_stream)
+        self._copy(scales.data_ptr(), sb, None, count, self.scales.data_ptr(), sb, index.data_ptr(),
+                   self.num_blocks, sb, count, stream.cuda_stream)
+        index.record_stream(stream)
+
     def workspace_bytes(self, num_seqs, num_q_heads, max_context_len,
                         partition_tokens=DEFAULT_PARTITION_TOKENS):
         return int(_native.lib().astr_paged_attention_i8_workspace_bytes(

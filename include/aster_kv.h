@@ -178,6 +178,28 @@ size_t astr_paged_attention_i8_workspace_bytes(int32_t num_seqs, int32_t num_q_h
                                                int32_t max_context_len,
                                                int32_t partition_tokens);
 
+/*
+ * Bit-exact copy of whole blocks: block i of `num_blocks` goes from
+ *   src + (src_index ? src_index[i] : i) * src_stride
+ * to
+ *   dst + (dst_index ? dst_index[i] : i) * dst_stride   (block_bytes bytes each).
+ * Replaces the raw page copies of copy_kv (src/aster/optimization/kv_quantization.py:113-127)
+ * as used for copy-on-write of a shared tail page (src/aster/inference/state.py:330-337)
+ * and for page transfers in restore_pages / PagedStateArchive (state.py:427-493,
+ * src/aster/inference/offload.py:140-190): one launch per array (codes, scales)
+ * moves every block of a step; gather (src_index) into a staging buffer and
+ * scatter (dst_index) out of one are the two halves of host swap.
+ *   src_index/dst_index: int32 device arrays of num_blocks entries, or NULL for
+ *              identity; an entry outside [0, src_blocks) / [0, dst_blocks) raises
+ *              ASTR_FLAG_BAD_INDEX and that block is not copied.
+ *   Blocks of one call must not overlap between source and destination.
+ * 16-byte vector copies when pointers, strides and block_bytes are multiples of 16.
+ */
+int astr_kv_copy_blocks(const void* src, int64_t src_stride, const int32_t* src_index,
+                        int32_t src_blocks, void* dst, int64_t dst_stride,
+                        const int32_t* dst_index, int32_t dst_blocks, int64_t block_bytes,
+                        int32_t num_blocks, int32_t* err_flag, void* stream);
+
 /* Thread-local description of the last non-zero return code. */
 const char* astr_last_error(void);
 

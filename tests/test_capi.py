@@ -127,3 +127,23 @@ def test_check_maps_codes_to_reference_exceptions():
     with pytest.raises(RuntimeError):
         _native.check(98, "x")
     _native.check(0, "x")
+
+
+def test_copy_blocks_rejects_bad_arguments_without_launching():
+    lib = _native.lib()
+    flag = ctypes.c_int32(0)
+    buf = ctypes.create_string_buffer(256)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    fp = ctypes.addressof(flag)
+    copy = lib.astr_kv_copy_blocks
+    # nothing to move: success without touching the pointers
+    assert copy(None, 16, None, 0, None, 16, None, 0, 16, 0, None, None) == 0
+    assert copy(p, 16, None, 4, p, 16, None, 4, 0, 3, fp, None) == 0
+    # negative sizes, missing pointers, block larger than its stride, identity beyond the end
+    assert copy(p, 16, None, 4, p, 16, None, 4, 16, -1, fp, None) == _native.ASTR_EINVAL
+    assert copy(None, 16, None, 4, p, 16, None, 4, 16, 1, fp, None) == _native.ASTR_EINVAL
+    assert copy(p, 16, None, 4, p, 16, None, 4, 16, 1, None, None) == _native.ASTR_EINVAL
+    assert copy(p, 8, None, 4, p, 16, None, 4, 16, 1, fp, None) == _native.ASTR_EINVAL
+    assert copy(p, 16, None, 2, p, 16, None, 4, 16, 3, fp, None) == _native.ASTR_EINVAL
+    assert copy(p, 16, None, 4, p, 16, None, 2, 16, 3, fp, None) == _native.ASTR_EINVAL
+    assert "dst_blocks" in _native.last_error()
