@@ -1,0 +1,136 @@
+"""Runner integration of the hip_int8_paged backend: a toy GQA decoder steps through
+PagedAttentionStep over the arena-backed pool (ragged prefill chunks, decode,
+fork + copy-on-write, a mixed step, an aborted step). At every layer the HIP
+attention output is checked against the oracle's rendering of the reference's
+forward_batch row loop (paged_attention.py:168-215): the row's quantized history
+pages plus the chunk's own quantized K/V as one more block, causal positions,
+dequantize-then-attend; and after every step the pool's pages equal the oracle's
+quantized history bit for bit."""
+
+import numpy as np
+import pytest
+import torch
+
+from aster_amd import KernelWork, PagedKVCache
+from aster_amd.paged_pool import PagedStatePool
+from aster_amd.runner import PagedAttentionStep, pack_rows, unpack_rows
+from oracle import reference_cpu as ref
+from tests.gpu_util import assert_attention_close
+from tests.tiny_decoder import TinyDecoder
+
+pytestmark = pytest.mark.gpu
+
+
+class OracleRows:
+    """Per sequence and layer, the reference path's quantized history (host)."""
+
+    def __init__(self, layers):
+        self.layers = layers
+        self.hist = {}  # (seq key, layer) -> (k codes/scales, v codes/scales) lists
+
+    def fork(self, src, dst):
+        for layer in range(self.layers):
+            self.hist[(dst, layer)] = [list(x) for x in self.hist.get((src, layer), ([], []))]
+
+    def attend(self, layer, rows, q, k, v, scale):
+        """rows: list of (seq key, start, count) in packed order; q/k/v packed host arrays."""
+        outs, cursor = [], 0
+        for key, start, count in rows:
+            qs = q[cursor: cursor + count].transpose(1, 0, 2)[None]
+            ks = k[cursor: cursor + count].transpose(1, 0, 2)[None]
+            vs = v[cursor: cursor + count].transpose(1, 0, 2)[None]
+            cursor += count
+            hk, hv = self.hist.setdefault((key, layer), ([], []))
+            qk, qv = ref.quantize_kv_int8(ks), ref.quantize_kv_int8(vs)
+            blocks = []
+            if hk:
+                blocks.append(ref.AttentionBlock(_cat(hk), _cat(hv), 0, None))
+            blocks.append(ref.AttentionBlock(qk, qv, start, None))
+            pos = np.arange(start, start + count)[None]
+            out = ref.online_attention(qs, blocks, query_positions=pos, causal=True, scale=scale)
+            outs.append(out[0].transpose(1, 0, 2))
+            hk.append(qk), hv.append(qv)
+        return np.concatenate(outs, 0)
+
+
+def _cat(parts):
+    return ref.QuantizedKV(np.concatenate([p.values for p in parts], 2),
+                           np.concatenate([p.scales for p in parts], 2))
+
+
+def run_step(model, pool, oracle, seqs, keys, chunks, work):
+    counts = [len(c) for c in chunks]
+    ids = torch.tensor([t for c in chunks for t in c], device=pool.cache.device)
+    with PagedAttentionStep(pool, seqs, counts, work=work) as step:
+        pos = torch.cat([torch.arange(p, p + n) for p, n in zip(step.positions, counts)])
+        rows = list(zip(keys, step.positions, counts))
+
+        def attend(layer, q, k, v):
+            out = step.attend(layer, q, k, v, scale=model.scale)
+            want = oracle.attend(layer, rows, q.cpu().numpy(), k.cpu().numpy(),
+                                 v.cpu().numpy(), model.scale)
+            assert_attention_close(out, want)
+            return out
+
+        logits = model.forward(ids, pos.to(ids.device), attend)
+    return logits
+
+
+def check_pool_matches_oracle(pool, oracle, seq, key):
+    state = pool.materialize(seq)
+    for layer, (k, v) in enumerate(state):
+        hk, hv = oracle.hist[(key, layer)]
+        np.testing.assert_array_equal(k.cpu().numpy(), _cat(hk).dequantize())
+        np.testing.assert_array_equal(v.cpu().numpy(), _cat(hv).dequantize())
+
+
+def test_runner_steps_match_reference_row_loop(device):
+    model = TinyDecoder(device)
+    pool = PagedStatePool(PagedKVCache(num_blocks=48, num_layers=model.layers,
+                                       num_kv_heads=model.hkv, head_dim=model.d, device=device))
+    oracle = OracleRows(model.layers)
+    rng = np.random.default_rng(0)
+    seqs = [pool.create("tenant") for _ in range(3)]
+    keys = ["a", "b", "c"]
+    work = KernelWork()
+
+    def tokens(n):
+        return rng.integers(0, model.vocab, n).tolist()
+
+    # 1. ragged prefill chunks
+    run_step(model, pool, oracle, seqs, keys, [tokens(20), tokens(7), tokens(33)], work)
+    assert [s.length for s in seqs] == [20, 7, 33] and work.backend == "hip_int8_paged"
+    # 2. one decode token each
+    logits = run_step(model, pool, oracle, seqs, keys, [tokens(1)] * 3, work)
+    assert logits.shape == (3, model.vocab) and torch.isfinite(logits).all()
+    # 3. fork seq 0 and run a mixed step: both the fork and its parent extend the
+    #    shared partial tail page, so each gets a private copy
+    fork = pool.fork(seqs[0])
+    oracle.fork("a", "d")
+    tail = seqs[0].pages[-1]
+    run_step(model, pool, oracle, [seqs[0], seqs[1], fork], ["a", "b", "d"],
+             [tokens(1), tokens(5), tokens(2)], work)
+    assert seqs[0].pages[-1] != tail and fork.pages[-1] != tail
+    assert [seqs[0].length, seqs[1].length, fork.length] == [22, 13, 23]
+    for s, k in zip(seqs + [fork], keys + ["d"]):
+        check_pool_matches_oracle(pool, oracle, s, k)
+    # 4. a step that fails midway commits nothing
+    used, lengths = pool.used_blocks, [s.length for s in seqs]
+    with pytest.raises(RuntimeError, match="layer failed"):
+        with PagedAttentionStep(pool, seqs, [16, 16, 16]) as step:
+            raise RuntimeError("layer failed")
+    assert pool.used_blocks == used and [s.length for s in seqs] == lengths
+    for s in seqs + [fork]:
+        pool.release(s)
+    assert pool.used_blocks == 0
+
+
+def test_pack_unpack_reference_layout(device):
+    x = torch.randn(3, 4, 5, 8, device=device)
+    counts = [5, 2, 4]
+    packed = pack_rows(x, counts)
+    assert packed.shape == (11, 4, 8)
+    back = unpack_rows(packed, counts, 5)
+    for b, n in enumerate(counts):
+        assert torch.equal(back[b, :, :n], x[b, :, :n])
+        assert (back[b, :, n:] == 0).all()
