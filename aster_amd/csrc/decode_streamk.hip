@@ -18,7 +18,13 @@ namespace astr {
 namespace attn {
 namespace {
 
-constexpr int kStagesSK = 2;
+// Waves per workgroup and LDS stages per wave: 4-wave workgroups with a 4-block ring
+// per wave (2 waves per SIMD) measured best among 4/8/16-wave workgroups with 2 or 4
+// stages (all within 3 %); D = 256 stages are twice as large, so 8 waves x 2 stages.
+template <int D>
+constexpr int sk_waves() { return D == 256 ? 8 : 4; }
+template <int D>
+constexpr int sk_stages() { return D == 256 ? 2 : 4; }
 constexpr int kMaxSeqsSK = 512;  // per-sequence table lives in LDS
 constexpr int kFastPieces = 16;  // merge: rows split into at most this many pieces load at once
 
@@ -47,21 +53,23 @@ __device__ __forceinline__ void store_row_zero(const AttnArgs& a, int tok, int D
     orow[(int64_t)(idx / D) * a.o_head + idx % D] = from_float<QT>(0.f);
 }
 
-template <typename QT, int D, int G, int NS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void decode_streamk_kernel(AttnArgs a) {
+template <typename QT, int D, int G>
+__global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(AttnArgs a) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   static_assert(G >= 1 && G <= 16, "GQA group");
-  static_assert(NS == 2, "stream-K runs two LDS stages per wave");
+  constexpr int NS = sk_stages<D>();
+  static_assert(NS >= 2 && NS <= 4, "LDS stages per wave");
   using S = Stage<D>;
   constexpr int NPV = D / 16;
   constexpr int VB = D / 16;
+  constexpr int NW = sk_waves<D>();
+  constexpr int SPT = (kMaxSeqsSK + NW * kWave - 1) / (NW * kWave);  // sequences per thread
 
-  __shared__ __attribute__((aligned(16))) char lds0[kWaves * S::kBytes];
-  __shared__ __attribute__((aligned(16))) char lds1[kWaves * S::kBytes];
+  __shared__ __attribute__((aligned(16))) char lds[NS * NW * S::kBytes];  // [stage][wave]
   __shared__ int s_ctx[kMaxSeqsSK];  // -1: not a decode row
   __shared__ int s_tok[kMaxSeqsSK];  // query/output token row
   __shared__ int s_cu[kMaxSeqsSK + 1];
-  __shared__ int s_wsum[kWaves];
+  __shared__ int s_wsum[NW];
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
@@ -70,12 +78,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   const int nseq = a.num_seqs;
   const int hkv = a.cache.num_kv_heads;
 
-  // ---- 1. visible blocks per sequence -> exclusive prefix s_cu (thread t owns 2t, 2t+1);
-  // sequences without exactly one query token take no blocks
-  int nb[2] = {0, 0};
+  // ---- 1. visible blocks per sequence -> exclusive prefix s_cu (thread t owns
+  // sequences SPT*t .. SPT*t + SPT-1); sequences without exactly one query token take
+  // no blocks
+  int nb[SPT];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int s = 2 * threadIdx.x + k;
+  for (int k = 0; k < SPT; ++k) {
+    nb[k] = 0;
+    const int s = SPT * threadIdx.x + k;
     if (s < nseq) {
       const int tok = decode_token(a, s);
       s_tok[s] = tok;
@@ -89,7 +99,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
       }
     }
   }
-  const int local = nb[0] + nb[1];
+  int local = 0;
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) local += nb[k];
   int incl = local;
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) {
@@ -100,10 +112,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   __syncthreads();
   int wbase = 0;
   for (int w = 0; w < wave; ++w) wbase += s_wsum[w];
-  const int excl = wbase + incl - local;
-  if (2 * (int)threadIdx.x < nseq) s_cu[2 * threadIdx.x] = excl;
-  if (2 * (int)threadIdx.x + 1 < nseq) s_cu[2 * threadIdx.x + 1] = excl + nb[0];
-  const int bseq = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+  int excl = wbase + incl - local;
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) {
+    if (SPT * (int)threadIdx.x + k < nseq) s_cu[SPT * threadIdx.x + k] = excl;
+    excl += nb[k];
+  }
+  int bseq = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) bseq += s_wsum[w];
   if (threadIdx.x == 0) s_cu[nseq] = bseq;
   __syncthreads();
   if (blockIdx.x == 0)
@@ -115,7 +132,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   // ---- 2. this wave's head, block range and block ids / rows (lane j <-> block b0 + j);
   // waves from Wr * Hkv on have nothing to do
   const int64_t Wr = streamk_ranges(a, bseq, hkv);
-  const int64_t gw = (int64_t)blockIdx.x * kWaves + wave;
+  const int64_t gw = (int64_t)blockIdx.x * NW + wave;
   const int kv = (int)(gw % hkv);
   const int64_t rg = gw / hkv;
   int64_t b0 = 0;
@@ -144,29 +161,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
       too_long || __ballot(lane < n && (unsigned)ids >= (unsigned)a.cache.num_blocks) != 0;
   const int nblk = bad_index ? 0 : n;
 
-  char* const st0 = lds0 + wave * S::kBytes;
-  char* const st1 = lds1 + wave * S::kBytes;
-  auto issue = [&](int j, char* st) __attribute__((always_inline)) {
-    stage_block<D>(a, __builtin_amdgcn_readlane(ids, j),
-                   __builtin_amdgcn_readlane(row_id, j) / nseq, lane, st);
+  auto stage = [&](int j) __attribute__((always_inline)) -> char* {
+    return lds + ((j % NS) * NW + wave) * S::kBytes;
   };
-  // First row's query: its G head rows go by direct-to-LDS loads into stage 1
-  // together with block 0, so the block stream starts without waiting for it;
-  // block 1 takes stage 1 once the query has been read out.
+  auto issue = [&](int j) __attribute__((always_inline)) {
+    stage_block<D>(a, __builtin_amdgcn_readlane(ids, j),
+                   __builtin_amdgcn_readlane(row_id, j) / nseq, lane, stage(j));
+  };
+  // Wait until block j has landed; the blocks after it (up to NS - 1) stay in flight.
+  auto wait_block = [&](int j) __attribute__((always_inline)) {
+    const int later = min(NS - 1, nblk - 1 - j);
+    if (NS > 3 && later >= 3) wait_vmcnt<3 * S::kLoads>();
+    else if (NS > 2 && later >= 2) wait_vmcnt<2 * S::kLoads>();
+    else if (later >= 1) wait_vmcnt<S::kLoads>();
+    else wait_vmcnt<0>();
+  };
+  // First row's query: its G head rows go by direct-to-LDS loads into the last
+  // stage, issued before blocks 0 .. NS-2, so the block stream starts without
+  // waiting for it; block NS-1 takes that stage once the query has been read out.
   QueryRaw<D> qr;
   half8_t qop[D / 32];
   float cf = 0.f;
   if (nblk > 0) {
-    stage_query<QT, D, G>(a, s_tok[row0 % nseq], row0 / nseq, lane, st1);
-    issue(0, st0);
-    wait_vmcnt<S::kLoads>();  // the query has landed; block 0 may still be in flight
-    lds_query<QT, D>(st1, gvalid ? r : 0, qg, qr);
+    stage_query<QT, D, G>(a, s_tok[row0 % nseq], row0 / nseq, lane, stage(NS - 1));
+    const int first = min(NS - 1, nblk);
+    for (int j = 0; j < first; ++j) issue(j);
+    if (first == 3) wait_vmcnt<3 * S::kLoads>();  // the query has landed
+    else if (first == 2) wait_vmcnt<2 * S::kLoads>();
+    else wait_vmcnt<S::kLoads>();
+    lds_query<QT, D>(stage(NS - 1), gvalid ? r : 0, qg, qr);
     cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop);
-    if (1 < nblk) issue(1, st1);  // after the query reads above (their values are consumed)
+    if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (their values are consumed)
   }
 
   // ---- 3. stream the blocks, one piece (the run of one row's blocks) at a time;
-  // block i sits in stage i % 2 and block i + 2 is issued into it once consumed
+  // block i sits in stage i % NS and block i + NS is issued into it once consumed
   float4_t acc[NPV];
   float m = 0.f, l = 0.f;
   bool bad_score = false;
@@ -190,12 +219,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     l = 0.f;
     const int blk0 = psp.first_blk + (int)(b0 + i - pfb);
     for (; i < iend; ++i) {
-      char* const st = (i & 1) ? st1 : st0;
-      if (i + 1 < nblk) wait_vmcnt<S::kLoads>();  // block i + 1 may stay in flight
-      else wait_vmcnt<0>();
-      mfma_block<D, G>(st, qop, cf, (blk0 + i - pstart) * kBlockTokens, psp.kv_begin, psp.ctx, r,
-                       qg, acc, m, l, bad_score);
-      if (i + 2 < nblk) issue(i + 2, st);
+      wait_block(i);
+      mfma_block<D, G>(stage(i), qop, cf, (blk0 + i - pstart) * kBlockTokens, psp.kv_begin,
+                       psp.ctx, r, qg, acc, m, l, bad_score);
+      if (i + NS < nblk) issue(i + NS);
     }
     // write the piece: the final output when the whole row is in this wave, else a
     // partial in slot 0 (the piece starts the wave's range) or 1 (it ends it)
@@ -327,11 +354,11 @@ __global__ __launch_bounds__(256) void merge_streamk_kernel(AttnArgs a) {
 
 // Workgroups of `kernel` one CU holds at once (queried once per kernel).
 template <typename Kernel>
-int resident_per_cu(Kernel kernel) {
+int resident_per_cu(Kernel kernel, int threads) {
   static int cached = 0;
   if (cached == 0) {
     int n = 0;
-    cached = (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kWaves * kWave, 0) ==
+    cached = (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) ==
                   hipSuccess && n > 0)
                  ? n
                  : 1;
@@ -349,18 +376,19 @@ int device_cus() {
 
 template <typename QT, int D, int G>
 int launch(AttnArgs a, hipStream_t stream) {
-  auto kernel = decode_streamk_kernel<QT, D, G, kStagesSK>;
+  auto kernel = decode_streamk_kernel<QT, D, G>;
+  constexpr int NW = sk_waves<D>();
   // launch one wave per resident slot (whole workgroups) and at least min_waves (the
   // host-side bound), at most the workspace capacity passed in total_waves; the
   // kernels settle the waves they use from the actual block count
-  const int64_t resident = (int64_t)device_cus() * resident_per_cu(kernel) * kWaves;
+  const int64_t resident = (int64_t)device_cus() * resident_per_cu(kernel, NW * kWave) * NW;
   int64_t waves = resident;
-  if (waves < a.min_waves) waves = (a.min_waves + kWaves - 1) / kWaves * kWaves;
-  if (waves > a.total_waves) waves = a.total_waves / kWaves * kWaves;
+  if (waves < a.min_waves) waves = (a.min_waves + NW - 1) / NW * NW;
+  if (waves > a.total_waves) waves = a.total_waves / NW * NW;
   a.total_waves = (int32_t)waves;
   a.pref_waves = (int32_t)(resident < waves ? resident : waves);
-  const int wgs = (int)(waves / kWaves);
-  hipLaunchKernelGGL(kernel, dim3(wgs), dim3(kWaves * kWave), 0, stream, a);
+  const int wgs = (int)(waves / NW);
+  hipLaunchKernelGGL(kernel, dim3(wgs), dim3(NW * kWave), 0, stream, a);
   const int units = a.num_seqs * a.num_q_heads;
   hipLaunchKernelGGL((merge_streamk_kernel<QT, D>), dim3((units + kWaves - 1) / kWaves),
                      dim3(kWaves * kWave), 0, stream, a);
