@@ -11,8 +11,10 @@
 // visible key range is streamed in steps of four 16-token blocks; each wave
 // stages one block of the step into LDS with direct global->LDS loads and then
 // all four waves run all four blocks through the MFMAs:
-//   S^T[t][c]  = K[t][:] . Q[c][:]     v_mfma_f32_16x16x32_f16 (int8 codes are exact in f16)
-//   O^T[d][c] += V^T[d][t] . P^T[t][c]  v_mfma_f32_16x16x16f16 (P^T carries V's scales)
+//   S^T[t][c]  = K[t][:] . Q[c][:]     v_mfma_i32_16x16x64_i8: the K codes as stored,
+//                                        the query as two int8 terms (exact int32 dot)
+//   O^T[d][c] += V^T[d][t] . P^T[t][c]  v_mfma_f32_16x16x32_f16 over two blocks (P^T
+//                                        carries V's scales)
 // so every K/V byte of the unit's range is read once per query tile and shared by
 // the G heads and TQ tokens of the tile. Softmax statistics are per column, in
 // base 2, with the lazy rescale of the decode kernels.
@@ -30,6 +32,7 @@ namespace attn {
 namespace {
 
 constexpr int kXcds = 8;
+constexpr int kPrefillBuffers = 3;
 
 template <int D>
 struct PrefillShape {
@@ -73,12 +76,23 @@ __device__ int scan_tiles(const AttnArgs& a, int tq, int unit, int* s_wsum, int*
   return base;
 }
 
-// f16 B-operand of one query column (lane r of its 16-lane group qg holds
-// d = 16*qg + 64*h + [0, 16)), after an exact 2^-e rescale keeping max|q| below
-// 2^15; returns the score factor with e folded in. Cross-lane: uniform control flow.
+typedef int int4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kQRange = 127 * 128;  // |Q| bound: hi = (Q + 64) >> 7 and lo = Q - 128 hi fit int8
+// |S_int| <= 127 * kQRange * 256; a score factor below this keeps every score finite
+constexpr float kSafeFactor = 1.0e29f;
+
+// Int8 B-operands of one query column for the QK MFMAs (lane r of its 16-lane group
+// qg holds d = 16*qg + 64*h + [0, 16)): the column is quantized once to integers
+// Q = rint(q * kQRange / max|q|), |Q| <= kQRange, split as Q = 128 * hi + lo with hi,
+// lo in int8, so that K.Q = 128 (K.hi) + K.lo is exact in int32 (a ~15-bit query,
+// finer than f16's 11 bits for every element within 2^-4 of the column maximum).
+// Returns the score factor max|q| / kQRange * qk_scale_log2 (NaN for a non-finite
+// query, which makes every score of the column non-finite as in fp32 arithmetic).
+// Cross-lane: uniform control flow.
 template <typename QT, int D>
-__device__ __forceinline__ float query_column(const QT* qp, bool valid, float qk_scale_log2,
-                                              half8_t (&qop)[D / 32]) {
+__device__ __forceinline__ float query_column_i8(const QT* qp, bool valid, float qk_scale_log2,
+                                                 int4_t (&qhi)[D / 64], int4_t (&qlo)[D / 64]) {
   constexpr int kVec = 16 / (int)sizeof(QT);  // elements per 16-byte load
   float x[D / 64][16];
 #pragma unroll
@@ -93,57 +107,51 @@ __device__ __forceinline__ float query_column(const QT* qp, bool valid, float qk
     }
   }
   float mx = 0.f;
+  bool finite = true;
 #pragma unroll
   for (int h = 0; h < D / 64; ++h)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(x[h][i]));
+    for (int i = 0; i < 16; ++i) {
+      mx = fmaxf(mx, fabsf(x[h][i]));
+      finite = finite && __builtin_isfinite(x[h][i]);
+    }
   mx = fmaxf(mx, shfl_xor(mx, 16));
   mx = fmaxf(mx, shfl_xor(mx, 32));
-  int ex = 0;
-  if (mx >= 32768.f) {
-    frexpf(mx, &ex);
-    ex -= 15;
-  }
-  const float down = ldexpf(1.f, -ex);
+  // the column's elements sit in lanes r, r+16, r+32, r+48
+  const uint64_t nonfinite_lanes = __ballot(!finite);
+  finite = ((nonfinite_lanes >> (threadIdx.x % 16)) & 0x0001000100010001ull) == 0;
+  const float inv = (finite && mx > 0.f) ? (float)kQRange / mx : 0.f;
 #pragma unroll
-  for (int kk = 0; kk < D / 32; ++kk)
+  for (int h = 0; h < D / 64; ++h)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qop[kk][i] = (_Float16)(x[kk / 2][(kk % 2) * 8 + i] * down);
-  return qk_scale_log2 * ldexpf(1.f, ex);
+    for (int w = 0; w < 4; ++w) {
+      uint32_t hw = 0, lw = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        int q = (int)__builtin_rintf(x[h][4 * w + e] * inv);
+        q = min(max(q, -kQRange), kQRange);
+        const int hi = (q + 64) >> 7;
+        const int lo = q - (hi << 7);
+        hw |= (uint32_t)(hi & 0xff) << (8 * e);
+        lw |= (uint32_t)(lo & 0xff) << (8 * e);
+      }
+      qhi[h][w] = (int)hw;
+      qlo[h][w] = (int)lw;
+    }
+  if (!finite) return __builtin_nanf("");
+  return mx > 0.f ? qk_scale_log2 * (mx / (float)kQRange) : 0.f;
 }
 
-// One staged 16-token block (first key position kb) through the MFMAs for the
-// wave's NT column tiles. `masked`: apply the per-column [lo, hi] key bounds
-// (blocks inside every column's range skip the compares).
-template <int D, int NT>
-__device__ __forceinline__ void prefill_block(const char* st, const half8_t (&qop)[NT][D / 32],
-                                              const float (&cf)[NT], int kb, const int (&lo)[NT],
-                                              const int (&hi)[NT], bool masked, int r, int qg,
-                                              float4_t (&acc)[NT][D / 16], float (&m)[NT],
-                                              float (&l)[NT], bool& bad_score) {
+// V codes of one staged block as the f16 A-operands of the PV MFMAs, written once
+// by the wave that loaded the block: entry n * 64 + lane holds, for that lane (qg, r)
+// of every wave, V[4 qg + j][r * VB + n], j = 0..3 (exact f16). Reading an entry
+// back at the reader's own lane index is conflict-free. `present` false writes
+// zeros (the slab never holds stale or uninitialized values).
+template <int D>
+__device__ __forceinline__ void convert_v(const char* st, bool present, int lane, uint2* vt) {
   using S = Stage<D>;
-  constexpr int KCH = D / 64;
   constexpr int VB = D / 16;
-  constexpr int NPV = D / 16;
-  float4_t s4[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) s4[t] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int h = 0; h < KCH; ++h) {
-    const uint4 c = *reinterpret_cast<const uint4*>(st + S::kK + r * D + 16 * qg + 64 * h);
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      half2_t p0, p1, p2, p3;
-      codes_to_f16(sub ? c.z : c.x, p0, p1);
-      codes_to_f16(sub ? c.w : c.y, p2, p3);
-      const half8_t kop = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        s4[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[t][2 * h + sub], s4[t], 0, 0, 0);
-    }
-  }
-  const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
-  const float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg);
+  const int r = lane & 15, qg = lane >> 4;
   uint32_t vw[4][VB / 4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -162,26 +170,109 @@ __device__ __forceinline__ void prefill_block(const char* st, const half8_t (&qo
       vw[j][3] = w.w;
     }
   }
-  const int k0 = kb + 4 * qg;  // keys k0 + j of column r
-  float sc[NT][4];
+#pragma unroll
+  for (int n = 0; n < VB; ++n) {
+    const uint32_t col[4] = {vw[0][n / 4], vw[1][n / 4], vw[2][n / 4], vw[3][n / 4]};
+    half4_t v;
+    switch (n % 4) {
+      case 0: v = v_operand<0>(col); break;
+      case 1: v = v_operand<1>(col); break;
+      case 2: v = v_operand<2>(col); break;
+      default: v = v_operand<3>(col); break;
+    }
+    vt[n * kWave + lane] = present ? __builtin_bit_cast(uint2, v) : uint2{0u, 0u};
+  }
+}
+
+// Two staged 16-token blocks A and B (first key positions kbA, kbB = kbA + 16) through
+// the MFMAs for the wave's NT column tiles:
+//   S^T = K . Q^T      v_mfma_i32_16x16x64_i8 twice per 64-wide d chunk (hi, then lo
+//                      on the hi result shifted by 7): exact int32 dot products
+//   O^T += V^T . P^T   v_mfma_f32_16x16x32_f16 over the pair's 32 keys
+// The pair's keys map to K-index slot i of lane group qg as key 4*qg + i of A (i < 4)
+// and of B (i >= 4), in both PV operands. An unused block contributes p = 0 (its
+// stage may hold stale codes, which are finite). `masked*`: apply the per-column
+// [lo, hi] key bounds. kEdge = false is the interior case (both blocks used, no bounds,
+// every key scale times query factor below kSafeFactor, so every score is finite) and
+// compiles without any of the per-score conditions; kEdge = true handles the rest and
+// checks scores for non-finite values one by one.
+template <int D, int NT, bool kEdge>
+__device__ __forceinline__ void prefill_pair(const char* stA, const char* stB, const uint2* vtA,
+                                             const uint2* vtB, bool useA, bool useB,
+                                             int kbA, bool maskedA, bool maskedB,
+                                             const int4_t (&qhi)[NT][D / 64],
+                                             const int4_t (&qlo)[NT][D / 64],
+                                             const float (&cf)[NT], const int (&lo)[NT],
+                                             const int (&hi)[NT], int r, int qg,
+                                             float4_t (&acc)[NT][D / 16], float (&m)[NT],
+                                             float (&l)[NT], bool& bad_score) {
+  using S = Stage<D>;
+  constexpr int KCH = D / 64;
+  constexpr int VB = D / 16;
+  constexpr int NPV = D / 16;
+  const char* st[2] = {stA, stB};
+  const bool use[2] = {kEdge ? useA : true, kEdge ? useB : true};
+  const bool masked[2] = {kEdge && maskedA, kEdge && maskedB};
+  int4_t sacc[2][NT];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) sacc[b][t] = int4_t{0, 0, 0, 0};
+    if (!use[b]) continue;
+    int4_t kop[KCH];
+#pragma unroll
+    for (int h = 0; h < KCH; ++h)
+      kop[h] = *reinterpret_cast<const int4_t*>(st[b] + S::kK + r * D + 16 * qg + 64 * h);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int h = 0; h < KCH; ++h)
+        sacc[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qhi[t][h], sacc[b][t], 0, 0, 0);
+      sacc[b][t] = sacc[b][t] << 7;
+#pragma unroll
+      for (int h = 0; h < KCH; ++h)
+        sacc[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qlo[t][h], sacc[b][t], 0, 0, 0);
+    }
+  }
+  float4_t ks[2], vs[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    // an unused block's stage may never have been written: zero scales keep it out of
+    // every product (0 * NaN would not be 0)
+    const float4_t zero = {0.f, 0.f, 0.f, 0.f};
+    ks[b] = use[b] ? *reinterpret_cast<const float4_t*>(st[b] + S::kS + 16 * qg) : zero;
+    vs[b] = use[b] ? *reinterpret_cast<const float4_t*>(st[b] + S::kS + 64 + 16 * qg) : zero;
+  }
+  const int lane = qg * 16 + r;
+  // scores (base 2): slot i < 4 -> key kbA + 4 qg + i, slot i >= 4 -> key kbA + 16 + 4 qg + i - 4
+  float sc[NT][8];
   bool need = false, nonfinite = false;
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int t = 0; t < NT; ++t) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float v = s4[t][j] * (ks[j] * cf[t]);
-      bool vis = true;
-      if (masked) vis = k0 + j >= lo[t] && k0 + j <= hi[t];
-      nonfinite |= vis && !__builtin_isfinite(v);
-      v = vis ? v : -INFINITY;
-      need |= v > m[t] + kRescaleSlack;
-      sc[t][j] = v;
+    for (int i = 0; i < 8; ++i) {
+      const int b = i / 4;
+      const float v = (float)sacc[b][t][i % 4] * (ks[b][i % 4] * cf[t]);
+      if constexpr (kEdge) {
+        const int key = kbA + 16 * b + 4 * qg + i % 4;
+        const bool inside = (unsigned)(key - lo[t]) <= (unsigned)(hi[t] - lo[t]);  // lo <= key <= hi
+        const bool vis = use[b] & (!masked[b] | inside);
+        nonfinite |= vis & !__builtin_isfinite(v);
+        sc[t][i] = vis ? v : -INFINITY;
+      } else {
+        sc[t][i] = v;
+      }
     }
-  if (__ballot(nonfinite) != 0) bad_score = true;
+    const float tmax = fmaxf(fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])),
+                             fmaxf(fmaxf(sc[t][4], sc[t][5]), fmaxf(sc[t][6], sc[t][7])));
+    need |= tmax > m[t] + kRescaleSlack;
+  }
+  if (kEdge && __ballot(nonfinite) != 0) bad_score = true;
   if (__ballot(need) != 0) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      float tmax = fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3]));
+      float tmax = fmaxf(fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])),
+                         fmaxf(fmaxf(sc[t][4], sc[t][5]), fmaxf(sc[t][6], sc[t][7])));
       tmax = fmaxf(tmax, shfl_xor(tmax, 16));
       tmax = fmaxf(tmax, shfl_xor(tmax, 32));
       const float mn = fmaxf(m[t], tmax);
@@ -192,28 +283,23 @@ __device__ __forceinline__ void prefill_block(const char* st, const half8_t (&qo
       m[t] = mn;
     }
   }
-  half4_t pop[NT];
+  half8_t pop[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float p = __builtin_amdgcn_exp2f(sc[t][j] - m[t]);
+    for (int i = 0; i < 8; ++i) {
+      const float p = __builtin_amdgcn_exp2f(sc[t][i] - m[t]);
       l[t] += p;
-      pop[t][j] = (_Float16)(p * vs[j]);
+      pop[t][i] = (_Float16)(p * vs[i / 4][i % 4]);
     }
 #pragma unroll
   for (int n = 0; n < NPV; ++n) {
-    const uint32_t col[4] = {vw[0][n / 4], vw[1][n / 4], vw[2][n / 4], vw[3][n / 4]};
-    half4_t vop;
-    switch (n % 4) {
-      case 0: vop = v_operand<0>(col); break;
-      case 1: vop = v_operand<1>(col); break;
-      case 2: vop = v_operand<2>(col); break;
-      default: vop = v_operand<3>(col); break;
-    }
+    const half4_t va = __builtin_bit_cast(half4_t, vtA[n * kWave + lane]);
+    const half4_t vb = __builtin_bit_cast(half4_t, vtB[n * kWave + lane]);
+    const half8_t vop = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-      acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop, pop[t], acc[t][n], 0, 0, 0);
+      acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[t], acc[t][n], 0, 0, 0);
   }
 }
 
@@ -252,8 +338,9 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   constexpr int VB = D / 16;
   static_assert(PrefillShape<D>::kCols % G == 0, "GQA group must divide the column tile");
 
-  __shared__ __attribute__((aligned(16))) char lds0[kWaves * S::kBytes];
-  __shared__ __attribute__((aligned(16))) char lds1[kWaves * S::kBytes];
+  constexpr int NB = kPrefillBuffers;  // key steps in flight: NB - 1 ahead of the one computed
+  __shared__ __attribute__((aligned(16))) char lds[NB * kWaves * S::kBytes];  // [step % NB][wave]
+  __shared__ uint2 vt[kWaves][VB * kWave];  // the current step's V operands, one slab per block
   __shared__ int s_wsum[kWaves];
   __shared__ int s_found[2];
 
@@ -291,7 +378,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   const int nsteps = (b_hi - b_lo + kWaves - 1) / kWaves;
 
   // ---- 2. this wave's columns: flat column f -> token t0 + f / G, head kvh * G + f % G
-  half8_t qop[NT][D / 32];
+  int4_t qhi[NT][D / 64], qlo[NT][D / 64];
   float cf[NT];
   int lo[NT], hi[NT], ctok[NT], chead[NT];
   bool cvalid[NT];
@@ -306,7 +393,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     hi[t] = cvalid[t] ? (a.causal ? p : ctx - 1) : -1;
     const QT* qp = static_cast<const QT*>(a.q) + (int64_t)(q0 + (cvalid[t] ? ctok[t] : t0)) * a.q_tok +
                    (int64_t)chead[t] * a.q_head + 16 * qg;
-    cf[t] = query_column<QT, D>(qp, cvalid[t], a.qk_scale_log2, qop[t]);
+    cf[t] = query_column_i8<QT, D>(qp, cvalid[t], a.qk_scale_log2, qhi[t], qlo[t]);
   }
   // key bounds over the wave's valid columns (positions grow with f)
   const int tk_lo = t0 + (wave * NT * 16) / G;
@@ -346,27 +433,69 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     stage_block<D>(a, id, kvh, lane, buf + wave * S::kBytes);
     return true;
   };
+  auto buffer = [&](int step) __attribute__((always_inline)) -> char* {
+    return lds + (step % NB) * kWaves * S::kBytes;
+  };
+  // bit (step % NB): this wave issued loads for that step (uniform over the wave)
+  uint32_t inflight = 0;
   if (nsteps > 0) load_ids(0);
-  bool nxt = nsteps > 0 ? issue(0, lds0) : false;
+  for (int j = 0; j < NB - 1 && j < nsteps; ++j)
+    if (issue(j, buffer(j))) inflight |= 1u << (j % NB);
   for (int i = 0; i < nsteps; ++i) {
-    char* const cur = (i & 1) ? lds1 : lds0;
-    char* const oth = (i & 1) ? lds0 : lds1;
-    nxt = false;
-    if (i + 1 < nsteps) {
-      if ((i + 1) % kWave == 0) load_ids(i + 1);
-      nxt = issue(i + 1, oth);  // `oth` was last read in step i - 1 (barrier below)
+    const int ahead = i + NB - 1;
+    if (ahead < nsteps) {
+      if (ahead % kWave == 0) load_ids(ahead);
+      // its buffer was last read in step i - 1 (barrier below)
+      if (issue(ahead, buffer(ahead))) inflight |= 1u << (ahead % NB);
+      else inflight &= ~(1u << (ahead % NB));
     }
-    if (nxt) wait_vmcnt<S::kLoads>();
-    else wait_vmcnt<0>();
-    __syncthreads();  // every wave's block of step i has landed
+    // wait for step i's loads; the later steps' loads stay in flight
+    int younger = 0;
 #pragma unroll
-    for (int bw = 0; bw < kWaves; ++bw) {
-      const int kb = (b_lo + i * kWaves + bw) * kBlockTokens;
-      if (kb >= b_hi * kBlockTokens) break;
-      if (!wave_any || kb > w_hi_max || kb + kBlockTokens - 1 < w_lo_min) continue;
-      const bool masked = !(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min);
-      prefill_block<D, NT>(cur + bw * S::kBytes, qop, cf, kb, lo, hi, masked, r, qg, acc, m, l,
-                           bad_score);
+    for (int k = 1; k < NB; ++k)
+      if (i + k < nsteps && (inflight >> ((i + k) % NB) & 1u)) ++younger;
+    if (younger >= 3) wait_vmcnt<3 * S::kLoads>();
+    else if (younger == 2) wait_vmcnt<2 * S::kLoads>();
+    else if (younger == 1) wait_vmcnt<S::kLoads>();
+    else wait_vmcnt<0>();
+    char* const cur = buffer(i);
+    // this wave's block of step i is in; its V operands go to the wave's slab (the
+    // previous step's readers are past the barrier that ended that step)
+    convert_v<D>(cur + wave * S::kBytes, (inflight >> (i % NB)) & 1u, lane, vt[wave]);
+    __syncthreads();  // every wave's block of step i has landed and been converted
+#pragma unroll 1
+    for (int bp = 0; bp < kWaves; bp += 2) {
+      const int kb = (b_lo + i * kWaves + bp) * kBlockTokens;
+      const int kend = b_hi * kBlockTokens;
+      if (kb >= kend) break;
+      const bool useA = wave_any && kb <= w_hi_max && kb + kBlockTokens - 1 >= w_lo_min;
+      const int kbB = kb + kBlockTokens;
+      const bool useB = wave_any && kbB < kend && kbB <= w_hi_max &&
+                        kbB + kBlockTokens - 1 >= w_lo_min;
+      if (!useA && !useB) continue;
+      const bool maskedA = !(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min);
+      const bool maskedB = !(kbB >= w_lo_max && kbB + kBlockTokens - 1 <= w_hi_min);
+      const char* stA = cur + bp * S::kBytes;
+      const char* stB = cur + (bp + 1) * S::kBytes;
+      // interior pair: both blocks used, no bounds, and every key scale times query
+      // factor in the range where no score can overflow
+      bool safe = useA && useB && !maskedA && !maskedB;
+      if (safe) {
+        const float4_t ka = *reinterpret_cast<const float4_t*>(stA + S::kS + 16 * qg);
+        const float4_t kb4 = *reinterpret_cast<const float4_t*>(stB + S::kS + 16 * qg);
+        const float kmax = fmaxf(fmaxf(fmaxf(ka[0], ka[1]), fmaxf(ka[2], ka[3])),
+                                 fmaxf(fmaxf(kb4[0], kb4[1]), fmaxf(kb4[2], kb4[3])));
+        bool ok = true;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) ok = ok && kmax * cf[t] <= kSafeFactor;
+        safe = __ballot(!ok) == 0;
+      }
+      if (safe)
+        prefill_pair<D, NT, false>(stA, stB, vt[bp], vt[bp + 1], true, true, kb, false, false,
+                                   qhi, qlo, cf, lo, hi, r, qg, acc, m, l, bad_score);
+      else
+        prefill_pair<D, NT, true>(stA, stB, vt[bp], vt[bp + 1], useA, useB, kb, maskedA, maskedB,
+                                  qhi, qlo, cf, lo, hi, r, qg, acc, m, l, bad_score);
     }
     __syncthreads();  // step i's stage may be refilled
   }
