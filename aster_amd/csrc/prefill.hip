@@ -143,12 +143,14 @@ __device__ __forceinline__ float query_column_i8(const QT* qp, bool valid, float
 }
 
 // V codes of one staged block as the f16 A-operands of the PV MFMAs, written once
-// by the wave that loaded the block: entry n * 64 + lane holds, for that lane (qg, r)
-// of every wave, V[4 qg + j][r * VB + n], j = 0..3 (exact f16). Reading an entry
-// back at the reader's own lane index is conflict-free. `present` false writes
-// zeros (the slab never holds stale or uninitialized values).
+// by the wave that loaded the block into the slab of its block pair: half `half` of
+// entry n * 64 + lane holds, for that lane (qg, r) of every wave, V[4 qg + j][r * VB + n],
+// j = 0..3 (exact f16), so that one 16-byte read at the reader's own lane index gives
+// the pair's whole operand (conflict-free). `present` false writes zeros (the slab
+// never holds stale or uninitialized values).
 template <int D>
-__device__ __forceinline__ void convert_v(const char* st, bool present, int lane, uint2* vt) {
+__device__ __forceinline__ void convert_v(const char* st, bool present, int lane, int half,
+                                          uint2* vt) {
   using S = Stage<D>;
   constexpr int VB = D / 16;
   const int r = lane & 15, qg = lane >> 4;
@@ -180,9 +182,11 @@ __device__ __forceinline__ void convert_v(const char* st, bool present, int lane
       case 2: v = v_operand<2>(col); break;
       default: v = v_operand<3>(col); break;
     }
-    vt[n * kWave + lane] = present ? __builtin_bit_cast(uint2, v) : uint2{0u, 0u};
+    vt[2 * (n * kWave + lane) + half] = present ? __builtin_bit_cast(uint2, v) : uint2{0u, 0u};
   }
 }
+
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 // Two staged 16-token blocks A and B (first key positions kbA, kbB = kbA + 16) through
 // the MFMAs for the wave's NT column tiles:
@@ -190,41 +194,39 @@ __device__ __forceinline__ void convert_v(const char* st, bool present, int lane
 //                      on the hi result shifted by 7): exact int32 dot products
 //   O^T += V^T . P^T   v_mfma_f32_16x16x32_f16 over the pair's 32 keys
 // The pair's keys map to K-index slot i of lane group qg as key 4*qg + i of A (i < 4)
-// and of B (i >= 4), in both PV operands. An unused block contributes p = 0 (its
-// stage may hold stale codes, which are finite). `masked*`: apply the per-column
-// [lo, hi] key bounds. kEdge = false is the interior case (both blocks used, no bounds,
-// every key scale times query factor below kSafeFactor, so every score is finite) and
-// compiles without any of the per-score conditions; kEdge = true handles the rest and
-// checks scores for non-finite values one by one.
-template <int D, int NT, bool kEdge>
-__device__ __forceinline__ void prefill_pair(const char* stA, const char* stB, const uint2* vtA,
-                                             const uint2* vtB, bool useA, bool useB,
-                                             int kbA, bool maskedA, bool maskedB,
+// and of B (i >= 4), in both PV operands. The base-2 score of a key is
+// u * cf with u = S_int * k_scale, folded into the exponent as fma(u, cfe, -m)
+// (cfe = cf, or FLT_MIN where cf = 0, so that a masked u = -inf stays -inf).
+// `interior` (wave-uniform: both blocks used, no key bounds) takes the path with no
+// per-score conditions when, in addition, every key scale times query factor is below
+// kSafeFactor (no score can overflow); otherwise the scores are masked to -inf outside
+// the column's [lo, hi] and for an unused block (whose stage holds stale but finite
+// codes and scales, and zero V operands), and checked for non-finite values. Both
+// cases share one softmax/PV tail, so the accumulators live in one set of registers.
+template <int D, int NT>
+__device__ __forceinline__ void prefill_pair(const char* stA, const char* stB, const uint4* vt,
+                                             bool interior, bool useA,
+                                             bool useB, int kbA, bool maskedA, bool maskedB,
                                              const int4_t (&qhi)[NT][D / 64],
                                              const int4_t (&qlo)[NT][D / 64],
-                                             const float (&cf)[NT], const int (&lo)[NT],
-                                             const int (&hi)[NT], int r, int qg,
-                                             float4_t (&acc)[NT][D / 16], float (&m)[NT],
+                                             const float (&cf)[NT], const float (&cfe)[NT],
+                                             const int (&lo)[NT], const int (&hi)[NT], int r,
+                                             int qg, float4_t (&acc)[NT][D / 16], float (&m)[NT],
                                              float (&l)[NT], bool& bad_score) {
   using S = Stage<D>;
   constexpr int KCH = D / 64;
-  constexpr int VB = D / 16;
   constexpr int NPV = D / 16;
   const char* st[2] = {stA, stB};
-  const bool use[2] = {kEdge ? useA : true, kEdge ? useB : true};
-  const bool masked[2] = {kEdge && maskedA, kEdge && maskedB};
   int4_t sacc[2][NT];
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) sacc[b][t] = int4_t{0, 0, 0, 0};
-    if (!use[b]) continue;
     int4_t kop[KCH];
 #pragma unroll
     for (int h = 0; h < KCH; ++h)
       kop[h] = *reinterpret_cast<const int4_t*>(st[b] + S::kK + r * D + 16 * qg + 64 * h);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
+      sacc[b][t] = int4_t{0, 0, 0, 0};
 #pragma unroll
       for (int h = 0; h < KCH; ++h)
         sacc[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qhi[t][h], sacc[b][t], 0, 0, 0);
@@ -237,45 +239,60 @@ __device__ __forceinline__ void prefill_pair(const char* stA, const char* stB, c
   float4_t ks[2], vs[2];
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    // an unused block's stage may never have been written: zero scales keep it out of
-    // every product (0 * NaN would not be 0)
-    const float4_t zero = {0.f, 0.f, 0.f, 0.f};
-    ks[b] = use[b] ? *reinterpret_cast<const float4_t*>(st[b] + S::kS + 16 * qg) : zero;
-    vs[b] = use[b] ? *reinterpret_cast<const float4_t*>(st[b] + S::kS + 64 + 16 * qg) : zero;
+    ks[b] = *reinterpret_cast<const float4_t*>(st[b] + S::kS + 16 * qg);
+    vs[b] = *reinterpret_cast<const float4_t*>(st[b] + S::kS + 64 + 16 * qg);
   }
-  const int lane = qg * 16 + r;
-  // scores (base 2): slot i < 4 -> key kbA + 4 qg + i, slot i >= 4 -> key kbA + 16 + 4 qg + i - 4
-  float sc[NT][8];
-  bool need = false, nonfinite = false;
+  bool edge = !interior;
+  if (interior) {
+    // scales are finite and >= 0: their order is that of their bit patterns
+    const int4_t ka = __builtin_bit_cast(int4_t, ks[0]), kb = __builtin_bit_cast(int4_t, ks[1]);
+    const float kmax = __builtin_bit_cast(
+        float, max(max(max(ka[0], ka[1]), max(ka[2], ka[3])), max(max(kb[0], kb[1]), max(kb[2], kb[3]))));
+    bool ok = true;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
+    for (int t = 0; t < NT; ++t) ok = ok && kmax * cf[t] <= kSafeFactor;  // false for NaN
+    edge = __ballot(!ok) != 0;
+  }
+  // u (base-2 score / cf): slot i < 4 -> key kbA + 4 qg + i, i >= 4 -> key kbA + 16 + 4 qg + i - 4
+  float u[NT][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int b = i / 4;
-      const float v = (float)sacc[b][t][i % 4] * (ks[b][i % 4] * cf[t]);
-      if constexpr (kEdge) {
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[t][i] = (float)sacc[i / 4][t][i % 4] * ks[i / 4][i % 4];
+  if (edge) {
+    asm volatile("");  // keeps this a branch: if-converted, the interior path would pay for it
+    const bool use[2] = {useA, useB};
+    const bool masked[2] = {maskedA, maskedB};
+    bool nonfinite = false;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int b = i / 4;
         const int key = kbA + 16 * b + 4 * qg + i % 4;
         const bool inside = (unsigned)(key - lo[t]) <= (unsigned)(hi[t] - lo[t]);  // lo <= key <= hi
         const bool vis = use[b] & (!masked[b] | inside);
-        nonfinite |= vis & !__builtin_isfinite(v);
-        sc[t][i] = vis ? v : -INFINITY;
-      } else {
-        sc[t][i] = v;
+        nonfinite |= vis & !__builtin_isfinite(u[t][i] * cf[t]);
+        u[t][i] = vis ? u[t][i] : -INFINITY;
       }
-    }
-    const float tmax = fmaxf(fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])),
-                             fmaxf(fmaxf(sc[t][4], sc[t][5]), fmaxf(sc[t][6], sc[t][7])));
-    need |= tmax > m[t] + kRescaleSlack;
+    if (__ballot(nonfinite) != 0) bad_score = true;
   }
-  if (kEdge && __ballot(nonfinite) != 0) bad_score = true;
+  float tmax[NT];
+  bool need = false;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    // NaN-propagating maximum (v_maximum3_f32: no operand canonicalization)
+    const float mu = vmax(vmax(vmax(u[t][0], u[t][1]), vmax(u[t][2], u[t][3])),
+                          vmax(vmax(u[t][4], u[t][5]), vmax(u[t][6], u[t][7])));
+    tmax[t] = mu * cfe[t];  // cfe > 0: the maximum of the scaled scores
+    need |= tmax[t] > m[t] + kRescaleSlack;
+  }
   if (__ballot(need) != 0) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      float tmax = fmaxf(fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])),
-                         fmaxf(fmaxf(sc[t][4], sc[t][5]), fmaxf(sc[t][6], sc[t][7])));
-      tmax = fmaxf(tmax, shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, shfl_xor(tmax, 32));
-      const float mn = fmaxf(m[t], tmax);
+      float x = fmaxf(tmax[t], shfl_xor(tmax[t], 16));
+      x = fmaxf(x, shfl_xor(x, 32));
+      const float mn = fmaxf(m[t], x);
       const float alpha = __builtin_amdgcn_exp2f(m[t] - mn);
       l[t] *= alpha;
 #pragma unroll
@@ -288,15 +305,14 @@ __device__ __forceinline__ void prefill_pair(const char* stA, const char* stB, c
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float p = __builtin_amdgcn_exp2f(sc[t][i] - m[t]);
+      const float p = __builtin_amdgcn_exp2f(fmaf(u[t][i], cfe[t], -m[t]));
       l[t] += p;
       pop[t][i] = (_Float16)(p * vs[i / 4][i % 4]);
     }
+  const int lane = qg * 16 + r;
 #pragma unroll
   for (int n = 0; n < NPV; ++n) {
-    const half4_t va = __builtin_bit_cast(half4_t, vtA[n * kWave + lane]);
-    const half4_t vb = __builtin_bit_cast(half4_t, vtB[n * kWave + lane]);
-    const half8_t vop = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+    const half8_t vop = __builtin_bit_cast(half8_t, vt[n * kWave + lane]);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
       acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[t], acc[t][n], 0, 0, 0);
@@ -340,7 +356,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
 
   constexpr int NB = kPrefillBuffers;  // key steps in flight: NB - 1 ahead of the one computed
   __shared__ __attribute__((aligned(16))) char lds[NB * kWaves * S::kBytes];  // [step % NB][wave]
-  __shared__ uint2 vt[kWaves][VB * kWave];  // the current step's V operands, one slab per block
+  __shared__ uint4 vt[kWaves / 2][VB * kWave];  // the current step's V operands, one slab per pair
   __shared__ int s_wsum[kWaves];
   __shared__ int s_found[2];
 
@@ -348,6 +364,12 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   const int lane = threadIdx.x % kWave;
   const int r = lane & 15, qg = lane >> 4;
   const int hkv = a.cache.num_kv_heads;
+  // zero scales in every stage: a stage that no step writes (a block past the range)
+  // then feeds finite products; stages written by loads only ever hold arena scales,
+  // which are finite (the append writes no non-finite value)
+  for (int j = lane; j < NB * 32; j += kWave)
+    reinterpret_cast<float*>(lds + (j / 32) * kWaves * S::kBytes + wave * S::kBytes + S::kS)[j % 32] = 0.f;
+  __syncthreads();
 
   // ---- 1. this workgroup's unit (uniform over the workgroup)
   const int per_kv = scan_tiles(a, TQ, -1, s_wsum, s_found);
@@ -379,7 +401,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
 
   // ---- 2. this wave's columns: flat column f -> token t0 + f / G, head kvh * G + f % G
   int4_t qhi[NT][D / 64], qlo[NT][D / 64];
-  float cf[NT];
+  float cf[NT], cfe[NT];
   int lo[NT], hi[NT], ctok[NT], chead[NT];
   bool cvalid[NT];
 #pragma unroll
@@ -394,6 +416,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     const QT* qp = static_cast<const QT*>(a.q) + (int64_t)(q0 + (cvalid[t] ? ctok[t] : t0)) * a.q_tok +
                    (int64_t)chead[t] * a.q_head + 16 * qg;
     cf[t] = query_column_i8<QT, D>(qp, cvalid[t], a.qk_scale_log2, qhi[t], qlo[t]);
+    cfe[t] = cf[t] > 0.f ? cf[t] : FLT_MIN;  // cf >= 0 or NaN (scale > 0)
   }
   // key bounds over the wave's valid columns (positions grow with f)
   const int tk_lo = t0 + (wave * NT * 16) / G;
@@ -461,7 +484,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     char* const cur = buffer(i);
     // this wave's block of step i is in; its V operands go to the wave's slab (the
     // previous step's readers are past the barrier that ended that step)
-    convert_v<D>(cur + wave * S::kBytes, (inflight >> (i % NB)) & 1u, lane, vt[wave]);
+    convert_v<D>(cur + wave * S::kBytes, (inflight >> (i % NB)) & 1u, lane, wave % 2,
+                 reinterpret_cast<uint2*>(vt[wave / 2]));
     __syncthreads();  // every wave's block of step i has landed and been converted
 #pragma unroll 1
     for (int bp = 0; bp < kWaves; bp += 2) {
@@ -475,27 +499,9 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
       if (!useA && !useB) continue;
       const bool maskedA = !(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min);
       const bool maskedB = !(kbB >= w_lo_max && kbB + kBlockTokens - 1 <= w_hi_min);
-      const char* stA = cur + bp * S::kBytes;
-      const char* stB = cur + (bp + 1) * S::kBytes;
-      // interior pair: both blocks used, no bounds, and every key scale times query
-      // factor in the range where no score can overflow
-      bool safe = useA && useB && !maskedA && !maskedB;
-      if (safe) {
-        const float4_t ka = *reinterpret_cast<const float4_t*>(stA + S::kS + 16 * qg);
-        const float4_t kb4 = *reinterpret_cast<const float4_t*>(stB + S::kS + 16 * qg);
-        const float kmax = fmaxf(fmaxf(fmaxf(ka[0], ka[1]), fmaxf(ka[2], ka[3])),
-                                 fmaxf(fmaxf(kb4[0], kb4[1]), fmaxf(kb4[2], kb4[3])));
-        bool ok = true;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) ok = ok && kmax * cf[t] <= kSafeFactor;
-        safe = __ballot(!ok) == 0;
-      }
-      if (safe)
-        prefill_pair<D, NT, false>(stA, stB, vt[bp], vt[bp + 1], true, true, kb, false, false,
-                                   qhi, qlo, cf, lo, hi, r, qg, acc, m, l, bad_score);
-      else
-        prefill_pair<D, NT, true>(stA, stB, vt[bp], vt[bp + 1], useA, useB, kb, maskedA, maskedB,
-                                  qhi, qlo, cf, lo, hi, r, qg, acc, m, l, bad_score);
+      prefill_pair<D, NT>(cur + bp * S::kBytes, cur + (bp + 1) * S::kBytes, vt[bp / 2],
+                          useA && useB && !maskedA && !maskedB, useA, useB, kb, maskedA, maskedB,
+                          qhi, qlo, cf, cfe, lo, hi, r, qg, acc, m, l, bad_score);
     }
     __syncthreads();  // step i's stage may be refilled
   }
