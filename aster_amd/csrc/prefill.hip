@@ -40,14 +40,115 @@ struct PrefillShape {
   static constexpr int kCols = kWaves * 16 * NT;  // (token, head) columns per workgroup
 };
 
+// Keys visible to query tile `tile` (tokens [t0, t1) of the sequence's n query tokens,
+// context ctx): positions [lo, hi], blocks [b_lo, b_hi).
+struct TileSpan {
+  int pos0, t0, t1, lo, hi, b_lo, b_hi;
+};
+
+__device__ __forceinline__ TileSpan tile_span(const AttnArgs& a, int ctx, int n, int tile, int tq) {
+  TileSpan t;
+  t.pos0 = ctx - n;  // position of the sequence's first query token
+  t.t0 = tile * tq;
+  t.t1 = min(n, t.t0 + tq);
+  t.lo = a.window > 0 ? max(0, t.pos0 + t.t0 - a.window + 1) : 0;
+  t.hi = a.causal ? min(t.pos0 + t.t1 - 1, ctx - 1) : ctx - 1;
+  t.b_lo = t.lo / kBlockTokens;
+  t.b_hi = t.hi >= t.lo ? t.hi / kBlockTokens + 1 : t.b_lo;  // exclusive
+  return t;
+}
+
+constexpr int kOrderMax = 256;  // chunk rows ordered longest first; beyond this, index order
+
 __device__ __forceinline__ int query_tiles(const AttnArgs& a, int s, int tq) {
   int begin;
   const int n = seq_queries(a, s, begin);
   return n > 1 ? (n + tq - 1) / tq : 0;
 }
 
-// Workgroup-wide scan of the query-tile counts of all sequences. Returns the
-// total; when `unit` >= 0, the sequence holding that unit and the unit's index
+// The dispatch plan, from one round of loads of the offsets and context lengths, in
+// the LDS table `tab` (PlanTab::kInts ints): the chunk rows (sequences with more than
+// one query token) with their sequence, query offset, query count and context length
+// as loaded, and the rows in dispatch order, longest first (key: key blocks of the
+// row's last tile, which sees the most keys; ties by index), with the inclusive prefix
+// of their tile counts in that order. Returns the number of rows and the total tile
+// count, or -1 when there are more than kOrderMax rows (then every sequence is taken
+// in index order by scan_tiles). Every thread calls it.
+struct PlanTab {
+  enum { kSeq, kTiles, kKey, kQ0, kN, kCtx, kOrder, kIncl, kArrays };
+  static constexpr int kInts = kArrays * kOrderMax;
+  __device__ static int* at(int* tab, int array) { return tab + array * kOrderMax; }
+};
+
+__device__ int plan_rows(const AttnArgs& a, int tq, int* tab, int* s_wsum, int& total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  int* const r_tiles = PlanTab::at(tab, PlanTab::kTiles);
+  int* const r_key = PlanTab::at(tab, PlanTab::kKey);
+  int* const o_row = PlanTab::at(tab, PlanTab::kOrder);
+  int* const o_incl = PlanTab::at(tab, PlanTab::kIncl);
+  int count = 0;
+  for (int c0 = 0; c0 < a.num_seqs; c0 += kWaves * kWave) {
+    const int s = c0 + (int)threadIdx.x;
+    int key = -1, tiles = 0, q0 = 0, n = 0, ctx_raw = 0;
+    if (s < a.num_seqs) {
+      n = seq_queries(a, s, q0);
+      if (n > 1) {
+        ctx_raw = a.context_lens[s];
+        const TileSpan sp = tile_span(a, clamp_ctx(a, ctx_raw, false), n, (n - 1) / tq, tq);
+        key = sp.b_hi - sp.b_lo;
+        tiles = (n + tq - 1) / tq;
+      }
+    }
+    const uint64_t rows = __ballot(key >= 0);
+    const int before = __builtin_popcountll(rows & ((1ull << lane) - 1));
+    if (lane == 0) s_wsum[wave] = __builtin_popcountll(rows);
+    __syncthreads();
+    int idx = count + before;
+    for (int w = 0; w < wave; ++w) idx += s_wsum[w];
+    if (key >= 0 && idx < kOrderMax) {
+      PlanTab::at(tab, PlanTab::kSeq)[idx] = s;
+      PlanTab::at(tab, PlanTab::kQ0)[idx] = q0;
+      PlanTab::at(tab, PlanTab::kN)[idx] = n;
+      PlanTab::at(tab, PlanTab::kCtx)[idx] = ctx_raw;
+      r_tiles[idx] = tiles;
+      r_key[idx] = key;
+    }
+    count += s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+    __syncthreads();
+  }
+  if (count > kOrderMax) return -1;
+  static_assert(kOrderMax == kWaves * kWave, "one row per thread below");
+  const int i = threadIdx.x;
+  int tiles = 0;
+  if (i < count) {
+    const int k = r_key[i];
+    int rank = 0;
+    for (int j = 0; j < count; ++j) {
+      const int kj = r_key[j];
+      rank += (kj > k) | ((kj == k) & (j < i));
+    }
+    o_row[rank] = i;
+    o_incl[rank] = r_tiles[i];
+  }
+  __syncthreads();
+  if (i < count) tiles = o_incl[i];
+  int incl = tiles;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int v = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += v;
+  }
+  if (lane == kWave - 1) s_wsum[wave] = incl;
+  __syncthreads();
+  for (int w = 0; w < wave; ++w) incl += s_wsum[w];
+  if (i < count) o_incl[i] = incl;
+  total = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+  __syncthreads();
+  return count;
+}
+
+// Workgroup-wide scan of the query-tile counts of all sequences in index order. Returns
+// the total; when `unit` >= 0, the sequence holding that unit and the unit's index
 // within the sequence land in found[0], found[1]. Every thread calls it.
 __device__ int scan_tiles(const AttnArgs& a, int tq, int unit, int* s_wsum, int* found) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
@@ -91,16 +192,30 @@ constexpr float kSafeFactor = 1.0e29f;
 // query, which makes every score of the column non-finite as in fp32 arithmetic).
 // Cross-lane: uniform control flow.
 template <typename QT, int D>
-__device__ __forceinline__ float query_column_i8(const QT* qp, bool valid, float qk_scale_log2,
-                                                 int4_t (&qhi)[D / 64], int4_t (&qlo)[D / 64]) {
+struct QueryColumn {  // the lane's 16 elements of each 64-wide d chunk, as loaded
+  uint4 w[D / 64][16 * sizeof(QT) / 16];
+};
+
+template <typename QT, int D>
+__device__ __forceinline__ void load_query_column(const QT* qp, QueryColumn<QT, D>& raw) {
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int c = 0; c < (int)(16 * sizeof(QT) / 16); ++c)
+      raw.w[h][c] = reinterpret_cast<const uint4*>(qp + 64 * h)[c];
+}
+
+template <typename QT, int D>
+__device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, bool valid,
+                                                 float qk_scale_log2, int4_t (&qhi)[D / 64],
+                                                 int4_t (&qlo)[D / 64]) {
   constexpr int kVec = 16 / (int)sizeof(QT);  // elements per 16-byte load
   float x[D / 64][16];
 #pragma unroll
   for (int h = 0; h < D / 64; ++h) {
-    const uint4* src = reinterpret_cast<const uint4*>(qp + 64 * h);
 #pragma unroll
     for (int c = 0; c < 16 / kVec; ++c) {
-      const uint4 w = src[c];
+      const uint4 w = raw.w[h][c];
       const QT* e = reinterpret_cast<const QT*>(&w);
 #pragma unroll
       for (int i = 0; i < kVec; ++i) x[h][c * kVec + i] = valid ? to_float<QT>(e[i]) : 0.f;
@@ -188,25 +303,25 @@ __device__ __forceinline__ void convert_v(const char* st, bool present, int lane
 
 __device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
-// Two staged 16-token blocks A and B (first key positions kbA, kbB = kbA + 16) through
-// the MFMAs for the wave's NT column tiles:
+// One key step: the four staged 16-token blocks w = 0..3 (first key position
+// kb0 + 16 w) through the MFMAs for the wave's NT column tiles:
 //   S^T = K . Q^T      v_mfma_i32_16x16x64_i8 twice per 64-wide d chunk (hi, then lo
 //                      on the hi result shifted by 7): exact int32 dot products
-//   O^T += V^T . P^T   v_mfma_f32_16x16x32_f16 over the pair's 32 keys
-// The pair's keys map to K-index slot i of lane group qg as key 4*qg + i of A (i < 4)
-// and of B (i >= 4), in both PV operands. The base-2 score of a key is
-// u * cf with u = S_int * k_scale, folded into the exponent as fma(u, cfe, -m)
-// (cfe = cf, or FLT_MIN where cf = 0, so that a masked u = -inf stays -inf).
-// `interior` (wave-uniform: both blocks used, no key bounds) takes the path with no
-// per-score conditions when, in addition, every key scale times query factor is below
-// kSafeFactor (no score can overflow); otherwise the scores are masked to -inf outside
-// the column's [lo, hi] and for an unused block (whose stage holds stale but finite
-// codes and scales, and zero V operands), and checked for non-finite values. Both
-// cases share one softmax/PV tail, so the accumulators live in one set of registers.
+//   O^T += V^T . P^T   v_mfma_f32_16x16x32_f16 over the 32 keys of block pair
+//                      (0, 1) and (2, 3)
+// Score slot j = 4 w + i of lane group qg is key 4 qg + i of block w; in the PV
+// operands, slots 8 p + [0, 8) of pair p match the interleaved V slab. The base-2
+// score of a key is u * cf with u = S_int * k_scale, folded into the exponent as
+// fma(u, cfe, -m) (cfe = cf, or FLT_MIN where cf = 0, so that a masked u = -inf stays
+// -inf). Bit w of `use` (wave-uniform): block w holds keys some column of the wave
+// sees; of `bounded`: the column bounds [lo, hi] cut into block w. With every block
+// used, none bounded and every key scale times query factor below kSafeFactor (no
+// score can overflow) the step takes no per-score condition; otherwise the scores are
+// masked to -inf outside the bounds and for unused blocks (whose stages hold stale but
+// finite codes and scales, and zero V operands) and checked for non-finite values.
 template <int D, int NT>
-__device__ __forceinline__ void prefill_pair(const char* stA, const char* stB, const uint4* vt,
-                                             bool interior, bool useA,
-                                             bool useB, int kbA, bool maskedA, bool maskedB,
+__device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, uint32_t use,
+                                             uint32_t bounded, int kb0,
                                              const int4_t (&qhi)[NT][D / 64],
                                              const int4_t (&qlo)[NT][D / 64],
                                              const float (&cf)[NT], const float (&cfe)[NT],
@@ -216,14 +331,15 @@ __device__ __forceinline__ void prefill_pair(const char* stA, const char* stB, c
   using S = Stage<D>;
   constexpr int KCH = D / 64;
   constexpr int NPV = D / 16;
-  const char* st[2] = {stA, stB};
-  int4_t sacc[2][NT];
+  constexpr int NBK = kWaves;  // blocks per step
+  int4_t sacc[NBK][NT];
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
+  for (int b = 0; b < NBK; ++b) {
+    const char* st = cur + b * S::kBytes;
     int4_t kop[KCH];
 #pragma unroll
     for (int h = 0; h < KCH; ++h)
-      kop[h] = *reinterpret_cast<const int4_t*>(st[b] + S::kK + r * D + 16 * qg + 64 * h);
+      kop[h] = *reinterpret_cast<const int4_t*>(st + S::kK + r * D + 16 * qg + 64 * h);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       sacc[b][t] = int4_t{0, 0, 0, 0};
@@ -236,44 +352,42 @@ __device__ __forceinline__ void prefill_pair(const char* stA, const char* stB, c
         sacc[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qlo[t][h], sacc[b][t], 0, 0, 0);
     }
   }
-  float4_t ks[2], vs[2];
+  float4_t ks[NBK];
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    ks[b] = *reinterpret_cast<const float4_t*>(st[b] + S::kS + 16 * qg);
-    vs[b] = *reinterpret_cast<const float4_t*>(st[b] + S::kS + 64 + 16 * qg);
-  }
-  bool edge = !interior;
-  if (interior) {
-    // scales are finite and >= 0: their order is that of their bit patterns
-    const int4_t ka = __builtin_bit_cast(int4_t, ks[0]), kb = __builtin_bit_cast(int4_t, ks[1]);
-    const float kmax = __builtin_bit_cast(
-        float, max(max(max(ka[0], ka[1]), max(ka[2], ka[3])), max(max(kb[0], kb[1]), max(kb[2], kb[3]))));
-    bool ok = true;
+  for (int b = 0; b < NBK; ++b)
+    ks[b] = *reinterpret_cast<const float4_t*>(cur + b * S::kBytes + S::kS + 16 * qg);
+  // computed without a branch, so that the QK MFMAs and the conversions below share
+  // one block: scales are finite and >= 0, their order is that of their bit patterns
+  int kx = 0;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) ok = ok && kmax * cf[t] <= kSafeFactor;  // false for NaN
-    edge = __ballot(!ok) != 0;
+  for (int b = 0; b < NBK; ++b) {
+    const int4_t kb = __builtin_bit_cast(int4_t, ks[b]);
+    kx = max(kx, max(max(kb[0], kb[1]), max(kb[2], kb[3])));
   }
-  // u (base-2 score / cf): slot i < 4 -> key kbA + 4 qg + i, i >= 4 -> key kbA + 16 + 4 qg + i - 4
-  float u[NT][8];
+  const float kmax = __builtin_bit_cast(float, kx);
+  bool ok = true;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) ok = ok && kmax * cf[t] <= kSafeFactor;  // false for NaN
+  const bool unsafe = __ballot(!ok) != 0;
+  const bool edge = (use != (1u << NBK) - 1) | (bounded != 0) | unsafe;
+  float u[NT][4 * NBK];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) u[t][i] = (float)sacc[i / 4][t][i % 4] * ks[i / 4][i % 4];
+    for (int j = 0; j < 4 * NBK; ++j) u[t][j] = (float)sacc[j / 4][t][j % 4] * ks[j / 4][j % 4];
   if (edge) {
-    asm volatile("");  // keeps this a branch: if-converted, the interior path would pay for it
-    const bool use[2] = {useA, useB};
-    const bool masked[2] = {maskedA, maskedB};
+    asm volatile("");  // keeps this a branch: if-converted, the interior steps would pay for it
     bool nonfinite = false;
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int b = i / 4;
-        const int key = kbA + 16 * b + 4 * qg + i % 4;
+      for (int j = 0; j < 4 * NBK; ++j) {
+        const int b = j / 4;
+        const int key = kb0 + 16 * b + 4 * qg + j % 4;
         const bool inside = (unsigned)(key - lo[t]) <= (unsigned)(hi[t] - lo[t]);  // lo <= key <= hi
-        const bool vis = use[b] & (!masked[b] | inside);
-        nonfinite |= vis & !__builtin_isfinite(u[t][i] * cf[t]);
-        u[t][i] = vis ? u[t][i] : -INFINITY;
+        const bool vis = ((use >> b) & 1u) && (!((bounded >> b) & 1u) || inside);
+        nonfinite |= vis & !__builtin_isfinite(u[t][j] * cf[t]);
+        u[t][j] = vis ? u[t][j] : -INFINITY;
       }
     if (__ballot(nonfinite) != 0) bad_score = true;
   }
@@ -282,8 +396,9 @@ __device__ __forceinline__ void prefill_pair(const char* stA, const char* stB, c
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     // NaN-propagating maximum (v_maximum3_f32: no operand canonicalization)
-    const float mu = vmax(vmax(vmax(u[t][0], u[t][1]), vmax(u[t][2], u[t][3])),
-                          vmax(vmax(u[t][4], u[t][5]), vmax(u[t][6], u[t][7])));
+    float mu = u[t][0];
+#pragma unroll
+    for (int j = 1; j < 4 * NBK; ++j) mu = vmax(mu, u[t][j]);
     tmax[t] = mu * cfe[t];  // cfe > 0: the maximum of the scaled scores
     need |= tmax[t] > m[t] + kRescaleSlack;
   }
@@ -300,22 +415,27 @@ __device__ __forceinline__ void prefill_pair(const char* stA, const char* stB, c
       m[t] = mn;
     }
   }
-  half8_t pop[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float p = __builtin_amdgcn_exp2f(fmaf(u[t][i], cfe[t], -m[t]));
-      l[t] += p;
-      pop[t][i] = (_Float16)(p * vs[i / 4][i % 4]);
-    }
   const int lane = qg * 16 + r;
 #pragma unroll
-  for (int n = 0; n < NPV; ++n) {
-    const half8_t vop = __builtin_bit_cast(half8_t, vt[n * kWave + lane]);
+  for (int pp = 0; pp < NBK / 2; ++pp) {
+    const float4_t vsA = *reinterpret_cast<const float4_t*>(cur + (2 * pp) * S::kBytes + S::kS + 64 + 16 * qg);
+    const float4_t vsB = *reinterpret_cast<const float4_t*>(cur + (2 * pp + 1) * S::kBytes + S::kS + 64 + 16 * qg);
+    half8_t pop[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-      acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[t], acc[t][n], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(u[t][8 * pp + i], cfe[t], -m[t]));
+        l[t] += p;
+        pop[t][i] = (_Float16)(p * (i < 4 ? vsA[i] : vsB[i - 4]));
+      }
+#pragma unroll
+    for (int n = 0; n < NPV; ++n) {
+      const half8_t vop = __builtin_bit_cast(half8_t, vt[pp * (NPV * kWave) + n * kWave + lane]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[t], acc[t][n], 0, 0, 0);
+    }
   }
 }
 
@@ -364,46 +484,80 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   const int lane = threadIdx.x % kWave;
   const int r = lane & 15, qg = lane >> 4;
   const int hkv = a.cache.num_kv_heads;
-  // zero scales in every stage: a stage that no step writes (a block past the range)
-  // then feeds finite products; stages written by loads only ever hold arena scales,
-  // which are finite (the append writes no non-finite value)
-  for (int j = lane; j < NB * 32; j += kWave)
-    reinterpret_cast<float*>(lds + (j / 32) * kWaves * S::kBytes + wave * S::kBytes + S::kS)[j % 32] = 0.f;
-  __syncthreads();
 
-  // ---- 1. this workgroup's unit (uniform over the workgroup)
-  const int per_kv = scan_tiles(a, TQ, -1, s_wsum, s_found);
+  // ---- 1. this workgroup's unit (uniform over the workgroup). The plan lives in the
+  // stage buffers until the first load.
+  static_assert(PlanTab::kInts * sizeof(int) <= sizeof(lds), "the dispatch plan fits the stages");
+  int* const tab = reinterpret_cast<int*>(lds);
+  int per_kv = 0;
+  const int nrows = plan_rows(a, TQ, tab, s_wsum, per_kv);
+  if (nrows < 0) per_kv = scan_tiles(a, TQ, -1, s_wsum, s_found);
   const int64_t units = (int64_t)per_kv * hkv;
   const int64_t per_xcd = (units + kXcds - 1) / kXcds;
   const int64_t slot = blockIdx.x / kXcds;
   const int64_t logical = (int64_t)(blockIdx.x % kXcds) * per_xcd + slot;
   if (slot >= per_xcd || logical >= units) return;
   const int kvh = (int)(logical / per_kv);
-  if (threadIdx.x == 0) s_found[0] = -1;  // ordered before the scan's writes by its barriers
-  scan_tiles(a, TQ, (int)(logical % per_kv), s_wsum, s_found);
-  const int seq = s_found[0];
-  if (seq < 0) return;  // unreachable for unit < per_kv; keeps every index below in range
-  int q0;
-  const int n = seq_queries(a, seq, q0);
+  const int unit = (int)(logical % per_kv);
+  int seq, within, q0, n, ctx_raw;
+  if (nrows >= 0) {
+    // the first row whose inclusive prefix exceeds the unit (prefixes strictly grow)
+    const int* const o_incl = PlanTab::at(tab, PlanTab::kIncl);
+    int lo_r = 0, hi_r = nrows - 1;
+    while (lo_r < hi_r) {
+      const int mid = (lo_r + hi_r) / 2;
+      if (o_incl[mid] > unit) hi_r = mid;
+      else lo_r = mid + 1;
+    }
+    // uniform values read from LDS: readfirstlane keeps them (and all they derive) scalar
+    const int row = __builtin_amdgcn_readfirstlane(PlanTab::at(tab, PlanTab::kOrder)[lo_r]);
+    within = __builtin_amdgcn_readfirstlane(unit - (lo_r > 0 ? o_incl[lo_r - 1] : 0));
+    seq = __builtin_amdgcn_readfirstlane(PlanTab::at(tab, PlanTab::kSeq)[row]);
+    q0 = __builtin_amdgcn_readfirstlane(PlanTab::at(tab, PlanTab::kQ0)[row]);
+    n = __builtin_amdgcn_readfirstlane(PlanTab::at(tab, PlanTab::kN)[row]);
+    ctx_raw = __builtin_amdgcn_readfirstlane(PlanTab::at(tab, PlanTab::kCtx)[row]);
+  } else {
+    if (threadIdx.x == 0) s_found[0] = -1;  // ordered before the scan's writes by its barriers
+    scan_tiles(a, TQ, unit, s_wsum, s_found);
+    seq = __builtin_amdgcn_readfirstlane(s_found[0]);
+    within = __builtin_amdgcn_readfirstlane(s_found[1]);
+    if (seq < 0) return;  // unreachable for unit < per_kv; keeps every index below in range
+    n = seq_queries(a, seq, q0);
+    ctx_raw = a.context_lens[seq];
+  }
   const int ntq = (n + TQ - 1) / TQ;
-  const int tile = ntq - 1 - s_found[1];  // latest (longest) tiles first
+  const int tile = ntq - 1 - within;  // latest (longest) tiles first
   const bool reporter = kvh == 0 && tile == ntq - 1 && threadIdx.x == 0;
-  const int ctx = clamp_ctx(a, a.context_lens[seq], reporter);
+  const int ctx = clamp_ctx(a, ctx_raw, reporter);
   if (ctx < n && reporter) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);  // chunk longer than the context
 
-  const int pos0 = ctx - n;  // position of the sequence's first query token
-  const int t0 = tile * TQ, t1 = min(n, t0 + TQ);
-  const int lo_wg = a.window > 0 ? max(0, pos0 + t0 - a.window + 1) : 0;
-  const int hi_wg = a.causal ? min(pos0 + t1 - 1, ctx - 1) : ctx - 1;
-  const int b_lo = lo_wg / kBlockTokens;
-  const int b_hi = hi_wg >= lo_wg ? hi_wg / kBlockTokens + 1 : b_lo;  // exclusive
+  const TileSpan span = tile_span(a, ctx, n, tile, TQ);
+  const int pos0 = span.pos0, t0 = span.t0, t1 = span.t1;
+  const int b_lo = span.b_lo, b_hi = span.b_hi;
   const int nsteps = (b_hi - b_lo + kWaves - 1) / kWaves;
 
-  // ---- 2. this wave's columns: flat column f -> token t0 + f / G, head kvh * G + f % G
-  int4_t qhi[NT][D / 64], qlo[NT][D / 64];
-  float cf[NT], cfe[NT];
+  // zero scales in every stage, once every wave is past its last read of the plan: a
+  // stage that no step writes (a block past the range) then feeds finite products;
+  // stages written by loads only ever hold arena scales, which are finite (the append
+  // writes no non-finite value)
+  __syncthreads();
+  for (int j = lane; j < NB * 32; j += kWave)
+    reinterpret_cast<float*>(lds + (j / 32) * kWaves * S::kBytes + wave * S::kBytes + S::kS)[j % 32] = 0.f;
+  __syncthreads();
+
+  // ---- 2. this wave's columns: flat column f -> token t0 + f / G, head kvh * G + f % G.
+  // The block ids and the query go out together; the first steps' loads are issued
+  // before the query is quantized.
   int lo[NT], hi[NT], ctok[NT], chead[NT];
   bool cvalid[NT];
+  QueryColumn<QT, D> qraw[NT];
+  const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
+  int ids = 0;
+  auto load_ids = [&](int s0) __attribute__((always_inline)) {
+    const int blk = b_lo + (s0 + lane) * kWaves + wave;
+    ids = (s0 + lane < nsteps && blk < b_hi) ? bt[blk] : 0;
+  };
+  if (nsteps > 0) load_ids(0);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int f = (wave * NT + t) * 16 + r;
@@ -413,9 +567,38 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     const int p = pos0 + ctok[t];
     lo[t] = cvalid[t] ? (a.window > 0 ? max(0, p - a.window + 1) : 0) : INT_MAX;
     hi[t] = cvalid[t] ? (a.causal ? p : ctx - 1) : -1;
+    // an invalid column reads token t0's row (in range) and is zeroed when quantized
     const QT* qp = static_cast<const QT*>(a.q) + (int64_t)(q0 + (cvalid[t] ? ctok[t] : t0)) * a.q_tok +
                    (int64_t)chead[t] * a.q_head + 16 * qg;
-    cf[t] = query_column_i8<QT, D>(qp, cvalid[t], a.qk_scale_log2, qhi[t], qlo[t]);
+    load_query_column<QT, D>(qp, qraw[t]);
+  }
+
+  // ---- 3. key steps: block b_lo + 4*step + w is staged by wave w. Lane i of `ids`
+  // holds the id for step (i + 64*k); reloaded every 64 steps.
+  bool bad_index = false, bad_score = false;
+  auto issue = [&](int step, char* buf) -> bool __attribute__((always_inline)) {
+    if (b_lo + step * kWaves + wave >= b_hi) return false;
+    const int id = __builtin_amdgcn_readlane(ids, step % kWave);
+    if ((unsigned)id >= (unsigned)a.cache.num_blocks) {
+      bad_index = true;
+      return false;
+    }
+    stage_block<D>(a, id, kvh, lane, buf + wave * S::kBytes);
+    return true;
+  };
+  auto buffer = [&](int step) __attribute__((always_inline)) -> char* {
+    return lds + (step % NB) * kWaves * S::kBytes;
+  };
+  // bit (step % NB): this wave issued loads for that step (uniform over the wave)
+  uint32_t inflight = 0;
+  for (int j = 0; j < NB - 1 && j < nsteps; ++j)
+    if (issue(j, buffer(j))) inflight |= 1u << (j % NB);
+
+  int4_t qhi[NT][D / 64], qlo[NT][D / 64];
+  float cf[NT], cfe[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    cf[t] = query_column_i8<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qhi[t], qlo[t]);
     cfe[t] = cf[t] > 0.f ? cf[t] : FLT_MIN;  // cf >= 0 or NaN (scale > 0)
   }
   // key bounds over the wave's valid columns (positions grow with f)
@@ -436,34 +619,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     m[t] = -FLT_MAX;  // finite start: fully masked blocks give exp2(-inf) = 0
     l[t] = 0.f;
   }
-  bool bad_index = false, bad_score = false;
 
-  // ---- 3. key steps: block b_lo + 4*step + w is staged by wave w. Lane i of `ids`
-  // holds the id for step (i + 64*k); reloaded every 64 steps.
-  const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
-  int ids = 0;
-  auto load_ids = [&](int s0) __attribute__((always_inline)) {
-    const int blk = b_lo + (s0 + lane) * kWaves + wave;
-    ids = (s0 + lane < nsteps && blk < b_hi) ? bt[blk] : 0;
-  };
-  auto issue = [&](int step, char* buf) -> bool __attribute__((always_inline)) {
-    if (b_lo + step * kWaves + wave >= b_hi) return false;
-    const int id = __builtin_amdgcn_readlane(ids, step % kWave);
-    if ((unsigned)id >= (unsigned)a.cache.num_blocks) {
-      bad_index = true;
-      return false;
-    }
-    stage_block<D>(a, id, kvh, lane, buf + wave * S::kBytes);
-    return true;
-  };
-  auto buffer = [&](int step) __attribute__((always_inline)) -> char* {
-    return lds + (step % NB) * kWaves * S::kBytes;
-  };
-  // bit (step % NB): this wave issued loads for that step (uniform over the wave)
-  uint32_t inflight = 0;
-  if (nsteps > 0) load_ids(0);
-  for (int j = 0; j < NB - 1 && j < nsteps; ++j)
-    if (issue(j, buffer(j))) inflight |= 1u << (j % NB);
   for (int i = 0; i < nsteps; ++i) {
     const int ahead = i + NB - 1;
     if (ahead < nsteps) {
@@ -487,21 +643,20 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     convert_v<D>(cur + wave * S::kBytes, (inflight >> (i % NB)) & 1u, lane, wave % 2,
                  reinterpret_cast<uint2*>(vt[wave / 2]));
     __syncthreads();  // every wave's block of step i has landed and been converted
-#pragma unroll 1
-    for (int bp = 0; bp < kWaves; bp += 2) {
-      const int kb = (b_lo + i * kWaves + bp) * kBlockTokens;
+    {
+      const int kb0 = (b_lo + i * kWaves) * kBlockTokens;
       const int kend = b_hi * kBlockTokens;
-      if (kb >= kend) break;
-      const bool useA = wave_any && kb <= w_hi_max && kb + kBlockTokens - 1 >= w_lo_min;
-      const int kbB = kb + kBlockTokens;
-      const bool useB = wave_any && kbB < kend && kbB <= w_hi_max &&
-                        kbB + kBlockTokens - 1 >= w_lo_min;
-      if (!useA && !useB) continue;
-      const bool maskedA = !(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min);
-      const bool maskedB = !(kbB >= w_lo_max && kbB + kBlockTokens - 1 <= w_hi_min);
-      prefill_pair<D, NT>(cur + bp * S::kBytes, cur + (bp + 1) * S::kBytes, vt[bp / 2],
-                          useA && useB && !maskedA && !maskedB, useA, useB, kb, maskedA, maskedB,
-                          qhi, qlo, cf, cfe, lo, hi, r, qg, acc, m, l, bad_score);
+      uint32_t use = 0, bounded = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const int kb = kb0 + w * kBlockTokens;
+        if (wave_any && kb < kend && kb <= w_hi_max && kb + kBlockTokens - 1 >= w_lo_min)
+          use |= 1u << w;
+        if (!(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min)) bounded |= 1u << w;
+      }
+      if (use != 0)
+        prefill_step<D, NT>(cur, vt[0], use, bounded & use, kb0, qhi, qlo, cf, cfe, lo, hi, r, qg,
+                            acc, m, l, bad_score);
     }
     __syncthreads();  // step i's stage may be refilled
   }

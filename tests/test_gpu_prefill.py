@@ -87,6 +87,21 @@ def test_scaled_config3_matches_oracle(device, part):
     assert_attention_close(out, oracle_decode(w, cache, q))
 
 
+@pytest.mark.parametrize("rows", [256, 257])
+def test_many_chunk_rows(device, rows):
+    """Chunk rows are dispatched longest first up to 256 of them and in index order
+    beyond: both sides of that boundary, with decode rows interleaved."""
+    rng = np.random.default_rng(rows)
+    q_lens = rng.integers(2, 24, rows + rows // 6)
+    q_lens[rng.choice(q_lens.size, rows // 6, replace=False)] = 1  # exactly `rows` chunk rows
+    ctx = q_lens + rng.integers(0, 160, q_lens.size)
+    w = _mixed(q_lens, ctx, hq=4, hkv=2, dim=64, seed=rows)
+    cache, tables, lens, qsl = _build(w, device)
+    q = wl.queries(w, device)
+    out = _run(cache, w, q, tables, lens, qsl)
+    assert_attention_close(out, oracle_decode(w, cache, q))
+
+
 def test_chunk_last_token_equals_decode_kernel(device):
     """The last query of a chunk sees exactly the keys a decode query at ctx-1 sees:
     the prefill kernel and the decode kernels agree on it."""
