@@ -257,18 +257,21 @@ __device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, 
   return mx > 0.f ? qk_scale_log2 * (mx / (float)kQRange) : 0.f;
 }
 
-// V codes of one staged block as the f16 A-operands of the PV MFMAs, written once
-// by the wave that loaded the block into the slab of its block pair: half `half` of
-// entry n * 64 + lane holds, for that lane (qg, r) of every wave, V[4 qg + j][r * VB + n],
-// j = 0..3 (exact f16), so that one 16-byte read at the reader's own lane index gives
-// the pair's whole operand (conflict-free). `present` false writes zeros (the slab
-// never holds stale or uninitialized values).
+// Dequantized V of one staged block as the f16 A-operands of the PV MFMAs, written
+// once by the wave that loaded the block into the slab of its block pair: half `half`
+// of entry n * 64 + lane holds, for that lane (qg, r) of every wave,
+// V[4 qg + j][r * VB + n] * v_scale[4 qg + j], j = 0..3, so that one 16-byte read at the
+// reader's own lane index gives the pair's whole operand (conflict-free). The code is
+// exact in f16 and multiplied by the f16-rounded scale. A block that was not loaded
+// this step leaves stale codes and finite (or zeroed) scales: finite values, which meet
+// p = 0 for its keys.
 template <int D>
-__device__ __forceinline__ void convert_v(const char* st, bool present, int lane, int half,
-                                          uint2* vt) {
+__device__ __forceinline__ void convert_v(const char* st, int lane, int half, uint2* vt) {
   using S = Stage<D>;
   constexpr int VB = D / 16;
   const int r = lane & 15, qg = lane >> 4;
+  const float4_t vsf = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg);
+  const half4_t vsh = {(_Float16)vsf[0], (_Float16)vsf[1], (_Float16)vsf[2], (_Float16)vsf[3]};
   uint32_t vw[4][VB / 4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -297,7 +300,7 @@ __device__ __forceinline__ void convert_v(const char* st, bool present, int lane
       case 2: v = v_operand<2>(col); break;
       default: v = v_operand<3>(col); break;
     }
-    vt[2 * (n * kWave + lane) + half] = present ? __builtin_bit_cast(uint2, v) : uint2{0u, 0u};
+    vt[2 * (n * kWave + lane) + half] = __builtin_bit_cast(uint2, v * vsh);
   }
 }
 
@@ -308,7 +311,8 @@ __device__ __forceinline__ float vmax(float a, float b) { return __builtin_eleme
 //   S^T = K . Q^T      v_mfma_i32_16x16x64_i8 twice per 64-wide d chunk (hi, then lo
 //                      on the hi result shifted by 7): exact int32 dot products
 //   O^T += V^T . P^T   v_mfma_f32_16x16x32_f16 over the 32 keys of block pair
-//                      (0, 1) and (2, 3)
+//                      (0, 1) and (2, 3); V^T carries the V scales, one more tile
+//                      with a row of ones accumulates the softmax row sums
 // Score slot j = 4 w + i of lane group qg is key 4 qg + i of block w; in the PV
 // operands, slots 8 p + [0, 8) of pair p match the interleaved V slab. The base-2
 // score of a key is u * cf with u = S_int * k_scale, folded into the exponent as
@@ -326,8 +330,9 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
                                              const int4_t (&qlo)[NT][D / 64],
                                              const float (&cf)[NT], const float (&cfe)[NT],
                                              const int (&lo)[NT], const int (&hi)[NT], int r,
-                                             int qg, float4_t (&acc)[NT][D / 16], float (&m)[NT],
-                                             float (&l)[NT], bool& bad_score) {
+                                             int qg, const half8_t& ones,
+                                             float4_t (&acc)[NT][D / 16 + 1], float (&m)[NT],
+                                             bool& bad_score) {
   using S = Stage<D>;
   constexpr int KCH = D / 64;
   constexpr int NPV = D / 16;
@@ -409,26 +414,20 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
       x = fmaxf(x, shfl_xor(x, 32));
       const float mn = fmaxf(m[t], x);
       const float alpha = __builtin_amdgcn_exp2f(m[t] - mn);
-      l[t] *= alpha;
 #pragma unroll
-      for (int n = 0; n < NPV; ++n) acc[t][n] *= alpha;
+      for (int n = 0; n <= NPV; ++n) acc[t][n] *= alpha;
       m[t] = mn;
     }
   }
   const int lane = qg * 16 + r;
 #pragma unroll
   for (int pp = 0; pp < NBK / 2; ++pp) {
-    const float4_t vsA = *reinterpret_cast<const float4_t*>(cur + (2 * pp) * S::kBytes + S::kS + 64 + 16 * qg);
-    const float4_t vsB = *reinterpret_cast<const float4_t*>(cur + (2 * pp + 1) * S::kBytes + S::kS + 64 + 16 * qg);
     half8_t pop[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(u[t][8 * pp + i], cfe[t], -m[t]));
-        l[t] += p;
-        pop[t][i] = (_Float16)(p * (i < 4 ? vsA[i] : vsB[i - 4]));
-      }
+      for (int i = 0; i < 8; ++i)
+        pop[t][i] = (_Float16)__builtin_amdgcn_exp2f(fmaf(u[t][8 * pp + i], cfe[t], -m[t]));
 #pragma unroll
     for (int n = 0; n < NPV; ++n) {
       const half8_t vop = __builtin_bit_cast(half8_t, vt[pp * (NPV * kWave) + n * kWave + lane]);
@@ -436,6 +435,11 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
       for (int t = 0; t < NT; ++t)
         acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[t], acc[t][n], 0, 0, 0);
     }
+    // row sums: a V^T row of ones (row 0 of the extra tile) gives sum_k f16(p_k), the
+    // same rounded weights the numerator uses
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      acc[t][NPV] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop[t], acc[t][NPV], 0, 0, 0);
   }
 }
 
@@ -610,14 +614,15 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   const int w_lo_min = a.window > 0 ? max(0, pos0 + tk_lo - a.window + 1) : 0;
   const int w_lo_max = a.window > 0 ? max(0, pos0 + tk_hi - a.window + 1) : 0;
 
-  float4_t acc[NT][NPV];
-  float m[NT], l[NT];
+  float4_t acc[NT][NPV + 1];  // [NPV]: row sums in row 0 (lanes qg = 0)
+  const _Float16 one = r == 0 ? (_Float16)1.f : (_Float16)0.f;
+  const half8_t ones = {one, one, one, one, one, one, one, one};  // A operand: row 0 all ones
+  float m[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
 #pragma unroll
-    for (int k = 0; k < NPV; ++k) acc[t][k] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k <= NPV; ++k) acc[t][k] = float4_t{0.f, 0.f, 0.f, 0.f};
     m[t] = -FLT_MAX;  // finite start: fully masked blocks give exp2(-inf) = 0
-    l[t] = 0.f;
   }
 
   for (int i = 0; i < nsteps; ++i) {
@@ -640,8 +645,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     char* const cur = buffer(i);
     // this wave's block of step i is in; its V operands go to the wave's slab (the
     // previous step's readers are past the barrier that ended that step)
-    convert_v<D>(cur + wave * S::kBytes, (inflight >> (i % NB)) & 1u, lane, wave % 2,
-                 reinterpret_cast<uint2*>(vt[wave / 2]));
+    convert_v<D>(cur + wave * S::kBytes, lane, wave % 2, reinterpret_cast<uint2*>(vt[wave / 2]));
     __syncthreads();  // every wave's block of step i has landed and been converted
     {
       const int kb0 = (b_lo + i * kWaves) * kBlockTokens;
@@ -656,7 +660,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
       }
       if (use != 0)
         prefill_step<D, NT>(cur, vt[0], use, bounded & use, kb0, qhi, qlo, cf, cfe, lo, hi, r, qg,
-                            acc, m, l, bad_score);
+                            ones, acc, m, bad_score);
     }
     __syncthreads();  // step i's stage may be refilled
   }
@@ -666,8 +670,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   // ---- 4. normalise and store (fully masked columns: l = 0, acc = 0 -> 0)
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    float lt = l[t] + shfl_xor(l[t], 16);
-    lt += shfl_xor(lt, 32);
+    const float lt = __shfl(acc[t][NPV][0], r, kWave);  // row 0 of the sum tile: lane (0, r)
     if (!cvalid[t]) continue;
     const float inv = 1.f / fmaxf(lt, FLT_MIN);
     QT* op = static_cast<QT*>(a.out) + (int64_t)(q0 + ctok[t]) * a.o_tok +
