@@ -28,6 +28,7 @@ ASTR_F32, ASTR_F16, ASTR_BF16 = 0, 1, 2
 # Every symbol include/aster_kv.h declares (checked by tests/test_capi.py).
 EXPORTED_SYMBOLS = (
     "astr_kv_quantize_append_i8",
+    "astr_kv_write_key_valid",
     "astr_paged_attention_i8",
     "astr_paged_attention_varlen_i8",
     "astr_paged_attention_i8_workspace_bytes",
@@ -53,6 +54,7 @@ class PagedKVDesc(ctypes.Structure):
         ("block_size", ctypes.c_int32),
         ("num_kv_heads", ctypes.c_int32),
         ("head_dim", ctypes.c_int32),
+        ("key_valid", ctypes.c_void_p),
     ]
 
 
@@ -82,6 +84,8 @@ def lib():
             desc_p, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp,
         ]
         handle.astr_kv_quantize_append_i8.restype = ctypes.c_int
+        handle.astr_kv_write_key_valid.argtypes = [desc_p, c_vp, c_vp, c_i64, c_vp, c_vp]
+        handle.astr_kv_write_key_valid.restype = ctypes.c_int
         handle.astr_paged_attention_i8.argtypes = [
             desc_p, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i32, c_vp, c_i32,
             c_i32, c_i32, ctypes.c_float, c_i32, c_i32, c_vp, c_sz, c_vp, c_vp,

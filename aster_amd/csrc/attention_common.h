@@ -105,13 +105,15 @@ __device__ __forceinline__ RowSpan row_span(const AttnArgs& a, int ctx) {
 }
 
 // ---- LDS stage of one 16-token block of one kv head, as it sits in HBM:
-// K codes (16 rows x D bytes), V codes, then 16 K and 16 V fp32 scales.
+// K codes (16 rows x D bytes), V codes, 16 K and 16 V fp32 scales, then the 16
+// key-padding bytes of the block (loaded only when the arena has them).
 template <int D>
 struct Stage {
   static constexpr int kK = 0;
   static constexpr int kV = 16 * D;
   static constexpr int kS = 32 * D;
-  static constexpr int kBytes = 32 * D + 128;
+  static constexpr int kF = 32 * D + 128;
+  static constexpr int kBytes = 32 * D + 144;
   static constexpr int kCodeLoads = 16 * D / 1024;   // 1 KiB wave-loads per K (and per V) tile
   static constexpr int kLoads = 2 * kCodeLoads + 1;  // vector-memory instructions per stage
 };
@@ -143,6 +145,23 @@ __device__ __forceinline__ void lds_dma_x1(const void* gptr, uint32_t lds) {
                : "memory");
 }
 
+// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset
+// (the saddr form: no 64-bit per-lane address to hold). No instruction offset: the
+// LDS destination is M0 + lane * 16 (or 4) exactly.
+__device__ __forceinline__ void lds_dma_x4_s(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(sbase)
+               : "memory");
+}
+
+__device__ __forceinline__ void lds_dma_x1_s(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(sbase)
+               : "memory");
+}
+
 // Wait until at most N vector-memory operations of this wave are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -151,27 +170,35 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // Issue the direct-to-LDS loads of block `phys` (kv head kvh) into stage `st`:
-// exactly Stage<D>::kLoads vector-memory instructions (waves are always full,
-// so the 32-lane scale load always issues).
+// Stage<D>::kLoads vector-memory instructions (waves are always full, so the
+// 32-lane scale load always issues), plus one for the block's 16 key-padding bytes
+// when the arena has them.
 template <int D>
 __device__ __forceinline__ void stage_block(const AttnArgs& a, int phys, int kvh, int lane,
                                             char* st) {
   using S = Stage<D>;
   const int64_t off = (int64_t)phys * a.cache.code_block_stride +
-                      (int64_t)kvh * a.cache.code_head_stride + lane * 16;
+                      (int64_t)kvh * a.cache.code_head_stride;  // wave-uniform
   const uint32_t base = lds_addr(st);
+  const int8_t* const kb = a.cache.k_codes + off;
+  const int8_t* const vb = a.cache.v_codes + off;
 #pragma unroll
   for (int j = 0; j < S::kCodeLoads; ++j)
-    lds_dma_x4(a.cache.k_codes + off + j * 1024, base + S::kK + j * 1024);
+    lds_dma_x4_s(kb, lane * 16 + j * 1024, base + S::kK + j * 1024);
 #pragma unroll
   for (int j = 0; j < S::kCodeLoads; ++j)
-    lds_dma_x4(a.cache.v_codes + off + j * 1024, base + S::kV + j * 1024);
+    lds_dma_x4_s(vb, lane * 16 + j * 1024, base + S::kV + j * 1024);
   const int64_t so = (int64_t)phys * a.cache.scale_block_stride +
                      (int64_t)kvh * a.cache.scale_head_stride;
   if (lane < 32) {
     const float* src = lane < 16 ? a.cache.k_scales + so + lane : a.cache.v_scales + so + lane - 16;
     lds_dma_x1(src, base + S::kS);
   }
+  // key padding bytes: one more instruction, issued last, only when the arena has
+  // them. Stage pipelines count kLoads per stage: with this extra load their waits
+  // let fewer loads stay in flight than allowed, never more, as loads complete in order.
+  if (a.cache.key_valid != nullptr && lane < 4)
+    lds_dma_x1_s(a.cache.key_valid + (int64_t)phys * kBlockTokens, lane * 4, base + S::kF);
 }
 
 // ---- exact int8 -> f16 operands
@@ -303,7 +330,7 @@ template <int D, int G>
 __device__ __forceinline__ void mfma_block(const char* st, const half8_t (&qop)[D / 32], float cf,
                                            int tok_base, int kv_begin, int ctx, int r, int qg,
                                            float4_t (&acc)[D / 16], float& m, float& l,
-                                           bool& bad_score) {
+                                           bool& bad_score, bool masks = false) {
   using S = Stage<D>;
   constexpr int KCH = D / 64;
   constexpr int VB = D / 16;
@@ -344,14 +371,18 @@ __device__ __forceinline__ void mfma_block(const char* st, const half8_t (&qop)[
   }
   // scores of tokens 4*qg + j for head g = r (base 2, dequantised)
   const int tok0 = tok_base + 4 * qg;
-  const bool edge = tok_base < kv_begin || tok_base + kBlockTokens > ctx;
+  // a block holding a padding key takes the edge path, which reads each key's byte
+  bool padded = false;
+  if (masks) padded = __ballot(*reinterpret_cast<const uint32_t*>(st + S::kF + 4 * qg) != 0x01010101u) != 0;
+  const bool edge = tok_base < kv_begin || tok_base + kBlockTokens > ctx || padded;
   float sc[4];
   bool need = false, nonfinite = false;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     float v = s4[j] * (ks[j] * cf);
     bool valid = gvalid;
-    if (edge) valid = valid && tok0 + j >= kv_begin && tok0 + j < ctx;
+    if (edge)
+      valid = valid && tok0 + j >= kv_begin && tok0 + j < ctx && (!masks || st[S::kF + 4 * qg + j] != 0);
     nonfinite |= valid && !__builtin_isfinite(v);
     v = valid ? v : -INFINITY;
     need |= v > m + kRescaleSlack;

@@ -164,7 +164,9 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   float4_t acc[NPV];
 #pragma unroll
   for (int n = 0; n < NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m = gvalid ? -INFINITY : 0.f;  // invalid head columns never contribute
+  // invalid head columns never contribute; a finite start makes a block whose keys are
+  // all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
+  float m = gvalid ? -FLT_MAX : 0.f;
   float l = 0.f;
   bool bad_score = false;
 
@@ -175,7 +177,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
     else if (later == 1) wait_vmcnt<S::kLoads>();
     else wait_vmcnt<0>();
     mfma_block<D, G>(st, qop, cf, (first + kWaves * i) * kBlockTokens, row.kv_begin, row.ctx, r,
-                     qg, acc, m, l, bad_score);
+                     qg, acc, m, l, bad_score, a.cache.key_valid != nullptr);
     // refill this stage with block i + NS (its LDS reads above fed the MFMAs)
     if (i + NS < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, i + NS), kvh, lane, st);
   };
@@ -218,6 +220,7 @@ struct ValuTile {
   uint4 v[NL];
   float ks[NL];
   float vs[NL];
+  uint8_t kv[NL];  // key padding bytes (1 without a mask)
 };
 
 // Heads of a GQA group one VALU workgroup serves: a lane keeps 16 query values and
@@ -272,7 +275,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
   float m[G], l[G], acc[G][16];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
+    m[g] = -FLT_MAX;  // finite: an all-masked block gives exp2(-inf) = 0
     l[g] = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[g][i] = 0.f;
@@ -281,6 +284,8 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
   const int8_t* vbase = a.cache.v_codes + (int64_t)kvh * a.cache.code_head_stride + lane * 16;
   const float* ksbase = a.cache.k_scales + (int64_t)kvh * a.cache.scale_head_stride + lrow;
   const float* vsbase = a.cache.v_scales + (int64_t)kvh * a.cache.scale_head_stride + lrow;
+  const bool masks = a.cache.key_valid != nullptr;  // key padding bytes of the token rows
+  const uint8_t* kvbase = masks ? a.cache.key_valid + lrow : nullptr;
   auto load = [&](int phys, ValuTile<NL>& t) __attribute__((always_inline)) {
     const int8_t* kp = kbase + (int64_t)phys * a.cache.code_block_stride;
     const int8_t* vp = vbase + (int64_t)phys * a.cache.code_block_stride;
@@ -292,6 +297,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
       t.v[j] = *reinterpret_cast<const uint4*>(vp + j * kLoadBytes);
       t.ks[j] = ksp[j * TPL];
       t.vs[j] = vsp[j * TPL];
+      t.kv[j] = masks ? kvbase[(int64_t)phys * kBlockTokens + j * TPL] : (uint8_t)1;
     }
   };
 
@@ -324,7 +330,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
       const int tok = blk * kBlockTokens + j * TPL + lrow;
-      const bool valid = tok >= row.kv_begin && tok < row.ctx;
+      const bool valid = tok >= row.kv_begin && tok < row.ctx && cur.kv[j] != 0;
       const float f = cur.ks[j] * a.qk_scale_log2;
 #pragma unroll
       for (int g = 0; g < G; ++g) {

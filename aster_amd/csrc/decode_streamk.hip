@@ -215,13 +215,15 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     }
 #pragma unroll
     for (int k = 0; k < NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
-    m = gvalid ? -INFINITY : 0.f;  // invalid head columns never contribute
+    // invalid head columns never contribute; a finite start makes a block whose keys
+    // are all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
+    m = gvalid ? -FLT_MAX : 0.f;
     l = 0.f;
     const int blk0 = psp.first_blk + (int)(b0 + i - pfb);
     for (; i < iend; ++i) {
       wait_block(i);
       mfma_block<D, G>(stage(i), qop, cf, (blk0 + i - pstart) * kBlockTokens, psp.kv_begin,
-                       psp.ctx, r, qg, acc, m, l, bad_score);
+                       psp.ctx, r, qg, acc, m, l, bad_score, a.cache.key_valid != nullptr);
       if (i + NS < nblk) issue(i + NS);
     }
     // write the piece: the final output when the whole row is in this wave, else a

@@ -185,8 +185,47 @@ int launch_append_dim(const AppendArgs& a, hipStream_t stream) {
   return launch_append<T, 0>(a, stream);
 }
 
+// One thread per token: the slot's key-padding byte (state.py:339-344 copies the
+// padding leaf into the page like every other leaf).
+__global__ __launch_bounds__(256) void write_key_valid_kernel(uint8_t* key_valid, int64_t slots,
+                                                              const int64_t* slot_mapping,
+                                                              const uint8_t* token_valid,
+                                                              int64_t num_tokens, int32_t* err_flag) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= num_tokens) return;
+  const int64_t slot = slot_mapping[i];
+  if (slot < 0) return;
+  if (slot >= slots) {
+    atomicOr(err_flag, ASTR_FLAG_BAD_INDEX);
+    return;
+  }
+  key_valid[slot] = token_valid == nullptr || token_valid[i] != 0 ? 1 : 0;
+}
+
 }  // namespace
 }  // namespace astr
+
+extern "C" int astr_kv_write_key_valid(const astr_paged_kv* cache, const int64_t* slot_mapping,
+                                       const uint8_t* token_valid, int64_t num_tokens,
+                                       int32_t* err_flag, void* stream) {
+  using namespace astr;
+  if (cache == nullptr || err_flag == nullptr)
+    return fail(ASTR_EINVAL, "cache descriptor and err_flag are required");
+  if (cache->key_valid == nullptr) return fail(ASTR_EINVAL, "cache key_valid pointer is required");
+  if (num_tokens < 0) return fail(ASTR_EINVAL, "num_tokens must be >= 0");
+  if (num_tokens == 0) return 0;
+  if (slot_mapping == nullptr) return fail(ASTR_EINVAL, "slot_mapping is required");
+  if (cache->num_blocks < 1 || cache->block_size < 1)
+    return fail(ASTR_EINVAL, "cache sizes must be positive");
+  const int64_t blocks = (num_tokens + 255) / 256;
+  if (blocks > INT32_MAX) return fail(ASTR_EINVAL, "too many tokens for one launch");
+  hipLaunchKernelGGL(write_key_valid_kernel, dim3((uint32_t)blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), cache->key_valid,
+                     (int64_t)cache->num_blocks * cache->block_size, slot_mapping, token_valid,
+                     num_tokens, err_flag);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "write_key_valid launch");
+}
 
 extern "C" int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void* key,
                                           const void* value, int32_t in_dtype, int64_t num_tokens,

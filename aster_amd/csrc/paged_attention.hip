@@ -187,6 +187,8 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
       !aligned16(cache->k_scales) || !aligned16(cache->v_scales) ||
       cache->scale_block_stride % 4 || cache->scale_head_stride % 4)
     return fail(ASTR_EINVAL, "cache code and scale blocks must be 16-byte aligned");
+  if (cache->key_valid != nullptr && !aligned16(cache->key_valid))
+    return fail(ASTR_EINVAL, "cache key_valid must be 16-byte aligned");
   const int64_t parts = max_parts_for(max_context_len, pt);
   if (!streamk && parts > 65535)
     return fail(ASTR_EUNSUPPORTED, "too many split-K partitions (%lld)", (long long)parts);

@@ -318,14 +318,17 @@ __device__ __forceinline__ float vmax(float a, float b) { return __builtin_eleme
 // score of a key is u * cf with u = S_int * k_scale, folded into the exponent as
 // fma(u, cfe, -m) (cfe = cf, or FLT_MIN where cf = 0, so that a masked u = -inf stays
 // -inf). Bit w of `use` (wave-uniform): block w holds keys some column of the wave
-// sees; of `bounded`: the column bounds [lo, hi] cut into block w. With every block
-// used, none bounded and every key scale times query factor below kSafeFactor (no
-// score can overflow) the step takes no per-score condition; otherwise the scores are
-// masked to -inf outside the bounds and for unused blocks (whose stages hold stale but
-// finite codes and scales, and zero V operands) and checked for non-finite values.
+// sees; of `bounded`: the column bounds [lo, hi] cut into block w. `masks`: the
+// stages carry the blocks' padding bytes (0 = padding key), and a step holding one
+// takes the edge path.
+// With every block used, none bounded and every key scale times query factor below
+// kSafeFactor (no score can overflow) the step takes no per-score condition; otherwise
+// the scores are masked to -inf outside the bounds, for padding keys and for unused
+// blocks (whose stages hold stale but finite codes and scales) and checked for
+// non-finite values.
 template <int D, int NT>
 __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, uint32_t use,
-                                             uint32_t bounded, int kb0,
+                                             uint32_t bounded, bool masks, int kb0,
                                              const int4_t (&qhi)[NT][D / 64],
                                              const int4_t (&qlo)[NT][D / 64],
                                              const float (&cf)[NT], const float (&cfe)[NT],
@@ -337,6 +340,15 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
   constexpr int KCH = D / 64;
   constexpr int NPV = D / 16;
   constexpr int NBK = kWaves;  // blocks per step
+  // a step holding a padding key takes the edge path (read ahead of the QK block)
+  bool padded = false;
+  if (masks) {
+    uint32_t bad = 0;
+#pragma unroll
+    for (int b = 0; b < NBK; ++b)
+      bad |= *reinterpret_cast<const uint32_t*>(cur + b * S::kBytes + S::kF + 4 * qg) ^ 0x01010101u;
+    padded = __ballot(bad != 0) != 0;
+  }
   int4_t sacc[NBK][NT];
 #pragma unroll
   for (int b = 0; b < NBK; ++b) {
@@ -374,7 +386,7 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
 #pragma unroll
   for (int t = 0; t < NT; ++t) ok = ok && kmax * cf[t] <= kSafeFactor;  // false for NaN
   const bool unsafe = __ballot(!ok) != 0;
-  const bool edge = (use != (1u << NBK) - 1) | (bounded != 0) | unsafe;
+  const bool edge = (use != (1u << NBK) - 1) | (bounded != 0) | unsafe | padded;
   float u[NT][4 * NBK];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -390,7 +402,8 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
         const int b = j / 4;
         const int key = kb0 + 16 * b + 4 * qg + j % 4;
         const bool inside = (unsigned)(key - lo[t]) <= (unsigned)(hi[t] - lo[t]);  // lo <= key <= hi
-        const bool vis = ((use >> b) & 1u) && (!((bounded >> b) & 1u) || inside);
+        const bool real = !masks || cur[b * S::kBytes + S::kF + 4 * qg + j % 4] != 0;  // not padding
+        const bool vis = ((use >> b) & 1u) && (!((bounded >> b) & 1u) || inside) && real;
         nonfinite |= vis & !__builtin_isfinite(u[t][j] * cf[t]);
         u[t][j] = vis ? u[t][j] : -INFINITY;
       }
@@ -580,6 +593,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   // ---- 3. key steps: block b_lo + 4*step + w is staged by wave w. Lane i of `ids`
   // holds the id for step (i + 64*k); reloaded every 64 steps.
   bool bad_index = false, bad_score = false;
+  const bool masks = a.cache.key_valid != nullptr;  // the arena has key padding bytes
   auto issue = [&](int step, char* buf) -> bool __attribute__((always_inline)) {
     if (b_lo + step * kWaves + wave >= b_hi) return false;
     const int id = __builtin_amdgcn_readlane(ids, step % kWave);
@@ -659,7 +673,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
         if (!(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min)) bounded |= 1u << w;
       }
       if (use != 0)
-        prefill_step<D, NT>(cur, vt[0], use, bounded & use, kb0, qhi, qlo, cf, cfe, lo, hi, r, qg,
+        prefill_step<D, NT>(cur, vt[0], use, bounded & use, masks, kb0, qhi, qlo, cf, cfe, lo, hi, r, qg,
                             ones, acc, m, bad_score);
     }
     __syncthreads();  // step i's stage may be refilled

@@ -34,6 +34,7 @@ class _PagedSnapshot:
     length: int
     codes: torch.Tensor   # host int8 [P, L, 2, Hkv, bs, D]
     scales: torch.Tensor  # host fp32 [P, L, 2, Hkv, bs]
+    valid: torch.Tensor   # host uint8 [P, bs]: the pages' padding leaves (0 = padding key)
     nbytes: int
 
 
@@ -86,10 +87,11 @@ class PagedStateArchive:
         return self._stream
 
     def _payload_bytes(self, length):
-        """Bytes of the archived leaves: codes and scales of every committed token
-        (what the reference sums over the narrowed page payloads)."""
+        """Bytes of the archived leaves: codes and scales of every committed token and
+        its bool padding byte (what the reference sums over the narrowed page
+        payloads, offload.py:146)."""
         c = self.pool.cache
-        return length * c.num_layers * 2 * c.num_kv_heads * (c.head_dim + 4)
+        return length * (c.num_layers * 2 * c.num_kv_heads * (c.head_dim + 4) + 1)
 
     def put(self, sequence):
         pool = self.pool
@@ -105,21 +107,21 @@ class PagedStateArchive:
             try:
                 stream = self._copy_stream()
                 stream.wait_stream(torch.cuda.current_stream(pool.cache.device))
-                codes, scales = pool.export_blocks(sequence, stream=stream)
+                blocks = pool.export_blocks(sequence, stream=stream)
                 with torch.cuda.stream(stream):
-                    host_codes = torch.empty(codes.shape, dtype=codes.dtype,
-                                             pin_memory=self.pin_memory)
-                    host_scales = torch.empty(scales.shape, dtype=scales.dtype,
-                                              pin_memory=self.pin_memory)
-                    host_codes.copy_(codes, non_blocking=self.pin_memory)
-                    host_scales.copy_(scales, non_blocking=self.pin_memory)
+                    host = []
+                    for t in blocks:
+                        h = torch.empty(t.shape, dtype=t.dtype, pin_memory=self.pin_memory)
+                        h.copy_(t, non_blocking=self.pin_memory)
+                        host.append(h)
+                    host_codes, host_scales, host_valid = host
                 done = torch.cuda.Event()
                 done.record(stream)
                 done.synchronize()
                 handle = uuid.uuid4().hex
                 with self._lock:
                     self._entries[handle] = _PagedSnapshot(sequence.identity, length, host_codes,
-                                                           host_scales, size)
+                                                           host_scales, host_valid, size)
                     self.offloaded_tokens += length
                 return handle
             except BaseException:
@@ -133,7 +135,8 @@ class PagedStateArchive:
             snapshot = self._entries.get(handle)
             if snapshot is None or snapshot.identity != identity:
                 raise StateError("Missing archived KV or identity mismatch")
-        state = self.pool.restore_pages((snapshot.codes, snapshot.scales), identity=identity,
+        state = self.pool.restore_pages((snapshot.codes, snapshot.scales, snapshot.valid),
+                                        identity=identity,
                                         length=snapshot.length, stream=self._copy_stream())
         with self._lock:
             self.restored_tokens += snapshot.length
@@ -148,8 +151,9 @@ class PagedStateArchive:
             self.stored_bytes -= snapshot.nbytes
 
     def pages(self, handle, *, identity):
-        """The archived pages as ``QuantizedKV`` leaves per page (host views),
-        narrowed to the committed tokens, in the ``read_pages`` payload order."""
+        """The archived pages as ``QuantizedKV`` leaves per page (host views), then the
+        bool padding leaf, narrowed to the committed tokens, in the ``read_pages``
+        payload order."""
         from .kv_quantization import QuantizedKV
 
         with self._lock:
@@ -166,6 +170,7 @@ class PagedStateArchive:
                     leaves.append(QuantizedKV(snapshot.codes[p, layer, kv][None, :, :count],
                                               snapshot.scales[p, layer, kv][None, :, :count, None],
                                               torch.float32))
+            leaves.append(snapshot.valid[p, :count].bool()[None, None, :, None])
             out.append(tuple(leaves))
         return tuple(out)
 

@@ -3,13 +3,18 @@
 Arena layout (one allocation per model, block-major so a physical page of all
 layers is contiguous for copy-on-write and host swap):
 
-    codes  int8  [num_blocks, num_layers, 2 (K, V), num_kv_heads, block_size, head_dim]
-    scales fp32  [num_blocks, num_layers, 2 (K, V), num_kv_heads, block_size]
+    codes     int8  [num_blocks, num_layers, 2 (K, V), num_kv_heads, block_size, head_dim]
+    scales    fp32  [num_blocks, num_layers, 2 (K, V), num_kv_heads, block_size]
+    key_valid uint8 [num_blocks, block_size]   (0: the slot holds a padding key)
 
 Block ``b`` is the reference's ``PageRef.index`` (src/aster/inference/state.py:131-134):
 the reference keeps per page and layer a ``QuantizedKV`` of codes ``[1, Hkv, bs, D]``
 and scales ``[1, Hkv, bs, 1]`` (state.py:319-327, kv_quantization.py:97-110);
-here those are ``codes[b, layer, 0|1]`` / ``scales[b, layer, 0|1]`` of one arena.
+here those are ``codes[b, layer, 0|1]`` / ``scales[b, layer, 0|1]`` of one arena,
+and the page's padding leaf ``[1, 1, bs, 1]`` (state.py:319-327; the runner appends it
+with every chunk, paged_attention.py:228) is ``key_valid[b]``, shared by all layers.
+The kernels see ``key_valid`` only once a padding key has been written
+(``write_key_valid``): until then every key is real and they skip the mask.
 
 ``append`` replaces quantize_kv + the per-token copy_kv loop of
 ``PagedStatePool._append_leaves`` (state.py:292, 339-344): token ``t`` goes to
@@ -54,6 +59,8 @@ class PagedKVCache:
                                  dtype=torch.int8, device=device)
         self.scales = torch.ones((num_blocks, num_layers, 2, num_kv_heads, block_size),
                                  dtype=torch.float32, device=device)
+        self.key_valid = torch.ones((num_blocks, block_size), dtype=torch.uint8, device=device)
+        self.has_padding = False  # some slot may hold a padding key (descriptors carry key_valid)
         self.err_flag = torch.zeros(1, dtype=torch.int32, device=device)
         self._workspace = None
         self._descs = [self._make_desc(layer) for layer in range(num_layers)]
@@ -67,14 +74,20 @@ class PagedKVCache:
             code_block_stride=c.stride(0), code_head_stride=c.stride(3),
             scale_block_stride=s.stride(0), scale_head_stride=s.stride(3),
             num_blocks=self.num_blocks, block_size=self.block_size,
-            num_kv_heads=self.num_kv_heads, head_dim=self.head_dim)
+            num_kv_heads=self.num_kv_heads, head_dim=self.head_dim,
+            key_valid=self.key_valid.data_ptr() if self.has_padding else None)
+
+    def _enable_padding(self):
+        if not self.has_padding:
+            self.has_padding = True
+            self._descs = [self._make_desc(layer) for layer in range(self.num_layers)]
 
     def layer_desc(self, layer):
         return self._descs[layer]
 
     @property
     def nbytes(self):
-        return self.codes.numel() + self.scales.numel() * 4
+        return self.codes.numel() + self.scales.numel() * 4 + self.key_valid.numel()
 
     def page(self, block, layer):
         """Zero-copy ``QuantizedKV`` views ``[1, Hkv, bs, D]`` of one page
@@ -84,6 +97,11 @@ class PagedKVCache:
         v = QuantizedKV(self.codes[block, layer, 1][None], self.scales[block, layer, 1][None, ..., None],
                         torch.float32)
         return k, v
+
+    def padding_leaf(self, block):
+        """Zero-copy bool view ``[1, 1, bs, 1]`` of one page's padding leaf (True =
+        real token; the reference's ``PageView.payload[-1]``, state.py:158-163)."""
+        return self.key_valid[block].view(torch.bool)[None, None, :, None]
 
     # ---- error flag ---------------------------------------------------------
     def pending_errors(self):
@@ -128,6 +146,31 @@ class PagedKVCache:
         if check:
             self.raise_errors()
 
+    def write_key_valid(self, slot_mapping, valid=None):
+        """Key-padding bytes of new tokens: ``valid`` (bool/uint8 device ``[T]``,
+        True = real token) into slots ``slot_mapping`` (int64 ``[T]``, negative =
+        skip); None marks every token real. Written once per step for all layers
+        (the padding leaf of state.py:292, 339-344). Without any padding so far and
+        ``valid`` None this is a no-op: every slot is still real."""
+        if (slot_mapping.dtype != torch.int64 or slot_mapping.ndim != 1
+                or slot_mapping.device != self.device or not slot_mapping.is_contiguous()):
+            raise ValueError("slot_mapping must be a contiguous int64 device vector [T]")
+        if valid is None and not self.has_padding:
+            return
+        if valid is not None:
+            valid = torch.as_tensor(valid, device=self.device)
+            if valid.shape != slot_mapping.shape or valid.dtype not in (torch.bool, torch.uint8):
+                raise ValueError("key padding must be a bool/uint8 vector aligned with slot_mapping")
+            valid = valid.to(torch.uint8).contiguous()
+            self._enable_padding()
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _native.check(
+            _native.lib().astr_kv_write_key_valid(
+                self._descs[0], slot_mapping.data_ptr(),
+                valid.data_ptr() if valid is not None else None, slot_mapping.shape[0],
+                self.err_flag.data_ptr(), stream),
+            "write_key_valid")
+
     # ---- whole-block moves (copy-on-write, host swap) ------------------------
     @property
     def block_code_bytes(self):
@@ -160,16 +203,17 @@ class PagedKVCache:
         stream = stream or torch.cuda.current_stream(self.device)
         with torch.cuda.stream(stream):
             src, dst = self._index(src_blocks), self._index(dst_blocks)
-        cb, sb = self.block_code_bytes, self.block_scale_bytes
-        for base, nbytes in ((self.codes.data_ptr(), cb), (self.scales.data_ptr(), sb)):
+        cb, sb, vb = self.block_code_bytes, self.block_scale_bytes, self.block_size
+        for base, nbytes in ((self.codes.data_ptr(), cb), (self.scales.data_ptr(), sb),
+                             (self.key_valid.data_ptr(), vb)):
             self._copy(base, nbytes, src.data_ptr(), self.num_blocks, base, nbytes, dst.data_ptr(),
                        self.num_blocks, nbytes, len(src_blocks), stream.cuda_stream)
         src.record_stream(stream), dst.record_stream(stream)
 
     def gather_blocks(self, blocks, *, stream=None):
-        """Blocks ``blocks`` packed into new device tensors ``codes [P, L, 2, Hkv, bs, D]``
-        and ``scales [P, L, 2, Hkv, bs]`` (the gather half of host swap), enqueued on
-        ``stream``."""
+        """Blocks ``blocks`` packed into new device tensors ``codes [P, L, 2, Hkv, bs, D]``,
+        ``scales [P, L, 2, Hkv, bs]`` and ``valid [P, bs]`` (the gather half of host
+        swap), enqueued on ``stream``."""
         stream = stream or torch.cuda.current_stream(self.device)
         count = len(blocks)
         with torch.cuda.stream(stream):
@@ -177,19 +221,27 @@ class PagedKVCache:
                                 device=self.device)
             scales = torch.empty((count,) + tuple(self.scales.shape[1:]), dtype=self.scales.dtype,
                                  device=self.device)
+            valid = torch.empty((count, self.block_size), dtype=torch.uint8, device=self.device)
             if count:
                 index = self._index(blocks)
-                cb, sb = self.block_code_bytes, self.block_scale_bytes
-                self._copy(self.codes.data_ptr(), cb, index.data_ptr(), self.num_blocks,
-                           codes.data_ptr(), cb, None, count, cb, count, stream.cuda_stream)
-                self._copy(self.scales.data_ptr(), sb, index.data_ptr(), self.num_blocks,
-                           scales.data_ptr(), sb, None, count, sb, count, stream.cuda_stream)
-        return codes, scales
+                for src, dst, nbytes in ((self.codes, codes, self.block_code_bytes),
+                                         (self.scales, scales, self.block_scale_bytes),
+                                         (self.key_valid, valid, self.block_size)):
+                    self._copy(src.data_ptr(), nbytes, index.data_ptr(), self.num_blocks,
+                               dst.data_ptr(), nbytes, None, count, nbytes, count,
+                               stream.cuda_stream)
+        return codes, scales, valid
 
-    def scatter_blocks(self, blocks, codes, scales, *, stream=None):
+    def scatter_blocks(self, blocks, codes, scales, valid=None, *, stream=None):
         """Write packed device blocks (``gather_blocks`` layout) into arena blocks
-        ``blocks`` (the scatter half of host swap), enqueued on ``stream``."""
+        ``blocks`` (the scatter half of host swap), enqueued on ``stream``. ``valid``
+        None marks every restored key real; a given ``valid`` makes the arena carry
+        padding bytes from now on."""
         count = len(blocks)
+        if valid is not None and (valid.shape != (count, self.block_size)
+                                  or valid.dtype != torch.uint8 or valid.device != self.device
+                                  or not valid.is_contiguous()):
+            raise ValueError("packed padding bytes do not match the arena layout")
         if codes.shape != (count,) + tuple(self.codes.shape[1:]) or codes.dtype != self.codes.dtype \
                 or scales.shape != (count,) + tuple(self.scales.shape[1:]) \
                 or scales.dtype != self.scales.dtype or not codes.is_contiguous() \
@@ -201,11 +253,16 @@ class PagedKVCache:
         stream = stream or torch.cuda.current_stream(self.device)
         with torch.cuda.stream(stream):
             index = self._index(blocks)
-        cb, sb = self.block_code_bytes, self.block_scale_bytes
-        self._copy(codes.data_ptr(), cb, None, count, self.codes.data_ptr(), cb, index.data_ptr(),
-                   self.num_blocks, cb, count, stream.cuda_stream)
-        self._copy(scales.data_ptr(), sb, None, count, self.scales.data_ptr(), sb, index.data_ptr(),
-                   self.num_blocks, sb, count, stream.cuda_stream)
+        if valid is None:
+            with torch.cuda.stream(stream):
+                valid = torch.ones((count, self.block_size), dtype=torch.uint8, device=self.device)
+        else:
+            self._enable_padding()
+        for src, dst, nbytes in ((codes, self.codes, self.block_code_bytes),
+                                 (scales, self.scales, self.block_scale_bytes),
+                                 (valid, self.key_valid, self.block_size)):
+            self._copy(src.data_ptr(), nbytes, None, count, dst.data_ptr(), nbytes, index.data_ptr(),
+                       self.num_blocks, nbytes, count, stream.cuda_stream)
         index.record_stream(stream)
 
     def workspace_bytes(self, num_seqs, num_q_heads, max_context_len,

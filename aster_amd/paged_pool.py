@@ -72,7 +72,9 @@ class PagedSequence:
 class PageView:
     """A borrowed page: ``offset`` is the absolute position of its first token;
     ``payload`` holds zero-copy ``QuantizedKV`` views ``(k_0, v_0, k_1, v_1, ...)``
-    of ``[1, Hkv, count, D]`` codes and ``[1, Hkv, count, 1]`` scales."""
+    of ``[1, Hkv, count, D]`` codes and ``[1, Hkv, count, 1]`` scales, then the
+    padding leaf: a bool view ``[1, 1, count, 1]`` (True = real token), as the
+    reference's ``2 * layers + 1`` leaves (paged_attention.py:171-182)."""
 
     offset: int
     payload: tuple
@@ -295,16 +297,19 @@ class PagedStatePool:
     def append_delta(self, sequence, layers, *, check=True):
         """Commit new-token K/V of every layer (state.py:261-267): ``layers`` is one
         ``(key, value)`` per arena layer, ``[1, Hkv, T, D]`` (the reference's state
-        leaves) or ``[T, Hkv, D]`` floating device tensors. Quantized on the device
-        into reserved slots; non-finite input raises ValueError and commits nothing
-        (kv_quantization.py:77-81)."""
-        rows = self._token_rows(layers)
+        leaves) or ``[T, Hkv, D]`` floating device tensors, optionally followed by the
+        padding leaf ``(padding,)``: ``[1, 1, T, 1]`` (or ``[T]``) bool/0-1, True = real
+        token, as the runner appends it (paged_attention.py:228-229). Quantized on the
+        device into reserved slots; non-finite input raises ValueError and commits
+        nothing (kv_quantization.py:77-81)."""
+        rows, padding = self._token_rows(layers)
         count = rows[0][0].shape[0]
         with self.transaction(sequence, count) as reservation:
             if count:
                 slots = reservation.slot_mapping(self.cache.device)
                 for layer, (key, value) in enumerate(rows):
                     self.cache.append(layer, key, value, slots)
+                self.cache.write_key_valid(slots, padding)
                 if check:
                     self.cache.raise_errors()
         return reservation
@@ -312,15 +317,34 @@ class PagedStatePool:
     def append(self, sequence, layers, *, check=True):
         """Append the suffix of a full state (state.py:254-258): tokens from the
         sequence's committed length on."""
-        rows = self._token_rows(layers)
+        rows, padding = self._token_rows(layers)
         total = rows[0][0].shape[0]
         if total < sequence.length:
             raise StateError("Append cannot shrink state")
         start = sequence.length
-        return self.append_delta(sequence, [(k[start:], v[start:]) for k, v in rows], check=check)
+        suffix = [(k[start:], v[start:]) for k, v in rows]
+        if padding is not None:
+            suffix.append((padding[start:],))
+        return self.append_delta(sequence, suffix, check=check)
 
     def _token_rows(self, layers):
+        """``(rows, padding)``: one ``[T, Hkv, D]`` ``(key, value)`` per layer and the
+        padding leaf as a bool device vector ``[T]`` (None when absent)."""
         layers = tuple(layers)
+        padding = None
+        if len(layers) == self.cache.num_layers + 1:
+            leaf = layers[-1]
+            if isinstance(leaf, (tuple, list)) and len(leaf) == 1:
+                leaf = leaf[0]
+            padding = torch.as_tensor(leaf, device=self.cache.device)
+            if padding.ndim == 4:
+                if padding.shape[0] != 1 or padding.shape[1] != 1 or padding.shape[3] != 1:
+                    raise StateError("Padding leaf must be [1, 1, tokens, 1]")
+                padding = padding[0, 0, :, 0]
+            if padding.ndim != 1 or not ((padding == 0) | (padding == 1)).all():
+                raise StateError("Padding leaf must be a binary token vector")
+            padding = padding.bool()
+            layers = layers[:-1]
         if len(layers) != self.cache.num_layers:
             raise StateError("Cache layout changed within a model pool")
         rows = []
@@ -338,9 +362,10 @@ class PagedStatePool:
             if pair[0].shape != pair[1].shape:
                 raise StateError("Every cache leaf must describe the same token span")
             rows.append(tuple(pair))
-        if len({k.shape[0] for k, _ in rows}) != 1:
+        if len({k.shape[0] for k, _ in rows}) != 1 or (
+                padding is not None and padding.shape[0] != rows[0][0].shape[0]):
             raise StateError("Every cache leaf must describe the same token span")
-        return rows
+        return rows, padding
 
     # ---- reads --------------------------------------------------------------
     @contextmanager
@@ -362,6 +387,7 @@ class PagedStatePool:
                 for layer in range(self.cache.num_layers):
                     for leaf in self.cache.page(ref.index, layer):
                         payload.append(leaf.narrow(2, 0, count))
+                payload.append(self.cache.padding_leaf(ref.index)[:, :, :count])
                 views.append(PageView(index * self.block_size, tuple(payload)))
             for ref in refs:
                 self._page(ref).readers += 1
@@ -408,8 +434,9 @@ class PagedStatePool:
             self._unlease(refs)
 
     def materialize(self, sequence):
-        """Dequantized history ``((k, v), ...)`` per layer, ``[1, Hkv, T, D]`` fp32
-        (state.py:392-409); None for an empty sequence."""
+        """Dequantized history ``((k, v), ..., (padding,))``: per layer ``[1, Hkv, T, D]``
+        fp32, then the padding leaf ``[1, 1, T, 1]`` bool, the structure the runner
+        appends (state.py:392-409); None for an empty sequence."""
         with self._lock:
             self._check(sequence)
             if not sequence.length:
@@ -430,14 +457,17 @@ class PagedStatePool:
                     x = x.permute(1, 0, 2, 3).reshape(x.shape[1], -1, x.shape[-1])
                     pair.append(x[None, :, : sequence.length])
                 layers.append(tuple(pair))
+            padding = self.cache.key_valid[blocks].reshape(-1)[: sequence.length]
+            layers.append((padding.bool()[None, None, :, None],))
             return tuple(layers)
 
     def storage_metrics(self):
         """Persistent page storage including scales (state.py:411-425): every page
-        in use holds 2 * num_layers quantized leaves."""
+        in use holds 2 * num_layers quantized leaves and the bool padding leaf."""
         with self._lock:
             used = self.used_blocks
-            per_page = self.cache.block_code_bytes + self.cache.block_scale_bytes
+            per_page = (self.cache.block_code_bytes + self.cache.block_scale_bytes
+                        + self.cache.block_size)
             return {
                 "format": self.quantization.format,
                 "allocated_tensor_bytes": used * per_page,
@@ -447,8 +477,8 @@ class PagedStatePool:
 
     # ---- host swap ------------------------------------------------------------
     def export_blocks(self, sequence, *, stream=None):
-        """Device copies ``(codes, scales)`` of the sequence's pages packed in page
-        order (the gather half of host swap), enqueued on ``stream``; the caller
+        """Device copies ``(codes, scales, valid)`` of the sequence's pages packed in
+        page order (the gather half of host swap), enqueued on ``stream``; the caller
         holds a read lease until the copy has finished."""
         with self._lock:
             self._check(sequence)
@@ -461,15 +491,22 @@ class PagedStatePool:
 
         ``payloads``: one tuple per page of ``2 * num_layers`` ``QuantizedKV`` leaves
         ``(k_0, v_0, ...)`` of ``[1, Hkv, count, D]`` int8 codes and
-        ``[1, Hkv, count, 1]`` fp32 scales (what ``read_pages`` exposes and
-        ``PagedStateArchive`` keeps), or ``(codes, scales)`` already packed in the
+        ``[1, Hkv, count, 1]`` fp32 scales, optionally followed by the padding leaf
+        ``[1, 1, count, 1]`` (what ``read_pages`` exposes and ``PagedStateArchive``
+        keeps), or ``(codes, scales[, valid])`` already packed in the
         ``export_blocks`` layout on the host."""
         sequence = self.create(identity)
         if type(length) is not int or length < 1:
             raise StateError("Archived page count and token length differ")
         count = math.ceil(length / self.block_size)
         packed = self._pack(payloads, length) if not _is_packed(payloads) else payloads
-        codes, scales = packed
+        codes, scales = packed[0], packed[1]
+        valid = packed[2] if len(packed) == 3 else None
+        if valid is not None:
+            if tuple(valid.shape) != (codes.shape[0], self.block_size):
+                raise StateError("Archived padding layout differs from model pool")
+            if bool(valid.reshape(-1)[:length].bool().all()):
+                valid = None  # every committed key real: the arena needs no padding bytes
         if codes.shape[0] != count:
             raise StateError("Archived page count and token length differ")
         with self._lock:
@@ -481,7 +518,9 @@ class PagedStatePool:
             with torch.cuda.stream(stream):
                 dcodes = codes.to(self.cache.device, non_blocking=True)
                 dscales = scales.to(self.cache.device, non_blocking=True)
-            self.cache.scatter_blocks([ref.index for ref in refs], dcodes, dscales,
+                dvalid = (valid.to(torch.uint8).to(self.cache.device, non_blocking=True)
+                          if valid is not None else None)
+            self.cache.scatter_blocks([ref.index for ref in refs], dcodes, dscales, dvalid,
                                       stream=stream)
             done = torch.cuda.Event()
             done.record(stream)
@@ -507,8 +546,16 @@ class PagedStatePool:
             raise StateError("Archived page count and token length differ")
         codes = torch.zeros((count,) + tuple(c.codes.shape[1:]), dtype=torch.int8)
         scales = torch.ones((count,) + tuple(c.scales.shape[1:]), dtype=torch.float32)
+        valid = torch.ones((count, self.block_size), dtype=torch.uint8)
         for p, leaves in enumerate(payloads):
             tokens = min(self.block_size, length - p * self.block_size)
+            if len(leaves) == 2 * c.num_layers + 1:
+                pad = leaves[-1]
+                if isinstance(pad, QuantizedKV) or tuple(pad.shape) != (1, 1, tokens, 1) or \
+                        not ((pad == 0) | (pad == 1)).all():
+                    raise StateError("Archived padding leaf differs")
+                valid[p, :tokens] = pad[0, 0, :, 0].to(torch.uint8).cpu()
+                leaves = leaves[:-1]
             if len(leaves) != 2 * c.num_layers:
                 raise StateError("Archived leaf plan differs")
             for i, leaf in enumerate(leaves):
@@ -522,9 +569,9 @@ class PagedStatePool:
                 layer, kv = divmod(i, 2)
                 codes[p, layer, kv, :, :tokens] = leaf.values[0].cpu()
                 scales[p, layer, kv, :, :tokens] = leaf.scales[0, ..., 0].cpu()
-        return codes, scales
+        return codes, scales, valid
 
 
 def _is_packed(payloads):
-    return (isinstance(payloads, tuple) and len(payloads) == 2
+    return (isinstance(payloads, tuple) and len(payloads) in (2, 3)
             and all(isinstance(t, torch.Tensor) for t in payloads))

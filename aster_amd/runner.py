@@ -17,15 +17,17 @@ that row loop:
     rolls all of them back if the step raised.
 
 Row lengths need not match (the reference groups equal ``start``/``count`` per
-call, :118-123); padding masks are not implemented by the kernels and raise
-``UnsupportedAttentionBackend`` rather than being ignored.
+call, :118-123). Chunk padding (``forward_batch(padding_masks=...)``, :137-143) is
+written once per step into the reserved slots' key bytes: a padding token is
+appended like any other but attended by no query, in this step or later, as the
+reference's padding leaf does (:181, :190, :228).
 """
 
 from __future__ import annotations
 
 import torch
 
-from .attention_backend import BACKEND, KernelWork, UnsupportedAttentionBackend
+from .attention_backend import BACKEND, KernelWork
 from .paged_pool import StateError
 
 
@@ -48,6 +50,30 @@ def unpack_rows(y, counts, width=None):
     return out
 
 
+def _padding_vector(padding, counts):
+    """Chunk padding as a host bool vector packed like the step's tokens: one 0/1
+    sequence per row (``len == counts[b]``) or a batch-by-token matrix whose row ``b``
+    starts with the row's ``counts[b]`` tokens (paged_attention.py:137-143)."""
+    rows = []
+    if isinstance(padding, (list, tuple)):
+        if len(padding) != len(counts):
+            raise ValueError("Chunk padding must be a binary batch-by-token matrix")
+        for row, n in zip(padding, counts):
+            row = torch.as_tensor(row).cpu()
+            if row.ndim != 1 or row.shape[0] != n:
+                raise ValueError("Chunk padding must be a binary batch-by-token matrix")
+            rows.append(row)
+    else:
+        matrix = torch.as_tensor(padding).cpu()
+        if matrix.ndim != 2 or matrix.shape[0] != len(counts) or matrix.shape[1] < max(counts):
+            raise ValueError("Chunk padding must be a binary batch-by-token matrix")
+        rows = [matrix[b, :n] for b, n in enumerate(counts)]
+    packed = torch.cat(rows)
+    if not ((packed == 0) | (packed == 1)).all():
+        raise ValueError("Chunk padding must be a binary batch-by-token matrix")
+    return packed.bool()
+
+
 class PagedAttentionStep:
     """One step of ``counts[b]`` new tokens for each sequence ``b`` of a batch."""
 
@@ -60,9 +86,7 @@ class PagedAttentionStep:
             raise ValueError("Every row needs at least one new token")
         if len({s.identity for s in sequences}) != 1:
             raise StateError("A projection batch cannot cross cache security domains")
-        if padding is not None and not bool(torch.as_tensor(padding).bool().all()):
-            raise UnsupportedAttentionBackend(
-                "hip_int8_paged kernels do not implement chunk padding masks")
+        valid = None if padding is None else _padding_vector(padding, counts)
         self.pool, self.counts = pool, list(counts)
         self.work = work if work is not None else KernelWork()
         self.partition_tokens = partition_tokens
@@ -88,6 +112,14 @@ class PagedAttentionStep:
         self.max_context_len = max(r.length for r in self.reservations)
         slots = [s for r in self.reservations for s in r.slots]
         self.slot_mapping = torch.tensor(slots, dtype=torch.int64).to(device, non_blocking=True)
+        try:
+            cache.write_key_valid(self.slot_mapping,
+                                  None if valid is None else valid.to(device, non_blocking=True))
+        except BaseException:
+            self._tables.__exit__(None, None, None)
+            for r in self.reservations:
+                pool.abort(r)
+            raise
         self._open = True
 
     def attend(self, layer, query, key, value, *, scale=None, window=None, out=None):

@@ -54,6 +54,11 @@ enum astr_dtype { ASTR_F32 = 0, ASTR_F16 = 1, ASTR_BF16 = 2 };
  * (same for v_*). This is the reference's per-page [1,Hkv,bs,D] codes and
  * [1,Hkv,bs,1] scales (kv_quantization.py:97-110, state.py:319-327) stacked
  * into one arena indexed by PageRef.index.
+ * Key padding: key_valid + b*block_size + s is 0 when that slot holds a padding
+ * token, which no query attends (the page's padding leaf [1,1,bs,1] of
+ * state.py:319-327, applied as a key mask by online_attention.py:185-186), and
+ * nonzero for a real token. One byte per slot, shared by every layer and head;
+ * NULL means every key is real (the attention kernels then skip the mask).
  */
 typedef struct astr_paged_kv {
   int8_t* k_codes;
@@ -68,6 +73,7 @@ typedef struct astr_paged_kv {
   int32_t block_size;   /* must be 16 */
   int32_t num_kv_heads;
   int32_t head_dim;     /* 64, 128 or 256 for attention; any 1..512 for append */
+  uint8_t* key_valid;   /* [num_blocks * block_size] or NULL; 16-byte aligned */
 } astr_paged_kv;
 
 /*
@@ -93,6 +99,18 @@ int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void* key, cons
                                int64_t key_head_stride, int64_t value_token_stride,
                                int64_t value_head_stride, const int64_t* slot_mapping,
                                int32_t* err_flag, void* stream);
+
+/*
+ * Write the key-padding bytes of new tokens: key_valid[slot_mapping[i]] =
+ * token_valid[i] != 0 (1 for every token when token_valid is NULL); slots < 0
+ * are skipped, slots outside the arena raise ASTR_FLAG_BAD_INDEX. The padding
+ * leaf of PagedStatePool._append_leaves (state.py:292, 339-344) as the runner
+ * appends it (paged_attention.py:228-229), written once per step for all
+ * layers. cache->key_valid must be set.
+ */
+int astr_kv_write_key_valid(const astr_paged_kv* cache, const int64_t* slot_mapping,
+                            const uint8_t* token_valid, int64_t num_tokens, int32_t* err_flag,
+                            void* stream);
 
 /*
  * Ragged paged attention over the INT8 arena, one query token per sequence

@@ -18,6 +18,8 @@ class FakeArena:
         self.codes = torch.zeros((num_blocks, num_layers, 2, num_kv_heads, block_size, head_dim),
                                  dtype=torch.int8)
         self.scales = torch.ones((num_blocks, num_layers, 2, num_kv_heads, block_size))
+        self.key_valid = torch.ones((num_blocks, block_size), dtype=torch.uint8)
+        self.has_padding = False
         self.flags = 0
         self.copies = []
         self.appends = 0
@@ -43,6 +45,17 @@ class FakeArena:
                 self.codes[b, layer, kv, :, o] = torch.from_numpy(q.values[0, :, t])
                 self.scales[b, layer, kv, :, o] = torch.from_numpy(q.scales[0, :, t, 0])
 
+    def write_key_valid(self, slots, valid=None):
+        if valid is None and not self.has_padding:
+            return
+        self.has_padding = self.has_padding or valid is not None
+        for t, slot in enumerate(slots.tolist()):
+            b, o = divmod(slot, self.block_size)
+            self.key_valid[b, o] = 1 if valid is None else int(bool(valid[t]))
+
+    def padding_leaf(self, block):
+        return self.key_valid[block].view(torch.bool)[None, None, :, None]
+
     def raise_errors(self):
         flags, self.flags = self.flags, 0
         if flags:
@@ -53,6 +66,7 @@ class FakeArena:
         for s, d in zip(src, dst):
             self.codes[d] = self.codes[s]
             self.scales[d] = self.scales[s]
+            self.key_valid[d] = self.key_valid[s]
 
     def page(self, block, layer):
         return tuple(QuantizedKV(self.codes[block, layer, kv][None],

@@ -30,8 +30,37 @@ def oracle_decode(workload_or_tables, cache, query, layer=0, context_lens=None, 
     else:
         tables, lens = workload_or_tables, context_lens
     q = query.float().cpu().numpy()
+    padding = cache.key_valid.cpu().numpy().astype(bool) if cache.has_padding else None
     return ref.paged_attention(q, *arena_numpy(cache, layer), tables, lens, block_size=16,
-                               scale=scale, window=window, query_lens=query_lens, causal=causal)
+                               scale=scale, window=window, query_lens=query_lens, causal=causal,
+                               padding=padding)
+
+
+def mark_padding(cache, tables, lens, fraction, seed, *, whole_rows=(), whole_blocks=0):
+    """Mark a seeded ``fraction`` of the committed keys of every row as padding keys
+    through ``write_key_valid`` (every row's slots in one launch), plus every key of
+    the rows in ``whole_rows`` and ``whole_blocks`` whole pages; returns the host
+    ``valid`` array [num_blocks, 16]."""
+    rng = np.random.default_rng(seed)
+    slots, valid = [], []
+    picked = set()
+    for b, ctx in enumerate(np.asarray(lens).tolist()):
+        pages = [int(x) for x in np.asarray(tables[b])[: (ctx + 15) // 16]]
+        for i in range(ctx):
+            slots.append(pages[i // 16] * 16 + i % 16)
+            valid.append(b not in whole_rows and rng.random() >= fraction)
+        if len(picked) < whole_blocks and len(pages) > 2:
+            picked.add(pages[1])
+    valid = np.array(valid)
+    for j, slot in enumerate(slots):
+        if slot // 16 in picked:
+            valid[j] = False
+    dev = cache.device
+    cache.write_key_valid(torch.tensor(slots, dtype=torch.int64, device=dev),
+                          torch.tensor(valid, dtype=torch.bool, device=dev))
+    torch.cuda.synchronize(dev)
+    cache.raise_errors()
+    return cache.key_valid.cpu().numpy()
 
 
 def assert_attention_close(actual, expected, atol=ATOL, rtol=RTOL):

@@ -98,7 +98,23 @@ def test_attention_argument_errors_need_no_device():
     assert _attn(_desc(), max_ctx=1024, bt_stride=64, part=64) == _native.ASTR_EINVAL  # no workspace
     assert "workspace" in _native.last_error()
     assert _attn(_desc(), num_seqs=0) == 0  # empty batch: nothing to launch
+    assert _attn(_desc(key_valid=20)) == _native.ASTR_EINVAL  # padding bytes misaligned
+    assert "key_valid" in _native.last_error()
     del lib
+
+
+def test_key_valid_argument_errors_need_no_device():
+    f = _native.lib().astr_kv_write_key_valid
+    flag = ctypes.c_int32(0)
+    fp = ctypes.addressof(flag)
+    assert f(None, 16, 16, 1, fp, None) == _native.ASTR_EINVAL
+    assert f(ctypes.byref(_desc()), 16, 16, 1, fp, None) == _native.ASTR_EINVAL  # no key_valid
+    assert "key_valid" in _native.last_error()
+    d = _desc(key_valid=16)
+    assert f(ctypes.byref(d), 16, 16, 1, None, None) == _native.ASTR_EINVAL
+    assert f(ctypes.byref(d), 16, 16, -1, fp, None) == _native.ASTR_EINVAL
+    assert f(ctypes.byref(d), None, 16, 1, fp, None) == _native.ASTR_EINVAL
+    assert f(ctypes.byref(d), 16, 16, 0, fp, None) == 0  # no tokens: nothing to launch
 
 
 def test_append_argument_errors_need_no_device():

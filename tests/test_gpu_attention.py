@@ -12,7 +12,7 @@ import torch
 
 from aster_amd import KernelWork, PagedKVCache, UnsupportedAttentionBackend
 from aster_amd import workloads as wl
-from tests.gpu_util import arena_numpy, assert_attention_close, oracle_decode
+from tests.gpu_util import arena_numpy, assert_attention_close, mark_padding, oracle_decode
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -89,6 +89,28 @@ def test_sliding_window(device, window, part):
     out = cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
                                 window=window, partition_tokens=part, check=True)
     assert_attention_close(out, oracle_decode(w, cache, q, window=window))
+
+
+@pytest.mark.parametrize("dim,hq,hkv", [(128, 32, 8), (64, 8, 2), (256, 8, 2)])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("part", [0, 128])
+def test_key_padding(device, dim, hq, hkv, qdtype, part):
+    """Padding keys (the pages' padding leaf, online_attention.py:185-186) are never
+    attended: a seeded 25 % of keys, two whole pages and one whole row (whose output
+    is zero, online_attention.py:37), on every decode kernel (stream-K, fixed
+    partitions, and the fp32 VALU kernel), with and without a sliding window."""
+    lens = np.array([300, 17, 600, 1, 64, 250, 129, 40], np.int32)
+    rng = np.random.default_rng(dim + hq)
+    tables, pool = wl._tables_from_lengths(lens, rng, spare_blocks=3)
+    w = wl.DecodeWorkload("pad", hq, hkv, dim, lens, tables, pool, qdtype, 5, dim ** -0.5)
+    cache, t, l = _build(w, device)
+    mark_padding(cache, tables, lens, 0.25, seed=dim, whole_rows=(5,), whole_blocks=2)
+    q = wl.queries(w, device)
+    for window in (None, 90):
+        out = cache.paged_attention(0, q, t, l, max_context_len=600, partition_tokens=part,
+                                    window=window, check=True)
+        assert (out[5] == 0).all()
+        assert_attention_close(out, oracle_decode(w, cache, q, window=window))
 
 
 def test_empty_rows_are_zero_and_ctx_one_returns_value(device):

@@ -72,14 +72,20 @@ def test_copy_blocks_gather_scatter_and_bad_index(device):
     cache.codes.copy_(torch.randint(-127, 128, cache.codes.shape, generator=g, device=device,
                                     dtype=torch.int8))
     cache.scales.copy_(torch.rand(cache.scales.shape, generator=g, device=device))
-    before_c, before_s = cache.codes.clone(), cache.scales.clone()
-    codes, scales = cache.gather_blocks([7, 2, 5])
+    cache.key_valid.copy_(torch.randint(0, 2, cache.key_valid.shape, generator=g, device=device,
+                                        dtype=torch.uint8))
+    before_c, before_s, before_v = cache.codes.clone(), cache.scales.clone(), cache.key_valid.clone()
+    codes, scales, valid = cache.gather_blocks([7, 2, 5])
     assert torch.equal(codes, before_c[[7, 2, 5]]) and torch.equal(scales, before_s[[7, 2, 5]])
-    cache.scatter_blocks([0, 8, 1], codes, scales)
+    assert torch.equal(valid, before_v[[7, 2, 5]])
+    cache.scatter_blocks([0, 8, 1], codes, scales, valid)
+    assert cache.has_padding
     assert torch.equal(cache.codes[[0, 8, 1]], before_c[[7, 2, 5]])
     assert torch.equal(cache.scales[[0, 8, 1]], before_s[[7, 2, 5]])
+    assert torch.equal(cache.key_valid[[0, 8, 1]], before_v[[7, 2, 5]])
     cache.copy_blocks([3], [4])
     assert torch.equal(cache.codes[4], before_c[3]) and torch.equal(cache.scales[4], before_s[3])
+    assert torch.equal(cache.key_valid[4], before_v[3])
     untouched = [2, 3, 5, 6, 7]
     assert torch.equal(cache.codes[untouched], before_c[untouched])
     # an index outside the arena is flagged and that block is skipped
@@ -128,27 +134,38 @@ def test_attention_over_pool_block_tables_matches_oracle(device):
 
 
 @pytest.mark.parametrize("pin", [False, True])
-def test_archive_roundtrip_is_bit_exact(device, pin):
+@pytest.mark.parametrize("padded", [False, True])
+def test_archive_roundtrip_is_bit_exact(device, pin, padded):
     pool = make_pool(device)
     seq = pool.create("tenant-policy")
-    pool.append_delta(seq, layers(37, 30, device))
+    suffix = layers(37, 30, device)
+    pad = torch.arange(37) % 5 != 3
+    if padded:
+        suffix = suffix + [(pad[None, None, :, None],)]
+    pool.append_delta(seq, suffix)
 
     def codes(sequence):
         with pool.read_pages(sequence) as pages:
-            return [[(x.values.clone(), x.scales.clone()) for x in page.payload] for page in pages]
+            return [[(x.values.clone(), x.scales.clone()) for x in page.payload[:-1]]
+                    + [page.payload[-1].clone()] for page in pages]
 
     before = codes(seq)
     archive = PagedStateArchive(pool, pin_memory=pin)
     handle = archive.put(seq)
     pool.release(seq)
-    assert pool.used_blocks == 0 and archive.stored_bytes == 37 * L * 2 * HKV * (D + 4)
+    assert pool.used_blocks == 0 and archive.stored_bytes == 37 * (L * 2 * HKV * (D + 4) + 1)
     pages = archive.pages(handle, identity="tenant-policy")
     assert len(pages) == 3 and pages[-1][0].values.shape == (1, HKV, 5, D)
+    assert len(pages[0]) == 2 * L + 1 and pages[-1][-1].shape == (1, 1, 5, 1)
     restored = archive.restore(handle, identity="tenant-policy")
     assert restored.length == 37
-    for page_a, page_b in zip(before, codes(restored)):
-        for (ca, sa), (cb, sb) in zip(page_a, page_b):
+    after = codes(restored)
+    for page_a, page_b in zip(before, after):
+        for (ca, sa), (cb, sb) in zip(page_a[:-1], page_b[:-1]):
             assert torch.equal(ca, cb) and torch.equal(sa, sb)
+        assert torch.equal(page_a[-1], page_b[-1])
+    got_pad = torch.cat([p[-1][0, 0, :, 0].cpu() for p in after])
+    assert torch.equal(got_pad, pad if padded else torch.ones(37, dtype=torch.bool))
     archive.release(handle, identity="tenant-policy")
     pool.release(restored)
     assert archive.metrics() == dict(host_bytes=0, snapshots=0, offloaded_tokens=37,

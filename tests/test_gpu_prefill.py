@@ -10,7 +10,7 @@ import torch
 
 from aster_amd import KernelWork, PagedKVCache
 from aster_amd import workloads as wl
-from tests.gpu_util import assert_attention_close, oracle_decode
+from tests.gpu_util import assert_attention_close, mark_padding, oracle_decode
 
 pytestmark = pytest.mark.gpu
 
@@ -68,6 +68,20 @@ def test_window_and_causality(device, window, causal):
     q = wl.queries(w, device)
     out = _run(cache, w, q, tables, lens, qsl, window=window, causal=causal)
     assert_attention_close(out, oracle_decode(w, cache, q, window=window, causal=causal))
+
+
+@pytest.mark.parametrize("dim,hq,hkv", [(128, 32, 8), (64, 16, 2), (256, 8, 2)])
+@pytest.mark.parametrize("window", [None, 40])
+def test_key_padding_in_chunks(device, dim, hq, hkv, window):
+    """Padding keys, in the history and in the step's own chunk (the runner appends
+    the chunk with its padding leaf before attention, paged_attention.py:190 and
+    :228-229), are seen by no query of the prefill or decode rows."""
+    w = _mixed(Q_LENS, CTX, hq=hq, hkv=hkv, dim=dim, seed=dim + 3)
+    cache, tables, lens, qsl = _build(w, device)
+    mark_padding(cache, w.block_tables, w.context_lens, 0.2, seed=dim, whole_blocks=2)
+    q = wl.queries(w, device)
+    out = _run(cache, w, q, tables, lens, qsl, window=window)
+    assert_attention_close(out, oracle_decode(w, cache, q, window=window))
 
 
 def test_non_causal_without_window(device):

@@ -27,29 +27,37 @@ class OracleRows:
     def __init__(self, layers):
         self.layers = layers
         self.hist = {}  # (seq key, layer) -> (k codes/scales, v codes/scales) lists
+        self.pad = {}   # seq key -> list of per-chunk bool padding leaves (True = real)
 
     def fork(self, src, dst):
         for layer in range(self.layers):
             self.hist[(dst, layer)] = [list(x) for x in self.hist.get((src, layer), ([], []))]
+        self.pad[dst] = list(self.pad.get(src, []))
 
-    def attend(self, layer, rows, q, k, v, scale):
-        """rows: list of (seq key, start, count) in packed order; q/k/v packed host arrays."""
+    def attend(self, layer, rows, q, k, v, scale, padding=None):
+        """rows: list of (seq key, start, count) in packed order; q/k/v packed host arrays;
+        padding: per row bool vector (True = real token) or None."""
         outs, cursor = [], 0
-        for key, start, count in rows:
+        for r, (key, start, count) in enumerate(rows):
+            pad = np.ones(count, bool) if padding is None else np.asarray(padding[r], bool)
             qs = q[cursor: cursor + count].transpose(1, 0, 2)[None]
             ks = k[cursor: cursor + count].transpose(1, 0, 2)[None]
             vs = v[cursor: cursor + count].transpose(1, 0, 2)[None]
             cursor += count
             hk, hv = self.hist.setdefault((key, layer), ([], []))
             qk, qv = ref.quantize_kv_int8(ks), ref.quantize_kv_int8(vs)
+            pads = self.pad.setdefault(key, [])
             blocks = []
             if hk:
-                blocks.append(ref.AttentionBlock(_cat(hk), _cat(hv), 0, None))
-            blocks.append(ref.AttentionBlock(qk, qv, start, None))
+                blocks.append(ref.AttentionBlock(_cat(hk), _cat(hv), 0,
+                                                 np.concatenate(pads[:len(hk)])[None]))
+            blocks.append(ref.AttentionBlock(qk, qv, start, pad[None]))
             pos = np.arange(start, start + count)[None]
             out = ref.online_attention(qs, blocks, query_positions=pos, causal=True, scale=scale)
             outs.append(out[0].transpose(1, 0, 2))
             hk.append(qk), hv.append(qv)
+            if layer == 0:
+                pads.append(pad)
         return np.concatenate(outs, 0)
 
 
@@ -58,17 +66,17 @@ def _cat(parts):
                            np.concatenate([p.scales for p in parts], 2))
 
 
-def run_step(model, pool, oracle, seqs, keys, chunks, work):
+def run_step(model, pool, oracle, seqs, keys, chunks, work, padding=None):
     counts = [len(c) for c in chunks]
     ids = torch.tensor([t for c in chunks for t in c], device=pool.cache.device)
-    with PagedAttentionStep(pool, seqs, counts, work=work) as step:
+    with PagedAttentionStep(pool, seqs, counts, work=work, padding=padding) as step:
         pos = torch.cat([torch.arange(p, p + n) for p, n in zip(step.positions, counts)])
         rows = list(zip(keys, step.positions, counts))
 
         def attend(layer, q, k, v):
             out = step.attend(layer, q, k, v, scale=model.scale)
             want = oracle.attend(layer, rows, q.cpu().numpy(), k.cpu().numpy(),
-                                 v.cpu().numpy(), model.scale)
+                                 v.cpu().numpy(), model.scale, padding)
             assert_attention_close(out, want)
             return out
 
@@ -78,10 +86,12 @@ def run_step(model, pool, oracle, seqs, keys, chunks, work):
 
 def check_pool_matches_oracle(pool, oracle, seq, key):
     state = pool.materialize(seq)
-    for layer, (k, v) in enumerate(state):
+    for layer, (k, v) in enumerate(state[:oracle.layers]):
         hk, hv = oracle.hist[(key, layer)]
         np.testing.assert_array_equal(k.cpu().numpy(), _cat(hk).dequantize())
         np.testing.assert_array_equal(v.cpu().numpy(), _cat(hv).dequantize())
+    np.testing.assert_array_equal(state[-1][0][0, 0, :, 0].cpu().numpy(),
+                                  np.concatenate(oracle.pad[key]))
 
 
 def test_runner_steps_match_reference_row_loop(device):
@@ -114,7 +124,19 @@ def test_runner_steps_match_reference_row_loop(device):
     assert [seqs[0].length, seqs[1].length, fork.length] == [22, 13, 23]
     for s, k in zip(seqs + [fork], keys + ["d"]):
         check_pool_matches_oracle(pool, oracle, s, k)
-    # 4. a step that fails midway commits nothing
+    # 4. chunks with padding tokens (forward_batch padding_masks, paged_attention.py:137-143):
+    #    appended, attended by no query, now or in the decode step after
+    pads = [rng.random(n) > 0.3 for n in (6, 1, 9)]
+    pads[2][:3] = False
+    run_step(model, pool, oracle, seqs, keys, [tokens(6), tokens(1), tokens(9)], work,
+             padding=[torch.tensor(p) for p in pads])
+    assert pool.cache.has_padding
+    run_step(model, pool, oracle, seqs, keys, [tokens(1)] * 3, work)
+    for s, k in zip(seqs + [fork], keys + ["d"]):
+        check_pool_matches_oracle(pool, oracle, s, k)
+    with pytest.raises(ValueError, match="binary"):
+        PagedAttentionStep(pool, seqs, [2, 2, 2], padding=[[1, 2], [1, 1], [1, 1]])
+    # 5. a step that fails midway commits nothing
     used, lengths = pool.used_blocks, [s.length for s in seqs]
     with pytest.raises(RuntimeError, match="layer failed"):
         with PagedAttentionStep(pool, seqs, [16, 16, 16]) as step:

@@ -72,7 +72,7 @@ def test_append_materialize_and_slot_placement():
     assert pool.used_blocks == 3
     assert pool.storage_metrics() == {
         "format": "int8", "physical_pages": 3, "quantized_leaves": 3 * 2 * L,
-        "allocated_tensor_bytes": 3 * (L * 2 * HKV * BS * D + L * 2 * HKV * BS * 4)}
+        "allocated_tensor_bytes": 3 * (L * 2 * HKV * BS * D + L * 2 * HKV * BS * 4 + BS)}
 
 
 def test_fork_then_append_copies_the_shared_tail_page():
@@ -201,3 +201,41 @@ def test_capacity_matches_pages_needed_for_many_sequences():
         pool.release(s)
     assert pool.used_blocks == 0 and pool.storage_metrics()["allocated_tensor_bytes"] == 0
     assert math.ceil(33 / BS) == 3
+
+
+def test_padding_leaf_is_stored_exposed_and_copied_on_write():
+    """The runner's suffix carries a padding leaf [1, 1, T, 1] (paged_attention.py:228):
+    it lands in the slots' key bytes, comes back as the last of 2L+1 page leaves
+    (paged_attention.py:171-182) and in materialize, follows a copied tail page, and a
+    later suffix without a leaf marks its tokens real."""
+    pool = make_pool()
+    seq = pool.create("p")
+    pad = torch.tensor([1, 0, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, 1, 1], dtype=torch.bool)
+    pool.append_delta(seq, layers(20, 1) + [(pad[None, None, :, None],)])
+    assert pool.cache.has_padding
+    with pool.read_pages(seq) as views:
+        assert [len(v.payload) for v in views] == [2 * L + 1] * 2
+        got = torch.cat([v.payload[-1][0, 0, :, 0] for v in views])
+        assert views[1].payload[-1].shape == (1, 1, 4, 1) and views[1].payload[-1].dtype == torch.bool
+    assert torch.equal(got, pad)
+    state = pool.materialize(seq)
+    assert len(state) == L + 1 and torch.equal(state[-1][0][0, 0, :, 0], pad)
+    # a fork shares the tail page; appending to it copies the page with its padding bytes
+    child = pool.fork(seq)
+    pool.append_delta(child, layers(3, 2))  # no leaf: real tokens
+    assert child.pages[-1].index != seq.pages[-1].index
+    with pool.read_pages(child) as views:
+        got_child = torch.cat([v.payload[-1][0, 0, :, 0] for v in views])
+    assert torch.equal(got_child, torch.cat([pad, torch.ones(3, dtype=torch.bool)]))
+    with pool.read_pages(seq) as views:
+        assert torch.equal(torch.cat([v.payload[-1][0, 0, :, 0] for v in views]), pad)
+    # the full-state append slices the leaf like every other leaf
+    more = torch.tensor([0, 1, 1], dtype=torch.bool)
+    whole = [(torch.cat([k, k2], 2), torch.cat([v, v2], 2))
+             for (k, v), (k2, v2) in zip(pool.materialize(seq)[:L], layers(3, 3))]
+    pool.append(seq, whole + [(torch.cat([pad, more])[None, None, :, None],)])
+    assert torch.equal(pool.materialize(seq)[-1][0][0, 0, :, 0], torch.cat([pad, more]))
+    with pytest.raises(StateError):
+        pool.append_delta(seq, layers(2, 4) + [(torch.tensor([1, 2])[None, None, :, None],)])
+    with pytest.raises(StateError):
+        pool.append_delta(seq, layers(2, 4) + [(torch.ones(1, 1, 3, 1, dtype=torch.bool),)])
