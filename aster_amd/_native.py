@@ -16,6 +16,7 @@ LIB_NAME = "libaster_kv.so"
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
+ASTR_KV_INT8, ASTR_KV_FP8_E4M3FN, ASTR_KV_FP8_E5M2 = 0, 1, 2  # astr_kv_format
 ASTR_EINVAL = -1
 ASTR_EUNSUPPORTED = -2
 
@@ -55,6 +56,7 @@ class PagedKVDesc(ctypes.Structure):
         ("num_kv_heads", ctypes.c_int32),
         ("head_dim", ctypes.c_int32),
         ("key_valid", ctypes.c_void_p),
+        ("code_format", ctypes.c_int32),
     ]
 
 

@@ -21,6 +21,22 @@ OUT_DIR = os.path.join(HERE, "_lib")
 OUT = os.path.join(OUT_DIR, "libaster_kv.so")
 SOURCES = ("errors.hip", "kv_quantize.hip", "paged_attention.hip", "decode_partition.hip",
            "decode_streamk.hip", "prefill.hip", "kv_copy.hip")
+# attention kernels built once per KV code format (int8, FP8 E4M3FN, FP8 E5M2):
+# -DASTR_KF=k selects the format of that object's instantiations
+PER_FORMAT = ("decode_partition.hip", "decode_streamk.hip", "prefill.hip")
+FORMATS = (0, 1, 2)
+
+
+def units():
+    """(source, object stem, extra flags) of every translation unit."""
+    out = []
+    for s in SOURCES:
+        stem = os.path.splitext(s)[0]
+        if s in PER_FORMAT:
+            out += [(s, f"{stem}_kf{k}", [f"-DASTR_KF={k}"]) for k in FORMATS]
+        else:
+            out.append((s, stem, []))
+    return out
 ARCH = "gfx950"
 
 FLAGS = [
@@ -78,9 +94,10 @@ def build(verbose=False, jobs=None):
     """Compile every translation unit (in parallel) and link the shared library."""
     obj_dir = os.path.join(OUT_DIR, "obj")
     os.makedirs(obj_dir, exist_ok=True)
-    objs = [os.path.join(obj_dir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
-    compiles = [[hipcc(), *FLAGS, RESOURCE_REMARKS, "-I", os.path.join(ROOT, "include"), "-c",
-                 os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+    plan = units()
+    objs = [os.path.join(obj_dir, stem + ".o") for _, stem, _ in plan]
+    compiles = [[hipcc(), *FLAGS, *extra, RESOURCE_REMARKS, "-I", os.path.join(ROOT, "include"),
+                 "-c", os.path.join(CSRC, s), "-o", o] for (s, _, extra), o in zip(plan, objs)]
     jobs = jobs or min(len(compiles), os.cpu_count() or 1, 8)
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
         for f in [pool.submit(_run, c, verbose) for c in compiles]:

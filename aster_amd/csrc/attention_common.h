@@ -201,32 +201,44 @@ __device__ __forceinline__ void stage_block(const AttnArgs& a, int phys, int kvh
     lds_dma_x1_s(a.cache.key_valid + (int64_t)phys * kBlockTokens, lane * 4, base + S::kF);
 }
 
-// ---- exact int8 -> f16 operands
+// ---- exact code -> f16 operands (int8; FP8 E4M3FN values times 2^-8; FP8 E5M2)
 
-// 4 int8 codes -> two f16 pairs holding exactly the codes: a byte permute builds
-// 0x64xx halves (1024 + u) with u = c + 128, then 1152 is subtracted.
+// 4 codes -> two f16 pairs. int8: a byte permute builds 0x64xx halves (1024 + u)
+// with u = c + 128, then 1152 is subtracted. FP8: each code byte goes to the high
+// byte of its half.
+template <int KF = kInt8>
 __device__ __forceinline__ void codes_to_f16(uint32_t w, half2_t& lo, half2_t& hi) {
-  const uint32_t u = w ^ 0x80808080u;                                      // bytes c + 128
-  const uint32_t l = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // 1024 + u0, 1024 + u1
-  const uint32_t h = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // 1024 + u2, 1024 + u3
-  const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-  lo = __builtin_bit_cast(half2_t, l) - bias;
-  hi = __builtin_bit_cast(half2_t, h) - bias;
+  if constexpr (KF == kInt8) {
+    const uint32_t u = w ^ 0x80808080u;                                      // bytes c + 128
+    const uint32_t l = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // 1024 + u0, 1024 + u1
+    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // 1024 + u2, 1024 + u3
+    const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(half2_t, l) - bias;
+    hi = __builtin_bit_cast(half2_t, h) - bias;
+  } else {
+    lo = __builtin_bit_cast(half2_t, fp8_hi_bytes_to_f16<KF>(__builtin_amdgcn_perm(0u, w, 0x010C000Cu)));
+    hi = __builtin_bit_cast(half2_t, fp8_hi_bytes_to_f16<KF>(__builtin_amdgcn_perm(0u, w, 0x030C020Cu)));
+  }
 }
 
 // Byte k of rows r0/r1 -> f16 pair (code[r0][k], code[r1][k]).
-template <int K>
+template <int K, int KF = kInt8>
 __device__ __forceinline__ half2_t column_pair(uint32_t r0, uint32_t r1) {
-  constexpr uint32_t sel = 0x0C000C00u | ((4u + K) << 16) | K;
-  const uint32_t p = __builtin_amdgcn_perm(r1, r0, sel) ^ 0x64806480u;  // 1152 + c
-  const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-  return __builtin_bit_cast(half2_t, p) - bias;
+  if constexpr (KF == kInt8) {
+    constexpr uint32_t sel = 0x0C000C00u | ((4u + K) << 16) | K;
+    const uint32_t p = __builtin_amdgcn_perm(r1, r0, sel) ^ 0x64806480u;  // 1152 + c
+    const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    return __builtin_bit_cast(half2_t, p) - bias;
+  } else {
+    constexpr uint32_t sel = ((4u + K) << 24) | 0x000C0000u | (K << 8) | 0x0Cu;
+    return __builtin_bit_cast(half2_t, fp8_hi_bytes_to_f16<KF>(__builtin_amdgcn_perm(r1, r0, sel)));
+  }
 }
 
-template <int K>
+template <int K, int KF = kInt8>
 __device__ __forceinline__ half4_t v_operand(const uint32_t (&v)[4]) {
-  const half2_t a01 = column_pair<K>(v[0], v[1]);
-  const half2_t a23 = column_pair<K>(v[2], v[3]);
+  const half2_t a01 = column_pair<K, KF>(v[0], v[1]);
+  const half2_t a23 = column_pair<K, KF>(v[2], v[3]);
   return half4_t{a01[0], a01[1], a23[0], a23[1]};
 }
 
@@ -326,7 +338,7 @@ __device__ __forceinline__ float query_operand(const QueryRaw<D>& q, bool gvalid
 // layout P^T needs, so the online softmax stays in registers. Tokens outside
 // [kv_begin, ctx) are masked; `tok_base` is the block's first token position.
 // Cross-lane (ballots, shuffles): call in uniform control flow.
-template <int D, int G>
+template <int D, int G, int KF = kInt8>
 __device__ __forceinline__ void mfma_block(const char* st, const half8_t (&qop)[D / 32], float cf,
                                            int tok_base, int kv_begin, int ctx, int r, int qg,
                                            float4_t (&acc)[D / 16], float& m, float& l,
@@ -343,14 +355,16 @@ __device__ __forceinline__ void mfma_block(const char* st, const half8_t (&qop)[
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
       half2_t p0, p1, p2, p3;
-      codes_to_f16(sub ? c.z : c.x, p0, p1);
-      codes_to_f16(sub ? c.w : c.y, p2, p3);
+      codes_to_f16<KF>(sub ? c.z : c.x, p0, p1);
+      codes_to_f16<KF>(sub ? c.w : c.y, p2, p3);
       const half8_t kop = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
       s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[2 * h + sub], s4, 0, 0, 0);
     }
   }
   const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
-  const float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg);
+  // V scales, times 2^8 for FP8 codes (E4M3FN operands carry 2^-8; E5M2 weights carry
+  // 2^8, as does the normaliser of this format)
+  const float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg) * v_weight_scale<KF>();
   uint32_t vw[4][VB / 4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -413,22 +427,44 @@ __device__ __forceinline__ void mfma_block(const char* st, const half8_t (&qop)[
     const uint32_t col[4] = {vw[0][n / 4], vw[1][n / 4], vw[2][n / 4], vw[3][n / 4]};
     half4_t vop;
     switch (n % 4) {
-      case 0: vop = v_operand<0>(col); break;
-      case 1: vop = v_operand<1>(col); break;
-      case 2: vop = v_operand<2>(col); break;
-      default: vop = v_operand<3>(col); break;
+      case 0: vop = v_operand<0, KF>(col); break;
+      case 1: vop = v_operand<1, KF>(col); break;
+      case 2: vop = v_operand<2, KF>(col); break;
+      default: vop = v_operand<3, KF>(col); break;
     }
     acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop, pop, acc[n], 0, 0, 0);
   }
 }
 
-// Kernel entry points (one per translation unit), dispatched on query dtype,
-// head dim and GQA group inside.
-int launch_partitioned(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
-int launch_streamk(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
+// Kernel entry points, one translation unit per code format KF (the source built
+// with -DASTR_KF=KF), dispatched on query dtype, head dim and GQA group inside.
+template <int KF> int launch_partitioned_kf(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
+template <int KF> int launch_streamk_kf(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
 // Rows with more than one query token (chunked prefill), one workgroup per
 // (kv head, sequence, tile of query tokens); needs q_start.
-int launch_prefill(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
+template <int KF> int launch_prefill_kf(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
+#define ASTR_DECLARE_LAUNCHERS(KF)                                                        \
+  template <> int launch_partitioned_kf<KF>(const AttnArgs&, int32_t, hipStream_t);       \
+  template <> int launch_streamk_kf<KF>(const AttnArgs&, int32_t, hipStream_t);           \
+  template <> int launch_prefill_kf<KF>(const AttnArgs&, int32_t, hipStream_t);
+ASTR_DECLARE_LAUNCHERS(kInt8)
+ASTR_DECLARE_LAUNCHERS(kE4M3)
+ASTR_DECLARE_LAUNCHERS(kE5M2)
+#undef ASTR_DECLARE_LAUNCHERS
+
+#define ASTR_BY_FORMAT(name)                                                     \
+  inline int name(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {      \
+    switch (a.cache.code_format) {                                               \
+      case kInt8: return name##_kf<kInt8>(a, q_dtype, stream);                   \
+      case kE4M3: return name##_kf<kE4M3>(a, q_dtype, stream);                   \
+      default: return name##_kf<kE5M2>(a, q_dtype, stream);                     \
+    }                                                                            \
+  }
+ASTR_BY_FORMAT(launch_partitioned)
+ASTR_BY_FORMAT(launch_streamk)
+ASTR_BY_FORMAT(launch_prefill)
+#undef ASTR_BY_FORMAT
+
 // Largest batch the stream-K kernel takes (its per-sequence table lives in LDS).
 int stream_k_max_seqs();
 

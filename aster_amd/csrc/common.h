@@ -117,9 +117,56 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// int8 byte `b` of a packed dword, as float (exact).
-__device__ __forceinline__ float i8_to_f(uint32_t w, int b) {
-  return (float)(int8_t)(w >> (8 * b));
+// Code formats (astr_kv_format) as template arguments.
+constexpr int kInt8 = ASTR_KV_INT8;
+constexpr int kE4M3 = ASTR_KV_FP8_E4M3FN;
+constexpr int kE5M2 = ASTR_KV_FP8_E5M2;
+
+// The f16 conversions below give a code's value times 2^-8 for E4M3FN (its bits
+// land one exponent step of 8 apart from f16's) and the value itself otherwise;
+// code_scale undoes that (exactly: a power of two) where the scales are applied.
+template <int KF>
+__device__ __forceinline__ constexpr float code_scale() {
+  return KF == kE4M3 ? 256.f : 1.f;
 }
+
+// PV weights and V operands are rounded to f16 after the V scale is applied, so the
+// scale enters times v_weight_scale: for E4M3FN that undoes its codes' 2^-8; E5M2's
+// scales (amax / 57344) lie below f16's normal range for |V| up to ~3.5, and 2^8
+// lifts them into it. Where the E5M2 codes enter at their own value (the decode
+// kernels) the softmax normaliser carries the same 2^8 (norm_scale), which cancels
+// in acc / l; the prefill kernel takes E5M2 codes times 2^-8 instead (exact in f16).
+template <int KF>
+__device__ __forceinline__ constexpr float v_weight_scale() {
+  return KF == kInt8 ? 1.f : 256.f;
+}
+template <int KF>
+__device__ __forceinline__ constexpr float norm_scale() {
+  return KF == kE5M2 ? 256.f : 1.f;
+}
+
+// FP8 codes placed in the high byte of each f16 half (low bytes zero) -> the f16
+// pair: E5M2 is the top byte of the f16 with the same value; E4M3FN keeps its
+// sign and shifts |code| right by one bit into f16's exponent/mantissa fields,
+// which is its value times 2^-8 (subnormals included).
+template <int KF>
+__device__ __forceinline__ uint32_t fp8_hi_bytes_to_f16(uint32_t h) {
+  if constexpr (KF == kE5M2) return h;
+  else return ((h >> 1) & 0x3f803f80u) | (h & 0x80008000u);
+}
+
+// Code byte `b` of a packed dword, as float (exact; times 2^-8 for E4M3FN).
+template <int KF>
+__device__ __forceinline__ float code_to_f(uint32_t w, int b) {
+  if constexpr (KF == kInt8) {
+    return (float)(int8_t)(w >> (8 * b));
+  } else {
+    const uint32_t h = fp8_hi_bytes_to_f16<KF>(((w >> (8 * b)) & 0xffu) << 8);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  }
+}
+
+// int8 byte `b` of a packed dword, as float (exact).
+__device__ __forceinline__ float i8_to_f(uint32_t w, int b) { return code_to_f<kInt8>(w, b); }
 
 }  // namespace astr

@@ -33,6 +33,11 @@ namespace astr {
 namespace attn {
 namespace {
 
+#ifndef ASTR_KF
+#define ASTR_KF 0
+#endif
+constexpr int KF = ASTR_KF;  // this translation unit's code format
+
 constexpr int kStages = 2;  // LDS stages per wave in the MFMA kernel
 
 struct RowPlan : RowSpan {
@@ -160,7 +165,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   if (NS == 3 && 2 < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, 2), kvh, lane, st2);
 
   half8_t qop[D / 32];
-  const float cf = query_operand<QT, D>(qraw, gvalid, a.qk_scale_log2, qop);
+  const float cf = query_operand<QT, D>(qraw, gvalid, a.qk_scale_log2, qop) * code_scale<KF>();
   float4_t acc[NPV];
 #pragma unroll
   for (int n = 0; n < NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -176,7 +181,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
     if (later >= 2) wait_vmcnt<2 * S::kLoads>();
     else if (later == 1) wait_vmcnt<S::kLoads>();
     else wait_vmcnt<0>();
-    mfma_block<D, G>(st, qop, cf, (first + kWaves * i) * kBlockTokens, row.kv_begin, row.ctx, r,
+    mfma_block<D, G, KF>(st, qop, cf, (first + kWaves * i) * kBlockTokens, row.kv_begin, row.ctx, r,
                      qg, acc, m, l, bad_score, a.cache.key_valid != nullptr);
     // refill this stage with block i + NS (its LDS reads above fed the MFMAs)
     if (i + NS < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, i + NS), kvh, lane, st);
@@ -196,6 +201,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   // ---- per-wave state to LDS (aliases the stages: wait for every wave first)
   l += shfl_xor(l, 16);
   l += shfl_xor(l, 32);
+  l *= norm_scale<KF>();  // the factor the PV weights carry
   __syncthreads();
   Shared<G, D>& sh = *reinterpret_cast<Shared<G, D>*>(lds0);
   if (gvalid) {
@@ -226,7 +232,10 @@ struct ValuTile {
 // Heads of a GQA group one VALU workgroup serves: a lane keeps 16 query values and
 // 16 accumulators per head in registers, so large groups at D >= 128 are served
 // in passes of 4 heads (each pass re-reads the group's K/V) instead of spilling.
-constexpr int valu_heads(int D, int group) { return (D >= 128 && group > 4) ? 4 : group; }
+// (FP8 codes convert with a few more live registers: passes of 4 heads from D = 64 up.)
+constexpr int valu_heads(int D, int group) {
+  return ((D >= 128 || KF != kInt8) && group > 4) ? 4 : group;
+}
 
 // GROUP: the GQA group size; G: the heads of it this workgroup serves
 // (blockIdx.y = kv head * GROUP/G + pass).
@@ -295,8 +304,8 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
     for (int j = 0; j < NL; ++j) {
       t.k[j] = *reinterpret_cast<const uint4*>(kp + j * kLoadBytes);
       t.v[j] = *reinterpret_cast<const uint4*>(vp + j * kLoadBytes);
-      t.ks[j] = ksp[j * TPL];
-      t.vs[j] = vsp[j * TPL];
+      t.ks[j] = ksp[j * TPL] * code_scale<KF>();  // 2^8 for E4M3FN (its codes convert to 2^-8 x)
+      t.vs[j] = vsp[j * TPL] * code_scale<KF>();
       t.kv[j] = masks ? kvbase[(int64_t)phys * kBlockTokens + j * TPL] : (uint8_t)1;
     }
   };
@@ -317,7 +326,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
       const uint32_t w[4] = {cur.k[j].x, cur.k[j].y, cur.k[j].z, cur.k[j].w};
       float kf[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) kf[e] = i8_to_f(w[e / 4], e % 4);
+      for (int e = 0; e < 16; ++e) kf[e] = code_to_f<KF>(w[e / 4], e % 4);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float dot = 0.f;
@@ -361,7 +370,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
       const uint32_t w[4] = {cur.v[j].x, cur.v[j].y, cur.v[j].z, cur.v[j].w};
       float vf[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) vf[e] = i8_to_f(w[e / 4], e % 4);
+      for (int e = 0; e < 16; ++e) vf[e] = code_to_f<KF>(w[e / 4], e % 4);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float p = __builtin_amdgcn_exp2f(s[j][g] - m[g]);
@@ -527,7 +536,8 @@ int dispatch_dim(const AttnArgs& a, int G, hipStream_t s) {
 
 }  // namespace
 
-int launch_partitioned(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
+template <>
+int launch_partitioned_kf<KF>(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
   const int G = a.num_q_heads / a.cache.num_kv_heads;
   switch (q_dtype) {
     case ASTR_F32: return dispatch_dim<float>(a, G, stream);

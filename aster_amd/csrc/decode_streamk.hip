@@ -18,6 +18,11 @@ namespace astr {
 namespace attn {
 namespace {
 
+#ifndef ASTR_KF
+#define ASTR_KF 0
+#endif
+constexpr int KF = ASTR_KF;  // this translation unit's code format
+
 // Waves per workgroup and LDS stages per wave: 4-wave workgroups with a 4-block ring
 // per wave (2 waves per SIMD) measured best among 4/8/16-wave workgroups with 2 or 4
 // stages (all within 3 %); D = 256 stages are twice as large, so 8 waves x 2 stages.
@@ -190,7 +195,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     else if (first == 2) wait_vmcnt<2 * S::kLoads>();
     else wait_vmcnt<S::kLoads>();
     lds_query<QT, D>(stage(NS - 1), gvalid ? r : 0, qg, qr);
-    cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop);
+    cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop) * code_scale<KF>();
     if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (their values are consumed)
   }
 
@@ -211,7 +216,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     const int64_t pfb = s_cu[pseq];  // first block of the row in the per-head order
     if (i > 0) {  // a new row starts inside this wave's range
       load_query<QT, D, G>(a, s_tok[pseq], pkvh, r, qg, qr);
-      cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop);
+      cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop) * code_scale<KF>();
     }
 #pragma unroll
     for (int k = 0; k < NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -222,7 +227,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     const int blk0 = psp.first_blk + (int)(b0 + i - pfb);
     for (; i < iend; ++i) {
       wait_block(i);
-      mfma_block<D, G>(stage(i), qop, cf, (blk0 + i - pstart) * kBlockTokens, psp.kv_begin,
+      mfma_block<D, G, KF>(stage(i), qop, cf, (blk0 + i - pstart) * kBlockTokens, psp.kv_begin,
                        psp.ctx, r, qg, acc, m, l, bad_score, a.cache.key_valid != nullptr);
       if (i + NS < nblk) issue(i + NS);
     }
@@ -230,6 +235,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     // partial in slot 0 (the piece starts the wave's range) or 1 (it ends it)
     float lt = l + shfl_xor(l, 16);
     lt += shfl_xor(lt, 32);
+    lt *= norm_scale<KF>();  // the factor the PV weights carry
     const int64_t pfe = pfb + (s_cu[pseq + 1] - s_cu[pseq]) - 1;
     if (b0 + pstart == pfb && b0 + iend - 1 == pfe) {
       if (gvalid) {
@@ -425,7 +431,8 @@ int dispatch_dim(const AttnArgs& a, int G, hipStream_t s) {
 
 }  // namespace
 
-int launch_streamk(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
+template <>
+int launch_streamk_kf<KF>(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
   if (a.min_waves > a.total_waves)
     return fail(ASTR_EINVAL, "stream-K workspace too small for this launch");
   const int G = a.num_q_heads / a.cache.num_kv_heads;
@@ -434,7 +441,9 @@ int launch_streamk(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
   return fail(ASTR_EUNSUPPORTED, "stream-K decode takes bf16/fp16 queries");
 }
 
+#if ASTR_KF == 0
 int stream_k_max_seqs() { return kMaxSeqsSK; }
+#endif
 
 }  // namespace attn
 }  // namespace astr

@@ -1,11 +1,14 @@
-// Fused quantize-and-append of new K/V token rows into the paged INT8 arena.
+// Fused quantize-and-append of new K/V token rows into the paged arena (INT8, FP8
+// E4M3FN or FP8 E5M2 codes).
 //
 // Arithmetic follows quantize_kv (src/aster/optimization/kv_quantization.py:82-94)
 // bit for bit: fp32 source, amax over the row, scale = amax==0 ? 1 :
-// max(amax/127, FLT_MIN) with an IEEE-correct division, codes =
-// rint(clamp(x/scale, -127, 127)) again with IEEE division (never x*(1/scale)),
-// round-half-to-even via v_rndne. The library is built with
-// -fhip-fp32-correctly-rounded-divide-sqrt and without denormal flushing.
+// max(amax/M, FLT_MIN) with an IEEE-correct division (M = 127, 448 or 57344),
+// c = clamp(x/scale, -M, M) again with IEEE division (never x*(1/scale)); int8
+// codes are rint(c) (half to even, v_rndne), FP8 codes c rounded to nearest even
+// in the format (the float32 -> float8 conversion of .to(dtype), :94). The library
+// is built with -fhip-fp32-correctly-rounded-divide-sqrt and without denormal
+// flushing.
 //
 // Two launches per call: a finiteness scan that sets ASTR_FLAG_NONFINITE_INPUT,
 // then the quantize/scatter kernel that does nothing when that bit is set, so a
@@ -19,6 +22,35 @@ namespace astr {
 namespace {
 
 constexpr int kRowsPerBlock = 4;  // one wave per (token, head, K|V) row
+
+// Largest code magnitude of a format (KVQuantization.maximum, kv_quantization.py:23-25).
+template <int KF>
+__device__ __forceinline__ constexpr float format_max() {
+  return KF == kInt8 ? 127.f : KF == kE4M3 ? 448.f : 57344.f;
+}
+
+// Finite c with |c| <= format_max -> FP8 bits, round to nearest even. With M mantissa
+// bits and exponent bias B: below the smallest normal 2^(1-B) the value counts
+// subnormal steps of 2^(1-B-M), rint(|c| * 2^(B-1+M)) in 0..2^M (scaling by a power of
+// two is exact; 2^M is the smallest normal's code); above it the fp32 mantissa is
+// rounded to M bits at bit 23-M (half to even, a carry steps the exponent) and the
+// exponent rebiased from 127 to B. The sign is kept (-0 for a negative underflow).
+template <int KF>
+__device__ __forceinline__ uint8_t fp8_round(float c) {
+  constexpr int M = KF == kE4M3 ? 3 : 2;
+  constexpr int B = KF == kE4M3 ? 7 : 15;
+  const uint32_t bits = __builtin_bit_cast(uint32_t, c);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  const uint32_t mag = bits & 0x7fffffffu;
+  uint32_t code;
+  if (mag < ((uint32_t)(128 - B) << 23)) {
+    code = (uint32_t)__builtin_rintf(__builtin_bit_cast(float, mag) * (float)(1 << (B - 1 + M)));
+  } else {
+    const uint32_t r = mag + ((1u << (22 - M)) - 1u) + ((mag >> (23 - M)) & 1u);
+    code = (r >> (23 - M)) - ((uint32_t)(127 - B) << M);
+  }
+  return (uint8_t)(code | sign);
+}
 constexpr int kMaxPerLane = 8;    // head_dim <= 512
 
 struct AppendArgs {
@@ -91,7 +123,7 @@ __global__ __launch_bounds__(256) void finite_scan_kernel(AppendArgs a) {
   if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_INPUT);
 }
 
-template <typename T, int VEC>
+template <typename T, int VEC, int KF>
 __global__ __launch_bounds__(256) void quantize_append_kernel(AppendArgs a) {
   // All-or-nothing: the finite scan of this call (or an unacknowledged earlier
   // one) flagged the input, so leave every slot untouched. The flag, slot and
@@ -117,15 +149,18 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(AppendArgs a) {
   for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(x[i]));
   amax = wave_max(amax);
   // kv_quantization.py:86-90 -- true division, then the FLT_MIN clamp.
-  const float scale = amax == 0.f ? 1.f : fmaxf(amax / 127.f, FLT_MIN);
+  constexpr float kMax = format_max<KF>();
+  const float scale = amax == 0.f ? 1.f : fmaxf(amax / kMax, FLT_MIN);
   int8_t* codes = (rr.is_v ? a.cache.v_codes : a.cache.k_codes) +
                   block * a.cache.code_block_stride + rr.h * a.cache.code_head_stride + offset * D;
   int8_t q[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    // kv_quantization.py:91-93 -- divide, clamp, round half to even.
-    const float n = fminf(fmaxf(x[i] / scale, -127.f), 127.f);
-    q[i] = (int8_t)__builtin_rintf(n);
+    // kv_quantization.py:91-94 -- divide, clamp, round half to even (int8) or to
+    // the nearest-even FP8 value
+    const float n = fminf(fmaxf(x[i] / scale, -kMax), kMax);
+    if constexpr (KF == kInt8) q[i] = (int8_t)__builtin_rintf(n);
+    else q[i] = (int8_t)fp8_round<KF>(n);
   }
   if constexpr (VEC > 0) {
     struct alignas(VEC) Pack {
@@ -154,8 +189,20 @@ int launch_append(const AppendArgs& a, hipStream_t stream) {
   const int64_t rows = (a.value ? 2 : 1) * a.num_tokens * a.cache.num_kv_heads;
   const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
   hipLaunchKernelGGL((finite_scan_kernel<T, VEC>), dim3((uint32_t)blocks), dim3(256), 0, stream, a);
-  hipLaunchKernelGGL((quantize_append_kernel<T, VEC>), dim3((uint32_t)blocks), dim3(256), 0,
-                     stream, a);
+  switch (a.cache.code_format) {
+    case kInt8:
+      hipLaunchKernelGGL((quantize_append_kernel<T, VEC, kInt8>), dim3((uint32_t)blocks),
+                         dim3(256), 0, stream, a);
+      break;
+    case kE4M3:
+      hipLaunchKernelGGL((quantize_append_kernel<T, VEC, kE4M3>), dim3((uint32_t)blocks),
+                         dim3(256), 0, stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((quantize_append_kernel<T, VEC, kE5M2>), dim3((uint32_t)blocks),
+                         dim3(256), 0, stream, a);
+      break;
+  }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "quantize_append launch");
 }
@@ -248,6 +295,10 @@ extern "C" int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void
                 kWave * kMaxPerLane);
   if (cache->num_kv_heads < 1 || cache->block_size < 1 || cache->num_blocks < 1)
     return fail(ASTR_EINVAL, "cache sizes must be positive");
+  if (cache->code_format != ASTR_KV_INT8 && cache->code_format != ASTR_KV_FP8_E4M3FN &&
+      cache->code_format != ASTR_KV_FP8_E5M2)
+    return fail(ASTR_EUNSUPPORTED, "code format %d is not int8 / fp8 e4m3fn / fp8 e5m2",
+                cache->code_format);
   if ((value ? 2 : 1) * num_tokens * (int64_t)cache->num_kv_heads >= INT32_MAX)
     return fail(ASTR_EINVAL, "too many rows for one append launch");
   AppendArgs a{key, value, key_token_stride, key_head_stride, value_token_stride,

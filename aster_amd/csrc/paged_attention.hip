@@ -162,6 +162,10 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
   if (window < 0) return fail(ASTR_EINVAL, "window must be >= 0 (0 = no window)");
   if (cache->block_size != kBlockTokens)
     return fail(ASTR_EUNSUPPORTED, "block_size %d != 16", cache->block_size);
+  if (cache->code_format != ASTR_KV_INT8 && cache->code_format != ASTR_KV_FP8_E4M3FN &&
+      cache->code_format != ASTR_KV_FP8_E5M2)
+    return fail(ASTR_EUNSUPPORTED, "code format %d is not int8 / fp8 e4m3fn / fp8 e5m2",
+                cache->code_format);
   if (cache->num_kv_heads < 1 || num_q_heads % cache->num_kv_heads != 0)
     return fail(ASTR_EINVAL, "num_q_heads %d must be a multiple of num_kv_heads %d", num_q_heads,
                 cache->num_kv_heads);

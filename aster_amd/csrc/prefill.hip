@@ -24,12 +24,18 @@
 // to the 8 XCDs round robin) runs one contiguous range of units: the tiles
 // sharing a sequence's K/V then share that XCD's L2.
 #include <climits>
+#include <type_traits>
 
 #include "attention_common.h"
 
 namespace astr {
 namespace attn {
 namespace {
+
+#ifndef ASTR_KF
+#define ASTR_KF 0
+#endif
+constexpr int KF = ASTR_KF;  // this translation unit's code format
 
 constexpr int kXcds = 8;
 constexpr int kPrefillBuffers = 3;
@@ -182,6 +188,13 @@ typedef int int4_t __attribute__((ext_vector_type(4)));
 constexpr int kQRange = 127 * 128;  // |Q| bound: hi = (Q + 64) >> 7 and lo = Q - 128 hi fit int8
 // |S_int| <= 127 * kQRange * 256; a score factor below this keeps every score finite
 constexpr float kSafeFactor = 1.0e29f;
+// FP8 codes take the f16 QK path: |S| <= D * 2^15 * max|code as f16| (448 * 2^-8 for
+// E4M3FN, 57344 for E5M2) with D <= 256, times a factor below these stays finite.
+constexpr float kSafeFactorE4M3 = 1.0e31f;
+constexpr float kSafeFactorE5M2 = 5.0e26f;
+constexpr float safe_factor() {
+  return KF == kInt8 ? kSafeFactor : KF == kE4M3 ? kSafeFactorE4M3 : kSafeFactorE5M2;
+}
 
 // Int8 B-operands of one query column for the QK MFMAs (lane r of its 16-lane group
 // qg holds d = 16*qg + 64*h + [0, 16)): the column is quantized once to integers
@@ -257,21 +270,85 @@ __device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, 
   return mx > 0.f ? qk_scale_log2 * (mx / (float)kQRange) : 0.f;
 }
 
+// Query operands of one column tile: two int8 terms per 64-wide d chunk for int8 codes
+// (the int8 QK MFMA), f16 halves per 32-wide chunk for FP8 codes (the f16 QK MFMA).
+template <int D>
+struct QOpI8 {
+  int4_t hi[D / 64], lo[D / 64];
+};
+template <int D>
+struct QOpF16 {
+  half8_t op[D / 32];
+};
+template <int D>
+using QOp = typename std::conditional<KF == kInt8, QOpI8<D>, QOpF16<D>>::type;
+
+// f16 B-operands of one query column for the f16 QK MFMAs (the FP8 path): chunk
+// kk = 2h + sub holds d = 16 qg + 64 h + 8 sub + [0, 8), like the K operands. The
+// column is scaled by an exact power of two 2^-ex that keeps max|q| < 2^15 before
+// rounding to f16; returns qk_scale_log2 * 2^ex * code_scale (NaN for a non-finite
+// query, which makes every score of the column non-finite as in fp32 arithmetic).
+// Cross-lane: uniform control flow.
+template <typename QT, int D>
+__device__ __forceinline__ float query_column_f16(const QueryColumn<QT, D>& raw, bool valid,
+                                                  float qk_scale_log2, half8_t (&qop)[D / 32]) {
+  constexpr int kVec = 16 / (int)sizeof(QT);
+  float mx = 0.f;
+  bool finite = true;
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int c = 0; c < 16 / kVec; ++c) {
+      const QT* e = reinterpret_cast<const QT*>(&raw.w[h][c]);
+#pragma unroll
+      for (int i = 0; i < kVec; ++i) {
+        const float x = to_float<QT>(e[i]);
+        mx = fmaxf(mx, fabsf(x));
+        finite = finite && __builtin_isfinite(x);
+      }
+    }
+  mx = valid ? mx : 0.f;
+  mx = fmaxf(mx, shfl_xor(mx, 16));
+  mx = fmaxf(mx, shfl_xor(mx, 32));
+  const uint64_t nonfinite_lanes = __ballot(valid && !finite);
+  finite = ((nonfinite_lanes >> (threadIdx.x % 16)) & 0x0001000100010001ull) == 0;
+  int ex = 0;
+  if (finite && mx >= 32768.f) {
+    frexpf(mx, &ex);
+    ex -= 15;  // mx * 2^-ex < 2^15
+  }
+  const float down = ldexpf(1.f, -ex);
+#pragma unroll
+  for (int kk = 0; kk < D / 32; ++kk) {
+    const int h = kk / 2, sub = kk % 2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int el = 8 * sub + i;  // element of the lane's 16 in chunk h
+      const QT* e = reinterpret_cast<const QT*>(&raw.w[h][el / kVec]);
+      qop[kk][i] = valid ? (_Float16)(to_float<QT>(e[el % kVec]) * down) : (_Float16)0.f;
+    }
+  }
+  if (!finite) return __builtin_nanf("");
+  return qk_scale_log2 * ldexpf(1.f, ex) * code_scale<KF>();
+}
+
 // Dequantized V of one staged block as the f16 A-operands of the PV MFMAs, written
 // once by the wave that loaded the block into the slab of its block pair: half `half`
 // of entry n * 64 + lane holds, for that lane (qg, r) of every wave,
 // V[4 qg + j][r * VB + n] * v_scale[4 qg + j], j = 0..3, so that one 16-byte read at the
 // reader's own lane index gives the pair's whole operand (conflict-free). The code is
-// exact in f16 and multiplied by the f16-rounded scale. A block that was not loaded
-// this step leaves stale codes and finite (or zeroed) scales: finite values, which meet
-// p = 0 for its keys.
+// exact in f16 (FP8 codes times 2^-8) and multiplied by the f16-rounded scale times
+// 2^8. A block that was not loaded this step leaves stale codes and finite (or zeroed)
+// scales: finite values, which meet p = 0 for its keys.
 template <int D>
 __device__ __forceinline__ void convert_v(const char* st, int lane, int half, uint2* vt) {
   using S = Stage<D>;
   constexpr int VB = D / 16;
   const int r = lane & 15, qg = lane >> 4;
   const float4_t vsf = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg);
-  const half4_t vsh = {(_Float16)vsf[0], (_Float16)vsf[1], (_Float16)vsf[2], (_Float16)vsf[3]};
+  constexpr float cs = v_weight_scale<KF>();
+  const half4_t vsh = {(_Float16)(vsf[0] * cs), (_Float16)(vsf[1] * cs), (_Float16)(vsf[2] * cs),
+                       (_Float16)(vsf[3] * cs)};
   uint32_t vw[4][VB / 4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -295,10 +372,14 @@ __device__ __forceinline__ void convert_v(const char* st, int lane, int half, ui
     const uint32_t col[4] = {vw[0][n / 4], vw[1][n / 4], vw[2][n / 4], vw[3][n / 4]};
     half4_t v;
     switch (n % 4) {
-      case 0: v = v_operand<0>(col); break;
-      case 1: v = v_operand<1>(col); break;
-      case 2: v = v_operand<2>(col); break;
-      default: v = v_operand<3>(col); break;
+      case 0: v = v_operand<0, KF>(col); break;
+      case 1: v = v_operand<1, KF>(col); break;
+      case 2: v = v_operand<2, KF>(col); break;
+      default: v = v_operand<3, KF>(col); break;
+    }
+    if constexpr (KF == kE5M2) {
+      constexpr _Float16 down = (_Float16)(1.f / 256.f);
+      v = v * half4_t{down, down, down, down};  // exact: E5M2 values times 2^-8 fit f16
     }
     vt[2 * (n * kWave + lane) + half] = __builtin_bit_cast(uint2, v * vsh);
   }
@@ -329,8 +410,7 @@ __device__ __forceinline__ float vmax(float a, float b) { return __builtin_eleme
 template <int D, int NT>
 __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, uint32_t use,
                                              uint32_t bounded, bool masks, int kb0,
-                                             const int4_t (&qhi)[NT][D / 64],
-                                             const int4_t (&qlo)[NT][D / 64],
+                                             const QOp<D> (&qop)[NT],
                                              const float (&cf)[NT], const float (&cfe)[NT],
                                              const int (&lo)[NT], const int (&hi)[NT], int r,
                                              int qg, const half8_t& ones,
@@ -349,24 +429,47 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
       bad |= *reinterpret_cast<const uint32_t*>(cur + b * S::kBytes + S::kF + 4 * qg) ^ 0x01010101u;
     padded = __ballot(bad != 0) != 0;
   }
-  int4_t sacc[NBK][NT];
+  // raw scores of key 4 qg + i of block b, column tile t: exact int32 (int8 codes) or
+  // f32 (FP8 codes as f16 against the f16 query)
+  using Acc = typename std::conditional<KF == kInt8, int4_t, float4_t>::type;
+  Acc sacc[NBK][NT];
 #pragma unroll
   for (int b = 0; b < NBK; ++b) {
     const char* st = cur + b * S::kBytes;
-    int4_t kop[KCH];
-#pragma unroll
-    for (int h = 0; h < KCH; ++h)
-      kop[h] = *reinterpret_cast<const int4_t*>(st + S::kK + r * D + 16 * qg + 64 * h);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      sacc[b][t] = int4_t{0, 0, 0, 0};
+    if constexpr (KF == kInt8) {
+      int4_t kop[KCH];
 #pragma unroll
       for (int h = 0; h < KCH; ++h)
-        sacc[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qhi[t][h], sacc[b][t], 0, 0, 0);
-      sacc[b][t] = sacc[b][t] << 7;
+        kop[h] = *reinterpret_cast<const int4_t*>(st + S::kK + r * D + 16 * qg + 64 * h);
 #pragma unroll
-      for (int h = 0; h < KCH; ++h)
-        sacc[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qlo[t][h], sacc[b][t], 0, 0, 0);
+      for (int t = 0; t < NT; ++t) {
+        sacc[b][t] = int4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int h = 0; h < KCH; ++h)
+          sacc[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop[t].hi[h], sacc[b][t], 0, 0, 0);
+        sacc[b][t] = sacc[b][t] << 7;
+#pragma unroll
+        for (int h = 0; h < KCH; ++h)
+          sacc[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop[t].lo[h], sacc[b][t], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) sacc[b][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int h = 0; h < KCH; ++h) {
+        const uint4 c = *reinterpret_cast<const uint4*>(st + S::kK + r * D + 16 * qg + 64 * h);
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+          half2_t p0, p1, p2, p3;
+          codes_to_f16<KF>(sub ? c.z : c.x, p0, p1);
+          codes_to_f16<KF>(sub ? c.w : c.y, p2, p3);
+          const half8_t kop = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            sacc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[t].op[2 * h + sub],
+                                                                 sacc[b][t], 0, 0, 0);
+        }
+      }
     }
   }
   float4_t ks[NBK];
@@ -384,7 +487,7 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
   const float kmax = __builtin_bit_cast(float, kx);
   bool ok = true;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) ok = ok && kmax * cf[t] <= kSafeFactor;  // false for NaN
+  for (int t = 0; t < NT; ++t) ok = ok && kmax * cf[t] <= safe_factor();  // false for NaN
   const bool unsafe = __ballot(!ok) != 0;
   const bool edge = (use != (1u << NBK) - 1) | (bounded != 0) | unsafe | padded;
   float u[NT][4 * NBK];
@@ -556,10 +659,16 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   // zero scales in every stage, once every wave is past its last read of the plan: a
   // stage that no step writes (a block past the range) then feeds finite products;
   // stages written by loads only ever hold arena scales, which are finite (the append
-  // writes no non-finite value)
+  // writes no non-finite value). Every int8 and E4M3FN byte is a finite code, but
+  // E5M2 bytes with all exponent bits set are Inf/NaN, so there the codes are zeroed too.
   __syncthreads();
   for (int j = lane; j < NB * 32; j += kWave)
     reinterpret_cast<float*>(lds + (j / 32) * kWaves * S::kBytes + wave * S::kBytes + S::kS)[j % 32] = 0.f;
+  if constexpr (KF == kE5M2) {
+    for (int j = lane; j < NB * 2 * D; j += kWave)
+      reinterpret_cast<uint4*>(lds + (j / (2 * D)) * kWaves * S::kBytes + wave * S::kBytes +
+                               S::kK)[j % (2 * D)] = uint4{0u, 0u, 0u, 0u};
+  }
   __syncthreads();
 
   // ---- 2. this wave's columns: flat column f -> token t0 + f / G, head kvh * G + f % G.
@@ -612,11 +721,14 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   for (int j = 0; j < NB - 1 && j < nsteps; ++j)
     if (issue(j, buffer(j))) inflight |= 1u << (j % NB);
 
-  int4_t qhi[NT][D / 64], qlo[NT][D / 64];
+  QOp<D> qop[NT];
   float cf[NT], cfe[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    cf[t] = query_column_i8<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qhi[t], qlo[t]);
+    if constexpr (KF == kInt8)
+      cf[t] = query_column_i8<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qop[t].hi, qop[t].lo);
+    else
+      cf[t] = query_column_f16<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qop[t].op);
     cfe[t] = cf[t] > 0.f ? cf[t] : FLT_MIN;  // cf >= 0 or NaN (scale > 0)
   }
   // key bounds over the wave's valid columns (positions grow with f)
@@ -673,7 +785,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
         if (!(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min)) bounded |= 1u << w;
       }
       if (use != 0)
-        prefill_step<D, NT>(cur, vt[0], use, bounded & use, masks, kb0, qhi, qlo, cf, cfe, lo, hi, r, qg,
+        prefill_step<D, NT>(cur, vt[0], use, bounded & use, masks, kb0, qop, cf, cfe, lo, hi, r, qg,
                             ones, acc, m, bad_score);
     }
     __syncthreads();  // step i's stage may be refilled
@@ -740,7 +852,8 @@ int dispatch_dim(const AttnArgs& a, int G, hipStream_t s) {
 
 }  // namespace
 
-int launch_prefill(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
+template <>
+int launch_prefill_kf<KF>(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
   const int G = a.num_q_heads / a.cache.num_kv_heads;
   switch (q_dtype) {
     case ASTR_F32: return dispatch_dim<float>(a, G, stream);

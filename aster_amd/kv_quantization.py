@@ -1,9 +1,11 @@
-"""INT8 KV format profile and the device quantizer (reference names and semantics).
+"""KV format profiles (INT8, FP8 E4M3FN, FP8 E5M2) and the device quantizer
+(reference names and semantics).
 
 Follows src/aster/optimization/kv_quantization.py: ``KVQuantization`` (:7-25),
 ``QuantizedKV`` (:28-68) and ``quantize_kv`` (:71-94). Quantization itself runs
-in the gfx950 kernel behind ``astr_kv_quantize_append_i8``; this module only
-validates, lays out the call and raises the reference's exceptions.
+in the gfx950 kernel behind ``astr_kv_quantize_append_i8`` (the arena descriptor
+carries the code format); this module only validates, lays out the call and raises
+the reference's exceptions.
 """
 
 from __future__ import annotations
@@ -17,13 +19,14 @@ from .attention_backend import UnsupportedAttentionBackend
 
 _DTYPE_CODES = {torch.float32: _native.ASTR_F32, torch.float16: _native.ASTR_F16,
                 torch.bfloat16: _native.ASTR_BF16}
+FORMAT_CODES = {"int8": _native.ASTR_KV_INT8, "fp8_e4m3fn": _native.ASTR_KV_FP8_E4M3FN,
+                "fp8_e5m2": _native.ASTR_KV_FP8_E5M2}
 
 
 @dataclass(frozen=True)
 class KVQuantization:
-    """Explicit KV storage format (kv_quantization.py:7-25). All three reference
-    formats are accepted as profiles; the HIP kernels implement ``int8`` and
-    raise ``UnsupportedAttentionBackend`` for the FP8 ones."""
+    """Explicit KV storage format (kv_quantization.py:7-25): ``int8``, ``fp8_e4m3fn``
+    or ``fp8_e5m2``, all three implemented by the HIP kernels (one byte per code)."""
 
     format: str = "int8"
 
@@ -85,12 +88,11 @@ class QuantizedKV:
         return (self.values.to(self.scales.dtype) * self.scales).to(dtype or self.source_dtype)
 
 
-def require_int8(config):
+def require_format(config):
+    """The code format of an explicit profile (an ``astr_kv_format`` value)."""
     if not isinstance(config, KVQuantization):
         raise ValueError("An explicit immutable KVQuantization profile is required")
-    if config.format != "int8":
-        raise UnsupportedAttentionBackend(
-            f"hip_int8_paged implements INT8 KV only, not {config.format}")
+    return FORMAT_CODES[config.format]
 
 
 @torch.no_grad()
@@ -99,9 +101,10 @@ def quantize_kv(value, config):
 
     Same contract: ``None`` config or non-floating input passes through; rank < 3
     or empty width, non fp16/bf16/fp32 dtype or non-finite values raise
-    ``ValueError``. Runs on the HIP device; a CPU tensor or an FP8 profile raises
-    ``UnsupportedAttentionBackend``. Synchronises to report non-finite input as the
-    reference does.
+    ``ValueError``. Runs on the HIP device (a CPU tensor raises
+    ``UnsupportedAttentionBackend``); the codes come back in the profile's dtype
+    (``int8``, ``float8_e4m3fn`` or ``float8_e5m2``). Synchronises to report
+    non-finite input as the reference does.
     """
     if config is None or not value.is_floating_point():
         return value
@@ -109,7 +112,7 @@ def quantize_kv(value, config):
         raise ValueError("Quantized KV needs explicit layout [...,tokens,width] and format")
     if value.dtype not in {torch.float16, torch.bfloat16, torch.float32, torch.float64}:
         raise ValueError("Quantized KV requires finite floating input")
-    require_int8(config)
+    code_format = require_format(config)
     if value.dtype == torch.float64:
         raise UnsupportedAttentionBackend("hip_int8_paged stores fp32 scales; fp64 KV is not supported")
     if value.device.type != "cuda":
@@ -128,7 +131,7 @@ def quantize_kv(value, config):
         v_scales=scales.data_ptr(), code_block_stride=rows * tokens * width,
         code_head_stride=tokens * width, scale_block_stride=rows * tokens,
         scale_head_stride=tokens, num_blocks=1, block_size=tokens, num_kv_heads=rows,
-        head_dim=width)
+        head_dim=width, code_format=code_format)
     stream = torch.cuda.current_stream(source.device).cuda_stream
     _native.check(
         _native.lib().astr_kv_quantize_append_i8(
@@ -137,4 +140,4 @@ def quantize_kv(value, config):
         "quantize_kv")
     if int(flag.item()) & _native.FLAG_NONFINITE_INPUT:
         raise ValueError("Quantized KV requires finite floating input")
-    return QuantizedKV(codes, scales, value.dtype)
+    return QuantizedKV(codes.view(config.dtype), scales, value.dtype)

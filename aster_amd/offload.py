@@ -167,7 +167,8 @@ class PagedStateArchive:
             leaves = []
             for layer in range(snapshot.codes.shape[1]):
                 for kv in (0, 1):
-                    leaves.append(QuantizedKV(snapshot.codes[p, layer, kv][None, :, :count],
+                    leaves.append(QuantizedKV(snapshot.codes[p, layer, kv][None, :, :count]
+                                              .view(self.pool.quantization.dtype),
                                               snapshot.scales[p, layer, kv][None, :, :count, None],
                                               torch.float32))
             leaves.append(snapshot.valid[p, :count].bool()[None, None, :, None])

@@ -1,9 +1,10 @@
-"""Device arena of the paged INT8 KV cache and the two hot-path calls on it.
+"""Device arena of the paged low-bit KV cache and the two hot-path calls on it.
 
 Arena layout (one allocation per model, block-major so a physical page of all
 layers is contiguous for copy-on-write and host swap):
 
     codes     int8  [num_blocks, num_layers, 2 (K, V), num_kv_heads, block_size, head_dim]
+                    (one byte per code: int8 values, or FP8 E4M3FN / E5M2 bit patterns)
     scales    fp32  [num_blocks, num_layers, 2 (K, V), num_kv_heads, block_size]
     key_valid uint8 [num_blocks, block_size]   (0: the slot holds a padding key)
 
@@ -32,18 +33,19 @@ import torch
 
 from . import _native
 from .attention_backend import BACKEND, KernelWork, UnsupportedAttentionBackend
-from .kv_quantization import KVQuantization, QuantizedKV, _DTYPE_CODES, require_int8
+from .kv_quantization import KVQuantization, QuantizedKV, _DTYPE_CODES, require_format
 
 DEFAULT_PARTITION_TOKENS = 0  # automatic: stream-K for bf16/fp16, else 512-token partitions
 
 
 class PagedKVCache:
-    """Caller-owned device arena for ``num_layers`` layers of INT8 paged K/V."""
+    """Caller-owned device arena for ``num_layers`` layers of paged K/V in one of the
+    reference's formats (``KVQuantization``: int8, fp8_e4m3fn, fp8_e5m2)."""
 
     def __init__(self, *, num_blocks, num_layers, num_kv_heads, head_dim, block_size=16,
                  device="cuda", quantization=None):
         quantization = KVQuantization("int8") if quantization is None else quantization
-        require_int8(quantization)
+        self.code_format = require_format(quantization)
         if min(num_blocks, num_layers, num_kv_heads, head_dim, block_size) < 1:
             raise ValueError("Cache capacities must be positive")
         if block_size != 16:
@@ -75,7 +77,8 @@ class PagedKVCache:
             scale_block_stride=s.stride(0), scale_head_stride=s.stride(3),
             num_blocks=self.num_blocks, block_size=self.block_size,
             num_kv_heads=self.num_kv_heads, head_dim=self.head_dim,
-            key_valid=self.key_valid.data_ptr() if self.has_padding else None)
+            key_valid=self.key_valid.data_ptr() if self.has_padding else None,
+            code_format=self.code_format)
 
     def _enable_padding(self):
         if not self.has_padding:
@@ -92,11 +95,16 @@ class PagedKVCache:
     def page(self, block, layer):
         """Zero-copy ``QuantizedKV`` views ``[1, Hkv, bs, D]`` of one page
         (the reference's ``PageView.payload[2*layer : 2*layer+2]``, state.py:158-163)."""
-        k = QuantizedKV(self.codes[block, layer, 0][None], self.scales[block, layer, 0][None, ..., None],
-                        torch.float32)
-        v = QuantizedKV(self.codes[block, layer, 1][None], self.scales[block, layer, 1][None, ..., None],
-                        torch.float32)
+        k = QuantizedKV(self.code_view(self.codes[block, layer, 0][None]),
+                        self.scales[block, layer, 0][None, ..., None], torch.float32)
+        v = QuantizedKV(self.code_view(self.codes[block, layer, 1][None]),
+                        self.scales[block, layer, 1][None, ..., None], torch.float32)
         return k, v
+
+    def code_view(self, raw):
+        """Raw code bytes (int8 storage) viewed in the format's dtype (int8,
+        float8_e4m3fn or float8_e5m2), zero-copy; ``.float()`` of it is the code value."""
+        return raw.view(self.quantization.dtype)
 
     def padding_leaf(self, block):
         """Zero-copy bool view ``[1, 1, bs, 1]`` of one page's padding leaf (True =

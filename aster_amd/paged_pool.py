@@ -31,7 +31,7 @@ import threading
 
 import torch
 
-from .kv_quantization import QuantizedKV, require_int8
+from .kv_quantization import QuantizedKV, require_format
 
 
 class StateError(RuntimeError):
@@ -106,7 +106,7 @@ class PagedStatePool:
     evidence_kind = "hip_arena_storage"
 
     def __init__(self, cache, *, kind="gqa_kv"):
-        require_int8(cache.quantization)
+        require_format(cache.quantization)
         self.cache = cache
         self.block_size, self.max_blocks = cache.block_size, cache.num_blocks
         self.kind = kind
@@ -453,7 +453,7 @@ class PagedStatePool:
                 for kv in (0, 1):
                     codes = self.cache.codes[blocks, layer, kv]    # [P, Hkv, bs, D]
                     scales = self.cache.scales[blocks, layer, kv]  # [P, Hkv, bs]
-                    x = codes.float() * scales[..., None]
+                    x = self.cache.code_view(codes).float() * scales[..., None]
                     x = x.permute(1, 0, 2, 3).reshape(x.shape[1], -1, x.shape[-1])
                     pair.append(x[None, :, : sequence.length])
                 layers.append(tuple(pair))
@@ -490,7 +490,7 @@ class PagedStatePool:
         without requantization, publish after the copy completes (state.py:427-493).
 
         ``payloads``: one tuple per page of ``2 * num_layers`` ``QuantizedKV`` leaves
-        ``(k_0, v_0, ...)`` of ``[1, Hkv, count, D]`` int8 codes and
+        ``(k_0, v_0, ...)`` of ``[1, Hkv, count, D]`` codes (in the format's dtype) and
         ``[1, Hkv, count, 1]`` fp32 scales, optionally followed by the padding leaf
         ``[1, 1, count, 1]`` (what ``read_pages`` exposes and ``PagedStateArchive``
         keeps), or ``(codes, scales[, valid])`` already packed in the
@@ -567,7 +567,7 @@ class PagedStatePool:
                 if tuple(leaf.values.shape) != want or tuple(leaf.scales.shape) != want[:3] + (1,):
                     raise StateError("Archived KV layout differs from model pool")
                 layer, kv = divmod(i, 2)
-                codes[p, layer, kv, :, :tokens] = leaf.values[0].cpu()
+                codes[p, layer, kv, :, :tokens] = leaf.values[0].cpu().view(torch.int8)
                 scales[p, layer, kv, :, :tokens] = leaf.scales[0, ..., 0].cpu()
         return codes, scales, valid
 

@@ -44,9 +44,16 @@ extern "C" {
 enum astr_dtype { ASTR_F32 = 0, ASTR_F16 = 1, ASTR_BF16 = 2 };
 
 /*
- * One layer of the paged INT8 KV arena (device memory, caller-owned).
- * Codes: a block holds num_kv_heads x block_size token rows of head_dim int8
- * codes; a token row is contiguous (token stride = head_dim bytes).
+ * Code formats of the arena (KVQuantization.format, kv_quantization.py:7-25): one byte
+ * per element, with maximum 127 (int8), 448 (OCP FP8 E4M3FN) or 57344 (OCP FP8 E5M2).
+ */
+enum astr_kv_format { ASTR_KV_INT8 = 0, ASTR_KV_FP8_E4M3FN = 1, ASTR_KV_FP8_E5M2 = 2 };
+
+/*
+ * One layer of the paged KV arena (device memory, caller-owned).
+ * Codes: a block holds num_kv_heads x block_size token rows of head_dim one-byte
+ * codes in `code_format` (int8, or FP8 E4M3FN / E5M2 bit patterns); a token row is
+ * contiguous (token stride = head_dim bytes).
  * Scales: one fp32 per (block, head, token); token stride = 1 float.
  * Physical block b, kv head h, token slot s lives at
  *   k_codes + b*code_block_stride + h*code_head_stride + s*head_dim
@@ -74,11 +81,12 @@ typedef struct astr_paged_kv {
   int32_t num_kv_heads;
   int32_t head_dim;     /* 64, 128 or 256 for attention; any 1..512 for append */
   uint8_t* key_valid;   /* [num_blocks * block_size] or NULL; 16-byte aligned */
+  int32_t code_format;  /* astr_kv_format */
 } astr_paged_kv;
 
 /*
- * Quantize new K and V token rows to INT8 + fp32 per-(token, head) scales and
- * write them into their cache slots.
+ * Quantize new K and V token rows to the arena's code format + fp32
+ * per-(token, head) scales and write them into their cache slots.
  * Replaces quantize_kv (src/aster/optimization/kv_quantization.py:71-94) as
  * called from PagedStatePool._append_leaves (src/aster/inference/state.py:292)
  * plus its per-token raw copy_kv into page slot divmod(offset, block_size)
@@ -88,8 +96,11 @@ typedef struct astr_paged_kv {
  *              to quantize key rows only (into k_codes/k_scales).
  *   slot_mapping: int64 [num_tokens], slot = block*block_size + offset;
  *              slot < 0 skips the token (padding).
- * Bit-exact with the reference: scale = amax==0 ? 1 : max(amax/127, FLT_MIN),
- * code = rint(clamp(x/scale, -127, 127)) with IEEE fp32 division.
+ * Bit-exact with the reference: scale = amax==0 ? 1 : max(amax/M, FLT_MIN) and
+ * c = clamp(x/scale, -M, M) with IEEE fp32 division (M the format's maximum); the
+ * code is rint(c) (half to even) for int8, and c rounded to nearest-even FP8
+ * (subnormals kept, -0 for negative underflow) for the FP8 formats, as torch's
+ * float32 -> float8 conversion does.
  * All-or-nothing: a NaN/Inf anywhere in key/value sets
  * ASTR_FLAG_NONFINITE_INPUT and no slot is written (kv_quantization.py:77-81).
  * A set input-flag bit also suppresses later appends until cleared.

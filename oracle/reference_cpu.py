@@ -1,4 +1,5 @@
-"""numpy restatement of the reference's INT8 paged-decode arithmetic.
+"""numpy restatement of the reference's low-bit (INT8, FP8 E4M3FN, FP8 E5M2)
+paged-decode arithmetic.
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``): the product never imports
 this module. Every function cites the reference file:line it restates, relative
@@ -10,6 +11,12 @@ Parity status of each function (how it is pinned, in ``tests/test_oracle.py``):
                             FLT_MIN clamp, true-division vs reciprocal cases,
                             error bound and |code|max == 127 invariants.
   dequantize                pinned: closed form fp32(code)*scale (atol 0).
+  fp8_values / fp8_round    pinned: every one of the 256 codes against torch's
+                            float8_e4m3fn / float8_e5m2 -> float32 conversion, and
+                            the rounding against torch's float32 -> float8
+                            conversion on random, tie, subnormal and extreme values.
+  quantize_kv_fp8           pinned: against the reference's own torch expression
+                            (amax / finfo.max, clamp, .to(float8)) on the CPU.
   merge_softmax / output    pinned: partition merge == whole, -inf partitions.
   online_attention_statistics
                             pinned: fp64 brute-force dense softmax (dense.py),
@@ -29,6 +36,8 @@ import numpy as np
 FLT_TINY = np.float32(np.finfo(np.float32).tiny)
 DBL_TINY = np.float64(np.finfo(np.float64).tiny)
 INT8_MAXIMUM = 127.0  # kv_quantization.py:23-25 (KVQuantization("int8").maximum)
+# KVQuantization(...).maximum of the FP8 formats: torch.finfo(dtype).max (:23-25)
+FP8_MAXIMUM = {"fp8_e4m3fn": 448.0, "fp8_e5m2": 57344.0}
 
 
 # ----------------------------------------------------------------------------
@@ -38,10 +47,12 @@ INT8_MAXIMUM = 127.0  # kv_quantization.py:23-25 (KVQuantization("int8").maximum
 
 @dataclass(frozen=True)
 class QuantizedKV:
-    """codes int8 [..., T, D] and scales [..., T, 1] (kv_quantization.py:28-68)."""
+    """codes [..., T, D] and scales [..., T, 1] (kv_quantization.py:28-68): int8 values,
+    or uint8 FP8 bit patterns of format ``fmt``."""
 
     values: np.ndarray
     scales: np.ndarray
+    fmt: str = "int8"
 
     @property
     def shape(self):
@@ -50,12 +61,19 @@ class QuantizedKV:
     def narrow(self, start, count):
         """Token-axis slice (kv_quantization.py:57-64)."""
         return QuantizedKV(
-            self.values[..., start : start + count, :], self.scales[..., start : start + count, :]
+            self.values[..., start : start + count, :], self.scales[..., start : start + count, :],
+            self.fmt,
         )
+
+    def code_values(self):
+        """The codes as exact floats (int8 values, or decoded FP8)."""
+        if self.fmt == "int8":
+            return self.values.astype(np.float64)
+        return fp8_values(self.fmt)[self.values.astype(np.uint8)]
 
     def dequantize(self, dtype=None):
         """``values.to(scales.dtype) * scales`` then cast (kv_quantization.py:66-68)."""
-        out = self.values.astype(self.scales.dtype) * self.scales
+        out = self.code_values().astype(self.scales.dtype) * self.scales
         return out if dtype is None else out.astype(dtype)
 
 
@@ -83,6 +101,73 @@ def quantize_kv_int8(x):
     normalized = np.clip(np.divide(source, scales, dtype=acc), -INT8_MAXIMUM, INT8_MAXIMUM)
     codes = np.rint(normalized).astype(np.int8)
     return QuantizedKV(codes, scales)
+
+
+def fp8_values(fmt):
+    """The 256 FP8 codes' values (float64; NaN/Inf codes as NaN/Inf), from the OCP
+    format definition: E4M3FN bias 7, 3 mantissa bits, no Inf, 0x7F/0xFF NaN; E5M2
+    bias 15, 2 mantissa bits, IEEE-style Inf/NaN (torch.float8_e4m3fn / float8_e5m2,
+    the dtypes of KVQuantization.dtype, kv_quantization.py:16-21)."""
+    e_bits, m_bits, bias = (4, 3, 7) if fmt == "fp8_e4m3fn" else (5, 2, 15)
+    out = np.empty(256, np.float64)
+    for code in range(256):
+        sign = -1.0 if code & 0x80 else 1.0
+        e = (code >> m_bits) & ((1 << e_bits) - 1)
+        m = code & ((1 << m_bits) - 1)
+        if fmt == "fp8_e4m3fn" and (code & 0x7F) == 0x7F:
+            out[code] = np.nan
+        elif fmt == "fp8_e5m2" and e == 31:
+            out[code] = sign * np.inf if m == 0 else np.nan
+        elif e == 0:
+            out[code] = sign * m * 2.0 ** (1 - bias - m_bits)
+        else:
+            out[code] = sign * (1 + m / (1 << m_bits)) * 2.0 ** (e - bias)
+    return out
+
+
+def fp8_round(c, fmt):
+    """float32 ``c`` (finite, |c| <= the format's maximum) -> FP8 codes (uint8),
+    round to the nearest representable value, ties to the even code, sign kept (-0
+    for negative values that round to zero): the float32 -> float8 conversion of
+    ``.to(dtype)`` at kv_quantization.py:94. Restated as a nearest-value search over
+    the format's finite non-negative values (exact in float64)."""
+    c = np.asarray(c, np.float32)
+    values = fp8_values(fmt)
+    finite = np.isfinite(values[:128])
+    grid = values[:128][finite]          # non-negative values, increasing with the code
+    codes = np.arange(128)[finite]
+    a = np.abs(c.astype(np.float64))
+    hi = np.clip(np.searchsorted(grid, a), 0, len(grid) - 1)
+    lo = np.clip(hi - 1, 0, len(grid) - 1)
+    dlo, dhi = a - grid[lo], grid[hi] - a
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & (codes[hi] % 2 == 0) & (hi != lo))
+    pick = np.where(a <= grid[0], 0, np.where(pick_hi, hi, lo))
+    code = codes[pick].astype(np.uint8)
+    return code | np.where(np.signbit(c), np.uint8(0x80), np.uint8(0))
+
+
+def quantize_kv_fp8(x, fmt):
+    """Per-(token, head) FP8 codes + scales (kv_quantization.py:71-94 with an FP8
+    profile): scale = 1 where amax == 0 else max(amax / M, tiny) (M =
+    finfo(dtype).max, :86-90), codes = float8(clamp(x / scale, -M, M)) (:91-94; no
+    rounding step before the cast, :92-93 apply to int8 only)."""
+    x = np.asarray(x)
+    if x.ndim < 3 or x.shape[-1] < 1:
+        raise ValueError("Quantized KV needs explicit layout [...,tokens,width] and format")
+    if x.dtype not in (np.float16, np.float32) or not np.isfinite(x).all():
+        raise ValueError("Quantized KV requires finite floating input")
+    maximum_code = np.float32(FP8_MAXIMUM[fmt])
+    source = x.astype(np.float32)
+    maximum = np.abs(source).max(axis=-1, keepdims=True)
+    divided = np.divide(maximum, maximum_code, dtype=np.float32)
+    scales = np.where(maximum == 0, np.float32(1.0), np.maximum(divided, FLT_TINY)).astype(np.float32)
+    normalized = np.clip(np.divide(source, scales, dtype=np.float32), -maximum_code, maximum_code)
+    return QuantizedKV(fp8_round(normalized, fmt), scales, fmt)
+
+
+def quantize_kv(x, fmt="int8"):
+    """``quantize_kv`` for any of the three formats."""
+    return quantize_kv_int8(x) if fmt == "int8" else quantize_kv_fp8(x, fmt)
 
 
 # ----------------------------------------------------------------------------
@@ -257,7 +342,7 @@ def online_attention(query, blocks, **kwargs):
 
 
 def page_blocks(k_codes, k_scales, v_codes, v_scales, block_table, length, block_size,
-                padding=None):
+                padding=None, fmt="int8"):
     """One AttentionBlock per page, narrowed to its valid tokens, at absolute
     offset ``index * block_size`` (state.py:358-390 read_pages;
     paged_attention.py:170-183). Arena layout: codes ``[blocks, Hkv, bs, D]``,
@@ -266,8 +351,9 @@ def page_blocks(k_codes, k_scales, v_codes, v_scales, block_table, length, block
     for index in range(math.ceil(length / block_size)):
         page = int(block_table[index])
         count = min(block_size, length - index * block_size)
-        key = QuantizedKV(k_codes[page][None, :, :count], k_scales[page][None, :, :count, None])
-        value = QuantizedKV(v_codes[page][None, :, :count], v_scales[page][None, :, :count, None])
+        key = QuantizedKV(k_codes[page][None, :, :count], k_scales[page][None, :, :count, None], fmt)
+        value = QuantizedKV(v_codes[page][None, :, :count], v_scales[page][None, :, :count, None],
+                            fmt)
         pad = None if padding is None else padding[page][None, :count]
         blocks.append(AttentionBlock(key, value, index * block_size, pad))
     return blocks
@@ -275,7 +361,7 @@ def page_blocks(k_codes, k_scales, v_codes, v_scales, block_table, length, block
 
 def paged_attention(query, k_codes, k_scales, v_codes, v_scales, block_tables, context_lens,
                     *, block_size, scale, query_lens=None, causal=True, window=None,
-                    query_block_size=32, key_block_size=64, padding=None):
+                    query_block_size=32, key_block_size=64, padding=None, fmt="int8"):
     """Ragged paged attention over a committed arena, row by row, as
     ``PagedAttentionRunner.forward_batch`` does (paged_attention.py:168-215).
 
@@ -302,7 +388,7 @@ def paged_attention(query, k_codes, k_scales, v_codes, v_scales, block_tables, c
             outputs.append(np.zeros((qn, query.shape[1], width), dtype=acc))
             continue
         blocks = page_blocks(k_codes, k_scales, v_codes, v_scales, block_tables[b], ctx,
-                             block_size, padding)
+                             block_size, padding, fmt)
         positions = np.arange(ctx - qn, ctx)[None]
         out = online_attention(q, blocks, query_positions=positions, causal=causal, window=window,
                                scale=scale, query_block_size=query_block_size,
@@ -311,12 +397,13 @@ def paged_attention(query, k_codes, k_scales, v_codes, v_scales, block_tables, c
     return np.concatenate(outputs, 0)
 
 
-def quantize_append(k, v, slot_mapping, k_codes, k_scales, v_codes, v_scales, block_size):
+def quantize_append(k, v, slot_mapping, k_codes, k_scales, v_codes, v_scales, block_size,
+                    fmt="int8"):
     """Quantize new tokens and copy raw codes/scales into ``slot // bs, slot % bs``
     (state.py:292 quantize, :339-344 per-token copy_kv). ``k``/``v`` ``[T, Hkv, D]``;
     slots < 0 are skipped. Mutates the arena arrays in place."""
-    qk = quantize_kv_int8(np.asarray(k).transpose(1, 0, 2)[None])
-    qv = quantize_kv_int8(np.asarray(v).transpose(1, 0, 2)[None])
+    qk = quantize_kv(np.asarray(k).transpose(1, 0, 2)[None], fmt)
+    qv = quantize_kv(np.asarray(v).transpose(1, 0, 2)[None], fmt)
     for t, slot in enumerate(np.asarray(slot_mapping).tolist()):
         if slot < 0:
             continue

@@ -53,6 +53,9 @@ class FakeArena:
             b, o = divmod(slot, self.block_size)
             self.key_valid[b, o] = 1 if valid is None else int(bool(valid[t]))
 
+    def code_view(self, raw):
+        return raw.view(self.quantization.dtype)
+
     def padding_leaf(self, block):
         return self.key_valid[block].view(torch.bool)[None, None, :, None]
 

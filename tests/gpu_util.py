@@ -33,7 +33,7 @@ def oracle_decode(workload_or_tables, cache, query, layer=0, context_lens=None, 
     padding = cache.key_valid.cpu().numpy().astype(bool) if cache.has_padding else None
     return ref.paged_attention(q, *arena_numpy(cache, layer), tables, lens, block_size=16,
                                scale=scale, window=window, query_lens=query_lens, causal=causal,
-                               padding=padding)
+                               padding=padding, fmt=cache.quantization.format)
 
 
 def mark_padding(cache, tables, lens, fraction, seed, *, whole_rows=(), whole_blocks=0):

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from aster_amd import KernelWork, PagedKVCache, UnsupportedAttentionBackend
+from aster_amd import KernelWork, KVQuantization, PagedKVCache, UnsupportedAttentionBackend
 from aster_amd import workloads as wl
 from tests.gpu_util import arena_numpy, assert_attention_close, mark_padding, oracle_decode
 
@@ -18,9 +18,9 @@ pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
-def _build(w, device, layers=1):
+def _build(w, device, layers=1, fmt="int8"):
     cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=layers, num_kv_heads=w.num_kv_heads,
-                         head_dim=w.head_dim, device=device)
+                         head_dim=w.head_dim, device=device, quantization=KVQuantization(fmt))
     wl.materialize(w, cache, device=device)
     tables, lens = wl.device_tables(w, device)
     return cache, tables, lens
@@ -111,6 +111,53 @@ def test_key_padding(device, dim, hq, hkv, qdtype, part):
                                     window=window, check=True)
         assert (out[5] == 0).all()
         assert_attention_close(out, oracle_decode(w, cache, q, window=window))
+
+
+@pytest.mark.parametrize("fmt", ["fp8_e4m3fn", "fp8_e5m2"])
+@pytest.mark.parametrize("dim,hq,hkv", [(128, 32, 8), (64, 8, 2), (256, 8, 2), (128, 64, 8)])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("part", [0, 128])
+def test_fp8_kv_formats(device, fmt, dim, hq, hkv, qdtype, part):
+    """FP8 E4M3FN / E5M2 arenas (KVQuantization formats, kv_quantization.py:7-25):
+    the codes enter the f16 MFMAs (or the fp32 VALU kernel) exactly, so the result
+    matches the oracle's dequantize-then-attend within the same tolerance; with a
+    window and key padding too."""
+    if hq // hkv == 16 and qdtype == torch.float32:
+        pytest.skip("fp32 queries run the VALU kernel, which takes GQA groups up to 8")
+    lens = np.array([1, 15, 16, 17, 255, 256, 257, 600, 0, 33], np.int32)
+    rng = np.random.default_rng(dim + hq)
+    tables, pool = wl._tables_from_lengths(lens, rng, spare_blocks=3)
+    w = wl.DecodeWorkload("fp8", hq, hkv, dim, lens, tables, pool, qdtype, 7, dim ** -0.5)
+    cache, t, l = _build(w, device, fmt=fmt)
+    q = wl.queries(w, device)
+    out = cache.paged_attention(0, q, t, l, max_context_len=600, partition_tokens=part,
+                                check=True)
+    assert (out[8] == 0).all()
+    assert_attention_close(out, oracle_decode(w, cache, q))
+    mark_padding(cache, tables, lens, 0.2, seed=dim)
+    out = cache.paged_attention(0, q, t, l, max_context_len=600, partition_tokens=part,
+                                window=50, check=True)
+    assert_attention_close(out, oracle_decode(w, cache, q, window=50))
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8_e4m3fn", "fp8_e5m2"])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("part", [0, 128])
+def test_small_values_keep_their_precision(device, fmt, qdtype, part):
+    """Attention is linear in V: V scales times 2^-6 (an exact change of the arena)
+    give outputs 2^-6 as large, within the tolerance scaled the same way. E5M2's
+    scales (amax / 57344) lie below f16's normal range, so this needs the kernels to
+    lift them before the PV weights are rounded to f16."""
+    lens = np.array([1, 17, 255, 600, 33, 1000], np.int32)
+    rng = np.random.default_rng(61)
+    tables, pool = wl._tables_from_lengths(lens, rng, spare_blocks=3)
+    w = wl.DecodeWorkload("small", 32, 8, 128, lens, tables, pool, qdtype, 9, 128 ** -0.5)
+    cache, t, l = _build(w, device, fmt=fmt)
+    cache.scales[:, 0, 1] *= 2.0 ** -6
+    q = wl.queries(w, device)
+    out = cache.paged_attention(0, q, t, l, max_context_len=1000, partition_tokens=part,
+                                check=True)
+    assert_attention_close(out, oracle_decode(w, cache, q), atol=2e-3 * 2.0 ** -6)
 
 
 def test_empty_rows_are_zero_and_ctx_one_returns_value(device):

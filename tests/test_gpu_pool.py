@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from aster_amd import PagedKVCache
+from aster_amd import KVQuantization, PagedKVCache
 from aster_amd import _native
 from aster_amd.offload import PagedStateArchive
 from aster_amd.paged_pool import CacheCapacityError, PagedStatePool, StateError
@@ -21,9 +21,10 @@ pytestmark = pytest.mark.gpu
 L, HKV, D = 2, 4, 64
 
 
-def make_pool(device, blocks=16):
+def make_pool(device, blocks=16, fmt="int8"):
     return PagedStatePool(PagedKVCache(num_blocks=blocks, num_layers=L, num_kv_heads=HKV,
-                                       head_dim=D, device=device))
+                                       head_dim=D, device=device,
+                                       quantization=KVQuantization(fmt)))
 
 
 def layers(tokens, seed, device, dtype=torch.bfloat16):
@@ -32,8 +33,8 @@ def layers(tokens, seed, device, dtype=torch.bfloat16):
                   for _ in range(2)) for _ in range(L)]
 
 
-def oracle_state(state_layers):
-    return [tuple(torch.from_numpy(ref.quantize_kv_int8(x.float().cpu().numpy()).dequantize())
+def oracle_state(state_layers, fmt="int8"):
+    return [tuple(torch.from_numpy(ref.quantize_kv(x.float().cpu().numpy(), fmt).dequantize())
                   for x in pair) for pair in state_layers]
 
 
@@ -221,3 +222,44 @@ def test_async_put_and_restore(device):
     assert restored.length == 20 and pool.used_blocks == 2
     archive.release(handle, identity="p")
     pool.release(restored)
+
+
+@pytest.mark.parametrize("fmt", ["fp8_e4m3fn", "fp8_e5m2"])
+def test_fp8_pool_append_fork_archive_and_attention(device, fmt):
+    """An FP8 arena behind the pool: appends dequantize to the oracle's FP8 values, page
+    views carry the profile's float8 dtype, copy-on-write and the host archive move the
+    bytes unchanged, and attention over the pool's block tables matches the oracle."""
+    pool = make_pool(device, blocks=24, fmt=fmt)
+    seq = pool.create("tenant")
+    base = layers(21, 50, device)
+    pool.append_delta(seq, base)
+    assert_state(pool, seq, oracle_state(base, fmt))
+    fork = pool.fork(seq)
+    extra = layers(6, 51, device)
+    pool.append_delta(fork, extra)  # copy of the shared partial tail page
+    assert_state(pool, seq, oracle_state(base, fmt))
+    assert_state(pool, fork, oracle_state([(torch.cat([a, c], 2), torch.cat([b, d], 2))
+                                           for (a, b), (c, d) in zip(base, extra)], fmt))
+    with pool.read_pages(fork) as views:
+        assert views[0].payload[0].values.dtype == KVQuantization(fmt).dtype
+        before = [[(x.values.view(torch.uint8).clone(), x.scales.clone()) for x in v.payload[:-1]]
+                  for v in views]
+    archive = PagedStateArchive(pool)
+    handle = archive.put(fork)
+    pool.release(fork)
+    restored = archive.restore(handle, identity="tenant")
+    with pool.read_pages(restored) as views:
+        after = [[(x.values.view(torch.uint8).clone(), x.scales.clone()) for x in v.payload[:-1]]
+                 for v in views]
+    for pa, pb in zip(before, after):
+        for (ca, sa), (cb, sb) in zip(pa, pb):
+            assert torch.equal(ca, cb) and torch.equal(sa, sb)
+    g = torch.Generator(device=device).manual_seed(52)
+    q = torch.randn(2, 2 * HKV, D, generator=g, device=device).to(torch.bfloat16)
+    for layer in range(L):
+        with pool.block_tables([seq, restored]) as (tables, lens):
+            out = pool.cache.paged_attention(layer, q, tables, lens, max_context_len=27, check=True)
+            torch.cuda.synchronize()
+            want = oracle_decode(tables.cpu().numpy(), pool.cache, q, layer=layer,
+                                 context_lens=lens.cpu().numpy(), scale=D ** -0.5)
+        assert_attention_close(out, want)

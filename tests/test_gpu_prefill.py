@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from aster_amd import KernelWork, PagedKVCache
+from aster_amd import KernelWork, KVQuantization, PagedKVCache
 from aster_amd import workloads as wl
 from tests.gpu_util import assert_attention_close, mark_padding, oracle_decode
 
@@ -24,9 +24,9 @@ def _mixed(q_lens, ctx, *, hq=32, hkv=8, dim=128, qdtype=torch.bfloat16, seed=11
                              query_lens=q_lens)
 
 
-def _build(w, device):
+def _build(w, device, fmt="int8"):
     cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=1, num_kv_heads=w.num_kv_heads,
-                         head_dim=w.head_dim, device=device)
+                         head_dim=w.head_dim, device=device, quantization=KVQuantization(fmt))
     wl.materialize(w, cache, device=device)
     tables, lens = wl.device_tables(w, device)
     return cache, tables, lens, wl.device_query_start(w, device)
@@ -82,6 +82,35 @@ def test_key_padding_in_chunks(device, dim, hq, hkv, window):
     q = wl.queries(w, device)
     out = _run(cache, w, q, tables, lens, qsl, window=window)
     assert_attention_close(out, oracle_decode(w, cache, q, window=window))
+
+
+@pytest.mark.parametrize("fmt", ["fp8_e4m3fn", "fp8_e5m2"])
+@pytest.mark.parametrize("dim,hq,hkv", [(128, 32, 8), (64, 16, 2), (256, 8, 2)])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_fp8_kv_formats_in_mixed_steps(device, fmt, dim, hq, hkv, qdtype):
+    """FP8 arenas on the prefill kernel's f16 QK path (chunk rows) and the decode kernels
+    (decode rows) of one mixed step, causal and windowed."""
+    if hq // hkv == 16 and qdtype == torch.float32:
+        pytest.skip("fp32 decode rows run the exact VALU kernel, which takes GQA groups up to 8")
+    w = _mixed(Q_LENS, CTX, hq=hq, hkv=hkv, dim=dim, qdtype=qdtype, seed=dim + 1)
+    cache, tables, lens, qsl = _build(w, device, fmt)
+    q = wl.queries(w, device)
+    for window in (None, 40):
+        out = _run(cache, w, q, tables, lens, qsl, window=window)
+        assert_attention_close(out, oracle_decode(w, cache, q, window=window))
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8_e4m3fn", "fp8_e5m2"])
+def test_small_values_keep_their_precision(device, fmt):
+    """V scales times 2^-6 (exact) give outputs 2^-6 as large within the tolerance
+    scaled the same way, on the chunk and decode rows of one step (E5M2's scales lie
+    below f16's normal range unless lifted before the V operands are rounded)."""
+    w = _mixed(Q_LENS, CTX, hq=32, hkv=8, dim=128, seed=62)
+    cache, tables, lens, qsl = _build(w, device, fmt)
+    cache.scales[:, 0, 1] *= 2.0 ** -6
+    q = wl.queries(w, device)
+    out = _run(cache, w, q, tables, lens, qsl)
+    assert_attention_close(out, oracle_decode(w, cache, q), atol=2e-3 * 2.0 ** -6)
 
 
 def test_non_causal_without_window(device):

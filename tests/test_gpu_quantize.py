@@ -16,9 +16,12 @@ pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
-def _cache(device, blocks, heads, dim, layers=1):
+FORMATS = ["int8", "fp8_e4m3fn", "fp8_e5m2"]
+
+
+def _cache(device, blocks, heads, dim, layers=1, fmt="int8"):
     return PagedKVCache(num_blocks=blocks, num_layers=layers, num_kv_heads=heads, head_dim=dim,
-                        device=device)
+                        device=device, quantization=KVQuantization(fmt))
 
 
 def test_config1_append_matches_golden_arena(device):
@@ -50,11 +53,25 @@ def test_quantize_kv_api_seed76_known_answer(device):
                                atol=0, rtol=0)
 
 
-def _edge_rows(dim, rng):
+def _edge_rows(dim, rng, fmt="int8"):
     """Rows that stress every branch: zero row, FLT_MIN clamp (denormal and tiny
-    normal amax), exact half-way ties, +-127 clamp, x8 outliers, mixed magnitudes."""
+    normal amax), exact half-way ties, +-127 clamp, x8 outliers, mixed magnitudes;
+    for FP8 also rows whose scale is a power of two (amax = max * 2^e), so that
+    midpoints between neighbouring FP8 values are exact ties and subnormal codes
+    appear."""
     tiny = np.finfo(np.float32).tiny
     rows = [np.zeros(dim, np.float32)]
+    if fmt != "int8":
+        values = ref.fp8_values(fmt)[:128]
+        finite = values[np.isfinite(values)]
+        mids = ((finite[1:] + finite[:-1]) / 2).astype(np.float32)
+        for e in (-20, 0, 5):
+            for start in range(0, mids.size, dim - 1):
+                r = np.zeros(dim, np.float32)
+                r[0] = ref.FP8_MAXIMUM[fmt]
+                chunk = mids[start : start + dim - 1]
+                r[1 : 1 + chunk.size] = chunk * np.where(np.arange(chunk.size) % 2, -1, 1)
+                rows.append((r * np.float32(2.0**e)).astype(np.float32))
     r = np.zeros(dim, np.float32)
     r[:3] = [1e-40, -7e-41, 3e-45]
     rows.append(r)
@@ -79,11 +96,14 @@ def _edge_rows(dim, rng):
     return np.stack(rows)
 
 
+@pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("dim", [64, 128, 32, 200])
-def test_append_edge_rows_bit_exact(device, dtype, dim):
+def test_append_edge_rows_bit_exact(device, dtype, dim, fmt):
     rng = np.random.default_rng(dim)
-    rows = _edge_rows(dim, rng)
+    rows = _edge_rows(dim, rng, fmt)
+    if dtype == torch.float16:  # FP8 E5M2 ties reach 57344 * 2^5: keep fp16-finite rows
+        rows = rows[np.abs(rows).max(1) < 60000]
     heads = 2
     tokens = rows.shape[0] // heads
     src = rows[: tokens * heads].reshape(tokens, heads, dim)
@@ -95,12 +115,12 @@ def test_append_edge_rows_bit_exact(device, dtype, dim):
         kf, vf = k.numpy(), v.numpy()
     blocks = (tokens + 15) // 16 + 3
     slots = np.random.default_rng(1).permutation(blocks * 16)[:tokens].astype(np.int64)
-    cache = _cache(device, blocks, heads, dim)
+    cache = _cache(device, blocks, heads, dim, fmt=fmt)
     cache.append(0, k.to(device), v.to(device), torch.from_numpy(slots).to(device), check=True)
     shape = (blocks, heads, 16, dim)
     want = [np.zeros(shape, np.int8), np.ones(shape[:3], np.float32),
             np.zeros(shape, np.int8), np.ones(shape[:3], np.float32)]
-    ref.quantize_append(kf, vf, slots, want[0], want[1], want[2], want[3], 16)
+    ref.quantize_append(kf, vf, slots, want[0], want[1], want[2], want[3], 16, fmt)
     got = arena_numpy(cache)
     for name, a, b in zip(("k_codes", "k_scales", "v_codes", "v_scales"), got, want):
         if a.dtype == np.float32:
@@ -161,8 +181,21 @@ def test_quantize_kv_passthrough_and_unsupported(device):
     x = torch.randn(1, 1, 2, 4, device=device)
     assert quantize_kv(x, None) is x
     with pytest.raises(UnsupportedAttentionBackend):
-        quantize_kv(x, KVQuantization("fp8_e4m3fn"))
-    with pytest.raises(UnsupportedAttentionBackend):
         quantize_kv(x.cpu(), KVQuantization())
     with pytest.raises(ValueError):
         quantize_kv(torch.randn(4, 4, device=device), KVQuantization())
+
+
+@pytest.mark.parametrize("fmt", ["fp8_e4m3fn", "fp8_e5m2"])
+def test_quantize_kv_api_fp8_matches_oracle(device, fmt):
+    """quantize_kv with an FP8 profile returns codes in the profile's float8 dtype,
+    bit-exact with the oracle (itself pinned to torch's float32 -> float8 cast)."""
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((2, 3, 9, 64)) * np.exp(rng.uniform(-8, 8, (2, 3, 9, 1))))
+    x = x.astype(np.float32)
+    packed = quantize_kv(torch.from_numpy(x).to(device), KVQuantization(fmt))
+    want = ref.quantize_kv_fp8(x, fmt)
+    assert packed.values.dtype == KVQuantization(fmt).dtype
+    np.testing.assert_array_equal(packed.values.cpu().view(torch.uint8).numpy(), want.values)
+    np.testing.assert_array_equal(packed.scales.cpu().numpy(), want.scales)
+    np.testing.assert_array_equal(packed.dequantize().cpu().numpy(), want.dequantize())

@@ -344,3 +344,66 @@ def test_runner_order_equivalence_chunk_block_vs_appended_page():
     chunk = ref.AttentionBlock(last, lastv, ctx - 1)
     separate = ref.online_attention(q, old + [chunk], query_positions=pos, scale=64 ** -0.5)
     np.testing.assert_allclose(appended, separate, rtol=1e-5, atol=1e-6)
+
+
+# ---- FP8 formats (KVQuantization("fp8_e4m3fn"/"fp8_e5m2"), kv_quantization.py:7-25, 71-94)
+import torch  # noqa: E402  (CPU conversions: the library routine FP8 reduces to)
+
+FP8 = {"fp8_e4m3fn": torch.float8_e4m3fn, "fp8_e5m2": torch.float8_e5m2}
+
+
+@pytest.mark.parametrize("fmt", sorted(FP8))
+def test_fp8_code_values_match_torch_for_all_256_codes(fmt):
+    got = ref.fp8_values(fmt)
+    want = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(FP8[fmt]).double().numpy()
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    keep = ~np.isnan(want)
+    np.testing.assert_array_equal(got[keep], want[keep])
+    assert ref.FP8_MAXIMUM[fmt] == torch.finfo(FP8[fmt]).max
+
+
+@pytest.mark.parametrize("fmt", sorted(FP8))
+def test_fp8_rounding_matches_torch_conversion(fmt):
+    """Random magnitudes over the whole range, exact midpoints between neighbouring
+    codes (ties to even), subnormal steps, +-0, the maximum and the values just below
+    it: codes equal torch's float32 -> float8 bits."""
+    rng = np.random.default_rng(9)
+    top = ref.FP8_MAXIMUM[fmt]
+    values = ref.fp8_values(fmt)[:128]
+    finite = values[np.isfinite(values)]
+    mids = (finite[1:] + finite[:-1]) / 2  # exact in float32 for these short mantissas
+    probe = np.concatenate([
+        rng.uniform(-top, top, 20000),
+        np.exp(rng.uniform(np.log(1e-12), np.log(top), 20000)) * rng.choice([-1, 1], 20000),
+        mids, -mids, finite, -finite,
+        np.nextafter(mids.astype(np.float32), np.float32(0)),
+        np.nextafter(mids.astype(np.float32), np.float32(np.inf)),
+        [0.0, -0.0, top, -top, np.nextafter(np.float32(top), np.float32(0))],
+    ]).astype(np.float32)
+    probe = np.clip(probe, -top, top).astype(np.float32)
+    want = torch.from_numpy(probe).to(FP8[fmt]).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(ref.fp8_round(probe, fmt), want)
+    # a plausible mistake: ties away from zero instead of to even
+    assert (ref.fp8_round(mids.astype(np.float32), fmt) % 2 == 0).all()
+
+
+@pytest.mark.parametrize("fmt", sorted(FP8))
+def test_quantize_kv_fp8_matches_reference_torch_expression(fmt):
+    """The reference's quantize_kv body (amax / finfo.max, FLT_MIN clamp, clamp,
+    .to(float8)) evaluated by torch on the CPU, on rows of very different ranges,
+    a zero row and fp16 input: identical codes and scales."""
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((2, 3, 17, 64)) * np.exp(rng.uniform(-12, 12, (2, 3, 17, 1))))
+    x = x.astype(np.float32)
+    x[1, 2, 5] = 0.0
+    for arr in (x, (x / np.abs(x).max() * 30000).astype(np.float16)):
+        got = ref.quantize_kv_fp8(arr, fmt)
+        source = torch.from_numpy(arr).float()
+        maximum = source.abs().amax(-1, keepdim=True)
+        top = torch.finfo(FP8[fmt]).max
+        scales = torch.where(maximum == 0, torch.ones_like(maximum),
+                             (maximum / top).clamp_min(torch.finfo(torch.float32).tiny))
+        codes = (source / scales).clamp(-top, top).to(FP8[fmt])
+        np.testing.assert_array_equal(got.scales, scales.numpy())
+        np.testing.assert_array_equal(got.values, codes.view(torch.uint8).numpy())
+        np.testing.assert_array_equal(got.dequantize(), (codes.float() * scales).numpy())
