@@ -15,6 +15,8 @@ namespace attn {
 constexpr int kBlockTokens = 16;
 constexpr int kWaves = 4;              // waves per workgroup
 constexpr int kMaxBlocksPerWave = 64;  // block ids one wave keeps in a register
+// stream-K: blocks one wave may stream (its block list goes in windows of 64)
+constexpr int kMaxBlocksPerWaveSK = 1024;
 constexpr float kRescaleSlack = 8.0f;  // p = exp2(s - m) <= 2^8 between rescales
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -169,6 +171,16 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
+// A wave-uniform pointer as the compiler's uniformity analysis sees it (values that
+// came out of LDS count as per-lane there): the saddr operands need it in SGPRs.
+template <typename T>
+__device__ __forceinline__ const T* uniform_ptr(const T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
+}
+
 // Issue the direct-to-LDS loads of block `phys` (kv head kvh) into stage `st`:
 // Stage<D>::kLoads vector-memory instructions (waves are always full, so the
 // 32-lane scale load always issues), plus one for the block's 16 key-padding bytes
@@ -180,8 +192,8 @@ __device__ __forceinline__ void stage_block(const AttnArgs& a, int phys, int kvh
   const int64_t off = (int64_t)phys * a.cache.code_block_stride +
                       (int64_t)kvh * a.cache.code_head_stride;  // wave-uniform
   const uint32_t base = lds_addr(st);
-  const int8_t* const kb = a.cache.k_codes + off;
-  const int8_t* const vb = a.cache.v_codes + off;
+  const int8_t* const kb = uniform_ptr(a.cache.k_codes + off);
+  const int8_t* const vb = uniform_ptr(a.cache.v_codes + off);
 #pragma unroll
   for (int j = 0; j < S::kCodeLoads; ++j)
     lds_dma_x4_s(kb, lane * 16 + j * 1024, base + S::kK + j * 1024);
@@ -198,7 +210,8 @@ __device__ __forceinline__ void stage_block(const AttnArgs& a, int phys, int kvh
   // them. Stage pipelines count kLoads per stage: with this extra load their waits
   // let fewer loads stay in flight than allowed, never more, as loads complete in order.
   if (a.cache.key_valid != nullptr && lane < 4)
-    lds_dma_x1_s(a.cache.key_valid + (int64_t)phys * kBlockTokens, lane * 4, base + S::kF);
+    lds_dma_x1_s(uniform_ptr(a.cache.key_valid + (int64_t)phys * kBlockTokens), lane * 4,
+                 base + S::kF);
 }
 
 // ---- exact code -> f16 operands (int8; FP8 E4M3FN values times 2^-8; FP8 E5M2)

@@ -34,13 +34,13 @@ constexpr int kMaxSeqsSK = 512;  // per-sequence table lives in LDS
 constexpr int kFastPieces = 16;  // merge: rows split into at most this many pieces load at once
 
 // Ranges per kv head over the Bh visible blocks of one head: the resident waves
-// (one round, no tail), more only where that would put over kMaxBlocksPerWave
+// (one round, no tail), more only where that would put over kMaxBlocksPerWaveSK
 // blocks on a wave, never more than launched, and at most one range per block (so
 // every range owns at least one block and a row split over ranges r0..r1 has
 // exactly one piece in each of them; the merge relies on it). The decode and the
 // merge kernel both derive Wr from Bh with this function.
 __device__ __forceinline__ int64_t streamk_ranges(const AttnArgs& a, int64_t Bh, int hkv) {
-  int64_t w = (Bh + kMaxBlocksPerWave - 1) / kMaxBlocksPerWave;
+  int64_t w = (Bh + kMaxBlocksPerWaveSK - 1) / kMaxBlocksPerWaveSK;
   if (w < a.pref_waves / hkv) w = a.pref_waves / hkv;
   if (w > a.total_waves / hkv) w = a.total_waves / hkv;
   return w < Bh ? w : Bh;
@@ -49,6 +49,18 @@ __device__ __forceinline__ int64_t streamk_ranges(const AttnArgs& a, int64_t Bh,
 // Range owning block b when range r owns [floor(Bh*r/Wr), floor(Bh*(r+1)/Wr)).
 __device__ __forceinline__ int64_t range_of(int64_t b, int64_t Bh, int64_t Wr) {
   return ((b + 1) * Wr - 1) / Bh;
+}
+
+// Sequence owning block b of the per-head order (s_cu[s] <= b < s_cu[s + 1], the last
+// such s where empty rows share an offset); wave-uniform.
+__device__ __forceinline__ int seq_of_block(const int* s_cu, int nseq, int64_t b) {
+  int lo = 0, hi = nseq;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (s_cu[mid] <= b) lo = mid;
+    else hi = mid;
+  }
+  return lo;
 }
 
 template <typename QT>
@@ -70,7 +82,11 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   constexpr int NW = sk_waves<D>();
   constexpr int SPT = (kMaxSeqsSK + NW * kWave - 1) / (NW * kWave);  // sequences per thread
 
+  // Per wave, besides its block ring: the next window's block ids (256 bytes), which
+  // arrive by direct-to-LDS loads issued well before use.
+  constexpr int kIdsBytes = 256;
   __shared__ __attribute__((aligned(16))) char lds[NS * NW * S::kBytes];  // [stage][wave]
+  __shared__ __attribute__((aligned(16))) char id_slots[NW * kIdsBytes];   // [wave]
   __shared__ int s_ctx[kMaxSeqsSK];  // -1: not a decode row
   __shared__ int s_tok[kMaxSeqsSK];  // query/output token row
   __shared__ int s_cu[kMaxSeqsSK + 1];
@@ -146,34 +162,50 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     b0 = (int64_t)bseq * rg / Wr;
     n = (int)((int64_t)bseq * (rg + 1) / Wr - b0);
   }
-  const bool too_long = n > kMaxBlocksPerWave;  // contexts beyond the declared maximum
-  if (too_long) n = kMaxBlocksPerWave;
-  int row_id = 0, ids = 0;  // row id = kv_head * nseq + seq
-  if (lane < n) {
-    const int rem = (int)(b0 + lane);
-    int lo = 0, hi = nseq;  // s_cu[lo] <= rem < s_cu[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (s_cu[mid] <= rem) lo = mid;
-      else hi = mid;
-    }
-    const RowSpan sp = row_span(a, s_ctx[lo]);
-    ids = a.block_tables[(int64_t)lo * a.bt_stride + sp.first_blk + rem - s_cu[lo]];
-    row_id = kv * nseq + lo;
-  }
-  const int row0 = __builtin_amdgcn_readfirstlane(row_id);
-  const bool bad_index =
+  const bool too_long = n > kMaxBlocksPerWaveSK;  // contexts beyond the declared maximum
+  if (too_long) n = kMaxBlocksPerWaveSK;
+  // Block list in windows of 64: lane j of window w holds block b0 + 64 w + j of the
+  // per-head order, as its physical id and its row id (kv_head * nseq + seq).
+  // Window 0 is read here; the ids of window w + 1 go by direct-to-LDS loads into the
+  // wave's id slot when window w starts, before block 64 w + NS is issued: direct-to-LDS
+  // loads complete in issue order, so once a block issued after them has landed, they
+  // have too (the block ring relies on the same), 64 - 2 NS blocks before they are read.
+  auto window_rows = [&](int w, int& row_id) __attribute__((always_inline)) -> const int32_t* {
+    const int j = 64 * w + lane;
+    if (j >= n) return nullptr;
+    const int64_t rem = b0 + j;
+    const int sq = seq_of_block(s_cu, nseq, rem);
+    row_id = kv * nseq + sq;
+    return a.block_tables + (int64_t)sq * a.bt_stride + row_span(a, s_ctx[sq]).first_blk +
+           (rem - s_cu[sq]);
+  };
+  int rows = 0, ids = 0, rows_nx = 0, ids_nx = 0;
+  char* const id_slot = id_slots + wave * kIdsBytes;
+  auto request_ids = [&](int w) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of the slot are done
+    if (const int32_t* t = window_rows(w, rows_nx)) lds_dma_x1(t, lds_addr(id_slot));
+  };
+  if (const int32_t* t = window_rows(0, rows)) ids = *t;
+  const int row0 = __builtin_amdgcn_readfirstlane(rows);
+  bool bad_index =
       too_long || __ballot(lane < n && (unsigned)ids >= (unsigned)a.cache.num_blocks) != 0;
-  const int nblk = bad_index ? 0 : n;
+  int nblk = bad_index ? 0 : n;
+  int cw = 0;  // window of `ids` / `rows`; `ids_nx` / `rows_nx` hold window cw + 1
 
   auto stage = [&](int j) __attribute__((always_inline)) -> char* {
     return lds + ((j % NS) * NW + wave) * S::kBytes;
   };
   auto issue = [&](int j) __attribute__((always_inline)) {
-    stage_block<D>(a, __builtin_amdgcn_readlane(ids, j),
-                   __builtin_amdgcn_readlane(row_id, j) / nseq, lane, stage(j));
+    const bool cur = (j >> 6) == cw;
+    const int id = cur ? __builtin_amdgcn_readlane(ids, j & 63)
+                       : __builtin_amdgcn_readlane(ids_nx, j & 63);
+    const int rid = cur ? __builtin_amdgcn_readlane(rows, j & 63)
+                        : __builtin_amdgcn_readlane(rows_nx, j & 63);
+    stage_block<D>(a, __builtin_amdgcn_readfirstlane(id), __builtin_amdgcn_readfirstlane(rid) / nseq,
+                   lane, stage(j));
   };
   // Wait until block j has landed; the blocks after it (up to NS - 1) stay in flight.
+  // Loads the compiler does not count only add to what is outstanding: never too few.
   auto wait_block = [&](int j) __attribute__((always_inline)) {
     const int later = min(NS - 1, nblk - 1 - j);
     if (NS > 3 && later >= 3) wait_vmcnt<3 * S::kLoads>();
@@ -197,6 +229,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     lds_query<QT, D>(stage(NS - 1), gvalid ? r : 0, qg, qr);
     cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop) * code_scale<KF>();
     if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (their values are consumed)
+    if (64 < nblk) request_ids(1);
   }
 
   // ---- 3. stream the blocks, one piece (the run of one row's blocks) at a time;
@@ -204,14 +237,12 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   float4_t acc[NPV];
   float m = 0.f, l = 0.f;
   bool bad_score = false;
+  const bool masks = a.cache.key_valid != nullptr;
   int i = 0;
   while (i < nblk) {
-    const int rid = __builtin_amdgcn_readlane(row_id, i);
-    // row ids grow with the lane: the piece ends at the first lane holding a larger id
-    const uint64_t beyond = __ballot(lane < nblk && row_id > rid);
-    const int iend = beyond ? (int)__builtin_ctzll(beyond) : nblk;
+    const int crid = __builtin_amdgcn_readlane(rows, i & 63);  // this piece's row
     const int pstart = i;
-    const int pseq = rid % nseq, pkvh = rid / nseq;
+    const int pseq = crid % nseq, pkvh = crid / nseq;
     const RowSpan psp = row_span(a, s_ctx[pseq]);
     const int64_t pfb = s_cu[pseq];  // first block of the row in the per-head order
     if (i > 0) {  // a new row starts inside this wave's range
@@ -224,15 +255,43 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     // are all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
     m = gvalid ? -FLT_MAX : 0.f;
     l = 0.f;
-    const int blk0 = psp.first_blk + (int)(b0 + i - pfb);
-    for (; i < iend; ++i) {
-      wait_block(i);
-      mfma_block<D, G, KF>(stage(i), qop, cf, (blk0 + i - pstart) * kBlockTokens, psp.kv_begin,
-                       psp.ctx, r, qg, acc, m, l, bad_score, a.cache.key_valid != nullptr);
-      if (i + NS < nblk) issue(i + NS);
+    const int pos0 = (psp.first_blk + (int)(b0 + i - pfb)) * kBlockTokens;
+    for (;;) {
+      // the row's blocks in the current window: up to the first lane with another row
+      const int wend = min(64 * (cw + 1), nblk);
+      const uint64_t beyond =
+          __ballot(lane >= (i & 63) && 64 * cw + lane < wend && rows != crid);
+      const int iend = beyond ? 64 * cw + (int)__builtin_ctzll(beyond) : wend;
+      for (; i < iend; ++i) {
+        wait_block(i);
+        mfma_block<D, G, KF>(stage(i), qop, cf, pos0 + (i - pstart) * kBlockTokens,
+                             psp.kv_begin, psp.ctx, r, qg, acc, m, l, bad_score, masks);
+        const int nx = i + NS;
+        if (nx < nblk && (nx & 63) == 0) {
+          // first block of window cw + 1: its ids were requested before block
+          // nx - 64 + NS <= i was issued, which has landed; check them before use
+          ids_nx = reinterpret_cast<const int*>(id_slot)[lane];
+          if (__ballot(lane < min(64, nblk - nx) &&
+                       (unsigned)ids_nx >= (unsigned)a.cache.num_blocks) != 0) {
+            bad_index = true;
+            nblk = nx;  // stop after the blocks already issued
+          }
+        }
+        if (nx < nblk) issue(nx);
+      }
+      if (i == wend && i < nblk) {  // into the next window of the block list
+        ids = ids_nx;
+        rows = rows_nx;
+        ++cw;
+        if (64 * (cw + 1) < nblk) request_ids(cw + 1);
+        if (__builtin_amdgcn_readlane(rows, 0) == crid) continue;  // the row goes on
+      }
+      break;
     }
-    // write the piece: the final output when the whole row is in this wave, else a
-    // partial in slot 0 (the piece starts the wave's range) or 1 (it ends it)
+    // write the piece [pstart, i): the final output when the whole row is in this
+    // wave, else a partial in slot 0 (the piece starts the wave's range) or 1 (it
+    // ends it)
+    const int iend = i;
     float lt = l + shfl_xor(l, 16);
     lt += shfl_xor(lt, 32);
     lt *= norm_scale<KF>();  // the factor the PV weights carry
@@ -283,7 +342,7 @@ __global__ __launch_bounds__(256) void merge_streamk_kernel(AttnArgs a) {
   if (r0 == r1) return;  // written whole by one wave
   const int pieces = (int)(r1 - r0 + 1);
   const bool first_is_tail = (int64_t)bseq * r0 / Wr < fb;  // the row is r0's last piece (slot 1)
-  auto slot_of = [&](int p) -> int64_t __attribute__((always_inline)) {
+  auto slot_of = [&](int p) __attribute__((always_inline)) -> int64_t {
     const int64_t w = (r0 + p) * hkv + kvh;  // the wave that streamed range r0 + p for this head
     return (w * 2 + (p == 0 && first_is_tail ? 1 : 0)) * G + g;
   };

@@ -84,7 +84,7 @@ Layout streamk_layout(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_head
                       int32_t head_dim, int32_t max_context_len, int32_t window,
                       int64_t launch_waves) {
   const int64_t need = (max_total_blocks(num_seqs, num_kv_heads, max_context_len, window) +
-                        kMaxBlocksPerWave - 1) / kMaxBlocksPerWave;
+                        kMaxBlocksPerWaveSK - 1) / kMaxBlocksPerWaveSK;
   int64_t cap = (int64_t)device_cus() * kMaxResidentWavesPerCU;
   cap = cap > need ? cap : need;
   cap = (cap + kWaves - 1) / kWaves * kWaves;
@@ -97,9 +97,9 @@ Layout streamk_layout(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_head
   return w;
 }
 
-// Fewest waves that keep every wave at kMaxBlocksPerWave blocks or less.
+// Fewest waves that keep every wave at kMaxBlocksPerWaveSK blocks or less.
 int64_t streamk_min_waves(int64_t total_blocks) {
-  const int64_t need = (total_blocks + kMaxBlocksPerWave - 1) / kMaxBlocksPerWave;
+  const int64_t need = (total_blocks + kMaxBlocksPerWaveSK - 1) / kMaxBlocksPerWaveSK;
   return (need + kWaves - 1) / kWaves * kWaves;
 }
 

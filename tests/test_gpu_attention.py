@@ -221,6 +221,36 @@ def test_full_config5_long_context_rows_match_oracle(device):
     assert_attention_close(out, oracle_decode(w, cache, q))
 
 
+def test_long_waves_stream_several_block_windows(device):
+    """Stream-K waves streaming more than 64 blocks keep their block list in windows
+    of 64 (the next window's ids load while the current one streams): 32 kv heads
+    leave few ranges per head, so 48 ragged rows of 1000-5000 tokens give each wave
+    well over 64 blocks, with row boundaries at many offsets inside later windows.
+    Every row matches the fixed-partition kernel, four match the oracle, and an
+    out-of-range block id deep inside a row is flagged, never read."""
+    rng = np.random.default_rng(71)
+    lens = rng.integers(1000, 5001, 48).astype(np.int32)
+    tables, pool = wl._tables_from_lengths(lens, rng, spare_blocks=4)
+    w = wl.DecodeWorkload("long_waves", 64, 32, 128, lens, tables, pool, torch.bfloat16, 72,
+                          128 ** -0.5)
+    cache, t, l = _build(w, device)
+    q = wl.queries(w, device)
+    mx = int(lens.max())
+    sk = cache.paged_attention(0, q, t, l, max_context_len=mx, partition_tokens=0, check=True)
+    part = cache.paged_attention(0, q, t, l, max_context_len=mx, partition_tokens=512,
+                                 check=True)
+    assert_attention_close(sk, part)
+    rows = [0, 17, 30, 47]
+    sub = wl.DecodeWorkload("long_waves_rows", 64, 32, 128, lens[rows], tables[rows], pool,
+                            torch.bfloat16, 72, 128 ** -0.5)
+    assert_attention_close(sk[rows], oracle_decode(sub, cache, q[rows]))
+    bad = t.clone()
+    longest = int(np.argmax(lens))
+    bad[longest, int(lens[longest]) // 32] = w.num_blocks + 5
+    with pytest.raises(ValueError, match="outside"):
+        cache.paged_attention(0, q, bad, l, max_context_len=mx, partition_tokens=0, check=True)
+
+
 def test_duplicate_rows_and_prefix_sharing(device):
     """Rows aliasing the same blocks give identical outputs for identical queries."""
     w = wl.scaled(wl.config4(), num_seqs=4)
