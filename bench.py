@@ -226,7 +226,8 @@ def main():
         "hbm_fraction_of_step": alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "roofline": {
             "kernel": ("decode_streamk_kernel + merge_streamk_kernel" if args.partition == 0 else
-                       "decode_mfma_kernel + merge_kernel") + " (one paged_attention call)",
+                       "decode_mfma_kernel + merge_kernel")
+                      + (" + prefill_mfma_kernel" if varlen else "") + " (one paged_attention call)",
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
             "algorithmic_bytes_per_launch": alg_bytes,
