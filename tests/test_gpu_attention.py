@@ -251,6 +251,50 @@ def test_long_waves_stream_several_block_windows(device):
         cache.paged_attention(0, q, bad, l, max_context_len=mx, partition_tokens=0, check=True)
 
 
+def test_automatic_mode_beyond_stream_k_limits(device):
+    """partition_tokens = 0 takes stream-K only for up to 512 sequences and 64 kv heads;
+    beyond either limit it runs 512-token partitions: bit-identical to asking for them,
+    and equal to the oracle (600 ragged rows, sampled; 80 kv heads; a 600-row mixed step)."""
+    rng = np.random.default_rng(81)
+    lens = rng.integers(1, 700, 600).astype(np.int32)
+    tables, pool = wl._tables_from_lengths(lens, rng, spare_blocks=2)
+    w = wl.DecodeWorkload("many_rows", 8, 2, 64, lens, tables, pool, torch.bfloat16, 82, 0.125)
+    cache, t, l = _build(w, device)
+    q = wl.queries(w, device)
+    mx = int(lens.max())
+    auto = cache.paged_attention(0, q, t, l, max_context_len=mx, partition_tokens=0, check=True)
+    fixed = cache.paged_attention(0, q, t, l, max_context_len=mx, partition_tokens=512, check=True)
+    assert torch.equal(auto, fixed)
+    rows = [0, 1, 299, 598, 599]
+    sub = wl.DecodeWorkload("many_rows_sample", 8, 2, 64, lens[rows], tables[rows], pool,
+                            torch.bfloat16, 82, 0.125)
+    assert_attention_close(auto[rows], oracle_decode(sub, cache, q[rows]))
+    # the same rows as one mixed step: every fifth row brings a 3-token chunk
+    qlens = np.where(np.arange(600) % 5 == 0, 3, 1).astype(np.int32)
+    qlens = np.minimum(qlens, lens)
+    mixed = wl.DecodeWorkload("many_rows_mixed", 8, 2, 64, lens, tables, pool, torch.bfloat16, 83,
+                              0.125, query_lens=qlens)
+    qm = wl.queries(mixed, device)
+    qsl = wl.device_query_start(mixed, device)
+    out = cache.paged_attention(0, qm, t, l, max_context_len=mx, query_start_loc=qsl,
+                                max_query_len=int(qlens.max()), check=True)
+    qsl_h = mixed.query_start_loc()
+    take = np.concatenate([np.arange(qsl_h[r], qsl_h[r + 1]) for r in rows])
+    subm = wl.DecodeWorkload("many_rows_mixed_sample", 8, 2, 64, lens[rows], tables[rows], pool,
+                             torch.bfloat16, 83, 0.125, query_lens=qlens[rows])
+    assert_attention_close(out[take], oracle_decode(subm, cache, qm[take]))
+    # more kv heads than the stream-K counters cover
+    lens80 = np.array([1, 40, 333, 17], np.int32)
+    tables80, pool80 = wl._tables_from_lengths(lens80, rng, spare_blocks=2)
+    w80 = wl.DecodeWorkload("heads80", 80, 80, 64, lens80, tables80, pool80, torch.bfloat16, 84,
+                            0.125)
+    cache80, t80, l80 = _build(w80, device)
+    q80 = wl.queries(w80, device)
+    out80 = cache80.paged_attention(0, q80, t80, l80, max_context_len=333, partition_tokens=0,
+                                    check=True)
+    assert_attention_close(out80, oracle_decode(w80, cache80, q80))
+
+
 def test_duplicate_rows_and_prefix_sharing(device):
     """Rows aliasing the same blocks give identical outputs for identical queries."""
     w = wl.scaled(wl.config4(), num_seqs=4)
