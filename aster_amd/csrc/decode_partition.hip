@@ -312,7 +312,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
 
   const int ids = wave_block_ids(a, seq, first, nbw, lane);
   bool bad_index = false, bad_score = false;
-  auto fetch = [&](int i, ValuTile<NL>& t) -> bool __attribute__((always_inline)) {
+  auto fetch = [&](int i, ValuTile<NL>& t) __attribute__((always_inline)) -> bool {
     const int phys = __builtin_amdgcn_readlane(ids, i);
     const bool ok = (unsigned)phys < (unsigned)a.cache.num_blocks;
     if (ok) load(phys, t);

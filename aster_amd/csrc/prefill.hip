@@ -703,7 +703,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   // holds the id for step (i + 64*k); reloaded every 64 steps.
   bool bad_index = false, bad_score = false;
   const bool masks = a.cache.key_valid != nullptr;  // the arena has key padding bytes
-  auto issue = [&](int step, char* buf) -> bool __attribute__((always_inline)) {
+  auto issue = [&](int step, char* buf) __attribute__((always_inline)) -> bool {
     if (b_lo + step * kWaves + wave >= b_hi) return false;
     const int id = __builtin_amdgcn_readlane(ids, step % kWave);
     if ((unsigned)id >= (unsigned)a.cache.num_blocks) {
