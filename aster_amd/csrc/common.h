@@ -40,11 +40,24 @@ template <>
 __device__ __forceinline__ _Float16 from_float<_Float16>(float v) { return (_Float16)v; }
 template <>
 __device__ __forceinline__ bf16_t from_float<bf16_t>(float v) {
-  // round-to-nearest-even fp32 -> bf16 (NaN kept quiet)
-  uint32_t u = __builtin_bit_cast(uint32_t, v);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t{(uint16_t)((u >> 16) | 0x40u)};
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return bf16_t{(uint16_t)(u >> 16)};
+  // round-to-nearest-even fp32 -> bf16, NaN stays NaN (v_cvt_pk_bf16_f32)
+  return bf16_t{__builtin_bit_cast(uint16_t, (__bf16)v)};
+}
+
+// Two values rounded to nearest even and packed in one word, a in the low half
+// (one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<bf16_t>(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<_Float16>(float a, float b) {
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
 }
 
 // ---- cross-lane reductions ----------------------------------------------------

@@ -113,6 +113,20 @@ def test_small_values_keep_their_precision(device, fmt):
     assert_attention_close(out, oracle_decode(w, cache, q), atol=2e-3 * 2.0 ** -6)
 
 
+def test_tiny_query_heads(device):
+    """Query heads scaled by 2^-100 (column maxima below the 2^-64 under which the int8
+    query path lifts a column by 2^64 before quantizing it) beside heads at full scale
+    in the same waves: the tiny heads' scores vanish (near-uniform attention over their
+    visible keys) and the other heads are unaffected."""
+    w = _mixed(Q_LENS, CTX, hq=32, hkv=8, dim=128, seed=63)
+    cache, tables, lens, qsl = _build(w, device)
+    q = wl.queries(w, device)
+    q[:, 1::3] *= 2.0 ** -100
+    out = _run(cache, w, q, tables, lens, qsl)
+    assert torch.isfinite(out).all()
+    assert_attention_close(out, oracle_decode(w, cache, q))
+
+
 def test_non_causal_without_window(device):
     w = _mixed(Q_LENS, CTX, seed=6)
     cache, tables, lens, qsl = _build(w, device)
