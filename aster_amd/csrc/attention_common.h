@@ -181,6 +181,27 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p) {
   return reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
 }
 
+// K tiles are staged with the 16-byte chunks of each key row XOR-swizzled: chunk c of
+// row r sits at chunk position c ^ k_swizzle<D>(r) of that row. Operand reads (lane
+// (qg, r) reads chunk qg + 4h of row r) on rows D bytes apart otherwise meet LDS bank
+// conflicts: 1.2x (D = 64, 128) to 1.45x (D = 256) the cycles of a contiguous
+// 16-byte-per-lane read on gfx950. These swizzles, picked by timing every linear map
+// of the row bits, read as fast as the contiguous pattern. The direct-to-LDS loads
+// apply it through each lane's source chunk; every byte stays in its row, and each
+// load still covers one contiguous KiB of the block.
+template <int D>
+__device__ __forceinline__ int k_swizzle(int r) {
+  if constexpr (D == 64) return (r >> 1) & 2;
+  else if constexpr (D == 128) return ((r << 1) & 4) | ((r >> 1) & 2);
+  else return r & 15;
+}
+// Byte offset of d-chunk c (bytes 16c .. 16c+15) of key row r in a staged K tile (and,
+// the swizzle being an involution, the source chunk of staging slot (r, c)).
+template <int D>
+__device__ __forceinline__ int k_chunk(int r, int c) {
+  return r * D + 16 * (c ^ k_swizzle<D>(r));
+}
+
 // Issue the direct-to-LDS loads of block `phys` (kv head kvh) into stage `st`:
 // Stage<D>::kLoads vector-memory instructions (waves are always full, so the
 // 32-lane scale load always issues), plus one for the block's 16 key-padding bytes
@@ -196,7 +217,8 @@ __device__ __forceinline__ void stage_block(const AttnArgs& a, int phys, int kvh
   const int8_t* const vb = uniform_ptr(a.cache.v_codes + off);
 #pragma unroll
   for (int j = 0; j < S::kCodeLoads; ++j)
-    lds_dma_x4_s(kb, lane * 16 + j * 1024, base + S::kK + j * 1024);
+    lds_dma_x4_s(kb, k_chunk<D>((64 * j + lane) / (D / 16), lane % (D / 16)),
+                 base + S::kK + j * 1024);
 #pragma unroll
   for (int j = 0; j < S::kCodeLoads; ++j)
     lds_dma_x4_s(vb, lane * 16 + j * 1024, base + S::kV + j * 1024);
@@ -364,7 +386,7 @@ __device__ __forceinline__ void mfma_block(const char* st, const half8_t (&qop)[
   float4_t s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int h = 0; h < KCH; ++h) {
-    const uint4 c = *reinterpret_cast<const uint4*>(st + S::kK + r * D + 16 * qg + 64 * h);
+    const uint4 c = *reinterpret_cast<const uint4*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
       half2_t p0, p1, p2, p3;

@@ -462,7 +462,7 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
       int4_t kop[KCH];
 #pragma unroll
       for (int h = 0; h < KCH; ++h)
-        kop[h] = *reinterpret_cast<const int4_t*>(st + S::kK + r * D + 16 * qg + 64 * h);
+        kop[h] = *reinterpret_cast<const int4_t*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         sacc[b][t] = int4_t{0, 0, 0, 0};
@@ -479,7 +479,7 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
       for (int t = 0; t < NT; ++t) sacc[b][t] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int h = 0; h < KCH; ++h) {
-        const uint4 c = *reinterpret_cast<const uint4*>(st + S::kK + r * D + 16 * qg + 64 * h);
+        const uint4 c = *reinterpret_cast<const uint4*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
           half2_t p0, p1, p2, p3;
