@@ -298,6 +298,99 @@ __device__ __forceinline__ void load_query(const AttnArgs& a, int tok, int kvh, 
   }
 }
 
+typedef int int4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kQRange = 127 * 128;  // |Q| bound: |hi| <= 127 and |lo| <= 64 fit int8
+
+// NaN-propagating maximum (v_maximum_f32: no operand canonicalization).
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// Byte 0 of each of four words, in order, as one word (v_perm_b32: selector 0x0c
+// reads as zero).
+__device__ __forceinline__ uint32_t low_bytes(const uint32_t (&v)[4]) {
+  const uint32_t p01 = __builtin_amdgcn_perm(v[1], v[0], 0x0c0c0400u);
+  const uint32_t p23 = __builtin_amdgcn_perm(v[3], v[2], 0x04000c0cu);
+  return p01 | p23;
+}
+
+template <typename QT, int D>
+struct QueryColumn {  // the lane's 16 elements of each 64-wide d chunk, as loaded
+  uint4 w[D / 64][16 * sizeof(QT) / 16];
+};
+
+// Int8 B-operands of one query column for the QK MFMAs (lane r of its 16-lane group
+// qg holds d = 16*qg + 64*h + [0, 16)): the column is quantized once to integers
+// Q = 128 * hi + lo within 1/2 of q * kQRange / max|q|, hi and lo in int8, so that
+// K.Q = 128 (K.hi) + K.lo is exact in int32 (a ~15-bit query, finer than f16's 11 bits
+// for every element within 2^-4 of the column maximum).
+// Returns the score factor max|q| / kQRange * qk_scale_log2 (NaN for a non-finite
+// query, which makes every score of the column non-finite as in fp32 arithmetic).
+// Cross-lane: uniform control flow.
+template <typename QT, int D>
+__device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, bool valid,
+                                                 float qk_scale_log2, int4_t (&qhi)[D / 64],
+                                                 int4_t (&qlo)[D / 64]) {
+  constexpr int kVec = 16 / (int)sizeof(QT);  // elements per 16-byte load
+  float x[D / 64][16];
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h) {
+#pragma unroll
+    for (int c = 0; c < 16 / kVec; ++c) {
+      const uint4 w = raw.w[h][c];
+      const QT* e = reinterpret_cast<const QT*>(&w);
+#pragma unroll
+      for (int i = 0; i < kVec; ++i) x[h][c * kVec + i] = to_float<QT>(e[i]);
+    }
+  }
+  // NaN-propagating maximum of |q| over the column (lanes r, r+16, r+32, r+48): one
+  // finiteness test covers every element
+  float mx = 0.f;
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) mx = vmax(mx, vmax(fabsf(x[h][i]), fabsf(x[h][i + 1])));
+  mx = vmax(mx, shfl_xor(mx, 16));
+  mx = vmax(mx, shfl_xor(mx, 32));
+  mx = valid ? mx : 0.f;  // an invalid column (its operands meet no output) quantizes with inv = 0
+  const bool finite = __builtin_isfinite(mx);
+  const float factor = finite ? qk_scale_log2 * (mx / (float)kQRange) : __builtin_nanf("");
+  // kQRange / mx overflows for mx below 2^-114: columns under 2^-64 are lifted by 2^64
+  // first (exact), which leaves Q unchanged
+  if (__ballot(mx > 0.f && mx < 0x1p-64f) != 0) {
+    const float up = mx > 0.f && mx < 0x1p-64f ? 0x1p64f : 1.f;
+#pragma unroll
+    for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[h][i] *= up;
+    mx *= up;
+  }
+  const float inv = (finite && mx > 0.f) ? (float)kQRange / mx : 0.f;
+  // hi = rint(q * inv / 128) and lo = rint(q * inv - 128 hi), ties to even, |hi| <= 127,
+  // |lo| <= 64: adding kRound (1.5 * 2^23, unit in the last place 1) to a value below
+  // 2^22 in magnitude rounds it to an integer held in the low mantissa bits, so the low
+  // byte of the sum's bit pattern is the two's-complement byte. Each fma rounds once.
+  constexpr float kRound = 12582912.f;
+  const float inv128 = inv * (1.f / 128.f);  // exact: a power of two
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t hb[4], lb[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float xv = x[h][4 * w + e];
+        const float th = __builtin_fmaf(xv, inv128, kRound);
+        const float hv = th - kRound;
+        const float tl = __builtin_fmaf(xv, inv, __builtin_fmaf(hv, -128.f, kRound));
+        hb[e] = __builtin_bit_cast(uint32_t, th);
+        lb[e] = __builtin_bit_cast(uint32_t, tl);
+      }
+      qhi[h][w] = (int)low_bytes(hb);
+      qlo[h][w] = (int)low_bytes(lb);
+    }
+  return factor;
+}
+
 // The G query rows of kv head kvh, token row tok, by direct-to-LDS loads into
 // `dst` as [G][D] elements of QT (16 bytes per lane, D*sizeof(QT)/16 lanes per
 // head): ceil(G*D*sizeof(QT)/1024) vector-memory instructions.
@@ -366,6 +459,37 @@ __device__ __forceinline__ float query_operand(const QueryRaw<D>& q, bool gvalid
   return qk_scale_log2 * ldexpf(1.f, ex);
 }
 
+// QK^T operands of one query row per lane for the decode kernels: int8 codes meet a
+// two-term int8 query on v_mfma_i32_16x16x64_i8 (the K codes need no conversion); FP8
+// codes, converted to f16, meet an f16 query on v_mfma_f32_16x16x32_f16.
+template <int D, int KF>
+struct QkOperand {
+  half8_t op[D / 32];
+};
+template <int D>
+struct QkOperand<D, kInt8> {
+  int4_t hi[D / 64], lo[D / 64];
+};
+
+// Builds the operand of query row r (lane layout of QueryRaw; rows r >= G are zero)
+// and returns its score factor, code scale included. Cross-lane: uniform control flow.
+template <typename QT, int D, int KF>
+__device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, float qk_scale_log2,
+                                            QkOperand<D, KF>& op) {
+  if constexpr (KF == kInt8) {
+    static_assert(sizeof(QT) == 2, "16-bit queries (fp32 queries take the exact VALU kernel)");
+    QueryColumn<QT, D> col;
+#pragma unroll
+    for (int h = 0; h < D / 64; ++h) {
+      col.w[h][0] = q.w[h][0];
+      col.w[h][1] = q.w[h][1];
+    }
+    return query_column_i8<QT, D>(col, gvalid, qk_scale_log2, op.hi, op.lo);
+  } else {
+    return query_operand<QT, D>(q, gvalid, qk_scale_log2, op.op) * code_scale<KF>();
+  }
+}
+
 // ---- one staged 16-token block through the MFMAs
 //   S^T[t][g] = K[t][:] . Q[g][:]     4 (D/32) x v_mfma_f32_16x16x32_f16
 //   O^T[d][g] += V^T[d][t] P^T[t][g]  8 (D/16) x v_mfma_f32_16x16x16_f16
@@ -374,7 +498,7 @@ __device__ __forceinline__ float query_operand(const QueryRaw<D>& q, bool gvalid
 // [kv_begin, ctx) are masked; `tok_base` is the block's first token position.
 // Cross-lane (ballots, shuffles): call in uniform control flow.
 template <int D, int G, int KF = kInt8>
-__device__ __forceinline__ void mfma_block(const char* st, const half8_t (&qop)[D / 32], float cf,
+__device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF>& qop, float cf,
                                            int tok_base, int kv_begin, int ctx, int r, int qg,
                                            float4_t (&acc)[D / 16], float& m, float& l,
                                            bool& bad_score, bool masks = false) {
@@ -383,17 +507,33 @@ __device__ __forceinline__ void mfma_block(const char* st, const half8_t (&qop)[
   constexpr int VB = D / 16;
   constexpr int NPV = D / 16;
   const bool gvalid = r < G;
-  float4_t s4 = {0.f, 0.f, 0.f, 0.f};
+  float4_t s4;
+  if constexpr (KF == kInt8) {
+    // exact int32 K.Q = 128 (K.hi) + K.lo straight from the staged codes
+    int4_t kop[KCH];
 #pragma unroll
-  for (int h = 0; h < KCH; ++h) {
-    const uint4 c = *reinterpret_cast<const uint4*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
+    for (int h = 0; h < KCH; ++h)
+      kop[h] = *reinterpret_cast<const int4_t*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
+    int4_t si = {0, 0, 0, 0};
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      half2_t p0, p1, p2, p3;
-      codes_to_f16<KF>(sub ? c.z : c.x, p0, p1);
-      codes_to_f16<KF>(sub ? c.w : c.y, p2, p3);
-      const half8_t kop = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-      s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[2 * h + sub], s4, 0, 0, 0);
+    for (int h = 0; h < KCH; ++h) si = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop.hi[h], si, 0, 0, 0);
+    si = si << 7;
+#pragma unroll
+    for (int h = 0; h < KCH; ++h) si = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop.lo[h], si, 0, 0, 0);
+    s4 = float4_t{(float)si[0], (float)si[1], (float)si[2], (float)si[3]};
+  } else {
+    s4 = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int h = 0; h < KCH; ++h) {
+      const uint4 c = *reinterpret_cast<const uint4*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        half2_t p0, p1, p2, p3;
+        codes_to_f16<KF>(sub ? c.z : c.x, p0, p1);
+        codes_to_f16<KF>(sub ? c.w : c.y, p2, p3);
+        const half8_t kop = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+        s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop.op[2 * h + sub], s4, 0, 0, 0);
+      }
     }
   }
   const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);

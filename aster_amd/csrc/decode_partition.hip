@@ -164,8 +164,8 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   if (1 < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, 1), kvh, lane, st1);
   if (NS == 3 && 2 < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, 2), kvh, lane, st2);
 
-  half8_t qop[D / 32];
-  const float cf = query_operand<QT, D>(qraw, gvalid, a.qk_scale_log2, qop) * code_scale<KF>();
+  QkOperand<D, KF> qop;
+  const float cf = qk_operand<QT, D, KF>(qraw, gvalid, a.qk_scale_log2, qop);
   float4_t acc[NPV];
 #pragma unroll
   for (int n = 0; n < NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};

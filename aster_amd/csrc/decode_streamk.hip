@@ -217,7 +217,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   // stage, issued before blocks 0 .. NS-2, so the block stream starts without
   // waiting for it; block NS-1 takes that stage once the query has been read out.
   QueryRaw<D> qr;
-  half8_t qop[D / 32];
+  QkOperand<D, KF> qop;
   float cf = 0.f;
   if (nblk > 0) {
     stage_query<QT, D, G>(a, s_tok[row0 % nseq], row0 / nseq, lane, stage(NS - 1));
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     else if (first == 2) wait_vmcnt<2 * S::kLoads>();
     else wait_vmcnt<S::kLoads>();
     lds_query<QT, D>(stage(NS - 1), gvalid ? r : 0, qg, qr);
-    cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop) * code_scale<KF>();
+    cf = qk_operand<QT, D, KF>(qr, gvalid, a.qk_scale_log2, qop);
     if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (their values are consumed)
     if (64 < nblk) request_ids(1);
   }
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     const int64_t pfb = s_cu[pseq];  // first block of the row in the per-head order
     if (i > 0) {  // a new row starts inside this wave's range
       load_query<QT, D, G>(a, s_tok[pseq], pkvh, r, qg, qr);
-      cf = query_operand<QT, D>(qr, gvalid, a.qk_scale_log2, qop) * code_scale<KF>();
+      cf = qk_operand<QT, D, KF>(qr, gvalid, a.qk_scale_log2, qop);
     }
 #pragma unroll
     for (int k = 0; k < NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};

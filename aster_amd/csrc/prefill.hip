@@ -183,9 +183,6 @@ __device__ int scan_tiles(const AttnArgs& a, int tq, int unit, int* s_wsum, int*
   return base;
 }
 
-typedef int int4_t __attribute__((ext_vector_type(4)));
-
-constexpr int kQRange = 127 * 128;  // |Q| bound: |hi| <= 127 and |lo| <= 64 fit int8
 // |S_int| <= 127 * kQRange * 256; a score factor below this keeps every score finite
 constexpr float kSafeFactor = 1.0e29f;
 // FP8 codes take the f16 QK path: |S| <= D * 2^15 * max|code as f16| (448 * 2^-8 for
@@ -196,22 +193,6 @@ constexpr float safe_factor() {
   return KF == kInt8 ? kSafeFactor : KF == kE4M3 ? kSafeFactorE4M3 : kSafeFactorE5M2;
 }
 
-// NaN-propagating maximum (v_maximum_f32: no operand canonicalization).
-__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
-
-// Byte 0 of each of four words, in order, as one word (v_perm_b32: selector 0x0c
-// reads as zero).
-__device__ __forceinline__ uint32_t low_bytes(const uint32_t (&v)[4]) {
-  const uint32_t p01 = __builtin_amdgcn_perm(v[1], v[0], 0x0c0c0400u);
-  const uint32_t p23 = __builtin_amdgcn_perm(v[3], v[2], 0x04000c0cu);
-  return p01 | p23;
-}
-
-template <typename QT, int D>
-struct QueryColumn {  // the lane's 16 elements of each 64-wide d chunk, as loaded
-  uint4 w[D / 64][16 * sizeof(QT) / 16];
-};
-
 template <typename QT, int D>
 __device__ __forceinline__ void load_query_column(const QT* qp, QueryColumn<QT, D>& raw) {
 #pragma unroll
@@ -219,79 +200,6 @@ __device__ __forceinline__ void load_query_column(const QT* qp, QueryColumn<QT, 
 #pragma unroll
     for (int c = 0; c < (int)(16 * sizeof(QT) / 16); ++c)
       raw.w[h][c] = reinterpret_cast<const uint4*>(qp + 64 * h)[c];
-}
-
-// Int8 B-operands of one query column for the QK MFMAs (lane r of its 16-lane group
-// qg holds d = 16*qg + 64*h + [0, 16)): the column is quantized once to integers
-// Q = 128 * hi + lo within 1/2 of q * kQRange / max|q|, hi and lo in int8, so that
-// K.Q = 128 (K.hi) + K.lo is exact in int32 (a ~15-bit query, finer than f16's 11 bits
-// for every element within 2^-4 of the column maximum).
-// Returns the score factor max|q| / kQRange * qk_scale_log2 (NaN for a non-finite
-// query, which makes every score of the column non-finite as in fp32 arithmetic).
-// Cross-lane: uniform control flow.
-template <typename QT, int D>
-__device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, bool valid,
-                                                 float qk_scale_log2, int4_t (&qhi)[D / 64],
-                                                 int4_t (&qlo)[D / 64]) {
-  constexpr int kVec = 16 / (int)sizeof(QT);  // elements per 16-byte load
-  float x[D / 64][16];
-#pragma unroll
-  for (int h = 0; h < D / 64; ++h) {
-#pragma unroll
-    for (int c = 0; c < 16 / kVec; ++c) {
-      const uint4 w = raw.w[h][c];
-      const QT* e = reinterpret_cast<const QT*>(&w);
-#pragma unroll
-      for (int i = 0; i < kVec; ++i) x[h][c * kVec + i] = to_float<QT>(e[i]);
-    }
-  }
-  // NaN-propagating maximum of |q| over the column (lanes r, r+16, r+32, r+48): one
-  // finiteness test covers every element
-  float mx = 0.f;
-#pragma unroll
-  for (int h = 0; h < D / 64; ++h)
-#pragma unroll
-    for (int i = 0; i < 16; i += 2) mx = vmax(mx, vmax(fabsf(x[h][i]), fabsf(x[h][i + 1])));
-  mx = vmax(mx, shfl_xor(mx, 16));
-  mx = vmax(mx, shfl_xor(mx, 32));
-  mx = valid ? mx : 0.f;  // an invalid column (its operands meet no output) quantizes with inv = 0
-  const bool finite = __builtin_isfinite(mx);
-  const float factor = finite ? qk_scale_log2 * (mx / (float)kQRange) : __builtin_nanf("");
-  // kQRange / mx overflows for mx below 2^-114: columns under 2^-64 are lifted by 2^64
-  // first (exact), which leaves Q unchanged
-  if (__ballot(mx > 0.f && mx < 0x1p-64f) != 0) {
-    const float up = mx > 0.f && mx < 0x1p-64f ? 0x1p64f : 1.f;
-#pragma unroll
-    for (int h = 0; h < D / 64; ++h)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) x[h][i] *= up;
-    mx *= up;
-  }
-  const float inv = (finite && mx > 0.f) ? (float)kQRange / mx : 0.f;
-  // hi = rint(q * inv / 128) and lo = rint(q * inv - 128 hi), ties to even, |hi| <= 127,
-  // |lo| <= 64: adding kRound (1.5 * 2^23, unit in the last place 1) to a value below
-  // 2^22 in magnitude rounds it to an integer held in the low mantissa bits, so the low
-  // byte of the sum's bit pattern is the two's-complement byte. Each fma rounds once.
-  constexpr float kRound = 12582912.f;
-  const float inv128 = inv * (1.f / 128.f);  // exact: a power of two
-#pragma unroll
-  for (int h = 0; h < D / 64; ++h)
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      uint32_t hb[4], lb[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float xv = x[h][4 * w + e];
-        const float th = __builtin_fmaf(xv, inv128, kRound);
-        const float hv = th - kRound;
-        const float tl = __builtin_fmaf(xv, inv, __builtin_fmaf(hv, -128.f, kRound));
-        hb[e] = __builtin_bit_cast(uint32_t, th);
-        lb[e] = __builtin_bit_cast(uint32_t, tl);
-      }
-      qhi[h][w] = (int)low_bytes(hb);
-      qlo[h][w] = (int)low_bytes(lb);
-    }
-  return factor;
 }
 
 // Query operands of one column tile: two int8 terms per 64-wide d chunk for int8 codes
