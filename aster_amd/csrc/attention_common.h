@@ -270,6 +270,27 @@ __device__ __forceinline__ half2_t column_pair(uint32_t r0, uint32_t r1) {
   }
 }
 
+// INT8 V operands of the decode kernels carry the code plus kVBias (exact in f16): the
+// byte permute and XOR build 1152 + c directly, and the PV accumulators drop
+// kVBias * sum_k(weight_k) once per piece (remove_v_bias) instead of every code paying
+// for a subtraction.
+constexpr float kVBias = 1152.f;
+// Where the decode kernels use them: INT8 codes at D <= 128 (at D = 256 the weight-sum
+// tile would take the partitioned kernel past 2 waves per SIMD).
+template <int D, int KF>
+constexpr bool biased_v() { return KF == kInt8 && D <= 128; }
+template <int K>
+__device__ __forceinline__ half2_t column_pair_biased(uint32_t r0, uint32_t r1) {
+  constexpr uint32_t sel = 0x0C000C00u | ((4u + K) << 16) | K;
+  return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(r1, r0, sel) ^ 0x64806480u);  // 1152 + c
+}
+template <int K>
+__device__ __forceinline__ half4_t v_operand_biased(const uint32_t (&v)[4]) {
+  const half2_t a01 = column_pair_biased<K>(v[0], v[1]);
+  const half2_t a23 = column_pair_biased<K>(v[2], v[3]);
+  return half4_t{a01[0], a01[1], a23[0], a23[1]};
+}
+
 template <int K, int KF = kInt8>
 __device__ __forceinline__ half4_t v_operand(const uint32_t (&v)[4]) {
   const half2_t a01 = column_pair<K, KF>(v[0], v[1]);
@@ -493,6 +514,8 @@ __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, f
 // ---- one staged 16-token block through the MFMAs
 //   S^T[t][g] = K[t][:] . Q[g][:]     4 (D/32) x v_mfma_f32_16x16x32_f16
 //   O^T[d][g] += V^T[d][t] P^T[t][g]  8 (D/16) x v_mfma_f32_16x16x16_f16
+// acc[D/16] is one more tile: with biased V operands (biased_v), a row of ones times
+// P^T, whose row 0 sums the rounded weights for remove_v_bias.
 // The S^T output layout (lane l: tokens 4*(l/16)+j of head l%16) is the B-operand
 // layout P^T needs, so the online softmax stays in registers. Tokens outside
 // [kv_begin, ctx) are masked; `tok_base` is the block's first token position.
@@ -500,7 +523,7 @@ __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, f
 template <int D, int G, int KF = kInt8>
 __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF>& qop, float cf,
                                            int tok_base, int kv_begin, int ctx, int r, int qg,
-                                           float4_t (&acc)[D / 16], float& m, float& l,
+                                           float4_t (&acc)[D / 16 + 1], float& m, float& l,
                                            bool& bad_score, bool masks = false) {
   using S = Stage<D>;
   constexpr int KCH = D / 64;
@@ -586,7 +609,7 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
     const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
     l *= alpha;
 #pragma unroll
-    for (int n = 0; n < NPV; ++n) acc[n] *= alpha;
+    for (int n = 0; n <= NPV; ++n) acc[n] *= alpha;
     m = mn;
   }
   half4_t pop;
@@ -601,13 +624,38 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
   for (int n = 0; n < NPV; ++n) {
     const uint32_t col[4] = {vw[0][n / 4], vw[1][n / 4], vw[2][n / 4], vw[3][n / 4]};
     half4_t vop;
-    switch (n % 4) {
-      case 0: vop = v_operand<0, KF>(col); break;
-      case 1: vop = v_operand<1, KF>(col); break;
-      case 2: vop = v_operand<2, KF>(col); break;
-      default: vop = v_operand<3, KF>(col); break;
+    if constexpr (biased_v<D, KF>()) {
+      switch (n % 4) {
+        case 0: vop = v_operand_biased<0>(col); break;
+        case 1: vop = v_operand_biased<1>(col); break;
+        case 2: vop = v_operand_biased<2>(col); break;
+        default: vop = v_operand_biased<3>(col); break;
+      }
+    } else {
+      switch (n % 4) {
+        case 0: vop = v_operand<0, KF>(col); break;
+        case 1: vop = v_operand<1, KF>(col); break;
+        case 2: vop = v_operand<2, KF>(col); break;
+        default: vop = v_operand<3, KF>(col); break;
+      }
     }
     acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop, pop, acc[n], 0, 0, 0);
+  }
+  if constexpr (biased_v<D, KF>()) {
+    const _Float16 one = r == 0 ? (_Float16)1.f : (_Float16)0.f;
+    acc[NPV] = __builtin_amdgcn_mfma_f32_16x16x16f16(half4_t{one, one, one, one}, pop, acc[NPV], 0, 0, 0);
+  }
+}
+
+// Ends a piece's accumulation: with biased V operands, subtracts kVBias times the
+// weight sum of head r (row 0 of acc[D/16], held by lane (0, r)) from every output of
+// that head. Cross-lane: call in uniform control flow.
+template <int D, int KF>
+__device__ __forceinline__ void remove_v_bias(float4_t (&acc)[D / 16 + 1], int r) {
+  if constexpr (biased_v<D, KF>()) {
+    const float b = kVBias * __shfl(acc[D / 16][0], r, kWave);
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) acc[n] -= float4_t{b, b, b, b};
   }
 }
 

@@ -166,9 +166,9 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
 
   QkOperand<D, KF> qop;
   const float cf = qk_operand<QT, D, KF>(qraw, gvalid, a.qk_scale_log2, qop);
-  float4_t acc[NPV];
+  float4_t acc[NPV + 1];  // [NPV]: weight sums (INT8)
 #pragma unroll
-  for (int n = 0; n < NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int n = 0; n <= NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
   // invalid head columns never contribute; a finite start makes a block whose keys are
   // all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
   float m = gvalid ? -FLT_MAX : 0.f;
@@ -199,6 +199,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
 
   // ---- per-wave state to LDS (aliases the stages: wait for every wave first)
+  remove_v_bias<D, KF>(acc, r);
   l += shfl_xor(l, 16);
   l += shfl_xor(l, 32);
   l *= norm_scale<KF>();  // the factor the PV weights carry

@@ -234,7 +234,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
 
   // ---- 3. stream the blocks, one piece (the run of one row's blocks) at a time;
   // block i sits in stage i % NS and block i + NS is issued into it once consumed
-  float4_t acc[NPV];
+  float4_t acc[NPV + 1];  // [NPV]: weight sums (INT8)
   float m = 0.f, l = 0.f;
   bool bad_score = false;
   const bool masks = a.cache.key_valid != nullptr;
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
       cf = qk_operand<QT, D, KF>(qr, gvalid, a.qk_scale_log2, qop);
     }
 #pragma unroll
-    for (int k = 0; k < NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k <= NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
     // invalid head columns never contribute; a finite start makes a block whose keys
     // are all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
     m = gvalid ? -FLT_MAX : 0.f;
@@ -292,6 +292,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     // wave, else a partial in slot 0 (the piece starts the wave's range) or 1 (it
     // ends it)
     const int iend = i;
+    remove_v_bias<D, KF>(acc, r);
     float lt = l + shfl_xor(l, 16);
     lt += shfl_xor(lt, 32);
     lt *= norm_scale<KF>();  // the factor the PV weights carry
