@@ -181,9 +181,10 @@ int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query, int32
  *   astr_paged_attention_i8_workspace_bytes for num_seqs rows; chunk rows need none).
  * Sequences with one query token take the decode kernels (the query sees every
  * key, as for astr_paged_attention_i8), longer ones the MFMA prefill kernel
- * (bf16/fp16/fp32 queries; fp32 queries enter the f16 MFMAs after an exact
- * power-of-two rescale, i.e. rounded to 11 significant bits), launched after
- * the decode kernels on the same stream.
+ * (bf16/fp16/fp32 queries; with int8 codes a query column enters the int8 QK
+ * MFMAs as integers within 1/2 of q * 16256 / max|q|, with FP8 codes it is
+ * rounded to f16 after an exact power-of-two rescale), launched after the
+ * decode kernels on the same stream.
  */
 int astr_paged_attention_varlen_i8(const astr_paged_kv* cache, const void* query,
                                    int32_t q_dtype, int64_t q_token_stride,
