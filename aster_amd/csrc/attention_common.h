@@ -445,9 +445,9 @@ __device__ __forceinline__ void lds_query(const char* buf, int g, int qg, QueryR
   }
 }
 
-// f16 B-operands of the QK MFMAs after an exact 2^-e rescale keeping max|q| below
-// 2^15 (e folded into the returned score factor). Cross-lane: call in uniform
-// control flow.
+// f16 B-operands of the QK MFMAs (FP8 codes) after an exact 2^-e rescale keeping
+// max|q| below 2^15 (e folded into the returned score factor). Cross-lane: call in
+// uniform control flow.
 template <typename QT, int D>
 __device__ __forceinline__ float query_operand(const QueryRaw<D>& q, bool gvalid,
                                                float qk_scale_log2, half8_t (&qop)[D / 32]) {
@@ -512,7 +512,9 @@ __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, f
 }
 
 // ---- one staged 16-token block through the MFMAs
-//   S^T[t][g] = K[t][:] . Q[g][:]     4 (D/32) x v_mfma_f32_16x16x32_f16
+//   S^T[t][g] = K[t][:] . Q[g][:]     INT8 codes: 2 (D/64) x 2 v_mfma_i32_16x16x64_i8
+//                                     (hi, then lo on the hi result shifted by 7);
+//                                     FP8 codes: 4 (D/32) x v_mfma_f32_16x16x32_f16
 //   O^T[d][g] += V^T[d][t] P^T[t][g]  8 (D/16) x v_mfma_f32_16x16x16_f16
 // acc[D/16] is one more tile: with biased V operands (biased_v), a row of ones times
 // P^T, whose row 0 sums the rounded weights for remove_v_bias.
