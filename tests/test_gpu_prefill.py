@@ -213,3 +213,33 @@ def test_invalid_offsets_and_short_context_are_flagged(device):
         _run(cache, w, q, tables, short, qsl)
     out = _run(cache, w, q, tables, lens, qsl)  # the flag was cleared by the raise
     assert_attention_close(out, oracle_decode(w, cache, q))
+
+
+@pytest.mark.parametrize("case", range(48))
+def test_random_mixed_steps_match_oracle(device, case):
+    """Seeded random mixed steps: head dim, GQA group, query dtype, decode/chunk/empty
+    rows, causal or not, sliding window, split mode, code format and key padding drawn
+    per case, each against the oracle at the north_star tolerance."""
+    rng = np.random.default_rng(7000 + case)
+    dim = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.choice([1, 2, 4, 8, 16] if dim != 256 else [1, 2, 4, 8]))
+    qdtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(3))]
+    if qdtype == torch.float32:
+        g = min(g, 8)  # fp32 decode rows run the exact VALU kernel (groups up to 8)
+    nrows = int(rng.integers(1, 24))
+    q_lens = np.where(rng.random(nrows) < 0.6, 1, rng.integers(2, 160, nrows)).astype(np.int32)
+    q_lens[rng.random(nrows) < 0.05] = 0
+    ctx = (q_lens + rng.integers(0, 900, nrows)).astype(np.int32)
+    window = None if rng.random() < 0.6 else int(rng.integers(1, 400))
+    causal = bool(rng.random() < 0.85)
+    part = int(rng.choice([0, 0, 512, 64]))
+    fmt = ["int8", "int8", "int8", "fp8_e4m3fn", "fp8_e5m2"][int(rng.integers(5))]
+    w = _mixed(q_lens, ctx, hq=hkv * g, hkv=hkv, dim=dim, qdtype=qdtype, seed=9000 + case)
+    cache, tables, lens, qsl = _build(w, device, fmt)
+    if rng.random() < 0.3:
+        mark_padding(cache, w.block_tables, w.context_lens, 0.15, seed=case)
+    q = wl.queries(w, device)
+    out = _run(cache, w, q, tables, lens, qsl, causal=causal, window=window,
+               partition_tokens=part)
+    assert_attention_close(out, oracle_decode(w, cache, q, causal=causal, window=window))
