@@ -323,8 +323,10 @@ typedef int int4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kQRange = 127 * 128;  // |Q| bound: |hi| <= 127 and |lo| <= 64 fit int8
 
-// NaN-propagating maximum (v_maximum_f32: no operand canonicalization).
+// NaN-propagating maximum and minimum (v_maximum_f32 / v_minimum_f32: no operand
+// canonicalization).
 __device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float vmin(float a, float b) { return __builtin_elementwise_minimum(a, b); }
 
 // Byte 0 of each of four words, in order, as one word (v_perm_b32: selector 0x0c
 // reads as zero).
@@ -591,16 +593,27 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
   const bool edge = tok_base < kv_begin || tok_base + kBlockTokens > ctx || padded;
   float sc[4];
   bool need = false, nonfinite = false;
+  if (edge) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float v = s4[j] * (ks[j] * cf);
-    bool valid = gvalid;
-    if (edge)
-      valid = valid && tok0 + j >= kv_begin && tok0 + j < ctx && (!masks || st[S::kF + 4 * qg + j] != 0);
-    nonfinite |= valid && !__builtin_isfinite(v);
-    v = valid ? v : -INFINITY;
-    need |= v > m + kRescaleSlack;
-    sc[j] = v;
+    for (int j = 0; j < 4; ++j) {
+      float v = s4[j] * (ks[j] * cf);
+      const bool valid = gvalid && tok0 + j >= kv_begin && tok0 + j < ctx &&
+                         (!masks || st[S::kF + 4 * qg + j] != 0);
+      nonfinite |= valid && !__builtin_isfinite(v);
+      v = valid ? v : -INFINITY;
+      need |= v > m + kRescaleSlack;
+      sc[j] = v;
+    }
+  } else {
+    // every key of the block is visible: a NaN-propagating maximum and minimum of the
+    // four scores stand for the per-score finiteness and rescale tests. Head columns
+    // r >= G (zero query, finite zero scores) feed no output and test nothing.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sc[j] = s4[j] * (ks[j] * cf);
+    const float hi = vmax(vmax(sc[0], sc[1]), vmax(sc[2], sc[3]));
+    const float lo = vmin(vmin(sc[0], sc[1]), vmin(sc[2], sc[3]));
+    nonfinite = gvalid && !(__builtin_isfinite(hi) && __builtin_isfinite(lo));
+    need = gvalid && hi > m + kRescaleSlack;
   }
   if (__ballot(nonfinite) != 0) bad_score = true;
   if (__ballot(need) != 0) {
