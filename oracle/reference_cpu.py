@@ -394,6 +394,9 @@ def paged_attention(query, k_codes, k_scales, v_codes, v_scales, block_tables, c
                                scale=scale, query_block_size=query_block_size,
                                key_block_size=key_block_size)
         outputs.append(out[0].transpose(1, 0, 2))
+    if not outputs:  # no sequence has a query token this step
+        acc = np.float64 if query.dtype == np.float64 else np.float32
+        return np.zeros((0, query.shape[1], v_codes.shape[-1]), dtype=acc)
     return np.concatenate(outputs, 0)
 
 

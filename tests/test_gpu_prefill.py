@@ -127,6 +127,17 @@ def test_tiny_query_heads(device):
     assert_attention_close(out, oracle_decode(w, cache, q))
 
 
+def test_step_without_query_tokens(device):
+    """Rows with no query token this step (and a step where no row has one) write
+    nothing and raise nothing."""
+    w = _mixed([0, 0, 0], [40, 0, 300], hq=32, hkv=8, dim=128, seed=64)
+    cache, tables, lens, qsl = _build(w, device)
+    q = wl.queries(w, device)
+    out = _run(cache, w, q, tables, lens, qsl)
+    assert out.shape == (0, 32, 128)
+    assert_attention_close(out, oracle_decode(w, cache, q))
+
+
 def test_non_causal_without_window(device):
     w = _mixed(Q_LENS, CTX, seed=6)
     cache, tables, lens, qsl = _build(w, device)

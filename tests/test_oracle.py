@@ -326,6 +326,26 @@ def test_paged_oracle_invariant_to_physical_block_permutation():
         g["context_lens"], block_size=16, scale=64 ** -0.5))
 
 
+def test_paged_oracle_step_without_query_tokens():
+    """Rows that carry no query token this step produce no output rows; a step where
+    no row does returns an empty [0, Hq, Dv] array."""
+    g = _config1()
+    n = len(g["context_lens"])
+    out = ref.paged_attention(g["q"][:0], g["k_codes"], g["k_scales"], g["v_codes"],
+                              g["v_scales"], g["block_tables"], g["context_lens"], block_size=16,
+                              scale=64 ** -0.5, query_lens=[0] * n)
+    assert out.shape == (0, g["q"].shape[1], g["v_codes"].shape[-1])
+    one = [0] * n
+    one[2] = 1
+    out = ref.paged_attention(g["q"][2:3], g["k_codes"], g["k_scales"], g["v_codes"],
+                              g["v_scales"], g["block_tables"], g["context_lens"], block_size=16,
+                              scale=64 ** -0.5, query_lens=one)
+    whole = ref.paged_attention(g["q"], g["k_codes"], g["k_scales"], g["v_codes"], g["v_scales"],
+                                g["block_tables"], g["context_lens"], block_size=16,
+                                scale=64 ** -0.5)
+    np.testing.assert_array_equal(out, whole[2:3])
+
+
 def test_runner_order_equivalence_chunk_block_vs_appended_page():
     """The reference attends old pages plus the quantized chunk as a separate block and
     appends afterwards (paged_attention.py:185-229); appending first and attending
