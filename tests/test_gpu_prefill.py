@@ -138,6 +138,23 @@ def test_step_without_query_tokens(device):
     assert_attention_close(out, oracle_decode(w, cache, q))
 
 
+@pytest.mark.parametrize("bad", [float("inf"), float("nan")])
+@pytest.mark.parametrize("row_kind", ["decode", "chunk"])
+@pytest.mark.parametrize("part,qdtype", [(0, torch.bfloat16), (512, torch.bfloat16),
+                                         (0, torch.float32)])
+def test_non_finite_query_is_reported(device, bad, row_kind, part, qdtype):
+    """A non-finite query element makes that head's scores non-finite, which the
+    reference rejects (online_attention.py:193-196): the call raises ValueError, from a
+    decode row (its interior and edge blocks) and from a chunk row alike."""
+    w = _mixed(Q_LENS, CTX, hq=32, hkv=8, dim=128, qdtype=qdtype, seed=65)
+    cache, tables, lens, qsl = _build(w, device)
+    q = wl.queries(w, device)
+    tok = 33 if row_kind == "decode" else 10  # row 2 (context 300) / a token of row 1's chunk
+    q[tok, 5, 17] = bad
+    with pytest.raises(ValueError, match="score overflow"):
+        _run(cache, w, q, tables, lens, qsl, partition_tokens=part)
+
+
 def test_non_causal_without_window(device):
     w = _mixed(Q_LENS, CTX, seed=6)
     cache, tables, lens, qsl = _build(w, device)
