@@ -140,14 +140,16 @@ def test_step_without_query_tokens(device):
 
 @pytest.mark.parametrize("bad", [float("inf"), float("nan")])
 @pytest.mark.parametrize("row_kind", ["decode", "chunk"])
-@pytest.mark.parametrize("part,qdtype", [(0, torch.bfloat16), (512, torch.bfloat16),
-                                         (0, torch.float32)])
-def test_non_finite_query_is_reported(device, bad, row_kind, part, qdtype):
+@pytest.mark.parametrize("part,qdtype,fmt", [(0, torch.bfloat16, "int8"),
+                                             (512, torch.bfloat16, "int8"),
+                                             (0, torch.float32, "int8"),
+                                             (0, torch.bfloat16, "fp8_e4m3fn")])
+def test_non_finite_query_is_reported(device, bad, row_kind, part, qdtype, fmt):
     """A non-finite query element makes that head's scores non-finite, which the
     reference rejects (online_attention.py:193-196): the call raises ValueError, from a
     decode row (its interior and edge blocks) and from a chunk row alike."""
     w = _mixed(Q_LENS, CTX, hq=32, hkv=8, dim=128, qdtype=qdtype, seed=65)
-    cache, tables, lens, qsl = _build(w, device)
+    cache, tables, lens, qsl = _build(w, device, fmt)
     q = wl.queries(w, device)
     tok = 33 if row_kind == "decode" else 10  # row 2 (context 300) / a token of row 1's chunk
     q[tok, 5, 17] = bad
