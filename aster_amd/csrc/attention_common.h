@@ -18,6 +18,9 @@ constexpr int kMaxBlocksPerWave = 64;  // block ids one wave keeps in a register
 // stream-K: blocks one wave may stream (its block list goes in windows of 64)
 constexpr int kMaxBlocksPerWaveSK = 1024;
 constexpr float kRescaleSlack = 8.0f;  // p = exp2(s - m) <= 2^8 between rescales
+// PV weights p * v_scale * wsc are rounded to f16: with p <= 2^8 and every
+// v_scale * wsc <= 2^7 they stay below 2^15 (f16's largest finite value is 65504).
+constexpr float kVWeightCap = 128.0f;
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
@@ -37,6 +40,7 @@ struct AttnArgs {
   // nullptr: one query token per sequence, at row s.
   const int32_t* q_start;
   int32_t num_q_tokens;  // rows of query/out (upper bound of q_start[num_seqs])
+  int32_t max_q_len;     // host-declared bound of q_start[s+1] - q_start[s] (1 without q_start)
   int32_t causal;        // multi-token rows: key k is visible to query position p iff k <= p
   int32_t num_seqs, num_q_heads;
   float qk_scale_log2;  // softmax scale * log2(e)
@@ -59,6 +63,9 @@ struct AttnArgs {
 // Query/output token rows [begin, begin + count) of sequence `seq` (count is
 // returned). A q_start entry that is negative, decreasing or beyond num_q_tokens
 // gives count 0 and raises the index flag, so no kernel indexes outside query/out.
+// So does a row longer than the declared max_q_len: the host launches the chunk
+// kernel only when that bound is 2 or more, and no kernel may leave such a row's
+// output unwritten without a flag.
 //
 // decode_token: the token row of `seq` when it carries exactly one query token
 // (a decode row), else -1: sequences with several query tokens belong to the
@@ -69,7 +76,7 @@ __device__ __forceinline__ int seq_queries(const AttnArgs& a, int seq, int& begi
     return 1;
   }
   const int b = a.q_start[seq], e = a.q_start[seq + 1];
-  if (b < 0 || e < b || e > a.num_q_tokens) {  // not a valid offset table: no rows, flagged
+  if (b < 0 || e < b || e > a.num_q_tokens || e - b > a.max_q_len) {  // no rows, flagged
     atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
     begin = 0;
     return 0;
@@ -130,19 +137,22 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
 // Direct global -> LDS loads. Each lane's 16 (or 4) bytes land at
 // M0 + lane * 16 (or 4). Issued as inline asm so the compiler does not add its
 // conservative "wait for every LDS DMA" before unrelated LDS reads; the stage
-// pipelines wait for exactly the loads they need with wait_vmcnt. M0 is a
-// reserved register the compiler sets right before each of its own uses (these
-// kernels have none besides this), so it is not listed as clobbered.
+// pipelines wait for exactly the loads they need with wait_vmcnt. Each helper
+// declares M0 as an output operand (a definition of M0 in the compiler's view), so
+// no value the compiler keeps in M0 (LDS DMA builtins, movrel indexing, M0
+// initialisations it hoists) is assumed to live across one of them.
 __device__ __forceinline__ void lds_dma_x4(const void* gptr, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :
+  int m0;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off"
+               : "={m0}"(m0)
                : "s"(lds), "v"(gptr)
                : "memory");
 }
 
 __device__ __forceinline__ void lds_dma_x1(const void* gptr, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
-               :
+  int m0;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %2, off"
+               : "={m0}"(m0)
                : "s"(lds), "v"(gptr)
                : "memory");
 }
@@ -151,15 +161,17 @@ __device__ __forceinline__ void lds_dma_x1(const void* gptr, uint32_t lds) {
 // (the saddr form: no 64-bit per-lane address to hold). No instruction offset: the
 // LDS destination is M0 + lane * 16 (or 4) exactly.
 __device__ __forceinline__ void lds_dma_x4_s(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :
+  int m0;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3"
+               : "={m0}"(m0)
                : "s"(lds), "v"(voff), "s"(sbase)
                : "memory");
 }
 
 __device__ __forceinline__ void lds_dma_x1_s(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
-               :
+  int m0;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %2, %3"
+               : "={m0}"(m0)
                : "s"(lds), "v"(voff), "s"(sbase)
                : "memory");
 }
@@ -524,11 +536,15 @@ __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, f
 // layout P^T needs, so the online softmax stays in registers. Tokens outside
 // [kv_begin, ctx) are masked; `tok_base` is the block's first token position.
 // Cross-lane (ballots, shuffles): call in uniform control flow.
+// `wsc` is the piece's weight factor (a power of two; start it at v_weight_scale<KF>()):
+// the PV weights are p * v_scale * wsc. A block whose V scales times wsc exceed
+// kVWeightCap lowers wsc by a power of two and scales the accumulators by the same
+// exact factor (f16 weights would overflow otherwise); end_piece undoes it.
 template <int D, int G, int KF = kInt8>
 __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF>& qop, float cf,
                                            int tok_base, int kv_begin, int ctx, int r, int qg,
                                            float4_t (&acc)[D / 16 + 1], float& m, float& l,
-                                           bool& bad_score, bool masks = false) {
+                                           float& wsc, bool& bad_score, bool masks = false) {
   using S = Stage<D>;
   constexpr int KCH = D / 64;
   constexpr int VB = D / 16;
@@ -564,9 +580,24 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
     }
   }
   const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
-  // V scales, times 2^8 for FP8 codes (E4M3FN operands carry 2^-8; E5M2 weights carry
-  // 2^8, as does the normaliser of this format)
-  const float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg) * v_weight_scale<KF>();
+  // V scales times the weight factor (2^8 at the start of a piece for FP8 codes:
+  // E4M3FN operands carry 2^-8; E5M2 weights carry 2^8, as does the normaliser of
+  // this format). Scales are finite and the same on the 16 lanes of a token group.
+  float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg) * wsc;
+  {
+    const float vsm = fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3]));
+    if (__ballot(vsm > kVWeightCap) != 0) {
+      float wm = fmaxf(vsm, shfl_xor(vsm, 16));
+      wm = fmaxf(wm, shfl_xor(wm, 32));
+      int e;
+      frexpf(wm * (1.f / kVWeightCap), &e);  // wm / cap in [2^(e-1), 2^e), e >= 1
+      const float f = ldexpf(1.f, -e);       // wm * f < cap
+      wsc *= f;
+      vs *= f;
+#pragma unroll
+      for (int n = 0; n <= NPV; ++n) acc[n] *= f;
+    }
+  }
   uint32_t vw[4][VB / 4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -664,13 +695,20 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
 
 // Ends a piece's accumulation: with biased V operands, subtracts kVBias times the
 // weight sum of head r (row 0 of acc[D/16], held by lane (0, r)) from every output of
-// that head. Cross-lane: call in uniform control flow.
+// that head; then undoes a lowered weight factor (exact: a power of two), so that
+// every piece's accumulators carry v_weight_scale<KF>(). Cross-lane: call in uniform
+// control flow.
 template <int D, int KF>
-__device__ __forceinline__ void remove_v_bias(float4_t (&acc)[D / 16 + 1], int r) {
+__device__ __forceinline__ void end_piece(float4_t (&acc)[D / 16 + 1], int r, float wsc) {
   if constexpr (biased_v<D, KF>()) {
     const float b = kVBias * __shfl(acc[D / 16][0], r, kWave);
 #pragma unroll
     for (int n = 0; n < D / 16; ++n) acc[n] -= float4_t{b, b, b, b};
+  }
+  if (wsc != v_weight_scale<KF>()) {
+    const float undo = v_weight_scale<KF>() / wsc;
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) acc[n] *= undo;
   }
 }
 

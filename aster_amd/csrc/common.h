@@ -135,6 +135,12 @@ constexpr int kInt8 = ASTR_KV_INT8;
 constexpr int kE4M3 = ASTR_KV_FP8_E4M3FN;
 constexpr int kE5M2 = ASTR_KV_FP8_E5M2;
 
+// Largest code magnitude of a format (KVQuantization.maximum, kv_quantization.py:23-25).
+template <int KF>
+__device__ __forceinline__ constexpr float format_max() {
+  return KF == kInt8 ? 127.f : KF == kE4M3 ? 448.f : 57344.f;
+}
+
 // The f16 conversions below give a code's value times 2^-8 for E4M3FN (its bits
 // land one exponent step of 8 apart from f16's) and the value itself otherwise;
 // code_scale undoes that (exactly: a power of two) where the scales are applied.

@@ -173,6 +173,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   // all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
   float m = gvalid ? -FLT_MAX : 0.f;
   float l = 0.f;
+  float wsc = v_weight_scale<KF>();
   bool bad_score = false;
 
   auto step = [&](int i, char* st) __attribute__((always_inline)) {
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
     else if (later == 1) wait_vmcnt<S::kLoads>();
     else wait_vmcnt<0>();
     mfma_block<D, G, KF>(st, qop, cf, (first + kWaves * i) * kBlockTokens, row.kv_begin, row.ctx, r,
-                     qg, acc, m, l, bad_score, a.cache.key_valid != nullptr);
+                     qg, acc, m, l, wsc, bad_score, a.cache.key_valid != nullptr);
     // refill this stage with block i + NS (its LDS reads above fed the MFMAs)
     if (i + NS < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, i + NS), kvh, lane, st);
   };
@@ -199,7 +200,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
 
   // ---- per-wave state to LDS (aliases the stages: wait for every wave first)
-  remove_v_bias<D, KF>(acc, r);
+  end_piece<D, KF>(acc, r, wsc);
   l += shfl_xor(l, 16);
   l += shfl_xor(l, 32);
   l *= norm_scale<KF>();  // the factor the PV weights carry

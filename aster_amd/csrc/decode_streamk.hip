@@ -255,6 +255,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     // are all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
     m = gvalid ? -FLT_MAX : 0.f;
     l = 0.f;
+    float wsc = v_weight_scale<KF>();
     const int pos0 = (psp.first_blk + (int)(b0 + i - pfb)) * kBlockTokens;
     for (;;) {
       // the row's blocks in the current window: up to the first lane with another row
@@ -265,7 +266,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
       for (; i < iend; ++i) {
         wait_block(i);
         mfma_block<D, G, KF>(stage(i), qop, cf, pos0 + (i - pstart) * kBlockTokens,
-                             psp.kv_begin, psp.ctx, r, qg, acc, m, l, bad_score, masks);
+                             psp.kv_begin, psp.ctx, r, qg, acc, m, l, wsc, bad_score, masks);
         const int nx = i + NS;
         if (nx < nblk && (nx & 63) == 0) {
           // first block of window cw + 1: its ids were requested before block
@@ -292,7 +293,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     // wave, else a partial in slot 0 (the piece starts the wave's range) or 1 (it
     // ends it)
     const int iend = i;
-    remove_v_bias<D, KF>(acc, r);
+    end_piece<D, KF>(acc, r, wsc);
     float lt = l + shfl_xor(l, 16);
     lt += shfl_xor(lt, 32);
     lt *= norm_scale<KF>();  // the factor the PV weights carry

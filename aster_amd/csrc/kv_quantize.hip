@@ -23,12 +23,6 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;  // one wave per (token, head, K|V) row
 
-// Largest code magnitude of a format (KVQuantization.maximum, kv_quantization.py:23-25).
-template <int KF>
-__device__ __forceinline__ constexpr float format_max() {
-  return KF == kInt8 ? 127.f : KF == kE4M3 ? 448.f : 57344.f;
-}
-
 // Finite c with |c| <= format_max -> FP8 bits, round to nearest even. With M mantissa
 // bits and exponent bias B: below the smallest normal 2^(1-B) the value counts
 // subnormal steps of 2^(1-B-M), rint(|c| * 2^(B-1+M)) in 0..2^M (scaling by a power of

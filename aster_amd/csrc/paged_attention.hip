@@ -210,6 +210,7 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
   AttnArgs a{};
   a.q_start = query_start_loc;
   a.num_q_tokens = query_start_loc != nullptr ? num_query_tokens : num_seqs;
+  a.max_q_len = query_start_loc != nullptr ? max_query_len : 1;
   a.causal = causal != 0;
   a.q = query;
   a.q_tok = q_token_stride;

@@ -267,20 +267,40 @@ __device__ __forceinline__ float query_column_f16(const QueryColumn<QT, D>& raw,
 // Dequantized V of one staged block as the f16 A-operands of the PV MFMAs, written
 // once by the wave that loaded the block into the slab of its block pair: half `half`
 // of entry n * 64 + lane holds, for that lane (qg, r) of every wave,
-// V[4 qg + j][r * VB + n] * v_scale[4 qg + j], j = 0..3, so that one 16-byte read at the
-// reader's own lane index gives the pair's whole operand (conflict-free). The code is
-// exact in f16 (FP8 codes times 2^-8) and multiplied by the f16-rounded scale times
-// 2^8. A block that was not loaded this step leaves stale codes and finite (or zeroed)
-// scales: finite values, which meet p = 0 for its keys.
+// V[4 qg + j][r * VB + n] * v_scale[4 qg + j] * 2^-e, j = 0..3, so that one 16-byte read
+// at the reader's own lane index gives the pair's whole operand (conflict-free). The
+// code is exact in f16 (FP8 codes times 2^-8) and multiplied by the f16-rounded scale
+// times 2^8 (times 2^-e). A slab value is at most v_scale * format_max in magnitude; the
+// block's exponent e (returned, wave-uniform) is the unit's current exponent `ve`, or
+// more when a scale exceeds `vlim` = 2^(15 + ve) / format_max, so every value stays
+// below 2^15. A block that was not loaded this step leaves stale codes and finite (or
+// zeroed) scales: finite values, which meet p = 0 for its keys.
 template <int D>
-__device__ __forceinline__ void convert_v(const char* st, int lane, int half, uint2* vt) {
+__device__ __forceinline__ int convert_v(const char* st, int lane, int half, uint2* vt, int ve,
+                                         float vlim) {
   using S = Stage<D>;
   constexpr int VB = D / 16;
   const int r = lane & 15, qg = lane >> 4;
   const float4_t vsf = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg);
   constexpr float cs = v_weight_scale<KF>();
-  const half4_t vsh = {(_Float16)(vsf[0] * cs), (_Float16)(vsf[1] * cs), (_Float16)(vsf[2] * cs),
-                       (_Float16)(vsf[3] * cs)};
+  half4_t vsh;
+  int e = ve;
+  const float vsm = fmaxf(fmaxf(vsf[0], vsf[1]), fmaxf(vsf[2], vsf[3]));
+  if (__ballot(vsm > vlim) != 0 || ve != 0) {
+    if (__ballot(vsm > vlim) != 0) {
+      float wm = fmaxf(vsm, shfl_xor(vsm, 16));
+      wm = fmaxf(wm, shfl_xor(wm, 32));
+      int x;
+      frexpf(wm * (format_max<KF>() / 32768.f), &x);  // wm * M / 2^15 in [2^(x-1), 2^x)
+      e = max(ve, __builtin_amdgcn_readfirstlane(x));
+    }
+    const float c = ldexpf(cs, -e);
+    vsh = half4_t{(_Float16)(vsf[0] * c), (_Float16)(vsf[1] * c), (_Float16)(vsf[2] * c),
+                  (_Float16)(vsf[3] * c)};
+  } else {
+    vsh = half4_t{(_Float16)(vsf[0] * cs), (_Float16)(vsf[1] * cs), (_Float16)(vsf[2] * cs),
+                  (_Float16)(vsf[3] * cs)};
+  }
   uint32_t vw[4][VB / 4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -315,6 +335,48 @@ __device__ __forceinline__ void convert_v(const char* st, int lane, int half, ui
     }
     vt[2 * (n * kWave + lane) + half] = __builtin_bit_cast(uint2, v * vsh);
   }
+  return e;
+}
+
+// The PV MFMAs of one step: weights p = exp2(u * cfe - m) rounded to f16 for the 32 keys
+// of each block pair, against the slab of that pair, and the row sums from the same
+// rounded weights. kMix: the step's blocks were converted with different exponents;
+// the weights of block b then carry 2^(e_b - ve) (vf[b], at most 1) for the numerator
+// only, so that every block's products are in units of 2^-ve.
+template <int D, int NT, bool kMix>
+__device__ __forceinline__ void prefill_pv(const uint4* vt, const float (&u)[NT][16],
+                                           const float (&cfe)[NT], const float (&m)[NT],
+                                           int lane, const half8_t& ones, const half4_t& vf,
+                                           float4_t (&acc)[NT][D / 16 + 1]) {
+  constexpr int NPV = D / 16;
+#pragma unroll
+  for (int pp = 0; pp < 2; ++pp) {
+    half8_t pop[NT], pv[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        pop[t][i] = (_Float16)__builtin_amdgcn_exp2f(fmaf(u[t][8 * pp + i], cfe[t], -m[t]));
+      if constexpr (kMix) {
+        const _Float16 f0 = vf[2 * pp], f1 = vf[2 * pp + 1];
+        pv[t] = pop[t] * half8_t{f0, f0, f0, f0, f1, f1, f1, f1};
+      } else {
+        pv[t] = pop[t];
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < NPV; ++n) {
+      const half8_t vop = __builtin_bit_cast(half8_t, vt[pp * (NPV * kWave) + n * kWave + lane]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pv[t], acc[t][n], 0, 0, 0);
+    }
+    // row sums: a V^T row of ones (row 0 of the extra tile) gives sum_k f16(p_k), the
+    // same rounded weights the numerator uses
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      acc[t][NPV] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop[t], acc[t][NPV], 0, 0, 0);
+  }
 }
 
 // One key step: the four staged 16-token blocks w = 0..3 (first key position
@@ -343,7 +405,8 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
                                              const QOp<D> (&qop)[NT],
                                              const float (&cf)[NT], const float (&cfe)[NT],
                                              const int (&lo)[NT], const int (&hi)[NT], int r,
-                                             int qg, const half8_t& ones,
+                                             int qg, const half8_t& ones, bool vmix,
+                                             const half4_t& vf,
                                              float4_t (&acc)[NT][D / 16 + 1], float (&m)[NT],
                                              bool& bad_score) {
   using S = Stage<D>;
@@ -465,28 +528,12 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
       m[t] = mn;
     }
   }
+  static_assert(NBK == 4, "two block pairs per step");
   const int lane = qg * 16 + r;
-#pragma unroll
-  for (int pp = 0; pp < NBK / 2; ++pp) {
-    half8_t pop[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        pop[t][i] = (_Float16)__builtin_amdgcn_exp2f(fmaf(u[t][8 * pp + i], cfe[t], -m[t]));
-#pragma unroll
-    for (int n = 0; n < NPV; ++n) {
-      const half8_t vop = __builtin_bit_cast(half8_t, vt[pp * (NPV * kWave) + n * kWave + lane]);
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[t], acc[t][n], 0, 0, 0);
-    }
-    // row sums: a V^T row of ones (row 0 of the extra tile) gives sum_k f16(p_k), the
-    // same rounded weights the numerator uses
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-      acc[t][NPV] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop[t], acc[t][NPV], 0, 0, 0);
-  }
+  if (vmix)
+    prefill_pv<D, NT, true>(vt, u, cfe, m, lane, ones, vf, acc);
+  else
+    prefill_pv<D, NT, false>(vt, u, cfe, m, lane, ones, vf, acc);
 }
 
 // N consecutive outputs from fp32, with 16-byte (or 8-byte) stores.
@@ -538,6 +585,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   __shared__ uint4 vt[kWaves / 2][VB * kWave];  // the current step's V operands, one slab per pair
   __shared__ int s_wsum[kWaves];
   __shared__ int s_found[2];
+  __shared__ __attribute__((aligned(16))) int s_vexp[kWaves];  // the step's block exponents
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
@@ -689,6 +737,10 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     for (int k = 0; k <= NPV; ++k) acc[t][k] = float4_t{0.f, 0.f, 0.f, 0.f};
     m[t] = -FLT_MAX;  // finite start: fully masked blocks give exp2(-inf) = 0
   }
+  // The PV accumulators are in units of 2^-ve: ve is the largest block exponent so far
+  // (0 unless a block's V scales need more, see convert_v); vlim is its scale limit.
+  int ve = 0;
+  float vlim = 32768.f / format_max<KF>();
 
   for (int i = 0; i < nsteps; ++i) {
     const int ahead = i + NB - 1;
@@ -710,8 +762,36 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     char* const cur = buffer(i);
     // this wave's block of step i is in; its V operands go to the wave's slab (the
     // previous step's readers are past the barrier that ended that step)
-    convert_v<D>(cur + wave * S::kBytes, lane, wave % 2, reinterpret_cast<uint2*>(vt[wave / 2]));
+    const int eb = convert_v<D>(cur + wave * S::kBytes, lane, wave % 2,
+                                reinterpret_cast<uint2*>(vt[wave / 2]), ve, vlim);
+    if (lane == 0) s_vexp[wave] = eb;
     __syncthreads();  // every wave's block of step i has landed and been converted
+    // the step's block exponents (each at least ve): a larger one becomes the new ve
+    // (the PV tiles, not the row sums, scale by the exact 2^(ve_old - ve)); blocks
+    // converted below ve weigh their products by 2^(e_b - ve)
+    bool vmix = false;
+    half4_t vf = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+    {
+      const int4_t ev = *reinterpret_cast<const int4_t*>(s_vexp);
+      int e4[kWaves];
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) e4[w] = __builtin_amdgcn_readfirstlane(ev[w]);
+      const int emax = max(max(e4[0], e4[1]), max(e4[2], e4[3]));
+      if (emax != ve) {
+        const float down = ldexpf(1.f, ve - emax);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int n = 0; n < NPV; ++n) acc[t][n] *= down;
+        ve = emax;
+        vlim = ldexpf(32768.f / format_max<KF>(), ve);
+      }
+      vmix = e4[0] != ve || e4[1] != ve || e4[2] != ve || e4[3] != ve;
+      if (vmix) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) vf[w] = (_Float16)ldexpf(1.f, e4[w] - ve);
+      }
+    }
     {
       const int kb0 = (b_lo + i * kWaves) * kBlockTokens;
       const int kend = b_hi * kBlockTokens;
@@ -725,7 +805,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
       }
       if (use != 0)
         prefill_step<D, NT>(cur, vt[0], use, bounded & use, masks, kb0, qop, cf, cfe, lo, hi, r, qg,
-                            ones, acc, m, bad_score);
+                            ones, vmix, vf, acc, m, bad_score);
     }
     __syncthreads();  // step i's stage may be refilled
   }
@@ -737,7 +817,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   for (int t = 0; t < NT; ++t) {
     const float lt = __shfl(acc[t][NPV][0], r, kWave);  // row 0 of the sum tile: lane (0, r)
     if (!cvalid[t]) continue;
-    const float inv = 1.f / fmaxf(lt, FLT_MIN);
+    const float inv = ldexpf(1.f, ve) / fmaxf(lt, FLT_MIN);  // the PV tiles carry 2^-ve
     QT* op = static_cast<QT*>(a.out) + (int64_t)(q0 + ctok[t]) * a.o_tok +
              (int64_t)chead[t] * a.o_head;
 #pragma unroll

@@ -347,11 +347,19 @@ class PagedKVCache:
             raise ValueError("Invalid causal/window semantics")
         if out is None:
             out = torch.empty_like(query)
+        elif (not isinstance(out, torch.Tensor) or out.shape != query.shape
+              or out.dtype != query.dtype or out.device != self.device or out.stride(-1) != 1):
+            raise ValueError("out must match the query's shape, dtype and device, with "
+                             "contiguous rows")
         need = self.workspace_bytes(num_seqs, num_q_heads, max_context_len, partition_tokens)
         if need and workspace is None:
             workspace = self.workspace(num_seqs, num_q_heads, max_context_len, partition_tokens)
-        elif need and workspace.numel() * workspace.element_size() < need:
-            raise ValueError(f"workspace of {need} bytes required")
+        elif need:
+            if (not isinstance(workspace, torch.Tensor) or workspace.dtype != torch.uint8
+                    or workspace.device != self.device or not workspace.is_contiguous()):
+                raise ValueError("workspace must be a contiguous uint8 tensor on the cache device")
+            if workspace.numel() < need:
+                raise ValueError(f"workspace of {need} bytes required")
         stream = torch.cuda.current_stream(self.device).cuda_stream
         ws = workspace.data_ptr() if need else None
         lib = _native.lib()

@@ -19,6 +19,12 @@ once the step is done.
 
 Free pages are taken lowest index first, like the reference's scan (state.py:312-314),
 from a heap instead of a scan over every page.
+
+Construction follows the reference (state.py:169-180): ``PagedStatePool(*, block_size,
+max_blocks, codec, quantization)`` knows no layer shape, and the arena is allocated
+at the first append from its leaves (layers, kv heads, head dim, device), which also
+locks the layout the way the reference's first append locks its leaf signature
+(state.py:297-300). A pool can also wrap an existing ``PagedKVCache``.
 """
 
 from __future__ import annotations
@@ -31,7 +37,8 @@ import threading
 
 import torch
 
-from .kv_quantization import QuantizedKV, require_format
+from .attention_backend import UnsupportedAttentionBackend
+from .kv_quantization import KVQuantization, QuantizedKV, require_format
 
 
 class StateError(RuntimeError):
@@ -43,6 +50,21 @@ class CacheCapacityError(StateError):
 
 
 @dataclass(frozen=True)
+class KVStateCodec:
+    """The pool's state tag (the reference's ``KVStateCodec``, state.py:45-62, of which
+    the arena pool needs only the kind): K/V leaves per layer with the token axis at
+    dimension 2. Any object with a ``kind`` attribute (the reference's codec too) can be
+    passed as ``codec``."""
+
+    kind: str = "dense_kv"
+    sequence_dim: int = 2
+
+    def __post_init__(self):
+        if self.kind not in {"dense_kv", "gqa_kv", "mla_latent_rope", "mla_latent", "indexed_mla"}:
+            raise ValueError("An explicit supported KV codec tag is required")
+
+
+@dataclass(frozen=True)
 class PageRef:
     index: int
     generation: int
@@ -50,10 +72,12 @@ class PageRef:
 
 @dataclass
 class _Page:
+    index: int = 0
     generation: int = 0
     owners: int = 0
     readers: int = 0
     valid: int = 0
+    free: bool = True  # on the free heap
 
 
 @dataclass
@@ -105,14 +129,45 @@ class SlotReservation:
 class PagedStatePool:
     evidence_kind = "hip_arena_storage"
 
-    def __init__(self, cache, *, kind="gqa_kv"):
-        require_format(cache.quantization)
+    def __init__(self, cache=None, *, block_size=16, max_blocks=256, codec=None,
+                 quantization=None, kind=None, device=None):
+        if cache is not None:
+            require_format(cache.quantization)
+            if quantization is not None and quantization != cache.quantization:
+                raise ValueError("quantization differs from the arena's format")
+            block_size, max_blocks = cache.block_size, cache.num_blocks
+            quantization = cache.quantization
+        if type(block_size) is not int or type(max_blocks) is not int or block_size < 1 \
+                or max_blocks < 1:
+            raise ValueError("Cache capacities must be positive")
+        if quantization is None:
+            raise UnsupportedAttentionBackend(
+                "hip_int8_paged pools store quantized codes: pass an explicit KVQuantization "
+                "('int8', 'fp8_e4m3fn' or 'fp8_e5m2')")
+        if not isinstance(quantization, KVQuantization):
+            raise ValueError("An explicit immutable KVQuantization profile is required")
+        require_format(quantization)
+        if block_size != 16:
+            raise UnsupportedAttentionBackend("hip_int8_paged kernels use 16-token blocks")
+        if codec is None:
+            codec = KVStateCodec(kind=kind or "gqa_kv")
+        elif kind is not None and kind != codec.kind:
+            raise ValueError("codec and kind disagree")
+        if codec.kind not in {"dense_kv", "gqa_kv"} or getattr(codec, "sequence_dim", 2) != 2 \
+                or getattr(codec, "sequence_dims", None):
+            raise UnsupportedAttentionBackend(
+                f"hip_int8_paged pools hold per-layer K/V leaves [1, Hkv, T, D]; codec kind "
+                f"{codec.kind!r} is not served")
+        self.codec, self.kind = codec, codec.kind
         self.cache = cache
-        self.block_size, self.max_blocks = cache.block_size, cache.num_blocks
-        self.kind = kind
-        self._pages = [_Page() for _ in range(self.max_blocks)]
+        self.block_size, self.max_blocks = block_size, max_blocks
+        self._quantization = quantization
+        self._device = torch.device(device) if device is not None else None
+        self._pages = [_Page(index=i) for i in range(self.max_blocks)]
         self._free = list(range(self.max_blocks))  # a sorted list is a valid heap
         self._lock = threading.RLock()
+        # the arena's layout lock: (layers, kv heads, head dim, input dtype, padding leaf)
+        self._signature = None
 
     @classmethod
     def with_arena(cls, *, num_layers, num_kv_heads, head_dim, block_size=16, max_blocks=256,
@@ -125,7 +180,33 @@ class PagedStatePool:
 
     @property
     def quantization(self):
-        return self.cache.quantization
+        return self._quantization
+
+    def bind_layout(self, *, num_layers, num_kv_heads, head_dim, device):
+        """Allocate the arena for this layout, or check an allocated one against it."""
+        with self._lock:
+            device = torch.device(device)
+            if device.type == "cuda" and device.index is None:
+                device = torch.device("cuda", torch.cuda.current_device())
+            if self.cache is None:
+                if self._device is not None and self._device != device:
+                    raise StateError("Cache layout changed within a model pool")
+                from .paged_kv import PagedKVCache
+
+                self.cache = PagedKVCache(num_blocks=self.max_blocks, num_layers=num_layers,
+                                          num_kv_heads=num_kv_heads, head_dim=head_dim,
+                                          block_size=self.block_size, device=device,
+                                          quantization=self._quantization)
+            c = self.cache
+            if (c.num_layers, c.num_kv_heads, c.head_dim) != (num_layers, num_kv_heads, head_dim) \
+                    or torch.device(c.device) != device:
+                raise StateError("Cache layout changed within a model pool")
+            return c
+
+    def _lock_signature(self, signature):
+        if self._signature is not None and signature != self._signature:
+            raise StateError("Cache layout changed within a model pool")
+        self._signature = signature
 
     # ---- page bookkeeping (state.py:190-206) --------------------------------
     def create(self, identity):
@@ -143,11 +224,13 @@ class PagedStatePool:
             raise StateError("Stale page reference")
         return page
 
-    def _collect(self, index):
-        page = self._pages[index]
-        if page.owners == 0 and page.readers == 0:
+    def _collect(self, page):
+        """Return a page nobody owns or reads to the free heap (state.py:199-202;
+        ``PrefixCache`` calls it with the page object after dropping an owner)."""
+        if page.owners == 0 and page.readers == 0 and not page.free:
             page.valid = 0
-            heapq.heappush(self._free, index)
+            page.free = True
+            heapq.heappush(self._free, page.index)
 
     def _allocate(self, count):
         """``count`` fresh pages (owners = 1) or CacheCapacityError, nothing taken."""
@@ -158,7 +241,7 @@ class PagedStatePool:
             index = heapq.heappop(self._free)
             page = self._pages[index]
             page.generation += 1
-            page.owners, page.readers, page.valid = 1, 0, 0
+            page.owners, page.readers, page.valid, page.free = 1, 0, 0, False
             refs.append(PageRef(index, page.generation))
         return refs
 
@@ -166,7 +249,7 @@ class PagedStatePool:
         for ref in refs:
             page = self._page(ref)
             page.owners -= 1
-            self._collect(ref.index)
+            self._collect(page)
 
     @property
     def used_blocks(self):
@@ -218,8 +301,9 @@ class PagedStatePool:
     def _unlease(self, refs):
         with self._lock:
             for ref in refs:
-                self._page(ref).readers -= 1
-                self._collect(ref.index)
+                page = self._page(ref)
+                page.readers -= 1
+                self._collect(page)
 
     # ---- appends ---------------------------------------------------------------
     def reserve(self, sequence, count):
@@ -329,42 +413,61 @@ class PagedStatePool:
 
     def _token_rows(self, layers):
         """``(rows, padding)``: one ``[T, Hkv, D]`` ``(key, value)`` per layer and the
-        padding leaf as a bool device vector ``[T]`` (None when absent)."""
+        padding leaf as a bool device vector ``[T]`` (None when absent; a trailing
+        one-element tuple is the padding leaf, as the runner appends it,
+        paged_attention.py:228). The first append allocates the arena from these
+        leaves; every append must match its layout, input dtype and device
+        (state.py:285-300)."""
         layers = tuple(layers)
+        if not layers:
+            raise StateError("KV state must be a nonempty tuple tree of tensors")
         padding = None
-        if len(layers) == self.cache.num_layers + 1:
-            leaf = layers[-1]
-            if isinstance(leaf, (tuple, list)) and len(leaf) == 1:
-                leaf = leaf[0]
-            padding = torch.as_tensor(leaf, device=self.cache.device)
+        last = layers[-1]
+        if not (isinstance(last, (tuple, list)) and len(last) == 2):
+            padding = last[0] if isinstance(last, (tuple, list)) and len(last) == 1 else last
+            layers = layers[:-1]
+        rows = []
+        for item in layers:
+            if not (isinstance(item, (tuple, list)) and len(item) == 2):
+                raise StateError("Cache layout changed within a model pool")
+            pair = []
+            for t in item:
+                if not isinstance(t, torch.Tensor) or not t.is_floating_point():
+                    raise StateError(
+                        "Quantized KV requires token/head vectors, not an arbitrary state tensor")
+                if t.ndim == 4:
+                    if t.shape[0] != 1:
+                        raise StateError("Page storage accepts single-sequence states only")
+                    t = t[0].transpose(0, 1)  # [1, Hkv, T, D] -> [T, Hkv, D] view
+                if t.ndim != 3:
+                    raise StateError("Invalid KV tensor layout")
+                pair.append(t)
+            if pair[0].shape != pair[1].shape:
+                raise StateError("Every cache leaf must describe the same token span")
+            rows.append(tuple(pair))
+        if not rows:
+            raise StateError("KV state must be a nonempty tuple tree of tensors")
+        first = rows[0][0]
+        if any(t.shape[1:] != first.shape[1:] or t.dtype != first.dtype
+               or t.device != first.device for pair in rows for t in pair):
+            raise StateError("Cache layout changed within a model pool")
+        if len({k.shape[0] for k, _ in rows}) != 1:
+            raise StateError("Every cache leaf must describe the same token span")
+        with self._lock:
+            cache = self.bind_layout(num_layers=len(rows), num_kv_heads=first.shape[1],
+                                     head_dim=first.shape[2], device=first.device)
+            self._lock_signature((len(rows), first.shape[1], first.shape[2], first.dtype))
+        if padding is not None:
+            padding = torch.as_tensor(padding, device=cache.device)
             if padding.ndim == 4:
                 if padding.shape[0] != 1 or padding.shape[1] != 1 or padding.shape[3] != 1:
                     raise StateError("Padding leaf must be [1, 1, tokens, 1]")
                 padding = padding[0, 0, :, 0]
             if padding.ndim != 1 or not ((padding == 0) | (padding == 1)).all():
                 raise StateError("Padding leaf must be a binary token vector")
-            padding = padding.bool()
-            layers = layers[:-1]
-        if len(layers) != self.cache.num_layers:
-            raise StateError("Cache layout changed within a model pool")
-        rows = []
-        for key, value in layers:
-            pair = []
-            for t in (key, value):
-                if t.ndim == 4:
-                    if t.shape[0] != 1:
-                        raise StateError("Page storage accepts single-sequence states only")
-                    t = t[0].transpose(0, 1)  # [1, Hkv, T, D] -> [T, Hkv, D] view
-                if t.ndim != 3 or tuple(t.shape[1:]) != (self.cache.num_kv_heads,
-                                                         self.cache.head_dim):
-                    raise StateError("Cache layout changed within a model pool")
-                pair.append(t)
-            if pair[0].shape != pair[1].shape:
+            if padding.shape[0] != first.shape[0]:
                 raise StateError("Every cache leaf must describe the same token span")
-            rows.append(tuple(pair))
-        if len({k.shape[0] for k, _ in rows}) != 1 or (
-                padding is not None and padding.shape[0] != rows[0][0].shape[0]):
-            raise StateError("Every cache leaf must describe the same token span")
+            padding = padding.bool()
         return rows, padding
 
     # ---- reads --------------------------------------------------------------
@@ -421,6 +524,8 @@ class PagedStatePool:
             width = width or max([len(t) for t in tables] + [1])
             if any(len(t) > width for t in tables):
                 raise ValueError("block table width too small")
+            if self.cache is None:
+                raise StateError("The pool's arena is not allocated before its first append")
             for ref in refs:
                 self._page(ref).readers += 1
         try:
@@ -466,12 +571,12 @@ class PagedStatePool:
         in use holds 2 * num_layers quantized leaves and the bool padding leaf."""
         with self._lock:
             used = self.used_blocks
-            per_page = (self.cache.block_code_bytes + self.cache.block_scale_bytes
-                        + self.cache.block_size)
+            c = self.cache
+            per_page = (c.block_code_bytes + c.block_scale_bytes + c.block_size) if c else 0
             return {
                 "format": self.quantization.format,
                 "allocated_tensor_bytes": used * per_page,
-                "quantized_leaves": used * 2 * self.cache.num_layers,
+                "quantized_leaves": used * 2 * c.num_layers if c else 0,
                 "physical_pages": used,
             }
 
@@ -498,6 +603,8 @@ class PagedStatePool:
         sequence = self.create(identity)
         if type(length) is not int or length < 1:
             raise StateError("Archived page count and token length differ")
+        if self.cache is None:  # no arena yet: its layout is unknown (state.py:453-454)
+            raise StateError("Restore requires this initialized model pool")
         count = math.ceil(length / self.block_size)
         packed = self._pack(payloads, length) if not _is_packed(payloads) else payloads
         codes, scales = packed[0], packed[1]

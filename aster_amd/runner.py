@@ -25,10 +25,14 @@ reference's padding leaf does (:181, :190, :228).
 
 from __future__ import annotations
 
+import copy
+import time
+
 import torch
 
-from .attention_backend import BACKEND, KernelWork
-from .paged_pool import StateError
+from .attention_backend import BACKEND, KernelWork, UnsupportedAttentionBackend
+from .kv_quantization import KVQuantization
+from .paged_pool import KVStateCodec, PagedStatePool, StateError
 
 
 def pack_rows(x, counts):
@@ -48,6 +52,11 @@ def unpack_rows(y, counts, width=None):
         out[b, :, :n] = y[cursor : cursor + n].transpose(0, 1)
         cursor += n
     return out
+
+
+def _device_ints(values, dtype, device):
+    """A host list of step metadata as a device vector (an async upload)."""
+    return torch.tensor(values, dtype=dtype).to(device, non_blocking=True)
 
 
 def _padding_vector(padding, counts):
@@ -91,32 +100,32 @@ class PagedAttentionStep:
         self.work = work if work is not None else KernelWork()
         self.partition_tokens = partition_tokens
         self.reservations = []
+        self._tables = None
+        self._open = False
+        # every reservation and the read leases are undone if anything below raises
         try:
             for sequence, n in zip(sequences, counts):
                 self.reservations.append(pool.reserve(sequence, n))
-        except BaseException:
-            for r in self.reservations:
-                pool.abort(r)
-            raise
-        cache = pool.cache
-        device = cache.device
-        self._tables = pool.block_tables(self.reservations)
-        self.block_tables, self.context_lens = self._tables.__enter__()
-        starts = [0]
-        for n in counts:
-            starts.append(starts[-1] + n)
-        self.num_tokens = starts[-1]
-        self.query_start_loc = torch.tensor(starts, dtype=torch.int32).to(device, non_blocking=True)
-        self.positions = [r.start for r in self.reservations]
-        self.max_query_len = max(counts)
-        self.max_context_len = max(r.length for r in self.reservations)
-        slots = [s for r in self.reservations for s in r.slots]
-        self.slot_mapping = torch.tensor(slots, dtype=torch.int64).to(device, non_blocking=True)
-        try:
+            cache = pool.cache
+            device = cache.device
+            tables = pool.block_tables(self.reservations)
+            self.block_tables, self.context_lens = tables.__enter__()
+            self._tables = tables
+            starts = [0]
+            for n in counts:
+                starts.append(starts[-1] + n)
+            self.num_tokens = starts[-1]
+            self.query_start_loc = _device_ints(starts, torch.int32, device)
+            self.positions = [r.start for r in self.reservations]
+            self.max_query_len = max(counts)
+            self.max_context_len = max(r.length for r in self.reservations)
+            slots = [s for r in self.reservations for s in r.slots]
+            self.slot_mapping = _device_ints(slots, torch.int64, device)
             cache.write_key_valid(self.slot_mapping,
                                   None if valid is None else valid.to(device, non_blocking=True))
         except BaseException:
-            self._tables.__exit__(None, None, None)
+            if self._tables is not None:
+                self._tables.__exit__(None, None, None)
             for r in self.reservations:
                 pool.abort(r)
             raise
@@ -177,3 +186,197 @@ class PagedAttentionStep:
         else:
             self.abort()
         return False
+
+
+_ATTENTION_PARTS = ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm", "rope",
+                    "num_heads", "num_kv_heads", "head_dim", "window", "scale")
+_LAYER_PARTS = ("input_layernorm", "self_attn", "mlp", "post_attention_layernorm")
+
+
+def _check_model(model):
+    """The attributes the reference's paged forward loop touches
+    (paged_attention.py:144-230), checked by shape instead of by the reference's model
+    classes (paged_attention.py:56-70): a decoder ``model.model`` with ``embed_tokens``,
+    ``layers`` and ``norm``, an ``lm_head``, a ``config`` with ``vocab_size`` and
+    ``max_position_embeddings``, and per layer the GQA attention parts. Returns
+    ``(num_layers, num_kv_heads, head_dim)``."""
+    body = getattr(model, "model", None)
+    if body is None or not all(hasattr(body, n) for n in ("embed_tokens", "layers", "norm")) \
+            or not hasattr(model, "lm_head") or not hasattr(model, "config"):
+        raise ValueError("Paged online runner needs a decoder with embed_tokens, layers, norm "
+                         "and lm_head")
+    config = model.config
+    if not all(hasattr(config, n) for n in ("vocab_size", "max_position_embeddings")):
+        raise ValueError("Paged online runner needs vocab_size and max_position_embeddings")
+    if getattr(config, "attention_dropout", 0) != 0:
+        raise ValueError("Unexpected attention/layer semantics or nonzero dropout")
+    layers = list(body.layers)
+    if not layers:
+        raise ValueError("Paged online runner needs at least one decoder layer")
+    shapes = set()
+    for layer in layers:
+        attention = getattr(layer, "self_attn", None)
+        if not all(hasattr(layer, n) for n in _LAYER_PARTS) or \
+                not all(hasattr(attention, n) for n in _ATTENTION_PARTS):
+            raise ValueError("Unexpected attention/layer semantics or nonzero dropout")
+        if attention.num_heads % attention.num_kv_heads:
+            raise ValueError("Query heads must divide into KV groups")
+        shapes.add((attention.num_kv_heads, attention.head_dim))
+    if len(shapes) != 1:
+        raise UnsupportedAttentionBackend("hip_int8_paged arenas hold one (kv heads, head dim) "
+                                          "layout for every layer")
+    hkv, dim = shapes.pop()
+    return len(layers), hkv, dim
+
+
+class PagedAttentionRunner:
+    """``PagedAttentionRunner`` (src/aster/inference/paged_attention.py:22-230) on the
+    ``hip_int8_paged`` backend, with the reference's constructor and ``forward_batch``
+    contract: the model's projections, norms, RoPE and MLP run as they are (PyTorch),
+    and every layer's attention over the rows' pages plus the chunk is one
+    quantize-append launch and one ragged attention launch on the HIP kernels
+    (``PagedAttentionStep``).
+
+    Kept: the argument checks and exceptions of forward_batch (:110-143), read leases
+    held until the device has finished (:144-148, :221), chunk K/V quantized before
+    attention (the step writes them into reserved slots first, then attends over
+    history + chunk: the same keys as the reference's extra quantized block,
+    :185-192), key padding from ``padding_masks`` (:137-143, :181, :228), the chunk
+    appended to the pool after the step (:226-229), CPU fp32 logits (:230),
+    ``attention_work``, and the counters of ``ModelRunner`` (runner.py:44-46).
+    Different: rows may not be committed one by one; the step commits all rows or, if
+    anything raises, none (a full pool raises ``CacheCapacityError`` before any layer
+    runs, not after). ``query_block_size``/``key_block_size`` are validated and kept
+    but do not shape the kernels (their tiles are fixed: 16-token blocks, query tiles
+    of 128 (token, head) columns). ``kv_quantization=None`` means the backend's INT8.
+    """
+
+    backend = BACKEND
+    kind = "token_predictor"
+
+    def __init__(self, model, *, policy_artifact_id, backend, tokenizer=None, block_size=16,
+                 max_blocks=256, query_block_size=32, key_block_size=None, chat_template=None,
+                 attention_fallback=None, kv_quantization=None, partition_tokens=0):
+        if backend != BACKEND:
+            raise ValueError(f"Select explicit backend={BACKEND!r}")
+        if attention_fallback is not None:
+            raise ValueError("The hip_int8_paged backend takes no fallback: a configuration "
+                             "it has no kernel for raises UnsupportedAttentionBackend")
+        kv_quantization = KVQuantization("int8") if kv_quantization is None else kv_quantization
+        if not isinstance(kv_quantization, KVQuantization):
+            raise ValueError("An explicit immutable KVQuantization profile is required")
+        key_block_size = 64 if key_block_size is None else key_block_size
+        if any(type(v) is not int or v < 1 for v in (query_block_size, key_block_size)):
+            raise ValueError("Attention tile sizes must be positive integers")
+        if not isinstance(policy_artifact_id, str) or not policy_artifact_id:
+            raise ValueError("An immutable policy identity is mandatory")
+        self.num_layers, self.num_kv_heads, self.head_dim = _check_model(model)
+        runtime = getattr(model, "_aster_shared_runtime_handles", ())
+        self.model = copy.deepcopy(model, {id(item): item for item in runtime}).eval()
+        self.model.requires_grad_(False)
+        self.policy_artifact_id = policy_artifact_id
+        self.codec = KVStateCodec(kind="gqa_kv")
+        self.pool = PagedStatePool(block_size=block_size, max_blocks=max_blocks, codec=self.codec,
+                                   quantization=kv_quantization)
+        self.tokenizer, self.chat_template = tokenizer, chat_template
+        self.device = next(self.model.parameters(), torch.empty(0)).device
+        self.query_block_size, self.key_block_size = query_block_size, key_block_size
+        self.attention_fallback = None
+        self.partition_tokens = partition_tokens
+        self.attention_work = KernelWork(backend=BACKEND)
+        self.input_tokens_computed = 0
+        self.forward_calls = 0
+        self.model_execution_seconds = 0.0
+
+    @classmethod
+    def from_artifact(cls, store, artifact_id, *, loader, tokenizer_loader=None, **kwargs):
+        artifact = store.get(artifact_id, verify=True)
+        tokenizer = tokenizer_loader(artifact.path) if tokenizer_loader else None
+        return cls(loader(artifact.path), policy_artifact_id=artifact.id, tokenizer=tokenizer,
+                   **kwargs)
+
+    def _synchronize(self):
+        if self.device.type == "cuda":
+            torch.cuda.synchronize(self.device)
+
+    def forward_batch(self, sequences, chunks, *, return_all_logits=False, padding_masks=None):
+        if not sequences or len(sequences) != len(chunks) or \
+                len({id(value) for value in sequences}) != len(sequences):
+            raise ValueError("Need a nonempty batch of distinct sequences and aligned chunks")
+        starts, counts = {s.length for s in sequences}, {len(chunk) for chunk in chunks}
+        if len(starts) != 1 or len(counts) != 1 or min(counts) < 1:
+            raise ValueError("Scheduler must group matching cached/chunk lengths")
+        if len({s.identity for s in sequences}) != 1:
+            raise StateError("A projection batch cannot cross cache security domains")
+        config = self.model.config
+        start, count, batch = next(iter(starts)), next(iter(counts)), len(sequences)
+        if start + count > config.max_position_embeddings:
+            raise ValueError("Sequence exceeds declared position support")
+        if any(type(t) is not int or not 0 <= t < config.vocab_size for c in chunks for t in c):
+            raise ValueError("Input token outside this immutable model vocabulary")
+        ids = torch.tensor(chunks, device=self.device, dtype=torch.long)
+        positions = torch.arange(start, start + count, device=self.device).expand(batch, -1)
+        padding = None
+        if padding_masks is not None:
+            padding = torch.as_tensor(padding_masks).cpu()
+            if padding.shape != ids.shape or not ((padding == 0) | (padding == 1)).all():
+                raise ValueError("Chunk padding must be a binary batch-by-token matrix")
+            padding = padding.bool()
+        self.pool.bind_layout(num_layers=self.num_layers, num_kv_heads=self.num_kv_heads,
+                              head_dim=self.head_dim, device=self.device)
+        layers = self.model.model.layers
+        with torch.inference_mode():
+            step = PagedAttentionStep(self.pool, sequences, [count] * batch, padding=padding,
+                                      work=self.attention_work,
+                                      partition_tokens=self.partition_tokens)
+            try:
+                self._synchronize()
+                started = time.monotonic()
+                hidden = self.model.model.embed_tokens(ids)
+                for index, layer in enumerate(layers):
+                    normalized = layer.input_layernorm(hidden)
+                    attention = layer.self_attn
+
+                    def split(value, heads):
+                        return value.reshape(batch, count, heads, attention.head_dim).transpose(1, 2)
+
+                    query = attention.rope(attention.q_norm(
+                        split(attention.q_proj(normalized), attention.num_heads)), positions)
+                    key = attention.rope(attention.k_norm(
+                        split(attention.k_proj(normalized), attention.num_kv_heads)), positions)
+                    value = split(attention.v_proj(normalized), attention.num_kv_heads)
+                    if index == 0:  # the appended leaves' layout (state.py:285-300)
+                        with self.pool._lock:
+                            self.pool._lock_signature((self.num_layers, self.num_kv_heads,
+                                                       self.head_dim, key.dtype))
+                    attended = step.attend(index, _packed(query), _packed(key), _packed(value),
+                                           scale=attention.scale, window=attention.window)
+                    hidden = hidden + attention.o_proj(attended.reshape(batch, count, -1))
+                    hidden = hidden + layer.mlp(layer.post_attention_layernorm(hidden))
+                logits = self.model.lm_head(self.model.model.norm(hidden))
+                step.commit()  # waits for the device, raises flagged errors, publishes
+            except BaseException:
+                step.abort()
+                raise
+            self.model_execution_seconds += time.monotonic() - started
+            self.forward_calls += 1
+            self.input_tokens_computed += ids.numel()
+        return [(row if return_all_logits else row[-1]).detach().float().cpu() for row in logits]
+
+    def forward_feature_batch(self, sequences, chunks, *, hidden_state_indices):
+        raise UnsupportedAttentionBackend("the hip_int8_paged runner serves logits only; hidden-"
+                                          "state features need the reference's ModelRunner")
+
+    def decode(self, token_ids):
+        if self.tokenizer is None:
+            return " ".join(str(token) for token in token_ids)
+        return self.tokenizer.decode(token_ids)
+
+    def stream_text(self, token_ids, *, final=False):
+        return self.decode(token_ids)
+
+
+def _packed(x):
+    """Reference layout ``[B, H, T, D]`` -> packed rows ``[B * T, H, D]`` (contiguous)."""
+    batch, heads, tokens, dim = x.shape
+    return x.transpose(1, 2).reshape(batch * tokens, heads, dim)

@@ -171,7 +171,8 @@ int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query, int32
  *              negative, decreasing or beyond num_query_tokens raises
  *              ASTR_FLAG_BAD_INDEX and that sequence produces nothing.
  *   max_query_len: host-side upper bound of qsl[s+1]-qsl[s]; <= 1 launches the
- *              decode kernels only.
+ *              decode kernels only. A sequence with more query tokens than this
+ *              bound raises ASTR_FLAG_BAD_INDEX and produces nothing.
  *   context_lens: int32 [num_seqs], counting the step's own tokens (the chunk
  *              is appended before attention). Query token i of a sequence with
  *              n query tokens sits at position ctx-n+i and sees key k iff

@@ -1,0 +1,158 @@
+"""Value ranges and argument contracts of the attention kernels beyond the seeded N(0,1)
+workloads, each against the oracle (online_attention.py:74-219 per row):
+
+* large V scales: the PV weights and V operands are rounded to f16, so V scales big
+  enough to overflow f16 (INT8 beyond ~3e4, E4M3FN beyond 448, E5M2 beyond ~5.7e4 in
+  decode; any format beyond 65504 in chunk rows) must be carried by a power-of-two
+  exponent instead; attention is linear in V, so V scales times 2^k give outputs 2^k
+  as large, within the tolerance scaled the same way;
+* extreme finite scores, after the reference's own test
+  (tests/unit/test_inference_online_attention.py:79-98: q x 100, k x 100), in decode
+  rows (both split modes) and chunk rows;
+* the checks on a caller's ``out`` and ``workspace``, and a ``max_query_len`` smaller
+  than a row's query count (which would leave that row unwritten) raising the index
+  flag."""
+
+import numpy as np
+import pytest
+import torch
+
+from aster_amd import KVQuantization, PagedKVCache
+from aster_amd import workloads as wl
+from tests.gpu_util import assert_attention_close, oracle_decode
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = ["int8", "fp8_e4m3fn", "fp8_e5m2"]
+
+
+def _workload(q_lens, ctx, *, hq=32, hkv=8, dim=128, qdtype=torch.bfloat16, seed=11):
+    ctx = np.asarray(ctx, np.int32)
+    rng = np.random.default_rng(seed)
+    tables, pool = wl._tables_from_lengths(ctx, rng, spare_blocks=3)
+    q_lens = None if q_lens is None else np.asarray(q_lens, np.int32)
+    return wl.DecodeWorkload("range", hq, hkv, dim, ctx, tables, pool, qdtype, seed, dim ** -0.5,
+                             query_lens=q_lens)
+
+
+def _build(w, device, fmt):
+    cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=1, num_kv_heads=w.num_kv_heads,
+                         head_dim=w.head_dim, device=device, quantization=KVQuantization(fmt))
+    wl.materialize(w, cache, device=device)
+    tables, lens = wl.device_tables(w, device)
+    return cache, tables, lens
+
+
+def _attend(cache, w, q, tables, lens, **kw):
+    if w.query_lens is not None:
+        kw.update(query_start_loc=wl.device_query_start(w, q.device),
+                  max_query_len=w.max_query_len)
+    return cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                                 scale=w.scale, check=True, **kw)
+
+
+DECODE_CTX = [1, 17, 255, 600, 33, 1000, 129, 2048]
+MIXED_Q = [2, 31, 1, 32, 33, 1, 65, 129, 1, 7]
+MIXED_CTX = [2, 71, 300, 48, 38, 1, 265, 462, 17, 1007]
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("part", [0, 128])
+@pytest.mark.parametrize("k", [9, 20])
+def test_large_v_scales_in_decode_rows(device, fmt, qdtype, part, k):
+    w = _workload(None, DECODE_CTX, qdtype=qdtype, seed=70 + k)
+    cache, tables, lens = _build(w, device, fmt)
+    cache.scales[:, 0, 1] *= 2.0 ** k
+    q = wl.queries(w, device)
+    out = _attend(cache, w, q, tables, lens, partition_tokens=part)
+    assert torch.isfinite(out).all()
+    assert_attention_close(out, oracle_decode(w, cache, q), atol=2e-3 * 2.0 ** k)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("part", [0, 512])
+@pytest.mark.parametrize("k", [9, 20])
+def test_large_v_scales_in_chunk_rows(device, fmt, part, k):
+    w = _workload(MIXED_Q, MIXED_CTX, seed=80 + k)
+    cache, tables, lens = _build(w, device, fmt)
+    cache.scales[:, 0, 1] *= 2.0 ** k
+    q = wl.queries(w, device)
+    out = _attend(cache, w, q, tables, lens, partition_tokens=part)
+    assert torch.isfinite(out).all()
+    assert_attention_close(out, oracle_decode(w, cache, q), atol=2e-3 * 2.0 ** k)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("part", [0, 128])
+def test_mixed_v_scale_ranges_within_rows(device, fmt, part):
+    """Every third block's V scales times 2^12, the others unchanged: pieces and query
+    tiles meet blocks of both ranges (the weight factor or the block exponent changes
+    mid-row), in decode and chunk rows of one step."""
+    w = _workload(MIXED_Q, MIXED_CTX, seed=90)
+    cache, tables, lens = _build(w, device, fmt)
+    cache.scales[::3, 0, 1] *= 2.0 ** 12
+    q = wl.queries(w, device)
+    out = _attend(cache, w, q, tables, lens, partition_tokens=part)
+    assert torch.isfinite(out).all()
+    assert_attention_close(out, oracle_decode(w, cache, q), atol=2e-3 * 2.0 ** 12)
+
+
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("part", [0, 512])
+def test_extreme_finite_scores(device, qdtype, dim, part):
+    """q x 100 and k x 100 (test_inference_online_attention.py:79-98): scores of
+    thousands, so every block past the first moves the running maximum far beyond the
+    lazy-rescale slack; outputs stay finite and match the oracle, in decode and chunk
+    rows."""
+    for q_lens, ctx in ((None, DECODE_CTX), (MIXED_Q, MIXED_CTX)):
+        w = _workload(q_lens, ctx, hq=16, hkv=4, dim=dim, qdtype=qdtype, seed=dim + 5)
+        cache, tables, lens = _build(w, device, "int8")
+        cache.scales[:, 0, 0] *= 100.0
+        q = (wl.queries(w, device).float() * 100.0).to(qdtype)
+        out = _attend(cache, w, q, tables, lens, partition_tokens=part)
+        assert torch.isfinite(out).all()
+        assert_attention_close(out, oracle_decode(w, cache, q))
+
+
+def test_out_and_workspace_are_checked(device):
+    w = _workload(None, [40, 300, 17])
+    cache, tables, lens = _build(w, device, "int8")
+    q = wl.queries(w, device)
+    kw = dict(max_context_len=w.max_context_len)
+    for bad in (torch.empty(2, 32, 128, device=device, dtype=q.dtype),       # shape
+                torch.empty_like(q, dtype=torch.float32),                     # dtype
+                torch.empty(3, 32, 256, device=device, dtype=q.dtype)[..., ::2],  # strides
+                torch.empty(q.shape, dtype=q.dtype)):                         # host
+        with pytest.raises(ValueError, match="out must"):
+            cache.paged_attention(0, q, tables, lens, out=bad, **kw)
+    need = cache.workspace_bytes(3, 32, w.max_context_len)
+    assert need > 0
+    for bad in (torch.empty(need, dtype=torch.uint8),                           # host
+                torch.empty(need // 4 + 1, dtype=torch.int32, device=device),  # dtype
+                torch.empty(2 * need, dtype=torch.uint8, device=device)[::2]):  # strided
+        with pytest.raises(ValueError, match="workspace must"):
+            cache.paged_attention(0, q, tables, lens, workspace=bad, **kw)
+    with pytest.raises(ValueError, match="bytes required"):
+        cache.paged_attention(0, q, tables, lens, workspace=torch.empty(
+            need - 256, dtype=torch.uint8, device=device), **kw)
+    out = torch.empty_like(q)
+    ws = torch.empty(need, dtype=torch.uint8, device=device)
+    got = cache.paged_attention(0, q, tables, lens, out=out, workspace=ws, check=True, **kw)
+    assert got.data_ptr() == out.data_ptr()
+    assert_attention_close(out, oracle_decode(w, cache, q))
+
+
+def test_max_query_len_below_a_rows_query_count_is_flagged(device):
+    w = _workload([4, 1, 3], [20, 30, 40], seed=3)
+    cache, tables, lens = _build(w, device, "int8")
+    q = wl.queries(w, device)
+    qsl = wl.device_query_start(w, device)
+    for stale in (1, 3):  # 1: no chunk kernel at all; 3: row 0 (4 tokens) is too long
+        with pytest.raises(ValueError, match="outside"):
+            cache.paged_attention(0, q, tables, lens, max_context_len=40, query_start_loc=qsl,
+                                  max_query_len=stale, check=True)
+    out = cache.paged_attention(0, q, tables, lens, max_context_len=40, query_start_loc=qsl,
+                                max_query_len=4, check=True)
+    assert_attention_close(out, oracle_decode(w, cache, q))

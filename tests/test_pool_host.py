@@ -239,3 +239,138 @@ def test_padding_leaf_is_stored_exposed_and_copied_on_write():
         pool.append_delta(seq, layers(2, 4) + [(torch.tensor([1, 2])[None, None, :, None],)])
     with pytest.raises(StateError):
         pool.append_delta(seq, layers(2, 4) + [(torch.ones(1, 1, 3, 1, dtype=torch.bool),)])
+
+
+def test_reference_constructor_and_lazy_arena():
+    """PagedStatePool(*, block_size, max_blocks, codec, quantization) as ModelRunner
+    builds it (runner.py:36-41, state.py:169-180): no layer shape is known until the
+    first append, so the arena is allocated then (here it cannot be: the leaves live on
+    the CPU, and the arena only on a HIP device)."""
+    from aster_amd import KVQuantization, UnsupportedAttentionBackend
+    from aster_amd.paged_pool import KVStateCodec
+
+    q8 = KVQuantization("int8")
+    with pytest.raises(ValueError, match="positive"):
+        PagedStatePool(block_size=0, max_blocks=4, quantization=q8)
+    with pytest.raises(ValueError, match="KVQuantization"):
+        PagedStatePool(quantization="int8")
+    with pytest.raises(UnsupportedAttentionBackend, match="quantized"):
+        PagedStatePool()  # native (unquantized) storage is the reference backend's
+    with pytest.raises(UnsupportedAttentionBackend, match="16-token"):
+        PagedStatePool(block_size=4, quantization=q8)
+    with pytest.raises(UnsupportedAttentionBackend, match="codec"):
+        PagedStatePool(quantization=q8, codec=KVStateCodec(kind="mla_latent"))
+    with pytest.raises(ValueError, match="codec tag"):
+        KVStateCodec(kind="unknown")
+    pool = PagedStatePool(block_size=16, max_blocks=4, codec=KVStateCodec(kind="gqa_kv"),
+                          quantization=q8)
+    assert pool.cache is None and pool.quantization is q8 and pool.codec.kind == "gqa_kv"
+    seq = pool.create("tenant")
+    child = pool.fork(seq)
+    assert seq.kind == child.kind == "gqa_kv" and pool.materialize(seq) is None
+    with pool.read_pages(seq) as views:
+        assert views == ()
+    assert pool.storage_metrics() == {"format": "int8", "allocated_tensor_bytes": 0,
+                                      "quantized_leaves": 0, "physical_pages": 0}
+    with pytest.raises(StateError, match="initialized"):
+        pool.restore_pages((), identity="tenant", length=3)
+    with pytest.raises(StateError, match="arena"):
+        with pool.block_tables([seq]):
+            pass
+    with pytest.raises(UnsupportedAttentionBackend, match="HIP device"):
+        pool.append_delta(seq, layers(3, 1))
+    with pytest.raises(StateError, match="token/head"):
+        pool.append_delta(seq, [(torch.zeros(1, 2, 3, 4, dtype=torch.int32),) * 2])
+    pool.release(child)
+    pool.release(seq)
+
+
+def test_layout_lock_and_padding_leaf_detection():
+    """The first append locks layers, heads, head dim and input dtype
+    (state.py:285-300); a trailing one-element tuple is the padding leaf."""
+    pool = make_pool()
+    seq = pool.create("t")
+    pool.append_delta(seq, layers(3, 1) + [(torch.ones(1, 1, 3, 1, dtype=torch.bool),)])
+    with pytest.raises(StateError, match="layout"):
+        pool.append_delta(seq, [(k.double(), v.double()) for k, v in layers(2, 2)])
+    with pytest.raises(StateError, match="layout"):
+        pool.append_delta(seq, [(k[:, :1], v[:, :1]) for k, v in layers(2, 3)])
+    with pytest.raises(StateError, match="layout"):
+        pool.append_delta(seq, layers(2, 4) + layers(2, 5))  # four layers
+    assert seq.length == 3
+
+
+def test_prefix_cache_internals_on_the_arena_pool():
+    """The reference's PrefixCache reaches into the pool (state.py:547-640): it holds
+    ``pool._lock``, calls ``pool._check``, reads ``pool._page(ref).valid``, adds and drops
+    owners on ``pool._page(ref)``, builds ``PagedSequence(id(pool), pool.codec.kind, ...)``
+    and returns pages with ``pool._collect(page)``. Those steps, as it takes them,
+    keep the arena pool's free list exact."""
+    from aster_amd.paged_pool import PagedSequence
+
+    pool = make_pool(blocks=6)
+    seq = pool.create("domain")
+    pool.append_delta(seq, layers(40, 1))  # 2 full pages + 1 partial
+    full = seq.pages[:2]
+    # publish: full pages only, one owner more each
+    with pool._lock:
+        pool._check(seq)
+        assert all(pool._page(ref).valid == BS for ref in full)
+        for ref in full:
+            pool._page(ref).owners += 1
+    # lookup: a new sequence sharing the published pages
+    with pool._lock:
+        for ref in full:
+            pool._page(ref).owners += 1
+        hit = PagedSequence(id(pool), pool.codec.kind, "domain", list(full), 2 * BS)
+    pool.append_delta(hit, layers(5, 2))  # extends onto a fresh page (tail was full)
+    assert hit.pages[:2] == full and hit.length == 2 * BS + 5
+    pool.release(seq)
+    pool.release(hit)
+    assert pool.used_blocks == 2  # still held by the cache entry
+    # evict: drop the cache's owner and collect, as _evict_one_locked does
+    with pool._lock:
+        for ref in full:
+            page = pool._page(ref)
+            page.owners -= 1
+            pool._collect(page)
+            pool._collect(page)  # a second collect must not free the page twice
+    assert pool.used_blocks == 0
+    fresh = pool.create("domain")
+    pool.append_delta(fresh, layers(6 * BS, 3))  # every page exactly once
+    assert sorted(ref.index for ref in fresh.pages) == list(range(6))
+
+
+def test_step_setup_failure_releases_leases_and_reservations(monkeypatch):
+    """A failure after the step has reserved slots and leased its pages (an upload of
+    the step's metadata, the padding write) undoes both."""
+    from aster_amd import runner as runner_module
+
+    pool = make_pool()
+    seqs = [pool.create("t") for _ in range(2)]
+    for i, s in enumerate(seqs):
+        pool.append_delta(s, layers(20, 10 + i))
+    used = pool.used_blocks
+    calls = []
+
+    def failing_upload(values, dtype, device):
+        calls.append(dtype)
+        if len(calls) == 2:
+            raise RuntimeError("upload failed")
+        return torch.tensor(values, dtype=dtype)
+
+    monkeypatch.setattr(runner_module, "_device_ints", failing_upload)
+    with pytest.raises(RuntimeError, match="upload failed"):
+        runner_module.PagedAttentionStep(pool, seqs, [5, 30])
+    assert pool.used_blocks == used
+    assert all(pool._pages[ref.index].readers == 0 for s in seqs for ref in s.pages)
+    monkeypatch.undo()
+
+    def failing_padding(slots, valid=None):
+        raise RuntimeError("padding write failed")
+
+    monkeypatch.setattr(pool.cache, "write_key_valid", failing_padding)
+    with pytest.raises(RuntimeError, match="padding write failed"):
+        runner_module.PagedAttentionStep(pool, seqs, [5, 30])
+    assert pool.used_blocks == used and [s.length for s in seqs] == [20, 20]
+    assert all(pool._pages[ref.index].readers == 0 for s in seqs for ref in s.pages)
