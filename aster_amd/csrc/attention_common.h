@@ -360,11 +360,19 @@ struct QueryColumn {  // the lane's 16 elements of each 64-wide d chunk, as load
 // for every element within 2^-4 of the column maximum).
 // Returns the score factor max|q| / kQRange * qk_scale_log2 (NaN for a non-finite
 // query, which makes every score of the column non-finite as in fp32 arithmetic).
+// kTerms > 2: more terms for blocks whose scores are large enough that the 15-bit
+// query's error would show. With x = q * kQRange / max|q| and r2 = x - Q (|r2| <= 1/2):
+// lo2 = rint(128 r2), so that 128 Q + lo2 is within 1/2 of 128 x (a ~22-bit query);
+// kTerms = 4 adds lo3 = rint(128 (128 r2 - lo2)), 2^14 Q + 2^7 lo2 + lo3 within 1/2 +
+// 2^-11 of 2^14 x (~29 bits). Every term is in [-64, 64]; the same raw column always
+// gives the same terms.
 // Cross-lane: uniform control flow.
-template <typename QT, int D>
+template <typename QT, int D, int kTerms = 2>
 __device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, bool valid,
                                                  float qk_scale_log2, int4_t (&qhi)[D / 64],
-                                                 int4_t (&qlo)[D / 64]) {
+                                                 int4_t (&qlo)[D / 64],
+                                                 int4_t* qlo2 = nullptr, int4_t* qlo3 = nullptr) {
+  static_assert(kTerms >= 2 && kTerms <= 4, "query terms");
   constexpr int kVec = 16 / (int)sizeof(QT);  // elements per 16-byte load
   float x[D / 64][16];
 #pragma unroll
@@ -410,7 +418,7 @@ __device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, 
   for (int h = 0; h < D / 64; ++h)
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      uint32_t hb[4], lb[4];
+      uint32_t hb[4], lb[4], fb[4], gb[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float xv = x[h][4 * w + e];
@@ -419,9 +427,22 @@ __device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, 
         const float tl = __builtin_fmaf(xv, inv, __builtin_fmaf(hv, -128.f, kRound));
         hb[e] = __builtin_bit_cast(uint32_t, th);
         lb[e] = __builtin_bit_cast(uint32_t, tl);
+        if constexpr (kTerms > 2) {
+          // residual of Q = 128 hi + lo (exact integers), one rounding: |r2| <= 1/2
+          const float q2 = __builtin_fmaf(hv, 128.f, tl - kRound);
+          const float r2 = __builtin_fmaf(xv, inv, -q2);
+          const float t2 = __builtin_fmaf(r2, 128.f, kRound);
+          fb[e] = __builtin_bit_cast(uint32_t, t2);
+          if constexpr (kTerms > 3) {
+            const float r3 = __builtin_fmaf(r2, 128.f, kRound - t2);  // exact
+            gb[e] = __builtin_bit_cast(uint32_t, __builtin_fmaf(r3, 128.f, kRound));
+          }
+        }
       }
       qhi[h][w] = (int)low_bytes(hb);
       qlo[h][w] = (int)low_bytes(lb);
+      if constexpr (kTerms > 2) qlo2[h][w] = (int)low_bytes(fb);
+      if constexpr (kTerms > 3) qlo3[h][w] = (int)low_bytes(gb);
     }
   return factor;
 }
@@ -503,8 +524,16 @@ struct QkOperand {
 };
 template <int D>
 struct QkOperand<D, kInt8> {
-  int4_t hi[D / 64], lo[D / 64];
+  int4_t hi[D / 64], lo[D / 64], lo2[D / 64];
+  // K scale above which a block takes the third query term: the two-term query's
+  // worst-case score error, 1/2 step times 127 D per unit of K scale times the score
+  // factor, would exceed kFineScoreError (base-2 units) there
+  float ks_fine;
 };
+// Largest worst-case score error (base 2) a block may carry from the two-term query
+// before the third term is added: typical errors are ~sqrt(D) times smaller, a few
+// 1e-4 of a softmax weight.
+constexpr float kFineScoreError = 1.f / 32.f;
 
 // Builds the operand of query row r (lane layout of QueryRaw; rows r >= G are zero)
 // and returns its score factor, code scale included. Cross-lane: uniform control flow.
@@ -519,7 +548,9 @@ __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, f
       col.w[h][0] = q.w[h][0];
       col.w[h][1] = q.w[h][1];
     }
-    return query_column_i8<QT, D>(col, gvalid, qk_scale_log2, op.hi, op.lo);
+    const float cf = query_column_i8<QT, D, 3>(col, gvalid, qk_scale_log2, op.hi, op.lo, op.lo2);
+    op.ks_fine = (kFineScoreError / (63.5f * D)) / cf;  // +inf for cf = 0, NaN for NaN
+    return cf;
   } else {
     return query_operand<QT, D>(q, gvalid, qk_scale_log2, op.op) * code_scale<KF>();
   }
@@ -550,6 +581,7 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
   constexpr int VB = D / 16;
   constexpr int NPV = D / 16;
   const bool gvalid = r < G;
+  const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
   float4_t s4;
   if constexpr (KF == kInt8) {
     // exact int32 K.Q = 128 (K.hi) + K.lo straight from the staged codes
@@ -564,6 +596,16 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
 #pragma unroll
     for (int h = 0; h < KCH; ++h) si = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop.lo[h], si, 0, 0, 0);
     s4 = float4_t{(float)si[0], (float)si[1], (float)si[2], (float)si[3]};
+    // large scores: add the third query term, K.lo2 / 128 (exact int32, then scaled
+    // by a power of two), wherever a block's K scales reach the column's threshold
+    const float kmx = fmaxf(fmaxf(ks[0], ks[1]), fmaxf(ks[2], ks[3]));
+    if (__ballot(kmx > qop.ks_fine) != 0) {
+      int4_t sf = {0, 0, 0, 0};
+#pragma unroll
+      for (int h = 0; h < KCH; ++h) sf = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop.lo2[h], sf, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s4[j] = __builtin_fmaf((float)sf[j], 1.f / 128.f, s4[j]);
+    }
   } else {
     s4 = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -579,7 +621,6 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
       }
     }
   }
-  const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
   // V scales times the weight factor (2^8 at the start of a piece for FP8 codes:
   // E4M3FN operands carry 2^-8; E5M2 weights carry 2^8, as does the normaliser of
   // this format). Scales are finite and the same on the 16 lanes of a token group.

@@ -207,6 +207,7 @@ __device__ __forceinline__ void load_query_column(const QT* qp, QueryColumn<QT, 
 template <int D>
 struct QOpI8 {
   int4_t hi[D / 64], lo[D / 64];
+  float ks_fine;  // K scale from which a step adds the finer query terms (QkOperand<D, kInt8>)
 };
 template <int D>
 struct QOpF16 {
@@ -399,12 +400,14 @@ __device__ __forceinline__ void prefill_pv(const uint4* vt, const float (&u)[NT]
 // the scores are masked to -inf outside the bounds, for padding keys and for unused
 // blocks (whose stages hold stale but finite codes and scales) and checked for
 // non-finite values.
-template <int D, int NT>
+template <typename QT, int D, int NT>
 __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, uint32_t use,
                                              uint32_t bounded, bool masks, int kb0,
                                              const QOp<D> (&qop)[NT],
                                              const float (&cf)[NT], const float (&cfe)[NT],
-                                             const int (&lo)[NT], const int (&hi)[NT], int r,
+                                             const int (&lo)[NT], const int (&hi)[NT],
+                                             const QT* const (&qptr)[NT],
+                                             const bool (&cvalid)[NT], int r,
                                              int qg, const half8_t& ones, bool vmix,
                                              const half4_t& vf,
                                              float4_t (&acc)[NT][D / 16 + 1], float (&m)[NT],
@@ -482,12 +485,48 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
 #pragma unroll
   for (int t = 0; t < NT; ++t) ok = ok && kmax * cf[t] <= safe_factor();  // false for NaN
   const bool unsafe = __ballot(!ok) != 0;
-  const bool edge = (use != (1u << NBK) - 1) | (bounded != 0) | unsafe | padded;
   float u[NT][4 * NBK];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int j = 0; j < 4 * NBK; ++j) u[t][j] = (float)sacc[j / 4][t][j % 4] * ks[j / 4][j % 4];
+  // large scores: where the step's K scales reach a column's threshold, the column's
+  // query is read again (the same raw values give the same hi and lo terms) and split
+  // into two finer terms, lo2 and lo3, whose exact int32 dot products with the K codes
+  // (read again from the stages) add S2 / 2^7 + S3 / 2^14 to each score
+  bool fine = false;
+  if constexpr (KF == kInt8) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) fine = fine || kmax > qop[t].ks_fine;
+  }
+  if (__ballot(fine) != 0) {
+    if constexpr (KF == kInt8) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        QueryColumn<QT, D> raw;
+        load_query_column<QT, D>(qptr[t], raw);
+        int4_t qh[KCH], ql[KCH], q2[KCH], q3[KCH];
+        query_column_i8<QT, D, 4>(raw, cvalid[t], 1.f, qh, ql, q2, q3);
+#pragma unroll
+        for (int b = 0; b < NBK; ++b) {
+          const char* st = cur + b * S::kBytes;
+          int4_t s2 = {0, 0, 0, 0}, s3 = {0, 0, 0, 0};
+#pragma unroll
+          for (int h = 0; h < KCH; ++h) {
+            const int4_t kop = *reinterpret_cast<const int4_t*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
+            s2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, q2[h], s2, 0, 0, 0);
+            s3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, q3[h], s3, 0, 0, 0);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float f = __builtin_fmaf((float)s3[i], 1.f / 128.f, (float)s2[i]);
+            u[t][4 * b + i] = __builtin_fmaf(f, ks[b][i] * (1.f / 128.f), u[t][4 * b + i]);
+          }
+        }
+      }
+    }
+  }
+  const bool edge = (use != (1u << NBK) - 1) | (bounded != 0) | unsafe | padded;
   if (edge) {
     asm volatile("");  // keeps this a branch: if-converted, the interior steps would pay for it
     bool nonfinite = false;
@@ -664,6 +703,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   int lo[NT], hi[NT], ctok[NT], chead[NT];
   bool cvalid[NT];
   QueryColumn<QT, D> qraw[NT];
+  const QT* qptr[NT];  // each lane's query column (read again by steps that need finer terms)
   const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
   int ids = 0;
   auto load_ids = [&](int s0) __attribute__((always_inline)) {
@@ -681,9 +721,9 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     lo[t] = cvalid[t] ? (a.window > 0 ? max(0, p - a.window + 1) : 0) : INT_MAX;
     hi[t] = cvalid[t] ? (a.causal ? p : ctx - 1) : -1;
     // an invalid column reads token t0's row (in range) and is zeroed when quantized
-    const QT* qp = static_cast<const QT*>(a.q) + (int64_t)(q0 + (cvalid[t] ? ctok[t] : t0)) * a.q_tok +
-                   (int64_t)chead[t] * a.q_head + 16 * qg;
-    load_query_column<QT, D>(qp, qraw[t]);
+    qptr[t] = static_cast<const QT*>(a.q) + (int64_t)(q0 + (cvalid[t] ? ctok[t] : t0)) * a.q_tok +
+              (int64_t)chead[t] * a.q_head + 16 * qg;
+    load_query_column<QT, D>(qptr[t], qraw[t]);
   }
 
   // ---- 3. key steps: block b_lo + 4*step + w is staged by wave w. Lane i of `ids`
@@ -713,7 +753,10 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     if constexpr (KF == kInt8)
+    {
       cf[t] = query_column_i8<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qop[t].hi, qop[t].lo);
+      qop[t].ks_fine = (kFineScoreError / (63.5f * D)) / cf[t];
+    }
     else
       cf[t] = query_column_f16<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qop[t].op);
     cfe[t] = cf[t] > 0.f ? cf[t] : FLT_MIN;  // cf >= 0 or NaN (scale > 0)
@@ -804,8 +847,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
         if (!(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min)) bounded |= 1u << w;
       }
       if (use != 0)
-        prefill_step<D, NT>(cur, vt[0], use, bounded & use, masks, kb0, qop, cf, cfe, lo, hi, r, qg,
-                            ones, vmix, vf, acc, m, bad_score);
+        prefill_step<QT, D, NT>(cur, vt[0], use, bounded & use, masks, kb0, qop, cf, cfe, lo, hi,
+                                qptr, cvalid, r, qg, ones, vmix, vf, acc, m, bad_score);
     }
     __syncthreads();  // step i's stage may be refilled
   }

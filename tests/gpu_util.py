@@ -18,9 +18,11 @@ def arena_numpy(cache, layer=0):
 
 
 def oracle_decode(workload_or_tables, cache, query, layer=0, context_lens=None, scale=None,
-                  window=None, query_lens=None, causal=True):
+                  window=None, query_lens=None, causal=True, fp64=False):
     """The oracle's row-by-row paged attention (paged_attention.py:168-215) over this
-    cache layer; a workload supplies tables, lengths, scale and query counts."""
+    cache layer; a workload supplies tables, lengths, scale and query counts. ``fp64``
+    runs it in float64, as the reference does for float64 queries (online_attention.py:
+    158-159): the exact result over the same codes and scales."""
     if context_lens is None:
         w = workload_or_tables
         tables, lens = w.block_tables, w.context_lens
@@ -29,7 +31,7 @@ def oracle_decode(workload_or_tables, cache, query, layer=0, context_lens=None, 
             query_lens = w.query_lens
     else:
         tables, lens = workload_or_tables, context_lens
-    q = query.float().cpu().numpy()
+    q = query.double().cpu().numpy() if fp64 else query.float().cpu().numpy()
     padding = cache.key_valid.cpu().numpy().astype(bool) if cache.has_padding else None
     return ref.paged_attention(q, *arena_numpy(cache, layer), tables, lens, block_size=16,
                                scale=scale, window=window, query_lens=query_lens, causal=causal,

@@ -5,14 +5,14 @@
 sliding-window layer and q/k norms, through prefill chunks, decode steps, padding, a
 fork with copy-on-write and groups of different lengths.
 
-fp32 model: a free-running CPU rendering of the reference's row loop over the same
-weights (torch fp32 model parts, the oracle's quantize-then-attend per row over
-quantized history pages plus the chunk block) gives every layer's attention output
-and the logits, which the GPU run matches at the north_star tolerance. Fed instead
-with the q/k/v the GPU run produced, the oracle's row loop gives each layer's
-attention to the same tolerance and a quantized history that the pool's pages equal
-bit for bit after every step (free-running, the two sides' fp32 projections differ
-in the last bits, which can move a code across a rounding boundary).
+fp32 model: a CPU rendering of the reference's row loop over the same weights (torch
+fp32 model parts, the oracle's quantize-then-attend per row over quantized history
+pages plus the chunk block) computes its own hidden states, queries, attention and
+logits over the codes of the K/V values the GPU run produced (OracleLoop explains
+why the codes are shared); every layer's attention and the logits match at the
+north_star tolerance. Fed with the GPU run's q/k/v, the oracle's row loop gives each
+layer's attention to the same tolerance and a quantized history that the pool's
+pages equal bit for bit after every step.
 bf16 model: the fed check only (the model parts in bf16 round differently on the
 two sides)."""
 
@@ -77,14 +77,22 @@ def _pack(x):
 
 class OracleLoop:
     """The reference's forward_batch (paged_attention.py:144-230) on the CPU for an
-    fp32 model: torch for the model parts, OracleRows for the paged attention."""
+    fp32 model: torch for the model parts, OracleRows for the paged attention.
+
+    ``shared_kv`` (per layer, the step's K/V as the GPU run produced them) makes the
+    oracle quantize those values instead of its own: quantization is a step function,
+    and after layer 0 the two sides' fp32 values differ in the last bits, which moves
+    a few codes by one quantization step (~1 % of a row's range); with the codes
+    shared (their bit-exactness is checked on the pool), everything else -- hidden
+    states, queries, attention, logits -- is computed independently here and differs
+    only by rounding."""
 
     def __init__(self, model):
         self.model = copy.deepcopy(model).float().cpu().eval()
         self.rows = OracleRows(len(self.model.model.layers))
 
     @torch.no_grad()
-    def forward(self, keys, start, chunks, padding=None):
+    def forward(self, keys, start, chunks, padding=None, shared_kv=None):
         batch, count = len(chunks), len(chunks[0])
         ids = torch.tensor(chunks)
         positions = torch.arange(start, start + count).expand(batch, -1)
@@ -104,8 +112,9 @@ class OracleLoop:
             k = attention.rope(attention.k_norm(split(attention.k_proj(normalized),
                                                       attention.num_kv_heads)), positions)
             v = split(attention.v_proj(normalized), attention.num_kv_heads)
-            out = self.rows.attend(index, rows, _pack(q), _pack(k), _pack(v), attention.scale,
-                                   pads, window=attention.window)
+            kp, vp = shared_kv[index] if shared_kv is not None else (_pack(k), _pack(v))
+            out = self.rows.attend(index, rows, _pack(q), kp, vp, attention.scale, pads,
+                                   window=attention.window)
             attended.append(out)
             result = torch.from_numpy(out).reshape(batch, count, -1)
             hidden = hidden + attention.o_proj(result)
@@ -137,16 +146,17 @@ def test_forward_batch_matches_reference_row_loop_fp32(device):
         recorder.begin()
         got = runner.forward_batch(seqs, chunks, return_all_logits=all_logits,
                                    padding_masks=padding)
-        want, attended = oracle.forward(keys, start, chunks, padding)
+        calls = recorder.calls[-1]
+        shared = {i: (_pack(c["k"]), _pack(c["v"].reshape(len(seqs), count, 2, 64)
+                                           .transpose(1, 2))) for i, c in calls.items()}
+        want, attended = oracle.forward(keys, start, chunks, padding, shared_kv=shared)
         pads = None if padding is None else [np.asarray(p, bool) for p in padding]
         for index, out in enumerate(attended):
-            rec = recorder.calls[-1][index]
-            o = rec["o"].reshape(out.shape)
+            o = calls[index]["o"].reshape(out.shape)
             assert_attention_close(o, out)
             attention = runner.model.model.layers[index].self_attn
-            v = rec["v"].reshape(len(seqs), count, 2, 64).transpose(1, 2)
             assert_attention_close(o, fed.attend(index, [(k, start, count) for k in keys],
-                                                 _pack(rec["q"]), _pack(rec["k"]), _pack(v),
+                                                 _pack(calls[index]["q"]), *shared[index],
                                                  attention.scale, pads,
                                                  window=attention.window))
         for row, logits in enumerate(got):

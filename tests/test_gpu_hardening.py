@@ -7,8 +7,8 @@ workloads, each against the oracle (online_attention.py:74-219 per row):
   exponent instead; attention is linear in V, so V scales times 2^k give outputs 2^k
   as large, within the tolerance scaled the same way;
 * extreme finite scores, after the reference's own test
-  (tests/unit/test_inference_online_attention.py:79-98: q x 100, k x 100), in decode
-  rows (both split modes) and chunk rows;
+  (tests/unit/test_inference_online_attention.py:79-98: q x 100, k x 100, against a
+  float64 oracle), in decode rows (both split modes) and chunk rows;
 * the checks on a caller's ``out`` and ``workspace``, and a ``max_query_len`` smaller
   than a row's query count (which would leave that row unwritten) raising the index
   flag."""
@@ -19,7 +19,7 @@ import torch
 
 from aster_amd import KVQuantization, PagedKVCache
 from aster_amd import workloads as wl
-from tests.gpu_util import assert_attention_close, oracle_decode
+from tests.gpu_util import arena_numpy, assert_attention_close, oracle_decode
 
 pytestmark = pytest.mark.gpu
 
@@ -98,6 +98,42 @@ def test_mixed_v_scale_ranges_within_rows(device, fmt, part):
     assert_attention_close(out, oracle_decode(w, cache, q), atol=2e-3 * 2.0 ** 12)
 
 
+def _fp32_score_sensitivity(w, cache, query, exact):
+    """Per output element, sum_t w_t |V_t - o| eps_t: how far the attention output of a
+    query moves (to first order: d o / d s_t = w_t (V_t - o)) when each score s_t
+    carries eps_t = 4 sqrt(D) 2^-24 sum_d |q_d k_td| scale of fp32 rounding, with the
+    exact weights and values (float64, dequantized codes, causal chunk positions)."""
+    kc, ks, vc, vs = arena_numpy(cache)
+    q = query.double().cpu().numpy()
+    dim, group = w.head_dim, w.num_q_heads // w.num_kv_heads
+    qlens = w.q_lens
+    extra = np.zeros_like(exact)
+    cursor = 0
+    for b, ctx in enumerate(w.context_lens.tolist()):
+        n = int(qlens[b])
+        if n == 0 or ctx == 0:
+            cursor += n
+            continue
+        pages = w.block_tables[b][: (ctx + 15) // 16]
+        keys = kc[pages].transpose(1, 0, 2, 3).reshape(w.num_kv_heads, -1, dim)[:, :ctx]
+        kscl = ks[pages].transpose(1, 0, 2).reshape(w.num_kv_heads, -1)[:, :ctx]
+        vals = vc[pages].transpose(1, 0, 2, 3).reshape(w.num_kv_heads, -1, dim)[:, :ctx]
+        vscl = vs[pages].transpose(1, 0, 2).reshape(w.num_kv_heads, -1)[:, :ctx]
+        k = keys.astype(np.float64) * kscl[..., None]
+        v = vals.astype(np.float64) * vscl[..., None]
+        for i in range(n):
+            pos = ctx - n + i
+            for h in range(w.num_q_heads):
+                qh, kh, vh = q[cursor + i, h], k[h // group, : pos + 1], v[h // group, : pos + 1]
+                s = kh @ qh * w.scale
+                p = np.exp(s - s.max())
+                p /= p.sum()
+                eps = 4 * np.sqrt(dim) * 2.0 ** -24 * (np.abs(kh) @ np.abs(qh)) * w.scale
+                extra[cursor + i, h] = (p * eps) @ np.abs(vh - exact[cursor + i, h])
+        cursor += n
+    return extra
+
+
 @pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("part", [0, 512])
@@ -113,7 +149,17 @@ def test_extreme_finite_scores(device, qdtype, dim, part):
         q = (wl.queries(w, device).float() * 100.0).to(qdtype)
         out = _attend(cache, w, q, tables, lens, partition_tokens=part)
         assert torch.isfinite(out).all()
-        assert_attention_close(out, oracle_decode(w, cache, q))
+        # Scores of ~1e4 carry ~1e-3 of rounding in any fp32 evaluation (the
+        # reference's own included), which moves the output where the top keys nearly
+        # tie: each element is held to the tolerance around the exact (float64) result,
+        # widened by the softmax's first-order response to that rounding (zero where
+        # the attention is well posed).
+        exact = oracle_decode(w, cache, q, fp64=True)
+        extra = _fp32_score_sensitivity(w, cache, q, exact)
+        err = np.abs(out.double().cpu().numpy() - exact)
+        bound = 2e-3 + 1e-2 * np.abs(exact) + extra
+        assert (err <= bound).all(), (float((err - bound).max()), int((err > bound).sum()))
+        assert (extra > 2e-3).any(-1).mean() < 0.05  # ill-posed (query, head) rows are rare
 
 
 def test_out_and_workspace_are_checked(device):
