@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "astr_kv_write_key_valid",
     "astr_paged_attention_i8",
     "astr_paged_attention_varlen_i8",
+    "astr_paged_attention_i8_noalloc",
     "astr_paged_attention_i8_workspace_bytes",
     "astr_kv_copy_blocks",
     "astr_last_error",
@@ -93,6 +94,11 @@ def lib():
             c_i32, c_i32, ctypes.c_float, c_i32, c_i32, c_vp, c_sz, c_vp, c_vp,
         ]
         handle.astr_paged_attention_i8.restype = ctypes.c_int
+        handle.astr_paged_attention_i8_noalloc.argtypes = [
+            desc_p, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i32, c_vp, c_i32,
+            c_i32, c_i32, ctypes.c_float, c_i32, c_i32, c_vp, c_vp,
+        ]
+        handle.astr_paged_attention_i8_noalloc.restype = ctypes.c_int
         handle.astr_paged_attention_varlen_i8.argtypes = [
             desc_p, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i32, c_i32, c_i32,
             c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, ctypes.c_float, c_i32, c_i32, c_vp, c_sz,

@@ -80,12 +80,15 @@ Layout partitioned_layout(int32_t num_seqs, int32_t num_q_heads, int32_t head_di
   return w;
 }
 
+// max_waves > 0 limits the capacity (the allocation-free entry point's fixed scratch);
+// the layout never holds fewer waves than the block count needs.
 Layout streamk_layout(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                       int32_t head_dim, int32_t max_context_len, int32_t window,
-                      int64_t launch_waves) {
+                      int64_t max_waves) {
   const int64_t need = (max_total_blocks(num_seqs, num_kv_heads, max_context_len, window) +
                         kMaxBlocksPerWaveSK - 1) / kMaxBlocksPerWaveSK;
   int64_t cap = (int64_t)device_cus() * kMaxResidentWavesPerCU;
+  if (max_waves > 0 && cap > max_waves) cap = max_waves / kWaves * kWaves;
   cap = cap > need ? cap : need;
   cap = (cap + kWaves - 1) / kWaves * kWaves;
   const int64_t group = num_q_heads / num_kv_heads;
@@ -93,8 +96,18 @@ Layout streamk_layout(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_head
   w.seq_bytes = align256(((size_t)num_seqs + 1) * sizeof(int32_t));
   w.o_bytes = align256((size_t)cap * 2 * group * head_dim * sizeof(float));
   w.ml_bytes = align256((size_t)cap * 2 * group * 2 * sizeof(float));
-  w.waves = launch_waves > 0 ? (launch_waves > cap ? cap : launch_waves) : cap;
+  w.waves = cap;
   return w;
+}
+
+// Bytes of one stream-K wave's partials (two slots of the group's rows) and the most
+// waves whose partials fit in `bytes` beside the per-sequence table.
+int64_t streamk_waves_in(size_t bytes, int32_t num_seqs, int32_t num_q_heads,
+                         int32_t num_kv_heads, int32_t head_dim) {
+  const size_t group = (size_t)(num_q_heads / num_kv_heads);
+  const size_t per_wave = 2 * group * ((size_t)head_dim + 2) * sizeof(float);
+  const size_t fixed = align256(((size_t)num_seqs + 1) * sizeof(int32_t)) + 2 * 256;
+  return bytes > fixed ? (int64_t)((bytes - fixed) / per_wave) : 0;
 }
 
 // Fewest waves that keep every wave at kMaxBlocksPerWaveSK blocks or less.
@@ -142,7 +155,7 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
                     int32_t block_table_stride, const int32_t* context_lens, int32_t num_seqs,
                     int32_t num_q_heads, int32_t max_context_len, float scale, int32_t window,
                     int32_t partition_tokens, void* workspace, size_t workspace_bytes,
-                    int32_t* err_flag, void* stream) {
+                    int32_t* err_flag, void* stream, bool fixed_scratch = false) {
   using namespace astr;
   using namespace astr::attn;
   if (cache == nullptr || err_flag == nullptr)
@@ -196,16 +209,29 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
   const int64_t parts = max_parts_for(max_context_len, pt);
   if (!streamk && parts > 65535)
     return fail(ASTR_EUNSUPPORTED, "too many split-K partitions (%lld)", (long long)parts);
-  const size_t need = astr_paged_attention_i8_workspace_bytes(
-      num_seqs, num_q_heads, cache->num_kv_heads, cache->head_dim, max_context_len,
-      partition_tokens);
+  // a caller's workspace is sized by astr_paged_attention_i8_workspace_bytes; the fixed
+  // scratch of the allocation-free entry point caps the stream-K capacity instead
+  const int64_t sk_limit = fixed_scratch ? streamk_waves_in(workspace_bytes, num_seqs,
+                                                            num_q_heads, cache->num_kv_heads,
+                                                            cache->head_dim) : 0;
+  if (fixed_scratch && streamk && sk_limit < kWaves)
+    return fail(ASTR_EINVAL, "the allocation-free entry point's %zu-byte scratch holds too few "
+                "stream-K partials for %d sequences x %d query heads", workspace_bytes, num_seqs,
+                num_q_heads);
+  const Layout ws = streamk ? streamk_layout(num_seqs, num_q_heads, cache->num_kv_heads,
+                                             cache->head_dim, max_context_len, 0, sk_limit)
+                            : partitioned_layout(num_seqs, num_q_heads, cache->head_dim, parts);
+  const size_t need = fixed_scratch ? ws.total()
+                                    : astr_paged_attention_i8_workspace_bytes(
+                                          num_seqs, num_q_heads, cache->num_kv_heads,
+                                          cache->head_dim, max_context_len, partition_tokens);
+  if (fixed_scratch && need > workspace_bytes)
+    return fail(ASTR_EINVAL, "this launch needs %zu bytes of split-K scratch, more than the "
+                "%zu bytes the allocation-free entry point holds", need, workspace_bytes);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need ||
                    (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0))
     return fail(ASTR_EINVAL, "a 256-byte aligned workspace of %zu bytes is required (%zu given)",
                 need, workspace_bytes);
-  const Layout ws = streamk ? streamk_layout(num_seqs, num_q_heads, cache->num_kv_heads,
-                                             cache->head_dim, max_context_len, 0, 0)
-                            : partitioned_layout(num_seqs, num_q_heads, cache->head_dim, parts);
 
   AttnArgs a{};
   a.q_start = query_start_loc;
@@ -277,4 +303,59 @@ extern "C" int astr_paged_attention_varlen_i8(
                          max_query_len, causal, block_tables, block_table_stride, context_lens,
                          num_seqs, num_q_heads, max_context_len, scale, window, partition_tokens,
                          workspace, workspace_bytes, err_flag, stream);
+}
+
+// ---- allocation-free decode entry point: split-K partials in a fixed device array
+
+namespace {
+
+// Scratch of astr_paged_attention_i8_noalloc, one copy per GPU for the life of the
+// process. In host code `scratch` only names the symbol: its device address comes from
+// hipGetSymbolAddress, once per device (scratch_on_current_device).
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+
+// The address of `scratch` on the current device in *ptr, looked up with that device
+// current the first time and kept per device. Returns 0, or an error code with
+// astr_last_error set.
+int scratch_on_current_device(void** ptr) {
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {nullptr};
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return astr::hip_fail(err, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return astr::fail(ASTR_EUNSUPPORTED, "device %d beyond the %d the scratch table holds", dev,
+                      kMaxDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return astr::hip_fail(err, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return astr::fail(ASTR_EINVAL, "hipGetSymbolAddress(scratch) gave NULL");
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int astr_paged_attention_i8_noalloc(
+    const astr_paged_kv* cache, const void* query, int32_t q_dtype, int64_t q_token_stride,
+    int64_t q_head_stride, void* out, int64_t out_token_stride, int64_t out_head_stride,
+    const int32_t* block_tables, int32_t block_table_stride, const int32_t* context_lens,
+    int32_t num_seqs, int32_t num_q_heads, int32_t max_context_len, float scale, int32_t window,
+    int32_t partition_tokens, int32_t* err_flag, void* stream) {
+  if (num_seqs <= 0) return num_seqs == 0 ? 0 : astr::fail(ASTR_EINVAL, "num_seqs must be >= 0");
+  void* ws = nullptr;
+  const int rc = scratch_on_current_device(&ws);
+  if (rc != 0) return rc;
+  return paged_attention(cache, query, q_dtype, q_token_stride, q_head_stride, out,
+                         out_token_stride, out_head_stride, nullptr, num_seqs, 1, 1, block_tables,
+                         block_table_stride, context_lens, num_seqs, num_q_heads, max_context_len,
+                         scale, window, partition_tokens, ws, kNoAllocScratchBytes, err_flag,
+                         stream, true);
 }

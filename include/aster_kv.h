@@ -159,6 +159,27 @@ int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query, int32
                             int32_t* err_flag, void* stream);
 
 /*
+ * astr_paged_attention_i8 without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation): no counterpart in the reference. The split-K partials live
+ * in a 32 MiB device array that the library holds on every GPU it runs on until the
+ * process ends; its address is looked up once per device, with that device current,
+ * on the first call (make that first call outside graph capture). Same arguments,
+ * kernels and results as astr_paged_attention_i8; a launch whose partials do not fit
+ * returns ASTR_EINVAL (the stream-K path uses at most the waves that fit). Calls
+ * on one GPU share the array and the last call's contents stay in it: calls that
+ * overlap on one GPU (different streams without ordering) race. Nothing is allocated.
+ */
+int astr_paged_attention_i8_noalloc(const astr_paged_kv* cache, const void* query,
+                                    int32_t q_dtype, int64_t q_token_stride,
+                                    int64_t q_head_stride, void* out, int64_t out_token_stride,
+                                    int64_t out_head_stride, const int32_t* block_tables,
+                                    int32_t block_table_stride, const int32_t* context_lens,
+                                    int32_t num_seqs, int32_t num_q_heads,
+                                    int32_t max_context_len, float scale, int32_t window,
+                                    int32_t partition_tokens, int32_t* err_flag, void* stream);
+
+/*
  * Ragged paged attention for a continuous-batching step that mixes prompt
  * chunks (several query tokens per sequence, chunked prefill) with decode rows.
  * Replaces the same per-row online_attention calls of
