@@ -18,9 +18,19 @@ constexpr int kMaxBlocksPerWave = 64;  // block ids one wave keeps in a register
 // stream-K: blocks one wave may stream (its block list goes in windows of 64)
 constexpr int kMaxBlocksPerWaveSK = 1024;
 constexpr float kRescaleSlack = 8.0f;  // p = exp2(s - m) <= 2^8 between rescales
-// PV weights p * v_scale * wsc are rounded to f16: with p <= 2^8 and every
-// v_scale * wsc <= 2^7 they stay below 2^15 (f16's largest finite value is 65504).
+// PV weights p * v_scale are rounded to f16: with p <= 2^8 (kRescaleSlack) and every
+// v_scale <= kVWeightCap they stay below 2^15 (f16's largest finite value is 65504).
 constexpr float kVWeightCap = 128.0f;
+
+// Larger V scales in the decode kernels: the piece's running maximum m is the scores'
+// running maximum plus koff (a non-negative integer), so every weight p = exp2(s - m)
+// and the normaliser l carry 2^-koff, which cancels in acc / l and in the merge of
+// (m, l, acc) partials. A block whose (weight-scaled) V scales exceed vlim =
+// kVWeightCap * 2^koff grows koff by the exponent they need, through the same
+// rescale of l and acc as a new score maximum. Every piece starts at {0, kVWeightCap}.
+struct VRange {
+  float koff, vlim;
+};
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
@@ -318,11 +328,19 @@ struct QueryRaw {
   uint4 w[D / 64][2];
 };
 
+// Lane (qg, r)'s part of query row r of kv head kvh, token row tok (rows r >= G read
+// row 0 and are zeroed where they are quantized).
+template <typename QT, int G>
+__device__ __forceinline__ const QT* query_lane_ptr(const AttnArgs& a, int tok, int kvh, int r,
+                                                    int qg) {
+  return static_cast<const QT*>(a.q) + (int64_t)tok * a.q_tok +
+         (int64_t)(kvh * G + (r < G ? r : 0)) * a.q_head + 16 * qg;
+}
+
 template <typename QT, int D, int G>
 __device__ __forceinline__ void load_query(const AttnArgs& a, int tok, int kvh, int r, int qg,
                                            QueryRaw<D>& q) {
-  const QT* qp = static_cast<const QT*>(a.q) + (int64_t)tok * a.q_tok +
-                 (int64_t)(kvh * G + (r < G ? r : 0)) * a.q_head + 16 * qg;
+  const QT* qp = query_lane_ptr<QT, G>(a, tok, kvh, r, qg);
 #pragma unroll
   for (int h = 0; h < D / 64; ++h) {
     const uint4* src = reinterpret_cast<const uint4*>(qp + 64 * h);
@@ -367,11 +385,43 @@ struct QueryColumn {  // the lane's 16 elements of each 64-wide d chunk, as load
 // 2^-11 of 2^14 x (~29 bits). Every term is in [-64, 64]; the same raw column always
 // gives the same terms.
 // Cross-lane: uniform control flow.
+// The int8 terms of one query element xv (already lifted) at the column's inv, as floats
+// whose low bytes are the terms' two's-complement bytes: adding kQRound (1.5 * 2^23, unit
+// in the last place 1) to a value below 2^22 in magnitude rounds it to an integer held in
+// the low mantissa bits. Each fma rounds once; hi = rint(xv * inv / 128) and
+// lo = rint(xv * inv - 128 hi) (ties to even, |hi| <= 127, |lo| <= 64); with kTerms > 2,
+// lo2 = rint(128 r2) where r2 = xv * inv - (128 hi + lo) (|r2| <= 1/2), and with
+// kTerms > 3, lo3 = rint(128 (128 r2 - lo2)).
+constexpr float kQRound = 12582912.f;
+struct QueryTerms {
+  float hi, lo, lo2, lo3;
+};
+template <int kTerms>
+__device__ __forceinline__ QueryTerms query_terms(float xv, float inv) {
+  QueryTerms t;
+  t.hi = __builtin_fmaf(xv, inv * (1.f / 128.f), kQRound);  // inv / 128: exact
+  const float hv = t.hi - kQRound;
+  t.lo = __builtin_fmaf(xv, inv, __builtin_fmaf(hv, -128.f, kQRound));
+  if constexpr (kTerms > 2) {
+    // residual of Q = 128 hi + lo (exact integers), one rounding: |r2| <= 1/2
+    const float q2 = __builtin_fmaf(hv, 128.f, t.lo - kQRound);
+    const float r2 = __builtin_fmaf(xv, inv, -q2);
+    t.lo2 = __builtin_fmaf(r2, 128.f, kQRound);
+    if constexpr (kTerms > 3) {
+      const float r3 = __builtin_fmaf(r2, 128.f, kQRound - t.lo2);  // exact
+      t.lo3 = __builtin_fmaf(r3, 128.f, kQRound);
+    }
+  }
+  return t;
+}
+
 template <typename QT, int D, int kTerms = 2>
 __device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, bool valid,
                                                  float qk_scale_log2, int4_t (&qhi)[D / 64],
                                                  int4_t (&qlo)[D / 64],
-                                                 int4_t* qlo2 = nullptr, int4_t* qlo3 = nullptr) {
+                                                 int4_t* qlo2 = nullptr, int4_t* qlo3 = nullptr,
+                                                 float* inv_out = nullptr,
+                                                 float* lift_out = nullptr) {
   static_assert(kTerms >= 2 && kTerms <= 4, "query terms");
   constexpr int kVec = 16 / (int)sizeof(QT);  // elements per 16-byte load
   float x[D / 64][16];
@@ -399,8 +449,8 @@ __device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, 
   const float factor = finite ? qk_scale_log2 * (mx / (float)kQRange) : __builtin_nanf("");
   // kQRange / mx overflows for mx below 2^-114: columns under 2^-64 are lifted by 2^64
   // first (exact), which leaves Q unchanged
-  if (__ballot(mx > 0.f && mx < 0x1p-64f) != 0) {
-    const float up = mx > 0.f && mx < 0x1p-64f ? 0x1p64f : 1.f;
+  const float up = mx > 0.f && mx < 0x1p-64f ? 0x1p64f : 1.f;
+  if (__ballot(up != 1.f) != 0) {
 #pragma unroll
     for (int h = 0; h < D / 64; ++h)
 #pragma unroll
@@ -408,12 +458,8 @@ __device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, 
     mx *= up;
   }
   const float inv = (finite && mx > 0.f) ? (float)kQRange / mx : 0.f;
-  // hi = rint(q * inv / 128) and lo = rint(q * inv - 128 hi), ties to even, |hi| <= 127,
-  // |lo| <= 64: adding kRound (1.5 * 2^23, unit in the last place 1) to a value below
-  // 2^22 in magnitude rounds it to an integer held in the low mantissa bits, so the low
-  // byte of the sum's bit pattern is the two's-complement byte. Each fma rounds once.
-  constexpr float kRound = 12582912.f;
-  const float inv128 = inv * (1.f / 128.f);  // exact: a power of two
+  if (inv_out != nullptr) *inv_out = inv;
+  if (lift_out != nullptr) *lift_out = up;
 #pragma unroll
   for (int h = 0; h < D / 64; ++h)
 #pragma unroll
@@ -421,23 +467,11 @@ __device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, 
       uint32_t hb[4], lb[4], fb[4], gb[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float xv = x[h][4 * w + e];
-        const float th = __builtin_fmaf(xv, inv128, kRound);
-        const float hv = th - kRound;
-        const float tl = __builtin_fmaf(xv, inv, __builtin_fmaf(hv, -128.f, kRound));
-        hb[e] = __builtin_bit_cast(uint32_t, th);
-        lb[e] = __builtin_bit_cast(uint32_t, tl);
-        if constexpr (kTerms > 2) {
-          // residual of Q = 128 hi + lo (exact integers), one rounding: |r2| <= 1/2
-          const float q2 = __builtin_fmaf(hv, 128.f, tl - kRound);
-          const float r2 = __builtin_fmaf(xv, inv, -q2);
-          const float t2 = __builtin_fmaf(r2, 128.f, kRound);
-          fb[e] = __builtin_bit_cast(uint32_t, t2);
-          if constexpr (kTerms > 3) {
-            const float r3 = __builtin_fmaf(r2, 128.f, kRound - t2);  // exact
-            gb[e] = __builtin_bit_cast(uint32_t, __builtin_fmaf(r3, 128.f, kRound));
-          }
-        }
+        const QueryTerms t = query_terms<kTerms>(x[h][4 * w + e], inv);
+        hb[e] = __builtin_bit_cast(uint32_t, t.hi);
+        lb[e] = __builtin_bit_cast(uint32_t, t.lo);
+        if constexpr (kTerms > 2) fb[e] = __builtin_bit_cast(uint32_t, t.lo2);
+        if constexpr (kTerms > 3) gb[e] = __builtin_bit_cast(uint32_t, t.lo3);
       }
       qhi[h][w] = (int)low_bytes(hb);
       qlo[h][w] = (int)low_bytes(lb);
@@ -524,22 +558,28 @@ struct QkOperand {
 };
 template <int D>
 struct QkOperand<D, kInt8> {
-  int4_t hi[D / 64], lo[D / 64], lo2[D / 64];
+  int4_t hi[D / 64], lo[D / 64];
   // K scale above which a block takes the third query term: the two-term query's
   // worst-case score error, 1/2 step times 127 D per unit of K scale times the score
   // factor, would exceed kFineScoreError (base-2 units) there
   float ks_fine;
+  // what the third term is rebuilt from: the lane's query elements (query_lane_ptr)
+  // and the column's quantization (query_column_i8)
+  const void* qptr;
+  float inv, lift;
 };
 // Largest worst-case score error (base 2) a block may carry from the two-term query
-// before the third term is added: typical errors are ~sqrt(D) times smaller, a few
-// 1e-4 of a softmax weight.
-constexpr float kFineScoreError = 1.f / 32.f;
+// before the third term is added. The worst case aligns every code at 127 with every
+// rounding; the typical error is ~sqrt(12 D) max|k| / rms|k| / 2 (about 50 at D = 128)
+// times smaller, a few 1e-3 of a softmax weight at most. (At 1/32, K rows with x8
+// outliers, as in BASELINE config 5, took the third term on most blocks.)
+constexpr float kFineScoreError = 1.f / 8.f;
 
 // Builds the operand of query row r (lane layout of QueryRaw; rows r >= G are zero)
 // and returns its score factor, code scale included. Cross-lane: uniform control flow.
 template <typename QT, int D, int KF>
 __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, float qk_scale_log2,
-                                            QkOperand<D, KF>& op) {
+                                            QkOperand<D, KF>& op, const QT* qptr) {
   if constexpr (KF == kInt8) {
     static_assert(sizeof(QT) == 2, "16-bit queries (fp32 queries take the exact VALU kernel)");
     QueryColumn<QT, D> col;
@@ -548,8 +588,10 @@ __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, f
       col.w[h][0] = q.w[h][0];
       col.w[h][1] = q.w[h][1];
     }
-    const float cf = query_column_i8<QT, D, 3>(col, gvalid, qk_scale_log2, op.hi, op.lo, op.lo2);
+    const float cf = query_column_i8<QT, D>(col, gvalid, qk_scale_log2, op.hi, op.lo, nullptr,
+                                            nullptr, &op.inv, &op.lift);
     op.ks_fine = (kFineScoreError / (63.5f * D)) / cf;  // +inf for cf = 0, NaN for NaN
+    op.qptr = qptr;
     return cf;
   } else {
     return query_operand<QT, D>(q, gvalid, qk_scale_log2, op.op) * code_scale<KF>();
@@ -567,20 +609,38 @@ __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, f
 // layout P^T needs, so the online softmax stays in registers. Tokens outside
 // [kv_begin, ctx) are masked; `tok_base` is the block's first token position.
 // Cross-lane (ballots, shuffles): call in uniform control flow.
-// `wsc` is the piece's weight factor (a power of two; start it at v_weight_scale<KF>()):
-// the PV weights are p * v_scale * wsc. A block whose V scales times wsc exceed
-// kVWeightCap lowers wsc by a power of two and scales the accumulators by the same
-// exact factor (f16 weights would overflow otherwise); end_piece undoes it.
-template <int D, int G, int KF = kInt8>
+// `vr` keeps the PV weights p * v_scale in f16 range for large V scales (VRange).
+template <typename QT, int D, int G, int KF = kInt8>
 __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF>& qop, float cf,
                                            int tok_base, int kv_begin, int ctx, int r, int qg,
                                            float4_t (&acc)[D / 16 + 1], float& m, float& l,
-                                           float& wsc, bool& bad_score, bool masks = false) {
+                                           VRange& vr, bool& bad_score, bool masks = false) {
   using S = Stage<D>;
   constexpr int KCH = D / 64;
   constexpr int VB = D / 16;
   constexpr int NPV = D / 16;
   const bool gvalid = r < G;
+  // V scales, times 2^8 for FP8 codes (E4M3FN operands carry 2^-8; E5M2 weights carry
+  // 2^8, as does the normaliser of this format); finite, and the same on the 16 lanes
+  // of a token group. Beyond vr.vlim they grow the running maximum's offset first: its
+  // own rescale of l and acc, before any score of the block exists.
+  const float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg) * v_weight_scale<KF>();
+  {
+    const float vsm = fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3]));
+    if (__ballot(vsm > vr.vlim) != 0) {
+      float wm = fmaxf(vsm, shfl_xor(vsm, 16));
+      wm = fmaxf(wm, shfl_xor(wm, 32));
+      int x;
+      frexpf(wm / vr.vlim, &x);  // in [2^(x-1), 2^x), x >= 1
+      vr.koff += (float)x;
+      vr.vlim = ldexpf(vr.vlim, x);
+      const float alpha = ldexpf(1.f, -x);  // m + x is the new maximum (with offset)
+      m += (float)x;
+      l *= alpha;
+#pragma unroll
+      for (int n = 0; n <= NPV; ++n) acc[n] *= alpha;
+    }
+  }
   const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
   float4_t s4;
   if constexpr (KF == kInt8) {
@@ -597,12 +657,33 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
     for (int h = 0; h < KCH; ++h) si = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop.lo[h], si, 0, 0, 0);
     s4 = float4_t{(float)si[0], (float)si[1], (float)si[2], (float)si[3]};
     // large scores: add the third query term, K.lo2 / 128 (exact int32, then scaled
-    // by a power of two), wherever a block's K scales reach the column's threshold
+    // by a power of two), wherever a block's K scales reach the column's threshold; the
+    // term is rebuilt from the query elements at the column's quantization, so that it
+    // completes the hi and lo terms used above (a rare path: nothing of it stays live)
     const float kmx = fmaxf(fmaxf(ks[0], ks[1]), fmaxf(ks[2], ks[3]));
     if (__ballot(kmx > qop.ks_fine) != 0) {
       int4_t sf = {0, 0, 0, 0};
+#pragma nounroll
+      for (int h = 0; h < KCH; ++h) {
+        const int4_t kh = *reinterpret_cast<const int4_t*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
+        constexpr int kVec = 16 / (int)sizeof(QT);
+        uint4 w[16 / kVec];
 #pragma unroll
-      for (int h = 0; h < KCH; ++h) sf = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop.lo2[h], sf, 0, 0, 0);
+        for (int c = 0; c < 16 / kVec; ++c)
+          w[c] = reinterpret_cast<const uint4*>(static_cast<const QT*>(qop.qptr) + 64 * h)[c];
+        const QT* e = reinterpret_cast<const QT*>(w);
+        int4_t q2;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          uint32_t fb[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            fb[i] = __builtin_bit_cast(
+                uint32_t, query_terms<3>(to_float<QT>(e[4 * k + i]) * qop.lift, qop.inv).lo2);
+          q2[k] = (int)low_bytes(fb);
+        }
+        sf = __builtin_amdgcn_mfma_i32_16x16x64_i8(kh, q2, sf, 0, 0, 0);
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) s4[j] = __builtin_fmaf((float)sf[j], 1.f / 128.f, s4[j]);
     }
@@ -619,24 +700,6 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
         const half8_t kop = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
         s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop.op[2 * h + sub], s4, 0, 0, 0);
       }
-    }
-  }
-  // V scales times the weight factor (2^8 at the start of a piece for FP8 codes:
-  // E4M3FN operands carry 2^-8; E5M2 weights carry 2^8, as does the normaliser of
-  // this format). Scales are finite and the same on the 16 lanes of a token group.
-  float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg) * wsc;
-  {
-    const float vsm = fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3]));
-    if (__ballot(vsm > kVWeightCap) != 0) {
-      float wm = fmaxf(vsm, shfl_xor(vsm, 16));
-      wm = fmaxf(wm, shfl_xor(wm, 32));
-      int e;
-      frexpf(wm * (1.f / kVWeightCap), &e);  // wm / cap in [2^(e-1), 2^e), e >= 1
-      const float f = ldexpf(1.f, -e);       // wm * f < cap
-      wsc *= f;
-      vs *= f;
-#pragma unroll
-      for (int n = 0; n <= NPV; ++n) acc[n] *= f;
     }
   }
   uint32_t vw[4][VB / 4];
@@ -692,7 +755,7 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
     float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
     tmax = fmaxf(tmax, shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, shfl_xor(tmax, 32));
-    const float mn = fmaxf(m, tmax);
+    const float mn = fmaxf(m, tmax + vr.koff);
     const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
     l *= alpha;
 #pragma unroll
@@ -736,20 +799,13 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
 
 // Ends a piece's accumulation: with biased V operands, subtracts kVBias times the
 // weight sum of head r (row 0 of acc[D/16], held by lane (0, r)) from every output of
-// that head; then undoes a lowered weight factor (exact: a power of two), so that
-// every piece's accumulators carry v_weight_scale<KF>(). Cross-lane: call in uniform
-// control flow.
+// that head. Cross-lane: call in uniform control flow.
 template <int D, int KF>
-__device__ __forceinline__ void end_piece(float4_t (&acc)[D / 16 + 1], int r, float wsc) {
+__device__ __forceinline__ void end_piece(float4_t (&acc)[D / 16 + 1], int r) {
   if constexpr (biased_v<D, KF>()) {
     const float b = kVBias * __shfl(acc[D / 16][0], r, kWave);
 #pragma unroll
     for (int n = 0; n < D / 16; ++n) acc[n] -= float4_t{b, b, b, b};
-  }
-  if (wsc != v_weight_scale<KF>()) {
-    const float undo = v_weight_scale<KF>() / wsc;
-#pragma unroll
-    for (int n = 0; n < D / 16; ++n) acc[n] *= undo;
   }
 }
 

@@ -165,7 +165,8 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   if (NS == 3 && 2 < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, 2), kvh, lane, st2);
 
   QkOperand<D, KF> qop;
-  const float cf = qk_operand<QT, D, KF>(qraw, gvalid, a.qk_scale_log2, qop);
+  const float cf = qk_operand<QT, D, KF>(qraw, gvalid, a.qk_scale_log2, qop,
+                                         query_lane_ptr<QT, G>(a, tok, kvh, r, qg));
   float4_t acc[NPV + 1];  // [NPV]: weight sums (INT8)
 #pragma unroll
   for (int n = 0; n <= NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -173,7 +174,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   // all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
   float m = gvalid ? -FLT_MAX : 0.f;
   float l = 0.f;
-  float wsc = v_weight_scale<KF>();
+  VRange vr = {0.f, kVWeightCap};
   bool bad_score = false;
 
   auto step = [&](int i, char* st) __attribute__((always_inline)) {
@@ -182,8 +183,8 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
     if (later >= 2) wait_vmcnt<2 * S::kLoads>();
     else if (later == 1) wait_vmcnt<S::kLoads>();
     else wait_vmcnt<0>();
-    mfma_block<D, G, KF>(st, qop, cf, (first + kWaves * i) * kBlockTokens, row.kv_begin, row.ctx, r,
-                     qg, acc, m, l, wsc, bad_score, a.cache.key_valid != nullptr);
+    mfma_block<QT, D, G, KF>(st, qop, cf, (first + kWaves * i) * kBlockTokens, row.kv_begin, row.ctx, r,
+                     qg, acc, m, l, vr, bad_score, a.cache.key_valid != nullptr);
     // refill this stage with block i + NS (its LDS reads above fed the MFMAs)
     if (i + NS < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, i + NS), kvh, lane, st);
   };
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
 
   // ---- per-wave state to LDS (aliases the stages: wait for every wave first)
-  end_piece<D, KF>(acc, r, wsc);
+  end_piece<D, KF>(acc, r);
   l += shfl_xor(l, 16);
   l += shfl_xor(l, 32);
   l *= norm_scale<KF>();  // the factor the PV weights carry

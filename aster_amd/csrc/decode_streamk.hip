@@ -227,7 +227,8 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     else if (first == 2) wait_vmcnt<2 * S::kLoads>();
     else wait_vmcnt<S::kLoads>();
     lds_query<QT, D>(stage(NS - 1), gvalid ? r : 0, qg, qr);
-    cf = qk_operand<QT, D, KF>(qr, gvalid, a.qk_scale_log2, qop);
+    cf = qk_operand<QT, D, KF>(qr, gvalid, a.qk_scale_log2, qop,
+                               query_lane_ptr<QT, G>(a, s_tok[row0 % nseq], row0 / nseq, r, qg));
     if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (their values are consumed)
     if (64 < nblk) request_ids(1);
   }
@@ -247,7 +248,8 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     const int64_t pfb = s_cu[pseq];  // first block of the row in the per-head order
     if (i > 0) {  // a new row starts inside this wave's range
       load_query<QT, D, G>(a, s_tok[pseq], pkvh, r, qg, qr);
-      cf = qk_operand<QT, D, KF>(qr, gvalid, a.qk_scale_log2, qop);
+      cf = qk_operand<QT, D, KF>(qr, gvalid, a.qk_scale_log2, qop,
+                                 query_lane_ptr<QT, G>(a, s_tok[pseq], pkvh, r, qg));
     }
 #pragma unroll
     for (int k = 0; k <= NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -255,7 +257,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     // are all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
     m = gvalid ? -FLT_MAX : 0.f;
     l = 0.f;
-    float wsc = v_weight_scale<KF>();
+    VRange vr = {0.f, kVWeightCap};
     const int pos0 = (psp.first_blk + (int)(b0 + i - pfb)) * kBlockTokens;
     for (;;) {
       // the row's blocks in the current window: up to the first lane with another row
@@ -265,8 +267,8 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
       const int iend = beyond ? 64 * cw + (int)__builtin_ctzll(beyond) : wend;
       for (; i < iend; ++i) {
         wait_block(i);
-        mfma_block<D, G, KF>(stage(i), qop, cf, pos0 + (i - pstart) * kBlockTokens,
-                             psp.kv_begin, psp.ctx, r, qg, acc, m, l, wsc, bad_score, masks);
+        mfma_block<QT, D, G, KF>(stage(i), qop, cf, pos0 + (i - pstart) * kBlockTokens,
+                             psp.kv_begin, psp.ctx, r, qg, acc, m, l, vr, bad_score, masks);
         const int nx = i + NS;
         if (nx < nblk && (nx & 63) == 0) {
           // first block of window cw + 1: its ids were requested before block
@@ -293,7 +295,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     // wave, else a partial in slot 0 (the piece starts the wave's range) or 1 (it
     // ends it)
     const int iend = i;
-    end_piece<D, KF>(acc, r, wsc);
+    end_piece<D, KF>(acc, r);
     float lt = l + shfl_xor(l, 16);
     lt += shfl_xor(lt, 32);
     lt *= norm_scale<KF>();  // the factor the PV weights carry

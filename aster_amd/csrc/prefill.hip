@@ -207,7 +207,6 @@ __device__ __forceinline__ void load_query_column(const QT* qp, QueryColumn<QT, 
 template <int D>
 struct QOpI8 {
   int4_t hi[D / 64], lo[D / 64];
-  float ks_fine;  // K scale from which a step adds the finer query terms (QkOperand<D, kInt8>)
 };
 template <int D>
 struct QOpF16 {
@@ -341,42 +340,41 @@ __device__ __forceinline__ int convert_v(const char* st, int lane, int half, uin
 
 // The PV MFMAs of one step: weights p = exp2(u * cfe - m) rounded to f16 for the 32 keys
 // of each block pair, against the slab of that pair, and the row sums from the same
-// rounded weights. kMix: the step's blocks were converted with different exponents;
-// the weights of block b then carry 2^(e_b - ve) (vf[b], at most 1) for the numerator
-// only, so that every block's products are in units of 2^-ve.
-template <int D, int NT, bool kMix>
+// rounded weights. vmix: the step's blocks were converted with different exponents; the
+// weights of block b then carry 2^(e_b - ve) (vf[b], at most 1, exact on f16) for the
+// numerator only (scaled in place after the row sums), so that every block's products
+// are in units of 2^-ve.
+template <int D, int NT>
 __device__ __forceinline__ void prefill_pv(const uint4* vt, const float (&u)[NT][16],
                                            const float (&cfe)[NT], const float (&m)[NT],
-                                           int lane, const half8_t& ones, const half4_t& vf,
-                                           float4_t (&acc)[NT][D / 16 + 1]) {
+                                           int lane, const half8_t& ones, bool vmix,
+                                           const half4_t& vf, float4_t (&acc)[NT][D / 16 + 1]) {
   constexpr int NPV = D / 16;
 #pragma unroll
   for (int pp = 0; pp < 2; ++pp) {
-    half8_t pop[NT], pv[NT];
+    half8_t pop[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         pop[t][i] = (_Float16)__builtin_amdgcn_exp2f(fmaf(u[t][8 * pp + i], cfe[t], -m[t]));
-      if constexpr (kMix) {
-        const _Float16 f0 = vf[2 * pp], f1 = vf[2 * pp + 1];
-        pv[t] = pop[t] * half8_t{f0, f0, f0, f0, f1, f1, f1, f1};
-      } else {
-        pv[t] = pop[t];
-      }
+    // row sums: a V^T row of ones (row 0 of the extra tile) gives sum_k f16(p_k), the
+    // same rounded weights the numerator uses
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      acc[t][NPV] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop[t], acc[t][NPV], 0, 0, 0);
+    if (vmix) {
+      const _Float16 f0 = vf[2 * pp], f1 = vf[2 * pp + 1];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) pop[t] = pop[t] * half8_t{f0, f0, f0, f0, f1, f1, f1, f1};
     }
 #pragma unroll
     for (int n = 0; n < NPV; ++n) {
       const half8_t vop = __builtin_bit_cast(half8_t, vt[pp * (NPV * kWave) + n * kWave + lane]);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pv[t], acc[t][n], 0, 0, 0);
+        acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[t], acc[t][n], 0, 0, 0);
     }
-    // row sums: a V^T row of ones (row 0 of the extra tile) gives sum_k f16(p_k), the
-    // same rounded weights the numerator uses
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-      acc[t][NPV] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop[t], acc[t][NPV], 0, 0, 0);
   }
 }
 
@@ -400,14 +398,12 @@ __device__ __forceinline__ void prefill_pv(const uint4* vt, const float (&u)[NT]
 // the scores are masked to -inf outside the bounds, for padding keys and for unused
 // blocks (whose stages hold stale but finite codes and scales) and checked for
 // non-finite values.
-template <typename QT, int D, int NT>
+template <int D, int NT>
 __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, uint32_t use,
                                              uint32_t bounded, bool masks, int kb0,
                                              const QOp<D> (&qop)[NT],
                                              const float (&cf)[NT], const float (&cfe)[NT],
-                                             const int (&lo)[NT], const int (&hi)[NT],
-                                             const QT* const (&qptr)[NT],
-                                             const bool (&cvalid)[NT], int r,
+                                             const int (&lo)[NT], const int (&hi)[NT], int r,
                                              int qg, const half8_t& ones, bool vmix,
                                              const half4_t& vf,
                                              float4_t (&acc)[NT][D / 16 + 1], float (&m)[NT],
@@ -490,42 +486,6 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int j = 0; j < 4 * NBK; ++j) u[t][j] = (float)sacc[j / 4][t][j % 4] * ks[j / 4][j % 4];
-  // large scores: where the step's K scales reach a column's threshold, the column's
-  // query is read again (the same raw values give the same hi and lo terms) and split
-  // into two finer terms, lo2 and lo3, whose exact int32 dot products with the K codes
-  // (read again from the stages) add S2 / 2^7 + S3 / 2^14 to each score
-  bool fine = false;
-  if constexpr (KF == kInt8) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) fine = fine || kmax > qop[t].ks_fine;
-  }
-  if (__ballot(fine) != 0) {
-    if constexpr (KF == kInt8) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        QueryColumn<QT, D> raw;
-        load_query_column<QT, D>(qptr[t], raw);
-        int4_t qh[KCH], ql[KCH], q2[KCH], q3[KCH];
-        query_column_i8<QT, D, 4>(raw, cvalid[t], 1.f, qh, ql, q2, q3);
-#pragma unroll
-        for (int b = 0; b < NBK; ++b) {
-          const char* st = cur + b * S::kBytes;
-          int4_t s2 = {0, 0, 0, 0}, s3 = {0, 0, 0, 0};
-#pragma unroll
-          for (int h = 0; h < KCH; ++h) {
-            const int4_t kop = *reinterpret_cast<const int4_t*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
-            s2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, q2[h], s2, 0, 0, 0);
-            s3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, q3[h], s3, 0, 0, 0);
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float f = __builtin_fmaf((float)s3[i], 1.f / 128.f, (float)s2[i]);
-            u[t][4 * b + i] = __builtin_fmaf(f, ks[b][i] * (1.f / 128.f), u[t][4 * b + i]);
-          }
-        }
-      }
-    }
-  }
   const bool edge = (use != (1u << NBK) - 1) | (bounded != 0) | unsafe | padded;
   if (edge) {
     asm volatile("");  // keeps this a branch: if-converted, the interior steps would pay for it
@@ -569,10 +529,7 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
   }
   static_assert(NBK == 4, "two block pairs per step");
   const int lane = qg * 16 + r;
-  if (vmix)
-    prefill_pv<D, NT, true>(vt, u, cfe, m, lane, ones, vf, acc);
-  else
-    prefill_pv<D, NT, false>(vt, u, cfe, m, lane, ones, vf, acc);
+  prefill_pv<D, NT>(vt, u, cfe, m, lane, ones, vmix, vf, acc);
 }
 
 // N consecutive outputs from fp32, with 16-byte (or 8-byte) stores.
@@ -703,7 +660,6 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   int lo[NT], hi[NT], ctok[NT], chead[NT];
   bool cvalid[NT];
   QueryColumn<QT, D> qraw[NT];
-  const QT* qptr[NT];  // each lane's query column (read again by steps that need finer terms)
   const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
   int ids = 0;
   auto load_ids = [&](int s0) __attribute__((always_inline)) {
@@ -721,9 +677,9 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
     lo[t] = cvalid[t] ? (a.window > 0 ? max(0, p - a.window + 1) : 0) : INT_MAX;
     hi[t] = cvalid[t] ? (a.causal ? p : ctx - 1) : -1;
     // an invalid column reads token t0's row (in range) and is zeroed when quantized
-    qptr[t] = static_cast<const QT*>(a.q) + (int64_t)(q0 + (cvalid[t] ? ctok[t] : t0)) * a.q_tok +
-              (int64_t)chead[t] * a.q_head + 16 * qg;
-    load_query_column<QT, D>(qptr[t], qraw[t]);
+    const QT* qp = static_cast<const QT*>(a.q) + (int64_t)(q0 + (cvalid[t] ? ctok[t] : t0)) * a.q_tok +
+                   (int64_t)chead[t] * a.q_head + 16 * qg;
+    load_query_column<QT, D>(qp, qraw[t]);
   }
 
   // ---- 3. key steps: block b_lo + 4*step + w is staged by wave w. Lane i of `ids`
@@ -753,10 +709,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     if constexpr (KF == kInt8)
-    {
       cf[t] = query_column_i8<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qop[t].hi, qop[t].lo);
-      qop[t].ks_fine = (kFineScoreError / (63.5f * D)) / cf[t];
-    }
     else
       cf[t] = query_column_f16<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qop[t].op);
     cfe[t] = cf[t] > 0.f ? cf[t] : FLT_MIN;  // cf >= 0 or NaN (scale > 0)
@@ -847,8 +800,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
         if (!(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min)) bounded |= 1u << w;
       }
       if (use != 0)
-        prefill_step<QT, D, NT>(cur, vt[0], use, bounded & use, masks, kb0, qop, cf, cfe, lo, hi,
-                                qptr, cvalid, r, qg, ones, vmix, vf, acc, m, bad_score);
+        prefill_step<D, NT>(cur, vt[0], use, bounded & use, masks, kb0, qop, cf, cfe, lo, hi, r, qg,
+                            ones, vmix, vf, acc, m, bad_score);
     }
     __syncthreads();  // step i's stage may be refilled
   }

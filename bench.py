@@ -8,9 +8,11 @@ slot_mapping, then ragged paged attention of the 64 bf16 query rows (32 q heads,
 K/V from HBM, not from the 256 MB MALL, as a real multi-layer decode does.
 
 value = attended KV-tokens/s = sum(context_lens) / step time. The ``roofline``
-object is for the attention call (decode_mfma_kernel plus the split-K
-merge_kernel), timed with HIP events on the launch stream; ``cpu_baseline`` times the numpy restatement of the
-reference's CPU path (oracle/) on a bounded sample on this host.
+object is for the attention call (decode_streamk_kernel plus the split-K
+merge_streamk_kernel), timed with HIP events on the launch stream. ``extra`` measures
+configs 3, 4 and 5 in the same run the same way (their calls alone).
+``cpu_baseline`` times the numpy restatement of the reference's CPU path (oracle/)
+on the whole config-2 step with one BLAS thread and with the host's CPU share.
 """
 
 from __future__ import annotations
@@ -18,6 +20,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -40,86 +43,210 @@ def parse():
     p.add_argument("--partition", type=int, default=0,
                    help="0 = automatic (stream-K); >0 = fixed split-K partition tokens")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--cpu-runs", type=int, default=5, help="timed CPU steps per thread setting")
+    p.add_argument("--no-extra", action="store_true", help="skip the config 3/4/5 measurements")
+    p.add_argument("--extra-calls", type=int, default=50)
     p.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
                    help="rocprof-derived HBM bytes per attention launch (optional)")
     return p.parse_args()
 
 
-def cpu_baseline(w, cache, step_batch, q, budget_s):
-    """Time the oracle (numpy restatement of PagedAttentionRunner's row/page/tile
-    loop + quantize_kv/copy_kv) on the whole workload, repeated for ~budget_s."""
-    import numpy as np
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_share():
+    """Threads for the all-cores leg: the host's CPU share (OMP_NUM_THREADS where the
+    environment sets it, else the CPUs this process may run on)."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(w, cache, step_batch, q, runs):
+    """The oracle (numpy restatement of PagedAttentionRunner's row/page/tile loop and
+    quantize_kv/copy_kv) on the whole config-2 step: one warmup, then the median of
+    ``runs`` steps, with one BLAS/torch thread and with the host's CPU share."""
+    import torch
+    from threadpoolctl import threadpool_limits
 
     from oracle import reference_cpu as ref
 
     codes = cache.codes[:, 0].cpu().numpy()
     scales = cache.scales[:, 0].cpu().numpy()
-    arena = [codes[:, 0].copy(), scales[:, 0].copy(), codes[:, 1].copy(), scales[:, 1].copy()]
     k, v, slots = (t.float().cpu().numpy() for t in step_batch)
     qn = q.float().cpu().numpy()
-    reps, tokens, start = 0, 0, time.perf_counter()
-    while True:
+
+    # appending the step's tokens again rewrites the same slots with the same codes
+    arena = [codes[:, 0].copy(), scales[:, 0].copy(), codes[:, 1].copy(), scales[:, 1].copy()]
+
+    def step():
+        t0 = time.perf_counter()
         ref.quantize_append(k, v, slots, arena[0], arena[1], arena[2], arena[3], 16)
         ref.paged_attention(qn, *arena, w.block_tables, w.context_lens, block_size=16,
                             scale=w.scale)
-        reps += 1
-        tokens += w.attended_tokens
-        elapsed = time.perf_counter() - start
-        if elapsed >= budget_s or reps >= 20:
-            break
-    return {"value": tokens / elapsed, "unit": "attended KV-tokens/s", "cores": 1,
-            "kind": "port",
-            "sample": f"{reps} full {w.name} steps (append 64 tokens + attend "
-                      f"{w.attended_tokens} KV-tokens) in {elapsed:.1f}s, numpy oracle, 1 thread"}
+        return time.perf_counter() - t0
+
+    legs = []
+    saved = torch.get_num_threads()
+    for threads in sorted({1, cpu_share()}):
+        with threadpool_limits(limits=threads), torch.inference_mode():
+            torch.set_num_threads(threads)
+            step()
+            times = [step() for _ in range(runs)]
+        med = statistics.median(times)
+        legs.append({"threads": threads, "median_s": med, "runs": runs,
+                     "value": w.attended_tokens / med})
+    torch.set_num_threads(saved)
+    best = max(legs, key=lambda leg: leg["value"])
+    return {"value": best["value"], "unit": "attended KV-tokens/s", "cores": best["threads"],
+            "kind": "port", "cpu_model": cpu_model(), "cpu_count": os.cpu_count(),
+            "legs": legs,
+            "sample": f"the whole {w.name} step (append {int(step_batch[0].shape[0])} tokens + "
+                      f"attend {w.attended_tokens} KV-tokens), numpy oracle, median of {runs} "
+                      f"after one warmup, per thread setting (BLAS/torch threads via "
+                      f"threadpoolctl)"}
 
 
-def prefill_measurement(w, cache, q, L, args, device):
-    """The rows with more than one query token alone (one varlen call over them):
-    MFMA flops of the causal chunks / call time. The call also launches the decode
-    kernels, which find no decode row, so the rate is a lower bound for the prefill
-    kernel itself (rocprofv3 gives the kernel's own time)."""
-    import numpy as np
+def time_calls(call, n, layers):
+    """Average and median ms of ``call(layer)`` from per-launch HIP events on the
+    current (launch) stream, after 5 warmup calls, cycling over ``layers`` arenas."""
     import torch
 
-    from aster_amd import workloads as wl
-
-    rows = np.nonzero(w.q_lens > 1)[0]
-    sub = wl.DecodeWorkload(w.name + "_prefill_rows", w.num_q_heads, w.num_kv_heads,
-                            w.head_dim, w.context_lens[rows], w.block_tables[rows],
-                            w.num_blocks, w.q_dtype, w.seed, w.scale, query_lens=w.q_lens[rows])
-    qsl_h = w.query_start_loc()
-    take = torch.as_tensor(np.concatenate([np.arange(qsl_h[r], qsl_h[r + 1]) for r in rows]),
-                           device=device).long()
-    qp = q[take].contiguous()
-    tables, lens = wl.device_tables(sub, device)
-    qsl = wl.device_query_start(sub, device)
-    out = torch.empty_like(qp)
-    ws = cache.workspace(sub.num_seqs, sub.num_q_heads, sub.max_context_len, args.partition)
-
-    def call(layer):
-        cache.paged_attention(layer, qp, tables, lens, max_context_len=sub.max_context_len,
-                              scale=sub.scale, partition_tokens=args.partition, out=out,
-                              workspace=ws, query_start_loc=qsl, max_query_len=sub.max_query_len)
-
     for i in range(5):
-        call(i % L)
-    n = max(args.steps // 4, 20)
+        call(i % layers)
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(n)]
     torch.cuda.synchronize()
     for i in range(n):
         evs[i][0].record()
-        call(i % L)
+        call(i % layers)
         evs[i][1].record()
     torch.cuda.synchronize()
-    cache.raise_errors()
-    avg_ms = sum(a.elapsed_time(b) for a, b in evs) / n
-    flops = sub.prefill_flops()
-    tflops = flops / (avg_ms * 1e-3) / 1e12
-    return {"rows": int(len(rows)), "query_tokens": sub.num_query_tokens, "flops": flops,
-            "call_us": avg_ms * 1e3, "achieved_tflops": tflops, "bound": "mfma",
-            "peak_tflops": MFMA_F16_PEAK_TFLOPS, "frac": tflops / MFMA_F16_PEAK_TFLOPS}
+    ms = sorted(a.elapsed_time(b) for a, b in evs)
+    return sum(ms) / n, ms[n // 2]
+
+
+def build_arena(w, layers, device, hold_last=False):
+    import torch
+
+    from aster_amd import PagedKVCache
+    from aster_amd import workloads as wl
+
+    cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=layers, num_kv_heads=w.num_kv_heads,
+                         head_dim=w.head_dim, device=device)
+    _, step_batch = wl.materialize(w, cache, layer=0, device=device, hold_last=hold_last)
+    for layer in range(1, layers):
+        cache.codes[:, layer].copy_(cache.codes[:, 0])
+        cache.scales[:, layer].copy_(cache.scales[:, 0])
+    torch.cuda.synchronize()
+    return cache, step_batch
+
+
+def attention_caller(w, cache, q, device, partition, rows=None):
+    """``call(layer)`` running one attention call over the workload (or over its rows
+    ``rows``, a sub-workload of the same arena) and the workload it covers."""
+    import numpy as np
+    import torch
+
+    from aster_amd import workloads as wl
+
+    if rows is not None:
+        qsl_h = w.query_start_loc()
+        take = torch.as_tensor(np.concatenate([np.arange(qsl_h[r], qsl_h[r + 1]) for r in rows]),
+                               device=device).long()
+        q = q[take].contiguous()
+        w = wl.DecodeWorkload(w.name + "_rows", w.num_q_heads, w.num_kv_heads, w.head_dim,
+                              w.context_lens[rows], w.block_tables[rows], w.num_blocks, w.q_dtype,
+                              w.seed, w.scale, query_lens=w.q_lens[rows])
+    tables, lens = wl.device_tables(w, device)
+    varlen = w.query_lens is not None
+    qsl = wl.device_query_start(w, device) if varlen else None
+    out = torch.empty_like(q)
+    ws_bytes = cache.workspace_bytes(w.num_seqs, w.num_q_heads, w.max_context_len, partition)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=device)
+
+    def call(layer):
+        cache.paged_attention(layer, q, tables, lens, max_context_len=w.max_context_len,
+                              scale=w.scale, partition_tokens=partition, out=out, workspace=ws,
+                              query_start_loc=qsl,
+                              max_query_len=w.max_query_len if varlen else None)
+
+    return call, w
+
+
+def hbm_entry(w, avg_ms, med_ms, nbytes=None):
+    nbytes = w.algorithmic_bytes() if nbytes is None else nbytes
+    gbs = nbytes / (avg_ms * 1e-3) / 1e9
+    return {"call_us": avg_ms * 1e3, "median_call_us": med_ms * 1e3, "algorithmic_bytes": nbytes,
+            "achieved_gbs": gbs, "frac": gbs / HBM_PEAK_GBS,
+            "attended_kv_tokens_per_s": w.attended_tokens / (avg_ms * 1e-3)}
+
+
+def extra_measurements(device, partition, calls):
+    """Configs 3, 4 and 5: one attention call each (two layer arenas, alternated, so
+    the calls do not reuse each other's K/V from the MALL), HIP events per launch."""
+    import numpy as np
+    import torch
+
+    from aster_amd import workloads as wl
+
+    out = {}
+    # config 3: the mixed call, its decode rows alone, its chunk rows alone (the chunk
+    # call also launches the decode kernels, which find no decode row: its MFMA rate is
+    # a lower bound for the prefill kernel)
+    w = wl.config3()
+    cache, _ = build_arena(w, 2, device)
+    q = wl.queries(w, device)
+    call, _ = attention_caller(w, cache, q, device, partition)
+    entry = hbm_entry(w, *time_calls(call, calls, 2))
+    dec_rows = np.nonzero(w.q_lens == 1)[0]
+    pre_rows = np.nonzero(w.q_lens > 1)[0]
+    call, wd = attention_caller(w, cache, q, device, partition, rows=dec_rows)
+    entry["decode_rows"] = hbm_entry(wd, *time_calls(call, calls, 2))
+    call, wp = attention_caller(w, cache, q, device, partition, rows=pre_rows)
+    avg, med = time_calls(call, calls, 2)
+    flops = wp.prefill_flops()
+    tflops = flops / (avg * 1e-3) / 1e12
+    entry["prefill_rows"] = {"call_us": avg * 1e3, "median_call_us": med * 1e3, "flops": flops,
+                             "achieved_tflops": tflops, "bound": "mfma",
+                             "peak_tflops": MFMA_F16_PEAK_TFLOPS,
+                             "frac": tflops / MFMA_F16_PEAK_TFLOPS}
+    out[w.name] = entry
+    del cache
+    torch.cuda.empty_cache()
+    # config 4: HBM fraction on the distinct K/V bytes, effective rate on the logical
+    w = wl.config4()
+    cache, _ = build_arena(w, 2, device)
+    q = wl.queries(w, device)
+    call, _ = attention_caller(w, cache, q, device, partition)
+    avg, med = time_calls(call, calls, 2)
+    entry = hbm_entry(w, avg, med)
+    entry["logical_effective_gbs"] = entry.pop("achieved_gbs")
+    entry["logical_frac"] = entry.pop("frac")
+    unique = w.unique_kv_bytes() + (w.algorithmic_bytes() - w.attended_tokens * w.num_kv_heads
+                                    * (2 * w.head_dim + 8))
+    entry["unique_bytes"] = unique
+    entry["unique_gbs"] = unique / (avg * 1e-3) / 1e9
+    entry["unique_frac"] = entry["unique_gbs"] / HBM_PEAK_GBS
+    out[w.name] = entry
+    del cache
+    torch.cuda.empty_cache()
+    # config 5
+    w = wl.config5()
+    cache, _ = build_arena(w, 2, device)
+    q = wl.queries(w, device)
+    call, _ = attention_caller(w, cache, q, device, partition)
+    out[w.name] = hbm_entry(w, *time_calls(call, calls, 2))
+    del cache
+    torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -130,37 +257,21 @@ def main():
         sys.exit(2)
     import torch
 
-    from aster_amd import PagedKVCache
     from aster_amd import workloads as wl
 
     device = torch.device("cuda:0")
     w = getattr(wl, args.config)()
     L = args.layers
-    cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=L, num_kv_heads=w.num_kv_heads,
-                         head_dim=w.head_dim, device=device)
-    _, step_batch = wl.materialize(w, cache, layer=0, device=device, hold_last=True)
-    for layer in range(1, L):
-        cache.codes[:, layer].copy_(cache.codes[:, 0])
-        cache.scales[:, layer].copy_(cache.scales[:, 0])
-    tables, lens = wl.device_tables(w, device)
-    varlen = w.query_lens is not None
-    qsl = wl.device_query_start(w, device) if varlen else None
+    cache, step_batch = build_arena(w, L, device, hold_last=True)
     q = wl.queries(w, device)
-    out = torch.empty_like(q)
+    call, _ = attention_caller(w, cache, q, device, args.partition)
     k_new, v_new, slots = step_batch
-    ws_bytes = cache.workspace_bytes(w.num_seqs, w.num_q_heads, w.max_context_len, args.partition)
-    workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=device)
-
-    def attend(layer):
-        cache.paged_attention(layer, q, tables, lens, max_context_len=w.max_context_len,
-                              scale=w.scale, partition_tokens=args.partition, out=out,
-                              workspace=workspace, query_start_loc=qsl,
-                              max_query_len=w.max_query_len if varlen else None)
+    varlen = w.query_lens is not None
 
     def step(i):
         layer = i % L
         cache.append(layer, k_new, v_new, slots)
-        attend(layer)
+        call(layer)
 
     for i in range(args.warmup):
         step(i)
@@ -180,18 +291,8 @@ def main():
     ms_per_step = start.elapsed_time(end) / args.steps
     cache.raise_errors()
 
-    # ---- roofline: attention call alone, per-launch HIP events on the launch stream
-    n = max(args.steps, 50)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(n)]
-    torch.cuda.synchronize()
-    for i in range(n):
-        evs[i][0].record()
-        attend(i % L)
-        evs[i][1].record()
-    torch.cuda.synchronize()
-    attn_ms = sorted(a.elapsed_time(b) for a, b in evs)
-    attn_avg_ms = sum(attn_ms) / n
+    # ---- roofline: the attention call alone, per-launch HIP events on the launch stream
+    attn_avg_ms, attn_med_ms = time_calls(call, max(args.steps, 50), L)
     alg_bytes = w.algorithmic_bytes()
     achieved = alg_bytes / (attn_avg_ms * 1e-3) / 1e9
     # HBM bytes per call measured by rocprofv3 (FETCH_SIZE/WRITE_SIZE, calibrated
@@ -231,16 +332,20 @@ def main():
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
             "algorithmic_bytes_per_launch": alg_bytes,
-            "avg_launch_us": attn_avg_ms * 1e3, "median_launch_us": attn_ms[n // 2] * 1e3,
+            "avg_launch_us": attn_avg_ms * 1e3, "median_launch_us": attn_med_ms * 1e3,
         },
         "wall_s_timed_region": wall,
     }
     if varlen:
         result["config"]["query_tokens"] = w.num_query_tokens
         result["config"]["max_query_len"] = w.max_query_len
-        result["prefill"] = prefill_measurement(w, cache, q, L, args, device)
+    if not args.no_extra and args.config == "config2":
+        del cache
+        torch.cuda.empty_cache()
+        result["extra"] = extra_measurements(device, args.partition, args.extra_calls)
+        cache, step_batch = build_arena(w, 1, device, hold_last=True)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(w, cache, step_batch, q, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(w, cache, step_batch, q, args.cpu_runs)
     print(json.dumps(result), flush=True)
 
 
