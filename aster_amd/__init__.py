@@ -14,6 +14,7 @@ from .offload import PagedStateArchive
 from .paged_kv import DEFAULT_PARTITION_TOKENS, PagedKVCache
 from .paged_pool import (CacheCapacityError, KVStateCodec, PagedSequence, PagedStatePool, PageRef,
                          PageView, SlotReservation, StateError)
+from .prefix_plan import PrefixPacks, plan_prefix_packs
 from .runner import PagedAttentionRunner, PagedAttentionStep
 
 __all__ = [
@@ -21,5 +22,5 @@ __all__ = [
     "KVQuantization", "QuantizedKV", "quantize_kv", "DEFAULT_PARTITION_TOKENS", "PagedKVCache",
     "KVStateCodec", "PagedStatePool", "PagedSequence", "PageRef", "PageView", "SlotReservation",
     "StateError", "CacheCapacityError", "PagedStateArchive", "PagedAttentionRunner",
-    "PagedAttentionStep",
+    "PagedAttentionStep", "PrefixPacks", "plan_prefix_packs",
 ]

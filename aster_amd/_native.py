@@ -33,7 +33,9 @@ EXPORTED_SYMBOLS = (
     "astr_paged_attention_i8",
     "astr_paged_attention_varlen_i8",
     "astr_paged_attention_i8_noalloc",
+    "astr_paged_attention_i8_shared",
     "astr_paged_attention_i8_workspace_bytes",
+    "astr_paged_attention_i8_shared_workspace_bytes",
     "astr_kv_copy_blocks",
     "astr_last_error",
     "astr_version",
@@ -99,6 +101,11 @@ def lib():
             c_i32, c_i32, ctypes.c_float, c_i32, c_i32, c_vp, c_vp,
         ]
         handle.astr_paged_attention_i8_noalloc.restype = ctypes.c_int
+        handle.astr_paged_attention_i8_shared.argtypes = [
+            desc_p, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i32, c_vp, c_i32,
+            c_i32, c_i32, ctypes.c_float, c_i32, c_vp, c_i32, c_i32, c_vp, c_sz, c_vp, c_vp,
+        ]
+        handle.astr_paged_attention_i8_shared.restype = ctypes.c_int
         handle.astr_paged_attention_varlen_i8.argtypes = [
             desc_p, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i32, c_i32, c_i32,
             c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, ctypes.c_float, c_i32, c_i32, c_vp, c_sz,
@@ -111,6 +118,8 @@ def lib():
         handle.astr_kv_copy_blocks.restype = ctypes.c_int
         handle.astr_paged_attention_i8_workspace_bytes.argtypes = [c_i32] * 6
         handle.astr_paged_attention_i8_workspace_bytes.restype = c_sz
+        handle.astr_paged_attention_i8_shared_workspace_bytes.argtypes = [c_i32] * 7
+        handle.astr_paged_attention_i8_shared_workspace_bytes.restype = c_sz
         handle.astr_last_error.argtypes = []
         handle.astr_last_error.restype = ctypes.c_char_p
         handle.astr_version.argtypes = []

@@ -66,7 +66,15 @@ struct AttnArgs {
   int32_t pref_waves;  // stream-K: waves the GPU holds at once (set by the launcher)
   float* ws_o;          // partial acc (layout depends on the split mode)
   float* ws_ml;         // partial (m, l)
-  int32_t* ws_seq;      // stream-K: per-sequence block prefix [num_seqs + 1]
+  int32_t* ws_seq;      // stream-K: block prefix over its work rows [num_packs + num_seqs + 1]
+  // stream-K prefix packs: num_packs records of 1 + pack_rows int32, [shared blocks,
+  // member sequences (-1: empty)]; members read the pack's blocks in one MFMA tile,
+  // query column p * G + g for member p, head g of the group (pack_rows * G <= 16)
+  const int32_t* packs;
+  int32_t num_packs, pack_rows;
+  int32_t slot_cols;    // stream-K: columns of one partial slot (G, or pack_rows * G)
+  int32_t* ws_pack;     // stream-K: per sequence, [pack column k * pack_rows + p or -1,
+                        // the pack's first block, its end] (the per-head order)
   int32_t* err_flag;
 };
 
@@ -337,16 +345,26 @@ __device__ __forceinline__ const QT* query_lane_ptr(const AttnArgs& a, int tok, 
          (int64_t)(kvh * G + (r < G ? r : 0)) * a.q_head + 16 * qg;
 }
 
-template <typename QT, int D, int G>
-__device__ __forceinline__ void load_query(const AttnArgs& a, int tok, int kvh, int r, int qg,
-                                           QueryRaw<D>& q) {
-  const QT* qp = query_lane_ptr<QT, G>(a, tok, kvh, r, qg);
+// Lane (qg, r)'s part of query head `head`, token row tok (any column layout).
+template <typename QT>
+__device__ __forceinline__ const QT* query_col_ptr(const AttnArgs& a, int tok, int head, int qg) {
+  return static_cast<const QT*>(a.q) + (int64_t)tok * a.q_tok + (int64_t)head * a.q_head + 16 * qg;
+}
+
+template <typename QT, int D>
+__device__ __forceinline__ void load_query_at(const QT* qp, QueryRaw<D>& q) {
 #pragma unroll
   for (int h = 0; h < D / 64; ++h) {
     const uint4* src = reinterpret_cast<const uint4*>(qp + 64 * h);
     q.w[h][0] = src[0];
     q.w[h][1] = src[1];
   }
+}
+
+template <typename QT, int D, int G>
+__device__ __forceinline__ void load_query(const AttnArgs& a, int tok, int kvh, int r, int qg,
+                                           QueryRaw<D>& q) {
+  load_query_at<QT, D>(query_lane_ptr<QT, G>(a, tok, kvh, r, qg), q);
 }
 
 typedef int int4_t __attribute__((ext_vector_type(4)));
@@ -610,16 +628,17 @@ __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, f
 // [kv_begin, ctx) are masked; `tok_base` is the block's first token position.
 // Cross-lane (ballots, shuffles): call in uniform control flow.
 // `vr` keeps the PV weights p * v_scale in f16 range for large V scales (VRange).
-template <typename QT, int D, int G, int KF = kInt8>
+// `gvalid`: this lane's query column feeds an output (its query operand is zero
+// otherwise).
+template <typename QT, int D, int KF = kInt8>
 __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF>& qop, float cf,
-                                           int tok_base, int kv_begin, int ctx, int r, int qg,
-                                           float4_t (&acc)[D / 16 + 1], float& m, float& l,
+                                           int tok_base, int kv_begin, int ctx, bool gvalid, int r,
+                                           int qg, float4_t (&acc)[D / 16 + 1], float& m, float& l,
                                            VRange& vr, bool& bad_score, bool masks = false) {
   using S = Stage<D>;
   constexpr int KCH = D / 64;
   constexpr int VB = D / 16;
   constexpr int NPV = D / 16;
-  const bool gvalid = r < G;
   // V scales, times 2^8 for FP8 codes (E4M3FN operands carry 2^-8; E5M2 weights carry
   // 2^8, as does the normaliser of this format); finite, and the same on the 16 lanes
   // of a token group. Beyond vr.vlim they grow the running maximum's offset first: its
@@ -741,8 +760,8 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
     }
   } else {
     // every key of the block is visible: a NaN-propagating maximum and minimum of the
-    // four scores stand for the per-score finiteness and rescale tests. Head columns
-    // r >= G (zero query, finite zero scores) feed no output and test nothing.
+    // four scores stand for the per-score finiteness and rescale tests. Columns
+    // without an output (zero query, finite zero scores) test nothing.
 #pragma unroll
     for (int j = 0; j < 4; ++j) sc[j] = s4[j] * (ks[j] * cf);
     const float hi = vmax(vmax(sc[0], sc[1]), vmax(sc[2], sc[3]));
@@ -797,6 +816,35 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
   }
 }
 
+// Lane (qg, r) holds, of head column r, the D/4 consecutive outputs
+// d = (D/4) qg + t, t = VB j + k (VB = D/16), output t in acc[t % VB][t / VB].
+// store_lane_f32 / store_lane_out write them with 16-byte stores from `dst`, the
+// lane's first element (16-byte aligned).
+template <int D>
+__device__ __forceinline__ void store_lane_f32(float* dst, const float4_t (&acc)[D / 16 + 1]) {
+  constexpr int VB = D / 16;
+#pragma unroll
+  for (int t = 0; t < D / 4; t += 4) {
+    float4_t v;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = acc[(t + u) % VB][(t + u) / VB];
+    *reinterpret_cast<float4_t*>(dst + t) = v;
+  }
+}
+template <typename QT, int D>
+__device__ __forceinline__ void store_lane_out(QT* dst, const float4_t (&acc)[D / 16 + 1],
+                                               float scale) {
+  static_assert(sizeof(QT) == 2, "16-bit outputs");
+  constexpr int VB = D / 16;
+#pragma unroll
+  for (int t = 0; t < D / 4; t += 8) {
+    QT v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = from_float<QT>(acc[(t + u) % VB][(t + u) / VB] * scale);
+    *reinterpret_cast<uint4*>(dst + t) = *reinterpret_cast<const uint4*>(v);
+  }
+}
+
 // Ends a piece's accumulation: with biased V operands, subtracts kVBias times the
 // weight sum of head r (row 0 of acc[D/16], held by lane (0, r)) from every output of
 // that head. Cross-lane: call in uniform control flow.
@@ -838,8 +886,13 @@ ASTR_BY_FORMAT(launch_streamk)
 ASTR_BY_FORMAT(launch_prefill)
 #undef ASTR_BY_FORMAT
 
-// Largest batch the stream-K kernel takes (its per-sequence table lives in LDS).
+// Largest batch the stream-K kernel takes (its per-sequence table lives in LDS), the
+// most prefix packs per launch and the largest batch that takes them, and the work
+// rows of its block prefix (ws_seq holds one more entry) for a head dim.
 int stream_k_max_seqs();
+int stream_k_max_packs();
+int stream_k_max_pack_seqs();
+int stream_k_work_rows(int head_dim);
 
 }  // namespace attn
 }  // namespace astr

@@ -183,8 +183,8 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
     if (later >= 2) wait_vmcnt<2 * S::kLoads>();
     else if (later == 1) wait_vmcnt<S::kLoads>();
     else wait_vmcnt<0>();
-    mfma_block<QT, D, G, KF>(st, qop, cf, (first + kWaves * i) * kBlockTokens, row.kv_begin, row.ctx, r,
-                     qg, acc, m, l, vr, bad_score, a.cache.key_valid != nullptr);
+    mfma_block<QT, D, KF>(st, qop, cf, (first + kWaves * i) * kBlockTokens, row.kv_begin, row.ctx,
+                          gvalid, r, qg, acc, m, l, vr, bad_score, a.cache.key_valid != nullptr);
     // refill this stage with block i + NS (its LDS reads above fed the MFMAs)
     if (i + NS < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, i + NS), kvh, lane, st);
   };

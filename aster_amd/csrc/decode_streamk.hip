@@ -1,17 +1,21 @@
 // Stream-K paged decode attention (gfx950, bf16/fp16 queries).
 //
-// The visible 16-token blocks of all sequences are laid end to end (sequence,
-// then block) and cut into Wr equal contiguous ranges; wave gw streams range
-// gw / Hkv for kv head gw % Hkv, so the Hkv waves working on a range at the same
-// time read the same blocks for different heads (all heads of a block sit in one
-// contiguous stretch of the arena) and every wave streams the same number of
-// blocks whatever the context lengths. Blocks go through a per-wave LDS ring
-// filled by direct global->LDS loads and the MFMA step of attention_common.h.
-// Where a range begins or ends inside a row (kv head, sequence), the wave writes
-// a partial (m, l, acc) for that piece; rows a single wave covers entirely are
-// normalised and written directly. A wave owns at most two partial slots (its
-// first and its last piece), and merge_streamk_kernel combines the pieces of
-// every split row with the merge_softmax rule (online_attention.py:42-63).
+// Work rows: the prefix packs of the call (host plan: sequences whose block tables
+// begin with the same blocks, read once for up to 16/G sequences, one query column
+// per member head), then the sequences (the blocks of a packed sequence after its
+// pack's). The blocks of all work rows are laid end to end and cut into Wr equal
+// contiguous ranges; wave gw streams range gw / Hkv for kv head gw % Hkv, so the Hkv
+// waves working on a range at the same time read the same blocks for different
+// heads (all heads of a block sit in one contiguous stretch of the arena) and every
+// wave streams the same number of blocks whatever the context lengths. Blocks go
+// through a per-wave LDS ring filled by direct global->LDS loads and the MFMA step
+// of attention_common.h. Where a range begins or ends inside a work row, the wave
+// writes a partial (m, l, acc) for that piece into one of its two slots (its first
+// and its last piece); a sequence row a single wave covers entirely is normalised
+// and written directly, unless it is packed: then that piece, like a pack's whole
+// piece, goes to the row's own slot. merge_streamk_kernel combines the pieces of a
+// sequence (its pack's column and its own) with the merge_softmax rule
+// (online_attention.py:42-63).
 #include "attention_common.h"
 
 namespace astr {
@@ -30,37 +34,82 @@ template <int D>
 constexpr int sk_waves() { return D == 256 ? 8 : 4; }
 template <int D>
 constexpr int sk_stages() { return D == 256 ? 2 : 4; }
-constexpr int kMaxSeqsSK = 512;  // per-sequence table lives in LDS
-constexpr int kFastPieces = 16;  // merge: rows split into at most this many pieces load at once
+constexpr int kMaxSeqsSK = 512;   // per-sequence tables live in LDS
+// With prefix packs the tables hold fewer sequences (their LDS goes to the pack
+// tables): at most kMaxPackSeqsSK sequences and kMaxPacksSK packs (thread k of a
+// workgroup owns pack k).
+constexpr int kMaxPackSeqsSK = 256;
+constexpr int kMaxPacksSK = 128;
+constexpr int kMaxRowsSK = kMaxSeqsSK + 1;  // block prefix entries over work rows (+ 1)
+constexpr int kFastPieces = 16;   // merge: sequences in at most this many pieces load at once
 
-// Ranges per kv head over the Bh visible blocks of one head: the resident waves
-// (one round, no tail), more only where that would put over kMaxBlocksPerWaveSK
-// blocks on a wave, never more than launched, and at most one range per block (so
-// every range owns at least one block and a row split over ranges r0..r1 has
-// exactly one piece in each of them; the merge relies on it). The decode and the
-// merge kernel both derive Wr from Bh with this function.
-__device__ __forceinline__ int64_t streamk_ranges(const AttnArgs& a, int64_t Bh, int hkv) {
-  int64_t w = (Bh + kMaxBlocksPerWaveSK - 1) / kMaxBlocksPerWaveSK;
-  if (w < a.pref_waves / hkv) w = a.pref_waves / hkv;
-  if (w > a.total_waves / hkv) w = a.total_waves / hkv;
-  return w < Bh ? w : Bh;
-}
 
-// Range owning block b when range r owns [floor(Bh*r/Wr), floor(Bh*(r+1)/Wr)).
-__device__ __forceinline__ int64_t range_of(int64_t b, int64_t Bh, int64_t Wr) {
-  return ((b + 1) * Wr - 1) / Bh;
-}
+// Work rows of one kv head: packs 0 .. npk-1, then sequence s as row npk + s.
+// row_seq: the sequence of row x, or -1 - k for pack k.
+__device__ __forceinline__ int row_seq(int x, int npk) { return x < npk ? -1 - x : x - npk; }
 
-// Sequence owning block b of the per-head order (s_cu[s] <= b < s_cu[s + 1], the last
-// such s where empty rows share an offset); wave-uniform.
-__device__ __forceinline__ int seq_of_block(const int* s_cu, int nseq, int64_t b) {
-  int lo = 0, hi = nseq;
+// The split of one kv head's Bh blocks (the PB blocks of the packs first) into Wr
+// contiguous ranges of equal cost: a pack block costs kPackCost, any other block
+// kSeqCost (pack blocks are shared by all rows of the call and mostly hit in cache,
+// while a sequence's own blocks stream from HBM). Block b starts at cost c(b); range r
+// owns the blocks whose start lies in [T r / Wr, T (r + 1) / Wr), T = c(Bh).
+// Without packs every block costs the same. Wr: the resident waves per head (one
+// round, no tail), more only where that would put over kMaxBlocksPerWaveSK blocks on
+// a wave, never more than launched, and ranges no shorter than a block's cost (so
+// every range owns at least one block and a row split over ranges r0..r1 has exactly
+// one piece in each of them; the merge relies on it). The decode and the merge kernel
+// both derive the split from (Bh, PB) with this type.
+constexpr int kPackCost = 7, kSeqCost = 10;
+struct SkSplit {
+  int64_t Bh, PB, T, Wr;
+  __device__ SkSplit(const AttnArgs& a, int64_t bh, int64_t pb, int hkv)
+      : Bh(bh), PB(pb), T(kPackCost * pb + kSeqCost * (bh - pb)) {
+    int64_t w = (Bh + kMaxBlocksPerWaveSK - 1) / kMaxBlocksPerWaveSK;
+    if (w < a.pref_waves / hkv) w = a.pref_waves / hkv;
+    if (w > a.total_waves / hkv) w = a.total_waves / hkv;
+    const int64_t most = T / kSeqCost > 1 ? T / kSeqCost : 1;
+    Wr = w < most ? w : most;
+  }
+  __device__ int64_t cost(int64_t b) const {
+    return b < PB ? kPackCost * b : kPackCost * PB + kSeqCost * (b - PB);
+  }
+  __device__ int64_t range_of(int64_t b) const { return cost(b) * Wr / T; }
+  // first block of range r (first(Wr) == Bh)
+  __device__ int64_t first(int64_t r) const {
+    const int64_t c = (T * r + Wr - 1) / Wr;
+    return c <= kPackCost * PB ? (c + kPackCost - 1) / kPackCost
+                               : PB + (c - kPackCost * PB + kSeqCost - 1) / kSeqCost;
+  }
+};
+
+// Work row owning block b of the per-head order (s_cu[x] <= b < s_cu[x + 1], the last
+// such x where empty rows share an offset); wave-uniform.
+__device__ __forceinline__ int row_of_block(const int* s_cu, int nrow, int64_t b) {
+  int lo = 0, hi = nrow;
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
     if (s_cu[mid] <= b) lo = mid;
     else hi = mid;
   }
   return lo;
+}
+
+// Partial slots, counted in columns of D floats (and (m, l) pairs): two per wave
+// (slot_cols columns each) for pieces cut by a range boundary, then the slots of
+// work rows that one wave streams whole but that still merge: pack k of kv head kvh
+// (pack_rows * G columns), then packed sequence at pack column pc (G columns).
+__device__ __forceinline__ int64_t wave_slot(const AttnArgs& a, int64_t wave, int which, int col) {
+  return (wave * 2 + which) * a.slot_cols + col;
+}
+__device__ __forceinline__ int64_t pack_slot(const AttnArgs& a, int G, int kvh, int k, int col) {
+  const int64_t base = (int64_t)a.total_waves * 2 * a.slot_cols;
+  return base + ((int64_t)kvh * a.num_packs + k) * a.pack_rows * G + col;
+}
+__device__ __forceinline__ int64_t packed_seq_slot(const AttnArgs& a, int G, int hkv, int kvh,
+                                                   int pc, int g) {
+  const int64_t base = (int64_t)a.total_waves * 2 * a.slot_cols +
+                       (int64_t)hkv * a.num_packs * a.pack_rows * G;
+  return base + ((int64_t)kvh * a.num_packs * a.pack_rows + pc) * G + g;
 }
 
 template <typename QT>
@@ -70,7 +119,9 @@ __device__ __forceinline__ void store_row_zero(const AttnArgs& a, int tok, int D
     orow[(int64_t)(idx / D) * a.o_head + idx % D] = from_float<QT>(0.f);
 }
 
-template <typename QT, int D, int G>
+// kPacks: the launch carries prefix packs (a separate instantiation, so that batches
+// without them run none of the pack code).
+template <typename QT, int D, int G, bool kPacks>
 __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(AttnArgs a) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   static_assert(G >= 1 && G <= 16, "GQA group");
@@ -78,30 +129,48 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   static_assert(NS >= 2 && NS <= 4, "LDS stages per wave");
   using S = Stage<D>;
   constexpr int NPV = D / 16;
-  constexpr int VB = D / 16;
   constexpr int NW = sk_waves<D>();
-  constexpr int SPT = (kMaxSeqsSK + NW * kWave - 1) / (NW * kWave);  // sequences per thread
+  constexpr int SEQS = kPacks ? kMaxPackSeqsSK : kMaxSeqsSK;
+  constexpr int PACKS = kPacks ? kMaxPacksSK : 1;
+  constexpr int SPT = (SEQS + NW * kWave - 1) / (NW * kWave);  // sequences per thread
+  constexpr int kPackRowsMax = 16 / G;
+  static_assert(NW * kWave >= kMaxPacksSK, "one pack per thread");
 
   // Per wave, besides its block ring: the next window's block ids (256 bytes), which
   // arrive by direct-to-LDS loads issued well before use.
   constexpr int kIdsBytes = 256;
   __shared__ __attribute__((aligned(16))) char lds[NS * NW * S::kBytes];  // [stage][wave]
   __shared__ __attribute__((aligned(16))) char id_slots[NW * kIdsBytes];   // [wave]
-  __shared__ int s_ctx[kMaxSeqsSK];  // -1: not a decode row
-  __shared__ int s_tok[kMaxSeqsSK];  // query/output token row
-  __shared__ int s_cu[kMaxSeqsSK + 1];
-  __shared__ int s_wsum[NW];
+  __shared__ int s_ctx[SEQS];   // -1: not a decode row
+  __shared__ int s_tok[SEQS];   // query/output token row
+  __shared__ int s_cu[SEQS + PACKS + 1];
+  __shared__ int s_wsum[2 * NW];  // per wave: pack blocks, sequence blocks
+  __shared__ int s_pcol[kPacks ? SEQS : 1];  // pack column k * pack_rows + p of a member, else INT_MAX
+  __shared__ short s_pmem[kPacks ? SEQS : 1];  // [k * pack_rows + p]: member sequence or -1
+  __shared__ int s_pblk[PACKS];               // shared blocks of pack k (0: no member left)
+  __shared__ short s_plead[PACKS];            // first member of pack k: its table holds the blocks
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   const int r = lane & 15, qg = lane >> 4;
-  const bool gvalid = r < G;
   const int nseq = a.num_seqs;
   const int hkv = a.cache.num_kv_heads;
+  const int npk = kPacks ? a.num_packs : 0, P = kPacks ? a.pack_rows : 1;
+  const int nrow = npk + nseq;
 
-  // ---- 1. visible blocks per sequence -> exclusive prefix s_cu (thread t owns
-  // sequences SPT*t .. SPT*t + SPT-1); sequences without exactly one query token take
-  // no blocks
+  // ---- 0. this thread's pack record (thread k: pack k), loaded with the lengths below
+  int mem[kPackRowsMax];
+  int shared = 0;
+  const bool mine = kPacks && (int)threadIdx.x < npk;
+  if constexpr (kPacks) {
+    const int32_t* rec = a.packs + (int64_t)threadIdx.x * (1 + P);
+    shared = mine ? rec[0] : 0;
+#pragma unroll
+    for (int p = 0; p < kPackRowsMax; ++p) mem[p] = (mine && p < P) ? rec[1 + p] : -1;
+  }
+
+  // ---- 1. per sequence: token row and visible context (thread t owns sequences
+  // SPT*t .. SPT*t + SPT-1); sequences without exactly one query token take no blocks
   int nb[SPT];
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
@@ -110,6 +179,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     if (s < nseq) {
       const int tok = decode_token(a, s);
       s_tok[s] = tok;
+      if constexpr (kPacks) s_pcol[s] = INT_MAX;
       if (tok >= 0) {
         const int ctx = clamp_ctx(a, a.context_lens[s], blockIdx.x == 0);
         s_ctx[s] = ctx;
@@ -120,52 +190,155 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
       }
     }
   }
-  int local = 0;
+  if constexpr (kPacks) {
+    // the pack record is needed after the barrier below: take it now, while the
+    // context lengths arrive, so that it is not loaded only then
 #pragma unroll
-  for (int k = 0; k < SPT; ++k) local += nb[k];
-  int incl = local;
+    for (int p = 0; p < kPackRowsMax; ++p) asm volatile("" ::"v"(mem[p]));
+    asm volatile("" ::"v"(shared));
+  }
+  // ---- 1b. packs (thread k checks pack k): a member must be a decode row listed once
+  // whose first shared-blocks * 16 tokens are all visible (no window); a member that
+  // fails is dropped from its pack (and the plan reported as bad), a pack without
+  // members streams nothing
+  int pack_blocks = 0;
+  bool bad_plan = false;
+  if constexpr (kPacks) if (npk > 0) {
+    __syncthreads();
+    // all members' LDS entries first (independent reads), then the tests
+    int mtok[kPackRowsMax], mctx[kPackRowsMax];
+#pragma unroll
+    for (int p = 0; p < kPackRowsMax; ++p) {
+      const int sm = mem[p] >= 0 && mem[p] < nseq ? mem[p] : 0;
+      mtok[p] = s_tok[sm];
+      mctx[p] = s_ctx[sm];
+    }
+#pragma unroll
+    for (int p = 0; p < kPackRowsMax; ++p) {
+      if (mem[p] == -1) continue;
+      const int sm = mem[p];
+      const bool ok = sm >= 0 && sm < nseq && shared >= 1 && a.window == 0 && mtok[p] >= 0 &&
+                      (int64_t)shared * kBlockTokens <= mctx[p];
+      if (ok) {
+        atomicMin(&s_pcol[sm], (int)threadIdx.x * P + p);
+      } else {
+        bad_plan = true;
+        mem[p] = -1;
+      }
+    }
+    __syncthreads();
+    int lead = -1, won[kPackRowsMax];
+#pragma unroll
+    for (int p = 0; p < kPackRowsMax; ++p) won[p] = s_pcol[mem[p] >= 0 ? mem[p] : 0];
+#pragma unroll
+    for (int p = 0; p < kPackRowsMax; ++p) {
+      if (mem[p] >= 0 && won[p] != (int)threadIdx.x * P + p) {  // listed twice
+        bad_plan = true;
+        mem[p] = -1;
+      }
+      if (mine && p < P) s_pmem[threadIdx.x * P + p] = (short)mem[p];
+      if (lead < 0) lead = mem[p];
+    }
+    if (mine) {
+      pack_blocks = lead >= 0 ? shared : 0;
+      s_pblk[threadIdx.x] = pack_blocks;
+      s_plead[threadIdx.x] = (short)lead;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {  // a packed sequence's own row starts after the pack's
+      const int s = SPT * threadIdx.x + k;
+      if (s < nseq && s_pcol[s] < npk * P) nb[k] -= s_pblk[s_pcol[s] / P];
+    }
+  }
+  auto pack_col = [&](int s) __attribute__((always_inline)) -> int {
+    if constexpr (kPacks) return npk > 0 && s_pcol[s] < npk * P ? s_pcol[s] : -1;
+    return -1;
+  };
+
+  // ---- 2. block prefix over work rows: the packs' blocks (pack t on thread t) and
+  // the sequences' blocks scanned side by side, the sequences placed after every pack
+  int lseq = 0;
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) lseq += nb[k];
+  int ip = pack_blocks, is = lseq;
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) {
-    const int v = __shfl_up(incl, off, kWave);
-    if (lane >= off) incl += v;
+    const int vp = __shfl_up(ip, off, kWave), vq = __shfl_up(is, off, kWave);
+    if (lane >= off) {
+      ip += vp;
+      is += vq;
+    }
   }
-  if (lane == kWave - 1) s_wsum[wave] = incl;
+  if (lane == kWave - 1) {
+    s_wsum[wave] = ip;
+    s_wsum[NW + wave] = is;
+  }
   __syncthreads();
-  int wbase = 0;
-  for (int w = 0; w < wave; ++w) wbase += s_wsum[w];
-  int excl = wbase + incl - local;
+  int bp = 0, bs = 0, pack_total = 0, bseq = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    if (w < wave) {
+      bp += s_wsum[w];
+      bs += s_wsum[NW + w];
+    }
+    pack_total += s_wsum[w];
+    bseq += s_wsum[NW + w];
+  }
+  bseq += pack_total;
+  if ((int)threadIdx.x < npk) s_cu[threadIdx.x] = bp + ip - pack_blocks;
+  int excl = pack_total + bs + is - lseq;
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
-    if (SPT * (int)threadIdx.x + k < nseq) s_cu[SPT * threadIdx.x + k] = excl;
+    const int s = SPT * threadIdx.x + k;
+    if (s < nseq) s_cu[npk + s] = excl;
     excl += nb[k];
   }
-  int bseq = 0;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) bseq += s_wsum[w];
-  if (threadIdx.x == 0) s_cu[nseq] = bseq;
+  if (threadIdx.x == 0) s_cu[nrow] = bseq;
   __syncthreads();
-  if (blockIdx.x == 0)
-    for (int s = threadIdx.x; s <= nseq; s += blockDim.x) a.ws_seq[s] = s_cu[s];
+  if (blockIdx.x == 0) {
+    for (int x = threadIdx.x; x <= nrow; x += blockDim.x) a.ws_seq[x] = s_cu[x];
+    if (npk > 0)
+      for (int s = threadIdx.x; s < nseq; s += blockDim.x) {
+        const int pc = pack_col(s);
+        a.ws_pack[3 * s] = pc;
+        a.ws_pack[3 * s + 1] = pc >= 0 ? s_cu[pc / P] : 0;
+        a.ws_pack[3 * s + 2] = pc >= 0 ? s_cu[pc / P + 1] : 0;
+      }
+    if (bad_plan) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+  }
   // rows with nothing visible (ctx == 0) are zero (online_attention.py:37)
-  for (int s = blockIdx.x; s < nseq; s += gridDim.x)
-    if (s_cu[s + 1] == s_cu[s] && s_ctx[s] >= 0) store_row_zero<QT>(a, s_tok[s], D);
+  for (int s = blockIdx.x; s < nseq; s += gridDim.x) {
+    const int x = npk + s;
+    if (s_cu[x + 1] == s_cu[x] && s_ctx[s] >= 0 && pack_col(s) < 0)
+      store_row_zero<QT>(a, s_tok[s], D);
+  }
 
-  // ---- 2. this wave's head, block range and block ids / rows (lane j <-> block b0 + j);
+  // ---- 3. this wave's head, block range and block ids / rows (lane j <-> block b0 + j);
   // waves from Wr * Hkv on have nothing to do
-  const int64_t Wr = streamk_ranges(a, bseq, hkv);
+  const SkSplit split(a, bseq, npk > 0 ? s_cu[npk] : 0, hkv);
   const int64_t gw = (int64_t)blockIdx.x * NW + wave;
   const int kv = (int)(gw % hkv);
   const int64_t rg = gw / hkv;
   int64_t b0 = 0;
   int n = 0;
-  if (rg < Wr) {
-    b0 = (int64_t)bseq * rg / Wr;
-    n = (int)((int64_t)bseq * (rg + 1) / Wr - b0);
+  if (rg < split.Wr) {
+    b0 = split.first(rg);
+    n = (int)(split.first(rg + 1) - b0);
   }
   const bool too_long = n > kMaxBlocksPerWaveSK;  // contexts beyond the declared maximum
   if (too_long) n = kMaxBlocksPerWaveSK;
+  // First block of work row x within its sequence's block table (packs: the first
+  // member's table from block 0; sequences: after the window start and the pack).
+  auto row_table = [&](int x) __attribute__((always_inline)) -> const int32_t* {
+    const int s = row_seq(x, npk);
+    if (s < 0) return a.block_tables + (int64_t)s_plead[-1 - s] * a.bt_stride;
+    const int pc = pack_col(s);
+    return a.block_tables + (int64_t)s * a.bt_stride + row_span(a, s_ctx[s]).first_blk +
+           (pc >= 0 ? s_pblk[pc / P] : 0);
+  };
   // Block list in windows of 64: lane j of window w holds block b0 + 64 w + j of the
-  // per-head order, as its physical id and its row id (kv_head * nseq + seq).
+  // per-head order, as its physical id and its row id (kv_head * nrow + work row).
   // Window 0 is read here; the ids of window w + 1 go by direct-to-LDS loads into the
   // wave's id slot when window w starts, before block 64 w + NS is issued: direct-to-LDS
   // loads complete in issue order, so once a block issued after them has landed, they
@@ -174,10 +347,9 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     const int j = 64 * w + lane;
     if (j >= n) return nullptr;
     const int64_t rem = b0 + j;
-    const int sq = seq_of_block(s_cu, nseq, rem);
-    row_id = kv * nseq + sq;
-    return a.block_tables + (int64_t)sq * a.bt_stride + row_span(a, s_ctx[sq]).first_blk +
-           (rem - s_cu[sq]);
+    const int x = row_of_block(s_cu, nrow, rem);
+    row_id = kv * nrow + x;
+    return row_table(x) + (rem - s_cu[x]);
   };
   int rows = 0, ids = 0, rows_nx = 0, ids_nx = 0;
   char* const id_slot = id_slots + wave * kIdsBytes;
@@ -195,14 +367,17 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   auto stage = [&](int j) __attribute__((always_inline)) -> char* {
     return lds + ((j % NS) * NW + wave) * S::kBytes;
   };
+  // row id of block j (in window cw or cw + 1); wave-uniform
+  auto row_at = [&](int j) __attribute__((always_inline)) -> int {
+    const bool cur = (j >> 6) == cw;
+    return __builtin_amdgcn_readfirstlane(cur ? __builtin_amdgcn_readlane(rows, j & 63)
+                                              : __builtin_amdgcn_readlane(rows_nx, j & 63));
+  };
   auto issue = [&](int j) __attribute__((always_inline)) {
     const bool cur = (j >> 6) == cw;
     const int id = cur ? __builtin_amdgcn_readlane(ids, j & 63)
                        : __builtin_amdgcn_readlane(ids_nx, j & 63);
-    const int rid = cur ? __builtin_amdgcn_readlane(rows, j & 63)
-                        : __builtin_amdgcn_readlane(rows_nx, j & 63);
-    stage_block<D>(a, __builtin_amdgcn_readfirstlane(id), __builtin_amdgcn_readfirstlane(rid) / nseq,
-                   lane, stage(j));
+    stage_block<D>(a, __builtin_amdgcn_readfirstlane(id), row_at(j) / nrow, lane, stage(j));
   };
   // Wait until block j has landed; the blocks after it (up to NS - 1) stay in flight.
   // Loads the compiler does not count only add to what is outstanding: never too few.
@@ -213,27 +388,52 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     else if (later >= 1) wait_vmcnt<S::kLoads>();
     else wait_vmcnt<0>();
   };
-  // First row's query: its G head rows go by direct-to-LDS loads into the last
-  // stage, issued before blocks 0 .. NS-2, so the block stream starts without
-  // waiting for it; block NS-1 takes that stage once the query has been read out.
+  // This lane's query column in work row x of kv head kvh: a sequence row's column r
+  // is head r of the group (r < G); a pack's column r = p G + g is head g of member p.
+  // Columns without an output read a valid row and are zeroed by qk_operand.
+  struct Column {
+    const QT* q;
+    bool valid;
+  };
+  auto column = [&](int x, int kvh) __attribute__((always_inline)) -> Column {
+    const int s = row_seq(x, npk);
+    if (s >= 0)
+      return {query_col_ptr<QT>(a, s_tok[s], kvh * G + (r < G ? r : 0), qg), r < G};
+    const int k = -1 - s;
+    const int sm = r < P * G ? s_pmem[k * P + r / G] : -1;
+    const int tok = s_tok[sm >= 0 ? sm : s_plead[k]];
+    return {query_col_ptr<QT>(a, tok, kvh * G + (sm >= 0 ? r % G : 0), qg), sm >= 0};
+  };
+  // First row's query: a sequence row's G head rows go by direct-to-LDS loads into the
+  // last stage, issued before blocks 0 .. NS-2, so the block stream starts without
+  // waiting for it; block NS-1 takes that stage once the query has been read out. A
+  // pack's columns come from several token rows and load into registers first.
   QueryRaw<D> qr;
   QkOperand<D, KF> qop;
   float cf = 0.f;
   if (nblk > 0) {
-    stage_query<QT, D, G>(a, s_tok[row0 % nseq], row0 / nseq, lane, stage(NS - 1));
-    const int first = min(NS - 1, nblk);
-    for (int j = 0; j < first; ++j) issue(j);
-    if (first == 3) wait_vmcnt<3 * S::kLoads>();  // the query has landed
-    else if (first == 2) wait_vmcnt<2 * S::kLoads>();
-    else wait_vmcnt<S::kLoads>();
-    lds_query<QT, D>(stage(NS - 1), gvalid ? r : 0, qg, qr);
-    cf = qk_operand<QT, D, KF>(qr, gvalid, a.qk_scale_log2, qop,
-                               query_lane_ptr<QT, G>(a, s_tok[row0 % nseq], row0 / nseq, r, qg));
-    if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (their values are consumed)
+    const int x0 = row0 % nrow, kvh0 = row0 / nrow;
+    const Column c0 = column(x0, kvh0);
+    if (row_seq(x0, npk) >= 0) {
+      stage_query<QT, D, G>(a, s_tok[row_seq(x0, npk)], kvh0, lane, stage(NS - 1));
+      const int first = min(NS - 1, nblk);
+      for (int j = 0; j < first; ++j) issue(j);
+      if (first == 3) wait_vmcnt<3 * S::kLoads>();  // the query has landed
+      else if (first == 2) wait_vmcnt<2 * S::kLoads>();
+      else wait_vmcnt<S::kLoads>();
+      lds_query<QT, D>(stage(NS - 1), r < G ? r : 0, qg, qr);
+      cf = qk_operand<QT, D, KF>(qr, c0.valid, a.qk_scale_log2, qop, c0.q);
+      if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (their values are consumed)
+    } else {
+      load_query_at<QT, D>(c0.q, qr);
+      const int first = min(NS, nblk);
+      for (int j = 0; j < first; ++j) issue(j);
+      cf = qk_operand<QT, D, KF>(qr, c0.valid, a.qk_scale_log2, qop, c0.q);
+    }
     if (64 < nblk) request_ids(1);
   }
 
-  // ---- 3. stream the blocks, one piece (the run of one row's blocks) at a time;
+  // ---- 4. stream the blocks, one piece (the run of one row's blocks) at a time;
   // block i sits in stage i % NS and block i + NS is issued into it once consumed
   float4_t acc[NPV + 1];  // [NPV]: weight sums (INT8)
   float m = 0.f, l = 0.f;
@@ -243,22 +443,35 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   while (i < nblk) {
     const int crid = __builtin_amdgcn_readlane(rows, i & 63);  // this piece's row
     const int pstart = i;
-    const int pseq = crid % nseq, pkvh = crid / nseq;
-    const RowSpan psp = row_span(a, s_ctx[pseq]);
-    const int64_t pfb = s_cu[pseq];  // first block of the row in the per-head order
+    const int px = crid % nrow, pkvh = crid / nrow;
+    const int ps = row_seq(px, npk);  // sequence, or -1 - pack
+    const Column col = column(px, pkvh);
+    // visible keys: a pack's blocks are whole and visible to every member
+    RowSpan psp;
+    int pblk0;  // block index of the row's first block within the sequence
+    if (ps >= 0) {
+      psp = row_span(a, s_ctx[ps]);
+      const int pc = pack_col(ps);
+      pblk0 = psp.first_blk + (pc >= 0 ? s_pblk[pc / P] : 0);
+    } else {
+      psp.kv_begin = 0;
+      psp.ctx = s_pblk[-1 - ps] * kBlockTokens;
+      pblk0 = 0;
+    }
+    const bool merged = ps < 0 || pack_col(ps) >= 0;  // the row's output goes through the merge
+    const int64_t pfb = s_cu[px];  // first block of the row in the per-head order
     if (i > 0) {  // a new row starts inside this wave's range
-      load_query<QT, D, G>(a, s_tok[pseq], pkvh, r, qg, qr);
-      cf = qk_operand<QT, D, KF>(qr, gvalid, a.qk_scale_log2, qop,
-                                 query_lane_ptr<QT, G>(a, s_tok[pseq], pkvh, r, qg));
+      load_query_at<QT, D>(col.q, qr);
+      cf = qk_operand<QT, D, KF>(qr, col.valid, a.qk_scale_log2, qop, col.q);
     }
 #pragma unroll
     for (int k = 0; k <= NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
     // invalid head columns never contribute; a finite start makes a block whose keys
     // are all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
-    m = gvalid ? -FLT_MAX : 0.f;
+    m = col.valid ? -FLT_MAX : 0.f;
     l = 0.f;
     VRange vr = {0.f, kVWeightCap};
-    const int pos0 = (psp.first_blk + (int)(b0 + i - pfb)) * kBlockTokens;
+    const int pos0 = (pblk0 + (int)(b0 + i - pfb)) * kBlockTokens;
     for (;;) {
       // the row's blocks in the current window: up to the first lane with another row
       const int wend = min(64 * (cw + 1), nblk);
@@ -267,8 +480,9 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
       const int iend = beyond ? 64 * cw + (int)__builtin_ctzll(beyond) : wend;
       for (; i < iend; ++i) {
         wait_block(i);
-        mfma_block<QT, D, G, KF>(stage(i), qop, cf, pos0 + (i - pstart) * kBlockTokens,
-                             psp.kv_begin, psp.ctx, r, qg, acc, m, l, vr, bad_score, masks);
+        mfma_block<QT, D, KF>(stage(i), qop, cf, pos0 + (i - pstart) * kBlockTokens,
+                              psp.kv_begin, psp.ctx, col.valid, r, qg, acc, m, l, vr, bad_score,
+                              masks);
         const int nx = i + NS;
         if (nx < nblk && (nx & 63) == 0) {
           // first block of window cw + 1: its ids were requested before block
@@ -291,32 +505,29 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
       }
       break;
     }
-    // write the piece [pstart, i): the final output when the whole row is in this
-    // wave, else a partial in slot 0 (the piece starts the wave's range) or 1 (it
-    // ends it)
+    // write the piece [pstart, i): the final output when a sequence row is whole in
+    // this wave and merges with nothing, else a partial: in the row's own slot when
+    // whole, in wave slot 0 (the piece starts the wave's range) or 1 (it ends it)
     const int iend = i;
     end_piece<D, KF>(acc, r);
     float lt = l + shfl_xor(l, 16);
     lt += shfl_xor(lt, 32);
     lt *= norm_scale<KF>();  // the factor the PV weights carry
-    const int64_t pfe = pfb + (s_cu[pseq + 1] - s_cu[pseq]) - 1;
-    if (b0 + pstart == pfb && b0 + iend - 1 == pfe) {
-      if (gvalid) {
+    const int64_t pfe = s_cu[px + 1] - 1;
+    const bool whole = b0 + pstart == pfb && b0 + iend - 1 == pfe;
+    if (whole && !merged) {
+      if (col.valid) {
         const float inv = 1.f / fmaxf(lt, FLT_MIN);
-        QT* op = static_cast<QT*>(a.out) + (int64_t)s_tok[pseq] * a.o_tok +
-                 (int64_t)(pkvh * G + r) * a.o_head;
-#pragma unroll
-        for (int k = 0; k < NPV; ++k)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) op[VB * (4 * qg + j) + k] = from_float<QT>(acc[k][j] * inv);
+        store_lane_out<QT, D>(static_cast<QT*>(a.out) + (int64_t)s_tok[ps] * a.o_tok +
+                                  (int64_t)(pkvh * G + r) * a.o_head + qg * (D / 4),
+                              acc, inv);
       }
-    } else if (gvalid) {
-      const int64_t slot = (gw * 2 + (pstart == 0 ? 0 : 1)) * G + r;
-      float* o = a.ws_o + slot * D;
-#pragma unroll
-      for (int k = 0; k < NPV; ++k)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[VB * (4 * qg + j) + k] = acc[k][j];
+    } else if (col.valid) {
+      const int64_t slot =
+          !whole ? wave_slot(a, gw, pstart == 0 ? 0 : 1, r)
+          : ps < 0 ? pack_slot(a, G, pkvh, -1 - ps, r)
+                   : packed_seq_slot(a, G, hkv, pkvh, pack_col(ps), r);
+      store_lane_f32<D>(a.ws_o + slot * D + qg * (D / 4), acc);
       if (qg == 0) {
         a.ws_ml[slot * 2] = m;
         a.ws_ml[slot * 2 + 1] = lt;
@@ -327,99 +538,160 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
 }
 
-// One wave per (sequence, q head): merge the pieces of rows split across waves.
-template <typename QT, int D>
-__global__ __launch_bounds__(256) void merge_streamk_kernel(AttnArgs a) {
-  constexpr int kPerLane = (D + kWave - 1) / kWave;
-  const int lane = threadIdx.x % kWave;
-  const int unit = blockIdx.x * kWaves + threadIdx.x / kWave;  // seq * Hq + h
-  if (unit >= a.num_seqs * a.num_q_heads) return;
-  const int seq = unit / a.num_q_heads, h = unit % a.num_q_heads;
-  const int G = a.num_q_heads / a.cache.num_kv_heads;
-  const int kvh = h / G, g = h % G;
-  const int cu0 = a.ws_seq[seq], cu1 = a.ws_seq[seq + 1], bseq = a.ws_seq[a.num_seqs];
-  if (cu1 == cu0) return;  // empty or not a decode row: nothing to merge
+// The pieces of one work row of kv head kvh over the per-head order [fb, fe]: their
+// count, and where piece p (0 <= p < count) keeps its partial for query column col.
+// A row within one range is one piece in the row's own slot (`own`, or -1 when the
+// wave wrote it as output); a longer row has one piece per range r0..r1, the first in
+// slot 1 of its wave when the row starts inside r0's range (it is that range's last
+// piece), every other in slot 0.
+struct RowPieces {
+  int64_t r0, own;
+  int count;
+  bool first_is_tail;
+};
+__device__ __forceinline__ RowPieces row_pieces(int64_t fb, int64_t fe, const SkSplit& sp,
+                                                int64_t own) {
+  RowPieces rp{0, own, 0, false};
+  if (fe < fb) return rp;  // no blocks
+  rp.r0 = sp.range_of(fb);
+  const int64_t r1 = sp.range_of(fe);
+  rp.count = (int)(r1 - rp.r0 + 1);
+  rp.first_is_tail = fb > 0 && sp.range_of(fb - 1) == rp.r0;
+  return rp;
+}
+__device__ __forceinline__ int64_t piece_slot(const AttnArgs& a, const RowPieces& rp, int p,
+                                              int hkv, int kvh, int col) {
+  const int64_t w = (rp.r0 + p) * hkv + kvh;  // the wave that streamed range r0 + p
+  const int64_t split = wave_slot(a, w, p == 0 && rp.first_is_tail ? 1 : 0, col);
+  return rp.count == 1 ? rp.own : split;
+}
+
+// One wave per (sequence, kv head): merge the pieces of sequences that no single
+// wave wrote: rows split across waves, and packed sequences (their pack's pieces,
+// columns p G .. p G + G-1 for member p, then their own). The G heads' rows of one
+// piece sit in consecutive slot columns (G x D contiguous floats), so lane L takes
+// elements [L E, L E + E) of them (E = G D / 64), of head hl = L E / D. Statistics go
+// lane-parallel: in a round of R = min(64 / G, kFast) pieces, lane u G + h holds
+// (m, l) of piece u, head h, and the maxima and weight sums reduce over the lanes of
+// one head. The merge_softmax rule (online_attention.py:42-63) and
+// SoftmaxState.output (:35-39).
+template <typename QT, int D, int G>
+__global__ __launch_bounds__(kWave) void merge_streamk_kernel(AttnArgs a) {
+  constexpr int E = G * D / kWave;  // floats per lane
+  static_assert(E >= 1 && G * D % kWave == 0, "lanes cover the group's rows");
+  constexpr int V = E >= 4 ? 4 : E;  // floats per load
+  constexpr int kRegs = 128 / E > 0 ? 128 / E : 1;  // partial rows held at once
+  constexpr int R0 = kWave / G < kFastPieces ? kWave / G : kFastPieces;
+  constexpr int R = R0 < kRegs ? R0 : kRegs;  // pieces per round
+  typedef float vec_t __attribute__((ext_vector_type(V)));
+  const int lane = threadIdx.x;
   const int hkv = a.cache.num_kv_heads;
-  const int64_t Wr = streamk_ranges(a, bseq, hkv);
-  const int64_t fb = cu0, fe = cu1 - 1;  // the row's blocks in the per-head order
-  const int64_t r0 = range_of(fb, bseq, Wr), r1 = range_of(fe, bseq, Wr);
-  if (r0 == r1) return;  // written whole by one wave
-  const int pieces = (int)(r1 - r0 + 1);
-  const bool first_is_tail = (int64_t)bseq * r0 / Wr < fb;  // the row is r0's last piece (slot 1)
+  const int seq = blockIdx.x / hkv, kvh = blockIdx.x % hkv;
+  const int hl = lane * E / D;
+  const int xs = a.num_packs + seq;
+  const int cu0 = a.ws_seq[xs], cu1 = a.ws_seq[xs + 1];
+  const int bseq = a.ws_seq[a.num_packs + a.num_seqs];
+  const int pb = a.ws_seq[a.num_packs];  // blocks of the packs
+  // a packed sequence: its pack column and the pack's block range, in one record
+  int pc = -1, pk0 = 0, pk1 = 0;
+  if (a.num_packs > 0) {
+    pc = a.ws_pack[3 * seq];
+    pk0 = a.ws_pack[3 * seq + 1];
+    pk1 = a.ws_pack[3 * seq + 2];
+  }
+  const SkSplit split(a, bseq, pb, hkv);
+  RowPieces own = row_pieces(cu0, cu1 - 1, split, -1);
+  RowPieces pack{0, -1, 0, false};
+  int pcol0 = 0;  // the pack column of this sequence's head 0
+  if (pc >= 0) {
+    const int k = pc / a.pack_rows;
+    pcol0 = (pc % a.pack_rows) * G;
+    pack = row_pieces(pk0, pk1 - 1, split, pack_slot(a, G, kvh, k, pcol0));
+    own.own = packed_seq_slot(a, G, hkv, kvh, pc, 0);
+  } else if (own.count <= 1) {
+    return;  // empty (zeroed) or written whole by one wave
+  }
+  const int pieces = pack.count + own.count;
+  // slot (column of head 0) of piece p, the pack's pieces first
   auto slot_of = [&](int p) __attribute__((always_inline)) -> int64_t {
-    const int64_t w = (r0 + p) * hkv + kvh;  // the wave that streamed range r0 + p for this head
-    return (w * 2 + (p == 0 && first_is_tail ? 1 : 0)) * G + g;
+    const bool in_pack = p < pack.count;
+    const RowPieces& rp = in_pack ? pack : own;
+    return piece_slot(a, rp, in_pack ? p : p - pack.count, hkv, kvh, in_pack ? pcol0 : 0);
   };
-  float L = 0.f, O[kPerLane];
+  const int su = lane / G, sh = lane % G;  // the (piece in round, head) of this lane's statistics
+  auto head_max = [&](float x) __attribute__((always_inline)) -> float {
 #pragma unroll
-  for (int e = 0; e < kPerLane; ++e) O[e] = 0.f;
-  if (pieces <= kFastPieces) {
-    // common case: every load (statistics and partial rows) issues before the first use
-    float mp = -INFINITY, lp = 0.f;
-    if (lane < pieces) {
-      mp = a.ws_ml[slot_of(lane) * 2];
-      lp = a.ws_ml[slot_of(lane) * 2 + 1];
-    }
-    float v[kFastPieces][kPerLane];
+    for (int off = G; off < kWave; off <<= 1) x = fmaxf(x, shfl_xor(x, off));
+    return x;
+  };
+  auto head_sum = [&](float x) __attribute__((always_inline)) -> float {
 #pragma unroll
-    for (int u = 0; u < kFastPieces; ++u) {
-      const float* op = a.ws_o + slot_of(u < pieces ? u : 0) * D;
-#pragma unroll
-      for (int e = 0; e < kPerLane; ++e) {
-        const int d = lane + e * kWave;
-        v[u][e] = (u < pieces && d < D) ? op[d] : 0.f;
-      }
-    }
-    const float M = wave_max(mp);
-    const float w = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
-    L = wave_sum(lp * w);
-#pragma unroll
-    for (int u = 0; u < kFastPieces; ++u) {
-      const float wq = __shfl(w, u, kWave);
-#pragma unroll
-      for (int e = 0; e < kPerLane; ++e) O[e] = fmaf(v[u][e], wq, O[e]);
-    }
-  } else {
-    float M = -INFINITY;
-    for (int p = lane; p < pieces; p += kWave) M = fmaxf(M, a.ws_ml[slot_of(p) * 2]);
-    M = wave_max(M);
-    for (int p0 = 0; p0 < pieces; p0 += kWave) {
-      const int p = p0 + lane;
-      float w = 0.f, lw = 0.f;
-      if (p < pieces) {
-        const float mp = a.ws_ml[slot_of(p) * 2];
-        w = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
-        lw = a.ws_ml[slot_of(p) * 2 + 1] * w;
-      }
-      L += wave_sum(lw);
-      const int np = min(kWave, pieces - p0);
-      for (int q0 = 0; q0 < np; q0 += 8) {
-        float v[8][kPerLane], wq[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int q = min(q0 + u, np - 1);
-          wq[u] = q0 + u < np ? __shfl(w, q, kWave) : 0.f;
-          const float* op = a.ws_o + slot_of(p0 + q) * D;
-#pragma unroll
-          for (int e = 0; e < kPerLane; ++e) {
-            const int d = lane + e * kWave;
-            v[u][e] = d < D ? op[d] : 0.f;
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-#pragma unroll
-          for (int e = 0; e < kPerLane; ++e) O[e] = fmaf(v[u][e], wq[u], O[e]);
-      }
+    for (int off = G; off < kWave; off <<= 1) x += shfl_xor(x, off);
+    return x;
+  };
+  // one round: pieces [p0, p0 + R); returns this lane's slot and loads its statistics
+  auto stats = [&](int p0, int64_t& sl, float& mp, float& lp) __attribute__((always_inline)) {
+    const int p = p0 + su;
+    const bool live = su < R && p < pieces;
+    sl = slot_of(live ? p : p0);
+    mp = live ? a.ws_ml[(sl + sh) * 2] : -INFINITY;
+    lp = live ? a.ws_ml[(sl + sh) * 2 + 1] : 0.f;
+  };
+  float M = -INFINITY;  // of head sh (lane-parallel layout)
+  if (pieces > R) {     // several rounds: the maxima first
+    for (int p0 = 0; p0 < pieces; p0 += R) {
+      int64_t sl;
+      float mp, lp;
+      stats(p0, sl, mp, lp);
+      M = fmaxf(M, head_max(mp));
     }
   }
-  QT* out = static_cast<QT*>(a.out) + (int64_t)decode_token(a, seq) * a.o_tok +
-            (int64_t)h * a.o_head;
-  const float inv_l = 1.f / fmaxf(L, FLT_MIN);
+  float L = 0.f, O[E];
 #pragma unroll
-  for (int e = 0; e < kPerLane; ++e) {
-    const int d = lane + e * kWave;
-    if (d < D) out[d] = from_float<QT>(O[e] * inv_l);
+  for (int e = 0; e < E; ++e) O[e] = 0.f;
+  for (int p0 = 0; p0 < pieces; p0 += R) {
+    int64_t sl;
+    float mp, lp;
+    stats(p0, sl, mp, lp);
+    float v[R][E];
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const int64_t s_u = ((int64_t)__builtin_amdgcn_readlane((int)(sl >> 32), u * G) << 32) |
+                          (uint32_t)__builtin_amdgcn_readlane((int)sl, u * G);
+      const float* src = a.ws_o + s_u * D + lane * E;
+      const bool live = p0 + u < pieces;
+#pragma unroll
+      for (int e = 0; e < E; e += V) {
+        const vec_t x = live ? *reinterpret_cast<const vec_t*>(src + e) : vec_t{};
+#pragma unroll
+        for (int c = 0; c < V; ++c) v[u][e + c] = x[c];
+      }
+    }
+    const float mx = pieces > R ? M : head_max(mp);
+    const float w = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - mx);
+    L += head_sum(lp * w);
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const float wu = __shfl(w, u * G + hl, kWave);
+#pragma unroll
+      for (int e = 0; e < E; ++e) O[e] = fmaf(v[u][e], wu, O[e]);
+    }
+  }
+  const float inv_l = 1.f / fmaxf(__shfl(L, hl, kWave), FLT_MIN);
+  QT* out = static_cast<QT*>(a.out) + (int64_t)decode_token(a, seq) * a.o_tok +
+            (int64_t)(kvh * G + hl) * a.o_head + lane * E % D;
+  QT r[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) r[e] = from_float<QT>(O[e] * inv_l);
+  if constexpr (E % 8 == 0) {
+#pragma unroll
+    for (int e = 0; e < E; e += 8)
+      *reinterpret_cast<uint4*>(out + e) = *reinterpret_cast<const uint4*>(r + e);
+  } else if constexpr (E == 4) {
+    *reinterpret_cast<uint2*>(out) = *reinterpret_cast<const uint2*>(r);
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) out[e] = r[e];
   }
 }
 
@@ -445,9 +717,9 @@ int device_cus() {
   return 256;
 }
 
-template <typename QT, int D, int G>
+template <typename QT, int D, int G, bool kPacks>
 int launch(AttnArgs a, hipStream_t stream) {
-  auto kernel = decode_streamk_kernel<QT, D, G>;
+  auto kernel = decode_streamk_kernel<QT, D, G, kPacks>;
   constexpr int NW = sk_waves<D>();
   // launch one wave per resident slot (whole workgroups) and at least min_waves (the
   // host-side bound), at most the workspace capacity passed in total_waves; the
@@ -460,9 +732,8 @@ int launch(AttnArgs a, hipStream_t stream) {
   a.pref_waves = (int32_t)(resident < waves ? resident : waves);
   const int wgs = (int)(waves / NW);
   hipLaunchKernelGGL(kernel, dim3(wgs), dim3(NW * kWave), 0, stream, a);
-  const int units = a.num_seqs * a.num_q_heads;
-  hipLaunchKernelGGL((merge_streamk_kernel<QT, D>), dim3((units + kWaves - 1) / kWaves),
-                     dim3(kWaves * kWave), 0, stream, a);
+  hipLaunchKernelGGL((merge_streamk_kernel<QT, D, G>), dim3(a.num_seqs * a.cache.num_kv_heads),
+                     dim3(kWave), 0, stream, a);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "paged_attention (stream-K) launch");
 }
@@ -470,12 +741,12 @@ int launch(AttnArgs a, hipStream_t stream) {
 template <typename QT, int D>
 int dispatch_group(const AttnArgs& a, int G, hipStream_t s) {
   switch (G) {
-    case 1: return launch<QT, D, 1>(a, s);
-    case 2: return launch<QT, D, 2>(a, s);
-    case 4: return launch<QT, D, 4>(a, s);
-    case 8: return launch<QT, D, 8>(a, s);
+    case 1: return a.num_packs > 0 ? launch<QT, D, 1, true>(a, s) : launch<QT, D, 1, false>(a, s);
+    case 2: return a.num_packs > 0 ? launch<QT, D, 2, true>(a, s) : launch<QT, D, 2, false>(a, s);
+    case 4: return a.num_packs > 0 ? launch<QT, D, 4, true>(a, s) : launch<QT, D, 4, false>(a, s);
+    case 8: return a.num_packs > 0 ? launch<QT, D, 8, true>(a, s) : launch<QT, D, 8, false>(a, s);
     case 16:
-      if constexpr (D <= 128) return launch<QT, D, 16>(a, s);
+      if constexpr (D <= 128) return launch<QT, D, 16, false>(a, s);  // 16 columns: no packs
       [[fallthrough]];
     default:
       return fail(ASTR_EUNSUPPORTED, "GQA group size %d not supported", G);
@@ -506,6 +777,9 @@ int launch_streamk_kf<KF>(const AttnArgs& a, int32_t q_dtype, hipStream_t stream
 
 #if ASTR_KF == 0
 int stream_k_max_seqs() { return kMaxSeqsSK; }
+int stream_k_max_packs() { return kMaxPacksSK; }
+int stream_k_max_pack_seqs() { return kMaxPackSeqsSK; }
+int stream_k_work_rows(int) { return kMaxRowsSK; }
 #endif
 
 }  // namespace attn

@@ -62,8 +62,9 @@ bool use_streamk(int32_t q_dtype, int32_t partition_tokens, int32_t num_seqs) {
 }
 
 // Workspace layouts. Partitioned: [acc][(m,l)] per (seq, q head, partition).
-// Stream-K: [per-sequence block prefix][acc][(m,l)] per (wave, 2 slots, head of the group),
-// sized for every wave the GPU can hold.
+// Stream-K: [block prefix over work rows, per-sequence pack column][acc][(m,l)] per
+// column of the partial slots: (wave, 2 slots, slot columns) sized for every wave the
+// GPU can hold, then with prefix packs the packs' and packed sequences' own slots.
 struct Layout {
   size_t seq_bytes, o_bytes, ml_bytes;
   int64_t waves;  // stream-K wave count of the launch (0 for partitioned)
@@ -84,7 +85,7 @@ Layout partitioned_layout(int32_t num_seqs, int32_t num_q_heads, int32_t head_di
 // the layout never holds fewer waves than the block count needs.
 Layout streamk_layout(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                       int32_t head_dim, int32_t max_context_len, int32_t window,
-                      int64_t max_waves) {
+                      int64_t max_waves, int32_t num_packs = 0, int32_t pack_rows = 0) {
   const int64_t need = (max_total_blocks(num_seqs, num_kv_heads, max_context_len, window) +
                         kMaxBlocksPerWaveSK - 1) / kMaxBlocksPerWaveSK;
   int64_t cap = (int64_t)device_cus() * kMaxResidentWavesPerCU;
@@ -92,10 +93,14 @@ Layout streamk_layout(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_head
   cap = cap > need ? cap : need;
   cap = (cap + kWaves - 1) / kWaves * kWaves;
   const int64_t group = num_q_heads / num_kv_heads;
+  const int64_t cols = num_packs > 0 ? (int64_t)pack_rows * group : group;
+  const int64_t row_cols = num_packs > 0 ? 2 * (int64_t)num_kv_heads * num_packs * pack_rows * group : 0;
+  const size_t slots = (size_t)(cap * 2 * cols + row_cols);
   Layout w;
-  w.seq_bytes = align256(((size_t)num_seqs + 1) * sizeof(int32_t));
-  w.o_bytes = align256((size_t)cap * 2 * group * head_dim * sizeof(float));
-  w.ml_bytes = align256((size_t)cap * 2 * group * 2 * sizeof(float));
+  w.seq_bytes =
+      align256(((size_t)stream_k_work_rows(head_dim) + 1 + 3 * (size_t)num_seqs) * sizeof(int32_t));
+  w.o_bytes = align256(slots * head_dim * sizeof(float));
+  w.ml_bytes = align256(slots * 2 * sizeof(float));
   w.waves = cap;
   return w;
 }
@@ -106,7 +111,9 @@ int64_t streamk_waves_in(size_t bytes, int32_t num_seqs, int32_t num_q_heads,
                          int32_t num_kv_heads, int32_t head_dim) {
   const size_t group = (size_t)(num_q_heads / num_kv_heads);
   const size_t per_wave = 2 * group * ((size_t)head_dim + 2) * sizeof(float);
-  const size_t fixed = align256(((size_t)num_seqs + 1) * sizeof(int32_t)) + 2 * 256;
+  const size_t fixed =
+      align256(((size_t)stream_k_work_rows(head_dim) + 1 + 3 * (size_t)num_seqs) * sizeof(int32_t)) +
+      2 * 256;
   return bytes > fixed ? (int64_t)((bytes - fixed) / per_wave) : 0;
 }
 
@@ -122,19 +129,22 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 }  // namespace attn
 }  // namespace astr
 
-extern "C" size_t astr_paged_attention_i8_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
-                                                          int32_t num_kv_heads, int32_t head_dim,
-                                                          int32_t max_context_len,
-                                                          int32_t partition_tokens) {
-  using namespace astr::attn;
+namespace astr {
+namespace attn {
+namespace {
+
+size_t required_workspace(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t max_context_len, int32_t partition_tokens,
+                       int32_t num_packs, int32_t pack_rows) {
   if (num_seqs < 0 || num_q_heads < 1 || num_kv_heads < 1 || head_dim < 1 ||
-      max_context_len < 0 || partition_tokens < 0 || num_q_heads % num_kv_heads)
+      max_context_len < 0 || partition_tokens < 0 || num_q_heads % num_kv_heads ||
+      num_packs < 0 || (num_packs > 0 && pack_rows < 1))
     return 0;
   if (num_seqs == 0) return 0;
   // stream-K is chosen per query dtype at launch; size for it whenever it may run
   if (partition_tokens == 0 && num_seqs <= stream_k_max_seqs()) {
     const Layout sk = streamk_layout(num_seqs, num_q_heads, num_kv_heads, head_dim,
-                                     max_context_len, 0, 0);
+                                     max_context_len, 0, 0, num_packs, pack_rows);
     const Layout pt = partitioned_layout(num_seqs, num_q_heads, head_dim,
                                          max_parts_for(max_context_len, kDefaultPartitionTokens));
     return sk.total() > pt.total() ? sk.total() : pt.total();
@@ -143,6 +153,25 @@ extern "C" size_t astr_paged_attention_i8_workspace_bytes(int32_t num_seqs, int3
   if (!valid_partition(pt)) return 0;
   return partitioned_layout(num_seqs, num_q_heads, head_dim, max_parts_for(max_context_len, pt))
       .total();
+}
+
+}  // namespace
+}  // namespace attn
+}  // namespace astr
+
+extern "C" size_t astr_paged_attention_i8_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                                          int32_t num_kv_heads, int32_t head_dim,
+                                                          int32_t max_context_len,
+                                                          int32_t partition_tokens) {
+  return astr::attn::required_workspace(num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                     max_context_len, partition_tokens, 0, 0);
+}
+
+extern "C" size_t astr_paged_attention_i8_shared_workspace_bytes(
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t max_context_len, int32_t num_packs, int32_t rows_per_pack) {
+  return astr::attn::required_workspace(num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                     max_context_len, 0, num_packs, rows_per_pack);
 }
 
 namespace {
@@ -155,7 +184,9 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
                     int32_t block_table_stride, const int32_t* context_lens, int32_t num_seqs,
                     int32_t num_q_heads, int32_t max_context_len, float scale, int32_t window,
                     int32_t partition_tokens, void* workspace, size_t workspace_bytes,
-                    int32_t* err_flag, void* stream, bool fixed_scratch = false) {
+                    int32_t* err_flag, void* stream, bool fixed_scratch = false,
+                    const int32_t* packs = nullptr, int32_t num_packs = 0,
+                    int32_t pack_rows = 0) {
   using namespace astr;
   using namespace astr::attn;
   if (cache == nullptr || err_flag == nullptr)
@@ -188,6 +219,25 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
                 "up to %d", partition_tokens, kBlockTokens * kWaves,
                 kBlockTokens * kWaves * kMaxBlocksPerWave);
   const bool streamk = use_streamk(q_dtype, partition_tokens, num_seqs);
+  const int group = num_q_heads / cache->num_kv_heads;
+  if (num_packs < 0) return fail(ASTR_EINVAL, "num_packs must be >= 0");
+  if (num_packs > 0) {
+    if (packs == nullptr || (reinterpret_cast<uintptr_t>(packs) & 3u) != 0)
+      return fail(ASTR_EINVAL, "a 4-byte aligned pack table is required for %d packs", num_packs);
+    if (pack_rows < 2 || pack_rows * group > 16)
+      return fail(ASTR_EINVAL, "rows_per_pack %d must be in [2, 16 / G = %d]", pack_rows,
+                  16 / group);
+    if (num_packs > stream_k_max_packs() ||
+        (int64_t)num_packs * pack_rows > stream_k_max_pack_seqs())
+      return fail(ASTR_EUNSUPPORTED, "%d packs of %d rows: at most %d packs and %d pack rows",
+                  num_packs, pack_rows, stream_k_max_packs(), stream_k_max_pack_seqs());
+    if (window != 0)
+      return fail(ASTR_EUNSUPPORTED, "prefix packs need window == 0 (the packed blocks are "
+                  "visible to every member)");
+    // the partitioned kernels read every row's blocks themselves, and batches beyond
+    // the pack tables run the stream-K kernel without them
+    if (!streamk || num_seqs > stream_k_max_pack_seqs()) num_packs = 0;
+  }
   const int pt = partition_tokens == 0 ? kDefaultPartitionTokens : partition_tokens;
   if ((int64_t)max_context_len > (int64_t)block_table_stride * kBlockTokens)
     return fail(ASTR_EINVAL, "max_context_len %d exceeds block table capacity %lld",
@@ -219,12 +269,13 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
                 "stream-K partials for %d sequences x %d query heads", workspace_bytes, num_seqs,
                 num_q_heads);
   const Layout ws = streamk ? streamk_layout(num_seqs, num_q_heads, cache->num_kv_heads,
-                                             cache->head_dim, max_context_len, 0, sk_limit)
+                                             cache->head_dim, max_context_len, 0, sk_limit,
+                                             num_packs, pack_rows)
                             : partitioned_layout(num_seqs, num_q_heads, cache->head_dim, parts);
   const size_t need = fixed_scratch ? ws.total()
-                                    : astr_paged_attention_i8_workspace_bytes(
-                                          num_seqs, num_q_heads, cache->num_kv_heads,
-                                          cache->head_dim, max_context_len, partition_tokens);
+                                    : required_workspace(num_seqs, num_q_heads, cache->num_kv_heads,
+                                                         cache->head_dim, max_context_len,
+                                                         partition_tokens, num_packs, pack_rows);
   if (fixed_scratch && need > workspace_bytes)
     return fail(ASTR_EINVAL, "this launch needs %zu bytes of split-K scratch, more than the "
                 "%zu bytes the allocation-free entry point holds", need, workspace_bytes);
@@ -257,9 +308,14 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
   a.total_waves = (int32_t)ws.waves;  // capacity; the stream-K launcher settles the count
   a.min_waves = (int32_t)streamk_min_waves(
       max_total_blocks(num_seqs, cache->num_kv_heads, max_context_len, window));
+  a.packs = num_packs > 0 ? packs : nullptr;
+  a.num_packs = num_packs;
+  a.pack_rows = num_packs > 0 ? pack_rows : 1;
+  a.slot_cols = a.pack_rows * group;
   if (ws.total() > 0) {
     char* base = static_cast<char*>(workspace);
     a.ws_seq = reinterpret_cast<int32_t*>(base);
+    if (streamk) a.ws_pack = a.ws_seq + stream_k_work_rows(cache->head_dim) + 1;
     a.ws_o = reinterpret_cast<float*>(base + ws.seq_bytes);
     a.ws_ml = reinterpret_cast<float*>(base + ws.seq_bytes + ws.o_bytes);
   }
@@ -303,6 +359,20 @@ extern "C" int astr_paged_attention_varlen_i8(
                          max_query_len, causal, block_tables, block_table_stride, context_lens,
                          num_seqs, num_q_heads, max_context_len, scale, window, partition_tokens,
                          workspace, workspace_bytes, err_flag, stream);
+}
+
+extern "C" int astr_paged_attention_i8_shared(
+    const astr_paged_kv* cache, const void* query, int32_t q_dtype, int64_t q_token_stride,
+    int64_t q_head_stride, void* out, int64_t out_token_stride, int64_t out_head_stride,
+    const int32_t* block_tables, int32_t block_table_stride, const int32_t* context_lens,
+    int32_t num_seqs, int32_t num_q_heads, int32_t max_context_len, float scale, int32_t window,
+    const int32_t* packs, int32_t num_packs, int32_t rows_per_pack, void* workspace,
+    size_t workspace_bytes, int32_t* err_flag, void* stream) {
+  return paged_attention(cache, query, q_dtype, q_token_stride, q_head_stride, out,
+                         out_token_stride, out_head_stride, nullptr, num_seqs, 1, 1, block_tables,
+                         block_table_stride, context_lens, num_seqs, num_q_heads, max_context_len,
+                         scale, window, 0, workspace, workspace_bytes, err_flag, stream, false,
+                         packs, num_packs, rows_per_pack);
 }
 
 // ---- allocation-free decode entry point: split-K partials in a fixed device array

@@ -274,15 +274,20 @@ class PagedKVCache:
         index.record_stream(stream)
 
     def workspace_bytes(self, num_seqs, num_q_heads, max_context_len,
-                        partition_tokens=DEFAULT_PARTITION_TOKENS):
+                        partition_tokens=DEFAULT_PARTITION_TOKENS, prefix_packs=None):
+        if prefix_packs is not None:
+            return int(_native.lib().astr_paged_attention_i8_shared_workspace_bytes(
+                num_seqs, num_q_heads, self.num_kv_heads, self.head_dim, max_context_len,
+                prefix_packs.num_packs, prefix_packs.rows_per_pack))
         return int(_native.lib().astr_paged_attention_i8_workspace_bytes(
             num_seqs, num_q_heads, self.num_kv_heads, self.head_dim, max_context_len,
             partition_tokens))
 
     def workspace(self, num_seqs, num_q_heads, max_context_len,
-                  partition_tokens=DEFAULT_PARTITION_TOKENS):
+                  partition_tokens=DEFAULT_PARTITION_TOKENS, prefix_packs=None):
         """Split-K scratch owned by this cache, grown on demand (None when unneeded)."""
-        need = self.workspace_bytes(num_seqs, num_q_heads, max_context_len, partition_tokens)
+        need = self.workspace_bytes(num_seqs, num_q_heads, max_context_len, partition_tokens,
+                                    prefix_packs)
         if not need:
             return None
         if self._workspace is None or self._workspace.numel() < need:
@@ -292,7 +297,7 @@ class PagedKVCache:
     def paged_attention(self, layer, query, block_tables, context_lens, *, max_context_len,
                         scale=None, window=None, partition_tokens=DEFAULT_PARTITION_TOKENS,
                         query_start_loc=None, max_query_len=None, causal=True,
-                        out=None, workspace=None, work=None, check=False):
+                        out=None, workspace=None, work=None, check=False, prefix_packs=None):
         """Paged attention of this layer's arena for every row of a step.
 
         Decode (``query_start_loc=None``): one query token per sequence, ``query``
@@ -311,7 +316,12 @@ class PagedKVCache:
         upper bound of ``context_lens``. ``scale`` defaults to ``head_dim ** -0.5``
         (nn/attention.py:130); ``window`` keeps keys ``k > position - window``
         (online_attention.py:183-184). Returns the query's shape in the query
-        dtype (online_attention.py:219)."""
+        dtype (online_attention.py:219).
+
+        ``prefix_packs`` (decode, automatic split, no window): a
+        ``prefix_plan.plan_prefix_packs`` plan of the same block tables; rows of a
+        pack read their shared prefix blocks once for the whole pack. Same outputs
+        as without it."""
         if query.ndim != 3 or query.shape[-1] != self.head_dim or query.device != self.device:
             raise ValueError("query must be [tokens, num_q_heads, head_dim] on the cache device")
         if query.dtype not in _DTYPE_CODES:
@@ -345,15 +355,23 @@ class PagedKVCache:
             raise ValueError("Attention scale must be finite and positive")
         if window is not None and (type(window) is not int or window < 1):
             raise ValueError("Invalid causal/window semantics")
+        if prefix_packs is not None:
+            if query_start_loc is not None or partition_tokens != 0 or window is not None:
+                raise ValueError("prefix packs serve decode batches under the automatic split "
+                                 "without a window")
+            if prefix_packs.num_seqs != num_seqs or prefix_packs.table.device != self.device:
+                raise ValueError("prefix packs were planned for other block tables")
         if out is None:
             out = torch.empty_like(query)
         elif (not isinstance(out, torch.Tensor) or out.shape != query.shape
               or out.dtype != query.dtype or out.device != self.device or out.stride(-1) != 1):
             raise ValueError("out must match the query's shape, dtype and device, with "
                              "contiguous rows")
-        need = self.workspace_bytes(num_seqs, num_q_heads, max_context_len, partition_tokens)
+        need = self.workspace_bytes(num_seqs, num_q_heads, max_context_len, partition_tokens,
+                                    prefix_packs)
         if need and workspace is None:
-            workspace = self.workspace(num_seqs, num_q_heads, max_context_len, partition_tokens)
+            workspace = self.workspace(num_seqs, num_q_heads, max_context_len, partition_tokens,
+                                       prefix_packs)
         elif need:
             if (not isinstance(workspace, torch.Tensor) or workspace.dtype != torch.uint8
                     or workspace.device != self.device or not workspace.is_contiguous()):
@@ -363,7 +381,15 @@ class PagedKVCache:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         ws = workspace.data_ptr() if need else None
         lib = _native.lib()
-        if query_start_loc is None:
+        if prefix_packs is not None:
+            rc = lib.astr_paged_attention_i8_shared(
+                self._descs[layer], query.data_ptr(), _DTYPE_CODES[query.dtype], query.stride(0),
+                query.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
+                block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(),
+                num_seqs, num_q_heads, max_context_len, scale, 0, prefix_packs.table.data_ptr(),
+                prefix_packs.num_packs, prefix_packs.rows_per_pack, ws, need,
+                self.err_flag.data_ptr(), stream)
+        elif query_start_loc is None:
             rc = lib.astr_paged_attention_i8(
                 self._descs[layer], query.data_ptr(), _DTYPE_CODES[query.dtype], query.stride(0),
                 query.stride(1), out.data_ptr(), out.stride(0), out.stride(1),

@@ -28,11 +28,13 @@ from __future__ import annotations
 import copy
 import time
 
+import numpy as np
 import torch
 
 from .attention_backend import BACKEND, KernelWork, UnsupportedAttentionBackend
 from .kv_quantization import KVQuantization
 from .paged_pool import KVStateCodec, PagedStatePool, StateError
+from .prefix_plan import plan_prefix_packs
 
 
 def pack_rows(x, counts):
@@ -123,6 +125,11 @@ class PagedAttentionStep:
             self.slot_mapping = _device_ints(slots, torch.int64, device)
             cache.write_key_valid(self.slot_mapping,
                                   None if valid is None else valid.to(device, non_blocking=True))
+            # decode steps: the rows' page lists, for prefix packs (planned per query-head
+            # count at the first attend)
+            self._pages = ([[ref.index for ref in r.pages] for r in self.reservations]
+                           if len(counts) > 1 and self.max_query_len == 1 else None)
+            self._packs = {}
         except BaseException:
             if self._tables is not None:
                 self._tables.__exit__(None, None, None)
@@ -143,11 +150,33 @@ class PagedAttentionStep:
         cache = self.pool.cache
         cache.append(layer, key, value, self.slot_mapping)
         ws_work = self.work
+        packs = (self._prefix_packs(query.shape[1])
+                 if window is None and self.partition_tokens == 0 else None)
+        if packs is not None:  # rows aliasing shared prefix pages read them once per pack
+            return cache.paged_attention(
+                layer, query, self.block_tables, self.context_lens,
+                max_context_len=self.max_context_len, scale=scale, out=out, work=ws_work,
+                partition_tokens=0, prefix_packs=packs)
         return cache.paged_attention(
             layer, query, self.block_tables, self.context_lens,
             max_context_len=self.max_context_len, scale=scale, window=window,
             partition_tokens=self.partition_tokens, query_start_loc=self.query_start_loc,
             max_query_len=self.max_query_len, causal=True, out=out, work=ws_work)
+
+    def _prefix_packs(self, num_q_heads):
+        if self._pages is None:
+            return None
+        if num_q_heads not in self._packs:
+            width = max(len(p) for p in self._pages)
+            tables = np.full((len(self._pages), width), -1, np.int64)
+            for row, pages in enumerate(self._pages):
+                tables[row, : len(pages)] = pages
+            lens = [r.length for r in self.reservations]
+            cache = self.pool.cache
+            self._packs[num_q_heads] = plan_prefix_packs(
+                tables, lens, num_q_heads, cache.num_kv_heads, device=cache.device,
+                block_size=cache.block_size)
+        return self._packs[num_q_heads]
 
     def commit(self):
         """Wait for the device, raise any flagged error (then nothing is committed),

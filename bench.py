@@ -149,9 +149,11 @@ def build_arena(w, layers, device, hold_last=False):
     return cache, step_batch
 
 
-def attention_caller(w, cache, q, device, partition, rows=None):
+def attention_caller(w, cache, q, device, partition, rows=None, packs=False):
     """``call(layer)`` running one attention call over the workload (or over its rows
-    ``rows``, a sub-workload of the same arena) and the workload it covers."""
+    ``rows``, a sub-workload of the same arena) and the workload it covers. With
+    ``packs`` a decode batch gets the prefix-pack plan of its block tables, built once
+    on the host as the runner builds it at schedule time (outside the timed calls)."""
     import numpy as np
     import torch
 
@@ -169,14 +171,22 @@ def attention_caller(w, cache, q, device, partition, rows=None):
     varlen = w.query_lens is not None
     qsl = wl.device_query_start(w, device) if varlen else None
     out = torch.empty_like(q)
-    ws_bytes = cache.workspace_bytes(w.num_seqs, w.num_q_heads, w.max_context_len, partition)
+    plan = None
+    if packs and not varlen and partition == 0:
+        from aster_amd import plan_prefix_packs
+
+        plan = plan_prefix_packs(w.block_tables, w.context_lens, w.num_q_heads, w.num_kv_heads,
+                                 device=device)
+    ws_bytes = cache.workspace_bytes(w.num_seqs, w.num_q_heads, w.max_context_len, partition,
+                                     prefix_packs=plan)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=device)
 
     def call(layer):
         cache.paged_attention(layer, q, tables, lens, max_context_len=w.max_context_len,
                               scale=w.scale, partition_tokens=partition, out=out, workspace=ws,
                               query_start_loc=qsl,
-                              max_query_len=w.max_query_len if varlen else None)
+                              max_query_len=w.max_query_len if varlen else None,
+                              prefix_packs=plan)
 
     return call, w
 
@@ -221,13 +231,17 @@ def extra_measurements(device, partition, calls):
     out[w.name] = entry
     del cache
     torch.cuda.empty_cache()
-    # config 4: HBM fraction on the distinct K/V bytes, effective rate on the logical
+    # config 4: HBM fraction on the distinct K/V bytes, effective rate on the logical;
+    # with the prefix-pack plan (as the runner plans decode steps), and without it
     w = wl.config4()
     cache, _ = build_arena(w, 2, device)
     q = wl.queries(w, device)
     call, _ = attention_caller(w, cache, q, device, partition)
+    unplanned = time_calls(call, calls, 2)
+    call, _ = attention_caller(w, cache, q, device, partition, packs=True)
     avg, med = time_calls(call, calls, 2)
     entry = hbm_entry(w, avg, med)
+    entry["without_plan_call_us"] = unplanned[0] * 1e3
     entry["logical_effective_gbs"] = entry.pop("achieved_gbs")
     entry["logical_frac"] = entry.pop("frac")
     unique = w.unique_kv_bytes() + (w.algorithmic_bytes() - w.attended_tokens * w.num_kv_heads
@@ -264,7 +278,7 @@ def main():
     L = args.layers
     cache, step_batch = build_arena(w, L, device, hold_last=True)
     q = wl.queries(w, device)
-    call, _ = attention_caller(w, cache, q, device, args.partition)
+    call, _ = attention_caller(w, cache, q, device, args.partition, packs=True)
     k_new, v_new, slots = step_batch
     varlen = w.query_lens is not None
 

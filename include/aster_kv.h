@@ -231,6 +231,45 @@ size_t astr_paged_attention_i8_workspace_bytes(int32_t num_seqs, int32_t num_q_h
                                                int32_t partition_tokens);
 
 /*
+ * astr_paged_attention_i8 (automatic split) for a decode batch whose block tables
+ * alias shared prefix pages: the reference reads such pages once per row, as
+ * PagedAttentionRunner.forward_batch does for the PrefixCache's shared page refs
+ * (paged_attention.py:168-215 over state.py:599-625). `packs` is a host-built plan
+ * of num_packs records of 1 + rows_per_pack int32 in device memory:
+ *   [shared_blocks, member_0, ..., member_{rows_per_pack-1}]  (member -1: empty)
+ * Every member's block table must begin with the same shared_blocks physical ids
+ * (those of the first member), all of them visible (shared_blocks * 16 <= ctx).
+ * The stream-K kernel reads each pack's blocks once for all its members, query
+ * column p * G + g for head g of member p (2 <= rows_per_pack, rows_per_pack * G <=
+ * 16), then each member's remaining blocks as its own row, and merges the two with
+ * the split-K rule. Outputs are those of astr_paged_attention_i8 on the same
+ * tables. At most 128 packs and 256 pack rows; window must be 0. A member that is
+ * not a decode row, is listed twice or sees fewer than shared_blocks * 16 tokens
+ * raises ASTR_FLAG_BAD_INDEX and is dropped from its pack. fp32 queries, batches
+ * beyond 256 sequences and num_packs == 0 run astr_paged_attention_i8's kernels
+ * without the plan. workspace: >=
+ * astr_paged_attention_i8_shared_workspace_bytes(...) bytes, 256-byte aligned.
+ */
+int astr_paged_attention_i8_shared(const astr_paged_kv* cache, const void* query,
+                                   int32_t q_dtype, int64_t q_token_stride,
+                                   int64_t q_head_stride, void* out, int64_t out_token_stride,
+                                   int64_t out_head_stride, const int32_t* block_tables,
+                                   int32_t block_table_stride, const int32_t* context_lens,
+                                   int32_t num_seqs, int32_t num_q_heads,
+                                   int32_t max_context_len, float scale, int32_t window,
+                                   const int32_t* packs, int32_t num_packs,
+                                   int32_t rows_per_pack, void* workspace,
+                                   size_t workspace_bytes, int32_t* err_flag, void* stream);
+
+/* Workspace bytes of astr_paged_attention_i8_shared (no reference counterpart: the
+ * pack plan is this library's). */
+size_t astr_paged_attention_i8_shared_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                                      int32_t num_kv_heads, int32_t head_dim,
+                                                      int32_t max_context_len,
+                                                      int32_t num_packs,
+                                                      int32_t rows_per_pack);
+
+/*
  * Bit-exact copy of whole blocks: block i of `num_blocks` goes from
  *   src + (src_index ? src_index[i] : i) * src_stride
  * to

@@ -38,12 +38,18 @@ def test_workspace_bytes():
     def partitioned(s, hq, d, parts):
         return a(s * hq * parts * d * 4) + a(s * hq * parts * 8)
 
-    def streamk(s, hq, hkv, d, max_ctx, cus=256):
+    def streamk(s, hq, hkv, d, max_ctx, cus=256, packs=0, rows=0):
+        # [block prefix over up to 512 work rows + 1, pack column per sequence]
+        # [acc][(m, l)] of 2 slots per wave of slot columns, then the packs' and
+        # packed sequences' own slots
         need = -(-(hkv * s * -(-max_ctx // 16)) // 64)
         cap = max(cus * 32, need)
         cap = -(-cap // 4) * 4
         g = hq // hkv
-        return a((s + 1) * 4) + a(cap * 2 * g * d * 4) + a(cap * 2 * g * 2 * 4)
+        cols = rows * g if packs else g
+        slots = cap * 2 * cols + (2 * hkv * packs * rows * g if packs else 0)
+        work_rows = 513
+        return a((work_rows + 1 + 3 * s) * 4) + a(slots * d * 4) + a(slots * 2 * 4)
 
     # fixed partitions (S, Hq, Hkv, D, max_ctx, partition_tokens)
     assert ws(64, 32, 8, 128, 512, 512) == 0
@@ -60,6 +66,14 @@ def test_workspace_bytes():
                                                partitioned(16, 64, 128, 64))
     # more than 512 sequences: partitioned only
     assert ws(600, 32, 8, 128, 4096, 0) == partitioned(600, 32, 128, 8)
+    # prefix packs (S, Hq, Hkv, D, max_ctx, num_packs, rows_per_pack)
+    shared = lib.astr_paged_attention_i8_shared_workspace_bytes
+    assert shared(256, 32, 8, 128, 2560, 64, 4) == max(
+        streamk(256, 32, 8, 128, 2560, packs=64, rows=4), partitioned(256, 32, 128, 5))
+    assert shared(256, 32, 8, 128, 2560, 0, 0) == ws(256, 32, 8, 128, 2560, 0)
+    assert shared(4, 8, 8, 256, 300, 2, 2) == max(
+        streamk(4, 8, 8, 256, 300, packs=2, rows=2), partitioned(4, 8, 256, 1))
+    assert shared(4, 8, 8, 64, 300, -1, 2) == 0 and shared(4, 8, 8, 64, 300, 1, 0) == 0
 
 
 def _desc(**kw):
@@ -163,3 +177,24 @@ def test_copy_blocks_rejects_bad_arguments_without_launching():
     assert copy(p, 16, None, 2, p, 16, None, 4, 16, 3, fp, None) == _native.ASTR_EINVAL
     assert copy(p, 16, None, 4, p, 16, None, 2, 16, 3, fp, None) == _native.ASTR_EINVAL
     assert "dst_blocks" in _native.last_error()
+
+
+def test_prefix_pack_argument_errors_need_no_device():
+    """astr_paged_attention_i8_shared checks its plan before any launch."""
+    d = _desc(num_kv_heads=2)
+
+    def shared(packs=16, num_packs=1, rows=2, window=0, hq=8):
+        return _native.lib().astr_paged_attention_i8_shared(
+            ctypes.byref(d), 16, 2, 128 * hq, 128, 16, 128 * hq, 128, 16, 4, 16, 1, hq, 64, 0.1,
+            window, packs, num_packs, rows, None, 0, 16, None)
+
+    assert shared(num_packs=-1) == _native.ASTR_EINVAL
+    assert shared(packs=None) == _native.ASTR_EINVAL
+    assert shared(packs=18) == _native.ASTR_EINVAL            # misaligned table
+    assert shared(rows=1) == _native.ASTR_EINVAL
+    assert shared(rows=5) == _native.ASTR_EINVAL              # 5 rows x G = 4 > 16 columns
+    assert "rows_per_pack" in _native.last_error()
+    assert shared(num_packs=129) == _native.ASTR_EUNSUPPORTED
+    assert shared(num_packs=100, rows=4) == _native.ASTR_EUNSUPPORTED  # 400 pack rows > 256
+    assert shared(window=8) == _native.ASTR_EUNSUPPORTED
+    assert "window" in _native.last_error()
