@@ -73,10 +73,16 @@ struct SkSplit {
   __device__ int64_t cost(int64_t b) const {
     return b < PB ? kPackCost * b : kPackCost * PB + kSeqCost * (b - PB);
   }
-  __device__ int64_t range_of(int64_t b) const { return cost(b) * Wr / T; }
+  // 32-bit quotients where the products fit (every launch up to ~2^31 / 10 / Wr
+  // blocks per head)
+  __device__ bool narrow() const { return T * (Wr + 1) < ((int64_t)1 << 31); }
+  __device__ int64_t range_of(int64_t b) const {
+    return narrow() ? (int64_t)((uint32_t)(cost(b) * Wr) / (uint32_t)T) : cost(b) * Wr / T;
+  }
   // first block of range r (first(Wr) == Bh)
   __device__ int64_t first(int64_t r) const {
-    const int64_t c = (T * r + Wr - 1) / Wr;
+    const int64_t c = narrow() ? (int64_t)((uint32_t)(T * r + Wr - 1) / (uint32_t)Wr)
+                               : (T * r + Wr - 1) / Wr;
     return c <= kPackCost * PB ? (c + kPackCost - 1) / kPackCost
                                : PB + (c - kPackCost * PB + kSeqCost - 1) / kSeqCost;
   }
@@ -264,14 +270,15 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   int ip = pack_blocks, is = lseq;
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) {
-    const int vp = __shfl_up(ip, off, kWave), vq = __shfl_up(is, off, kWave);
-    if (lane >= off) {
-      ip += vp;
-      is += vq;
+    const int vq = __shfl_up(is, off, kWave);
+    if constexpr (kPacks) {
+      const int vp = __shfl_up(ip, off, kWave);
+      if (lane >= off) ip += vp;
     }
+    if (lane >= off) is += vq;
   }
   if (lane == kWave - 1) {
-    s_wsum[wave] = ip;
+    if constexpr (kPacks) s_wsum[wave] = ip;
     s_wsum[NW + wave] = is;
   }
   __syncthreads();
@@ -279,14 +286,14 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     if (w < wave) {
-      bp += s_wsum[w];
+      if constexpr (kPacks) bp += s_wsum[w];
       bs += s_wsum[NW + w];
     }
-    pack_total += s_wsum[w];
+    if constexpr (kPacks) pack_total += s_wsum[w];
     bseq += s_wsum[NW + w];
   }
   bseq += pack_total;
-  if ((int)threadIdx.x < npk) s_cu[threadIdx.x] = bp + ip - pack_blocks;
+  if (kPacks && (int)threadIdx.x < npk) s_cu[threadIdx.x] = bp + ip - pack_blocks;
   int excl = pack_total + bs + is - lseq;
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
@@ -361,6 +368,10 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   const int row0 = __builtin_amdgcn_readfirstlane(rows);
   bool bad_index =
       too_long || __ballot(lane < n && (unsigned)ids >= (unsigned)a.cache.num_blocks) != 0;
+  // `ids` has landed (the test above read it); redefine it here so that the compiler's
+  // wait tracking stops treating it as a pending load inside the block loop (where it
+  // would add waits of its own; the loop's waits are the explicit ones below)
+  asm volatile("" : "+v"(ids));
   int nblk = bad_index ? 0 : n;
   int cw = 0;  // window of `ids` / `rows`; `ids_nx` / `rows_nx` hold window cw + 1
 
@@ -494,7 +505,15 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
             nblk = nx;  // stop after the blocks already issued
           }
         }
-        if (nx < nblk) issue(nx);
+        if (nx < nblk) {
+          // one block in flight per wave: every earlier block has landed before the next
+          // one is issued (the ring then holds landed blocks ahead of the MFMAs). With
+          // 2 048 resident waves streaming from HBM this measured best: 2 or 3 blocks in
+          // flight per wave took config 2 from 70.7 to 71.6 / 71.9 us and config 5 from
+          // 202 to 212 / 216 us (more outstanding 4 KiB gathers, less HBM throughput)
+          wait_vmcnt<0>();
+          issue(nx);
+        }
       }
       if (i == wend && i < nblk) {  // into the next window of the block list
         ids = ids_nx;
