@@ -234,10 +234,11 @@ struct ValuTile {
 
 // Heads of a GQA group one VALU workgroup serves: a lane keeps 16 query values and
 // 16 accumulators per head in registers, so large groups at D >= 128 are served
-// in passes of 4 heads (each pass re-reads the group's K/V) instead of spilling.
-// (FP8 codes convert with a few more live registers: passes of 4 heads from D = 64 up.)
+// in passes of 4 heads (each pass re-reads the group's K/V) instead of spilling, as
+// are groups of 16 at any D. (FP8 codes convert with a few more live registers: passes
+// of 4 heads from D = 64 up.)
 constexpr int valu_heads(int D, int group) {
-  return ((D >= 128 || KF != kInt8) && group > 4) ? 4 : group;
+  return (((D >= 128 || KF != kInt8) && group > 4) || group > 8) ? 4 : group;
 }
 
 // GROUP: the GQA group size; G: the heads of it this workgroup serves
@@ -519,8 +520,8 @@ int dispatch_group(const AttnArgs& a, int G, hipStream_t s) {
     case 2: return launch<QT, D, 2>(a, s);
     case 4: return launch<QT, D, 4>(a, s);
     case 8: return launch<QT, D, 8>(a, s);
-    case 16:
-      if constexpr (sizeof(QT) == 2 && D <= 128) return launch<QT, D, 16>(a, s);
+    case 16:  // fp32 queries: the VALU kernel's passes of 4 heads; f16/bf16 up to D = 128
+      if constexpr (sizeof(QT) == 4 || D <= 128) return launch<QT, D, 16>(a, s);
       [[fallthrough]];
     default:
       return fail(ASTR_EUNSUPPORTED, "GQA group size %d not supported for this query dtype", G);

@@ -50,16 +50,17 @@ __device__ __forceinline__ int row_seq(int x, int npk) { return x < npk ? -1 - x
 
 // The split of one kv head's Bh blocks (the PB blocks of the packs first) into Wr
 // contiguous ranges of equal cost: a pack block costs kPackCost, any other block
-// kSeqCost (pack blocks are shared by all rows of the call and mostly hit in cache,
-// while a sequence's own blocks stream from HBM). Block b starts at cost c(b); range r
-// owns the blocks whose start lies in [T r / Wr, T (r + 1) / Wr), T = c(Bh).
+// kSeqCost (pack blocks are shared by all rows of the call and hit in cache, so they
+// are bound by the waves' own work, while a sequence's own blocks stream from HBM;
+// 5:10 measured best on BASELINE config 4 among 4..7:10). Block b starts at cost c(b);
+// range r owns the blocks whose start lies in [T r / Wr, T (r + 1) / Wr), T = c(Bh).
 // Without packs every block costs the same. Wr: the resident waves per head (one
 // round, no tail), more only where that would put over kMaxBlocksPerWaveSK blocks on
 // a wave, never more than launched, and ranges no shorter than a block's cost (so
 // every range owns at least one block and a row split over ranges r0..r1 has exactly
 // one piece in each of them; the merge relies on it). The decode and the merge kernel
 // both derive the split from (Bh, PB) with this type.
-constexpr int kPackCost = 7, kSeqCost = 10;
+constexpr int kPackCost = 5, kSeqCost = 10;
 struct SkSplit {
   int64_t Bh, PB, T, Wr;
   __device__ SkSplit(const AttnArgs& a, int64_t bh, int64_t pb, int hkv)
@@ -511,7 +512,8 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
           // 2 048 resident waves streaming from HBM this measured best: 2 or 3 blocks in
           // flight per wave took config 2 from 70.7 to 71.6 / 71.9 us and config 5 from
           // 202 to 212 / 216 us (more outstanding 4 KiB gathers, less HBM throughput)
-          wait_vmcnt<0>();
+          if (kPacks && ps < 0) wait_vmcnt<(NS - 2) * S::kLoads>();  // pack blocks: cache hits
+          else wait_vmcnt<0>();
           issue(nx);
         }
       }

@@ -66,8 +66,6 @@ def test_scaled_configs_match_oracle(device, builder, rows, max_len, part):
 @pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("part", [0, 128])
 def test_head_dims_groups_dtypes(device, dim, hq, hkv, qdtype, part):
-    if hq // hkv == 16 and qdtype == torch.float32:
-        pytest.skip("fp32 queries run the VALU kernel, which takes GQA groups up to 8")
     lens = np.array([1, 15, 16, 17, 255, 256, 257, 600, 0, 33], np.int32)
     rng = np.random.default_rng(dim + hq)
     tables, pool = wl._tables_from_lengths(lens, rng, spare_blocks=3)
@@ -122,8 +120,6 @@ def test_fp8_kv_formats(device, fmt, dim, hq, hkv, qdtype, part):
     the codes enter the f16 MFMAs (or the fp32 VALU kernel) exactly, so the result
     matches the oracle's dequantize-then-attend within the same tolerance; with a
     window and key padding too."""
-    if hq // hkv == 16 and qdtype == torch.float32:
-        pytest.skip("fp32 queries run the VALU kernel, which takes GQA groups up to 8")
     lens = np.array([1, 15, 16, 17, 255, 256, 257, 600, 0, 33], np.int32)
     rng = np.random.default_rng(dim + hq)
     tables, pool = wl._tables_from_lengths(lens, rng, spare_blocks=3)

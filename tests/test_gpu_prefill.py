@@ -48,8 +48,6 @@ CTX = [2, 31 + 40, 300, 32 + 16, 33 + 5, 1, 65 + 200, 50, 129 + 333, 17, 7 + 100
                                         (256, 8, 2), (128, 128, 8)])
 @pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_mixed_rows_match_oracle(device, dim, hq, hkv, qdtype):
-    if hq // hkv == 16 and qdtype == torch.float32:
-        pytest.skip("fp32 decode rows run the exact VALU kernel, which takes GQA groups up to 8")
     w = _mixed(Q_LENS, CTX, hq=hq, hkv=hkv, dim=dim, qdtype=qdtype, seed=dim + hq)
     cache, tables, lens, qsl = _build(w, device)
     q = wl.queries(w, device)
@@ -90,8 +88,6 @@ def test_key_padding_in_chunks(device, dim, hq, hkv, window):
 def test_fp8_kv_formats_in_mixed_steps(device, fmt, dim, hq, hkv, qdtype):
     """FP8 arenas on the prefill kernel's f16 QK path (chunk rows) and the decode kernels
     (decode rows) of one mixed step, causal and windowed."""
-    if hq // hkv == 16 and qdtype == torch.float32:
-        pytest.skip("fp32 decode rows run the exact VALU kernel, which takes GQA groups up to 8")
     w = _mixed(Q_LENS, CTX, hq=hq, hkv=hkv, dim=dim, qdtype=qdtype, seed=dim + 1)
     cache, tables, lens, qsl = _build(w, device, fmt)
     q = wl.queries(w, device)
