@@ -662,9 +662,14 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   QueryColumn<QT, D> qraw[NT];
   const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
   int ids = 0;
+  // After each load the ids pass through an empty asm that redefines them: the one wait
+  // for their load happens there (once per 64 steps), and the compiler's wait tracking
+  // no longer treats them as a pending load at every issue below (where it would wait
+  // for every stage in flight, vmcnt(0), each step).
   auto load_ids = [&](int s0) __attribute__((always_inline)) {
     const int blk = b_lo + (s0 + lane) * kWaves + wave;
     ids = (s0 + lane < nsteps && blk < b_hi) ? bt[blk] : 0;
+    asm volatile("" : "+v"(ids));
   };
   if (nsteps > 0) load_ids(0);
 #pragma unroll
