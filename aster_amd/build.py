@@ -101,23 +101,31 @@ def _run(cmd, verbose):
         print(err, file=sys.stderr)
 
 
-def build(verbose=False, jobs=None):
-    """Compile every translation unit (in parallel) and link the shared library."""
-    obj_dir = os.path.join(OUT_DIR, "obj")
+TRACE_OUT = os.path.join(OUT_DIR, "trace", "libaster_kv.so")
+
+
+def build(verbose=False, jobs=None, trace=False):
+    """Compile every translation unit (in parallel) and link the shared library. With
+    ``trace`` the stream-K kernel records per-wave wall-clock marks (-DASTR_TRACE=1)
+    into a separate library, TRACE_OUT, for ``aster_amd.profiling timeline``."""
+    out = TRACE_OUT if trace else OUT
+    obj_dir = os.path.join(os.path.dirname(out), "obj")
     os.makedirs(obj_dir, exist_ok=True)
     plan = units()
     objs = [os.path.join(obj_dir, stem + ".o") for _, stem, _ in plan]
-    compiles = [[hipcc(), *FLAGS, *extra, RESOURCE_REMARKS, "-I", os.path.join(ROOT, "include"),
-                 "-c", os.path.join(CSRC, s), "-o", o] for (s, _, extra), o in zip(plan, objs)]
+    defs = ["-DASTR_TRACE=1"] if trace else []
+    compiles = [[hipcc(), *FLAGS, *extra, *defs, RESOURCE_REMARKS, "-I",
+                 os.path.join(ROOT, "include"), "-c", os.path.join(CSRC, s), "-o", o]
+                for (s, _, extra), o in zip(plan, objs)]
     jobs = jobs or min(len(compiles), os.cpu_count() or 1, 8)
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
         for f in [pool.submit(_run, c, verbose) for c in compiles]:
             f.result()
-    tmp = OUT + ".tmp"
+    tmp = out + ".tmp"
     _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose="--verbose" in sys.argv))
+    print(build(verbose="--verbose" in sys.argv, trace="--trace" in sys.argv))

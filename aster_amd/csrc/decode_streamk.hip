@@ -27,6 +27,23 @@ namespace {
 #endif
 constexpr int KF = ASTR_KF;  // this translation unit's code format
 
+// Per-wave timeline (trace builds only, -DASTR_TRACE=1, built apart from the product
+// library by `python -m aster_amd.build --trace`): wall-clock marks (100 MHz
+// s_memrealtime) of each wave of the last stream-K launch, read back with
+// astr_trace_read. Marks: 0 entry, 1 block prefix done, 2 block ids in hand, 3 first
+// block landed, 4 exit; of the wave's second piece: 5 end of the first piece's blocks,
+// 6 its query loaded and quantised, 7 its first block landed. Info: blocks, pieces,
+// pack blocks, XCC id.
+#ifndef ASTR_TRACE
+#define ASTR_TRACE 0
+#endif
+constexpr bool kTrace = ASTR_TRACE != 0;
+#if ASTR_TRACE
+constexpr int kTraceWaves = 16384;
+static __device__ long long g_trace[kTraceWaves][8];
+static __device__ int g_trace_info[kTraceWaves][4];
+#endif
+
 // Waves per workgroup and LDS stages per wave: 4-wave workgroups with a 4-block ring
 // per wave (2 waves per SIMD) measured best among 4/8/16-wave workgroups with 2 or 4
 // stages (all within 3 %); D = 256 stages are twice as large, so 8 waves x 2 stages.
@@ -157,6 +174,8 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   __shared__ int s_pblk[PACKS];               // shared blocks of pack k (0: no member left)
   __shared__ short s_plead[PACKS];            // first member of pack k: its table holds the blocks
 
+  long long tm[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // trace marks (kTrace)
+  if constexpr (kTrace) tm[0] = wall_clock64();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   const int r = lane & 15, qg = lane >> 4;
@@ -322,6 +341,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
       store_row_zero<QT>(a, s_tok[s], D);
   }
 
+  if constexpr (kTrace) tm[1] = wall_clock64();
   // ---- 3. this wave's head, block range and block ids / rows (lane j <-> block b0 + j);
   // waves from Wr * Hkv on have nothing to do
   const SkSplit split(a, bseq, npk > 0 ? s_cu[npk] : 0, hkv);
@@ -423,6 +443,8 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   QueryRaw<D> qr;
   QkOperand<D, KF> qop;
   float cf = 0.f;
+  if constexpr (kTrace) tm[2] = wall_clock64();
+  int pieces_seen = 0, pack_seen = 0;  // trace info
   if (nblk > 0) {
     const int x0 = row0 % nrow, kvh0 = row0 / nrow;
     const Column c0 = column(x0, kvh0);
@@ -453,6 +475,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   const bool masks = a.cache.key_valid != nullptr;
   int i = 0;
   while (i < nblk) {
+    if constexpr (kTrace) ++pieces_seen;
     const int crid = __builtin_amdgcn_readlane(rows, i & 63);  // this piece's row
     const int pstart = i;
     const int px = crid % nrow, pkvh = crid / nrow;
@@ -475,6 +498,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     if (i > 0) {  // a new row starts inside this wave's range
       load_query_at<QT, D>(col.q, qr);
       cf = qk_operand<QT, D, KF>(qr, col.valid, a.qk_scale_log2, qop, col.q);
+      if (kTrace && pieces_seen == 2) tm[6] = wall_clock64();
     }
 #pragma unroll
     for (int k = 0; k <= NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -492,6 +516,11 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
       const int iend = beyond ? 64 * cw + (int)__builtin_ctzll(beyond) : wend;
       for (; i < iend; ++i) {
         wait_block(i);
+        if constexpr (kTrace) {
+          if (i == 0) tm[3] = wall_clock64();
+          if (i == pstart && pieces_seen == 2) tm[7] = wall_clock64();
+          if (ps < 0) ++pack_seen;
+        }
         mfma_block<QT, D, KF>(stage(i), qop, cf, pos0 + (i - pstart) * kBlockTokens,
                               psp.kv_begin, psp.ctx, col.valid, r, qg, acc, m, l, vr, bad_score,
                               masks);
@@ -526,6 +555,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
       }
       break;
     }
+    if (kTrace && pieces_seen == 1) tm[5] = wall_clock64();
     // write the piece [pstart, i): the final output when a sequence row is whole in
     // this wave and merges with nothing, else a partial: in the row's own slot when
     // whole, in wave slot 0 (the piece starts the wave's range) or 1 (it ends it)
@@ -557,6 +587,16 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   }
   if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
   if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
+#if ASTR_TRACE
+  tm[4] = wall_clock64();
+  if (lane == 0 && gw < kTraceWaves) {
+    for (int k = 0; k < 8; ++k) g_trace[gw][k] = tm[k];
+    g_trace_info[gw][0] = nblk;
+    g_trace_info[gw][1] = pieces_seen;
+    g_trace_info[gw][2] = pack_seen;
+    g_trace_info[gw][3] = (int)__builtin_amdgcn_s_getreg((20 << 0) | (0 << 6) | (3 << 11));  // XCC_ID
+  }
+#endif
 }
 
 // The pieces of one work row of kv head kvh over the per-head order [fb, fe]: their
@@ -798,6 +838,16 @@ int launch_streamk_kf<KF>(const AttnArgs& a, int32_t q_dtype, hipStream_t stream
 
 #if ASTR_KF == 0
 int stream_k_max_seqs() { return kMaxSeqsSK; }
+#if ASTR_TRACE
+// Trace builds: copies the marks and info of the first `waves` waves of the last
+// stream-K launch of the int8 format (8 int64 + 4 int32 per wave) to host memory.
+extern "C" int astr_trace_read(void* marks, void* info, int waves) {
+  if (waves < 0 || waves > kTraceWaves) return ASTR_EINVAL;
+  hipError_t e = hipMemcpyFromSymbol(marks, HIP_SYMBOL(g_trace), (size_t)waves * 64);
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(info, HIP_SYMBOL(g_trace_info), (size_t)waves * 16);
+  return e == hipSuccess ? 0 : (int)e;
+}
+#endif
 int stream_k_max_packs() { return kMaxPacksSK; }
 int stream_k_max_pack_seqs() { return kMaxPackSeqsSK; }
 int stream_k_work_rows(int) { return kMaxRowsSK; }

@@ -12,6 +12,12 @@
       launches of one kernel, e.g. bench.py's prefill-only calls in a mixed step).
   python -m aster_amd.profiling durations <rocprof_dir> [kernel_substring]
       The same statistics of kernel durations (us) from ``*_kernel_trace.csv``.
+  python -m aster_amd.profiling timeline [config2|config4|config5] [--packs]
+      Per-wave timeline of the stream-K decode kernel on a BASELINE workload, from
+      the trace build (``python -m aster_amd.build --trace``, which records wall-clock
+      marks per wave): when waves start, have their block ids and first block, and
+      end, per XCC and by the number of pieces (rows) a wave streams, and what a row
+      start inside a wave costs. Runs a few calls and reads the last one.
 """
 
 from __future__ import annotations
@@ -74,6 +80,90 @@ def durations(root, pattern=""):
     return _stats(values)
 
 
+def timeline(config="config2", packs=False, calls=7):
+    """The trace build's per-wave marks of the last of ``calls`` attention calls over
+    ``config`` (four layer arenas, cycled), as a report dict (times in us from the
+    first wave's start)."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from . import _native, build
+    from . import workloads as wl
+    from .paged_kv import PagedKVCache
+    from .prefix_plan import plan_prefix_packs
+
+    _native.LIB_PATH = build.TRACE_OUT
+    _native._lib = None
+    lib = _native.lib()
+    lib.astr_trace_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+    w = getattr(wl, config)()
+    dev = torch.device("cuda:0")
+    # four layer arenas, cycled, so that a call does not find the previous call's K/V
+    # in the memory-side cache (as bench.py does)
+    layers = 4
+    cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=layers,
+                         num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, device=dev)
+    wl.materialize(w, cache, device=dev)
+    for layer in range(1, layers):
+        cache.codes[:, layer].copy_(cache.codes[:, 0])
+        cache.scales[:, layer].copy_(cache.scales[:, 0])
+    tables, lens = wl.device_tables(w, dev)
+    q = wl.queries(w, dev)
+    plan = (plan_prefix_packs(w.block_tables, w.context_lens, w.num_q_heads, w.num_kv_heads,
+                              device=dev) if packs else None)
+    for i in range(calls):
+        cache.paged_attention(i % layers, q, tables, lens, max_context_len=w.max_context_len,
+                              scale=w.scale, prefix_packs=plan)
+    torch.cuda.synchronize()
+    n = 16384
+    marks = np.zeros((n, 8), np.int64)
+    info = np.zeros((n, 4), np.int32)
+    rc = lib.astr_trace_read(marks.ctypes.data, info.ctypes.data, n)
+    if rc != 0:
+        raise RuntimeError(f"astr_trace_read failed ({rc})")
+    live = marks[:, 0] != 0
+    marks, info = marks[live], info[live]
+    t = (marks - marks[:, 0].min()) / 100.0  # s_memrealtime ticks at 100 MHz
+    nblk, pieces, packblk, xcc = info.T
+    pct = lambda x, p: [round(float(v), 2) for v in np.percentile(x, p)]
+    rep = {"config": config, "packs": bool(packs), "waves": int(live.sum()),
+           "span_us": round(float(t[:, 4].max()), 2),
+           "start_us": pct(t[:, 0], [0, 50, 100]),
+           "prefix_done_us": pct(t[:, 1] - t[:, 0], [50, 90]),
+           "ids_us": pct(t[:, 2] - t[:, 0], [50, 90]),
+           "first_block_us": pct(t[:, 3] - t[:, 0], [50, 90]),
+           "end_pct_10_50_90_99_100_us": pct(t[:, 4], [10, 50, 90, 99, 100]),
+           "blocks_per_wave": pct(nblk, [0, 50, 100])}
+    rep["per_xcc"] = {int(x): {"waves": int((xcc == x).sum()),
+                               "mean_start": round(float(t[xcc == x, 0].mean()), 2),
+                               "mean_end": round(float(t[xcc == x, 4].mean()), 2),
+                               "max_end": round(float(t[xcc == x, 4].max()), 2)}
+                      for x in np.unique(xcc)}
+    groups = {}
+    for k in sorted(np.unique(np.minimum(pieces, 3))):
+        m = np.minimum(pieces, 3) == k
+        groups[f"{k}{'+' if k == 3 else ''} pieces"] = {
+            "waves": int(m.sum()), "mean_end": round(float(t[m, 4].mean()), 2),
+            "p90_end": round(float(np.percentile(t[m, 4], 90)), 2),
+            "us_per_block": round(float(((t[m, 4] - t[m, 3]) / np.maximum(nblk[m], 1)).mean()), 3)}
+    rep["by_pieces"] = groups
+    two = pieces >= 2
+    if two.any():
+        rep["row_start_us"] = {
+            "end_of_first_piece_to_query_ready": pct(t[two, 6] - t[two, 5], [50, 90]),
+            "query_ready_to_first_block": pct(t[two, 7] - t[two, 6], [50, 90])}
+    if packs:
+        kind = np.where(packblk == nblk, "pack", np.where(packblk == 0, "sequence", "mixed"))
+        rep["by_kind"] = {k: {"waves": int((kind == k).sum()),
+                              "mean_end": round(float(t[kind == k, 4].mean()), 2),
+                              "us_per_block": round(float(((t[kind == k, 4] - t[kind == k, 3]) /
+                                                          np.maximum(nblk[kind == k], 1)).mean()), 3)}
+                          for k in np.unique(kind)}
+    return rep
+
+
 def main():
     p = argparse.ArgumentParser()
     sub = p.add_subparsers(dest="cmd", required=True)
@@ -83,9 +173,17 @@ def main():
         s = sub.add_parser(cmd)
         s.add_argument("root")
         s.add_argument("pattern", nargs="?", default="")
+    t = sub.add_parser("timeline")
+    t.add_argument("config", nargs="?", default="config2")
+    t.add_argument("--packs", action="store_true")
     args = p.parse_args()
     if args.cmd == "copy":
         copy(args.gib)
+        return
+    if args.cmd == "timeline":
+        import json
+
+        print(json.dumps(timeline(args.config, args.packs), indent=1))
         return
     table = (summarize if args.cmd == "summarize" else durations)(args.root, args.pattern)
     for (kernel, counter), (n, mean, median, top) in table.items():

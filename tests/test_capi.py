@@ -28,6 +28,8 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in declared_symbols():
         assert hasattr(lib, name), name
     assert lib.astr_version().decode().endswith("gfx950")
+    # the per-wave trace reader exists only in the separate trace build
+    assert not hasattr(lib, "astr_trace_read")
 
 
 def test_workspace_bytes():
