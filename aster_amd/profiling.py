@@ -18,6 +18,15 @@
       marks per wave): when waves start, have their block ids and first block, and
       end, per XCC and by the number of pieces (rows) a wave streams, and what a row
       start inside a wave costs. Runs a few calls and reads the last one.
+  python -m aster_amd.profiling traffic <fetch_dir> <write_dir> <cal_fetch_dir> <cal_write_dir> [kernel_substring]
+      HBM bytes per launch per kernel (median dispatch) from a FETCH_SIZE and a
+      WRITE_SIZE run, each scaled by what the counter reads for ``copy`` (the
+      ``cal_*`` runs): the figures of profiles/decode_traffic.json.
+  python -m aster_amd.profiling calls [config] [--packs] [--q-dtype T] [--calls N]
+      N paged_attention calls of a BASELINE decode workload (four layer arenas,
+      cycled), with the workload's queries cast to T: the program to run under
+      rocprofv3 for a kernel bench.py does not time (float32 queries run the exact
+      fp32 decode kernel).
 """
 
 from __future__ import annotations
@@ -80,28 +89,39 @@ def durations(root, pattern=""):
     return _stats(values)
 
 
-def timeline(config="config2", packs=False, calls=7):
-    """The trace build's per-wave marks of the last of ``calls`` attention calls over
-    ``config`` (four layer arenas, cycled), as a report dict (times in us from the
-    first wave's start)."""
-    import ctypes
+def traffic(fetch_dir, write_dir, cal_fetch_dir, cal_write_dir, pattern="astr", gib=1.0):
+    """HBM bytes per launch of each kernel matching ``pattern`` (median dispatch) from
+    a FETCH_SIZE run and a WRITE_SIZE run, each counter scaled by what it reads for
+    ``copy(gib)``: {"bytes_per_launch", "kernels", "calibration"}."""
+    known = gib * (1 << 30)
 
-    import numpy as np
+    def per_kernel(root, counter, pat):
+        return {k: med for (k, c), (_, _, med, _) in summarize(root, pat).items() if c == counter}
+
+    cal_f = max(per_kernel(cal_fetch_dir, "FETCH_SIZE", "").values())
+    cal_w = max(per_kernel(cal_write_dir, "WRITE_SIZE", "").values())
+    fs, ws = known / (cal_f * 1024), known / (cal_w * 1024)
+    fetch = per_kernel(fetch_dir, "FETCH_SIZE", pattern)
+    write = per_kernel(write_dir, "WRITE_SIZE", pattern)
+    kernels = {k.split("<")[0]: round(fetch[k] * 1024 * fs + write.get(k, 0.0) * 1024 * ws)
+               for k in fetch}
+    return {"bytes_per_launch": sum(kernels.values()), "kernels": kernels,
+            "calibration": {"fetch_scale": round(fs, 7), "write_scale": round(ws, 7)}}
+
+
+def _decode_calls(config, packs, q_dtype, calls):
+    """Run ``calls`` paged_attention calls of a BASELINE decode workload over four layer
+    arenas, cycled, so that a call does not find the previous call's K/V in the
+    memory-side cache (as bench.py does). ``q_dtype`` overrides the workload's query
+    type ("float32" routes to the exact fp32 kernel)."""
     import torch
 
-    from . import _native, build
     from . import workloads as wl
     from .paged_kv import PagedKVCache
     from .prefix_plan import plan_prefix_packs
 
-    _native.LIB_PATH = build.TRACE_OUT
-    _native._lib = None
-    lib = _native.lib()
-    lib.astr_trace_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
     w = getattr(wl, config)()
     dev = torch.device("cuda:0")
-    # four layer arenas, cycled, so that a call does not find the previous call's K/V
-    # in the memory-side cache (as bench.py does)
     layers = 4
     cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=layers,
                          num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, device=dev)
@@ -111,12 +131,35 @@ def timeline(config="config2", packs=False, calls=7):
         cache.scales[:, layer].copy_(cache.scales[:, 0])
     tables, lens = wl.device_tables(w, dev)
     q = wl.queries(w, dev)
+    if q_dtype:
+        q = q.to(getattr(torch, q_dtype))
     plan = (plan_prefix_packs(w.block_tables, w.context_lens, w.num_q_heads, w.num_kv_heads,
                               device=dev) if packs else None)
     for i in range(calls):
         cache.paged_attention(i % layers, q, tables, lens, max_context_len=w.max_context_len,
                               scale=w.scale, prefix_packs=plan)
     torch.cuda.synchronize()
+    print(f"{calls} calls of {config} (packs={bool(packs)}, queries {q.dtype})", flush=True)
+
+
+def timeline(config="config2", packs=False, calls=7):
+    """The trace build's per-wave marks of the last of ``calls`` attention calls over
+    ``config`` (four layer arenas, cycled), as a report dict (times in us from the
+    first wave's start)."""
+    import ctypes
+    import contextlib
+    import io
+
+    import numpy as np
+
+    from . import _native, build
+
+    _native.LIB_PATH = build.TRACE_OUT
+    _native._lib = None
+    lib = _native.lib()
+    lib.astr_trace_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+    with contextlib.redirect_stdout(io.StringIO()):
+        _decode_calls(config, packs, None, calls)
     n = 16384
     marks = np.zeros((n, 8), np.int64)
     info = np.zeros((n, 4), np.int32)
@@ -176,9 +219,27 @@ def main():
     t = sub.add_parser("timeline")
     t.add_argument("config", nargs="?", default="config2")
     t.add_argument("--packs", action="store_true")
+    d = sub.add_parser("calls")
+    d.add_argument("config", nargs="?", default="config2")
+    d.add_argument("--packs", action="store_true")
+    d.add_argument("--q-dtype", default=None, choices=["float32", "float16", "bfloat16"])
+    d.add_argument("--calls", type=int, default=50)
+    h = sub.add_parser("traffic")
+    for name in ("fetch_dir", "write_dir", "cal_fetch_dir", "cal_write_dir"):
+        h.add_argument(name)
+    h.add_argument("pattern", nargs="?", default="astr")
     args = p.parse_args()
     if args.cmd == "copy":
         copy(args.gib)
+        return
+    if args.cmd == "traffic":
+        import json
+
+        print(json.dumps(traffic(args.fetch_dir, args.write_dir, args.cal_fetch_dir,
+                                 args.cal_write_dir, args.pattern), indent=1))
+        return
+    if args.cmd == "calls":
+        _decode_calls(args.config, args.packs, args.q_dtype, args.calls)
         return
     if args.cmd == "timeline":
         import json
