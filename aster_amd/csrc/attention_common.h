@@ -17,6 +17,11 @@ constexpr int kWaves = 4;              // waves per workgroup
 constexpr int kMaxBlocksPerWave = 64;  // block ids one wave keeps in a register
 // stream-K: blocks one wave may stream (its block list goes in windows of 64)
 constexpr int kMaxBlocksPerWaveSK = 1024;
+// stream-K split costs: a block of a prefix pack, any other block, and the start of a
+// work row with blocks (its query load and the partial written when it ends). The
+// split gives every wave an equal share of the total; the host sizes the wave
+// capacity from the same figures.
+constexpr int kSkPackCost = 6, kSkSeqCost = 10, kSkRowCost = 27;
 constexpr float kRescaleSlack = 8.0f;  // p = exp2(s - m) <= 2^8 between rescales
 // PV weights p * v_scale are rounded to f16: with p <= 2^8 (kRescaleSlack) and every
 // v_scale <= kVWeightCap they stay below 2^15 (f16's largest finite value is 65504).
@@ -67,6 +72,7 @@ struct AttnArgs {
   float* ws_o;          // partial acc (layout depends on the split mode)
   float* ws_ml;         // partial (m, l)
   int32_t* ws_seq;      // stream-K: block prefix over its work rows [num_packs + num_seqs + 1]
+  int32_t* ws_ne;       // stream-K: work rows with blocks before each row [same]
   // stream-K prefix packs: num_packs records of 1 + pack_rows int32, [shared blocks,
   // member sequences (-1: empty)]; members read the pack's blocks in one MFMA tile,
   // query column p * G + g for member p, head g of the group (pack_rows * G <= 16)
@@ -74,7 +80,8 @@ struct AttnArgs {
   int32_t num_packs, pack_rows;
   int32_t slot_cols;    // stream-K: columns of one partial slot (G, or pack_rows * G)
   int32_t* ws_pack;     // stream-K: per sequence, [pack column k * pack_rows + p or -1,
-                        // the pack's first block, its end] (the per-head order)
+                        // the pack's first block, its end (the per-head order), the
+                        // rows with blocks before the pack]
   int32_t* err_flag;
 };
 
@@ -888,7 +895,7 @@ ASTR_BY_FORMAT(launch_prefill)
 
 // Largest batch the stream-K kernel takes (its per-sequence table lives in LDS), the
 // most prefix packs per launch and the largest batch that takes them, and the work
-// rows of its block prefix (ws_seq holds one more entry) for a head dim.
+// rows of its block prefix (ws_seq and ws_ne hold one more entry each) for a head dim.
 int stream_k_max_seqs();
 int stream_k_max_packs();
 int stream_k_max_pack_seqs();

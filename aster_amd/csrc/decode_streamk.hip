@@ -66,45 +66,85 @@ constexpr int kFastPieces = 16;   // merge: sequences in at most this many piece
 __device__ __forceinline__ int row_seq(int x, int npk) { return x < npk ? -1 - x : x - npk; }
 
 // The split of one kv head's Bh blocks (the PB blocks of the packs first) into Wr
-// contiguous ranges of equal cost: a pack block costs kPackCost, any other block
+// contiguous ranges of equal cost. A pack block costs kPackCost and any other block
 // kSeqCost (pack blocks are shared by all rows of the call and hit in cache, so they
-// are bound by the waves' own work, while a sequence's own blocks stream from HBM;
-// 5:10 measured best on BASELINE config 4 among 4..7:10). Block b starts at cost c(b);
-// range r owns the blocks whose start lies in [T r / Wr, T (r + 1) / Wr), T = c(Bh).
-// Without packs every block costs the same. Wr: the resident waves per head (one
-// round, no tail), more only where that would put over kMaxBlocksPerWaveSK blocks on
-// a wave, never more than launched, and ranges no shorter than a block's cost (so
-// every range owns at least one block and a row split over ranges r0..r1 has exactly
-// one piece in each of them; the merge relies on it). The decode and the merge kernel
-// both derive the split from (Bh, PB) with this type.
-constexpr int kPackCost = 5, kSeqCost = 10;
+// are bound by the waves' own work, while a sequence's own blocks stream from HBM),
+// and every work row with blocks costs kRowCost more, charged to its first block:
+// block b of a row with ne rows with blocks before it starts at cost
+// c(b) = wcost(b) + kRowCost (ne + 1), wcost(b) the block costs before b. Range r
+// owns the blocks whose start lies in [T r / Wr, T (r + 1) / Wr), T = wcost(Bh) +
+// kRowCost * (rows with blocks). The row costs were fitted to per-wave timelines of
+// BASELINE configs 2 and 4 (a row start measured ~3.4 us against ~1.27 us per
+// streamed block; pack blocks ~0.9 us). Wr: the resident waves per head (one round,
+// no tail), more where a range could otherwise hold over kMaxBlocksPerWaveSK
+// blocks, never more than launched, and ranges no shorter than a block's cost, so
+// that a row split over ranges r0..r1 has exactly one piece in each of them (the
+// merge relies on it; a range between two rows may own no block, its wave then
+// has nothing to do). The decode and the merge kernel both derive the split with
+// this type.
+constexpr int kPackCost = kSkPackCost, kSeqCost = kSkSeqCost, kRowCost = kSkRowCost;
 struct SkSplit {
-  int64_t Bh, PB, T, Wr;
-  __device__ SkSplit(const AttnArgs& a, int64_t bh, int64_t pb, int hkv)
-      : Bh(bh), PB(pb), T(kPackCost * pb + kSeqCost * (bh - pb)) {
-    int64_t w = (Bh + kMaxBlocksPerWaveSK - 1) / kMaxBlocksPerWaveSK;
+  int64_t PB, T, Wr;
+  __device__ SkSplit(const AttnArgs& a, int64_t bh, int64_t pb, int64_t rows_with_blocks,
+                     int hkv)
+      : PB(pb), T(kPackCost * pb + kSeqCost * (bh - pb) + kRowCost * rows_with_blocks) {
+    int64_t w = (T + kPackCost * kMaxBlocksPerWaveSK - 1) / (kPackCost * kMaxBlocksPerWaveSK);
     if (w < a.pref_waves / hkv) w = a.pref_waves / hkv;
     if (w > a.total_waves / hkv) w = a.total_waves / hkv;
     const int64_t most = T / kSeqCost > 1 ? T / kSeqCost : 1;
     Wr = w < most ? w : most;
   }
-  __device__ int64_t cost(int64_t b) const {
+  __device__ int64_t wcost(int64_t b) const {
     return b < PB ? kPackCost * b : kPackCost * PB + kSeqCost * (b - PB);
   }
-  // 32-bit quotients where the products fit (every launch up to ~2^31 / 10 / Wr
-  // blocks per head)
+  // start of block b of a row with `ne` rows with blocks before it
+  __device__ int64_t cost(int64_t b, int ne) const { return wcost(b) + kRowCost * (ne + 1); }
+  // 32-bit quotients where the products fit (every launch up to ~2^31 / Wr cost)
   __device__ bool narrow() const { return T * (Wr + 1) < ((int64_t)1 << 31); }
-  __device__ int64_t range_of(int64_t b) const {
-    return narrow() ? (int64_t)((uint32_t)(cost(b) * Wr) / (uint32_t)T) : cost(b) * Wr / T;
+  __device__ int64_t range_at(int64_t c) const {
+    return narrow() ? (int64_t)((uint32_t)(c * Wr) / (uint32_t)T) : c * Wr / T;
   }
-  // first block of range r (first(Wr) == Bh)
-  __device__ int64_t first(int64_t r) const {
-    const int64_t c = narrow() ? (int64_t)((uint32_t)(T * r + Wr - 1) / (uint32_t)Wr)
-                               : (T * r + Wr - 1) / Wr;
-    return c <= kPackCost * PB ? (c + kPackCost - 1) / kPackCost
-                               : PB + (c - kPackCost * PB + kSeqCost - 1) / kSeqCost;
+  __device__ int64_t range_of(int64_t b, int ne) const { return range_at(cost(b, ne)); }
+  // the least cost range r may start at: ceil(T r / Wr)
+  __device__ int64_t target(int64_t r) const {
+    return narrow() ? (int64_t)((uint32_t)(T * r + Wr - 1) / (uint32_t)Wr)
+                    : (T * r + Wr - 1) / Wr;
   }
 };
+
+// First block of ranges r and r + 1 (wave-uniform): the first block whose start
+// cost reaches the range's target. A lane-parallel search over the work rows' start
+// costs (monotone; a row without blocks shares the next row's): lane l tests rows
+// l * S (S = ceil(nrow / 64)), then the S rows after the last passing one, for both
+// targets at once (lanes 0-31 and 32-63 in the second round).
+__device__ __forceinline__ void range_bounds(const SkSplit& sp, int64_t r, const int* s_cu,
+                                            const short* s_ne, int nrow, int npk, int lane,
+                                            int64_t& b0, int64_t& b1) {
+  const int64_t c0 = sp.target(r), c1 = sp.target(r + 1);
+  auto start = [&](int x) __attribute__((always_inline)) -> int64_t {
+    return sp.cost(s_cu[x], s_ne[x]);
+  };
+  const int S = (nrow + kWave - 1) / kWave;
+  const int xa = lane * S;
+  const int64_t ca = xa < nrow ? start(xa) : INT64_MAX;
+  const int la = __popcll(__ballot(ca <= c0)) - 1, lb = __popcll(__ballot(ca <= c1)) - 1;
+  const int half = lane >> 5, j = lane & 31;
+  const int base = (half == 0 ? la : lb) * S;
+  const int xb = base + j;
+  const int64_t cb = base >= 0 && j < S && xb < nrow ? start(xb) : INT64_MAX;
+  const uint64_t pass = __ballot(cb <= (half == 0 ? c0 : c1));
+  const int x0 = la < 0 ? -1 : la * S + __popcll(pass & 0xffffffffull) - 1;
+  const int x1 = lb < 0 ? -1 : lb * S + __popcll(pass >> 32) - 1;
+  auto first_at = [&](int x, int64_t c) __attribute__((always_inline)) -> int64_t {
+    if (x < 0) return 0;  // before the first row's start
+    const int64_t w = x < npk ? kPackCost : kSeqCost;
+    const int64_t k = (c - start(x) + w - 1) / w;
+    const int64_t b = s_cu[x] + k;
+    return b < s_cu[x + 1] ? b : s_cu[x + 1];
+  };
+  b0 = first_at(x0, c0);
+  b1 = first_at(x1, c1);
+}
 
 // Work row owning block b of the per-head order (s_cu[x] <= b < s_cu[x + 1], the last
 // such x where empty rows share an offset); wave-uniform.
@@ -168,7 +208,8 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   __shared__ int s_ctx[SEQS];   // -1: not a decode row
   __shared__ int s_tok[SEQS];   // query/output token row
   __shared__ int s_cu[SEQS + PACKS + 1];
-  __shared__ int s_wsum[2 * NW];  // per wave: pack blocks, sequence blocks
+  __shared__ short s_ne[SEQS + PACKS + 1];  // work rows with blocks before row x
+  __shared__ int s_wsum[4 * NW];  // per wave: pack blocks, sequence blocks, and their rows
   __shared__ int s_pcol[kPacks ? SEQS : 1];  // pack column k * pack_rows + p of a member, else INT_MAX
   __shared__ short s_pmem[kPacks ? SEQS : 1];  // [k * pack_rows + p]: member sequence or -1
   __shared__ int s_pblk[PACKS];               // shared blocks of pack k (0: no member left)
@@ -283,54 +324,95 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   };
 
   // ---- 2. block prefix over work rows: the packs' blocks (pack t on thread t) and
-  // the sequences' blocks scanned side by side, the sequences placed after every pack
-  int lseq = 0;
+  // the sequences' blocks scanned side by side, the sequences placed after every
+  // pack; beside them the counts of rows with blocks (the split's row costs)
+  int lseq = 0, lrows = 0;
 #pragma unroll
-  for (int k = 0; k < SPT; ++k) lseq += nb[k];
-  int ip = pack_blocks, is = lseq;
+  for (int k = 0; k < SPT; ++k) {
+    lseq += nb[k];
+    lrows += nb[k] > 0;
+  }
+  int ip = pack_blocks, is = lseq, ipr = pack_blocks > 0, isr = lrows;
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) {
     const int vq = __shfl_up(is, off, kWave);
+    const int vqr = __shfl_up(isr, off, kWave);
     if constexpr (kPacks) {
       const int vp = __shfl_up(ip, off, kWave);
-      if (lane >= off) ip += vp;
+      const int vpr = __shfl_up(ipr, off, kWave);
+      if (lane >= off) {
+        ip += vp;
+        ipr += vpr;
+      }
     }
-    if (lane >= off) is += vq;
+    if (lane >= off) {
+      is += vq;
+      isr += vqr;
+    }
   }
   if (lane == kWave - 1) {
-    if constexpr (kPacks) s_wsum[wave] = ip;
+    if constexpr (kPacks) {
+      s_wsum[wave] = ip;
+      s_wsum[2 * NW + wave] = ipr;
+    }
     s_wsum[NW + wave] = is;
+    s_wsum[3 * NW + wave] = isr;
   }
   __syncthreads();
   int bp = 0, bs = 0, pack_total = 0, bseq = 0;
+  int rp = 0, rs = 0, pack_rows_total = 0, rows_total = 0;
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     if (w < wave) {
-      if constexpr (kPacks) bp += s_wsum[w];
+      if constexpr (kPacks) {
+        bp += s_wsum[w];
+        rp += s_wsum[2 * NW + w];
+      }
       bs += s_wsum[NW + w];
+      rs += s_wsum[3 * NW + w];
     }
-    if constexpr (kPacks) pack_total += s_wsum[w];
+    if constexpr (kPacks) {
+      pack_total += s_wsum[w];
+      pack_rows_total += s_wsum[2 * NW + w];
+    }
     bseq += s_wsum[NW + w];
+    rows_total += s_wsum[3 * NW + w];
   }
   bseq += pack_total;
-  if (kPacks && (int)threadIdx.x < npk) s_cu[threadIdx.x] = bp + ip - pack_blocks;
+  rows_total += pack_rows_total;
+  if (kPacks && (int)threadIdx.x < npk) {
+    s_cu[threadIdx.x] = bp + ip - pack_blocks;
+    s_ne[threadIdx.x] = (short)(rp + ipr - (pack_blocks > 0));
+  }
   int excl = pack_total + bs + is - lseq;
+  int rexcl = pack_rows_total + rs + isr - lrows;
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
     const int s = SPT * threadIdx.x + k;
-    if (s < nseq) s_cu[npk + s] = excl;
+    if (s < nseq) {
+      s_cu[npk + s] = excl;
+      s_ne[npk + s] = (short)rexcl;
+    }
     excl += nb[k];
+    rexcl += nb[k] > 0;
   }
-  if (threadIdx.x == 0) s_cu[nrow] = bseq;
+  if (threadIdx.x == 0) {
+    s_cu[nrow] = bseq;
+    s_ne[nrow] = (short)rows_total;
+  }
   __syncthreads();
   if (blockIdx.x == 0) {
-    for (int x = threadIdx.x; x <= nrow; x += blockDim.x) a.ws_seq[x] = s_cu[x];
+    for (int x = threadIdx.x; x <= nrow; x += blockDim.x) {
+      a.ws_seq[x] = s_cu[x];
+      a.ws_ne[x] = s_ne[x];
+    }
     if (npk > 0)
       for (int s = threadIdx.x; s < nseq; s += blockDim.x) {
         const int pc = pack_col(s);
-        a.ws_pack[3 * s] = pc;
-        a.ws_pack[3 * s + 1] = pc >= 0 ? s_cu[pc / P] : 0;
-        a.ws_pack[3 * s + 2] = pc >= 0 ? s_cu[pc / P + 1] : 0;
+        a.ws_pack[4 * s] = pc;
+        a.ws_pack[4 * s + 1] = pc >= 0 ? s_cu[pc / P] : 0;
+        a.ws_pack[4 * s + 2] = pc >= 0 ? s_cu[pc / P + 1] : 0;
+        a.ws_pack[4 * s + 3] = pc >= 0 ? s_ne[pc / P] : 0;
       }
     if (bad_plan) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
   }
@@ -344,15 +426,16 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
   if constexpr (kTrace) tm[1] = wall_clock64();
   // ---- 3. this wave's head, block range and block ids / rows (lane j <-> block b0 + j);
   // waves from Wr * Hkv on have nothing to do
-  const SkSplit split(a, bseq, npk > 0 ? s_cu[npk] : 0, hkv);
+  const SkSplit split(a, bseq, npk > 0 ? s_cu[npk] : 0, rows_total, hkv);
   const int64_t gw = (int64_t)blockIdx.x * NW + wave;
   const int kv = (int)(gw % hkv);
   const int64_t rg = gw / hkv;
   int64_t b0 = 0;
   int n = 0;
   if (rg < split.Wr) {
-    b0 = split.first(rg);
-    n = (int)(split.first(rg + 1) - b0);
+    int64_t b1;
+    range_bounds(split, rg, s_cu, s_ne, nrow, npk, lane, b0, b1);
+    n = (int)(b1 - b0);
   }
   const bool too_long = n > kMaxBlocksPerWaveSK;  // contexts beyond the declared maximum
   if (too_long) n = kMaxBlocksPerWaveSK;
@@ -610,14 +693,18 @@ struct RowPieces {
   int count;
   bool first_is_tail;
 };
-__device__ __forceinline__ RowPieces row_pieces(int64_t fb, int64_t fe, const SkSplit& sp,
+// ne: the rows with blocks before this one. Block fb - 1 ends the previous row with
+// blocks, which starts kRowCost + its own cost earlier than fb.
+__device__ __forceinline__ RowPieces row_pieces(int64_t fb, int64_t fe, int ne, const SkSplit& sp,
                                                 int64_t own) {
   RowPieces rp{0, own, 0, false};
   if (fe < fb) return rp;  // no blocks
-  rp.r0 = sp.range_of(fb);
-  const int64_t r1 = sp.range_of(fe);
+  const int64_t cf = sp.cost(fb, ne);
+  rp.r0 = sp.range_at(cf);
+  const int64_t r1 = sp.range_of(fe, ne);
   rp.count = (int)(r1 - rp.r0 + 1);
-  rp.first_is_tail = fb > 0 && sp.range_of(fb - 1) == rp.r0;
+  rp.first_is_tail =
+      fb > 0 && sp.range_at(cf - kRowCost - (fb - 1 < sp.PB ? kPackCost : kSeqCost)) == rp.r0;
   return rp;
 }
 __device__ __forceinline__ int64_t piece_slot(const AttnArgs& a, const RowPieces& rp, int p,
@@ -653,21 +740,23 @@ __global__ __launch_bounds__(kWave) void merge_streamk_kernel(AttnArgs a) {
   const int cu0 = a.ws_seq[xs], cu1 = a.ws_seq[xs + 1];
   const int bseq = a.ws_seq[a.num_packs + a.num_seqs];
   const int pb = a.ws_seq[a.num_packs];  // blocks of the packs
-  // a packed sequence: its pack column and the pack's block range, in one record
-  int pc = -1, pk0 = 0, pk1 = 0;
+  // a packed sequence: its pack column, the pack's block range and the rows with
+  // blocks before the pack, in one record
+  int pc = -1, pk0 = 0, pk1 = 0, pne = 0;
   if (a.num_packs > 0) {
-    pc = a.ws_pack[3 * seq];
-    pk0 = a.ws_pack[3 * seq + 1];
-    pk1 = a.ws_pack[3 * seq + 2];
+    pc = a.ws_pack[4 * seq];
+    pk0 = a.ws_pack[4 * seq + 1];
+    pk1 = a.ws_pack[4 * seq + 2];
+    pne = a.ws_pack[4 * seq + 3];
   }
-  const SkSplit split(a, bseq, pb, hkv);
-  RowPieces own = row_pieces(cu0, cu1 - 1, split, -1);
+  const SkSplit split(a, bseq, pb, a.ws_ne[a.num_packs + a.num_seqs], hkv);
+  RowPieces own = row_pieces(cu0, cu1 - 1, a.ws_ne[xs], split, -1);
   RowPieces pack{0, -1, 0, false};
   int pcol0 = 0;  // the pack column of this sequence's head 0
   if (pc >= 0) {
     const int k = pc / a.pack_rows;
     pcol0 = (pc % a.pack_rows) * G;
-    pack = row_pieces(pk0, pk1 - 1, split, pack_slot(a, G, kvh, k, pcol0));
+    pack = row_pieces(pk0, pk1 - 1, pne, split, pack_slot(a, G, kvh, k, pcol0));
     own.own = packed_seq_slot(a, G, hkv, kvh, pc, 0);
   } else if (own.count <= 1) {
     return;  // empty (zeroed) or written whole by one wave

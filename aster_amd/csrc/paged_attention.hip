@@ -57,14 +57,29 @@ int64_t max_total_blocks(int32_t num_seqs, int32_t num_kv_heads, int32_t max_con
   return per_row * num_seqs * num_kv_heads;
 }
 
+// Fewest stream-K waves that keep every wave at kMaxBlocksPerWaveSK blocks or less:
+// the split's ranges hold an equal share of the block and row costs, so a range of
+// pack blocks only (the cheapest) sets the bound. rows: work rows of one kv head.
+int64_t streamk_need_waves(int64_t total_blocks, int32_t num_kv_heads, int64_t rows) {
+  const int64_t per_head = (total_blocks + num_kv_heads - 1) / num_kv_heads;
+  const int64_t cost = kSkSeqCost * per_head + kSkRowCost * rows;
+  const int64_t unit = (int64_t)kSkPackCost * kMaxBlocksPerWaveSK;
+  return num_kv_heads * ((cost + unit - 1) / unit);
+}
+
 bool use_streamk(int32_t q_dtype, int32_t partition_tokens, int32_t num_seqs) {
   return partition_tokens == 0 && q_dtype != ASTR_F32 && num_seqs <= stream_k_max_seqs();
 }
 
 // Workspace layouts. Partitioned: [acc][(m,l)] per (seq, q head, partition).
-// Stream-K: [block prefix over work rows, per-sequence pack column][acc][(m,l)] per
-// column of the partial slots: (wave, 2 slots, slot columns) sized for every wave the
-// GPU can hold, then with prefix packs the packs' and packed sequences' own slots.
+// Stream-K: [block prefix over work rows, rows with blocks before each row,
+// per-sequence pack record][acc][(m,l)] per column of the partial slots: (wave, 2
+// slots, slot columns) sized for every wave the GPU can hold, then with prefix packs
+// the packs' and packed sequences' own slots.
+size_t seq_table_bytes(int32_t head_dim, int32_t num_seqs) {
+  return (2 * ((size_t)stream_k_work_rows(head_dim) + 1) + 4 * (size_t)num_seqs) *
+         sizeof(int32_t);
+}
 struct Layout {
   size_t seq_bytes, o_bytes, ml_bytes;
   int64_t waves;  // stream-K wave count of the launch (0 for partitioned)
@@ -86,8 +101,9 @@ Layout partitioned_layout(int32_t num_seqs, int32_t num_q_heads, int32_t head_di
 Layout streamk_layout(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                       int32_t head_dim, int32_t max_context_len, int32_t window,
                       int64_t max_waves, int32_t num_packs = 0, int32_t pack_rows = 0) {
-  const int64_t need = (max_total_blocks(num_seqs, num_kv_heads, max_context_len, window) +
-                        kMaxBlocksPerWaveSK - 1) / kMaxBlocksPerWaveSK;
+  const int64_t need =
+      streamk_need_waves(max_total_blocks(num_seqs, num_kv_heads, max_context_len, window),
+                         num_kv_heads, (int64_t)num_seqs + num_packs);
   int64_t cap = (int64_t)device_cus() * kMaxResidentWavesPerCU;
   if (max_waves > 0 && cap > max_waves) cap = max_waves / kWaves * kWaves;
   cap = cap > need ? cap : need;
@@ -97,8 +113,7 @@ Layout streamk_layout(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_head
   const int64_t row_cols = num_packs > 0 ? 2 * (int64_t)num_kv_heads * num_packs * pack_rows * group : 0;
   const size_t slots = (size_t)(cap * 2 * cols + row_cols);
   Layout w;
-  w.seq_bytes =
-      align256(((size_t)stream_k_work_rows(head_dim) + 1 + 3 * (size_t)num_seqs) * sizeof(int32_t));
+  w.seq_bytes = align256(seq_table_bytes(head_dim, num_seqs));
   w.o_bytes = align256(slots * head_dim * sizeof(float));
   w.ml_bytes = align256(slots * 2 * sizeof(float));
   w.waves = cap;
@@ -111,15 +126,13 @@ int64_t streamk_waves_in(size_t bytes, int32_t num_seqs, int32_t num_q_heads,
                          int32_t num_kv_heads, int32_t head_dim) {
   const size_t group = (size_t)(num_q_heads / num_kv_heads);
   const size_t per_wave = 2 * group * ((size_t)head_dim + 2) * sizeof(float);
-  const size_t fixed =
-      align256(((size_t)stream_k_work_rows(head_dim) + 1 + 3 * (size_t)num_seqs) * sizeof(int32_t)) +
-      2 * 256;
+  const size_t fixed = align256(seq_table_bytes(head_dim, num_seqs)) + 2 * 256;
   return bytes > fixed ? (int64_t)((bytes - fixed) / per_wave) : 0;
 }
 
-// Fewest waves that keep every wave at kMaxBlocksPerWaveSK blocks or less.
-int64_t streamk_min_waves(int64_t total_blocks) {
-  const int64_t need = (total_blocks + kMaxBlocksPerWaveSK - 1) / kMaxBlocksPerWaveSK;
+// streamk_need_waves in whole workgroups.
+int64_t streamk_min_waves(int64_t total_blocks, int32_t num_kv_heads, int64_t rows) {
+  const int64_t need = streamk_need_waves(total_blocks, num_kv_heads, rows);
   return (need + kWaves - 1) / kWaves * kWaves;
 }
 
@@ -307,7 +320,8 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
   a.max_parts = (int32_t)parts;
   a.total_waves = (int32_t)ws.waves;  // capacity; the stream-K launcher settles the count
   a.min_waves = (int32_t)streamk_min_waves(
-      max_total_blocks(num_seqs, cache->num_kv_heads, max_context_len, window));
+      max_total_blocks(num_seqs, cache->num_kv_heads, max_context_len, window),
+      cache->num_kv_heads, (int64_t)num_seqs + (num_packs > 0 ? num_packs : 0));
   a.packs = num_packs > 0 ? packs : nullptr;
   a.num_packs = num_packs;
   a.pack_rows = num_packs > 0 ? pack_rows : 1;
@@ -315,7 +329,10 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
   if (ws.total() > 0) {
     char* base = static_cast<char*>(workspace);
     a.ws_seq = reinterpret_cast<int32_t*>(base);
-    if (streamk) a.ws_pack = a.ws_seq + stream_k_work_rows(cache->head_dim) + 1;
+    if (streamk) {
+      a.ws_ne = a.ws_seq + stream_k_work_rows(cache->head_dim) + 1;
+      a.ws_pack = a.ws_ne + stream_k_work_rows(cache->head_dim) + 1;
+    }
     a.ws_o = reinterpret_cast<float*>(base + ws.seq_bytes);
     a.ws_ml = reinterpret_cast<float*>(base + ws.seq_bytes + ws.o_bytes);
   }

@@ -41,17 +41,20 @@ def test_workspace_bytes():
         return a(s * hq * parts * d * 4) + a(s * hq * parts * 8)
 
     def streamk(s, hq, hkv, d, max_ctx, cus=256, packs=0, rows=0):
-        # [block prefix over up to 512 work rows + 1, pack column per sequence]
-        # [acc][(m, l)] of 2 slots per wave of slot columns, then the packs' and
-        # packed sequences' own slots
-        need = -(-(hkv * s * -(-max_ctx // 16)) // 64)
+        # [block prefix over up to 512 work rows + 1, rows with blocks before each,
+        # 4-int pack record per sequence][acc][(m, l)] of 2 slots per wave of slot
+        # columns, then the packs' and packed sequences' own slots. Waves: at least
+        # enough that a range of the cheapest blocks (7 per block against 10, plus 27
+        # per work row) holds at most 1024 blocks.
+        per_head = s * -(-max_ctx // 16)
+        need = hkv * -(-(10 * per_head + 27 * (s + packs)) // (7 * 1024))
         cap = max(cus * 32, need)
         cap = -(-cap // 4) * 4
         g = hq // hkv
         cols = rows * g if packs else g
         slots = cap * 2 * cols + (2 * hkv * packs * rows * g if packs else 0)
         work_rows = 513
-        return a((work_rows + 1 + 3 * s) * 4) + a(slots * d * 4) + a(slots * 2 * 4)
+        return a((2 * (work_rows + 1) + 4 * s) * 4) + a(slots * d * 4) + a(slots * 2 * 4)
 
     # fixed partitions (S, Hq, Hkv, D, max_ctx, partition_tokens)
     assert ws(64, 32, 8, 128, 512, 512) == 0
