@@ -489,20 +489,36 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
   const bool edge = (use != (1u << NBK) - 1) | (bounded != 0) | unsafe | padded;
   if (edge) {
     asm volatile("");  // keeps this a branch: if-converted, the interior steps would pay for it
-    bool nonfinite = false;
+    // Per-score masks as all-ones/zero words in VGPRs (sign bits of differences, bit
+    // selects), not as compare results: lane masks from 32 unrolled compares per tile
+    // would stay live in SGPRs and push the loop's uniform values into spills.
+    uint32_t nonfinite = 0;
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+    for (int b = 0; b < NBK; ++b) {
+      // the padding bytes of this lane's four keys of block b (1 = real, 0 = padding)
+      const uint32_t pad = masks ? *reinterpret_cast<const uint32_t*>(cur + b * S::kBytes + S::kF +
+                                                                      4 * qg)
+                                 : 0x01010101u;
+      const bool used = (use >> b) & 1u, bnd = (bounded >> b) & 1u;  // wave-uniform
 #pragma unroll
-      for (int j = 0; j < 4 * NBK; ++j) {
-        const int b = j / 4;
-        const int key = kb0 + 16 * b + 4 * qg + j % 4;
-        const bool inside = (unsigned)(key - lo[t]) <= (unsigned)(hi[t] - lo[t]);  // lo <= key <= hi
-        const bool real = !masks || cur[b * S::kBytes + S::kF + 4 * qg + j % 4] != 0;  // not padding
-        const bool vis = ((use >> b) & 1u) && (!((bounded >> b) & 1u) || inside) && real;
-        nonfinite |= vis & !__builtin_isfinite(u[t][j] * cf[t]);
-        u[t][j] = vis ? u[t][j] : -INFINITY;
+      for (int k = 0; k < 4; ++k) {
+        const int j = 4 * b + k;
+        const int key = kb0 + 16 * b + 4 * qg + k;
+        const int32_t padding = (int32_t)(((pad >> (8 * k)) & 0xffu) - 1u) >> 31;  // -1: padding
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          // -1 when key < lo or key > hi (either difference negative), else 0
+          const int32_t outside = bnd ? ((key - lo[t]) | (hi[t] - key)) >> 31 : 0;
+          const uint32_t hide = used ? (uint32_t)(outside | padding) : 0xffffffffu;
+          const uint32_t ub = __builtin_bit_cast(uint32_t, u[t][j]);
+          const uint32_t xb = __builtin_bit_cast(uint32_t, u[t][j] * cf[t]);
+          // exponent field all ones (inf or NaN) -> bit 31 after the carry
+          nonfinite |= ((xb & 0x7f800000u) + 0x00800000u) & ~hide;
+          u[t][j] = __builtin_bit_cast(float, (ub & ~hide) | (0xff800000u & hide));  // -inf
+        }
       }
-    if (__ballot(nonfinite) != 0) bad_score = true;
+    }
+    if (__ballot((nonfinite >> 31) != 0) != 0) bad_score = true;
   }
   float tmax[NT];
   bool need = false;
