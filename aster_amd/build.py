@@ -102,6 +102,10 @@ def _run(cmd, verbose):
 
 
 TRACE_OUT = os.path.join(OUT_DIR, "trace", "libaster_kv.so")
+# roctx ranges of the C-ABI calls (rocprofiler-sdk's roctx, part of the ROCm image and
+# found at run time through the system library path, like the HIP runtime)
+ROCM_LIB = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
+LINK = [f"-L{ROCM_LIB}", "-lrocprofiler-sdk-roctx"]
 
 
 def build(verbose=False, jobs=None, trace=False):
@@ -122,7 +126,7 @@ def build(verbose=False, jobs=None, trace=False):
         for f in [pool.submit(_run, c, verbose) for c in compiles]:
             f.result()
     tmp = out + ".tmp"
-    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, *LINK, "-o", tmp], verbose)
     os.replace(tmp, out)
     return out
 

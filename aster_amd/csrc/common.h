@@ -15,6 +15,16 @@ constexpr float kLog2e = 1.4426950408889634f;
 int fail(int code, const char* fmt, ...);
 int hip_fail(hipError_t err, const char* what);
 
+// A roctx range over one C-ABI call on the host (argument checks and launches), named
+// after the entry point: `rocprofv3 --marker-trace` shows each call beside the
+// kernels it enqueued. Without a profiler attached the push and pop are no-ops.
+struct CallRange {
+  explicit CallRange(const char* name);
+  ~CallRange();
+  CallRange(const CallRange&) = delete;
+  CallRange& operator=(const CallRange&) = delete;
+};
+
 // ---- element conversion -----------------------------------------------------
 
 struct bf16_t {

@@ -1,4 +1,7 @@
-// Error reporting for the C ABI (thread-local last-error message).
+// Error reporting for the C ABI (thread-local last-error message) and the roctx
+// range of each call.
+#include <rocprofiler-sdk-roctx/roctx.h>
+
 #include <cstdarg>
 #include <cstdio>
 
@@ -20,6 +23,9 @@ int hip_fail(hipError_t err, const char* what) {
   snprintf(g_last_error, sizeof(g_last_error), "%s: %s", what, hipGetErrorString(err));
   return (int)err;
 }
+
+CallRange::CallRange(const char* name) { roctxRangePushA(name); }
+CallRange::~CallRange() { roctxRangePop(); }
 
 }  // namespace astr
 

@@ -66,6 +66,7 @@ extern "C" int astr_kv_copy_blocks(const void* src, int64_t src_stride, const in
                                    const int32_t* dst_index, int32_t dst_blocks,
                                    int64_t block_bytes, int32_t num_blocks, int32_t* err_flag,
                                    void* stream) {
+  astr::CallRange range("astr_kv_copy_blocks");
   using namespace astr;
   if (num_blocks < 0 || block_bytes < 0 || src_blocks < 0 || dst_blocks < 0)
     return fail(ASTR_EINVAL, "counts and sizes must be >= 0");

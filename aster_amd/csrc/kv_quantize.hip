@@ -249,6 +249,7 @@ __global__ __launch_bounds__(256) void write_key_valid_kernel(uint8_t* key_valid
 extern "C" int astr_kv_write_key_valid(const astr_paged_kv* cache, const int64_t* slot_mapping,
                                        const uint8_t* token_valid, int64_t num_tokens,
                                        int32_t* err_flag, void* stream) {
+  astr::CallRange range("astr_kv_write_key_valid");
   using namespace astr;
   if (cache == nullptr || err_flag == nullptr)
     return fail(ASTR_EINVAL, "cache descriptor and err_flag are required");
@@ -274,6 +275,7 @@ extern "C" int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void
                                           int64_t value_token_stride, int64_t value_head_stride,
                                           const int64_t* slot_mapping, int32_t* err_flag,
                                           void* stream) {
+  astr::CallRange range("astr_kv_quantize_append_i8");
   using namespace astr;
   if (cache == nullptr || err_flag == nullptr)
     return fail(ASTR_EINVAL, "cache descriptor and err_flag are required");

@@ -354,6 +354,7 @@ extern "C" int astr_paged_attention_i8(const astr_paged_kv* cache, const void* q
                                        int32_t max_context_len, float scale, int32_t window,
                                        int32_t partition_tokens, void* workspace,
                                        size_t workspace_bytes, int32_t* err_flag, void* stream) {
+  astr::CallRange range("astr_paged_attention_i8");
   return paged_attention(cache, query, q_dtype, q_token_stride, q_head_stride, out,
                          out_token_stride, out_head_stride, nullptr, num_seqs, 1, 1, block_tables,
                          block_table_stride, context_lens, num_seqs, num_q_heads, max_context_len,
@@ -369,6 +370,7 @@ extern "C" int astr_paged_attention_varlen_i8(
     const int32_t* context_lens, int32_t num_seqs, int32_t num_q_heads, int32_t max_context_len,
     float scale, int32_t window, int32_t partition_tokens, void* workspace, size_t workspace_bytes,
     int32_t* err_flag, void* stream) {
+  astr::CallRange range("astr_paged_attention_varlen_i8");
   if (query_start_loc == nullptr)
     return astr::fail(ASTR_EINVAL, "query_start_loc is required (int32 [num_seqs + 1])");
   return paged_attention(cache, query, q_dtype, q_token_stride, q_head_stride, out,
@@ -385,6 +387,7 @@ extern "C" int astr_paged_attention_i8_shared(
     int32_t num_seqs, int32_t num_q_heads, int32_t max_context_len, float scale, int32_t window,
     const int32_t* packs, int32_t num_packs, int32_t rows_per_pack, void* workspace,
     size_t workspace_bytes, int32_t* err_flag, void* stream) {
+  astr::CallRange range("astr_paged_attention_i8_shared");
   return paged_attention(cache, query, q_dtype, q_token_stride, q_head_stride, out,
                          out_token_stride, out_head_stride, nullptr, num_seqs, 1, 1, block_tables,
                          block_table_stride, context_lens, num_seqs, num_q_heads, max_context_len,
@@ -436,6 +439,7 @@ extern "C" int astr_paged_attention_i8_noalloc(
     const int32_t* block_tables, int32_t block_table_stride, const int32_t* context_lens,
     int32_t num_seqs, int32_t num_q_heads, int32_t max_context_len, float scale, int32_t window,
     int32_t partition_tokens, int32_t* err_flag, void* stream) {
+  astr::CallRange range("astr_paged_attention_i8_noalloc");
   if (num_seqs <= 0) return num_seqs == 0 ? 0 : astr::fail(ASTR_EINVAL, "num_seqs must be >= 0");
   void* ws = nullptr;
   const int rc = scratch_on_current_device(&ws);
