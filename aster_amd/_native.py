@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "astr_paged_attention_i8_workspace_bytes",
     "astr_paged_attention_i8_shared_workspace_bytes",
     "astr_kv_copy_blocks",
+    "astr_merge_softmax_f32",
     "astr_last_error",
     "astr_version",
 )
@@ -116,6 +117,8 @@ def lib():
             c_vp, c_i64, c_vp, c_i32, c_vp, c_i64, c_vp, c_i32, c_i64, c_i32, c_vp, c_vp,
         ]
         handle.astr_kv_copy_blocks.restype = ctypes.c_int
+        handle.astr_merge_softmax_f32.argtypes = [c_vp] * 9 + [c_i64, c_i32, c_vp]
+        handle.astr_merge_softmax_f32.restype = ctypes.c_int
         handle.astr_paged_attention_i8_workspace_bytes.argtypes = [c_i32] * 6
         handle.astr_paged_attention_i8_workspace_bytes.restype = c_sz
         handle.astr_paged_attention_i8_shared_workspace_bytes.argtypes = [c_i32] * 7

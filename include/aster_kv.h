@@ -291,6 +291,20 @@ int astr_kv_copy_blocks(const void* src, int64_t src_stride, const int32_t* src_
                         const int32_t* dst_index, int32_t dst_blocks, int64_t block_bytes,
                         int32_t num_blocks, int32_t* err_flag, void* stream);
 
+/*
+ * merge_softmax of two fp32 softmax states over disjoint key partitions of the same
+ * queries (src/aster/optimization/online_attention.py:42-63): maximum M = max(m_l, m_r)
+ * (NaN propagates), weights exp(m - M) for finite m and 0 otherwise (M replaced by 0
+ * when it is not finite), mass and weighted numerator summed under those weights.
+ *   *_max, *_mass: [rows] contiguous; *_weighted: [rows, width] contiguous, device
+ *   memory. The outputs may alias either input (elementwise).
+ */
+int astr_merge_softmax_f32(const float* left_max, const float* left_mass,
+                           const float* left_weighted, const float* right_max,
+                           const float* right_mass, const float* right_weighted,
+                           float* out_max, float* out_mass, float* out_weighted, int64_t rows,
+                           int32_t width, void* stream);
+
 /* Thread-local description of the last non-zero return code. */
 const char* astr_last_error(void);
 

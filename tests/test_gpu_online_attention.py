@@ -1,0 +1,147 @@
+"""The op-level API on the HIP kernels, against the oracle's restatement of
+online_attention / merge_softmax (online_attention.py:42-63, 74-219): explicit
+``AttentionBlock`` pages with gaps, offsets, key and query padding, causal and
+non-causal rows, windows, GQA, the three code formats and three query dtypes."""
+
+import numpy as np
+import pytest
+import torch
+
+import aster_amd
+from aster_amd import AttentionBlock, QuantizedKV, UnsupportedAttentionBackend
+from oracle import reference_cpu as ref
+from tests.gpu_util import assert_attention_close
+
+pytestmark = pytest.mark.gpu
+
+FP8_DTYPE = {"fp8_e4m3fn": torch.float8_e4m3fn, "fp8_e5m2": torch.float8_e5m2}
+
+
+def _pages(rng, batch, hkv, dim, spans, fmt, qdtype, device, pad_fraction=0.0):
+    """Blocks over the token spans [(offset, length), ...]: (device blocks, oracle blocks)."""
+    dev_blocks, ref_blocks = [], []
+    for offset, length in spans:
+        sides = []
+        for _ in range(2):
+            x = rng.standard_normal((batch, hkv, length, dim)).astype(np.float32)
+            q = ref.quantize_kv(x, fmt)
+            codes = torch.from_numpy(np.ascontiguousarray(q.values)).to(device)
+            if fmt != "int8":
+                codes = codes.view(FP8_DTYPE[fmt])
+            scales = torch.from_numpy(np.ascontiguousarray(q.scales)).to(device)
+            sides.append((QuantizedKV(codes, scales, qdtype), q))
+        padding = None
+        if pad_fraction:
+            padding = (rng.random((batch, length)) >= pad_fraction).astype(np.int32)
+        dev_blocks.append(AttentionBlock(sides[0][0], sides[1][0], offset,
+                                         None if padding is None else
+                                         torch.from_numpy(padding).to(device)))
+        ref_blocks.append(ref.AttentionBlock(sides[0][1], sides[1][1], offset, padding))
+    return dev_blocks, ref_blocks
+
+
+def _run(device, *, batch=2, hq=8, hkv=2, dim=128, queries=5, spans=((0, 20), (24, 33), (57, 7)),
+         fmt="int8", qdtype=torch.bfloat16, causal=True, window=None, pad_fraction=0.0,
+         query_pad=False, positions=None, seed=0):
+    rng = np.random.default_rng(seed)
+    dev_blocks, ref_blocks = _pages(rng, batch, hkv, dim, spans, fmt, qdtype, device, pad_fraction)
+    q32 = rng.standard_normal((batch, hq, queries, dim)).astype(np.float32)
+    query = torch.from_numpy(q32).to(device).to(qdtype)
+    last = max(o + n for o, n in spans)
+    if positions is None:
+        positions = np.stack([np.sort(rng.choice(last + 3, queries, replace=False))
+                              for _ in range(batch)])
+    positions = np.asarray(positions, np.int64)
+    qpad = (rng.random((batch, queries)) >= 0.3).astype(np.int32) if query_pad else None
+    kw = dict(causal=causal, window=window, scale=dim ** -0.5)
+    got = aster_amd.online_attention(
+        query, dev_blocks, query_positions=torch.from_numpy(positions).to(device),
+        query_padding=None if qpad is None else torch.from_numpy(qpad).to(device), **kw)
+    want = ref.online_attention(query.double().cpu().numpy(), ref_blocks, query_positions=positions,
+                                query_padding=qpad, **kw)
+    assert got.shape == query.shape and got.dtype == qdtype and got.is_contiguous()
+    assert_attention_close(got.float().cpu().numpy(), want)
+    return got
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8_e4m3fn", "fp8_e5m2"])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_formats_and_query_dtypes(device, fmt, qdtype):
+    _run(device, fmt=fmt, qdtype=qdtype)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dim", [64, 128, 256])
+def test_causality_and_head_dims(device, causal, dim):
+    _run(device, causal=causal, dim=dim, seed=dim)
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (16, 1)])
+def test_gqa_groups(device, hq, hkv):
+    _run(device, hq=hq, hkv=hkv, seed=hq)
+
+
+def test_window_key_and_query_padding(device):
+    _run(device, window=12, pad_fraction=0.25, query_pad=True, queries=9, seed=3)
+
+
+def test_gaps_offsets_and_queries_before_any_key(device):
+    # keys only at [40, 56) and [70, 100); queries at 0 and 10 see nothing (zero rows)
+    got = _run(device, spans=((40, 16), (70, 30)), positions=[[0, 10, 45, 69, 99]] * 2, seed=4)
+    assert torch.count_nonzero(got[:, :, :2]) == 0
+
+
+def test_many_rows_take_the_partitioned_path(device):
+    # 4 x 160 query tokens = 640 decode rows, beyond the stream-K kernel's 512
+    _run(device, batch=4, queries=160, spans=((0, 90), (100, 80)), seed=5)
+
+
+def test_work_counters_and_unsupported_cases(device):
+    rng = np.random.default_rng(6)
+    dev_blocks, _ = _pages(rng, 1, 2, 64, ((0, 16),), "int8", torch.bfloat16, device)
+    q = torch.randn(1, 4, 2, 64, device=device, dtype=torch.bfloat16)
+    pos = torch.tensor([[3, 15]], device=device)
+    work = aster_amd.AttentionWork()
+    aster_amd.online_attention(q, dev_blocks, query_positions=pos, work=work)
+    assert work.query_tiles == 2 and work.key_tiles == 2 * 2 and work.max_key_tile == 16
+    with pytest.raises(UnsupportedAttentionBackend):  # non-causal windows
+        aster_amd.online_attention(q, dev_blocks, query_positions=pos, causal=False, window=4)
+    plain = AttentionBlock(torch.randn(1, 2, 16, 64, device=device, dtype=torch.bfloat16),
+                           torch.randn(1, 2, 16, 64, device=device, dtype=torch.bfloat16), 0)
+    with pytest.raises(UnsupportedAttentionBackend):  # unquantized pages
+        aster_amd.online_attention(q, [plain], query_positions=pos)
+    # a finite query whose scores exceed fp32 raises the reference's overflow error
+    f32_blocks, _ = _pages(rng, 1, 2, 64, ((0, 16),), "int8", torch.float32, device)
+    huge = torch.full((1, 4, 2, 64), 3e38, device=device)
+    with pytest.raises(ValueError, match="overflow"):
+        aster_amd.online_attention(huge, f32_blocks, query_positions=pos, scale=1.0)
+
+
+def _state(rng, shape, width, device, kinds=()):
+    m = rng.standard_normal(shape).astype(np.float32) * 4
+    for index, value in kinds:
+        m[index] = value
+    l = rng.random(shape).astype(np.float32) + 0.5
+    n = rng.standard_normal(shape + (width,)).astype(np.float32)
+    dev = aster_amd.SoftmaxState(*(torch.from_numpy(a).to(device) for a in (m, l, n)))
+    return dev, ref.SoftmaxState(m, l, n)
+
+
+@pytest.mark.parametrize("width", [128, 6])
+def test_merge_softmax(device, width):
+    rng = np.random.default_rng(width)
+    shape = (2, 3, 4, 5)
+    specials_left = [((0, 0, 0, 0), -np.inf), ((0, 0, 0, 1), -np.inf), ((1, 2, 3, 4), np.nan)]
+    specials_right = [((0, 0, 0, 0), -np.inf), ((0, 0, 0, 2), np.inf)]
+    left, left_ref = _state(rng, shape, width, device, specials_left)
+    right, right_ref = _state(rng, shape, width, device, specials_right)
+    got = aster_amd.merge_softmax(left, right)
+    want = ref.merge_softmax(left_ref, right_ref)
+    for g, w in ((got.maximum, want.maximum), (got.mass, want.mass), (got.weighted, want.weighted)):
+        np.testing.assert_allclose(g.cpu().numpy(), w, rtol=2e-6, atol=1e-6, equal_nan=True)
+    # the merged state normalises to the attention output, as the reference's does
+    np.testing.assert_allclose(got.output().cpu().numpy(), want.output(), rtol=2e-6, atol=1e-6,
+                               equal_nan=True)
+    with pytest.raises(ValueError, match="same queries"):
+        bad, _ = _state(rng, (2, 3, 4, 6), width, device)
+        aster_amd.merge_softmax(left, bad)
