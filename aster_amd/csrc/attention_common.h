@@ -33,8 +33,10 @@ constexpr float kVWeightCap = 128.0f;
 // (m, l, acc) partials. A block whose (weight-scaled) V scales exceed vlim =
 // kVWeightCap * 2^koff grows koff by the exponent they need, through the same
 // rescale of l and acc as a new score maximum. Every piece starts at {0, kVWeightCap}.
+// `screen` is the lane's limit for the one staged scale it tests per block, so that a
+// single compare and ballot per block finds the rare blocks (vrange_start).
 struct VRange {
-  float koff, vlim;
+  float koff, vlim, screen;
 };
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -623,6 +625,23 @@ __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, f
   }
 }
 
+// Screening of the rare blocks in mfma_block: lanes of odd token group qg test the
+// staged V scale of token r against vlim (before the weight scale, a power of two, so
+// the test is exact); lanes of even qg test the K scale of token r against the
+// column's third-term threshold (none for FP8 codes). Together they cover every scale
+// of the block; a block with any scale above its limit takes the full tests.
+template <int D, int KF>
+__device__ __forceinline__ float screen_limit(const QkOperand<D, KF>& qop, float vlim, int qg) {
+  if (qg & 1) return vlim * (1.f / v_weight_scale<KF>());
+  if constexpr (KF == kInt8) return qop.ks_fine;
+  else return INFINITY;
+}
+// A piece's starting VRange for the column operand qop (built before it).
+template <int D, int KF>
+__device__ __forceinline__ VRange vrange_start(const QkOperand<D, KF>& qop, int qg) {
+  return VRange{0.f, kVWeightCap, screen_limit<D, KF>(qop, kVWeightCap, qg)};
+}
+
 // ---- one staged 16-token block through the MFMAs
 //   S^T[t][g] = K[t][:] . Q[g][:]     INT8 codes: 2 (D/64) x 2 v_mfma_i32_16x16x64_i8
 //                                     (hi, then lo on the hi result shifted by 7);
@@ -648,10 +667,15 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
   constexpr int NPV = D / 16;
   // V scales, times 2^8 for FP8 codes (E4M3FN operands carry 2^-8; E5M2 weights carry
   // 2^8, as does the normaliser of this format); finite, and the same on the 16 lanes
-  // of a token group. Beyond vr.vlim they grow the running maximum's offset first: its
-  // own rescale of l and acc, before any score of the block exists.
+  // of a token group
   const float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg) * v_weight_scale<KF>();
-  {
+  const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
+  // the one staged scale this lane screens against vr.screen (screen_limit)
+  const float screened = *reinterpret_cast<const float*>(st + S::kS + 64 * (qg & 1) + 4 * r);
+  // rare blocks, found by the screen: V scales beyond vr.vlim grow the running
+  // maximum's offset, with its own rescale of l and acc, before the block's weights
+  // are formed
+  auto grow_vrange = [&]() __attribute__((always_inline)) {
     const float vsm = fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3]));
     if (__ballot(vsm > vr.vlim) != 0) {
       float wm = fmaxf(vsm, shfl_xor(vsm, 16));
@@ -660,14 +684,56 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
       frexpf(wm / vr.vlim, &x);  // in [2^(x-1), 2^x), x >= 1
       vr.koff += (float)x;
       vr.vlim = ldexpf(vr.vlim, x);
+      vr.screen = screen_limit<D, KF>(qop, vr.vlim, qg);
       const float alpha = ldexpf(1.f, -x);  // m + x is the new maximum (with offset)
       m += (float)x;
       l *= alpha;
 #pragma unroll
       for (int n = 0; n <= NPV; ++n) acc[n] *= alpha;
     }
+  };
+  // ... and large scores take the third query term, K.lo2 / 128 (exact int32, then
+  // scaled by a power of two), wherever a block's K scales reach the column's
+  // threshold; the term is rebuilt from the query elements at the column's
+  // quantization, so that it completes the hi and lo terms
+  auto third_term = [&](float4_t& sc4) __attribute__((always_inline)) {
+    if constexpr (KF == kInt8) {
+      const float kmx = fmaxf(fmaxf(ks[0], ks[1]), fmaxf(ks[2], ks[3]));
+      if (__ballot(kmx > qop.ks_fine) != 0) {
+        int4_t sf = {0, 0, 0, 0};
+#pragma nounroll
+        for (int h = 0; h < KCH; ++h) {
+          const int4_t kh = *reinterpret_cast<const int4_t*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
+          constexpr int kVec = 16 / (int)sizeof(QT);
+          uint4 w[16 / kVec];
+#pragma unroll
+          for (int c = 0; c < 16 / kVec; ++c)
+            w[c] = reinterpret_cast<const uint4*>(static_cast<const QT*>(qop.qptr) + 64 * h)[c];
+          const QT* e = reinterpret_cast<const QT*>(w);
+          int4_t q2;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            uint32_t fb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              fb[i] = __builtin_bit_cast(
+                  uint32_t, query_terms<3>(to_float<QT>(e[4 * k + i]) * qop.lift, qop.inv).lo2);
+            q2[k] = (int)low_bytes(fb);
+          }
+          sf = __builtin_amdgcn_mfma_i32_16x16x64_i8(kh, q2, sf, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc4[j] = __builtin_fmaf((float)sf[j], 1.f / 128.f, sc4[j]);
+      }
+    }
+  };
+  // Up to D = 128 the screen follows the QK MFMAs, off their path; at D = 256 the V
+  // range goes first, which keeps the registers of the PV accumulators free of the
+  // scores while it rescales them
+  constexpr bool kScreenLate = D <= 128;
+  if constexpr (!kScreenLate) {
+    if (__ballot(screened > vr.screen) != 0) grow_vrange();
   }
-  const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
   float4_t s4;
   if constexpr (KF == kInt8) {
     // exact int32 K.Q = 128 (K.hi) + K.lo straight from the staged codes
@@ -682,37 +748,10 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
 #pragma unroll
     for (int h = 0; h < KCH; ++h) si = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop.lo[h], si, 0, 0, 0);
     s4 = float4_t{(float)si[0], (float)si[1], (float)si[2], (float)si[3]};
-    // large scores: add the third query term, K.lo2 / 128 (exact int32, then scaled
-    // by a power of two), wherever a block's K scales reach the column's threshold; the
-    // term is rebuilt from the query elements at the column's quantization, so that it
-    // completes the hi and lo terms used above (a rare path: nothing of it stays live)
-    const float kmx = fmaxf(fmaxf(ks[0], ks[1]), fmaxf(ks[2], ks[3]));
-    if (__ballot(kmx > qop.ks_fine) != 0) {
-      int4_t sf = {0, 0, 0, 0};
-#pragma nounroll
-      for (int h = 0; h < KCH; ++h) {
-        const int4_t kh = *reinterpret_cast<const int4_t*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
-        constexpr int kVec = 16 / (int)sizeof(QT);
-        uint4 w[16 / kVec];
-#pragma unroll
-        for (int c = 0; c < 16 / kVec; ++c)
-          w[c] = reinterpret_cast<const uint4*>(static_cast<const QT*>(qop.qptr) + 64 * h)[c];
-        const QT* e = reinterpret_cast<const QT*>(w);
-        int4_t q2;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          uint32_t fb[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            fb[i] = __builtin_bit_cast(
-                uint32_t, query_terms<3>(to_float<QT>(e[4 * k + i]) * qop.lift, qop.inv).lo2);
-          q2[k] = (int)low_bytes(fb);
-        }
-        sf = __builtin_amdgcn_mfma_i32_16x16x64_i8(kh, q2, sf, 0, 0, 0);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s4[j] = __builtin_fmaf((float)sf[j], 1.f / 128.f, s4[j]);
-    }
+    // keeps these conversions of MFMA results ahead of the branches below: sunk into
+    // their blocks, they were issued without the wait states an MFMA result needs
+    // (wrong scores at D = 64)
+    asm volatile("" : "+v"(s4[0]), "+v"(s4[1]), "+v"(s4[2]), "+v"(s4[3]));
   } else {
     s4 = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -727,6 +766,14 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
         s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop.op[2 * h + sub], s4, 0, 0, 0);
       }
     }
+  }
+  if constexpr (kScreenLate) {
+    if (__ballot(screened > vr.screen) != 0) {  // one compare and ballot per block
+      grow_vrange();
+      third_term(s4);
+    }
+  } else {
+    third_term(s4);
   }
   uint32_t vw[4][VB / 4];
 #pragma unroll

@@ -174,7 +174,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   // all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
   float m = gvalid ? -FLT_MAX : 0.f;
   float l = 0.f;
-  VRange vr = {0.f, kVWeightCap};
+  VRange vr = vrange_start<D, KF>(qop, qg);
   bool bad_score = false;
 
   auto step = [&](int i, char* st) __attribute__((always_inline)) {

@@ -589,7 +589,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     // are all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
     m = col.valid ? -FLT_MAX : 0.f;
     l = 0.f;
-    VRange vr = {0.f, kVWeightCap};
+    VRange vr = vrange_start<D, KF>(qop, qg);
     const int pos0 = (pblk0 + (int)(b0 + i - pfb)) * kBlockTokens;
     for (;;) {
       // the row's blocks in the current window: up to the first lane with another row
