@@ -734,6 +734,30 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
   if constexpr (!kScreenLate) {
     if (__ballot(screened > vr.screen) != 0) grow_vrange();
   }
+  // V code words of the PV operands. Up to D = 128 they are read with the K codes, so
+  // that their LDS latency passes under the QK MFMAs; at D = 256 they would stay live
+  // in too many registers, and are read after the QK MFMAs.
+  uint32_t vw[4][VB / 4];
+  auto read_v_words = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const char* rowp = st + S::kV + (4 * qg + j) * D + r * VB;
+      if constexpr (VB == 4) {
+        vw[j][0] = *reinterpret_cast<const uint32_t*>(rowp);
+      } else if constexpr (VB == 8) {
+        const uint2 w = *reinterpret_cast<const uint2*>(rowp);
+        vw[j][0] = w.x;
+        vw[j][1] = w.y;
+      } else {
+        const uint4 w = *reinterpret_cast<const uint4*>(rowp);
+        vw[j][0] = w.x;
+        vw[j][1] = w.y;
+        vw[j][2] = w.z;
+        vw[j][3] = w.w;
+      }
+    }
+  };
+  if constexpr (kScreenLate) read_v_words();
   float4_t s4;
   if constexpr (KF == kInt8) {
     // exact int32 K.Q = 128 (K.hi) + K.lo straight from the staged codes
@@ -768,30 +792,14 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
     }
   }
   if constexpr (kScreenLate) {
-    if (__ballot(screened > vr.screen) != 0) {  // one compare and ballot per block
+    // one compare and ballot per block; the rare paths are laid out away from the loop
+    if (__builtin_expect(__ballot(screened > vr.screen) != 0, 0)) {
       grow_vrange();
       third_term(s4);
     }
   } else {
     third_term(s4);
-  }
-  uint32_t vw[4][VB / 4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const char* rowp = st + S::kV + (4 * qg + j) * D + r * VB;
-    if constexpr (VB == 4) {
-      vw[j][0] = *reinterpret_cast<const uint32_t*>(rowp);
-    } else if constexpr (VB == 8) {
-      const uint2 w = *reinterpret_cast<const uint2*>(rowp);
-      vw[j][0] = w.x;
-      vw[j][1] = w.y;
-    } else {
-      const uint4 w = *reinterpret_cast<const uint4*>(rowp);
-      vw[j][0] = w.x;
-      vw[j][1] = w.y;
-      vw[j][2] = w.z;
-      vw[j][3] = w.w;
-    }
+    read_v_words();
   }
   // scores of tokens 4*qg + j for head g = r (base 2, dequantised)
   const int tok0 = tok_base + 4 * qg;
@@ -823,8 +831,8 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
     nonfinite = gvalid && !(__builtin_isfinite(hi) && __builtin_isfinite(lo));
     need = gvalid && hi > m + kRescaleSlack;
   }
-  if (__ballot(nonfinite) != 0) bad_score = true;
-  if (__ballot(need) != 0) {
+  if (__builtin_expect(__ballot(nonfinite) != 0, 0)) bad_score = true;
+  if (__builtin_expect(__ballot(need) != 0, 0)) {
     float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
     tmax = fmaxf(tmax, shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, shfl_xor(tmax, 32));
