@@ -78,6 +78,9 @@ def merge_softmax(left, right):
     tensors = (left.maximum, left.mass, left.weighted, right.maximum, right.mass, right.weighted)
     if any(t.device.type != "cuda" for t in tensors):
         raise UnsupportedAttentionBackend("hip_int8_paged merges device states")
+    if any(t.device != left.maximum.device for t in tensors):
+        raise ValueError(
+            "Attention partitions must describe the same queries and accumulator layout")
     if any(t.dtype != torch.float32 for t in tensors):
         raise UnsupportedAttentionBackend("hip_int8_paged merges fp32 softmax states")
     if (left.mass.shape != left.maximum.shape or right.mass.shape != right.maximum.shape
