@@ -85,11 +85,13 @@ def test_large_v_scales_in_chunk_rows(device, fmt, part, k):
 
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("part", [0, 128])
-def test_mixed_v_scale_ranges_within_rows(device, fmt, part):
+@pytest.mark.parametrize("dim", [64, 128, 256])
+def test_mixed_v_scale_ranges_within_rows(device, fmt, part, dim):
     """Every third block's V scales times 2^12, the others unchanged: pieces and query
     tiles meet blocks of both ranges (the weight factor or the block exponent changes
-    mid-row), in decode and chunk rows of one step."""
-    w = _workload(MIXED_Q, MIXED_CTX, seed=90)
+    mid-row), in decode and chunk rows of one step. Every head size: the decode blocks
+    screen their scales after the QK MFMAs up to D = 128 and before them at D = 256."""
+    w = _workload(MIXED_Q, MIXED_CTX, hq=16, hkv=4, dim=dim, seed=90 + dim)
     cache, tables, lens = _build(w, device, fmt)
     cache.scales[::3, 0, 1] *= 2.0 ** 12
     q = wl.queries(w, device)
@@ -142,7 +144,7 @@ def _fp32_score_sensitivity(w, cache, query, exact):
 
 
 @pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("dim", [64, 128, 256])
 @pytest.mark.parametrize("part", [0, 512])
 def test_extreme_finite_scores(device, qdtype, dim, part):
     """q x 100 and k x 100 (test_inference_online_attention.py:79-98): scores of
