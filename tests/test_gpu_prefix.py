@@ -88,6 +88,31 @@ def test_packs_with_padding_keys_and_large_v_scales(device, fmt):
     assert_attention_close(out, oracle_decode(w, cache, q), atol=2e-3 * 2.0 ** 13)
 
 
+@pytest.mark.parametrize("dim", [64, 128, 256])
+def test_packs_with_extreme_finite_scores(device, dim):
+    """q x 100 and the shared blocks' K x 100 (test_inference_online_attention.py:79-98):
+    pack blocks, whose 16 query columns come from several rows, screen and take the
+    third query term per column; held to the float64 oracle within the tolerance plus
+    the kernels' stated score precision, as in test_gpu_hardening."""
+    from tests.test_gpu_hardening import _fp32_score_sensitivity
+
+    w = _shared_workload(16, 4, dim, torch.bfloat16, seed=40 + dim)
+    plan = _plan(w, device)
+    assert plan is not None and plan.num_packs >= 2
+    cache, tables, lens = _build(w, device)
+    shared = np.concatenate([w.block_tables[0, :12], w.block_tables[9, :7]]).astype(np.int64)
+    cache.scales[torch.from_numpy(shared).to(device), 0, 0] *= 100.0
+    q = (wl.queries(w, device).float() * 100.0).to(torch.bfloat16)
+    out = cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                                scale=w.scale, prefix_packs=plan, check=True)
+    assert torch.isfinite(out).all()
+    exact = oracle_decode(w, cache, q, fp64=True)
+    extra = _fp32_score_sensitivity(w, cache, q, exact)
+    err = np.abs(out.double().cpu().numpy() - exact)
+    bound = 2e-3 + 1e-2 * np.abs(exact) + extra
+    assert (err <= bound).all(), (float((err - bound).max()), int((err > bound).sum()))
+
+
 def test_plans_that_contradict_the_call_are_flagged(device):
     """A member listed twice, a member that sees fewer keys than the shared blocks and
     a member index past the batch raise the index flag; those members are served as
