@@ -283,24 +283,7 @@ __device__ __forceinline__ int convert_v(const char* st, int lane, int half, uin
   const int r = lane & 15, qg = lane >> 4;
   const float4_t vsf = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg);
   constexpr float cs = v_weight_scale<KF>();
-  half4_t vsh;
-  int e = ve;
-  const float vsm = fmaxf(fmaxf(vsf[0], vsf[1]), fmaxf(vsf[2], vsf[3]));
-  if (__ballot(vsm > vlim) != 0 || ve != 0) {
-    if (__ballot(vsm > vlim) != 0) {
-      float wm = fmaxf(vsm, shfl_xor(vsm, 16));
-      wm = fmaxf(wm, shfl_xor(wm, 32));
-      int x;
-      frexpf(wm * (format_max<KF>() / 32768.f), &x);  // wm * M / 2^15 in [2^(x-1), 2^x)
-      e = max(ve, __builtin_amdgcn_readfirstlane(x));
-    }
-    const float c = ldexpf(cs, -e);
-    vsh = half4_t{(_Float16)(vsf[0] * c), (_Float16)(vsf[1] * c), (_Float16)(vsf[2] * c),
-                  (_Float16)(vsf[3] * c)};
-  } else {
-    vsh = half4_t{(_Float16)(vsf[0] * cs), (_Float16)(vsf[1] * cs), (_Float16)(vsf[2] * cs),
-                  (_Float16)(vsf[3] * cs)};
-  }
+  // the V code words go out with the scales, so that both LDS latencies overlap
   uint32_t vw[4][VB / 4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -318,6 +301,24 @@ __device__ __forceinline__ int convert_v(const char* st, int lane, int half, uin
       vw[j][2] = w.z;
       vw[j][3] = w.w;
     }
+  }
+  half4_t vsh;
+  int e = ve;
+  const float vsm = fmaxf(fmaxf(vsf[0], vsf[1]), fmaxf(vsf[2], vsf[3]));
+  if (__ballot(vsm > vlim) != 0 || ve != 0) {
+    if (__ballot(vsm > vlim) != 0) {
+      float wm = fmaxf(vsm, shfl_xor(vsm, 16));
+      wm = fmaxf(wm, shfl_xor(wm, 32));
+      int x;
+      frexpf(wm * (format_max<KF>() / 32768.f), &x);  // wm * M / 2^15 in [2^(x-1), 2^x)
+      e = max(ve, __builtin_amdgcn_readfirstlane(x));
+    }
+    const float c = ldexpf(cs, -e);
+    vsh = half4_t{(_Float16)(vsf[0] * c), (_Float16)(vsf[1] * c), (_Float16)(vsf[2] * c),
+                  (_Float16)(vsf[3] * c)};
+  } else {
+    vsh = half4_t{(_Float16)(vsf[0] * cs), (_Float16)(vsf[1] * cs), (_Float16)(vsf[2] * cs),
+                  (_Float16)(vsf[3] * cs)};
   }
 #pragma unroll
   for (int n = 0; n < VB; ++n) {
