@@ -714,27 +714,35 @@ __device__ __forceinline__ int64_t piece_slot(const AttnArgs& a, const RowPieces
   return rp.count == 1 ? rp.own : split;
 }
 
-// One wave per (sequence, kv head): merge the pieces of sequences that no single
-// wave wrote: rows split across waves, and packed sequences (their pack's pieces,
-// columns p G .. p G + G-1 for member p, then their own). The G heads' rows of one
-// piece sit in consecutive slot columns (G x D contiguous floats), so lane L takes
-// elements [L E, L E + E) of them (E = G D / 64), of head hl = L E / D. Statistics go
-// lane-parallel: in a round of R = min(64 / G, kFast) pieces, lane u G + h holds
-// (m, l) of piece u, head h, and the maxima and weight sums reduce over the lanes of
-// one head. The merge_softmax rule (online_attention.py:42-63) and
-// SoftmaxState.output (:35-39).
-template <typename QT, int D, int G>
+// Heads of a GQA group that one merge wave takes: at most 4, so that a wave holds the
+// partials of up to kFastPieces pieces at once (groups of 8 and 16 split over 2 and 4
+// waves).
+template <int G>
+constexpr int merge_heads() { return G < 4 ? G : 4; }
+
+// One wave per (sequence, kv head, GS heads of the group): merge the pieces of
+// sequences that no single wave wrote: rows split across waves, and packed sequences
+// (their pack's pieces, columns p G .. p G + G-1 for member p, then their own). The
+// heads' rows of one piece sit in consecutive slot columns (G x D contiguous floats);
+// the wave takes heads h0 .. h0 + GS-1, lane L elements [L E, L E + E) of them
+// (E = GS D / 64), of head h0 + hl, hl = L E / D. Statistics go lane-parallel: in a
+// round of R = min(64 / GS, kFast) pieces, lane u GS + h holds (m, l) of piece u, head
+// h0 + h, and the maxima and weight sums reduce over the lanes of one head. The
+// merge_softmax rule (online_attention.py:42-63) and SoftmaxState.output (:35-39).
+template <typename QT, int D, int G, int GS>
 __global__ __launch_bounds__(kWave) void merge_streamk_kernel(AttnArgs a) {
-  constexpr int E = G * D / kWave;  // floats per lane
-  static_assert(E >= 1 && G * D % kWave == 0, "lanes cover the group's rows");
+  constexpr int E = GS * D / kWave;  // floats per lane
+  static_assert(G % GS == 0 && E >= 1 && GS * D % kWave == 0, "lanes cover the heads' rows");
+  constexpr int HS = G / GS;  // waves per (sequence, kv head)
   constexpr int V = E >= 4 ? 4 : E;  // floats per load
   constexpr int kRegs = 128 / E > 0 ? 128 / E : 1;  // partial rows held at once
-  constexpr int R0 = kWave / G < kFastPieces ? kWave / G : kFastPieces;
+  constexpr int R0 = kWave / GS < kFastPieces ? kWave / GS : kFastPieces;
   constexpr int R = R0 < kRegs ? R0 : kRegs;  // pieces per round
   typedef float vec_t __attribute__((ext_vector_type(V)));
   const int lane = threadIdx.x;
   const int hkv = a.cache.num_kv_heads;
-  const int seq = blockIdx.x / hkv, kvh = blockIdx.x % hkv;
+  const int seq = blockIdx.x / (hkv * HS), kvh = blockIdx.x / HS % hkv;
+  const int h0 = blockIdx.x % HS * GS;  // first head of the group this wave takes
   const int hl = lane * E / D;
   const int xs = a.num_packs + seq;
   const int cu0 = a.ws_seq[xs], cu1 = a.ws_seq[xs + 1];
@@ -768,15 +776,15 @@ __global__ __launch_bounds__(kWave) void merge_streamk_kernel(AttnArgs a) {
     const RowPieces& rp = in_pack ? pack : own;
     return piece_slot(a, rp, in_pack ? p : p - pack.count, hkv, kvh, in_pack ? pcol0 : 0);
   };
-  const int su = lane / G, sh = lane % G;  // the (piece in round, head) of this lane's statistics
+  const int su = lane / GS, sh = lane % GS;  // the (piece in round, head) of this lane's statistics
   auto head_max = [&](float x) __attribute__((always_inline)) -> float {
 #pragma unroll
-    for (int off = G; off < kWave; off <<= 1) x = fmaxf(x, shfl_xor(x, off));
+    for (int off = GS; off < kWave; off <<= 1) x = fmaxf(x, shfl_xor(x, off));
     return x;
   };
   auto head_sum = [&](float x) __attribute__((always_inline)) -> float {
 #pragma unroll
-    for (int off = G; off < kWave; off <<= 1) x += shfl_xor(x, off);
+    for (int off = GS; off < kWave; off <<= 1) x += shfl_xor(x, off);
     return x;
   };
   // one round: pieces [p0, p0 + R); returns this lane's slot and loads its statistics
@@ -784,8 +792,8 @@ __global__ __launch_bounds__(kWave) void merge_streamk_kernel(AttnArgs a) {
     const int p = p0 + su;
     const bool live = su < R && p < pieces;
     sl = slot_of(live ? p : p0);
-    mp = live ? a.ws_ml[(sl + sh) * 2] : -INFINITY;
-    lp = live ? a.ws_ml[(sl + sh) * 2 + 1] : 0.f;
+    mp = live ? a.ws_ml[(sl + h0 + sh) * 2] : -INFINITY;
+    lp = live ? a.ws_ml[(sl + h0 + sh) * 2 + 1] : 0.f;
   };
   float M = -INFINITY;  // of head sh (lane-parallel layout)
   if (pieces > R) {     // several rounds: the maxima first
@@ -806,9 +814,9 @@ __global__ __launch_bounds__(kWave) void merge_streamk_kernel(AttnArgs a) {
     float v[R][E];
 #pragma unroll
     for (int u = 0; u < R; ++u) {
-      const int64_t s_u = ((int64_t)__builtin_amdgcn_readlane((int)(sl >> 32), u * G) << 32) |
-                          (uint32_t)__builtin_amdgcn_readlane((int)sl, u * G);
-      const float* src = a.ws_o + s_u * D + lane * E;
+      const int64_t s_u = ((int64_t)__builtin_amdgcn_readlane((int)(sl >> 32), u * GS) << 32) |
+                          (uint32_t)__builtin_amdgcn_readlane((int)sl, u * GS);
+      const float* src = a.ws_o + (s_u + h0) * D + lane * E;
       const bool live = p0 + u < pieces;
 #pragma unroll
       for (int e = 0; e < E; e += V) {
@@ -822,14 +830,14 @@ __global__ __launch_bounds__(kWave) void merge_streamk_kernel(AttnArgs a) {
     L += head_sum(lp * w);
 #pragma unroll
     for (int u = 0; u < R; ++u) {
-      const float wu = __shfl(w, u * G + hl, kWave);
+      const float wu = __shfl(w, u * GS + hl, kWave);
 #pragma unroll
       for (int e = 0; e < E; ++e) O[e] = fmaf(v[u][e], wu, O[e]);
     }
   }
   const float inv_l = 1.f / fmaxf(__shfl(L, hl, kWave), FLT_MIN);
   QT* out = static_cast<QT*>(a.out) + (int64_t)decode_token(a, seq) * a.o_tok +
-            (int64_t)(kvh * G + hl) * a.o_head + lane * E % D;
+            (int64_t)(kvh * G + h0 + hl) * a.o_head + lane * E % D;
   QT r[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) r[e] = from_float<QT>(O[e] * inv_l);
@@ -882,8 +890,9 @@ int launch(AttnArgs a, hipStream_t stream) {
   a.pref_waves = (int32_t)(resident < waves ? resident : waves);
   const int wgs = (int)(waves / NW);
   hipLaunchKernelGGL(kernel, dim3(wgs), dim3(NW * kWave), 0, stream, a);
-  hipLaunchKernelGGL((merge_streamk_kernel<QT, D, G>), dim3(a.num_seqs * a.cache.num_kv_heads),
-                     dim3(kWave), 0, stream, a);
+  constexpr int GS = merge_heads<G>();
+  hipLaunchKernelGGL((merge_streamk_kernel<QT, D, G, GS>),
+                     dim3(a.num_seqs * a.cache.num_kv_heads * (G / GS)), dim3(kWave), 0, stream, a);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "paged_attention (stream-K) launch");
 }
