@@ -599,7 +599,7 @@ struct QkOperand<D, kInt8> {
 // before the third term is added. The worst case aligns every code at 127 with every
 // rounding; the typical error is ~sqrt(12 D) max|k| / rms|k| / 2 (about 50 at D = 128)
 // times smaller, a few 1e-3 of a softmax weight at most. (At 1/32, K rows with x8
-// outliers, as in BASELINE config 5, took the third term on most blocks.)
+// outliers, as in the config5 workload, took the third term on most blocks.)
 constexpr float kFineScoreError = 1.f / 8.f;
 
 // Builds the operand of query row r (lane layout of QueryRaw; rows r >= G are zero)

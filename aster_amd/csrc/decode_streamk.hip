@@ -74,7 +74,7 @@ __device__ __forceinline__ int row_seq(int x, int npk) { return x < npk ? -1 - x
 // c(b) = wcost(b) + kRowCost (ne + 1), wcost(b) the block costs before b. Range r
 // owns the blocks whose start lies in [T r / Wr, T (r + 1) / Wr), T = wcost(Bh) +
 // kRowCost * (rows with blocks). The row costs were fitted to per-wave timelines of
-// BASELINE configs 2 and 4 (a row start measured ~3.4 us against ~1.27 us per
+// the config2 and config4 workloads (a row start measured ~3.4 us against ~1.27 us per
 // streamed block; pack blocks ~0.9 us). Wr: the resident waves per head (one round,
 // no tail), more where a range could otherwise hold over kMaxBlocksPerWaveSK
 // blocks, never more than launched, and ranges no shorter than a block's cost, so

@@ -1,4 +1,4 @@
-"""INT8 paged decode benchmark (BASELINE config 2 on one MI355X).
+"""INT8 paged decode benchmark (the config2 workload on one MI355X).
 
 A step is one decode-attention layer invocation of the hot path over the batch:
 quantize-and-append of the 64 new bf16 K/V tokens (one per sequence) via

@@ -4,7 +4,7 @@
 Fixtures are data only: seeded inputs and the outputs of the pinned numpy oracle
 (oracle/reference_cpu.py; see tests/test_oracle.py for what pins it).
 
-  config1.npz        BASELINE config 1 (tiny ragged INT8 paged decode): fp32
+  config1.npz        the config1 workload (tiny ragged INT8 paged decode): fp32
                      queries and K/V sources, block tables, context lengths, the
                      quantized arena (codes + scales) and the fp32 attention
                      output of the reference's page-by-page online softmax.

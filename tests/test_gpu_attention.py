@@ -174,7 +174,7 @@ def test_empty_rows_are_zero_and_ctx_one_returns_value(device):
 
 
 def test_full_config2_split_invariance_and_permutation(device):
-    """Full BASELINE config 2: split-K partition size does not change the result
+    """The full config2 workload: split-K partition size does not change the result
     beyond tolerance, and relabelling physical blocks (permuting the arena and the
     block tables together) gives bit-identical output."""
     w = wl.config2()

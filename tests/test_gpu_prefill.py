@@ -199,7 +199,7 @@ def test_chunk_last_token_equals_decode_kernel(device):
 
 
 def test_full_config3_step(device):
-    """Full BASELINE config 3: quantize-append the step's 4216 tokens, then one
+    """The full config3 workload: quantize-append the step's 4216 tokens, then one
     mixed launch; oracle on two chunks and four decode rows, and every output row
     finite with |o| bounded by max|v| (a convex combination of dequantized values)."""
     w = wl.config3()

@@ -4,7 +4,7 @@ state.py:599-625) read them once per pack of 16 // G rows. Every output is held 
 the oracle's row-by-row attention (online_attention.py:74-219 via
 paged_attention.py:168-215) at the north_star tolerance, and to the kernels without
 the plan; a plan that contradicts the call is flagged and its bad members fall back
-to ordinary rows. Includes BASELINE config 4 at full size (256 rows)."""
+to ordinary rows. Includes the config4 workload at full size (256 rows)."""
 
 import numpy as np
 import pytest
@@ -155,7 +155,7 @@ def test_python_arguments(device):
 
 
 def test_full_config4(device):
-    """BASELINE config 4 at full size: 256 rows aliasing one 128-block prefix. The plan
+    """The config4 workload at full size: 256 rows aliasing one 128-block prefix. The plan
     packs all 256 rows; stream-K with packs agrees with fixed 512-token partitions over
     every row and with the oracle on sampled rows."""
     w = wl.config4()

@@ -130,7 +130,7 @@ def test_append_edge_rows_bit_exact(device, dtype, dim, fmt):
 
 
 def test_config2_step_append_bit_exact(device):
-    """BASELINE config 2's step: 64 new bf16 tokens (one per sequence) appended via
+    """The config2 workload's step: 64 new bf16 tokens (one per sequence) appended via
     slot_mapping into a shuffled pool, with strided (non-contiguous) K/V rows."""
     w = wl.config2()
     cache = _cache(device, w.num_blocks, w.num_kv_heads, w.head_dim)
