@@ -27,12 +27,26 @@ PER_FORMAT = ("decode_partition.hip", "decode_streamk.hip", "prefill.hip")
 FORMATS = (0, 1, 2)
 
 
-def units():
+# The stream-K source builds as two units per format (decode_streamk.hip, ASTR_SK_PART):
+# the launches with prefix packs and the entry point, and the launches without packs
+# under the max-ilp scheduler (measured: config 2 69.8 -> 69.4 us, config 4 without a
+# plan 154.6 -> 151.8 us; the pack launches, 74.9 -> 76.9 us under it, and the head-dim
+# 256 launches, which spill to scratch under it, keep the default scheduler). Trace
+# builds keep it as one unit.
+STREAMK_PLAIN_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
+
+
+def units(trace=False):
     """(source, object stem, extra flags) of every translation unit."""
     out = []
     for s in SOURCES:
         stem = os.path.splitext(s)[0]
-        if s in PER_FORMAT:
+        if s == "decode_streamk.hip" and not trace:
+            for k in FORMATS:
+                out.append((s, f"{stem}_kf{k}", [f"-DASTR_KF={k}", "-DASTR_SK_PART=1"]))
+                out.append((s, f"{stem}_plain_kf{k}",
+                            [f"-DASTR_KF={k}", "-DASTR_SK_PART=2", *STREAMK_PLAIN_FLAGS]))
+        elif s in PER_FORMAT:
             out += [(s, f"{stem}_kf{k}", [f"-DASTR_KF={k}"]) for k in FORMATS]
         else:
             out.append((s, stem, []))
@@ -115,7 +129,7 @@ def build(verbose=False, jobs=None, trace=False):
     out = TRACE_OUT if trace else OUT
     obj_dir = os.path.join(os.path.dirname(out), "obj")
     os.makedirs(obj_dir, exist_ok=True)
-    plan = units()
+    plan = units(trace)
     objs = [os.path.join(obj_dir, stem + ".o") for _, stem, _ in plan]
     defs = ["-DASTR_TRACE=1"] if trace else []
     compiles = [[hipcc(), *FLAGS, *extra, *defs, RESOURCE_REMARKS, "-I",

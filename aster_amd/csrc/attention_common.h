@@ -923,12 +923,17 @@ __device__ __forceinline__ void end_piece(float4_t (&acc)[D / 16 + 1], int r) {
 // with -DASTR_KF=KF), dispatched on query dtype, head dim and GQA group inside.
 template <int KF> int launch_partitioned_kf(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
 template <int KF> int launch_streamk_kf(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
+// the stream-K launches without prefix packs (a unit of their own; launch_streamk_kf
+// routes to it)
+template <int KF>
+int launch_streamk_plain_kf(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
 // Rows with more than one query token (chunked prefill), one workgroup per
 // (kv head, sequence, tile of query tokens); needs q_start.
 template <int KF> int launch_prefill_kf(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
 #define ASTR_DECLARE_LAUNCHERS(KF)                                                        \
   template <> int launch_partitioned_kf<KF>(const AttnArgs&, int32_t, hipStream_t);       \
   template <> int launch_streamk_kf<KF>(const AttnArgs&, int32_t, hipStream_t);           \
+  template <> int launch_streamk_plain_kf<KF>(const AttnArgs&, int32_t, hipStream_t);     \
   template <> int launch_prefill_kf<KF>(const AttnArgs&, int32_t, hipStream_t);
 ASTR_DECLARE_LAUNCHERS(kInt8)
 ASTR_DECLARE_LAUNCHERS(kE4M3)

@@ -27,6 +27,15 @@ namespace {
 #endif
 constexpr int KF = ASTR_KF;  // this translation unit's code format
 
+// The product build compiles this source twice per code format: the launches with
+// prefix packs, the entry point and the shared tables (ASTR_SK_PART 1), and the
+// launches without packs (ASTR_SK_PART 2), a unit scheduled for instruction-level
+// parallelism (measured faster for sequence rows, slower for pack rows). Trace builds
+// compile it once (ASTR_SK_PART 0), so that one set of trace marks serves every launch.
+#ifndef ASTR_SK_PART
+#define ASTR_SK_PART 0
+#endif
+
 // Per-wave timeline (trace builds only, -DASTR_TRACE=1, built apart from the product
 // library by `python -m aster_amd.build --trace`): wall-clock marks (100 MHz
 // s_memrealtime) of each wave of the last stream-K launch, read back with
@@ -897,41 +906,63 @@ int launch(AttnArgs a, hipStream_t stream) {
   return err == hipSuccess ? 0 : hip_fail(err, "paged_attention (stream-K) launch");
 }
 
-template <typename QT, int D>
+template <typename QT, int D, bool kP>
 int dispatch_group(const AttnArgs& a, int G, hipStream_t s) {
   switch (G) {
-    case 1: return a.num_packs > 0 ? launch<QT, D, 1, true>(a, s) : launch<QT, D, 1, false>(a, s);
-    case 2: return a.num_packs > 0 ? launch<QT, D, 2, true>(a, s) : launch<QT, D, 2, false>(a, s);
-    case 4: return a.num_packs > 0 ? launch<QT, D, 4, true>(a, s) : launch<QT, D, 4, false>(a, s);
-    case 8: return a.num_packs > 0 ? launch<QT, D, 8, true>(a, s) : launch<QT, D, 8, false>(a, s);
+    case 1: return launch<QT, D, 1, kP>(a, s);
+    case 2: return launch<QT, D, 2, kP>(a, s);
+    case 4: return launch<QT, D, 4, kP>(a, s);
+    case 8: return launch<QT, D, 8, kP>(a, s);
     case 16:
-      if constexpr (D <= 128) return launch<QT, D, 16, false>(a, s);  // 16 columns: no packs
+      if constexpr (D <= 128 && !kP) return launch<QT, D, 16, false>(a, s);  // 16 columns: no packs
       [[fallthrough]];
     default:
       return fail(ASTR_EUNSUPPORTED, "GQA group size %d not supported", G);
   }
 }
 
-template <typename QT>
+// kDims: the head dims this unit launches (bits: 1 = 64, 2 = 128, 4 = 256)
+template <typename QT, bool kP, int kDims>
 int dispatch_dim(const AttnArgs& a, int G, hipStream_t s) {
-  switch (a.cache.head_dim) {
-    case 64: return dispatch_group<QT, 64>(a, G, s);
-    case 128: return dispatch_group<QT, 128>(a, G, s);
-    case 256: return dispatch_group<QT, 256>(a, G, s);
-    default: return fail(ASTR_EUNSUPPORTED, "head_dim %d not in {64,128,256}", a.cache.head_dim);
-  }
+  const int d = a.cache.head_dim;
+  if constexpr ((kDims & 1) != 0) if (d == 64) return dispatch_group<QT, 64, kP>(a, G, s);
+  if constexpr ((kDims & 2) != 0) if (d == 128) return dispatch_group<QT, 128, kP>(a, G, s);
+  if constexpr ((kDims & 4) != 0) if (d == 256) return dispatch_group<QT, 256, kP>(a, G, s);
+  return fail(ASTR_EUNSUPPORTED, "head_dim %d not in {64,128,256}", d);
+}
+
+template <bool kP, int kDims>
+int dispatch_dtype(const AttnArgs& a, int G, int32_t q_dtype, hipStream_t s) {
+  if (q_dtype == ASTR_F16) return dispatch_dim<_Float16, kP, kDims>(a, G, s);
+  if (q_dtype == ASTR_BF16) return dispatch_dim<bf16_t, kP, kDims>(a, G, s);
+  return fail(ASTR_EUNSUPPORTED, "stream-K decode takes bf16/fp16 queries");
 }
 
 }  // namespace
 
+#if ASTR_SK_PART != 1
+// head dim 256 stays with the entry point's unit: under the max-ilp scheduler its
+// kernels spill to scratch
+template <>
+int launch_streamk_plain_kf<KF>(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
+  constexpr int kDims = ASTR_SK_PART == 2 ? 1 | 2 : 1 | 2 | 4;
+  return dispatch_dtype<false, kDims>(a, a.num_q_heads / a.cache.num_kv_heads, q_dtype, stream);
+}
+#endif
+
+#if ASTR_SK_PART != 2
 template <>
 int launch_streamk_kf<KF>(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {
   if (a.min_waves > a.total_waves)
     return fail(ASTR_EINVAL, "stream-K workspace too small for this launch");
   const int G = a.num_q_heads / a.cache.num_kv_heads;
-  if (q_dtype == ASTR_F16) return dispatch_dim<_Float16>(a, G, stream);
-  if (q_dtype == ASTR_BF16) return dispatch_dim<bf16_t>(a, G, stream);
-  return fail(ASTR_EUNSUPPORTED, "stream-K decode takes bf16/fp16 queries");
+  // a group of 16 fills the 16 query columns alone: no packs
+  if (a.num_packs == 0 || G == 16) {
+    if constexpr (ASTR_SK_PART == 1)
+      if (a.cache.head_dim == 256) return dispatch_dtype<false, 4>(a, G, q_dtype, stream);
+    return launch_streamk_plain_kf<KF>(a, q_dtype, stream);
+  }
+  return dispatch_dtype<true, 1 | 2 | 4>(a, G, q_dtype, stream);
 }
 
 #if ASTR_KF == 0
@@ -950,6 +981,7 @@ int stream_k_max_packs() { return kMaxPacksSK; }
 int stream_k_max_pack_seqs() { return kMaxPackSeqsSK; }
 int stream_k_work_rows(int) { return kMaxRowsSK; }
 #endif
+#endif  // ASTR_SK_PART != 2
 
 }  // namespace attn
 }  // namespace astr
