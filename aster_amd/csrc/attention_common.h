@@ -17,11 +17,14 @@ constexpr int kWaves = 4;              // waves per workgroup
 constexpr int kMaxBlocksPerWave = 64;  // block ids one wave keeps in a register
 // stream-K: blocks one wave may stream (its block list goes in windows of 64)
 constexpr int kMaxBlocksPerWaveSK = 1024;
-// stream-K split costs: a block of a prefix pack, any other block, and the start of a
-// work row with blocks (its query load and the partial written when it ends). The
-// split gives every wave an equal share of the total; the host sizes the wave
-// capacity from the same figures.
-constexpr int kSkPackCost = 6, kSkSeqCost = 10, kSkRowCost = 27;
+// stream-K split costs: any block that is not a prefix pack's, and the start of a work
+// row with blocks (its query load and the partial written when it ends). A pack
+// block's cost is chosen per launch within [kSkPackCostMin, kSkPackCostMax]: at most
+// the share that keeps the pack blocks' cost at half the total (SkSplit). The split
+// gives every wave an equal share of the total; the host sizes the wave capacity from
+// the same figures (the cheapest pack cost).
+constexpr int kSkSeqCost = 50, kSkRowCost = 135;
+constexpr int kSkPackCostMax = 32, kSkPackCostMin = 16;
 constexpr float kRescaleSlack = 8.0f;  // p = exp2(s - m) <= 2^8 between rescales
 // PV weights p * v_scale are rounded to f16: with p <= 2^8 (kRescaleSlack) and every
 // v_scale <= kVWeightCap they stay below 2^15 (f16's largest finite value is 65504).

@@ -75,36 +75,50 @@ constexpr int kFastPieces = 16;   // merge: sequences in at most this many piece
 __device__ __forceinline__ int row_seq(int x, int npk) { return x < npk ? -1 - x : x - npk; }
 
 // The split of one kv head's Bh blocks (the PB blocks of the packs first) into Wr
-// contiguous ranges of equal cost. A pack block costs kPackCost and any other block
-// kSeqCost (pack blocks are shared by all rows of the call and hit in cache, so they
-// are bound by the waves' own work, while a sequence's own blocks stream from HBM),
-// and every work row with blocks costs kRowCost more, charged to its first block:
-// block b of a row with ne rows with blocks before it starts at cost
-// c(b) = wcost(b) + kRowCost (ne + 1), wcost(b) the block costs before b. Range r
-// owns the blocks whose start lies in [T r / Wr, T (r + 1) / Wr), T = wcost(Bh) +
-// kRowCost * (rows with blocks). The row costs were fitted to per-wave timelines of
-// the config2 and config4 workloads (a row start measured ~3.4 us against ~1.27 us per
-// streamed block; pack blocks ~0.9 us). Wr: the resident waves per head (one round,
+// contiguous ranges of equal cost. A pack block costs KP and any other block kSeqCost
+// (pack blocks are shared by all rows of the call and hit in cache, so they are bound
+// by the waves' own work, while a sequence's own blocks stream from HBM), and every
+// work row with blocks costs kRowCost more, charged to its first block: block b of a
+// row with ne rows with blocks before it starts at cost c(b) = wcost(b) +
+// kRowCost (ne + 1), wcost(b) the block costs before b. Range r owns the blocks whose
+// start lies in [T r / Wr, T (r + 1) / Wr), T = wcost(Bh) + kRowCost * (rows with
+// blocks). The costs were fitted to per-wave timelines of the config2 and config4
+// workloads (a row start measured ~3.4 us against ~1.27 us per streamed block; pack
+// blocks ~0.85 us). KP is 32 (against 50 per sequence block) unless the pack blocks
+// would then take over half of T: each CU holds the workgroups of ranges r and
+// r + Wr / 2, and two compute-bound pack waves on one CU run ~25 % slower per block
+// (config 4 with packs: 72.8 us at KP 32, 78.9 at 33, where the packs pass one half).
+// Wr: the resident waves per head (one round,
 // no tail), more where a range could otherwise hold over kMaxBlocksPerWaveSK
 // blocks, never more than launched, and ranges no shorter than a block's cost, so
 // that a row split over ranges r0..r1 has exactly one piece in each of them (the
 // merge relies on it; a range between two rows may own no block, its wave then
 // has nothing to do). The decode and the merge kernel both derive the split with
 // this type.
-constexpr int kPackCost = kSkPackCost, kSeqCost = kSkSeqCost, kRowCost = kSkRowCost;
+constexpr int kSeqCost = kSkSeqCost, kRowCost = kSkRowCost;
+// pack block cost: the pack blocks' cost at most the rest of the split's
+__device__ __forceinline__ int64_t sk_pack_cost(int64_t bh, int64_t pb, int64_t rows) {
+  if (pb <= 0) return kSkPackCostMax;
+  const int64_t even = (kSeqCost * (bh - pb) + kRowCost * rows) / pb;
+  return even < kSkPackCostMin ? kSkPackCostMin : even > kSkPackCostMax ? kSkPackCostMax : even;
+}
 struct SkSplit {
-  int64_t PB, T, Wr;
+  int64_t PB, KP, T, Wr;
   __device__ SkSplit(const AttnArgs& a, int64_t bh, int64_t pb, int64_t rows_with_blocks,
                      int hkv)
-      : PB(pb), T(kPackCost * pb + kSeqCost * (bh - pb) + kRowCost * rows_with_blocks) {
-    int64_t w = (T + kPackCost * kMaxBlocksPerWaveSK - 1) / (kPackCost * kMaxBlocksPerWaveSK);
-    if (w < a.pref_waves / hkv) w = a.pref_waves / hkv;
+      : PB(pb), KP(sk_pack_cost(bh, pb, rows_with_blocks)),
+        T(KP * pb + kSeqCost * (bh - pb) + kRowCost * rows_with_blocks) {
+    // the resident waves, or more where a range would pass kMaxBlocksPerWaveSK pack
+    // blocks (divided only then: KP is not a constant)
+    int64_t w = a.pref_waves / hkv;
+    if (T > w * KP * kMaxBlocksPerWaveSK)
+      w = (T + KP * kMaxBlocksPerWaveSK - 1) / (KP * kMaxBlocksPerWaveSK);
     if (w > a.total_waves / hkv) w = a.total_waves / hkv;
     const int64_t most = T / kSeqCost > 1 ? T / kSeqCost : 1;
     Wr = w < most ? w : most;
   }
   __device__ int64_t wcost(int64_t b) const {
-    return b < PB ? kPackCost * b : kPackCost * PB + kSeqCost * (b - PB);
+    return b < PB ? KP * b : KP * PB + kSeqCost * (b - PB);
   }
   // start of block b of a row with `ne` rows with blocks before it
   __device__ int64_t cost(int64_t b, int ne) const { return wcost(b) + kRowCost * (ne + 1); }
@@ -146,7 +160,7 @@ __device__ __forceinline__ void range_bounds(const SkSplit& sp, int64_t r, const
   const int x1 = lb < 0 ? -1 : lb * S + __popcll(pass >> 32) - 1;
   auto first_at = [&](int x, int64_t c) __attribute__((always_inline)) -> int64_t {
     if (x < 0) return 0;  // before the first row's start
-    const int64_t w = x < npk ? kPackCost : kSeqCost;
+    const int64_t w = x < npk ? sp.KP : kSeqCost;
     const int64_t k = (c - start(x) + w - 1) / w;
     const int64_t b = s_cu[x] + k;
     return b < s_cu[x + 1] ? b : s_cu[x + 1];
@@ -713,7 +727,7 @@ __device__ __forceinline__ RowPieces row_pieces(int64_t fb, int64_t fe, int ne, 
   const int64_t r1 = sp.range_of(fe, ne);
   rp.count = (int)(r1 - rp.r0 + 1);
   rp.first_is_tail =
-      fb > 0 && sp.range_at(cf - kRowCost - (fb - 1 < sp.PB ? kPackCost : kSeqCost)) == rp.r0;
+      fb > 0 && sp.range_at(cf - kRowCost - (fb - 1 < sp.PB ? sp.KP : kSeqCost)) == rp.r0;
   return rp;
 }
 __device__ __forceinline__ int64_t piece_slot(const AttnArgs& a, const RowPieces& rp, int p,

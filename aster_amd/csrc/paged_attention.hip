@@ -63,7 +63,7 @@ int64_t max_total_blocks(int32_t num_seqs, int32_t num_kv_heads, int32_t max_con
 int64_t streamk_need_waves(int64_t total_blocks, int32_t num_kv_heads, int64_t rows) {
   const int64_t per_head = (total_blocks + num_kv_heads - 1) / num_kv_heads;
   const int64_t cost = kSkSeqCost * per_head + kSkRowCost * rows;
-  const int64_t unit = (int64_t)kSkPackCost * kMaxBlocksPerWaveSK;
+  const int64_t unit = (int64_t)kSkPackCostMin * kMaxBlocksPerWaveSK;
   return num_kv_heads * ((cost + unit - 1) / unit);
 }
 

@@ -44,10 +44,10 @@ def test_workspace_bytes():
         # [block prefix over up to 512 work rows + 1, rows with blocks before each,
         # 4-int pack record per sequence][acc][(m, l)] of 2 slots per wave of slot
         # columns, then the packs' and packed sequences' own slots. Waves: at least
-        # enough that a range of the cheapest blocks (7 per block against 10, plus 27
-        # per work row) holds at most 1024 blocks.
+        # enough that a range of the cheapest blocks (pack blocks at no less than 16
+        # against 50, plus 135 per work row) holds at most 1024 blocks.
         per_head = s * -(-max_ctx // 16)
-        need = hkv * -(-(10 * per_head + 27 * (s + packs)) // (7 * 1024))
+        need = hkv * -(-(50 * per_head + 135 * (s + packs)) // (16 * 1024))
         cap = max(cus * 32, need)
         cap = -(-cap // 4) * 4
         g = hq // hkv
