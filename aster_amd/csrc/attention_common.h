@@ -580,36 +580,28 @@ __device__ __forceinline__ float query_operand(const QueryRaw<D>& q, bool gvalid
 }
 
 // QK^T operands of one query row per lane for the decode kernels: int8 codes meet a
-// two-term int8 query on v_mfma_i32_16x16x64_i8 (the K codes need no conversion); FP8
+// three-term int8 query on v_mfma_i32_16x16x64_i8 (the K codes need no conversion); FP8
 // codes, converted to f16, meet an f16 query on v_mfma_f32_16x16x32_f16.
 template <int D, int KF>
 struct QkOperand {
   half8_t op[D / 32];
 };
+// INT8 codes: the query column as 128 Q + lo2 within 1/2 of 128 x (query_column_i8 with
+// three terms, x = q * kQRange / max|q|), i.e. within 2^-8 of a ~15-bit step of q, about
+// 2^-22 of max|q| per element: the score K.q carries, per unit of K, the error an fp32
+// dot product's own rounding has. Every block takes all three terms (the third on a
+// separate int32 accumulator: 128 (K.Q) + K.lo2 can exceed int32), so no key scale,
+// however large, sees the coarser two-term query.
 template <int D>
 struct QkOperand<D, kInt8> {
-  int4_t hi[D / 64], lo[D / 64];
-  // K scale above which a block takes the third query term: the two-term query's
-  // worst-case score error, 1/2 step times 127 D per unit of K scale times the score
-  // factor, would exceed kFineScoreError (base-2 units) there
-  float ks_fine;
-  // what the third term is rebuilt from: the lane's query elements (query_lane_ptr)
-  // and the column's quantization (query_column_i8)
-  const void* qptr;
-  float inv, lift;
+  int4_t hi[D / 64], lo[D / 64], lo2[D / 64];
 };
-// Largest worst-case score error (base 2) a block may carry from the two-term query
-// before the third term is added. The worst case aligns every code at 127 with every
-// rounding; the typical error is ~sqrt(12 D) max|k| / rms|k| / 2 (about 50 at D = 128)
-// times smaller, a few 1e-3 of a softmax weight at most. (At 1/32, K rows with x8
-// outliers, as in the config5 workload, took the third term on most blocks.)
-constexpr float kFineScoreError = 1.f / 8.f;
 
 // Builds the operand of query row r (lane layout of QueryRaw; rows r >= G are zero)
 // and returns its score factor, code scale included. Cross-lane: uniform control flow.
 template <typename QT, int D, int KF>
 __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, float qk_scale_log2,
-                                            QkOperand<D, KF>& op, const QT* qptr) {
+                                            QkOperand<D, KF>& op) {
   if constexpr (KF == kInt8) {
     static_assert(sizeof(QT) == 2, "16-bit queries (fp32 queries take the exact VALU kernel)");
     QueryColumn<QT, D> col;
@@ -618,36 +610,31 @@ __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, f
       col.w[h][0] = q.w[h][0];
       col.w[h][1] = q.w[h][1];
     }
-    const float cf = query_column_i8<QT, D>(col, gvalid, qk_scale_log2, op.hi, op.lo, nullptr,
-                                            nullptr, &op.inv, &op.lift);
-    op.ks_fine = (kFineScoreError / (63.5f * D)) / cf;  // +inf for cf = 0, NaN for NaN
-    op.qptr = qptr;
-    return cf;
+    return query_column_i8<QT, D, 3>(col, gvalid, qk_scale_log2, op.hi, op.lo, op.lo2);
   } else {
     return query_operand<QT, D>(q, gvalid, qk_scale_log2, op.op) * code_scale<KF>();
   }
 }
 
-// Screening of the rare blocks in mfma_block: lanes of odd token group qg test the
-// staged V scale of token r against vlim (before the weight scale, a power of two, so
-// the test is exact); lanes of even qg test the K scale of token r against the
-// column's third-term threshold (none for FP8 codes). Together they cover every scale
-// of the block; a block with any scale above its limit takes the full tests.
-template <int D, int KF>
-__device__ __forceinline__ float screen_limit(const QkOperand<D, KF>& qop, float vlim, int qg) {
-  if (qg & 1) return vlim * (1.f / v_weight_scale<KF>());
-  if constexpr (KF == kInt8) return qop.ks_fine;
-  else return INFINITY;
+// Screening of the rare blocks in mfma_block: every lane tests the staged V scale of
+// token r against vlim (before the weight scale, a power of two, so the test is exact);
+// the four lanes of each r test the same scale, so together the 16 lanes of a token
+// group cover every V scale of the block, and a block with one above the limit takes
+// the full test.
+template <int KF>
+__device__ __forceinline__ float screen_limit(float vlim) {
+  return vlim * (1.f / v_weight_scale<KF>());
 }
-// A piece's starting VRange for the column operand qop (built before it).
-template <int D, int KF>
-__device__ __forceinline__ VRange vrange_start(const QkOperand<D, KF>& qop, int qg) {
-  return VRange{0.f, kVWeightCap, screen_limit<D, KF>(qop, kVWeightCap, qg)};
+// A piece's starting VRange.
+template <int KF>
+__device__ __forceinline__ VRange vrange_start() {
+  return VRange{0.f, kVWeightCap, screen_limit<KF>(kVWeightCap)};
 }
 
 // ---- one staged 16-token block through the MFMAs
-//   S^T[t][g] = K[t][:] . Q[g][:]     INT8 codes: 2 (D/64) x 2 v_mfma_i32_16x16x64_i8
-//                                     (hi, then lo on the hi result shifted by 7);
+//   S^T[t][g] = K[t][:] . Q[g][:]     INT8 codes: 3 (D/64) x v_mfma_i32_16x16x64_i8
+//                                     (hi, then lo on the hi result shifted by 7, and
+//                                     lo2 on its own accumulator);
 //                                     FP8 codes: 4 (D/32) x v_mfma_f32_16x16x32_f16
 //   O^T[d][g] += V^T[d][t] P^T[t][g]  8 (D/16) x v_mfma_f32_16x16x16_f16
 // acc[D/16] is one more tile: with biased V operands (biased_v), a row of ones times
@@ -673,8 +660,9 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
   // of a token group
   const float4_t vs = *reinterpret_cast<const float4_t*>(st + S::kS + 64 + 16 * qg) * v_weight_scale<KF>();
   const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
-  // the one staged scale this lane screens against vr.screen (screen_limit)
-  const float screened = *reinterpret_cast<const float*>(st + S::kS + 64 * (qg & 1) + 4 * r);
+  // the one staged scale this lane screens against vr.screen (screen_limit): the V scale
+  // of token r
+  const float screened = *reinterpret_cast<const float*>(st + S::kS + 64 + 4 * r);
   // rare blocks, found by the screen: V scales beyond vr.vlim grow the running
   // maximum's offset, with its own rescale of l and acc, before the block's weights
   // are formed
@@ -687,47 +675,12 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
       frexpf(wm / vr.vlim, &x);  // in [2^(x-1), 2^x), x >= 1
       vr.koff += (float)x;
       vr.vlim = ldexpf(vr.vlim, x);
-      vr.screen = screen_limit<D, KF>(qop, vr.vlim, qg);
+      vr.screen = screen_limit<KF>(vr.vlim);
       const float alpha = ldexpf(1.f, -x);  // m + x is the new maximum (with offset)
       m += (float)x;
       l *= alpha;
 #pragma unroll
       for (int n = 0; n <= NPV; ++n) acc[n] *= alpha;
-    }
-  };
-  // ... and large scores take the third query term, K.lo2 / 128 (exact int32, then
-  // scaled by a power of two), wherever a block's K scales reach the column's
-  // threshold; the term is rebuilt from the query elements at the column's
-  // quantization, so that it completes the hi and lo terms
-  auto third_term = [&](float4_t& sc4) __attribute__((always_inline)) {
-    if constexpr (KF == kInt8) {
-      const float kmx = fmaxf(fmaxf(ks[0], ks[1]), fmaxf(ks[2], ks[3]));
-      if (__ballot(kmx > qop.ks_fine) != 0) {
-        int4_t sf = {0, 0, 0, 0};
-#pragma nounroll
-        for (int h = 0; h < KCH; ++h) {
-          const int4_t kh = *reinterpret_cast<const int4_t*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
-          constexpr int kVec = 16 / (int)sizeof(QT);
-          uint4 w[16 / kVec];
-#pragma unroll
-          for (int c = 0; c < 16 / kVec; ++c)
-            w[c] = reinterpret_cast<const uint4*>(static_cast<const QT*>(qop.qptr) + 64 * h)[c];
-          const QT* e = reinterpret_cast<const QT*>(w);
-          int4_t q2;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            uint32_t fb[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              fb[i] = __builtin_bit_cast(
-                  uint32_t, query_terms<3>(to_float<QT>(e[4 * k + i]) * qop.lift, qop.inv).lo2);
-            q2[k] = (int)low_bytes(fb);
-          }
-          sf = __builtin_amdgcn_mfma_i32_16x16x64_i8(kh, q2, sf, 0, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sc4[j] = __builtin_fmaf((float)sf[j], 1.f / 128.f, sc4[j]);
-      }
     }
   };
   // Up to D = 128 the screen follows the QK MFMAs, off their path; at D = 256 the V
@@ -763,18 +716,22 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
   if constexpr (kScreenLate) read_v_words();
   float4_t s4;
   if constexpr (KF == kInt8) {
-    // exact int32 K.Q = 128 (K.hi) + K.lo straight from the staged codes
+    // exact int32 K.Q = 128 (K.hi) + K.lo and K.lo2 straight from the staged codes; the
+    // score is K.Q + K.lo2 / 128 (one rounding each for the conversions and the fma)
     int4_t kop[KCH];
 #pragma unroll
     for (int h = 0; h < KCH; ++h)
       kop[h] = *reinterpret_cast<const int4_t*>(st + S::kK + k_chunk<D>(r, qg + 4 * h));
-    int4_t si = {0, 0, 0, 0};
+    int4_t si = {0, 0, 0, 0}, sf = {0, 0, 0, 0};
 #pragma unroll
     for (int h = 0; h < KCH; ++h) si = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop.hi[h], si, 0, 0, 0);
+#pragma unroll
+    for (int h = 0; h < KCH; ++h) sf = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop.lo2[h], sf, 0, 0, 0);
     si = si << 7;
 #pragma unroll
     for (int h = 0; h < KCH; ++h) si = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[h], qop.lo[h], si, 0, 0, 0);
-    s4 = float4_t{(float)si[0], (float)si[1], (float)si[2], (float)si[3]};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s4[j] = __builtin_fmaf((float)sf[j], 1.f / 128.f, (float)si[j]);
     // keeps these conversions of MFMA results ahead of the branches below: sunk into
     // their blocks, they were issued without the wait states an MFMA result needs
     // (wrong scores at D = 64)
@@ -795,13 +752,9 @@ __device__ __forceinline__ void mfma_block(const char* st, const QkOperand<D, KF
     }
   }
   if constexpr (kScreenLate) {
-    // one compare and ballot per block; the rare paths are laid out away from the loop
-    if (__builtin_expect(__ballot(screened > vr.screen) != 0, 0)) {
-      grow_vrange();
-      third_term(s4);
-    }
+    // one compare and ballot per block; the rare path is laid out away from the loop
+    if (__builtin_expect(__ballot(screened > vr.screen) != 0, 0)) grow_vrange();
   } else {
-    third_term(s4);
     read_v_words();
   }
   // scores of tokens 4*qg + j for head g = r (base 2, dequantised)

@@ -165,8 +165,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   if (NS == 3 && 2 < nblk) stage_block<D>(a, __builtin_amdgcn_readlane(ids, 2), kvh, lane, st2);
 
   QkOperand<D, KF> qop;
-  const float cf = qk_operand<QT, D, KF>(qraw, gvalid, a.qk_scale_log2, qop,
-                                         query_lane_ptr<QT, G>(a, tok, kvh, r, qg));
+  const float cf = qk_operand<QT, D, KF>(qraw, gvalid, a.qk_scale_log2, qop);
   float4_t acc[NPV + 1];  // [NPV]: weight sums (INT8)
 #pragma unroll
   for (int n = 0; n <= NPV; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -174,7 +173,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(AttnArgs a) {
   // all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
   float m = gvalid ? -FLT_MAX : 0.f;
   float l = 0.f;
-  VRange vr = vrange_start<D, KF>(qop, qg);
+  VRange vr = vrange_start<KF>();
   bool bad_score = false;
 
   auto step = [&](int i, char* st) __attribute__((always_inline)) {

@@ -562,13 +562,13 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
       else if (first == 2) wait_vmcnt<2 * S::kLoads>();
       else wait_vmcnt<S::kLoads>();
       lds_query<QT, D>(stage(NS - 1), r < G ? r : 0, qg, qr);
-      cf = qk_operand<QT, D, KF>(qr, c0.valid, a.qk_scale_log2, qop, c0.q);
+      cf = qk_operand<QT, D, KF>(qr, c0.valid, a.qk_scale_log2, qop);
       if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (their values are consumed)
     } else {
       load_query_at<QT, D>(c0.q, qr);
       const int first = min(NS, nblk);
       for (int j = 0; j < first; ++j) issue(j);
-      cf = qk_operand<QT, D, KF>(qr, c0.valid, a.qk_scale_log2, qop, c0.q);
+      cf = qk_operand<QT, D, KF>(qr, c0.valid, a.qk_scale_log2, qop);
     }
     if (64 < nblk) request_ids(1);
   }
@@ -603,7 +603,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     const int64_t pfb = s_cu[px];  // first block of the row in the per-head order
     if (i > 0) {  // a new row starts inside this wave's range
       load_query_at<QT, D>(col.q, qr);
-      cf = qk_operand<QT, D, KF>(qr, col.valid, a.qk_scale_log2, qop, col.q);
+      cf = qk_operand<QT, D, KF>(qr, col.valid, a.qk_scale_log2, qop);
       if (kTrace && pieces_seen == 2) tm[6] = wall_clock64();
     }
 #pragma unroll
@@ -612,7 +612,7 @@ __global__ __launch_bounds__(sk_waves<D>() * kWave) void decode_streamk_kernel(A
     // are all masked (padding) give exp2(-inf) = 0, not exp2(-inf + inf)
     m = col.valid ? -FLT_MAX : 0.f;
     l = 0.f;
-    VRange vr = vrange_start<D, KF>(qop, qg);
+    VRange vr = vrange_start<KF>();
     const int pos0 = (pblk0 + (int)(b0 + i - pfb)) * kBlockTokens;
     for (;;) {
       // the row's blocks in the current window: up to the first lane with another row
@@ -876,18 +876,14 @@ __global__ __launch_bounds__(kWave) void merge_streamk_kernel(AttnArgs a) {
   }
 }
 
-// Workgroups of `kernel` one CU holds at once (queried once per kernel).
+// Workgroups of `kernel` one CU holds at once.
 template <typename Kernel>
-int resident_per_cu(Kernel kernel, int threads) {
-  static int cached = 0;
-  if (cached == 0) {
-    int n = 0;
-    cached = (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) ==
-                  hipSuccess && n > 0)
-                 ? n
-                 : 1;
-  }
-  return cached;
+int query_resident_per_cu(Kernel kernel, int threads) {
+  int n = 0;
+  return (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) == hipSuccess &&
+          n > 0)
+             ? n
+             : 1;
 }
 
 int device_cus() {
@@ -902,10 +898,12 @@ template <typename QT, int D, int G, bool kPacks>
 int launch(AttnArgs a, hipStream_t stream) {
   auto kernel = decode_streamk_kernel<QT, D, G, kPacks>;
   constexpr int NW = sk_waves<D>();
+  // queried once per instantiation (each has its own registers and LDS tables)
+  static const int per_cu = query_resident_per_cu(kernel, NW * kWave);
   // launch one wave per resident slot (whole workgroups) and at least min_waves (the
   // host-side bound), at most the workspace capacity passed in total_waves; the
   // kernels settle the waves they use from the actual block count
-  const int64_t resident = (int64_t)device_cus() * resident_per_cu(kernel, NW * kWave) * NW;
+  const int64_t resident = (int64_t)device_cus() * per_cu * NW;
   int64_t waves = resident;
   if (waves < a.min_waves) waves = (a.min_waves + NW - 1) / NW * NW;
   if (waves > a.total_waves) waves = a.total_waves / NW * NW;

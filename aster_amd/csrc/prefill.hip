@@ -12,7 +12,8 @@
 // stages one block of the step into LDS with direct global->LDS loads and then
 // all four waves run all four blocks through the MFMAs:
 //   S^T[t][c]  = K[t][:] . Q[c][:]     v_mfma_i32_16x16x64_i8: the K codes as stored,
-//                                        the query as two int8 terms (exact int32 dot)
+//                                        the query as two int8 terms (exact int32 dot),
+//                                        three on steps with large key scales
 //   O^T[d][c] += V^T[d][t] . P^T[t][c]  v_mfma_f32_16x16x32_f16 over two blocks (P^T
 //                                        carries V's scales)
 // so every K/V byte of the unit's range is read once per query tile and shared by
@@ -185,6 +186,16 @@ __device__ int scan_tiles(const AttnArgs& a, int tq, int unit, int* s_wsum, int*
 
 // |S_int| <= 127 * kQRange * 256; a score factor below this keeps every score finite
 constexpr float kSafeFactor = 1.0e29f;
+// INT8 codes: the two-term query Q is within 1/2 of x = q * kQRange / max|q| per
+// element, so a key with scale ks carries at most 1/2 * 127 D * ks * cf of score error
+// (base 2; cf the column's score factor). A step in which any key scale times a
+// column's cf exceeds kFineScoreError / (63.5 D) adds the third term, K.lo2 / 128 (lo2 =
+// rint(128 (x - Q))), which divides that bound by 128. The worst case aligns every code
+// at 127 with every rounding; the typical error is ~50 times smaller (the rounding
+// errors are independent and codes average ~1/4 of 127), so steps without the term
+// carry ~2e-4 nats of score error at most, well inside what moves an output by the
+// north_star's 2e-3. Seeded N(0,1) queries and keys stay ~4x below the threshold.
+constexpr float kFineScoreError = 1.f / 64.f;
 // FP8 codes take the f16 QK path: |S| <= D * 2^15 * max|code as f16| (448 * 2^-8 for
 // E4M3FN, 57344 for E5M2) with D <= 256, times a factor below these stays finite.
 constexpr float kSafeFactorE4M3 = 1.0e31f;
@@ -399,7 +410,89 @@ __device__ __forceinline__ void prefill_pv(const uint4* vt, const float (&u)[NT]
 // the scores are masked to -inf outside the bounds, for padding keys and for unused
 // blocks (whose stages hold stale but finite codes and scales) and checked for
 // non-finite values.
-template <int D, int NT>
+// The query columns of a wave's NT tiles, for the third query term: column t of lane
+// (qg, r) is head chead[t] of token row q0 + ctok[t] (token row q0 + t0 when it is not
+// valid, as loaded for the first two terms).
+template <int NT>
+struct ColumnRefs {
+  int q0, t0;
+  const int (&ctok)[NT];
+  const int (&chead)[NT];
+  const bool (&cvalid)[NT];
+};
+
+// The third query term of a step (INT8 codes, every tile of the wave): per 64-wide d
+// chunk, lo2 rebuilt from the query elements by the column's own quantization (the terms
+// query_column_i8 gives for three terms), that chunk's K.lo2 exact in int32 on the
+// staged codes, added to the dequantized scores as (K.lo2 / 128) * ks. One chunk of one
+// tile is live at a time and the key scales are read again from LDS, so the path fits
+// beside the step's accumulators.
+template <typename QT, int D, int NT>
+__device__ __forceinline__ void prefill_third_term(const char* cur, const AttnArgs& a,
+                                                   const ColumnRefs<NT>& col, int r, int qg,
+                                                   float (&u)[NT][4 * kWaves]) {
+  using S = Stage<D>;
+  constexpr int KCH = D / 64;
+  constexpr int kVec = 16 / (int)sizeof(QT);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const QT* qp = static_cast<const QT*>(a.q) +
+                   (int64_t)(col.q0 + (col.cvalid[t] ? col.ctok[t] : col.t0)) * a.q_tok +
+                   (int64_t)col.chead[t] * a.q_head + 16 * qg;
+    // the column's quantization as query_column_i8 sets it: the NaN-propagating maximum
+    // of |q| over the column (lanes r, r + 16, r + 32, r + 48), the exact lift of columns
+    // below 2^-64 and inv = kQRange / max (a maximum does not depend on its order)
+    float mx = 0.f;
+#pragma nounroll
+    for (int h = 0; h < KCH; ++h) {
+      uint4 w[16 / kVec];
+#pragma unroll
+      for (int c = 0; c < 16 / kVec; ++c) w[c] = reinterpret_cast<const uint4*>(qp + 64 * h)[c];
+      const QT* e = reinterpret_cast<const QT*>(w);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = vmax(mx, fabsf(to_float<QT>(e[i])));
+    }
+    mx = vmax(mx, shfl_xor(mx, 16));
+    mx = vmax(mx, shfl_xor(mx, 32));
+    mx = col.cvalid[t] ? mx : 0.f;
+    const bool finite = __builtin_isfinite(mx);
+    const float up = mx > 0.f && mx < 0x1p-64f ? 0x1p64f : 1.f;
+    mx *= up;
+    const float inv = (finite && mx > 0.f) ? (float)kQRange / mx : 0.f;
+#pragma nounroll
+    for (int h = 0; h < KCH; ++h) {
+      uint4 w[16 / kVec];
+#pragma unroll
+      for (int c = 0; c < 16 / kVec; ++c) w[c] = reinterpret_cast<const uint4*>(qp + 64 * h)[c];
+      const QT* e = reinterpret_cast<const QT*>(w);
+      int4_t lo2;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t fb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          fb[i] = __builtin_bit_cast(
+              uint32_t,
+              query_terms<3>(to_float<QT>(e[4 * k + i]) * up, inv).lo2);
+        lo2[k] = (int)low_bytes(fb);
+      }
+      // chunk h's share of K.lo2 (exact), added to each score on its own
+#pragma unroll
+      for (int b = 0; b < kWaves; ++b) {
+        const char* st = cur + b * S::kBytes;
+        const int4_t sf = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+            *reinterpret_cast<const int4_t*>(st + S::kK + k_chunk<D>(r, qg + 4 * h)), lo2,
+            int4_t{0, 0, 0, 0}, 0, 0, 0);
+        const float4_t ks = *reinterpret_cast<const float4_t*>(st + S::kS + 16 * qg);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          u[t][4 * b + k] = __builtin_fmaf((float)sf[k], ks[k] * (1.f / 128.f), u[t][4 * b + k]);
+      }
+    }
+  }
+}
+
+template <typename QT, int D, int NT>
 __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, uint32_t use,
                                              uint32_t bounded, bool masks, int kb0,
                                              const QOp<D> (&qop)[NT],
@@ -408,7 +501,8 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
                                              int qg, const half8_t& ones, bool vmix,
                                              const half4_t& vf,
                                              float4_t (&acc)[NT][D / 16 + 1], float (&m)[NT],
-                                             bool& bad_score) {
+                                             bool& bad_score, const AttnArgs& a,
+                                             const ColumnRefs<NT>& cols) {
   using S = Stage<D>;
   constexpr int KCH = D / 64;
   constexpr int NPV = D / 16;
@@ -478,15 +572,23 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
     kx = max(kx, max(max(kb[0], kb[1]), max(kb[2], kb[3])));
   }
   const float kmax = __builtin_bit_cast(float, kx);
-  bool ok = true;
+  bool ok = true, fine = false;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) ok = ok && kmax * cf[t] <= safe_factor();  // false for NaN
+  for (int t = 0; t < NT; ++t) {
+    const float x = kmax * cf[t];
+    ok = ok && x <= safe_factor();  // false for NaN
+    if constexpr (KF == kInt8) fine = fine || x > kFineScoreError / (63.5f * D);
+  }
   const bool unsafe = __ballot(!ok) != 0;
   float u[NT][4 * NBK];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int j = 0; j < 4 * NBK; ++j) u[t][j] = (float)sacc[j / 4][t][j % 4] * ks[j / 4][j % 4];
+  if constexpr (KF == kInt8) {
+    // steps whose key scales make the two-term query's error bound pass the budget
+    if (__builtin_expect(__ballot(fine) != 0, 0)) prefill_third_term<QT, D, NT>(cur, a, cols, r, qg, u);
+  }
   const bool edge = (use != (1u << NBK) - 1) | (bounded != 0) | unsafe | padded;
   if (edge) {
     asm volatile("");  // keeps this a branch: if-converted, the interior steps would pay for it
@@ -745,6 +847,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   const int w_lo_min = a.window > 0 ? max(0, pos0 + tk_lo - a.window + 1) : 0;
   const int w_lo_max = a.window > 0 ? max(0, pos0 + tk_hi - a.window + 1) : 0;
 
+  const ColumnRefs<NT> cols{q0, t0, ctok, chead, cvalid};
   float4_t acc[NT][NPV + 1];  // [NPV]: row sums in row 0 (lanes qg = 0)
   const _Float16 one = r == 0 ? (_Float16)1.f : (_Float16)0.f;
   const half8_t ones = {one, one, one, one, one, one, one, one};  // A operand: row 0 all ones
@@ -822,8 +925,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
         if (!(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min)) bounded |= 1u << w;
       }
       if (use != 0)
-        prefill_step<D, NT>(cur, vt[0], use, bounded & use, masks, kb0, qop, cf, cfe, lo, hi, r, qg,
-                            ones, vmix, vf, acc, m, bad_score);
+        prefill_step<QT, D, NT>(cur, vt[0], use, bounded & use, masks, kb0, qop, cf, cfe, lo, hi, r,
+                                qg, ones, vmix, vf, acc, m, bad_score, a, cols);
     }
     __syncthreads();  // step i's stage may be refilled
   }

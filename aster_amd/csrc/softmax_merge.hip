@@ -53,6 +53,12 @@ __global__ __launch_bounds__(256) void merge_softmax_kernel(
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// [p, p + bytes) and [q, q + bytes_q) share a byte.
+bool overlap(const void* p, size_t bytes, const void* q, size_t bytes_q) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
+  return a < b + bytes_q && b < a + bytes;
+}
+
 }  // namespace
 }  // namespace astr
 
@@ -68,6 +74,22 @@ extern "C" int astr_merge_softmax_f32(const float* left_max, const float* left_m
   if (!left_max || !left_mass || !left_weighted || !right_max || !right_mass ||
       !right_weighted || !out_max || !out_mass || !out_weighted)
     return fail(ASTR_EINVAL, "every state pointer is required");
+  // Every thread of a row reads the row's two maxima while one of them writes the
+  // merged maximum: an output over an input would let later threads of the row weigh
+  // by the merged maximum. Outputs therefore may not overlap any input or each other.
+  const size_t rb = (size_t)rows * sizeof(float), wb = rb * (size_t)width;
+  const void* in[6] = {left_max, left_mass, left_weighted, right_max, right_mass, right_weighted};
+  const size_t in_bytes[6] = {rb, rb, wb, rb, rb, wb};
+  const void* outs[3] = {out_max, out_mass, out_weighted};
+  const size_t out_bytes[3] = {rb, rb, wb};
+  for (int o = 0; o < 3; ++o) {
+    for (int i = 0; i < 6; ++i)
+      if (astr::overlap(outs[o], out_bytes[o], in[i], in_bytes[i]))
+        return fail(ASTR_EINVAL, "merge_softmax outputs must not overlap its inputs");
+    for (int p = 0; p < o; ++p)
+      if (astr::overlap(outs[o], out_bytes[o], outs[p], out_bytes[p]))
+        return fail(ASTR_EINVAL, "merge_softmax outputs must not overlap each other");
+  }
   const bool vec = width % 4 == 0 && astr::aligned16(left_weighted) &&
                    astr::aligned16(right_weighted) && astr::aligned16(out_weighted);
   const int v = vec ? 4 : 1;

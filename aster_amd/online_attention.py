@@ -212,12 +212,32 @@ def online_attention(query, blocks, *, query_positions, causal=True, window=None
     device = query.device
     positions = query_positions.to(torch.int64)
 
-    # transient arena: row b owns blocks [b * nb, (b + 1) * nb); every position up to
-    # the last key (and, causal, the last query) has a slot
-    last = max(b.offset + _length(b.key) for b in blocks)
+    # transient arena: row b owns blocks [b * nb, (b + 1) * nb) holding positions from
+    # `base` (the first page's offset rounded down to a block) on: causal and window
+    # masks are translation invariant, so memory and streamed blocks follow the span of
+    # keys, not their absolute offsets. Positions between pages are padding keys.
+    base = min(b.offset for b in blocks) // BLOCK * BLOCK
+    end = max(b.offset + _length(b.key) for b in blocks)  # one past the last key
+    # one decode row per query token, its context ending at its position (causal), or
+    # at the last key; keys past the last page are never visible, so a causal row's
+    # context stops there unless a window counts back from its own position (then a
+    # row whose window starts past the last key sees nothing); a padded query, or one
+    # before every key, sees nothing and comes out zero
     if causal:
-        last = max(last, int(positions.max()) + 1)
-    nb = -(-last // BLOCK)
+        ctx = positions + 1 - base
+        if window is None:
+            ctx = torch.clamp(ctx, max=end - base)
+        else:
+            ctx = torch.where(positions + 1 - window >= end, torch.zeros_like(ctx), ctx)
+        ctx = torch.clamp(ctx, min=0)
+    else:
+        ctx = torch.full_like(positions, end - base)
+    if query_padding is not None:
+        ctx = torch.where(query_padding, ctx, torch.zeros_like(ctx))
+    span = max(int(ctx.max()), 1)
+    if span >= 2**31:
+        raise UnsupportedAttentionBackend("hip_int8_paged contexts are int32")
+    nb = -(-span // BLOCK)
     cache = PagedKVCache(num_blocks=batch * nb, num_layers=1, num_kv_heads=heads,
                          head_dim=width, device=device,
                          quantization=KVQuantization(formats.pop()))
@@ -225,22 +245,19 @@ def online_attention(query, blocks, *, query_positions, causal=True, window=None
     cache.key_valid.zero_()
     rows = torch.arange(batch, device=device)[:, None]
     for block in blocks:
-        pos = block.offset + torch.arange(_length(block.key), device=device)
+        pos = block.offset - base + torch.arange(_length(block.key), device=device)
+        keep = pos < nb * BLOCK                                     # keys no row can see
+        pos = pos[keep]
         blk = rows * nb + pos[None, :] // BLOCK                     # [B, T]
         slot = (pos % BLOCK).expand(batch, -1)                      # [B, T]
         for side, kv in ((0, block.key), (1, block.value)):
-            codes = kv.values.view(torch.int8).permute(0, 2, 1, 3)  # [B, T, Hkv, D]
+            codes = kv.values.view(torch.int8)[:, :, keep].permute(0, 2, 1, 3)  # [B, T, Hkv, D]
             cache.codes[blk, 0, side, :, slot, :] = codes
-            cache.scales[blk, 0, side, :, slot] = kv.scales[..., 0].permute(0, 2, 1).float()
+            cache.scales[blk, 0, side, :, slot] = kv.scales[:, :, keep, 0].permute(0, 2, 1).float()
         real = (torch.ones_like(blk, dtype=torch.uint8) if block.padding is None
-                else block.padding.to(torch.uint8))
+                else block.padding[:, keep].to(torch.uint8))
         cache.key_valid[blk, slot] = real
 
-    # one decode row per query token: its context ends at its position (causal), or
-    # holds every slot; a padded query sees nothing and comes out zero
-    ctx = (positions + 1) if causal else torch.full_like(positions, nb * BLOCK)
-    if query_padding is not None:
-        ctx = torch.where(query_padding, ctx, torch.zeros_like(ctx))
     ctx = ctx.reshape(-1).to(torch.int32).contiguous()
     tables = (rows * nb + torch.arange(nb, device=device)[None, :]).to(torch.int32)
     tables = tables.repeat_interleave(queries, dim=0).contiguous()  # [B * Q, nb]

@@ -329,6 +329,26 @@ class PagedAttentionRunner:
             torch.cuda.synchronize(self.device)
 
     def forward_batch(self, sequences, chunks, *, return_all_logits=False, padding_masks=None):
+        return self._forward(sequences, chunks, return_all_logits=return_all_logits,
+                             padding_masks=padding_masks)
+
+    def forward_feature_batch(self, sequences, chunks, *, hidden_state_indices):
+        """``ModelRunner.forward_feature_batch`` (src/aster/inference/runner.py:72-83,
+        124-134, 143-145) through the paged step: every row's logits for all chunk
+        tokens (CPU fp32) with the concatenation, along the hidden axis, of the
+        requested hidden states (index i < num_layers: the input of layer i, index 0
+        the embeddings; index num_layers: the final normed output, as the reference
+        decoder's ``output_hidden_states`` lists them, models/decoder.py:153-172), on
+        the model's device. An index past the last state raises the reference's
+        ``StateError`` and nothing is appended."""
+        if not hidden_state_indices or any(type(i) is not int or i < 0
+                                           for i in hidden_state_indices):
+            raise ValueError("Explicit nonnegative hidden-state indices are required")
+        return self._forward(sequences, chunks, return_all_logits=True,
+                             hidden_state_indices=tuple(hidden_state_indices))
+
+    def _forward(self, sequences, chunks, *, return_all_logits, padding_masks=None,
+                 hidden_state_indices=None):
         if not sequences or len(sequences) != len(chunks) or \
                 len({id(value) for value in sequences}) != len(sequences):
             raise ValueError("Need a nonempty batch of distinct sequences and aligned chunks")
@@ -362,7 +382,10 @@ class PagedAttentionRunner:
                 self._synchronize()
                 started = time.monotonic()
                 hidden = self.model.model.embed_tokens(ids)
+                states = []  # each layer's input, then the normed output (hidden states)
                 for index, layer in enumerate(layers):
+                    if hidden_state_indices is not None:
+                        states.append(hidden)
                     normalized = layer.input_layernorm(hidden)
                     attention = layer.self_attn
 
@@ -382,7 +405,14 @@ class PagedAttentionRunner:
                                            scale=attention.scale, window=attention.window)
                     hidden = hidden + attention.o_proj(attended.reshape(batch, count, -1))
                     hidden = hidden + layer.mlp(layer.post_attention_layernorm(hidden))
-                logits = self.model.lm_head(self.model.model.norm(hidden))
+                normed = self.model.model.norm(hidden)
+                logits = self.model.lm_head(normed)
+                features = None
+                if hidden_state_indices is not None:
+                    states.append(normed)
+                    if max(hidden_state_indices) >= len(states):
+                        raise StateError("TokenPredictor did not return aligned target features")
+                    features = torch.cat([states[i] for i in hidden_state_indices], -1)
                 step.commit()  # waits for the device, raises flagged errors, publishes
             except BaseException:
                 step.abort()
@@ -390,11 +420,10 @@ class PagedAttentionRunner:
             self.model_execution_seconds += time.monotonic() - started
             self.forward_calls += 1
             self.input_tokens_computed += ids.numel()
-        return [(row if return_all_logits else row[-1]).detach().float().cpu() for row in logits]
-
-    def forward_feature_batch(self, sequences, chunks, *, hidden_state_indices):
-        raise UnsupportedAttentionBackend("the hip_int8_paged runner serves logits only; hidden-"
-                                          "state features need the reference's ModelRunner")
+        rows = [(row if return_all_logits else row[-1]).detach().float().cpu() for row in logits]
+        if features is not None:
+            return [(row, feature.detach()) for row, feature in zip(rows, features)]
+        return rows
 
     def decode(self, token_ids):
         if self.tokenizer is None:

@@ -297,7 +297,8 @@ int astr_kv_copy_blocks(const void* src, int64_t src_stride, const int32_t* src_
  * (NaN propagates), weights exp(m - M) for finite m and 0 otherwise (M replaced by 0
  * when it is not finite), mass and weighted numerator summed under those weights.
  *   *_max, *_mass: [rows] contiguous; *_weighted: [rows, width] contiguous, device
- *   memory. The outputs may alias either input (elementwise).
+ *   memory. The outputs must not overlap any input or each other (ASTR_EINVAL): the
+ *   threads of a row read both maxima while one of them writes the merged maximum.
  */
 int astr_merge_softmax_f32(const float* left_max, const float* left_mass,
                            const float* left_weighted, const float* right_max,

@@ -203,3 +203,23 @@ def test_prefix_pack_argument_errors_need_no_device():
     assert shared(num_packs=100, rows=4) == _native.ASTR_EUNSUPPORTED  # 400 pack rows > 256
     assert shared(window=8) == _native.ASTR_EUNSUPPORTED
     assert "window" in _native.last_error()
+
+
+def test_merge_softmax_rejects_overlapping_outputs_without_launching():
+    """Outputs that overlap an input or each other are refused before any launch: the
+    threads of a row read both maxima while one of them writes the merged maximum."""
+    f = _native.lib().astr_merge_softmax_f32
+    rows, width = 4, 512
+    row_b, wide_b = rows * 4, rows * width * 4
+    base = 1 << 20  # fake device addresses: nothing is dereferenced on these paths
+    lm, ll, ln = base, base + 4096, base + 8192
+    rm, rl, rn = base + 16384, base + 20480, base + 65536
+    om, ol, on = base + 131072, base + 135168, base + 139264
+    assert wide_b <= 16384
+    ins = (lm, ll, ln, rm, rl, rn)
+    assert f(*ins, lm, ol, on, rows, width, None) == _native.ASTR_EINVAL  # max over left max
+    assert "overlap" in _native.last_error()
+    assert f(*ins, om, ol, rn, rows, width, None) == _native.ASTR_EINVAL  # numerator in place
+    assert f(*ins, om, ol, ln + wide_b - 4, rows, width, None) == _native.ASTR_EINVAL  # partial
+    assert f(*ins, om, om + row_b - 4, on, rows, width, None) == _native.ASTR_EINVAL  # out/out
+    assert f(*ins, om, ol, on, 0, width, None) == 0  # no rows: nothing to launch

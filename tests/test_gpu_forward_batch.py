@@ -100,7 +100,9 @@ class OracleLoop:
         rows = [(key, start, count) for key in keys]
         pads = None if padding is None else [np.asarray(p, bool) for p in padding]
         attended = []
+        self.states = []  # each layer's input, then the normed output
         for index, layer in enumerate(self.model.model.layers):
+            self.states.append(hidden)
             attention = layer.self_attn
             normalized = layer.input_layernorm(hidden)
 
@@ -119,7 +121,9 @@ class OracleLoop:
             result = torch.from_numpy(out).reshape(batch, count, -1)
             hidden = hidden + attention.o_proj(result)
             hidden = hidden + layer.mlp(layer.post_attention_layernorm(hidden))
-        logits = self.model.lm_head(self.model.model.norm(hidden))
+        normed = self.model.model.norm(hidden)
+        self.states.append(normed)
+        logits = self.model.lm_head(normed)
         return logits, attended
 
 
@@ -256,3 +260,45 @@ def test_forward_batch_argument_checks_and_rollback(device):
     with pytest.raises(UnsupportedAttentionBackend):
         PagedAttentionRunner(model, policy_artifact_id="p", backend="hip_int8_paged",
                              block_size=32)
+
+
+def test_forward_feature_batch_returns_the_requested_hidden_states(device):
+    """forward_feature_batch (src/aster/inference/runner.py:72-83, 124-145): every row's
+    logits for all chunk tokens with the requested hidden states concatenated along the
+    hidden axis (index 0 the embeddings, i the input of layer i, num_layers the normed
+    output), against the oracle's row loop; an index past the last state raises the
+    reference's StateError and appends nothing."""
+    model = LlamaLike(seed=5).to(device)
+    runner = PagedAttentionRunner(model, policy_artifact_id="f", backend="hip_int8_paged",
+                                  max_blocks=32)
+    recorder = Recorder(runner.model)
+    oracle = OracleLoop(model)
+    pool = runner.pool
+    rng = np.random.default_rng(6)
+    vocab, hidden = model.config.vocab_size, model.model.embed_tokens.embedding_dim
+    seqs = [pool.create("f") for _ in range(2)]
+    for count, picks in ((19, (0, 1, 2)), (1, (2,)), (4, (1, 0))):
+        start = seqs[0].length
+        chunks = _tokens(rng, vocab, 2, count)
+        recorder.begin()
+        got = runner.forward_feature_batch(seqs, chunks, hidden_state_indices=picks)
+        calls = recorder.calls[-1]
+        shared = {i: (_pack(c["k"]), _pack(c["v"].reshape(2, count, 2, 64).transpose(1, 2)))
+                  for i, c in calls.items()}
+        want, _ = oracle.forward(["a", "b"], start, chunks, shared_kv=shared)
+        expect = torch.cat([oracle.states[i] for i in picks], -1)
+        assert len(got) == 2
+        for row, (logits, feature) in enumerate(got):
+            assert logits.shape == (count, vocab) and logits.device.type == "cpu"
+            assert feature.shape == (count, hidden * len(picks))
+            assert feature.device == torch.device(device)
+            assert_attention_close(logits, want[row])
+            assert_attention_close(feature, expect[row])
+    length = seqs[0].length
+    with pytest.raises(StateError, match="aligned target features"):
+        runner.forward_feature_batch(seqs, _tokens(rng, vocab, 2, 1), hidden_state_indices=(3,))
+    assert seqs[0].length == seqs[1].length == length
+    with pytest.raises(ValueError, match="nonnegative"):
+        runner.forward_feature_batch(seqs, _tokens(rng, vocab, 2, 1), hidden_state_indices=(-1,))
+    with pytest.raises(ValueError, match="nonnegative"):
+        runner.forward_feature_batch(seqs, _tokens(rng, vocab, 2, 1), hidden_state_indices=())

@@ -145,3 +145,15 @@ def test_merge_softmax(device, width):
     with pytest.raises(ValueError, match="same queries"):
         bad, _ = _state(rng, (2, 3, 4, 6), width, device)
         aster_amd.merge_softmax(left, bad)
+
+
+@pytest.mark.parametrize("causal,window", [(True, None), (True, 24), (False, None)])
+def test_pages_at_large_offsets(device, causal, window):
+    """Pages around position 1e5 (and a second group near 1e5 + 4000): the transient
+    arena spans the keys, not their absolute offsets. Queries before every key, between
+    the groups and past the last key, with and without a window."""
+    spans = ((100000, 20), (100024, 33), (100057, 7), (104000, 40))
+    positions = [[5, 100010, 100040, 100063, 102000, 104039, 104100, 200000],
+                 [99999, 100000, 100030, 100064, 104000, 104020, 104063, 104070]]
+    _run(device, spans=spans, queries=8, positions=positions, causal=causal, window=window,
+         seed=31)
