@@ -258,13 +258,171 @@ def _check_model(model):
     return len(layers), hkv, dim
 
 
+def bind_hip_backend(runner, model, *, policy_artifact_id, backend=BACKEND, tokenizer=None,
+                     block_size=16, max_blocks=256, query_block_size=32, key_block_size=None,
+                     chat_template=None, attention_fallback=None, kv_quantization=None,
+                     partition_tokens=0):
+    """Make ``runner`` a ``hip_int8_paged`` runner: the attributes the reference's
+    ``PagedAttentionRunner.__init__`` sets (paged_attention.py:26-95 with
+    ``ModelRunner.__init__``, runner.py:16-46), with this library's arena-backed pool.
+    ``runner`` may be an instance of any class: the reference's own
+    ``PagedAttentionRunner`` calls this from its constructor for
+    ``backend="hip_int8_paged"``, so that callers which gate on the
+    reference's class (``MultiLoRARunner``, adapters.py:47-50) accept it, and its
+    ``forward_batch``/``forward_feature_batch`` then call :func:`hip_forward` /
+    :func:`hip_forward_features` on it. The model is deep-copied once, as the
+    reference does; everything later reads ``runner.model``, so module swaps on it
+    (LoRA adapters) are seen by the step."""
+    if backend != BACKEND:
+        raise ValueError(f"Select explicit backend={BACKEND!r}")
+    if attention_fallback is not None:
+        raise ValueError("The hip_int8_paged backend takes no fallback: a configuration "
+                         "it has no kernel for raises UnsupportedAttentionBackend")
+    kv_quantization = KVQuantization("int8") if kv_quantization is None else kv_quantization
+    if not isinstance(kv_quantization, KVQuantization):
+        raise ValueError("An explicit immutable KVQuantization profile is required")
+    key_block_size = 64 if key_block_size is None else key_block_size
+    if any(type(v) is not int or v < 1 for v in (query_block_size, key_block_size)):
+        raise ValueError("Attention tile sizes must be positive integers")
+    if not isinstance(policy_artifact_id, str) or not policy_artifact_id:
+        raise ValueError("An immutable policy identity is mandatory")
+    runner.num_layers, runner.num_kv_heads, runner.head_dim = _check_model(model)
+    shared = getattr(model, "_aster_shared_runtime_handles", ())
+    runner.model = copy.deepcopy(model, {id(item): item for item in shared}).eval()
+    runner.model.requires_grad_(False)
+    runner.policy_artifact_id = policy_artifact_id
+    runner.codec = KVStateCodec(kind="gqa_kv")
+    runner.pool = PagedStatePool(block_size=block_size, max_blocks=max_blocks, codec=runner.codec,
+                                 quantization=kv_quantization)
+    runner.tokenizer, runner.chat_template = tokenizer, chat_template
+    runner.device = next(runner.model.parameters(), torch.empty(0)).device
+    runner.query_block_size, runner.key_block_size = query_block_size, key_block_size
+    runner.backend = BACKEND
+    runner.attention_fallback = None
+    runner.partition_tokens = partition_tokens
+    runner.attention_work = KernelWork(backend=BACKEND)
+    runner.input_tokens_computed = 0
+    runner.forward_calls = 0
+    runner.model_execution_seconds = 0.0
+    return runner
+
+
+def _synchronize(device):
+    if device.type == "cuda":
+        torch.cuda.synchronize(device)
+
+
+def hip_forward(runner, sequences, chunks, *, return_all_logits=False, padding_masks=None,
+                hidden_state_indices=None):
+    """``PagedAttentionRunner.forward_batch`` (paged_attention.py:110-230) on a runner set
+    up by :func:`bind_hip_backend`: the reference's argument checks and model walk, with
+    every layer's attention as one ``PagedAttentionStep`` launch pair. With
+    ``hidden_state_indices`` (see :func:`hip_forward_features`) every row's result is
+    ``(logits, features)``."""
+    if not sequences or len(sequences) != len(chunks) or \
+            len({id(value) for value in sequences}) != len(sequences):
+        raise ValueError("Need a nonempty batch of distinct sequences and aligned chunks")
+    starts, counts = {s.length for s in sequences}, {len(chunk) for chunk in chunks}
+    if len(starts) != 1 or len(counts) != 1 or min(counts) < 1:
+        raise ValueError("Scheduler must group matching cached/chunk lengths")
+    if len({s.identity for s in sequences}) != 1:
+        raise StateError("A projection batch cannot cross cache security domains")
+    model = runner.model
+    config = model.config
+    start, count, batch = next(iter(starts)), next(iter(counts)), len(sequences)
+    if start + count > config.max_position_embeddings:
+        raise ValueError("Sequence exceeds declared position support")
+    if any(type(t) is not int or not 0 <= t < config.vocab_size for c in chunks for t in c):
+        raise ValueError("Input token outside this immutable model vocabulary")
+    device = runner.device
+    ids = torch.tensor(chunks, device=device, dtype=torch.long)
+    positions = torch.arange(start, start + count, device=device).expand(batch, -1)
+    padding = None
+    if padding_masks is not None:
+        padding = torch.as_tensor(padding_masks).cpu()
+        if padding.shape != ids.shape or not ((padding == 0) | (padding == 1)).all():
+            raise ValueError("Chunk padding must be a binary batch-by-token matrix")
+        padding = padding.bool()
+    pool = runner.pool
+    pool.bind_layout(num_layers=runner.num_layers, num_kv_heads=runner.num_kv_heads,
+                     head_dim=runner.head_dim, device=device)
+    layers = model.model.layers
+    with torch.inference_mode():
+        step = PagedAttentionStep(pool, sequences, [count] * batch, padding=padding,
+                                  work=runner.attention_work,
+                                  partition_tokens=runner.partition_tokens)
+        try:
+            _synchronize(device)
+            started = time.monotonic()
+            hidden = model.model.embed_tokens(ids)
+            states = []  # each layer's input, then the normed output (hidden states)
+            for index, layer in enumerate(layers):
+                if hidden_state_indices is not None:
+                    states.append(hidden)
+                normalized = layer.input_layernorm(hidden)
+                attention = layer.self_attn
+
+                def split(value, heads):
+                    return value.reshape(batch, count, heads, attention.head_dim).transpose(1, 2)
+
+                query = attention.rope(attention.q_norm(
+                    split(attention.q_proj(normalized), attention.num_heads)), positions)
+                key = attention.rope(attention.k_norm(
+                    split(attention.k_proj(normalized), attention.num_kv_heads)), positions)
+                value = split(attention.v_proj(normalized), attention.num_kv_heads)
+                if index == 0:  # the appended leaves' layout (state.py:285-300)
+                    with pool._lock:
+                        pool._lock_signature((runner.num_layers, runner.num_kv_heads,
+                                              runner.head_dim, key.dtype))
+                attended = step.attend(index, _packed(query), _packed(key), _packed(value),
+                                       scale=attention.scale, window=attention.window)
+                hidden = hidden + attention.o_proj(attended.reshape(batch, count, -1))
+                hidden = hidden + layer.mlp(layer.post_attention_layernorm(hidden))
+            normed = model.model.norm(hidden)
+            logits = model.lm_head(normed)
+            features = None
+            if hidden_state_indices is not None:
+                states.append(normed)
+                if max(hidden_state_indices) >= len(states):
+                    raise StateError("TokenPredictor did not return aligned target features")
+                features = torch.cat([states[i] for i in hidden_state_indices], -1)
+            step.commit()  # waits for the device, raises flagged errors, publishes
+        except BaseException:
+            step.abort()
+            raise
+        runner.model_execution_seconds += time.monotonic() - started
+        runner.forward_calls += 1
+        runner.input_tokens_computed += ids.numel()
+    rows = [(row if return_all_logits else row[-1]).detach().float().cpu() for row in logits]
+    if features is not None:
+        return [(row, feature.detach()) for row, feature in zip(rows, features)]
+    return rows
+
+
+def hip_forward_features(runner, sequences, chunks, *, hidden_state_indices):
+    """``ModelRunner.forward_feature_batch`` (src/aster/inference/runner.py:72-83,
+    124-134, 143-145) through the paged step: every row's logits for all chunk tokens
+    (CPU fp32) with the concatenation, along the hidden axis, of the requested hidden
+    states (index i < num_layers: the input of layer i, index 0 the embeddings; index
+    num_layers: the final normed output, as the reference decoder's
+    ``output_hidden_states`` lists them, models/decoder.py:153-172), on the model's
+    device. An index past the last state raises the reference's ``StateError`` and
+    nothing is appended."""
+    if not hidden_state_indices or any(type(i) is not int or i < 0 for i in hidden_state_indices):
+        raise ValueError("Explicit nonnegative hidden-state indices are required")
+    return hip_forward(runner, sequences, chunks, return_all_logits=True,
+                       hidden_state_indices=tuple(hidden_state_indices))
+
+
 class PagedAttentionRunner:
     """``PagedAttentionRunner`` (src/aster/inference/paged_attention.py:22-230) on the
     ``hip_int8_paged`` backend, with the reference's constructor and ``forward_batch``
     contract: the model's projections, norms, RoPE and MLP run as they are (PyTorch),
     and every layer's attention over the rows' pages plus the chunk is one
     quantize-append launch and one ragged attention launch on the HIP kernels
-    (``PagedAttentionStep``).
+    (``PagedAttentionStep``). A thin class over :func:`bind_hip_backend`,
+    :func:`hip_forward` and :func:`hip_forward_features`, which the reference's own class
+    calls for ``backend="hip_int8_paged"``.
 
     Kept: the argument checks and exceptions of forward_batch (:110-143), read leases
     held until the device has finished (:144-148, :221), chunk K/V quantized before
@@ -283,39 +441,9 @@ class PagedAttentionRunner:
     backend = BACKEND
     kind = "token_predictor"
 
-    def __init__(self, model, *, policy_artifact_id, backend, tokenizer=None, block_size=16,
-                 max_blocks=256, query_block_size=32, key_block_size=None, chat_template=None,
-                 attention_fallback=None, kv_quantization=None, partition_tokens=0):
-        if backend != BACKEND:
-            raise ValueError(f"Select explicit backend={BACKEND!r}")
-        if attention_fallback is not None:
-            raise ValueError("The hip_int8_paged backend takes no fallback: a configuration "
-                             "it has no kernel for raises UnsupportedAttentionBackend")
-        kv_quantization = KVQuantization("int8") if kv_quantization is None else kv_quantization
-        if not isinstance(kv_quantization, KVQuantization):
-            raise ValueError("An explicit immutable KVQuantization profile is required")
-        key_block_size = 64 if key_block_size is None else key_block_size
-        if any(type(v) is not int or v < 1 for v in (query_block_size, key_block_size)):
-            raise ValueError("Attention tile sizes must be positive integers")
-        if not isinstance(policy_artifact_id, str) or not policy_artifact_id:
-            raise ValueError("An immutable policy identity is mandatory")
-        self.num_layers, self.num_kv_heads, self.head_dim = _check_model(model)
-        runtime = getattr(model, "_aster_shared_runtime_handles", ())
-        self.model = copy.deepcopy(model, {id(item): item for item in runtime}).eval()
-        self.model.requires_grad_(False)
-        self.policy_artifact_id = policy_artifact_id
-        self.codec = KVStateCodec(kind="gqa_kv")
-        self.pool = PagedStatePool(block_size=block_size, max_blocks=max_blocks, codec=self.codec,
-                                   quantization=kv_quantization)
-        self.tokenizer, self.chat_template = tokenizer, chat_template
-        self.device = next(self.model.parameters(), torch.empty(0)).device
-        self.query_block_size, self.key_block_size = query_block_size, key_block_size
-        self.attention_fallback = None
-        self.partition_tokens = partition_tokens
-        self.attention_work = KernelWork(backend=BACKEND)
-        self.input_tokens_computed = 0
-        self.forward_calls = 0
-        self.model_execution_seconds = 0.0
+    def __init__(self, model, *, policy_artifact_id, backend, **kwargs):
+        bind_hip_backend(self, model, policy_artifact_id=policy_artifact_id, backend=backend,
+                         **kwargs)
 
     @classmethod
     def from_artifact(cls, store, artifact_id, *, loader, tokenizer_loader=None, **kwargs):
@@ -324,106 +452,13 @@ class PagedAttentionRunner:
         return cls(loader(artifact.path), policy_artifact_id=artifact.id, tokenizer=tokenizer,
                    **kwargs)
 
-    def _synchronize(self):
-        if self.device.type == "cuda":
-            torch.cuda.synchronize(self.device)
-
     def forward_batch(self, sequences, chunks, *, return_all_logits=False, padding_masks=None):
-        return self._forward(sequences, chunks, return_all_logits=return_all_logits,
-                             padding_masks=padding_masks)
+        return hip_forward(self, sequences, chunks, return_all_logits=return_all_logits,
+                           padding_masks=padding_masks)
 
     def forward_feature_batch(self, sequences, chunks, *, hidden_state_indices):
-        """``ModelRunner.forward_feature_batch`` (src/aster/inference/runner.py:72-83,
-        124-134, 143-145) through the paged step: every row's logits for all chunk
-        tokens (CPU fp32) with the concatenation, along the hidden axis, of the
-        requested hidden states (index i < num_layers: the input of layer i, index 0
-        the embeddings; index num_layers: the final normed output, as the reference
-        decoder's ``output_hidden_states`` lists them, models/decoder.py:153-172), on
-        the model's device. An index past the last state raises the reference's
-        ``StateError`` and nothing is appended."""
-        if not hidden_state_indices or any(type(i) is not int or i < 0
-                                           for i in hidden_state_indices):
-            raise ValueError("Explicit nonnegative hidden-state indices are required")
-        return self._forward(sequences, chunks, return_all_logits=True,
-                             hidden_state_indices=tuple(hidden_state_indices))
-
-    def _forward(self, sequences, chunks, *, return_all_logits, padding_masks=None,
-                 hidden_state_indices=None):
-        if not sequences or len(sequences) != len(chunks) or \
-                len({id(value) for value in sequences}) != len(sequences):
-            raise ValueError("Need a nonempty batch of distinct sequences and aligned chunks")
-        starts, counts = {s.length for s in sequences}, {len(chunk) for chunk in chunks}
-        if len(starts) != 1 or len(counts) != 1 or min(counts) < 1:
-            raise ValueError("Scheduler must group matching cached/chunk lengths")
-        if len({s.identity for s in sequences}) != 1:
-            raise StateError("A projection batch cannot cross cache security domains")
-        config = self.model.config
-        start, count, batch = next(iter(starts)), next(iter(counts)), len(sequences)
-        if start + count > config.max_position_embeddings:
-            raise ValueError("Sequence exceeds declared position support")
-        if any(type(t) is not int or not 0 <= t < config.vocab_size for c in chunks for t in c):
-            raise ValueError("Input token outside this immutable model vocabulary")
-        ids = torch.tensor(chunks, device=self.device, dtype=torch.long)
-        positions = torch.arange(start, start + count, device=self.device).expand(batch, -1)
-        padding = None
-        if padding_masks is not None:
-            padding = torch.as_tensor(padding_masks).cpu()
-            if padding.shape != ids.shape or not ((padding == 0) | (padding == 1)).all():
-                raise ValueError("Chunk padding must be a binary batch-by-token matrix")
-            padding = padding.bool()
-        self.pool.bind_layout(num_layers=self.num_layers, num_kv_heads=self.num_kv_heads,
-                              head_dim=self.head_dim, device=self.device)
-        layers = self.model.model.layers
-        with torch.inference_mode():
-            step = PagedAttentionStep(self.pool, sequences, [count] * batch, padding=padding,
-                                      work=self.attention_work,
-                                      partition_tokens=self.partition_tokens)
-            try:
-                self._synchronize()
-                started = time.monotonic()
-                hidden = self.model.model.embed_tokens(ids)
-                states = []  # each layer's input, then the normed output (hidden states)
-                for index, layer in enumerate(layers):
-                    if hidden_state_indices is not None:
-                        states.append(hidden)
-                    normalized = layer.input_layernorm(hidden)
-                    attention = layer.self_attn
-
-                    def split(value, heads):
-                        return value.reshape(batch, count, heads, attention.head_dim).transpose(1, 2)
-
-                    query = attention.rope(attention.q_norm(
-                        split(attention.q_proj(normalized), attention.num_heads)), positions)
-                    key = attention.rope(attention.k_norm(
-                        split(attention.k_proj(normalized), attention.num_kv_heads)), positions)
-                    value = split(attention.v_proj(normalized), attention.num_kv_heads)
-                    if index == 0:  # the appended leaves' layout (state.py:285-300)
-                        with self.pool._lock:
-                            self.pool._lock_signature((self.num_layers, self.num_kv_heads,
-                                                       self.head_dim, key.dtype))
-                    attended = step.attend(index, _packed(query), _packed(key), _packed(value),
-                                           scale=attention.scale, window=attention.window)
-                    hidden = hidden + attention.o_proj(attended.reshape(batch, count, -1))
-                    hidden = hidden + layer.mlp(layer.post_attention_layernorm(hidden))
-                normed = self.model.model.norm(hidden)
-                logits = self.model.lm_head(normed)
-                features = None
-                if hidden_state_indices is not None:
-                    states.append(normed)
-                    if max(hidden_state_indices) >= len(states):
-                        raise StateError("TokenPredictor did not return aligned target features")
-                    features = torch.cat([states[i] for i in hidden_state_indices], -1)
-                step.commit()  # waits for the device, raises flagged errors, publishes
-            except BaseException:
-                step.abort()
-                raise
-            self.model_execution_seconds += time.monotonic() - started
-            self.forward_calls += 1
-            self.input_tokens_computed += ids.numel()
-        rows = [(row if return_all_logits else row[-1]).detach().float().cpu() for row in logits]
-        if features is not None:
-            return [(row, feature.detach()) for row, feature in zip(rows, features)]
-        return rows
+        return hip_forward_features(self, sequences, chunks,
+                                    hidden_state_indices=hidden_state_indices)
 
     def decode(self, token_ids):
         if self.tokenizer is None:
