@@ -38,6 +38,11 @@ EXPORTED_SYMBOLS = (
     "astr_paged_attention_i8_shared_workspace_bytes",
     "astr_kv_copy_blocks",
     "astr_merge_softmax_f32",
+    "astr_decode_plan_workgroups",
+    "astr_decode_plan_words_bound",
+    "astr_decode_plan",
+    "astr_paged_attention_i8_planned_workspace_bytes",
+    "astr_paged_attention_i8_planned",
     "astr_last_error",
     "astr_version",
 )
@@ -123,6 +128,21 @@ def lib():
         handle.astr_paged_attention_i8_workspace_bytes.restype = c_sz
         handle.astr_paged_attention_i8_shared_workspace_bytes.argtypes = [c_i32] * 7
         handle.astr_paged_attention_i8_shared_workspace_bytes.restype = c_sz
+        i32p = ctypes.POINTER(c_i32)
+        handle.astr_decode_plan_workgroups.argtypes = [c_i32] * 5 + [i32p, i32p]
+        handle.astr_decode_plan_workgroups.restype = ctypes.c_int
+        handle.astr_decode_plan_words_bound.argtypes = [c_i32, c_i32, c_i64, c_i32, c_i32]
+        handle.astr_decode_plan_words_bound.restype = c_i64
+        handle.astr_decode_plan.argtypes = [i32p, c_i32, i32p, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                            i32p, c_i64, c_vp]
+        handle.astr_decode_plan.restype = ctypes.c_int
+        handle.astr_paged_attention_i8_planned_workspace_bytes.argtypes = [c_vp, c_i32, c_i32]
+        handle.astr_paged_attention_i8_planned_workspace_bytes.restype = c_sz
+        handle.astr_paged_attention_i8_planned.argtypes = [
+            desc_p, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i32, ctypes.c_float,
+            c_vp, c_vp, c_vp, c_sz, c_vp, c_vp,
+        ]
+        handle.astr_paged_attention_i8_planned.restype = ctypes.c_int
         handle.astr_last_error.argtypes = []
         handle.astr_last_error.restype = ctypes.c_char_p
         handle.astr_version.argtypes = []

@@ -20,10 +20,11 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_lib")
 OUT = os.path.join(OUT_DIR, "libaster_kv.so")
 SOURCES = ("errors.hip", "kv_quantize.hip", "paged_attention.hip", "decode_partition.hip",
-           "decode_streamk.hip", "prefill.hip", "kv_copy.hip", "softmax_merge.hip")
+           "decode_streamk.hip", "decode_planned.hip", "prefill.hip", "kv_copy.hip",
+           "softmax_merge.hip", "decode_plan.cpp")
 # attention kernels built once per KV code format (int8, FP8 E4M3FN, FP8 E5M2):
 # -DASTR_KF=k selects the format of that object's instantiations
-PER_FORMAT = ("decode_partition.hip", "decode_streamk.hip", "prefill.hip")
+PER_FORMAT = ("decode_partition.hip", "decode_streamk.hip", "decode_planned.hip", "prefill.hip")
 FORMATS = (0, 1, 2)
 
 

@@ -875,6 +875,14 @@ __device__ __forceinline__ void end_piece(float4_t (&acc)[D / 16 + 1], int r) {
   }
 }
 
+// Launch arguments of the planned decode kernel: the attention arguments and the host
+// plan (its int32 words in device memory, sizes and offsets in `info`).
+struct PlanArgs {
+  AttnArgs a;
+  const int32_t* plan;
+  astr_decode_plan_info info;
+};
+
 // Kernel entry points, one translation unit per code format KF (the source built
 // with -DASTR_KF=KF), dispatched on query dtype, head dim and GQA group inside.
 template <int KF> int launch_partitioned_kf(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
@@ -886,11 +894,16 @@ int launch_streamk_plain_kf(const AttnArgs& a, int32_t q_dtype, hipStream_t stre
 // Rows with more than one query token (chunked prefill), one workgroup per
 // (kv head, sequence, tile of query tokens); needs q_start.
 template <int KF> int launch_prefill_kf(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
+// Decode rows on a host plan (decode_planned.hip); with `resident` non-null nothing is
+// launched and the kernel's resident workgroups per CU land there.
+template <int KF>
+int launch_planned_kf(const PlanArgs& p, int32_t q_dtype, hipStream_t stream, int* resident);
 #define ASTR_DECLARE_LAUNCHERS(KF)                                                        \
   template <> int launch_partitioned_kf<KF>(const AttnArgs&, int32_t, hipStream_t);       \
   template <> int launch_streamk_kf<KF>(const AttnArgs&, int32_t, hipStream_t);           \
   template <> int launch_streamk_plain_kf<KF>(const AttnArgs&, int32_t, hipStream_t);     \
-  template <> int launch_prefill_kf<KF>(const AttnArgs&, int32_t, hipStream_t);
+  template <> int launch_prefill_kf<KF>(const AttnArgs&, int32_t, hipStream_t);             \
+  template <> int launch_planned_kf<KF>(const PlanArgs&, int32_t, hipStream_t, int*);
 ASTR_DECLARE_LAUNCHERS(kInt8)
 ASTR_DECLARE_LAUNCHERS(kE4M3)
 ASTR_DECLARE_LAUNCHERS(kE5M2)
@@ -908,6 +921,13 @@ ASTR_BY_FORMAT(launch_partitioned)
 ASTR_BY_FORMAT(launch_streamk)
 ASTR_BY_FORMAT(launch_prefill)
 #undef ASTR_BY_FORMAT
+inline int launch_planned(const PlanArgs& p, int32_t q_dtype, hipStream_t stream, int* resident) {
+  switch (p.a.cache.code_format) {
+    case kInt8: return launch_planned_kf<kInt8>(p, q_dtype, stream, resident);
+    case kE4M3: return launch_planned_kf<kE4M3>(p, q_dtype, stream, resident);
+    default: return launch_planned_kf<kE5M2>(p, q_dtype, stream, resident);
+  }
+}
 
 // Largest batch the stream-K kernel takes (its per-sequence table lives in LDS), the
 // most prefix packs per launch and the largest batch that takes them, and the work

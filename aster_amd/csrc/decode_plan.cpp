@@ -1,0 +1,250 @@
+// Host-side schedule of a decode batch for decode_planned_kernel (decode_planned.hip).
+//
+// The work of a decode step is one item per (sequence, kv head): the row's visible
+// blocks. The planner knows every row's length on the host (the runner built the block
+// tables there) and settles the whole split before the launch, so that no workgroup
+// spends the start of the kernel on it:
+//   * items whose cost passes the per-workgroup share are cut into equal chunks;
+//   * items and chunks go to workgroups longest first, each to the least loaded one
+//     (LPT), one workgroup per resident slot of the GPU (a single round);
+//   * inside a workgroup the items' blocks are laid end to end and cut into one equal
+//     range per wave. Pieces of an item that two or more of the workgroup's waves hold
+//     are merged in that workgroup after its waves finish; chunks of an item that two
+//     or more workgroups hold are merged by the chunk-merge kernel.
+// The cost model is the stream-K kernel's: 50 per block and 135 per row start (a
+// row's query load and the partial it writes when it ends).
+//
+// Plan layout (int32 words, offsets in astr_decode_plan_info):
+//   workgroups  [num_workgroups][waves + 3]: first item, end item, then waves + 1 bounds
+//               of the workgroup's block list: wave w streams its blocks [bound[w],
+//               bound[w + 1]) (positions counted from the workgroup's first block)
+//   items       [num_items][8]: sequence, kv head, first block within the sequence's
+//               block table, blocks, context length, output (-1: the output row, else
+//               the chunk slot of its partial), position of its first block in the
+//               workgroup's list, offset of its first block id in `ids`
+//   ids         [num_ids]: the physical ids of every sequence's visible blocks, once per
+//               sequence (the items of its kv heads and chunks point into them)
+//   chunked     [num_chunked][4]: sequence, kv head, first chunk slot, chunks
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <functional>
+#include <queue>
+#include <vector>
+
+#include "aster_kv.h"
+
+namespace astr {
+int fail(int code, const char* fmt, ...);
+
+namespace plan {
+
+constexpr int kBlockTokens = 16;
+constexpr int64_t kBlockCost = 50, kRowCost = 135;
+constexpr int kItemWords = 8, kChunkedWords = 4;
+constexpr int kMaxItemsPerWorkgroup = 64;  // the kernel's LDS item table
+constexpr int kMaxBlocksPerWave = 1024;    // the kernel's block list windows
+
+struct Unit {
+  int seq, kvh, blk_begin, nblk, ctx, out, ids_off;
+  int64_t cost;
+};
+
+int64_t words_for(int64_t workgroups, int waves, int64_t items, int64_t ids, int64_t chunked) {
+  return workgroups * (waves + 3) + items * kItemWords + ids + chunked * kChunkedWords;
+}
+
+}  // namespace plan
+}  // namespace astr
+
+using namespace astr::plan;
+
+extern "C" int64_t astr_decode_plan_words_bound(int32_t num_seqs, int32_t num_kv_heads,
+                                                int64_t visible_blocks, int32_t num_workgroups,
+                                                int32_t waves_per_workgroup) {
+  if (num_seqs < 0 || num_kv_heads < 1 || visible_blocks < 0 || num_workgroups < 1 ||
+      waves_per_workgroup < 1)
+    return 0;
+  // every item may be cut into at most num_workgroups chunks, and no more chunks exist
+  // than blocks
+  const int64_t rows = (int64_t)num_seqs * num_kv_heads;
+  const int64_t items = rows + std::min<int64_t>(visible_blocks * num_kv_heads,
+                                                 rows * (int64_t)num_workgroups);
+  return words_for(num_workgroups, waves_per_workgroup, items, visible_blocks, rows);
+}
+
+extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table_stride,
+                                const int32_t* context_lens, int32_t num_seqs,
+                                int32_t num_kv_heads, int32_t window, int32_t num_workgroups,
+                                int32_t waves_per_workgroup, int32_t* plan, int64_t plan_words,
+                                astr_decode_plan_info* info) {
+  using astr::fail;
+  if (info == nullptr || (num_seqs > 0 && (block_tables == nullptr || context_lens == nullptr)))
+    return fail(ASTR_EINVAL, "plan: block_tables, context_lens and info are required");
+  if (num_seqs < 0 || num_kv_heads < 1 || block_table_stride < 0 || window < 0 ||
+      num_workgroups < 1 || waves_per_workgroup < 1 || waves_per_workgroup > 16)
+    return fail(ASTR_EINVAL, "plan: invalid sizes");
+  std::memset(info, 0, sizeof(*info));
+  const int NW = waves_per_workgroup;
+  // ---- rows: visible blocks of every sequence (the kernels' row_span)
+  std::vector<Unit> units;
+  std::vector<int64_t> row_ids(num_seqs);  // offset of sequence s's visible ids
+  int64_t total_cost = 0, visible = 0;
+  for (int s = 0; s < num_seqs; ++s) {
+    const int ctx = context_lens[s];
+    if (ctx < 0 || (int64_t)ctx > (int64_t)block_table_stride * kBlockTokens)
+      return fail(ASTR_EINVAL, "plan: context length %d of sequence %d outside its block table",
+                  ctx, s);
+    const int kv_begin = (window > 0 && ctx > window) ? ctx - window : 0;
+    const int first = kv_begin / kBlockTokens, last = (ctx + kBlockTokens - 1) / kBlockTokens;
+    const int nb = last - first;
+    row_ids[s] = visible;
+    visible += nb;
+    for (int h = 0; h < num_kv_heads; ++h) {
+      const int64_t cost = nb > 0 ? kBlockCost * nb + kRowCost : 0;
+      units.push_back(Unit{s, h, first, nb, ctx, -1, (int)row_ids[s], cost});
+      total_cost += cost;
+    }
+  }
+  if (visible > INT32_MAX / 2) return fail(ASTR_EUNSUPPORTED, "plan: batch too large");
+  // ---- chunks: an item costing more than the per-workgroup share is cut evenly
+  const double share = (double)total_cost / num_workgroups;
+  std::vector<Unit> work;
+  std::vector<int32_t> chunked;  // [seq, kvh, first slot, chunks]
+  int chunk_slots = 0;
+  for (const Unit& u : units) {
+    int k = 1;
+    if (u.nblk > 1 && (double)u.cost > share) {
+      k = (int)std::ceil((double)u.cost / share);
+      k = std::min(k, u.nblk);
+    }
+    if (k == 1) {
+      work.push_back(u);
+      continue;
+    }
+    chunked.insert(chunked.end(), {u.seq, u.kvh, chunk_slots, k});
+    for (int c = 0; c < k; ++c) {
+      const int b0 = (int)((int64_t)u.nblk * c / k), b1 = (int)((int64_t)u.nblk * (c + 1) / k);
+      Unit part = u;
+      part.blk_begin = u.blk_begin + b0;
+      part.nblk = b1 - b0;
+      part.ids_off = u.ids_off + b0;
+      part.out = chunk_slots + c;
+      part.cost = kBlockCost * part.nblk + kRowCost;
+      work.push_back(part);
+    }
+    chunk_slots += k;
+  }
+  // ---- LPT: longest first onto the least loaded workgroup (ties: lowest index)
+  std::vector<int> order(work.size());
+  for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int x, int y) { return work[x].cost > work[y].cost; });
+  typedef std::pair<int64_t, int> Load;  // (cost, workgroup)
+  std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+  for (int g = 0; g < num_workgroups; ++g) heap.push(Load{0, g});
+  std::vector<std::vector<int>> members(num_workgroups);
+  for (int i : order) {
+    Load top = heap.top();
+    heap.pop();
+    members[top.second].push_back(i);
+    top.first += work[i].cost;
+    heap.push(top);
+  }
+  // ---- sizes and layout
+  const int64_t num_items = (int64_t)work.size();
+  int64_t num_blocks = 0;
+  for (const Unit& u : work) num_blocks += u.nblk;
+  const int64_t num_chunked = (int64_t)chunked.size() / kChunkedWords;
+  const int64_t need = words_for(num_workgroups, NW, num_items, visible, num_chunked);
+  if (num_items > INT32_MAX / kItemWords || num_blocks > INT32_MAX / 4)
+    return fail(ASTR_EUNSUPPORTED, "plan: batch too large");
+  for (int g = 0; g < num_workgroups; ++g)
+    if ((int)members[g].size() > kMaxItemsPerWorkgroup)
+      return fail(ASTR_EUNSUPPORTED, "plan: %zu items on one workgroup (at most %d)",
+                  members[g].size(), kMaxItemsPerWorkgroup);
+  info->num_workgroups = num_workgroups;
+  info->waves_per_workgroup = NW;
+  info->num_items = (int32_t)num_items;
+  info->num_blocks = (int32_t)num_blocks;
+  info->num_ids = (int32_t)visible;
+  info->num_chunks = chunk_slots;
+  info->num_chunked = (int32_t)num_chunked;
+  info->num_seqs = num_seqs;
+  info->num_kv_heads = num_kv_heads;
+  info->window = window;
+  info->off_workgroups = 0;
+  info->off_items = (int64_t)num_workgroups * (NW + 3);
+  info->off_ids = info->off_items + num_items * kItemWords;
+  info->off_chunked = info->off_ids + visible;
+  info->plan_words = need;
+  if (plan == nullptr) return 0;  // sizing call
+  if (plan_words < need)
+    return fail(ASTR_EINVAL, "plan: %lld words given, %lld needed", (long long)plan_words,
+                (long long)need);
+  int32_t* wgt = plan + info->off_workgroups;
+  int32_t* items = plan + info->off_items;
+  int32_t* ids = plan + info->off_ids;
+  for (int s = 0; s < num_seqs; ++s) {  // every sequence's visible ids, once
+    const int ctx = context_lens[s];
+    const int kv_begin = (window > 0 && ctx > window) ? ctx - window : 0;
+    const int first = kv_begin / kBlockTokens, last = (ctx + kBlockTokens - 1) / kBlockTokens;
+    if (last > first)
+      std::memcpy(ids + row_ids[s], block_tables + (int64_t)s * block_table_stride + first,
+                  (size_t)(last - first) * sizeof(int32_t));
+  }
+  int64_t item = 0, most_per_wave = 0;
+  for (int g = 0; g < num_workgroups; ++g) {
+    int32_t* rec = wgt + (int64_t)g * (NW + 3);
+    rec[0] = (int32_t)item;
+    int64_t pos = 0, g_cost = 0;
+    for (int i : members[g]) {
+      const Unit& u = work[i];
+      int32_t* it = items + item * kItemWords;
+      it[0] = u.seq;
+      it[1] = u.kvh;
+      it[2] = u.blk_begin;
+      it[3] = u.nblk;
+      it[4] = u.ctx;
+      it[5] = u.out;
+      it[6] = (int32_t)pos;
+      it[7] = u.ids_off;
+      pos += u.nblk;
+      g_cost += u.cost;
+      ++item;
+    }
+    rec[1] = (int32_t)item;
+    // equal-cost wave ranges: block b of an item starts at the cost of the items before
+    // it, plus a row start, plus b blocks; wave w takes the blocks whose start lies in
+    // [C w / NW, C (w + 1) / NW). Bound w is the first block starting at or after
+    // ceil(C w / NW).
+    int32_t* bound = rec + 2;
+    bound[0] = 0;
+    bound[NW] = (int32_t)pos;
+    size_t k = 0;
+    int64_t k_cost = 0, k_pos = 0;  // cost and position at the start of member k
+    for (int w = 1; w < NW; ++w) {
+      const int64_t target = (g_cost * w + NW - 1) / NW;
+      // skip members whose last block starts before the target
+      while (k < members[g].size()) {
+        const Unit& u = work[members[g][k]];
+        if (u.nblk > 0 && k_cost + kRowCost + kBlockCost * (u.nblk - 1) >= target) break;
+        k_cost += u.cost;
+        k_pos += u.nblk;
+        ++k;
+      }
+      int64_t b = k_pos;
+      if (k < members[g].size()) {
+        const int64_t over = target - k_cost - kRowCost;
+        b += over <= 0 ? 0 : (over + kBlockCost - 1) / kBlockCost;
+      }
+      bound[w] = (int32_t)b;
+    }
+    for (int w = 0; w < NW; ++w) most_per_wave = std::max<int64_t>(most_per_wave, bound[w + 1] - bound[w]);
+  }
+  if (most_per_wave > kMaxBlocksPerWave)
+    return fail(ASTR_EUNSUPPORTED, "plan: %lld blocks on one wave (at most %d): launch more "
+                "workgroups", (long long)most_per_wave, kMaxBlocksPerWave);
+  std::memcpy(plan + info->off_chunked, chunked.data(), chunked.size() * sizeof(int32_t));
+  return 0;
+}

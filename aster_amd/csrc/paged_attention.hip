@@ -450,3 +450,139 @@ extern "C" int astr_paged_attention_i8_noalloc(
                          scale, window, partition_tokens, ws, kNoAllocScratchBytes, err_flag,
                          stream, true);
 }
+
+// ---- decode rows on a host plan (decode_plan.cpp, decode_planned.hip)
+
+namespace {
+
+constexpr int kPlanWavesPerWorkgroup = 8;  // the planned kernel's workgroup
+
+// Partial slots of a plan: two per wave, G per chunk; bytes of their (acc, (m, l)).
+size_t planned_workspace(const astr_decode_plan_info& info, int32_t num_q_heads, int32_t head_dim) {
+  using astr::attn::align256;
+  if (info.num_kv_heads < 1 || num_q_heads % info.num_kv_heads) return 0;
+  const size_t group = (size_t)(num_q_heads / info.num_kv_heads);
+  const size_t slots = ((size_t)info.num_workgroups * info.waves_per_workgroup * 2 +
+                        (size_t)info.num_chunks) * group;
+  return align256(slots * head_dim * sizeof(float)) + align256(slots * 2 * sizeof(float));
+}
+
+}  // namespace
+
+extern "C" int astr_decode_plan_workgroups(int32_t head_dim, int32_t num_q_heads,
+                                           int32_t num_kv_heads, int32_t q_dtype,
+                                           int32_t code_format, int32_t* num_workgroups,
+                                           int32_t* waves_per_workgroup) {
+  using namespace astr;
+  using namespace astr::attn;
+  if (num_workgroups == nullptr || waves_per_workgroup == nullptr || num_kv_heads < 1 ||
+      num_q_heads < 1 || num_q_heads % num_kv_heads)
+    return fail(ASTR_EINVAL, "plan workgroups: invalid arguments");
+  if (code_format != ASTR_KV_INT8 && code_format != ASTR_KV_FP8_E4M3FN &&
+      code_format != ASTR_KV_FP8_E5M2)
+    return fail(ASTR_EUNSUPPORTED, "code format %d", code_format);
+  PlanArgs p{};
+  p.a.cache.head_dim = head_dim;
+  p.a.cache.num_kv_heads = num_kv_heads;
+  p.a.cache.code_format = code_format;
+  p.a.num_q_heads = num_q_heads;
+  int per_cu = 0;
+  const int rc = launch_planned(p, q_dtype, nullptr, &per_cu);
+  if (rc != 0) return rc;
+  *num_workgroups = device_cus() * per_cu;
+  *waves_per_workgroup = kPlanWavesPerWorkgroup;
+  return 0;
+}
+
+extern "C" size_t astr_paged_attention_i8_planned_workspace_bytes(
+    const astr_decode_plan_info* info, int32_t num_q_heads, int32_t head_dim) {
+  if (info == nullptr || head_dim < 1 || num_q_heads < 1) return 0;
+  return planned_workspace(*info, num_q_heads, head_dim);
+}
+
+extern "C" int astr_paged_attention_i8_planned(
+    const astr_paged_kv* cache, const void* query, int32_t q_dtype, int64_t q_token_stride,
+    int64_t q_head_stride, void* out, int64_t out_token_stride, int64_t out_head_stride,
+    const int32_t* context_lens, int32_t num_q_heads, float scale, const int32_t* plan,
+    const astr_decode_plan_info* info, void* workspace, size_t workspace_bytes,
+    int32_t* err_flag, void* stream) {
+  astr::CallRange range("astr_paged_attention_i8_planned");
+  using namespace astr;
+  using namespace astr::attn;
+  if (cache == nullptr || err_flag == nullptr || info == nullptr)
+    return fail(ASTR_EINVAL, "cache descriptor, plan info and err_flag are required");
+  const astr_decode_plan_info& pi = *info;
+  if (pi.num_seqs == 0) return 0;
+  if (pi.num_seqs < 0 || pi.num_workgroups < 1 || pi.waves_per_workgroup != kPlanWavesPerWorkgroup ||
+      pi.num_items < 0 || pi.num_blocks < 0 || pi.num_chunks < 0 || pi.num_chunked < 0 ||
+      pi.window < 0 || pi.tail_blocks < 0 || pi.num_kv_heads != cache->num_kv_heads)
+    return fail(ASTR_EINVAL, "plan info does not describe a plan for this arena");
+  const int64_t wg_words = (int64_t)pi.num_workgroups * (pi.waves_per_workgroup + 3);
+  const bool layout =
+      pi.off_workgroups == 0 && pi.off_items == wg_words && pi.num_ids >= 0 &&
+      pi.off_ids == pi.off_items + (int64_t)pi.num_items * 8 &&
+      pi.off_chunked == pi.off_ids + pi.num_ids &&
+      pi.plan_words == pi.off_chunked + (int64_t)pi.num_chunked * 4;
+  if (!layout) return fail(ASTR_EINVAL, "plan info offsets are inconsistent");
+  if (plan == nullptr || (reinterpret_cast<uintptr_t>(plan) & 3u) != 0)
+    return fail(ASTR_EINVAL, "a 4-byte aligned device plan is required");
+  if (query == nullptr || out == nullptr || context_lens == nullptr)
+    return fail(ASTR_EINVAL, "query, out and context_lens are required");
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(ASTR_EINVAL, "attention scale must be finite and positive");
+  if (cache->block_size != kBlockTokens)
+    return fail(ASTR_EUNSUPPORTED, "block_size %d != 16", cache->block_size);
+  if (cache->code_format != ASTR_KV_INT8 && cache->code_format != ASTR_KV_FP8_E4M3FN &&
+      cache->code_format != ASTR_KV_FP8_E5M2)
+    return fail(ASTR_EUNSUPPORTED, "code format %d", cache->code_format);
+  if (cache->num_kv_heads < 1 || num_q_heads % cache->num_kv_heads != 0)
+    return fail(ASTR_EINVAL, "num_q_heads %d must be a multiple of num_kv_heads %d", num_q_heads,
+                cache->num_kv_heads);
+  if (cache->num_blocks < 1) return fail(ASTR_EINVAL, "cache has no blocks");
+  if (q_dtype != ASTR_F16 && q_dtype != ASTR_BF16)
+    return fail(ASTR_EUNSUPPORTED, "the planned decode takes bf16/fp16 queries");
+  if (!aligned16(query) || !aligned16(out) || (q_token_stride * 2) % 16 ||
+      (q_head_stride * 2) % 16 || (out_token_stride * 2) % 16 || (out_head_stride * 2) % 16)
+    return fail(ASTR_EINVAL, "query/out rows must be 16-byte aligned");
+  if (!aligned16(cache->k_codes) || !aligned16(cache->v_codes) ||
+      cache->code_block_stride % 16 || cache->code_head_stride % 16 ||
+      !aligned16(cache->k_scales) || !aligned16(cache->v_scales) ||
+      cache->scale_block_stride % 4 || cache->scale_head_stride % 4)
+    return fail(ASTR_EINVAL, "cache code and scale blocks must be 16-byte aligned");
+  if (cache->key_valid != nullptr && !aligned16(cache->key_valid))
+    return fail(ASTR_EINVAL, "cache key_valid must be 16-byte aligned");
+  const size_t need = planned_workspace(pi, num_q_heads, cache->head_dim);
+  if (workspace == nullptr || workspace_bytes < need ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(ASTR_EINVAL, "a 256-byte aligned workspace of %zu bytes is required (%zu given)",
+                need, workspace_bytes);
+  const size_t group = (size_t)(num_q_heads / cache->num_kv_heads);
+  const size_t slots = ((size_t)pi.num_workgroups * pi.waves_per_workgroup * 2 +
+                        (size_t)pi.num_chunks) * group;
+  PlanArgs p{};
+  AttnArgs& a = p.a;
+  a.q = query;
+  a.q_tok = q_token_stride;
+  a.q_head = q_head_stride;
+  a.out = out;
+  a.o_tok = out_token_stride;
+  a.o_head = out_head_stride;
+  a.cache = *cache;
+  // the block tables are not read (the plan holds the block ids); bt_stride bounds the
+  // context lengths as the plan's tables did
+  a.bt_stride = INT32_MAX / kBlockTokens;
+  a.context_lens = context_lens;
+  a.num_q_tokens = pi.num_seqs;
+  a.max_q_len = 1;
+  a.num_seqs = pi.num_seqs;
+  a.num_q_heads = num_q_heads;
+  a.qk_scale_log2 = scale * kLog2e;
+  a.window = pi.window;
+  a.ws_o = static_cast<float*>(workspace);
+  a.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                     align256(slots * cache->head_dim * sizeof(float)));
+  a.err_flag = err_flag;
+  p.plan = plan;
+  p.info = pi;
+  return launch_planned(p, q_dtype, static_cast<hipStream_t>(stream), nullptr);
+}

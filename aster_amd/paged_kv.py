@@ -27,6 +27,7 @@ with one launch over all rows.
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -286,8 +287,10 @@ class PagedKVCache:
     def workspace(self, num_seqs, num_q_heads, max_context_len,
                   partition_tokens=DEFAULT_PARTITION_TOKENS, prefix_packs=None):
         """Split-K scratch owned by this cache, grown on demand (None when unneeded)."""
-        need = self.workspace_bytes(num_seqs, num_q_heads, max_context_len, partition_tokens,
-                                    prefix_packs)
+        return self._scratch(self.workspace_bytes(num_seqs, num_q_heads, max_context_len,
+                                                  partition_tokens, prefix_packs))
+
+    def _scratch(self, need):
         if not need:
             return None
         if self._workspace is None or self._workspace.numel() < need:
@@ -297,7 +300,8 @@ class PagedKVCache:
     def paged_attention(self, layer, query, block_tables, context_lens, *, max_context_len,
                         scale=None, window=None, partition_tokens=DEFAULT_PARTITION_TOKENS,
                         query_start_loc=None, max_query_len=None, causal=True,
-                        out=None, workspace=None, work=None, check=False, prefix_packs=None):
+                        out=None, workspace=None, work=None, check=False, prefix_packs=None,
+                        decode_plan=None):
         """Paged attention of this layer's arena for every row of a step.
 
         Decode (``query_start_loc=None``): one query token per sequence, ``query``
@@ -321,7 +325,12 @@ class PagedKVCache:
         ``prefix_packs`` (decode, automatic split, no window): a
         ``prefix_plan.plan_prefix_packs`` plan of the same block tables; rows of a
         pack read their shared prefix blocks once for the whole pack. Same outputs
-        as without it."""
+        as without it.
+
+        ``decode_plan`` (decode, bf16/fp16 queries): a ``decode_plan.plan_decode``
+        schedule of the same block tables and lengths (and window); the planned kernel
+        streams the blocks the plan names and does not read ``block_tables``. Same
+        outputs as without it."""
         if query.ndim != 3 or query.shape[-1] != self.head_dim or query.device != self.device:
             raise ValueError("query must be [tokens, num_q_heads, head_dim] on the cache device")
         if query.dtype not in _DTYPE_CODES:
@@ -361,17 +370,26 @@ class PagedKVCache:
                                  "without a window")
             if prefix_packs.num_seqs != num_seqs or prefix_packs.table.device != self.device:
                 raise ValueError("prefix packs were planned for other block tables")
+        if decode_plan is not None:
+            if query_start_loc is not None or partition_tokens != 0 or prefix_packs is not None:
+                raise ValueError("a decode plan serves decode batches under the automatic "
+                                 "split, without prefix packs")
+            if (decode_plan.num_seqs != num_seqs or decode_plan.num_q_heads != num_q_heads
+                    or decode_plan.head_dim != self.head_dim or decode_plan.window != window
+                    or decode_plan.info.num_kv_heads != self.num_kv_heads
+                    or decode_plan.words.device != self.device):
+                raise ValueError("the decode plan was built for another batch")
         if out is None:
             out = torch.empty_like(query)
         elif (not isinstance(out, torch.Tensor) or out.shape != query.shape
               or out.dtype != query.dtype or out.device != self.device or out.stride(-1) != 1):
             raise ValueError("out must match the query's shape, dtype and device, with "
                              "contiguous rows")
-        need = self.workspace_bytes(num_seqs, num_q_heads, max_context_len, partition_tokens,
-                                    prefix_packs)
+        need = (decode_plan.workspace_bytes() if decode_plan is not None else
+                self.workspace_bytes(num_seqs, num_q_heads, max_context_len, partition_tokens,
+                                     prefix_packs))
         if need and workspace is None:
-            workspace = self.workspace(num_seqs, num_q_heads, max_context_len, partition_tokens,
-                                       prefix_packs)
+            workspace = self._scratch(need)
         elif need:
             if (not isinstance(workspace, torch.Tensor) or workspace.dtype != torch.uint8
                     or workspace.device != self.device or not workspace.is_contiguous()):
@@ -381,7 +399,13 @@ class PagedKVCache:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         ws = workspace.data_ptr() if need else None
         lib = _native.lib()
-        if prefix_packs is not None:
+        if decode_plan is not None:
+            rc = lib.astr_paged_attention_i8_planned(
+                self._descs[layer], query.data_ptr(), _DTYPE_CODES[query.dtype], query.stride(0),
+                query.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
+                context_lens.data_ptr(), num_q_heads, scale, decode_plan.words.data_ptr(),
+                ctypes.byref(decode_plan.info), ws, need, self.err_flag.data_ptr(), stream)
+        elif prefix_packs is not None:
             rc = lib.astr_paged_attention_i8_shared(
                 self._descs[layer], query.data_ptr(), _DTYPE_CODES[query.dtype], query.stride(0),
                 query.stride(1), out.data_ptr(), out.stride(0), out.stride(1),

@@ -12,8 +12,9 @@
       launches of one kernel, e.g. bench.py's prefill-only calls in a mixed step).
   python -m aster_amd.profiling durations <rocprof_dir> [kernel_substring]
       The same statistics of kernel durations (us) from ``*_kernel_trace.csv``.
-  python -m aster_amd.profiling timeline [config2|config4|config5] [--packs]
-      Per-wave timeline of the stream-K decode kernel on a BASELINE workload, from
+  python -m aster_amd.profiling timeline [config2|config4|config5] [--packs | --planned [--tail N]]
+      Per-wave timeline of the stream-K (or, --planned, the planned) decode kernel on a
+      BASELINE workload, from
       the trace build (``python -m aster_amd.build --trace``, which records wall-clock
       marks per wave): when waves start, have their block ids and first block, and
       end, per XCC and by the number of pieces (rows) a wave streams, and what a row
@@ -22,7 +23,7 @@
       HBM bytes per launch per kernel (median dispatch) from a FETCH_SIZE and a
       WRITE_SIZE run, each scaled by what the counter reads for ``copy`` (the
       ``cal_*`` runs): the figures of profiles/decode_traffic.json.
-  python -m aster_amd.profiling calls [config] [--packs] [--q-dtype T] [--calls N]
+  python -m aster_amd.profiling calls [config] [--packs] [--q-dtype T] [--calls N] [--planned]
       N paged_attention calls of a BASELINE decode workload (four layer arenas,
       cycled), with the workload's queries cast to T: the program to run under
       rocprofv3 for a kernel bench.py does not time (float32 queries run the exact
@@ -109,7 +110,7 @@ def traffic(fetch_dir, write_dir, cal_fetch_dir, cal_write_dir, pattern="astr", 
             "calibration": {"fetch_scale": round(fs, 7), "write_scale": round(ws, 7)}}
 
 
-def _decode_calls(config, packs, q_dtype, calls):
+def _decode_calls(config, packs, q_dtype, calls, planned=False, tail=None):
     """Run ``calls`` paged_attention calls of a BASELINE decode workload over four layer
     arenas, cycled, so that a call does not find the previous call's K/V in the
     memory-side cache (as bench.py does). ``q_dtype`` overrides the workload's query
@@ -135,11 +136,76 @@ def _decode_calls(config, packs, q_dtype, calls):
         q = q.to(getattr(torch, q_dtype))
     plan = (plan_prefix_packs(w.block_tables, w.context_lens, w.num_q_heads, w.num_kv_heads,
                               device=dev) if packs else None)
+    schedule = None
+    if planned:
+        from .decode_plan import DEFAULT_TAIL_BLOCKS, plan_decode
+
+        schedule = plan_decode(w.block_tables, w.context_lens, num_q_heads=w.num_q_heads,
+                               num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
+                               q_dtype=q.dtype, device=dev,
+                               tail_blocks=DEFAULT_TAIL_BLOCKS if tail is None else tail)
+        plan = None
     for i in range(calls):
         cache.paged_attention(i % layers, q, tables, lens, max_context_len=w.max_context_len,
-                              scale=w.scale, prefix_packs=plan)
+                              scale=w.scale, prefix_packs=plan, decode_plan=schedule)
     torch.cuda.synchronize()
-    print(f"{calls} calls of {config} (packs={bool(packs)}, queries {q.dtype})", flush=True)
+    print(f"{calls} calls of {config} (packs={bool(packs)}, planned={bool(planned)}, "
+          f"queries {q.dtype})", flush=True)
+
+
+def planned_timeline(config="config2", calls=7, tail=None):
+    """The trace build's per-wave marks of the planned decode kernel (the last of
+    ``calls`` planned calls over ``config``), as a report dict (us from the first wave's
+    start): startup to items checked, block ids, first block; streaming end; the
+    workgroup barrier; exit after the workgroup's merges."""
+    import ctypes
+    import contextlib
+    import io
+
+    import numpy as np
+
+    from . import _native, build
+
+    _native.LIB_PATH = build.TRACE_OUT
+    _native._lib = None
+    lib = _native.lib()
+    lib.astr_trace_read_planned.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+    with contextlib.redirect_stdout(io.StringIO()):
+        _decode_calls(config, False, None, calls, planned=True, tail=tail)
+    n = 16384
+    marks = np.zeros((n, 8), np.int64)
+    info = np.zeros((n, 4), np.int32)
+    rc = lib.astr_trace_read_planned(marks.ctypes.data, info.ctypes.data, n)
+    if rc != 0:
+        raise RuntimeError(f"astr_trace_read_planned failed ({rc})")
+    live = marks[:, 0] != 0
+    wave_ids = np.nonzero(live)[0]
+    marks, info = marks[live], info[live]
+    t = (marks - marks[:, 0].min()) / 100.0
+    nblk, pieces, items, xcc = info.T
+    pct = lambda x, p: [round(float(v), 2) for v in np.percentile(x, p)]
+    streaming = nblk > 0
+    wg = wave_ids // 8
+    wg_end = np.array([t[wg == g, 4].max() for g in np.unique(wg)])
+    rep = {"config": config, "waves": int(live.sum()), "span_us": round(float(t[:, 6].max()), 2),
+           "start_us": pct(t[:, 0], [0, 50, 100]),
+           "items_checked_us": pct(t[:, 1] - t[:, 0], [50, 90]),
+           "ids_us": pct(t[:, 2] - t[:, 0], [50, 90]),
+           "first_block_us": pct(t[streaming, 3] - t[streaming, 0], [50, 90]),
+           "stream_end_pct_10_50_90_99_100_us": pct(t[:, 4], [10, 50, 90, 99, 100]),
+           "workgroup_stream_end_pct_10_50_90_100_us": pct(wg_end, [10, 50, 90, 100]),
+           "barrier_wait_us": pct(t[:, 5] - t[:, 4], [50, 90]),
+           "merge_us": pct(t[:, 6] - t[:, 5], [50, 90, 100]),
+           "exit_pct_50_90_100_us": pct(t[:, 6], [50, 90, 100]),
+           "blocks_per_wave": pct(nblk, [0, 50, 100]),
+           "items_per_workgroup": pct(items, [0, 50, 100]),
+           "us_per_block": round(float(((t[streaming, 4] - t[streaming, 3]) /
+                                        np.maximum(nblk[streaming], 1)).mean()), 3)}
+    rep["per_xcc"] = {int(x): {"waves": int((xcc == x).sum()),
+                               "mean_end": round(float(t[xcc == x, 4].mean()), 2),
+                               "max_end": round(float(t[xcc == x, 4].max()), 2)}
+                      for x in np.unique(xcc)}
+    return rep
 
 
 def timeline(config="config2", packs=False, calls=7):
@@ -219,11 +285,15 @@ def main():
     t = sub.add_parser("timeline")
     t.add_argument("config", nargs="?", default="config2")
     t.add_argument("--packs", action="store_true")
+    t.add_argument("--planned", action="store_true")
+    t.add_argument("--tail", type=int, default=None)
     d = sub.add_parser("calls")
     d.add_argument("config", nargs="?", default="config2")
     d.add_argument("--packs", action="store_true")
     d.add_argument("--q-dtype", default=None, choices=["float32", "float16", "bfloat16"])
     d.add_argument("--calls", type=int, default=50)
+    d.add_argument("--planned", action="store_true")
+    d.add_argument("--tail", type=int, default=None)
     h = sub.add_parser("traffic")
     for name in ("fetch_dir", "write_dir", "cal_fetch_dir", "cal_write_dir"):
         h.add_argument(name)
@@ -239,12 +309,14 @@ def main():
                                  args.cal_write_dir, args.pattern), indent=1))
         return
     if args.cmd == "calls":
-        _decode_calls(args.config, args.packs, args.q_dtype, args.calls)
+        _decode_calls(args.config, args.packs, args.q_dtype, args.calls, args.planned, args.tail)
         return
     if args.cmd == "timeline":
         import json
 
-        print(json.dumps(timeline(args.config, args.packs), indent=1))
+        rep = (planned_timeline(args.config, tail=args.tail) if args.planned else
+               timeline(args.config, args.packs))
+        print(json.dumps(rep, indent=1))
         return
     table = (summarize if args.cmd == "summarize" else durations)(args.root, args.pattern)
     for (kernel, counter), (n, mean, median, top) in table.items():

@@ -45,6 +45,11 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-runs", type=int, default=5, help="timed CPU steps per thread setting")
     p.add_argument("--no-extra", action="store_true", help="skip the config 3/4/5 measurements")
+    p.add_argument("--no-plan", action="store_true",
+                   help="decode on the unplanned stream-K kernel instead of a host plan")
+    p.add_argument("--tail", type=int, default=None,
+                   help="planned decode: blocks at the end of each wave's range loaded two "
+                        "at a time (default: the library's)")
     p.add_argument("--extra-calls", type=int, default=50)
     p.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
                    help="rocprof-derived HBM bytes per attention launch (optional)")
@@ -149,11 +154,14 @@ def build_arena(w, layers, device, hold_last=False):
     return cache, step_batch
 
 
-def attention_caller(w, cache, q, device, partition, rows=None, packs=False):
+def attention_caller(w, cache, q, device, partition, rows=None, packs=False, planned=False,
+                     tail=None):
     """``call(layer)`` running one attention call over the workload (or over its rows
     ``rows``, a sub-workload of the same arena) and the workload it covers. With
-    ``packs`` a decode batch gets the prefix-pack plan of its block tables, built once
-    on the host as the runner builds it at schedule time (outside the timed calls)."""
+    ``packs`` a decode batch gets the prefix-pack plan of its block tables, and with
+    ``planned`` the host schedule of the planned decode kernel, each built once on the
+    host as the runner builds them once per step for every layer (outside the timed
+    calls; ``call.plan_us`` is the host time of building the schedule)."""
     import numpy as np
     import torch
 
@@ -177,8 +185,22 @@ def attention_caller(w, cache, q, device, partition, rows=None, packs=False):
 
         plan = plan_prefix_packs(w.block_tables, w.context_lens, w.num_q_heads, w.num_kv_heads,
                                  device=device)
-    ws_bytes = cache.workspace_bytes(w.num_seqs, w.num_q_heads, w.max_context_len, partition,
-                                     prefix_packs=plan)
+    decode_plan, plan_us = None, None
+    if planned and not varlen and partition == 0:
+        from aster_amd.decode_plan import DEFAULT_TAIL_BLOCKS, plan_decode
+
+        kw = dict(num_q_heads=w.num_q_heads, num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
+                  q_dtype=w.q_dtype, device=device,
+                  tail_blocks=DEFAULT_TAIL_BLOCKS if tail is None else tail)
+        plan_decode(w.block_tables, w.context_lens, **kw)  # warm the occupancy query
+        t0 = time.perf_counter()
+        for _ in range(20):
+            decode_plan = plan_decode(w.block_tables, w.context_lens, **kw)
+        plan_us = (time.perf_counter() - t0) / 20 * 1e6
+        plan = None
+    ws_bytes = (decode_plan.workspace_bytes() if decode_plan is not None else
+                cache.workspace_bytes(w.num_seqs, w.num_q_heads, w.max_context_len, partition,
+                                      prefix_packs=plan))
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=device)
 
     def call(layer):
@@ -186,8 +208,11 @@ def attention_caller(w, cache, q, device, partition, rows=None, packs=False):
                               scale=w.scale, partition_tokens=partition, out=out, workspace=ws,
                               query_start_loc=qsl,
                               max_query_len=w.max_query_len if varlen else None,
-                              prefix_packs=plan)
+                              prefix_packs=plan, decode_plan=decode_plan)
 
+    call.plan_us = plan_us
+    call.planned = decode_plan is not None
+    call.chunked = decode_plan is not None and decode_plan.info.num_chunked > 0
     return call, w
 
 
@@ -199,7 +224,7 @@ def hbm_entry(w, avg_ms, med_ms, nbytes=None):
             "attended_kv_tokens_per_s": w.attended_tokens / (avg_ms * 1e-3)}
 
 
-def extra_measurements(device, partition, calls):
+def extra_measurements(device, partition, calls, planned=True, tail=None):
     """Configs 3, 4 and 5: one attention call each (two layer arenas, alternated, so
     the calls do not reuse each other's K/V from the MALL), HIP events per launch."""
     import numpy as np
@@ -242,6 +267,9 @@ def extra_measurements(device, partition, calls):
     avg, med = time_calls(call, calls, 2)
     entry = hbm_entry(w, avg, med)
     entry["without_plan_call_us"] = unplanned[0] * 1e3
+    if planned:  # the host schedule of the planned kernel, without prefix packs
+        call, _ = attention_caller(w, cache, q, device, partition, planned=True, tail=tail)
+        entry["planned_call_us"] = time_calls(call, calls, 2)[0] * 1e3
     entry["logical_effective_gbs"] = entry.pop("achieved_gbs")
     entry["logical_frac"] = entry.pop("frac")
     unique = w.unique_kv_bytes() + (w.algorithmic_bytes() - w.attended_tokens * w.num_kv_heads
@@ -252,12 +280,19 @@ def extra_measurements(device, partition, calls):
     out[w.name] = entry
     del cache
     torch.cuda.empty_cache()
-    # config 5
+    # config 5: the planned call (rows cut into chunks across workgroups), the unplanned
+    # stream-K call, and the 512-token split-K partitions the configuration names
     w = wl.config5()
     cache, _ = build_arena(w, 2, device)
     q = wl.queries(w, device)
+    call, _ = attention_caller(w, cache, q, device, partition, planned=planned, tail=tail)
+    entry = hbm_entry(w, *time_calls(call, calls, 2))
+    entry["planned"] = call.planned
     call, _ = attention_caller(w, cache, q, device, partition)
-    out[w.name] = hbm_entry(w, *time_calls(call, calls, 2))
+    entry["streamk"] = hbm_entry(w, *time_calls(call, calls, 2))
+    call, _ = attention_caller(w, cache, q, device, 512)
+    entry["partition_512"] = hbm_entry(w, *time_calls(call, calls, 2))
+    out[w.name] = entry
     del cache
     torch.cuda.empty_cache()
     return out
@@ -278,7 +313,9 @@ def main():
     L = args.layers
     cache, step_batch = build_arena(w, L, device, hold_last=True)
     q = wl.queries(w, device)
-    call, _ = attention_caller(w, cache, q, device, args.partition, packs=True)
+    planned = not args.no_plan
+    call, _ = attention_caller(w, cache, q, device, args.partition, packs=True, planned=planned,
+                               tail=args.tail)
     k_new, v_new, slots = step_batch
     varlen = w.query_lens is not None
 
@@ -311,11 +348,22 @@ def main():
     achieved = alg_bytes / (attn_avg_ms * 1e-3) / 1e9
     # HBM bytes per call measured by rocprofv3 (FETCH_SIZE/WRITE_SIZE, calibrated
     # against a copy of known size) for this workload and split mode
+    # for this workload, split mode and library build: a figure measured on another build
+    # of the library is not reported (traffic then stays null)
     traffic = None
     if os.path.exists(args.traffic):
-        mode = "streamk" if args.partition == 0 else f"partition_{args.partition}"
+        import hashlib
+
+        from aster_amd import _native
+
+        mode = ("planned" if call.planned else "streamk") if args.partition == 0 else \
+            f"partition_{args.partition}"
         with open(args.traffic) as f:
-            traffic = json.load(f).get(w.name, {}).get(mode, {}).get("bytes_per_launch")
+            rec = json.load(f).get(w.name, {}).get(mode, {})
+        with open(_native.LIB_PATH, "rb") as f:
+            built = hashlib.sha256(f.read()).hexdigest()
+        if rec.get("library_sha256") == built:
+            traffic = rec.get("bytes_per_launch")
 
     result = {
         "metric": "attended KV-tokens/s and % of HBM peak, INT8 paged decode, 1xMI355X",
@@ -340,7 +388,9 @@ def main():
         },
         "hbm_fraction_of_step": alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "roofline": {
-            "kernel": ("decode_streamk_kernel + merge_streamk_kernel" if args.partition == 0 else
+            "kernel": ("decode_planned_kernel" + (" + merge_chunks_kernel" if call.chunked else "")
+                       if call.planned else
+                       "decode_streamk_kernel + merge_streamk_kernel" if args.partition == 0 else
                        "decode_mfma_kernel + merge_kernel")
                       + (" + prefill_mfma_kernel" if varlen else "") + " (one paged_attention call)",
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -350,13 +400,20 @@ def main():
         },
         "wall_s_timed_region": wall,
     }
+    if call.planned:
+        # the schedule is built once per decode step on the host and serves every layer
+        result["roofline"]["plan_host_us"] = call.plan_us
+        result["config"]["decode_plan"] = "host schedule (astr_decode_plan), built once per step"
+        plain, _ = attention_caller(w, cache, q, device, args.partition, packs=True)
+        result["roofline"]["unplanned_call_us"] = time_calls(plain, max(args.steps, 50), L)[0] * 1e3
     if varlen:
         result["config"]["query_tokens"] = w.num_query_tokens
         result["config"]["max_query_len"] = w.max_query_len
     if not args.no_extra and args.config == "config2":
         del cache
         torch.cuda.empty_cache()
-        result["extra"] = extra_measurements(device, args.partition, args.extra_calls)
+        result["extra"] = extra_measurements(device, args.partition, args.extra_calls,
+                                               planned=planned, tail=args.tail)
         cache, step_batch = build_arena(w, 1, device, hold_last=True)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, cache, step_batch, q, args.cpu_runs)

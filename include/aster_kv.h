@@ -270,6 +270,91 @@ size_t astr_paged_attention_i8_shared_workspace_bytes(int32_t num_seqs, int32_t 
                                                       int32_t rows_per_pack);
 
 /*
+ * A host-built schedule of a decode batch (astr_decode_plan): sizes and word offsets of
+ * its int32 arrays. The plan itself is copied to device memory by the caller; this
+ * struct stays on the host and is passed by pointer to the planned entry points.
+ */
+typedef struct astr_decode_plan_info {
+  int32_t num_workgroups;       /* grid of the planned launch (one per resident slot) */
+  int32_t waves_per_workgroup;
+  int32_t num_items;            /* (sequence, kv head) rows and row chunks */
+  int32_t num_blocks;           /* blocks the plan streams (over all kv heads) */
+  int32_t num_ids;              /* block ids it holds (each sequence's, once) */
+  int32_t num_chunks;           /* chunk partial slots (rows split across workgroups) */
+  int32_t num_chunked;          /* rows split across workgroups */
+  int32_t num_seqs;
+  int32_t num_kv_heads;
+  int32_t window;
+  int32_t tail_blocks;          /* blocks at the end of each wave's range that it loads
+                                   two at a time (0: one at a time throughout) */
+  int32_t reserved;
+  int64_t off_workgroups, off_items, off_ids, off_chunked;
+  int64_t plan_words;           /* int32 words of the plan */
+} astr_decode_plan_info;
+
+/*
+ * Resident workgroups of the planned decode kernel on the current device (the
+ * num_workgroups to plan for) and its waves per workgroup, for this head dim, GQA
+ * group, query dtype and code format. No reference counterpart: the reference has no
+ * device schedule.
+ */
+int astr_decode_plan_workgroups(int32_t head_dim, int32_t num_q_heads, int32_t num_kv_heads,
+                                int32_t q_dtype, int32_t code_format, int32_t* num_workgroups,
+                                int32_t* waves_per_workgroup);
+
+/* Upper bound of the int32 words of a plan (visible_blocks: sum over sequences). */
+int64_t astr_decode_plan_words_bound(int32_t num_seqs, int32_t num_kv_heads,
+                                     int64_t visible_blocks, int32_t num_workgroups,
+                                     int32_t waves_per_workgroup);
+
+/*
+ * Builds, on the host, the schedule of a decode batch: the same work as
+ * astr_paged_attention_i8 over these HOST block tables and context lengths (the
+ * per-row online_attention calls of PagedAttentionRunner.forward_batch,
+ * paged_attention.py:168-215, as the runner holds the rows' page lists on the host,
+ * state.py:358-390). Each (sequence, kv head) row's visible blocks become an item;
+ * items go to workgroups longest first onto the least loaded (rows costing more than
+ * a workgroup's share are cut into chunks), and each workgroup's blocks are cut into
+ * equal-cost ranges, one per wave. A plan holds the physical block ids, so it is
+ * valid for these tables and lengths only (one plan per decode step serves every
+ * layer). plan == NULL only sizes it (info->plan_words). Host memory only; nothing
+ * is launched.
+ */
+int astr_decode_plan(const int32_t* block_tables, int32_t block_table_stride,
+                     const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
+                     int32_t window, int32_t num_workgroups, int32_t waves_per_workgroup,
+                     int32_t* plan, int64_t plan_words, astr_decode_plan_info* info);
+
+/* Workspace bytes of astr_paged_attention_i8_planned for this plan. */
+size_t astr_paged_attention_i8_planned_workspace_bytes(const astr_decode_plan_info* info,
+                                                       int32_t num_q_heads, int32_t head_dim);
+
+/*
+ * astr_paged_attention_i8 (decode rows, bf16/fp16 queries) on a plan from
+ * astr_decode_plan: no device-side split, and the pieces of a row that several waves
+ * of one workgroup hold are merged by that workgroup after its waves finish, so no
+ * merge kernel runs unless the plan cut a row across workgroups. Same outputs as
+ * astr_paged_attention_i8 on the tables the plan was built from.
+ *   plan: the plan's int32 words in device memory (info->plan_words, 4-byte aligned);
+ *         info: its host record. The plan is untrusted: every index read from it is
+ *         checked (block ids against the arena, items against the batch, context
+ *         lengths against context_lens); a workgroup whose part fails a check writes
+ *         nothing and raises ASTR_FLAG_BAD_INDEX.
+ *   context_lens: int32 [num_seqs] device lengths, which the plan's must equal.
+ *   query/out: [num_seqs, num_q_heads, head_dim], strides in elements (token row s is
+ *         sequence s).
+ *   workspace: >= astr_paged_attention_i8_planned_workspace_bytes(info, ...) bytes,
+ *         256-byte aligned.
+ */
+int astr_paged_attention_i8_planned(const astr_paged_kv* cache, const void* query,
+                                    int32_t q_dtype, int64_t q_token_stride,
+                                    int64_t q_head_stride, void* out, int64_t out_token_stride,
+                                    int64_t out_head_stride, const int32_t* context_lens,
+                                    int32_t num_q_heads, float scale, const int32_t* plan,
+                                    const astr_decode_plan_info* info, void* workspace,
+                                    size_t workspace_bytes, int32_t* err_flag, void* stream);
+
+/*
  * Bit-exact copy of whole blocks: block i of `num_blocks` goes from
  *   src + (src_index ? src_index[i] : i) * src_stride
  * to

@@ -1,0 +1,173 @@
+"""The host planner of the planned decode kernel (astr_decode_plan, C++): on random
+batches its plan covers every visible block of every (sequence, kv head) row exactly
+once with the row's physical ids, cuts only rows costing more than a workgroup's share,
+balances workgroups within one item of the mean (LPT) and waves within one block and
+one row start, and refuses what the kernel cannot take. No GPU: host memory only."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from aster_amd import _native
+from aster_amd.decode_plan import DecodePlanInfo
+
+I32P = ctypes.POINTER(ctypes.c_int32)
+BLOCK_COST, ROW_COST = 50, 135
+
+
+def _plan(tables, lens, hkv, window, wg, nw=8):
+    lib = _native.lib()
+    tables = np.ascontiguousarray(tables, np.int32)
+    lens = np.ascontiguousarray(lens, np.int32)
+    ctx = lens.astype(np.int64)
+    first = np.where((window > 0) & (ctx > window), ctx - window, 0) // 16
+    visible = int(np.maximum(-(-ctx // 16) - first, 0).sum())
+    bound = lib.astr_decode_plan_words_bound(len(lens), hkv, visible, wg, nw)
+    buf = np.zeros(max(bound, 1), np.int32)
+    info = DecodePlanInfo()
+    rc = lib.astr_decode_plan(tables.ctypes.data_as(I32P), tables.shape[1],
+                              lens.ctypes.data_as(I32P), len(lens), hkv, window, wg, nw,
+                              buf.ctypes.data_as(I32P), buf.size, ctypes.byref(info))
+    return rc, info, buf
+
+
+def _batch(rng, seqs, max_ctx, pool_extra=7):
+    lens = rng.integers(0, max_ctx + 1, seqs).astype(np.int32)
+    need = (lens + 15) // 16
+    width = max(int(need.max()), 1)
+    pool = int(need.sum()) + pool_extra
+    perm = rng.permutation(pool).astype(np.int32)
+    tables = np.full((seqs, width), -1, np.int32)
+    cur = 0
+    for s, n in enumerate(need):
+        tables[s, :n] = perm[cur:cur + n]
+        cur += n
+    return tables, lens
+
+
+def _check(tables, lens, hkv, window, wg, nw=8):
+    rc, info, buf = _plan(tables, lens, hkv, window, wg, nw)
+    assert rc == 0, _native.last_error()
+    n_items = info.num_items
+    wgt = buf[info.off_workgroups:info.off_items].reshape(wg, nw + 3)
+    items = buf[info.off_items:info.off_ids].reshape(n_items, 8)
+    ids = buf[info.off_ids:info.off_chunked]
+    chunked = buf[info.off_chunked:info.plan_words].reshape(info.num_chunked, 4)
+    assert info.plan_words == info.off_chunked + 4 * info.num_chunked
+    assert info.num_ids == ids.size
+    # workgroups partition the items in order; each one's list starts at 0
+    assert wgt[0, 0] == 0 and wgt[-1, 1] == n_items
+    assert (wgt[1:, 0] == wgt[:-1, 1]).all()
+    assert (wgt[:, 2] == 0).all()
+    assert (np.diff(wgt[:, 2:], axis=1) >= 0).all()
+    assert int(wgt[:, 2 + nw].sum()) == info.num_blocks
+    # items: laid end to end in their workgroup's list, their ids the rows' ids
+    covered = {}
+    loads = []
+    for g in range(wg):
+        cost, pos = 0, 0
+        for k in range(wgt[g, 0], wgt[g, 1]):
+            seq, kvh, blk0, nb, ctx, out, ipos, off = items[k]
+            assert ctx == lens[seq] and 0 <= kvh < hkv and ipos == pos
+            assert (ids[off:off + nb] == tables[seq, blk0:blk0 + nb]).all()
+            covered.setdefault((seq, kvh), []).append((blk0, nb, out))
+            cost += BLOCK_COST * nb + (ROW_COST if nb else 0)
+            pos += nb
+        assert pos == wgt[g, 2 + nw]
+        loads.append(cost)
+        # waves: equal shares of the workgroup's cost, within one block and a row start
+        starts = []
+        c = 0
+        for k in range(wgt[g, 0], wgt[g, 1]):
+            for b in range(items[k, 3]):
+                c += ROW_COST if b == 0 else 0
+                starts.append(c)
+                c += BLOCK_COST
+        for w in range(nw):
+            lo, hi = wgt[g, 2 + w], wgt[g, 3 + w]
+            if hi > lo:
+                assert starts[lo] >= cost * w / nw - 1e-9
+                assert starts[hi - 1] < cost * (w + 1) / nw
+    # every row covered once; rows in several items are chunked, with consecutive slots
+    chunk_rows = {(int(s), int(h)): (int(c0), int(n)) for s, h, c0, n in chunked}
+    slots = []
+    total = 0
+    for s, ctx in enumerate(lens.tolist()):
+        kv0 = ctx - window if window and ctx > window else 0
+        first, last = kv0 // 16, (ctx + 15) // 16
+        for h in range(hkv):
+            parts = sorted(covered[(s, h)])
+            assert parts[0][0] == first and sum(p[1] for p in parts) == last - first
+            for (a0, an, _), (b0, _, _) in zip(parts, parts[1:]):
+                assert a0 + an == b0
+            if len(parts) == 1:
+                assert parts[0][2] == -1 and (s, h) not in chunk_rows
+            else:
+                c0, n = chunk_rows[(s, h)]
+                assert n == len(parts)
+                assert sorted(p[2] for p in parts) == list(range(c0, c0 + n))
+                slots += list(range(c0, c0 + n))
+            total += BLOCK_COST * (last - first) + (ROW_COST if last > first else 0)
+    assert sorted(slots) == list(range(info.num_chunks))
+    # LPT: no workgroup beyond the mean plus one item (a chunk is at most a share)
+    share = total / wg
+    biggest = max(BLOCK_COST * it[3] + ROW_COST for it in items) if n_items else 0
+    assert max(loads) <= share + biggest + 1e-9
+    return info, loads
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_batches_are_covered_and_balanced(seed):
+    rng = np.random.default_rng(seed)
+    seqs = int(rng.integers(1, 80))
+    tables, lens = _batch(rng, seqs, int(rng.choice([40, 700, 5000])))
+    window = int(rng.choice([0, 0, 100, 1000]))
+    hkv = int(rng.choice([1, 2, 8]))
+    wg = max(int(rng.choice([4, 16, 64])), -(-seqs * hkv // 40))  # <= 64 items per workgroup
+    _check(tables, lens, hkv, window, wg)
+
+
+def test_config2_needs_no_chunks_and_balances():
+    from aster_amd import workloads as wl
+
+    w = wl.config2()
+    info, loads = _check(w.block_tables, w.context_lens, w.num_kv_heads, 0, 256)
+    assert info.num_chunked == 0  # every row fits one workgroup: no merge kernel
+    assert max(loads) / np.mean(loads) < 1.05
+
+
+def test_long_rows_are_cut_into_chunks():
+    from aster_amd import workloads as wl
+
+    w = wl.config5()
+    info, loads = _check(w.block_tables, w.context_lens, w.num_kv_heads, 0, 256)
+    assert info.num_chunked == 16 * 8 and info.num_chunks == 16 * 8 * 2
+    assert max(loads) / np.mean(loads) < 1.01
+
+
+def test_empty_rows_and_single_row():
+    tables = np.arange(8, dtype=np.int32).reshape(2, 4)
+    info, _ = _check(tables, np.array([0, 50], np.int32), 2, 0, 4)
+    assert info.num_items >= 4  # the empty row still has an item per head (zero output)
+    _check(tables[:1], np.array([64], np.int32), 1, 0, 3)
+
+
+def test_refusals():
+    tables = np.zeros((2, 4), np.int32)
+    rc, _, _ = _plan(tables, np.array([65, 3], np.int32), 1, 0, 4)  # 65 > 4 blocks
+    assert rc == _native.ASTR_EINVAL and "outside" in _native.last_error()
+    rc, _, _ = _plan(tables, np.array([-1, 3], np.int32), 1, 0, 4)
+    assert rc == _native.ASTR_EINVAL
+    rc, _, _ = _plan(tables, np.array([3, 3], np.int32), 1, 0, 4, nw=17)
+    assert rc == _native.ASTR_EINVAL
+    # more than 64 items on one workgroup
+    many = np.zeros((130, 1), np.int32)
+    rc, _, _ = _plan(many, np.full(130, 16, np.int32), 1, 0, 2)
+    assert rc == _native.ASTR_EUNSUPPORTED and "items" in _native.last_error()
+    # a sizing call writes nothing and reports the words
+    info = DecodePlanInfo()
+    lens = np.array([33, 3], np.int32)
+    rc = _native.lib().astr_decode_plan(tables.ctypes.data_as(I32P), 4, lens.ctypes.data_as(I32P),
+                                        2, 1, 0, 4, 8, None, 0, ctypes.byref(info))
+    assert rc == 0 and info.plan_words > 0

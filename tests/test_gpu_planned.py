@@ -1,0 +1,149 @@
+"""The planned decode path (a host schedule from astr_decode_plan, the planned kernel,
+workgroup-local merges and the chunk merge) against the oracle's page-by-page online
+softmax (online_attention.py:74-219 via paged_attention.py:168-215) at the north_star
+tolerance, and against the unplanned stream-K call on the full BASELINE workloads;
+plans that disagree with the device lengths or hold bad indices are flagged."""
+
+import numpy as np
+import pytest
+import torch
+
+from aster_amd import KVQuantization, PagedKVCache
+from aster_amd import _native
+from aster_amd import workloads as wl
+from aster_amd.decode_plan import plan_decode
+from tests.gpu_util import assert_attention_close, mark_padding, oracle_decode
+
+pytestmark = pytest.mark.gpu
+
+FORMAT_CODES = {"int8": _native.ASTR_KV_INT8, "fp8_e4m3fn": _native.ASTR_KV_FP8_E4M3FN,
+                "fp8_e5m2": _native.ASTR_KV_FP8_E5M2}
+
+
+def _build(w, device, fmt="int8"):
+    cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=1, num_kv_heads=w.num_kv_heads,
+                         head_dim=w.head_dim, device=device, quantization=KVQuantization(fmt))
+    wl.materialize(w, cache, device=device)
+    tables, lens = wl.device_tables(w, device)
+    return cache, tables, lens
+
+
+def _planned(cache, w, q, tables, lens, *, window=None, fmt="int8", **plan_kw):
+    plan = plan_decode(w.block_tables, w.context_lens, num_q_heads=w.num_q_heads,
+                       num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, q_dtype=w.q_dtype,
+                       device=q.device, code_format=FORMAT_CODES[fmt], window=window, **plan_kw)
+    out = cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                                scale=w.scale, window=window, decode_plan=plan, check=True)
+    return out, plan
+
+
+def _edge_workload(dim, hq, hkv, qdtype, seed=7):
+    lens = np.array([1, 15, 16, 17, 255, 256, 257, 600, 0, 33, 2048, 90], np.int32)
+    rng = np.random.default_rng(dim + hq + seed)
+    tables, pool = wl._tables_from_lengths(lens, rng, spare_blocks=3)
+    return wl.DecodeWorkload("edge", hq, hkv, dim, lens, tables, pool, qdtype, seed, dim ** -0.5)
+
+
+@pytest.mark.parametrize("dim,hq,hkv", [(64, 8, 8), (128, 16, 8), (128, 32, 8), (128, 64, 8),
+                                        (128, 128, 8), (256, 8, 2), (256, 32, 4), (64, 16, 2)])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16])
+def test_head_dims_groups_dtypes(device, dim, hq, hkv, qdtype):
+    w = _edge_workload(dim, hq, hkv, qdtype)
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    out, _ = _planned(cache, w, q, tables, lens)
+    assert (out[8] == 0).all()
+    assert_attention_close(out, oracle_decode(w, cache, q))
+
+
+@pytest.mark.parametrize("workgroups", [2, 3, 7, 40, 150])
+@pytest.mark.parametrize("tail", [0, 3])
+def test_rows_cut_across_workgroups(device, workgroups, tail):
+    """Few workgroups: every long row is cut into chunks that several workgroups
+    stream and the chunk kernel merges; many waves hold empty ranges."""
+    w = _edge_workload(128, 32, 8, torch.bfloat16, seed=workgroups)
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    out, plan = _planned(cache, w, q, tables, lens, num_workgroups=workgroups, tail_blocks=tail)
+    nb = (w.context_lens + 15) // 16
+    cost = 50 * nb + 135 * (nb > 0)
+    share = cost.sum() * w.num_kv_heads / workgroups
+    assert (plan.info.num_chunked > 0) == bool((cost > share).any())
+    assert_attention_close(out, oracle_decode(w, cache, q))
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8_e4m3fn", "fp8_e5m2"])
+@pytest.mark.parametrize("window", [None, 100])
+def test_formats_windows_padding(device, fmt, window):
+    w = _edge_workload(128, 16, 4, torch.bfloat16, seed=3)
+    cache, tables, lens = _build(w, device, fmt)
+    mark_padding(cache, w.block_tables, w.context_lens, 0.2, seed=5, whole_blocks=2)
+    q = wl.queries(w, device)
+    out, _ = _planned(cache, w, q, tables, lens, window=window, fmt=fmt, num_workgroups=9)
+    assert_attention_close(out, oracle_decode(w, cache, q, window=window))
+
+
+def test_large_v_scales_and_extreme_scores(device):
+    from tests.test_gpu_hardening import _assert_within_fp32_rounding
+
+    w = _edge_workload(128, 16, 4, torch.bfloat16, seed=11)
+    cache, tables, lens = _build(w, device)
+    cache.scales[::3, 0, 1] *= 2.0 ** 12
+    q = wl.queries(w, device)
+    out, _ = _planned(cache, w, q, tables, lens, num_workgroups=5)
+    assert_attention_close(out, oracle_decode(w, cache, q), atol=2e-3 * 2.0 ** 12)
+    cache, tables, lens = _build(w, device)
+    cache.scales[:, 0, 0] *= 100.0
+    q = (wl.queries(w, device).float() * 100.0).to(torch.bfloat16)
+    out, _ = _planned(cache, w, q, tables, lens, num_workgroups=5)
+    _assert_within_fp32_rounding(w, cache, q, out)
+
+
+@pytest.mark.parametrize("builder", [wl.config2, wl.config4, wl.config5])
+def test_full_configs_match_the_unplanned_call(device, builder):
+    """BASELINE configs 2, 4 and 5 at full size: the planned call equals the stream-K
+    call within the tolerance on every output, and the oracle on sampled rows."""
+    w = builder()
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    out, plan = _planned(cache, w, q, tables, lens)
+    if builder is wl.config2:
+        assert plan.info.num_chunked == 0
+    if builder is wl.config5:
+        assert plan.info.num_chunked > 0
+    ref = cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                                scale=w.scale, check=True)
+    assert_attention_close(out, ref)
+    rows = np.random.default_rng(0).choice(w.num_seqs, 3, replace=False)
+    sub = wl.DecodeWorkload(w.name, w.num_q_heads, w.num_kv_heads, w.head_dim,
+                            w.context_lens[rows], w.block_tables[rows], w.num_blocks, w.q_dtype,
+                            w.seed, w.scale)
+    assert_attention_close(out[torch.as_tensor(rows, device=device)],
+                           oracle_decode(sub, cache, q[torch.as_tensor(rows, device=device)]))
+
+
+def test_plans_that_contradict_the_call_are_flagged(device):
+    w = _edge_workload(128, 32, 8, torch.bfloat16, seed=21)
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    plan = plan_decode(w.block_tables, w.context_lens, num_q_heads=32, num_kv_heads=8,
+                       head_dim=128, q_dtype=torch.bfloat16, device=device, num_workgroups=6)
+    kw = dict(max_context_len=w.max_context_len, scale=w.scale, decode_plan=plan, check=True)
+    # device lengths other than the plan's
+    other = lens.clone()
+    other[4] += 1
+    with pytest.raises(ValueError):
+        cache.paged_attention(0, q, tables, other, **kw)
+    # a block id beyond the arena and an item naming a sequence past the batch
+    info = plan.info
+    for offset, value in ((info.off_ids + 3, w.num_blocks + 5), (info.off_items, 10 ** 6)):
+        words = plan.words.clone()
+        plan.words[offset] = value
+        with pytest.raises(ValueError):
+            cache.paged_attention(0, q, tables, lens, **kw)
+        plan.words.copy_(words)
+    out = cache.paged_attention(0, q, tables, lens, **kw)  # the intact plan still serves
+    assert_attention_close(out, oracle_decode(w, cache, q))
+    with pytest.raises(ValueError, match="another batch"):
+        cache.paged_attention(0, q[:5], tables[:5], lens[:5], max_context_len=w.max_context_len,
+                              decode_plan=plan)
