@@ -401,6 +401,16 @@ struct QueryColumn {  // the lane's 16 elements of each 64-wide d chunk, as load
   uint4 w[D / 64][16 * sizeof(QT) / 16];
 };
 
+// The lane's part of one query column (qp: its first element, 16 * qg past the row's).
+template <typename QT, int D>
+__device__ __forceinline__ void load_query_column(const QT* qp, QueryColumn<QT, D>& raw) {
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int c = 0; c < (int)(16 * sizeof(QT) / 16); ++c)
+      raw.w[h][c] = reinterpret_cast<const uint4*>(qp + 64 * h)[c];
+}
+
 // Int8 B-operands of one query column for the QK MFMAs (lane r of its 16-lane group
 // qg holds d = 16*qg + 64*h + [0, 16)): the column is quantized once to integers
 // Q = 128 * hi + lo within 1/2 of q * kQRange / max|q|, hi and lo in int8, so that
@@ -613,6 +623,22 @@ __device__ __forceinline__ float qk_operand(const QueryRaw<D>& q, bool gvalid, f
     return query_column_i8<QT, D, 3>(col, gvalid, qk_scale_log2, op.hi, op.lo, op.lo2);
   } else {
     return query_operand<QT, D>(q, gvalid, qk_scale_log2, op.op) * code_scale<KF>();
+  }
+}
+
+// The same operand from a QueryColumn of any query type: int8 codes only for fp32
+// queries (their three int8 terms keep ~22 bits of each element; an f16 query for the
+// FP8 formats would keep 11).
+template <typename QT, int D, int KF>
+__device__ __forceinline__ float qk_operand_column(const QueryColumn<QT, D>& col, bool gvalid,
+                                                   float qk_scale_log2, QkOperand<D, KF>& op) {
+  if constexpr (KF == kInt8) {
+    return query_column_i8<QT, D, 3>(col, gvalid, qk_scale_log2, op.hi, op.lo, op.lo2);
+  } else {
+    static_assert(sizeof(QT) == 2, "FP8 codes take 16-bit queries on the MFMA path");
+    return query_operand<QT, D>(reinterpret_cast<const QueryRaw<D>&>(col), gvalid,
+                                qk_scale_log2, op.op) *
+           code_scale<KF>();
   }
 }
 
@@ -852,13 +878,13 @@ __device__ __forceinline__ void store_lane_f32(float* dst, const float4_t (&acc)
 template <typename QT, int D>
 __device__ __forceinline__ void store_lane_out(QT* dst, const float4_t (&acc)[D / 16 + 1],
                                                float scale) {
-  static_assert(sizeof(QT) == 2, "16-bit outputs");
   constexpr int VB = D / 16;
+  constexpr int kVec = 16 / (int)sizeof(QT);  // elements per 16-byte store
 #pragma unroll
-  for (int t = 0; t < D / 4; t += 8) {
-    QT v[8];
+  for (int t = 0; t < D / 4; t += kVec) {
+    QT v[kVec];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = from_float<QT>(acc[(t + u) % VB][(t + u) / VB] * scale);
+    for (int u = 0; u < kVec; ++u) v[u] = from_float<QT>(acc[(t + u) % VB][(t + u) / VB] * scale);
     *reinterpret_cast<uint4*>(dst + t) = *reinterpret_cast<const uint4*>(v);
   }
 }

@@ -18,7 +18,9 @@
 //   workgroups  [num_workgroups][waves + 3]: first item, end item, then waves + 1 bounds
 //               of the workgroup's block list: wave w streams its blocks [bound[w],
 //               bound[w + 1]) (positions counted from the workgroup's first block)
-//   items       [num_items][8]: sequence, kv head, first block within the sequence's
+//   items       [num_workgroups][item_stride][8] (workgroup g's items at g * item_stride,
+//               so a workgroup loads them without its record): sequence, kv head, first
+//               block within the sequence's
 //               block table, blocks, context length, output (-1: the output row, else
 //               the chunk slot of its partial), position of its first block in the
 //               workgroup's list, offset of its first block id in `ids`
@@ -67,9 +69,9 @@ extern "C" int64_t astr_decode_plan_words_bound(int32_t num_seqs, int32_t num_kv
     return 0;
   // every item may be cut into at most num_workgroups chunks, and no more chunks exist
   // than blocks
+  // items: at most kMaxItemsPerWorkgroup per workgroup, at a common stride
   const int64_t rows = (int64_t)num_seqs * num_kv_heads;
-  const int64_t items = rows + std::min<int64_t>(visible_blocks * num_kv_heads,
-                                                 rows * (int64_t)num_workgroups);
+  const int64_t items = (int64_t)num_workgroups * kMaxItemsPerWorkgroup;
   return words_for(num_workgroups, waves_per_workgroup, items, visible_blocks, rows);
 }
 
@@ -152,7 +154,9 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
     heap.push(top);
   }
   // ---- sizes and layout
-  const int64_t num_items = (int64_t)work.size();
+  int64_t stride = 1;  // items of the fullest workgroup
+  for (int g = 0; g < num_workgroups; ++g) stride = std::max<int64_t>(stride, (int64_t)members[g].size());
+  const int64_t num_items = stride * num_workgroups;
   int64_t num_blocks = 0;
   for (const Unit& u : work) num_blocks += u.nblk;
   const int64_t num_chunked = (int64_t)chunked.size() / kChunkedWords;
@@ -166,6 +170,7 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
   info->num_workgroups = num_workgroups;
   info->waves_per_workgroup = NW;
   info->num_items = (int32_t)num_items;
+  info->item_stride = (int32_t)stride;
   info->num_blocks = (int32_t)num_blocks;
   info->num_ids = (int32_t)visible;
   info->num_chunks = chunk_slots;
@@ -185,6 +190,7 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
   int32_t* wgt = plan + info->off_workgroups;
   int32_t* items = plan + info->off_items;
   int32_t* ids = plan + info->off_ids;
+  std::memset(items, 0, (size_t)num_items * kItemWords * sizeof(int32_t));
   for (int s = 0; s < num_seqs; ++s) {  // every sequence's visible ids, once
     const int ctx = context_lens[s];
     const int kv_begin = (window > 0 && ctx > window) ? ctx - window : 0;
@@ -193,9 +199,10 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
       std::memcpy(ids + row_ids[s], block_tables + (int64_t)s * block_table_stride + first,
                   (size_t)(last - first) * sizeof(int32_t));
   }
-  int64_t item = 0, most_per_wave = 0;
+  int64_t most_per_wave = 0;
   for (int g = 0; g < num_workgroups; ++g) {
     int32_t* rec = wgt + (int64_t)g * (NW + 3);
+    int64_t item = g * stride;
     rec[0] = (int32_t)item;
     int64_t pos = 0, g_cost = 0;
     for (int i : members[g]) {

@@ -89,9 +89,17 @@ struct Partial {
 // one row with the merge_softmax rule in base 2, and writes the normalised row to
 // `orow` (head h at orow + h * o_head), or, when orow is null, the merged partial to
 // workspace slot `dest`. One wave; lane L takes elements [L E, L E + E) of the G x D
-// floats, of head L E / D. Pieces with maximum -inf weigh 0 (a row with no visible key
-// has l = 0 and acc = 0 in every piece, and comes out 0).
-template <typename QT, int D, int G, typename SrcOf>
+// floats, of head L E / D. Pieces go in groups of MAXK whose loads are all issued
+// together; between groups the running (M, L, O) is rescaled to the new maximum.
+// Pieces with maximum -inf weigh 0 (a row with no visible key has l = 0 and acc = 0 in
+// every piece, and comes out 0).
+// Pieces merge_pieces loads at once: up to a wave's share of 64 floats per lane.
+template <int D, int G>
+constexpr int merge_group() {
+  return 64 / (G * D / kWave) < 1 ? 1 : 64 / (G * D / kWave) > 8 ? 8 : 64 / (G * D / kWave);
+}
+
+template <typename QT, int D, int G, int MAXK, typename SrcOf>
 __device__ __forceinline__ void merge_pieces(const AttnArgs& a, SrcOf src_of, int count,
                                              QT* orow, int64_t dest, int lane) {
   constexpr int E = G * D / kWave;
@@ -99,26 +107,45 @@ __device__ __forceinline__ void merge_pieces(const AttnArgs& a, SrcOf src_of, in
   constexpr int V = E >= 4 ? 4 : E;
   typedef float vec_t __attribute__((ext_vector_type(V)));
   const int h = lane * E / D, d0 = lane * E % D;
-  float M = -INFINITY;
-  for (int k = 0; k < count; ++k) {
-    const Partial pk = src_of(k);
-    if (pk.o != nullptr) M = fmaxf(M, pk.ml[2 * h]);
-  }
-  float L = 0.f, O[E];
+  float M = -INFINITY, L = 0.f, O[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) O[e] = 0.f;
-  for (int k = 0; k < count; ++k) {
-    const Partial pk = src_of(k);
-    if (pk.o == nullptr) continue;
-    const float mp = pk.ml[2 * h], lp = pk.ml[2 * h + 1];
-    const float w = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
-    L += lp * w;
-    const float* src = pk.o + h * D + d0;
+  for (int k0 = 0; k0 < count; k0 += MAXK) {
+    const float* po[MAXK];
+    float mp[MAXK], lp[MAXK];
+#pragma unroll
+    for (int j = 0; j < MAXK; ++j) {
+      const Partial pk = k0 + j < count ? src_of(k0 + j) : Partial{nullptr, nullptr};
+      po[j] = pk.o == nullptr ? nullptr : pk.o + h * D + d0;
+      mp[j] = pk.o == nullptr ? -INFINITY : pk.ml[2 * h];
+      lp[j] = pk.o == nullptr ? 0.f : pk.ml[2 * h + 1];
+    }
+    float Mn = M;
+#pragma unroll
+    for (int j = 0; j < MAXK; ++j) Mn = fmaxf(Mn, mp[j]);
+    if (Mn != M) {  // the running merge moves to the new maximum
+      const float f = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+      L *= f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) O[e] *= f;
+      M = Mn;
+    }
+    float w[MAXK];
+#pragma unroll
+    for (int j = 0; j < MAXK; ++j) {
+      w[j] = mp[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp[j] - M);
+      L += lp[j] * w[j];
+    }
 #pragma unroll
     for (int e = 0; e < E; e += V) {
-      const vec_t x = *reinterpret_cast<const vec_t*>(src + e);
+      vec_t x[MAXK];
 #pragma unroll
-      for (int c = 0; c < V; ++c) O[e + c] = fmaf(x[c], w, O[e + c]);
+      for (int j = 0; j < MAXK; ++j)
+        x[j] = po[j] == nullptr ? vec_t{} : *reinterpret_cast<const vec_t*>(po[j] + e);
+#pragma unroll
+      for (int j = 0; j < MAXK; ++j)
+#pragma unroll
+        for (int c = 0; c < V; ++c) O[e + c] = fmaf(x[j][c], w[j], O[e + c]);
     }
   }
   if (orow == nullptr) {
@@ -141,11 +168,12 @@ __device__ __forceinline__ void merge_pieces(const AttnArgs& a, SrcOf src_of, in
 #pragma unroll
   for (int e = 0; e < E; ++e) r[e] = from_float<QT>(O[e] * inv);
   QT* o = orow + (int64_t)h * a.o_head + d0;
-  if constexpr (E % 8 == 0) {
+  constexpr int kVec = 16 / (int)sizeof(QT);  // elements per 16-byte store
+  if constexpr (E % kVec == 0) {
 #pragma unroll
-    for (int e = 0; e < E; e += 8)
+    for (int e = 0; e < E; e += kVec)
       *reinterpret_cast<uint4*>(o + e) = *reinterpret_cast<const uint4*>(r + e);
-  } else if constexpr (E == 4) {
+  } else if constexpr (E * sizeof(QT) == 8) {
     *reinterpret_cast<uint2*>(o) = *reinterpret_cast<const uint2*>(r);
   } else {
 #pragma unroll
@@ -186,35 +214,37 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
   const int hkv = a.cache.num_kv_heads;
   const int32_t* const ids_tab = p.plan + p.info.off_ids;
 
-  // ---- 1. the workgroup's record and items into LDS, every index checked
+  // ---- 1. the workgroup's record and items (at a fixed stride, loaded together) into
+  // LDS, every index checked
   if (threadIdx.x == 0) s_bad = 0;
   if (threadIdx.x < NW + 3)
     s_rec[threadIdx.x] = p.plan[p.info.off_workgroups + (int64_t)g * (NW + 3) + threadIdx.x];
-  __syncthreads();
-  const int ib = s_rec[0], ie = s_rec[1];
-  const int total = s_rec[2 + NW];  // blocks of the workgroup's list
-  bool bad = !(0 <= ib && ib <= ie && ie <= p.info.num_items && ie - ib <= kMaxItems &&
-               s_rec[2] == 0 && total <= p.info.num_blocks);
-  if (threadIdx.x < NW)  // wave bounds: non-decreasing
-    bad |= s_rec[3 + threadIdx.x] < s_rec[2 + threadIdx.x];
-  const int ni = ie - ib;
+  const int stride = p.info.item_stride;  // checked on the host: 1..kMaxItems
   Item mine{};
-  if (!bad && (int)threadIdx.x < ni) {
-    const int32_t* src = p.plan + p.info.off_items + (int64_t)(ib + threadIdx.x) * kItemWords;
+  if ((int)threadIdx.x < stride) {
+    const int32_t* src = p.plan + p.info.off_items + ((int64_t)g * stride + threadIdx.x) * kItemWords;
     int v[kItemWords];
 #pragma unroll
     for (int k = 0; k < kItemWords; ++k) v[k] = src[k];
     mine = Item{v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
-    const bool ok = mine.seq >= 0 && mine.seq < a.num_seqs && mine.kvh >= 0 && mine.kvh < hkv &&
-                    mine.nblk >= 0 && mine.blk0 >= 0 && mine.pos >= 0 &&
-                    (int64_t)mine.pos + mine.nblk <= total && mine.ids_off >= 0 &&
-                    (int64_t)mine.ids_off + mine.nblk <= p.info.num_ids && mine.ctx >= 0 &&
-                    mine.out >= -1 && mine.out < p.info.num_chunks;
 #pragma unroll
     for (int k = 0; k < kItemWords; ++k) s_item[threadIdx.x * kItemWords + k] = v[k];
     s_pos[threadIdx.x] = mine.pos;
-    bad |= !ok;
   }
+  __syncthreads();
+  const int ib = s_rec[0], ie = s_rec[1];
+  const int total = s_rec[2 + NW];  // blocks of the workgroup's list
+  bool bad = !(ib == g * stride && ib <= ie && ie - ib <= stride && s_rec[2] == 0 &&
+               total <= p.info.num_blocks);
+  if (threadIdx.x < NW)  // wave bounds: non-decreasing
+    bad |= s_rec[3 + threadIdx.x] < s_rec[2 + threadIdx.x];
+  const int ni = ie - ib;
+  if (!bad && (int)threadIdx.x < ni)
+    bad = !(mine.seq >= 0 && mine.seq < a.num_seqs && mine.kvh >= 0 && mine.kvh < hkv &&
+            mine.nblk >= 0 && mine.blk0 >= 0 && mine.pos >= 0 &&
+            (int64_t)mine.pos + mine.nblk <= total && mine.ids_off >= 0 &&
+            (int64_t)mine.ids_off + mine.nblk <= p.info.num_ids && mine.ctx >= 0 &&
+            mine.out >= -1 && mine.out < p.info.num_chunks);
   if (bad) s_bad = 1;
   __syncthreads();
   if (s_bad) {
@@ -310,21 +340,29 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
 
   // The first item's query rows go by direct-to-LDS loads into the last stage, issued
   // before blocks 0 .. NS-2, so the block stream starts without waiting for them.
-  QueryRaw<D> qr;
+  // fp32 queries (int8 codes) load into registers before the first blocks are issued.
+  QueryColumn<QT, D> qr;
   QkOperand<D, KF> qop;
   float cf = 0.f;
   const bool valid = r < G;
   if (nblk > 0) {
     const Item it0 = item_at(s_item, __builtin_amdgcn_readfirstlane(rows));
-    stage_query<QT, D, G>(a, it0.seq, it0.kvh, lane, stage(NS - 1));
-    const int first = min(NS - 1, nblk);
-    for (int j = 0; j < first; ++j) issue(j);
-    if (first == 3) wait_vmcnt<3 * S::kLoads>();  // the query has landed
-    else if (first == 2) wait_vmcnt<2 * S::kLoads>();
-    else wait_vmcnt<S::kLoads>();
-    lds_query<QT, D>(stage(NS - 1), r < G ? r : 0, qg, qr);
-    cf = qk_operand<QT, D, KF>(qr, valid, a.qk_scale_log2, qop);
-    if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (their values are consumed)
+    if constexpr (sizeof(QT) == 2) {
+      stage_query<QT, D, G>(a, it0.seq, it0.kvh, lane, stage(NS - 1));
+      const int first = min(NS - 1, nblk);
+      for (int j = 0; j < first; ++j) issue(j);
+      if (first == 3) wait_vmcnt<3 * S::kLoads>();  // the query has landed
+      else if (first == 2) wait_vmcnt<2 * S::kLoads>();
+      else wait_vmcnt<S::kLoads>();
+      lds_query<QT, D>(stage(NS - 1), r < G ? r : 0, qg, reinterpret_cast<QueryRaw<D>&>(qr));
+      cf = qk_operand_column<QT, D, KF>(qr, valid, a.qk_scale_log2, qop);
+      if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (values consumed)
+    } else {
+      load_query_column<QT, D>(column_ptr(it0), qr);
+      cf = qk_operand_column<QT, D, KF>(qr, valid, a.qk_scale_log2, qop);
+      const int first = min(NS, nblk);
+      for (int j = 0; j < first; ++j) issue(j);
+    }
     if (64 < nblk) request_ids(1);
   }
 
@@ -350,8 +388,8 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
     const Item it = item_at(s_item, crid);
     const RowSpan psp = row_span(a, it.ctx);
     if (i > 0) {  // a new item starts inside this wave's range
-      load_query_at<QT, D>(column_ptr(it), qr);
-      cf = qk_operand<QT, D, KF>(qr, valid, a.qk_scale_log2, qop);
+      load_query_column<QT, D>(column_ptr(it), qr);
+      cf = qk_operand_column<QT, D, KF>(qr, valid, a.qk_scale_log2, qop);
     }
 #pragma unroll
     for (int k = 0; k <= NPV; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -511,8 +549,8 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
       const int col = (w * 2 + which) * G;
       return Partial{lo_ + col * D, lml + col * 2};
     };
-    merge_pieces<QT, D, G>(a, src_of, w1 - w0 + 1, orow,
-                           it.out < 0 ? 0 : chunk_slot(p, it.out, G), lane);
+    merge_pieces<QT, D, G, merge_group<D, G>()>(a, src_of, w1 - w0 + 1, orow,
+                                                it.out < 0 ? 0 : chunk_slot(p, it.out, G), lane);
   }
 #if ASTR_TRACE
   tm[6] = wall_clock64();
@@ -542,7 +580,7 @@ __global__ __launch_bounds__(kWave) void merge_chunks_kernel(PlanArgs p) {
     return Partial{a.ws_o + slot * D, a.ws_ml + slot * 2};
   };
   QT* orow = static_cast<QT*>(a.out) + (int64_t)seq * a.o_tok + (int64_t)kvh * G * a.o_head;
-  merge_pieces<QT, D, G>(a, src_of, count, orow, 0, threadIdx.x);
+  merge_pieces<QT, D, G, merge_group<D, G>()>(a, src_of, count, orow, 0, threadIdx.x);
 }
 
 // Workgroups of `kernel` one CU holds at once.
@@ -616,7 +654,9 @@ int launch_planned_kf<KF>(const PlanArgs& p, int32_t q_dtype, hipStream_t stream
   const int G = p.a.num_q_heads / p.a.cache.num_kv_heads;
   if (q_dtype == ASTR_F16) return dispatch_dim<_Float16>(p, G, stream, resident);
   if (q_dtype == ASTR_BF16) return dispatch_dim<bf16_t>(p, G, stream, resident);
-  return fail(ASTR_EUNSUPPORTED, "planned decode takes bf16/fp16 queries");
+  if constexpr (KF == kInt8)
+    if (q_dtype == ASTR_F32) return dispatch_dim<float>(p, G, stream, resident);
+  return fail(ASTR_EUNSUPPORTED, "planned decode takes bf16/fp16 queries (fp32 with int8 codes)");
 }
 
 }  // namespace attn

@@ -520,6 +520,8 @@ extern "C" int astr_paged_attention_i8_planned(
   const int64_t wg_words = (int64_t)pi.num_workgroups * (pi.waves_per_workgroup + 3);
   const bool layout =
       pi.off_workgroups == 0 && pi.off_items == wg_words && pi.num_ids >= 0 &&
+      pi.item_stride >= 1 && pi.item_stride <= 64 &&
+      pi.num_items == (int64_t)pi.num_workgroups * pi.item_stride &&
       pi.off_ids == pi.off_items + (int64_t)pi.num_items * 8 &&
       pi.off_chunked == pi.off_ids + pi.num_ids &&
       pi.plan_words == pi.off_chunked + (int64_t)pi.num_chunked * 4;
@@ -539,10 +541,14 @@ extern "C" int astr_paged_attention_i8_planned(
     return fail(ASTR_EINVAL, "num_q_heads %d must be a multiple of num_kv_heads %d", num_q_heads,
                 cache->num_kv_heads);
   if (cache->num_blocks < 1) return fail(ASTR_EINVAL, "cache has no blocks");
-  if (q_dtype != ASTR_F16 && q_dtype != ASTR_BF16)
-    return fail(ASTR_EUNSUPPORTED, "the planned decode takes bf16/fp16 queries");
-  if (!aligned16(query) || !aligned16(out) || (q_token_stride * 2) % 16 ||
-      (q_head_stride * 2) % 16 || (out_token_stride * 2) % 16 || (out_head_stride * 2) % 16)
+  if (q_dtype != ASTR_F16 && q_dtype != ASTR_BF16 &&
+      !(q_dtype == ASTR_F32 && cache->code_format == ASTR_KV_INT8))
+    return fail(ASTR_EUNSUPPORTED, "the planned decode takes bf16/fp16 queries, or fp32 "
+                "queries with int8 codes");
+  const int64_t esize = q_dtype == ASTR_F32 ? 4 : 2;
+  if (!aligned16(query) || !aligned16(out) || (q_token_stride * esize) % 16 ||
+      (q_head_stride * esize) % 16 || (out_token_stride * esize) % 16 ||
+      (out_head_stride * esize) % 16)
     return fail(ASTR_EINVAL, "query/out rows must be 16-byte aligned");
   if (!aligned16(cache->k_codes) || !aligned16(cache->v_codes) ||
       cache->code_block_stride % 16 || cache->code_head_stride % 16 ||

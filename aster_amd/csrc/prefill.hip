@@ -204,15 +204,6 @@ constexpr float safe_factor() {
   return KF == kInt8 ? kSafeFactor : KF == kE4M3 ? kSafeFactorE4M3 : kSafeFactorE5M2;
 }
 
-template <typename QT, int D>
-__device__ __forceinline__ void load_query_column(const QT* qp, QueryColumn<QT, D>& raw) {
-#pragma unroll
-  for (int h = 0; h < D / 64; ++h)
-#pragma unroll
-    for (int c = 0; c < (int)(16 * sizeof(QT) / 16); ++c)
-      raw.w[h][c] = reinterpret_cast<const uint4*>(qp + 64 * h)[c];
-}
-
 // Query operands of one column tile: two int8 terms per 64-wide d chunk for int8 codes
 // (the int8 QK MFMA), f16 halves per 32-wide chunk for FP8 codes (the f16 QK MFMA).
 template <int D>

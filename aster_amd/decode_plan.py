@@ -29,7 +29,7 @@ class DecodePlanInfo(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "num_workgroups", "waves_per_workgroup", "num_items", "num_blocks", "num_ids",
         "num_chunks", "num_chunked", "num_seqs", "num_kv_heads", "window", "tail_blocks",
-        "reserved")] + \
+        "item_stride")] + \
         [(name, ctypes.c_int64) for name in (
             "off_workgroups", "off_items", "off_ids", "off_chunked", "plan_words")]
 

@@ -130,6 +130,7 @@ class PagedAttentionStep:
             self._pages = ([[ref.index for ref in r.pages] for r in self.reservations]
                            if len(counts) > 1 and self.max_query_len == 1 else None)
             self._packs = {}
+            self._plans = {}
         except BaseException:
             if self._tables is not None:
                 self._tables.__exit__(None, None, None)
@@ -157,21 +158,50 @@ class PagedAttentionStep:
                 layer, query, self.block_tables, self.context_lens,
                 max_context_len=self.max_context_len, scale=scale, out=out, work=ws_work,
                 partition_tokens=0, prefix_packs=packs)
+        plan = self._decode_plan(query, window) if self.partition_tokens == 0 else None
+        if plan is not None:  # decode rows on the host schedule (one per step and shape)
+            return cache.paged_attention(
+                layer, query, self.block_tables, self.context_lens,
+                max_context_len=self.max_context_len, scale=scale, window=window, out=out,
+                work=ws_work, decode_plan=plan)
         return cache.paged_attention(
             layer, query, self.block_tables, self.context_lens,
             max_context_len=self.max_context_len, scale=scale, window=window,
             partition_tokens=self.partition_tokens, query_start_loc=self.query_start_loc,
             max_query_len=self.max_query_len, causal=True, out=out, work=ws_work)
 
+    def _host_tables(self):
+        width = max(len(p) for p in self._pages)
+        tables = np.full((len(self._pages), width), -1, np.int64)
+        for row, pages in enumerate(self._pages):
+            tables[row, : len(pages)] = pages
+        return tables, [r.length for r in self.reservations]
+
+    def _decode_plan(self, query, window):
+        """The step's decode schedule for this query shape and window (built at the first
+        layer that asks, reused by the others), or None where the planned kernel does
+        not serve the step (a single row; fp32 queries over FP8 codes)."""
+        cache = self.pool.cache
+        if self._pages is None or not (query.dtype in (torch.bfloat16, torch.float16) or (
+                query.dtype == torch.float32 and cache.code_format == 0)):
+            return None  # fp32 queries: the planned kernel takes them over int8 codes
+        key = (query.shape[1], query.dtype, window)
+        if key not in self._plans:
+            from .decode_plan import plan_decode
+
+            cache = self.pool.cache
+            tables, lens = self._host_tables()
+            self._plans[key] = plan_decode(
+                tables, lens, num_q_heads=query.shape[1], num_kv_heads=cache.num_kv_heads,
+                head_dim=cache.head_dim, q_dtype=query.dtype, device=cache.device,
+                code_format=cache.code_format, window=window)
+        return self._plans[key]
+
     def _prefix_packs(self, num_q_heads):
         if self._pages is None:
             return None
         if num_q_heads not in self._packs:
-            width = max(len(p) for p in self._pages)
-            tables = np.full((len(self._pages), width), -1, np.int64)
-            for row, pages in enumerate(self._pages):
-                tables[row, : len(pages)] = pages
-            lens = [r.length for r in self.reservations]
+            tables, lens = self._host_tables()
             cache = self.pool.cache
             self._packs[num_q_heads] = plan_prefix_packs(
                 tables, lens, num_q_heads, cache.num_kv_heads, device=cache.device,

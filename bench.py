@@ -280,6 +280,22 @@ def extra_measurements(device, partition, calls, planned=True, tail=None):
     out[w.name] = entry
     del cache
     torch.cuda.empty_cache()
+    # config 2 with fp32 queries: the planned MFMA path over int8 codes, against the exact
+    # fp32 VALU kernel the unplanned call takes
+    if planned:
+        w = wl.config2()
+        cache, _ = build_arena(w, 2, device)
+        q32 = wl.queries(w, device).float()
+        w32 = wl.DecodeWorkload(w.name + "_fp32_queries", w.num_q_heads, w.num_kv_heads,
+                                w.head_dim, w.context_lens, w.block_tables, w.num_blocks,
+                                torch.float32, w.seed, w.scale)
+        call, _ = attention_caller(w32, cache, q32, device, partition, planned=True, tail=tail)
+        entry = hbm_entry(w32, *time_calls(call, calls, 2))
+        call, _ = attention_caller(w32, cache, q32, device, partition)
+        entry["exact_fp32_kernel"] = hbm_entry(w32, *time_calls(call, calls, 2))
+        out[w32.name] = entry
+        del cache
+        torch.cuda.empty_cache()
     # config 5: the planned call (rows cut into chunks across workgroups), the unplanned
     # stream-K call, and the 512-token split-K partitions the configuration names
     w = wl.config5()

@@ -277,7 +277,8 @@ size_t astr_paged_attention_i8_shared_workspace_bytes(int32_t num_seqs, int32_t 
 typedef struct astr_decode_plan_info {
   int32_t num_workgroups;       /* grid of the planned launch (one per resident slot) */
   int32_t waves_per_workgroup;
-  int32_t num_items;            /* (sequence, kv head) rows and row chunks */
+  int32_t num_items;            /* entries of the item table: (sequence, kv head) rows
+                                   and row chunks, item_stride per workgroup */
   int32_t num_blocks;           /* blocks the plan streams (over all kv heads) */
   int32_t num_ids;              /* block ids it holds (each sequence's, once) */
   int32_t num_chunks;           /* chunk partial slots (rows split across workgroups) */
@@ -287,7 +288,7 @@ typedef struct astr_decode_plan_info {
   int32_t window;
   int32_t tail_blocks;          /* blocks at the end of each wave's range that it loads
                                    two at a time (0: one at a time throughout) */
-  int32_t reserved;
+  int32_t item_stride;          /* item-table entries per workgroup */
   int64_t off_workgroups, off_items, off_ids, off_chunked;
   int64_t plan_words;           /* int32 words of the plan */
 } astr_decode_plan_info;

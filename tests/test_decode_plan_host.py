@@ -52,13 +52,15 @@ def _check(tables, lens, hkv, window, wg, nw=8):
     n_items = info.num_items
     wgt = buf[info.off_workgroups:info.off_items].reshape(wg, nw + 3)
     items = buf[info.off_items:info.off_ids].reshape(n_items, 8)
+    stride = info.item_stride
+    assert n_items == wg * stride and 1 <= stride <= 64
     ids = buf[info.off_ids:info.off_chunked]
     chunked = buf[info.off_chunked:info.plan_words].reshape(info.num_chunked, 4)
     assert info.plan_words == info.off_chunked + 4 * info.num_chunked
     assert info.num_ids == ids.size
-    # workgroups partition the items in order; each one's list starts at 0
-    assert wgt[0, 0] == 0 and wgt[-1, 1] == n_items
-    assert (wgt[1:, 0] == wgt[:-1, 1]).all()
+    # workgroup g's items start at g * stride; each one's list starts at 0
+    assert (wgt[:, 0] == np.arange(wg) * stride).all()
+    assert (wgt[:, 1] - wgt[:, 0] <= stride).all() and (wgt[:, 1] >= wgt[:, 0]).all()
     assert (wgt[:, 2] == 0).all()
     assert (np.diff(wgt[:, 2:], axis=1) >= 0).all()
     assert int(wgt[:, 2 + nw].sum()) == info.num_blocks

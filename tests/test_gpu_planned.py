@@ -46,7 +46,7 @@ def _edge_workload(dim, hq, hkv, qdtype, seed=7):
 
 @pytest.mark.parametrize("dim,hq,hkv", [(64, 8, 8), (128, 16, 8), (128, 32, 8), (128, 64, 8),
                                         (128, 128, 8), (256, 8, 2), (256, 32, 4), (64, 16, 2)])
-@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_head_dims_groups_dtypes(device, dim, hq, hkv, qdtype):
     w = _edge_workload(dim, hq, hkv, qdtype)
     cache, tables, lens = _build(w, device)
@@ -147,3 +147,37 @@ def test_plans_that_contradict_the_call_are_flagged(device):
     with pytest.raises(ValueError, match="another batch"):
         cache.paged_attention(0, q[:5], tables[:5], lens[:5], max_context_len=w.max_context_len,
                               decode_plan=plan)
+
+
+def test_fp32_queries_on_the_full_config2_and_config1(device):
+    """fp32 queries take the planned MFMA path over int8 codes (three int8 query terms):
+    config 1 against its golden output and config 2 against the exact fp32 kernel, at
+    the north_star tolerance; fp32 queries over FP8 codes are refused."""
+    import os
+
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config1.npz"))
+    cache = PagedKVCache(num_blocks=64, num_layers=1, num_kv_heads=4, head_dim=64, device=device)
+    cache.append(0, torch.from_numpy(g["k"]).to(device), torch.from_numpy(g["v"]).to(device),
+                 torch.from_numpy(g["slots"]).to(device), check=True)
+    q = torch.from_numpy(g["q"]).to(device)
+    plan = plan_decode(g["block_tables"], g["context_lens"], num_q_heads=4, num_kv_heads=4,
+                       head_dim=64, q_dtype=torch.float32, device=device)
+    out = cache.paged_attention(0, q, torch.from_numpy(g["block_tables"]).to(device),
+                                torch.from_numpy(g["context_lens"]).to(device),
+                                max_context_len=300, scale=64 ** -0.5, decode_plan=plan,
+                                check=True)
+    assert out.dtype == torch.float32
+    assert_attention_close(out, g["out"])
+    w = wl.config2()
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device).float()
+    w32 = wl.DecodeWorkload(w.name, w.num_q_heads, w.num_kv_heads, w.head_dim, w.context_lens,
+                            w.block_tables, w.num_blocks, torch.float32, w.seed, w.scale)
+    out, _ = _planned(cache, w32, q, tables, lens)
+    exact = cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                                  scale=w.scale, check=True)  # the exact fp32 VALU kernel
+    assert_attention_close(out, exact)
+    with pytest.raises(Exception):
+        plan_decode(w.block_tables, w.context_lens, num_q_heads=32, num_kv_heads=8,
+                    head_dim=128, q_dtype=torch.float32, device=device,
+                    code_format=FORMAT_CODES["fp8_e4m3fn"])
