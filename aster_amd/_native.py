@@ -131,10 +131,10 @@ def lib():
         i32p = ctypes.POINTER(c_i32)
         handle.astr_decode_plan_workgroups.argtypes = [c_i32] * 5 + [i32p, i32p]
         handle.astr_decode_plan_workgroups.restype = ctypes.c_int
-        handle.astr_decode_plan_words_bound.argtypes = [c_i32, c_i32, c_i64, c_i32, c_i32]
+        handle.astr_decode_plan_words_bound.argtypes = [c_i32, c_i32, c_i64, c_i32, c_i32, c_i32]
         handle.astr_decode_plan_words_bound.restype = c_i64
         handle.astr_decode_plan.argtypes = [i32p, c_i32, i32p, c_i32, c_i32, c_i32, c_i32, c_i32,
-                                            i32p, c_i64, c_vp]
+                                            c_i32, c_i32, c_i32, i32p, c_i64, c_vp]
         handle.astr_decode_plan.restype = ctypes.c_int
         handle.astr_paged_attention_i8_planned_workspace_bytes.argtypes = [c_vp, c_i32, c_i32]
         handle.astr_paged_attention_i8_planned_workspace_bytes.restype = c_sz

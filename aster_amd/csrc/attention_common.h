@@ -909,6 +909,16 @@ struct PlanArgs {
   astr_decode_plan_info info;
 };
 
+// Partial slots of a plan in the workspace, in columns of D floats (and (m, l) pairs):
+// two per wave of the planned kernel, then G per chunk slot (rows cut across
+// workgroups, and the ranges of shared prefixes).
+__device__ __forceinline__ int64_t plan_chunk_slot(const PlanArgs& p, int64_t c, int G) {
+  return ((int64_t)p.info.num_workgroups * p.info.waves_per_workgroup * 2 + c) * G;
+}
+// Column capacity of a prefix tile (decode_plan.cpp): the chunked-prefill kernel's
+// columns per workgroup, the most tile_rows * G may be.
+constexpr int prefix_tile_columns(int head_dim) { return head_dim == 256 ? 64 : 128; }
+
 // Kernel entry points, one translation unit per code format KF (the source built
 // with -DASTR_KF=KF), dispatched on query dtype, head dim and GQA group inside.
 template <int KF> int launch_partitioned_kf(const AttnArgs& a, int32_t q_dtype, hipStream_t stream);
@@ -924,12 +934,17 @@ template <int KF> int launch_prefill_kf(const AttnArgs& a, int32_t q_dtype, hipS
 // launched and the kernel's resident workgroups per CU land there.
 template <int KF>
 int launch_planned_kf(const PlanArgs& p, int32_t q_dtype, hipStream_t stream, int* resident);
+// The prefix tiles of a host plan (prefill.hip): partials for the chunk-merge kernel,
+// which the planned launch runs after the decode kernel.
+template <int KF>
+int launch_prefix_tiles_kf(const PlanArgs& p, int32_t q_dtype, hipStream_t stream);
 #define ASTR_DECLARE_LAUNCHERS(KF)                                                        \
   template <> int launch_partitioned_kf<KF>(const AttnArgs&, int32_t, hipStream_t);       \
   template <> int launch_streamk_kf<KF>(const AttnArgs&, int32_t, hipStream_t);           \
   template <> int launch_streamk_plain_kf<KF>(const AttnArgs&, int32_t, hipStream_t);     \
   template <> int launch_prefill_kf<KF>(const AttnArgs&, int32_t, hipStream_t);             \
-  template <> int launch_planned_kf<KF>(const PlanArgs&, int32_t, hipStream_t, int*);
+  template <> int launch_planned_kf<KF>(const PlanArgs&, int32_t, hipStream_t, int*);     \
+  template <> int launch_prefix_tiles_kf<KF>(const PlanArgs&, int32_t, hipStream_t);
 ASTR_DECLARE_LAUNCHERS(kInt8)
 ASTR_DECLARE_LAUNCHERS(kE4M3)
 ASTR_DECLARE_LAUNCHERS(kE5M2)
@@ -952,6 +967,13 @@ inline int launch_planned(const PlanArgs& p, int32_t q_dtype, hipStream_t stream
     case kInt8: return launch_planned_kf<kInt8>(p, q_dtype, stream, resident);
     case kE4M3: return launch_planned_kf<kE4M3>(p, q_dtype, stream, resident);
     default: return launch_planned_kf<kE5M2>(p, q_dtype, stream, resident);
+  }
+}
+inline int launch_prefix_tiles(const PlanArgs& p, int32_t q_dtype, hipStream_t stream) {
+  switch (p.a.cache.code_format) {
+    case kInt8: return launch_prefix_tiles_kf<kInt8>(p, q_dtype, stream);
+    case kE4M3: return launch_prefix_tiles_kf<kE4M3>(p, q_dtype, stream);
+    default: return launch_prefix_tiles_kf<kE5M2>(p, q_dtype, stream);
   }
 }
 

@@ -14,6 +14,14 @@
 // The cost model is the stream-K kernel's: 50 per block and 135 per row start (a
 // row's query load and the partial it writes when it ends).
 //
+// Shared prefixes (tile_rows >= 2): sequences whose block tables begin with the same
+// blocks, every key of them visible to each, are read together by the prefix-tile
+// kernel (prefill.hip): a tile holds up to tile_rows such sequences (tile_rows * G
+// query columns, one MFMA column tile of the chunked-prefill kernel) and covers, per kv
+// head, one of tile_ranges equal ranges of their shared blocks. Each member row's
+// partials (one per range, then its own blocks' chunks) take consecutive chunk slots
+// and the chunk-merge kernel merges them; its own blocks are an item like any row's.
+//
 // Plan layout (int32 words, offsets in astr_decode_plan_info):
 //   workgroups  [num_workgroups][waves + 3]: first item, end item, then waves + 1 bounds
 //               of the workgroup's block list: wave w streams its blocks [bound[w],
@@ -27,6 +35,12 @@
 //   ids         [num_ids]: the physical ids of every sequence's visible blocks, once per
 //               sequence (the items of its kv heads and chunks point into them)
 //   chunked     [num_chunked][4]: sequence, kv head, first chunk slot, chunks
+//   tiles       [num_tiles][8]: first member (index into tile members), members, kv
+//               head, range, first block, blocks, offset of the first block's id in
+//               `ids`, the sequence whose ids those are
+//   tile members [num_tile_members][3]: sequence, its first chunk slot (kv head h,
+//               range r: slot + h * span + r), span (slots per kv head: ranges, then
+//               the chunks of its own blocks)
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -43,17 +57,22 @@ namespace plan {
 
 constexpr int kBlockTokens = 16;
 constexpr int64_t kBlockCost = 50, kRowCost = 135;
-constexpr int kItemWords = 8, kChunkedWords = 4;
+constexpr int kItemWords = 8, kChunkedWords = 4, kTileWords = 8, kMemberWords = 3;
 constexpr int kMaxItemsPerWorkgroup = 64;  // the kernel's LDS item table
 constexpr int kMaxBlocksPerWave = 1024;    // the kernel's block list windows
+constexpr int kMaxTileRanges = 16;
+constexpr int kMinTileRangeBlocks = 8;     // automatic ranges: at least two key steps each
 
 struct Unit {
   int seq, kvh, blk_begin, nblk, ctx, out, ids_off;
   int64_t cost;
+  bool member;  // the row's shared prefix is a tile's
 };
 
-int64_t words_for(int64_t workgroups, int waves, int64_t items, int64_t ids, int64_t chunked) {
-  return workgroups * (waves + 3) + items * kItemWords + ids + chunked * kChunkedWords;
+int64_t words_for(int64_t workgroups, int waves, int64_t items, int64_t ids, int64_t chunked,
+                  int64_t tiles, int64_t members) {
+  return workgroups * (waves + 3) + items * kItemWords + ids + chunked * kChunkedWords +
+         tiles * kTileWords + members * kMemberWords;
 }
 
 }  // namespace plan
@@ -63,79 +82,171 @@ using namespace astr::plan;
 
 extern "C" int64_t astr_decode_plan_words_bound(int32_t num_seqs, int32_t num_kv_heads,
                                                 int64_t visible_blocks, int32_t num_workgroups,
-                                                int32_t waves_per_workgroup) {
+                                                int32_t waves_per_workgroup, int32_t tile_rows) {
   if (num_seqs < 0 || num_kv_heads < 1 || visible_blocks < 0 || num_workgroups < 1 ||
-      waves_per_workgroup < 1)
+      waves_per_workgroup < 1 || tile_rows < 0)
     return 0;
-  // every item may be cut into at most num_workgroups chunks, and no more chunks exist
-  // than blocks
-  // items: at most kMaxItemsPerWorkgroup per workgroup, at a common stride
+  // items: at most kMaxItemsPerWorkgroup per workgroup, at a common stride; every row
+  // may be chunked; a tile holds two sequences at least, and each sequence is a member
+  // of one tile at most
   const int64_t rows = (int64_t)num_seqs * num_kv_heads;
   const int64_t items = (int64_t)num_workgroups * kMaxItemsPerWorkgroup;
-  return words_for(num_workgroups, waves_per_workgroup, items, visible_blocks, rows);
+  const int64_t tiles = tile_rows >= 2 ? (int64_t)(num_seqs / 2) * num_kv_heads * kMaxTileRanges : 0;
+  const int64_t members = tile_rows >= 2 ? num_seqs : 0;
+  return words_for(num_workgroups, waves_per_workgroup, items, visible_blocks, rows, tiles,
+                   members);
 }
 
 extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table_stride,
                                 const int32_t* context_lens, int32_t num_seqs,
                                 int32_t num_kv_heads, int32_t window, int32_t num_workgroups,
-                                int32_t waves_per_workgroup, int32_t* plan, int64_t plan_words,
-                                astr_decode_plan_info* info) {
+                                int32_t waves_per_workgroup, int32_t tile_rows,
+                                int32_t tile_ranges, int32_t min_shared_blocks, int32_t* plan,
+                                int64_t plan_words, astr_decode_plan_info* info) {
   using astr::fail;
   if (info == nullptr || (num_seqs > 0 && (block_tables == nullptr || context_lens == nullptr)))
     return fail(ASTR_EINVAL, "plan: block_tables, context_lens and info are required");
   if (num_seqs < 0 || num_kv_heads < 1 || block_table_stride < 0 || window < 0 ||
-      num_workgroups < 1 || waves_per_workgroup < 1 || waves_per_workgroup > 16)
+      num_workgroups < 1 || waves_per_workgroup < 1 || waves_per_workgroup > 16 ||
+      tile_rows < 0 || tile_ranges < 0 || tile_ranges > kMaxTileRanges || min_shared_blocks < 0)
     return fail(ASTR_EINVAL, "plan: invalid sizes");
   std::memset(info, 0, sizeof(*info));
   const int NW = waves_per_workgroup;
   // ---- rows: visible blocks of every sequence (the kernels' row_span)
-  std::vector<Unit> units;
   std::vector<int64_t> row_ids(num_seqs);  // offset of sequence s's visible ids
-  int64_t total_cost = 0, visible = 0;
+  std::vector<int> first_blk(num_seqs), last_blk(num_seqs);
+  int64_t visible = 0;
   for (int s = 0; s < num_seqs; ++s) {
     const int ctx = context_lens[s];
     if (ctx < 0 || (int64_t)ctx > (int64_t)block_table_stride * kBlockTokens)
       return fail(ASTR_EINVAL, "plan: context length %d of sequence %d outside its block table",
                   ctx, s);
     const int kv_begin = (window > 0 && ctx > window) ? ctx - window : 0;
-    const int first = kv_begin / kBlockTokens, last = (ctx + kBlockTokens - 1) / kBlockTokens;
-    const int nb = last - first;
+    first_blk[s] = kv_begin / kBlockTokens;
+    last_blk[s] = (ctx + kBlockTokens - 1) / kBlockTokens;
     row_ids[s] = visible;
-    visible += nb;
+    visible += last_blk[s] - first_blk[s];
+  }
+  if (visible > INT32_MAX / 2) return fail(ASTR_EUNSUPPORTED, "plan: batch too large");
+  // ---- shared prefixes: sequences that see every key of their first blocks, grouped
+  // by their first block's id; within a group, each sequence's run of leading blocks
+  // equal to the group leader's (the first sequence of the group), longest runs first,
+  // cut into tiles of tile_rows; a tile shares the shortest run of its members (a tile
+  // sharing fewer than min_shared_blocks ends its group)
+  struct Tile {
+    int lead, shared, m0, n;
+  };
+  std::vector<Tile> tiles;
+  std::vector<int> tile_seqs;           // members of tile t at [m0, m0 + n)
+  std::vector<int> shared_of(num_seqs, 0);
+  if (tile_rows >= 2 && min_shared_blocks >= 1 && block_table_stride > 0) {
+    std::vector<int> cand;
+    for (int s = 0; s < num_seqs; ++s)
+      if (first_blk[s] == 0 && context_lens[s] / kBlockTokens >= min_shared_blocks) cand.push_back(s);
+    std::stable_sort(cand.begin(), cand.end(), [&](int x, int y) {
+      return block_tables[(int64_t)x * block_table_stride] < block_tables[(int64_t)y * block_table_stride];
+    });
+    std::vector<int> common(num_seqs, 0);
+    for (size_t g0 = 0; g0 < cand.size();) {
+      const int32_t id0 = block_tables[(int64_t)cand[g0] * block_table_stride];
+      size_t g1 = g0 + 1;
+      while (g1 < cand.size() && block_tables[(int64_t)cand[g1] * block_table_stride] == id0) ++g1;
+      if (g1 - g0 >= 2) {
+        const int lead = cand[g0];
+        const int32_t* lt = block_tables + (int64_t)lead * block_table_stride;
+        const int lead_full = context_lens[lead] / kBlockTokens;
+        std::vector<int> group(cand.begin() + g0, cand.begin() + g1);
+        for (int s : group) {
+          const int32_t* st = block_tables + (int64_t)s * block_table_stride;
+          const int reach = std::min(context_lens[s] / kBlockTokens, lead_full);
+          int c = 0;
+          while (c < reach && st[c] == lt[c]) ++c;
+          common[s] = c;
+        }
+        std::stable_sort(group.begin(), group.end(), [&](int x, int y) { return common[x] > common[y]; });
+        for (size_t t0 = 0; t0 + 1 < group.size(); t0 += tile_rows) {
+          const size_t t1 = std::min(group.size(), t0 + (size_t)tile_rows);
+          int shared = INT32_MAX;
+          for (size_t i = t0; i < t1; ++i) shared = std::min(shared, common[group[i]]);
+          if (shared < min_shared_blocks) break;  // later tiles share even less
+          tiles.push_back(Tile{lead, shared, (int)tile_seqs.size(), (int)(t1 - t0)});
+          for (size_t i = t0; i < t1; ++i) {
+            tile_seqs.push_back(group[i]);
+            shared_of[group[i]] = shared;
+          }
+        }
+      }
+      g0 = g1;
+    }
+  }
+  int ranges = 0;
+  if (!tiles.empty()) {
+    int least = INT32_MAX;  // the shortest shared run: every range holds a block at least
+    for (const Tile& t : tiles) least = std::min(least, t.shared);
+    if (tile_ranges > 0) {
+      ranges = std::min(tile_ranges, least);
+    } else {  // about one tile per resident workgroup of the decode kernel
+      const int64_t per_range = (int64_t)tiles.size() * num_kv_heads;
+      ranges = (int)std::max<int64_t>(1, num_workgroups / per_range);
+      ranges = std::min({ranges, kMaxTileRanges, std::max(1, least / kMinTileRangeBlocks)});
+    }
+  }
+  // ---- items: every row's visible blocks after its shared prefix
+  std::vector<Unit> units;
+  int64_t total_cost = 0;
+  for (int s = 0; s < num_seqs; ++s) {
+    const int b0 = first_blk[s] + shared_of[s], nb = last_blk[s] - b0;
     for (int h = 0; h < num_kv_heads; ++h) {
       const int64_t cost = nb > 0 ? kBlockCost * nb + kRowCost : 0;
-      units.push_back(Unit{s, h, first, nb, ctx, -1, (int)row_ids[s], cost});
+      units.push_back(Unit{s, h, b0, nb, context_lens[s], -1, (int)(row_ids[s] + shared_of[s]),
+                           cost, shared_of[s] > 0});
       total_cost += cost;
     }
   }
-  if (visible > INT32_MAX / 2) return fail(ASTR_EUNSUPPORTED, "plan: batch too large");
-  // ---- chunks: an item costing more than the per-workgroup share is cut evenly
-  const double share = (double)total_cost / num_workgroups;
+  // ---- chunks: an item costing more than the per-workgroup share is cut evenly; a
+  // member row's slots are its ranges' partials, then its chunks (all its kv heads'
+  // slots together, span per head)
+  const double share = std::max(1.0, (double)total_cost / num_workgroups);
   std::vector<Unit> work;
   std::vector<int32_t> chunked;  // [seq, kvh, first slot, chunks]
-  int chunk_slots = 0;
+  std::vector<int> member_c0(num_seqs, -1), member_span(num_seqs, 0);
+  int64_t chunk_slots = 0;
   for (const Unit& u : units) {
     int k = 1;
     if (u.nblk > 1 && (double)u.cost > share) {
       k = (int)std::ceil((double)u.cost / share);
       k = std::min(k, u.nblk);
     }
-    if (k == 1) {
+    if (!u.member && k == 1) {
       work.push_back(u);
       continue;
     }
-    chunked.insert(chunked.end(), {u.seq, u.kvh, chunk_slots, k});
+    int64_t c0 = chunk_slots;
+    int lead_slots = 0;  // the ranges' slots before the chunks
+    if (u.member) {
+      if (u.nblk == 0) k = 0;  // the prefix is the whole row
+      if (u.kvh == 0) {
+        member_c0[u.seq] = (int)chunk_slots;
+        member_span[u.seq] = ranges + k;
+        chunk_slots += (int64_t)num_kv_heads * (ranges + k);
+      }
+      c0 = member_c0[u.seq] + (int64_t)u.kvh * member_span[u.seq];
+      lead_slots = ranges;
+    } else {
+      chunk_slots += k;
+    }
+    chunked.insert(chunked.end(), {u.seq, u.kvh, (int32_t)c0, lead_slots + k});
     for (int c = 0; c < k; ++c) {
       const int b0 = (int)((int64_t)u.nblk * c / k), b1 = (int)((int64_t)u.nblk * (c + 1) / k);
       Unit part = u;
       part.blk_begin = u.blk_begin + b0;
       part.nblk = b1 - b0;
       part.ids_off = u.ids_off + b0;
-      part.out = chunk_slots + c;
+      part.out = (int)(c0 + lead_slots + c);
       part.cost = kBlockCost * part.nblk + kRowCost;
       work.push_back(part);
     }
-    chunk_slots += k;
+    if (chunk_slots > INT32_MAX / 2) return fail(ASTR_EUNSUPPORTED, "plan: batch too large");
   }
   // ---- LPT: longest first onto the least loaded workgroup (ties: lowest index)
   std::vector<int> order(work.size());
@@ -160,7 +271,10 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
   int64_t num_blocks = 0;
   for (const Unit& u : work) num_blocks += u.nblk;
   const int64_t num_chunked = (int64_t)chunked.size() / kChunkedWords;
-  const int64_t need = words_for(num_workgroups, NW, num_items, visible, num_chunked);
+  const int64_t num_tiles = (int64_t)tiles.size() * num_kv_heads * ranges;
+  const int64_t num_members = (int64_t)tile_seqs.size();
+  const int64_t need = words_for(num_workgroups, NW, num_items, visible, num_chunked, num_tiles,
+                                 num_members);
   if (num_items > INT32_MAX / kItemWords || num_blocks > INT32_MAX / 4)
     return fail(ASTR_EUNSUPPORTED, "plan: batch too large");
   for (int g = 0; g < num_workgroups; ++g)
@@ -182,6 +296,12 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
   info->off_items = (int64_t)num_workgroups * (NW + 3);
   info->off_ids = info->off_items + num_items * kItemWords;
   info->off_chunked = info->off_ids + visible;
+  info->num_tiles = (int32_t)num_tiles;
+  info->tile_rows = num_tiles > 0 ? tile_rows : 0;
+  info->tile_ranges = ranges;
+  info->num_tile_members = (int32_t)num_members;
+  info->off_tiles = info->off_chunked + num_chunked * kChunkedWords;
+  info->off_tile_members = info->off_tiles + num_tiles * kTileWords;
   info->plan_words = need;
   if (plan == nullptr) return 0;  // sizing call
   if (plan_words < need)
@@ -253,5 +373,25 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
     return fail(ASTR_EUNSUPPORTED, "plan: %lld blocks on one wave (at most %d): launch more "
                 "workgroups", (long long)most_per_wave, kMaxBlocksPerWave);
   std::memcpy(plan + info->off_chunked, chunked.data(), chunked.size() * sizeof(int32_t));
+  // tiles by (kv head, range, tile): the tiles reading the same blocks are consecutive
+  // (the tile kernel runs consecutive tiles on one XCD)
+  int32_t* trec = plan + info->off_tiles;
+  for (int h = 0; h < num_kv_heads; ++h)
+    for (int r = 0; r < ranges; ++r)
+      for (const Tile& t : tiles) {
+        const int b0 = (int)((int64_t)t.shared * r / ranges);
+        const int b1 = (int)((int64_t)t.shared * (r + 1) / ranges);
+        const int32_t rec[kTileWords] = {t.m0, t.n, h, r, b0, b1 - b0,
+                                         (int32_t)(row_ids[t.lead] + b0), t.lead};
+        std::memcpy(trec, rec, sizeof(rec));
+        trec += kTileWords;
+      }
+  int32_t* mrec = plan + info->off_tile_members;
+  for (int s : tile_seqs) {
+    mrec[0] = s;
+    mrec[1] = member_c0[s];
+    mrec[2] = member_span[s];
+    mrec += kMemberWords;
+  }
   return 0;
 }

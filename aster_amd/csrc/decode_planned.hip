@@ -68,14 +68,13 @@ __device__ __forceinline__ Item item_at(const int* s_item, int k) {
   return Item{v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
 }
 
-// Partial slots in the workspace, in columns of D floats (and (m, l) pairs): two per
-// wave (at D = 256 its first piece's), then G per chunk of a row cut across
-// workgroups.
+// Partial slots in the workspace (plan_chunk_slot): two per wave (at D = 256 its first
+// piece's), then the chunk slots.
 __device__ __forceinline__ int64_t wave_slot(int64_t gw, int which, int G) {
   return (gw * 2 + which) * G;
 }
 __device__ __forceinline__ int64_t chunk_slot(const PlanArgs& p, int c, int G) {
-  return ((int64_t)p.info.num_workgroups * kPlanWaves * 2 + c) * G;
+  return plan_chunk_slot(p, c, G);
 }
 
 // Where a partial of G heads lies: acc rows (head h at o + h * D) and (m, l) pairs

@@ -524,8 +524,14 @@ extern "C" int astr_paged_attention_i8_planned(
       pi.num_items == (int64_t)pi.num_workgroups * pi.item_stride &&
       pi.off_ids == pi.off_items + (int64_t)pi.num_items * 8 &&
       pi.off_chunked == pi.off_ids + pi.num_ids &&
-      pi.plan_words == pi.off_chunked + (int64_t)pi.num_chunked * 4;
+      pi.off_tiles == pi.off_chunked + (int64_t)pi.num_chunked * 4 &&
+      pi.off_tile_members == pi.off_tiles + (int64_t)pi.num_tiles * 8 &&
+      pi.plan_words == pi.off_tile_members + (int64_t)pi.num_tile_members * 3;
   if (!layout) return fail(ASTR_EINVAL, "plan info offsets are inconsistent");
+  if (pi.num_tiles < 0 || pi.num_tile_members < 0 ||
+      (pi.num_tiles > 0 && (pi.tile_ranges < 1 || pi.tile_ranges > 16 || pi.tile_rows < 2)))
+    return fail(ASTR_EINVAL, "plan info describes invalid prefix tiles");
+
   if (plan == nullptr || (reinterpret_cast<uintptr_t>(plan) & 3u) != 0)
     return fail(ASTR_EINVAL, "a 4-byte aligned device plan is required");
   if (query == nullptr || out == nullptr || context_lens == nullptr)
@@ -540,6 +546,10 @@ extern "C" int astr_paged_attention_i8_planned(
   if (cache->num_kv_heads < 1 || num_q_heads % cache->num_kv_heads != 0)
     return fail(ASTR_EINVAL, "num_q_heads %d must be a multiple of num_kv_heads %d", num_q_heads,
                 cache->num_kv_heads);
+  if (pi.num_tiles > 0 &&
+      (int64_t)pi.tile_rows * (num_q_heads / cache->num_kv_heads) > prefix_tile_columns(cache->head_dim))
+    return fail(ASTR_EINVAL, "prefix tiles of %d rows exceed the %d query columns of a tile",
+                pi.tile_rows, prefix_tile_columns(cache->head_dim));
   if (cache->num_blocks < 1) return fail(ASTR_EINVAL, "cache has no blocks");
   if (q_dtype != ASTR_F16 && q_dtype != ASTR_BF16 &&
       !(q_dtype == ASTR_F32 && cache->code_format == ASTR_KV_INT8))
@@ -590,5 +600,10 @@ extern "C" int astr_paged_attention_i8_planned(
   a.err_flag = err_flag;
   p.plan = plan;
   p.info = pi;
+  // the prefix tiles' partials, then the decode kernel and the chunk merge that reads them
+  if (pi.num_tiles > 0) {
+    const int rc = launch_prefix_tiles(p, q_dtype, static_cast<hipStream_t>(stream));
+    if (rc != 0) return rc;
+  }
   return launch_planned(p, q_dtype, static_cast<hipStream_t>(stream), nullptr);
 }

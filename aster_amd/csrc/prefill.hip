@@ -676,32 +676,244 @@ __device__ __forceinline__ void store_run(QT* dst, const float (&v)[N]) {
   }
 }
 
+// The LDS of one prefill workgroup: the key-step stages, the V operand slabs of the
+// current step and the step's block exponents.
+template <int D>
+struct PrefillLds {
+  static constexpr int NB = kPrefillBuffers;  // key steps in flight: NB - 1 ahead of the one computed
+  __attribute__((aligned(16))) char stages[NB * kWaves * Stage<D>::kBytes];  // [step % NB][wave]
+  uint4 vt[kWaves / 2][(D / 16) * kWave];  // the current step's V operands, one slab per pair
+  __attribute__((aligned(16))) int vexp[kWaves];  // the step's block exponents
+};
+
+// A workgroup's columns: flat column f = (wave * NT + t) * 16 + r. The unit's columns
+// read query token rows q0 + tok (an invalid column reads row q0 + t0 and is zeroed)
+// and see keys [lo, hi]; per wave, the bounds of its columns' key ranges (lo_min ..
+// hi_max: keys some column sees; lo_max .. hi_min: keys every valid column sees) and
+// whether it has a valid column.
+struct ColumnInfo {
+  int tok, head, lo, hi;
+  bool valid;
+};
+struct WaveBounds {
+  int lo_min, lo_max, hi_min, hi_max;
+  bool any;
+};
+
+// One unit of the chunked-prefill kernels: the key blocks [b_lo, b_hi) of kv head kvh
+// (physical id of block b: blocks[b], a window of the arena's ids) against the
+// workgroup's query columns (column_of(f), bounds_of(wave)), through the key steps
+// described at the top of this file; store(t, acc, m, lt, ve, col) then takes column
+// tile t of each wave (acc in units of 2^-ve, lt the row sums of lane (0, r)'s column).
+template <typename QT, int D, int G, typename ColumnOf, typename BoundsOf, typename Store>
+__device__ __forceinline__ void prefill_unit(const AttnArgs& a, PrefillLds<D>& L, int kvh,
+                                             int b_lo, int b_hi, const int32_t* blocks, int q0,
+                                             int t0, ColumnOf column_of, BoundsOf bounds_of,
+                                             Store store) {
+  using S = Stage<D>;
+  constexpr int NT = PrefillShape<D>::NT;
+  constexpr int NPV = D / 16;
+  constexpr int NB = PrefillLds<D>::NB;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int r = lane & 15, qg = lane >> 4;
+  char* const lds = L.stages;
+  const int nsteps = (b_hi - b_lo + kWaves - 1) / kWaves;
+
+  // zero scales in every stage, once every wave is past its last read of what the
+  // stages held before (the dispatch plan): a stage that no step writes (a block past
+  // the range) then feeds finite products; stages written by loads only ever hold arena
+  // scales, which are finite (the append writes no non-finite value). Every int8 and
+  // E4M3FN byte is a finite code, but E5M2 bytes with all exponent bits set are Inf/NaN,
+  // so there the codes are zeroed too.
+  __syncthreads();
+  for (int j = lane; j < NB * 32; j += kWave)
+    reinterpret_cast<float*>(lds + (j / 32) * kWaves * S::kBytes + wave * S::kBytes + S::kS)[j % 32] = 0.f;
+  if constexpr (KF == kE5M2) {
+    for (int j = lane; j < NB * 2 * D; j += kWave)
+      reinterpret_cast<uint4*>(lds + (j / (2 * D)) * kWaves * S::kBytes + wave * S::kBytes +
+                               S::kK)[j % (2 * D)] = uint4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+
+  // ---- this wave's columns. The block ids and the query go out together; the first
+  // steps' loads are issued before the query is quantized.
+  int lo[NT], hi[NT], ctok[NT], chead[NT];
+  bool cvalid[NT];
+  QueryColumn<QT, D> qraw[NT];
+  int ids = 0;
+  // After each load the ids pass through an empty asm that redefines them: the one wait
+  // for their load happens there (once per 64 steps), and the compiler's wait tracking
+  // no longer treats them as a pending load at every issue below (where it would wait
+  // for every stage in flight, vmcnt(0), each step).
+  auto load_ids = [&](int s0) __attribute__((always_inline)) {
+    const int blk = b_lo + (s0 + lane) * kWaves + wave;
+    ids = (s0 + lane < nsteps && blk < b_hi) ? blocks[blk] : 0;
+    asm volatile("" : "+v"(ids));
+  };
+  if (nsteps > 0) load_ids(0);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const ColumnInfo c = column_of((wave * NT + t) * 16 + r);
+    ctok[t] = c.tok;
+    chead[t] = c.head;
+    cvalid[t] = c.valid;
+    lo[t] = c.valid ? c.lo : INT_MAX;
+    hi[t] = c.valid ? c.hi : -1;
+    // an invalid column reads token t0's row (in range) and is zeroed when quantized
+    const QT* qp = static_cast<const QT*>(a.q) + (int64_t)(q0 + (c.valid ? c.tok : t0)) * a.q_tok +
+                   (int64_t)c.head * a.q_head + 16 * qg;
+    load_query_column<QT, D>(qp, qraw[t]);
+  }
+
+  // ---- key steps: block b_lo + 4*step + w is staged by wave w. Lane i of `ids`
+  // holds the id for step (i + 64*k); reloaded every 64 steps.
+  bool bad_index = false, bad_score = false;
+  const bool masks = a.cache.key_valid != nullptr;  // the arena has key padding bytes
+  auto issue = [&](int step, char* buf) __attribute__((always_inline)) -> bool {
+    if (b_lo + step * kWaves + wave >= b_hi) return false;
+    const int id = __builtin_amdgcn_readlane(ids, step % kWave);
+    if ((unsigned)id >= (unsigned)a.cache.num_blocks) {
+      bad_index = true;
+      return false;
+    }
+    stage_block<D>(a, id, kvh, lane, buf + wave * S::kBytes);
+    return true;
+  };
+  auto buffer = [&](int step) __attribute__((always_inline)) -> char* {
+    return lds + (step % NB) * kWaves * S::kBytes;
+  };
+  // bit (step % NB): this wave issued loads for that step (uniform over the wave)
+  uint32_t inflight = 0;
+  for (int j = 0; j < NB - 1 && j < nsteps; ++j)
+    if (issue(j, buffer(j))) inflight |= 1u << (j % NB);
+
+  QOp<D> qop[NT];
+  float cf[NT], cfe[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if constexpr (KF == kInt8)
+      cf[t] = query_column_i8<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qop[t].hi, qop[t].lo);
+    else
+      cf[t] = query_column_f16<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qop[t].op);
+    cfe[t] = cf[t] > 0.f ? cf[t] : FLT_MIN;  // cf >= 0 or NaN (scale > 0)
+  }
+  const WaveBounds wb = bounds_of(wave);
+
+  const ColumnRefs<NT> cols{q0, t0, ctok, chead, cvalid};
+  float4_t acc[NT][NPV + 1];  // [NPV]: row sums in row 0 (lanes qg = 0)
+  const _Float16 one = r == 0 ? (_Float16)1.f : (_Float16)0.f;
+  const half8_t ones = {one, one, one, one, one, one, one, one};  // A operand: row 0 all ones
+  float m[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int k = 0; k <= NPV; ++k) acc[t][k] = float4_t{0.f, 0.f, 0.f, 0.f};
+    m[t] = -FLT_MAX;  // finite start: fully masked blocks give exp2(-inf) = 0
+  }
+  // The PV accumulators are in units of 2^-ve: ve is the largest block exponent so far
+  // (0 unless a block's V scales need more, see convert_v); vlim is its scale limit.
+  int ve = 0;
+  float vlim = 32768.f / format_max<KF>();
+
+  for (int i = 0; i < nsteps; ++i) {
+    const int ahead = i + NB - 1;
+    if (ahead < nsteps) {
+      if (ahead % kWave == 0) load_ids(ahead);
+      // its buffer was last read in step i - 1 (barrier below)
+      if (issue(ahead, buffer(ahead))) inflight |= 1u << (ahead % NB);
+      else inflight &= ~(1u << (ahead % NB));
+    }
+    // wait for step i's loads; the later steps' loads stay in flight
+    int younger = 0;
+#pragma unroll
+    for (int k = 1; k < NB; ++k)
+      if (i + k < nsteps && (inflight >> ((i + k) % NB) & 1u)) ++younger;
+    if (younger >= 3) wait_vmcnt<3 * S::kLoads>();
+    else if (younger == 2) wait_vmcnt<2 * S::kLoads>();
+    else if (younger == 1) wait_vmcnt<S::kLoads>();
+    else wait_vmcnt<0>();
+    char* const cur = buffer(i);
+    // this wave's block of step i is in; its V operands go to the wave's slab (the
+    // previous step's readers are past the barrier that ended that step)
+    const int eb = convert_v<D>(cur + wave * S::kBytes, lane, wave % 2,
+                                reinterpret_cast<uint2*>(L.vt[wave / 2]), ve, vlim);
+    if (lane == 0) L.vexp[wave] = eb;
+    __syncthreads();  // every wave's block of step i has landed and been converted
+    // the step's block exponents (each at least ve): a larger one becomes the new ve
+    // (the PV tiles, not the row sums, scale by the exact 2^(ve_old - ve)); blocks
+    // converted below ve weigh their products by 2^(e_b - ve)
+    bool vmix = false;
+    half4_t vf = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+    {
+      const int4_t ev = *reinterpret_cast<const int4_t*>(L.vexp);
+      int e4[kWaves];
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) e4[w] = __builtin_amdgcn_readfirstlane(ev[w]);
+      const int emax = max(max(e4[0], e4[1]), max(e4[2], e4[3]));
+      if (emax != ve) {
+        const float down = ldexpf(1.f, ve - emax);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int n = 0; n < NPV; ++n) acc[t][n] *= down;
+        ve = emax;
+        vlim = ldexpf(32768.f / format_max<KF>(), ve);
+      }
+      vmix = e4[0] != ve || e4[1] != ve || e4[2] != ve || e4[3] != ve;
+      if (vmix) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) vf[w] = (_Float16)ldexpf(1.f, e4[w] - ve);
+      }
+    }
+    {
+      const int kb0 = (b_lo + i * kWaves) * kBlockTokens;
+      const int kend = b_hi * kBlockTokens;
+      uint32_t use = 0, bounded = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const int kb = kb0 + w * kBlockTokens;
+        if (wb.any && kb < kend && kb <= wb.hi_max && kb + kBlockTokens - 1 >= wb.lo_min)
+          use |= 1u << w;
+        if (!(kb >= wb.lo_max && kb + kBlockTokens - 1 <= wb.hi_min)) bounded |= 1u << w;
+      }
+      if (use != 0)
+        prefill_step<QT, D, NT>(cur, L.vt[0], use, bounded & use, masks, kb0, qop, cf, cfe, lo, hi,
+                                r, qg, ones, vmix, vf, acc, m, bad_score, a, cols);
+    }
+    __syncthreads();  // step i's stage may be refilled
+  }
+  if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+  if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
+
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const float lt = __shfl(acc[t][NPV][0], r, kWave);  // row 0 of the sum tile: lane (0, r)
+    store(t, acc[t], m[t], lt, ve, ColumnInfo{ctok[t], chead[t], lo[t], hi[t], cvalid[t]});
+  }
+}
+
 template <typename QT, int D, int G>
 __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim");
-  using S = Stage<D>;
   constexpr int NT = PrefillShape<D>::NT;
   constexpr int TQ = PrefillShape<D>::kCols / G;
   constexpr int NPV = D / 16;
   constexpr int VB = D / 16;
   static_assert(PrefillShape<D>::kCols % G == 0, "GQA group must divide the column tile");
 
-  constexpr int NB = kPrefillBuffers;  // key steps in flight: NB - 1 ahead of the one computed
-  __shared__ __attribute__((aligned(16))) char lds[NB * kWaves * S::kBytes];  // [step % NB][wave]
-  __shared__ uint4 vt[kWaves / 2][VB * kWave];  // the current step's V operands, one slab per pair
+  __shared__ PrefillLds<D> L;
   __shared__ int s_wsum[kWaves];
   __shared__ int s_found[2];
-  __shared__ __attribute__((aligned(16))) int s_vexp[kWaves];  // the step's block exponents
 
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
-  const int r = lane & 15, qg = lane >> 4;
+  const int qg = lane >> 4;
   const int hkv = a.cache.num_kv_heads;
 
   // ---- 1. this workgroup's unit (uniform over the workgroup). The plan lives in the
   // stage buffers until the first load.
-  static_assert(PlanTab::kInts * sizeof(int) <= sizeof(lds), "the dispatch plan fits the stages");
-  int* const tab = reinterpret_cast<int*>(lds);
+  static_assert(PlanTab::kInts * sizeof(int) <= sizeof(L.stages), "the dispatch plan fits the stages");
+  int* const tab = reinterpret_cast<int*>(L.stages);
   int per_kv = 0;
   const int nrows = plan_rows(a, TQ, tab, s_wsum, per_kv);
   if (nrows < 0) per_kv = scan_tiles(a, TQ, -1, s_wsum, s_found);
@@ -746,200 +958,139 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
 
   const TileSpan span = tile_span(a, ctx, n, tile, TQ);
   const int pos0 = span.pos0, t0 = span.t0, t1 = span.t1;
-  const int b_lo = span.b_lo, b_hi = span.b_hi;
-  const int nsteps = (b_hi - b_lo + kWaves - 1) / kWaves;
 
-  // zero scales in every stage, once every wave is past its last read of the plan: a
-  // stage that no step writes (a block past the range) then feeds finite products;
-  // stages written by loads only ever hold arena scales, which are finite (the append
-  // writes no non-finite value). Every int8 and E4M3FN byte is a finite code, but
-  // E5M2 bytes with all exponent bits set are Inf/NaN, so there the codes are zeroed too.
-  __syncthreads();
-  for (int j = lane; j < NB * 32; j += kWave)
-    reinterpret_cast<float*>(lds + (j / 32) * kWaves * S::kBytes + wave * S::kBytes + S::kS)[j % 32] = 0.f;
-  if constexpr (KF == kE5M2) {
-    for (int j = lane; j < NB * 2 * D; j += kWave)
-      reinterpret_cast<uint4*>(lds + (j / (2 * D)) * kWaves * S::kBytes + wave * S::kBytes +
-                               S::kK)[j % (2 * D)] = uint4{0u, 0u, 0u, 0u};
-  }
-  __syncthreads();
-
-  // ---- 2. this wave's columns: flat column f -> token t0 + f / G, head kvh * G + f % G.
-  // The block ids and the query go out together; the first steps' loads are issued
-  // before the query is quantized.
-  int lo[NT], hi[NT], ctok[NT], chead[NT];
-  bool cvalid[NT];
-  QueryColumn<QT, D> qraw[NT];
-  const int32_t* bt = a.block_tables + (int64_t)seq * a.bt_stride;
-  int ids = 0;
-  // After each load the ids pass through an empty asm that redefines them: the one wait
-  // for their load happens there (once per 64 steps), and the compiler's wait tracking
-  // no longer treats them as a pending load at every issue below (where it would wait
-  // for every stage in flight, vmcnt(0), each step).
-  auto load_ids = [&](int s0) __attribute__((always_inline)) {
-    const int blk = b_lo + (s0 + lane) * kWaves + wave;
-    ids = (s0 + lane < nsteps && blk < b_hi) ? bt[blk] : 0;
-    asm volatile("" : "+v"(ids));
+  // flat column f -> token t0 + f / G, head kvh * G + f % G, keys by its position
+  auto column_of = [&](int f) __attribute__((always_inline)) -> ColumnInfo {
+    const int tok = t0 + f / G;
+    const int p = pos0 + tok;
+    return ColumnInfo{tok, kvh * G + f % G, a.window > 0 ? max(0, p - a.window + 1) : 0,
+                      a.causal ? p : ctx - 1, tok < t1};
   };
-  if (nsteps > 0) load_ids(0);
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int f = (wave * NT + t) * 16 + r;
-    ctok[t] = t0 + f / G;
-    chead[t] = kvh * G + f % G;
-    cvalid[t] = ctok[t] < t1;
-    const int p = pos0 + ctok[t];
-    lo[t] = cvalid[t] ? (a.window > 0 ? max(0, p - a.window + 1) : 0) : INT_MAX;
-    hi[t] = cvalid[t] ? (a.causal ? p : ctx - 1) : -1;
-    // an invalid column reads token t0's row (in range) and is zeroed when quantized
-    const QT* qp = static_cast<const QT*>(a.q) + (int64_t)(q0 + (cvalid[t] ? ctok[t] : t0)) * a.q_tok +
-                   (int64_t)chead[t] * a.q_head + 16 * qg;
-    load_query_column<QT, D>(qp, qraw[t]);
-  }
-
-  // ---- 3. key steps: block b_lo + 4*step + w is staged by wave w. Lane i of `ids`
-  // holds the id for step (i + 64*k); reloaded every 64 steps.
-  bool bad_index = false, bad_score = false;
-  const bool masks = a.cache.key_valid != nullptr;  // the arena has key padding bytes
-  auto issue = [&](int step, char* buf) __attribute__((always_inline)) -> bool {
-    if (b_lo + step * kWaves + wave >= b_hi) return false;
-    const int id = __builtin_amdgcn_readlane(ids, step % kWave);
-    if ((unsigned)id >= (unsigned)a.cache.num_blocks) {
-      bad_index = true;
-      return false;
-    }
-    stage_block<D>(a, id, kvh, lane, buf + wave * S::kBytes);
-    return true;
-  };
-  auto buffer = [&](int step) __attribute__((always_inline)) -> char* {
-    return lds + (step % NB) * kWaves * S::kBytes;
-  };
-  // bit (step % NB): this wave issued loads for that step (uniform over the wave)
-  uint32_t inflight = 0;
-  for (int j = 0; j < NB - 1 && j < nsteps; ++j)
-    if (issue(j, buffer(j))) inflight |= 1u << (j % NB);
-
-  QOp<D> qop[NT];
-  float cf[NT], cfe[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    if constexpr (KF == kInt8)
-      cf[t] = query_column_i8<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qop[t].hi, qop[t].lo);
-    else
-      cf[t] = query_column_f16<QT, D>(qraw[t], cvalid[t], a.qk_scale_log2, qop[t].op);
-    cfe[t] = cf[t] > 0.f ? cf[t] : FLT_MIN;  // cf >= 0 or NaN (scale > 0)
-  }
   // key bounds over the wave's valid columns (positions grow with f)
-  const int tk_lo = t0 + (wave * NT * 16) / G;
-  const int tk_hi = min(t1 - 1, t0 + ((wave + 1) * NT * 16 - 1) / G);
-  const bool wave_any = tk_lo < t1;
-  const int w_hi_max = a.causal ? pos0 + tk_hi : ctx - 1;
-  const int w_hi_min = a.causal ? pos0 + tk_lo : ctx - 1;
-  const int w_lo_min = a.window > 0 ? max(0, pos0 + tk_lo - a.window + 1) : 0;
-  const int w_lo_max = a.window > 0 ? max(0, pos0 + tk_hi - a.window + 1) : 0;
-
-  const ColumnRefs<NT> cols{q0, t0, ctok, chead, cvalid};
-  float4_t acc[NT][NPV + 1];  // [NPV]: row sums in row 0 (lanes qg = 0)
-  const _Float16 one = r == 0 ? (_Float16)1.f : (_Float16)0.f;
-  const half8_t ones = {one, one, one, one, one, one, one, one};  // A operand: row 0 all ones
-  float m[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-#pragma unroll
-    for (int k = 0; k <= NPV; ++k) acc[t][k] = float4_t{0.f, 0.f, 0.f, 0.f};
-    m[t] = -FLT_MAX;  // finite start: fully masked blocks give exp2(-inf) = 0
-  }
-  // The PV accumulators are in units of 2^-ve: ve is the largest block exponent so far
-  // (0 unless a block's V scales need more, see convert_v); vlim is its scale limit.
-  int ve = 0;
-  float vlim = 32768.f / format_max<KF>();
-
-  for (int i = 0; i < nsteps; ++i) {
-    const int ahead = i + NB - 1;
-    if (ahead < nsteps) {
-      if (ahead % kWave == 0) load_ids(ahead);
-      // its buffer was last read in step i - 1 (barrier below)
-      if (issue(ahead, buffer(ahead))) inflight |= 1u << (ahead % NB);
-      else inflight &= ~(1u << (ahead % NB));
-    }
-    // wait for step i's loads; the later steps' loads stay in flight
-    int younger = 0;
-#pragma unroll
-    for (int k = 1; k < NB; ++k)
-      if (i + k < nsteps && (inflight >> ((i + k) % NB) & 1u)) ++younger;
-    if (younger >= 3) wait_vmcnt<3 * S::kLoads>();
-    else if (younger == 2) wait_vmcnt<2 * S::kLoads>();
-    else if (younger == 1) wait_vmcnt<S::kLoads>();
-    else wait_vmcnt<0>();
-    char* const cur = buffer(i);
-    // this wave's block of step i is in; its V operands go to the wave's slab (the
-    // previous step's readers are past the barrier that ended that step)
-    const int eb = convert_v<D>(cur + wave * S::kBytes, lane, wave % 2,
-                                reinterpret_cast<uint2*>(vt[wave / 2]), ve, vlim);
-    if (lane == 0) s_vexp[wave] = eb;
-    __syncthreads();  // every wave's block of step i has landed and been converted
-    // the step's block exponents (each at least ve): a larger one becomes the new ve
-    // (the PV tiles, not the row sums, scale by the exact 2^(ve_old - ve)); blocks
-    // converted below ve weigh their products by 2^(e_b - ve)
-    bool vmix = false;
-    half4_t vf = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
-    {
-      const int4_t ev = *reinterpret_cast<const int4_t*>(s_vexp);
-      int e4[kWaves];
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) e4[w] = __builtin_amdgcn_readfirstlane(ev[w]);
-      const int emax = max(max(e4[0], e4[1]), max(e4[2], e4[3]));
-      if (emax != ve) {
-        const float down = ldexpf(1.f, ve - emax);
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-          for (int n = 0; n < NPV; ++n) acc[t][n] *= down;
-        ve = emax;
-        vlim = ldexpf(32768.f / format_max<KF>(), ve);
-      }
-      vmix = e4[0] != ve || e4[1] != ve || e4[2] != ve || e4[3] != ve;
-      if (vmix) {
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) vf[w] = (_Float16)ldexpf(1.f, e4[w] - ve);
-      }
-    }
-    {
-      const int kb0 = (b_lo + i * kWaves) * kBlockTokens;
-      const int kend = b_hi * kBlockTokens;
-      uint32_t use = 0, bounded = 0;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const int kb = kb0 + w * kBlockTokens;
-        if (wave_any && kb < kend && kb <= w_hi_max && kb + kBlockTokens - 1 >= w_lo_min)
-          use |= 1u << w;
-        if (!(kb >= w_lo_max && kb + kBlockTokens - 1 <= w_hi_min)) bounded |= 1u << w;
-      }
-      if (use != 0)
-        prefill_step<QT, D, NT>(cur, vt[0], use, bounded & use, masks, kb0, qop, cf, cfe, lo, hi, r,
-                                qg, ones, vmix, vf, acc, m, bad_score, a, cols);
-    }
-    __syncthreads();  // step i's stage may be refilled
-  }
-  if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
-  if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
-
-  // ---- 4. normalise and store (fully masked columns: l = 0, acc = 0 -> 0)
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const float lt = __shfl(acc[t][NPV][0], r, kWave);  // row 0 of the sum tile: lane (0, r)
-    if (!cvalid[t]) continue;
+  auto bounds_of = [&](int wave) __attribute__((always_inline)) -> WaveBounds {
+    const int tk_lo = t0 + (wave * NT * 16) / G;
+    const int tk_hi = min(t1 - 1, t0 + ((wave + 1) * NT * 16 - 1) / G);
+    return WaveBounds{a.window > 0 ? max(0, pos0 + tk_lo - a.window + 1) : 0,
+                      a.window > 0 ? max(0, pos0 + tk_hi - a.window + 1) : 0,
+                      a.causal ? pos0 + tk_lo : ctx - 1, a.causal ? pos0 + tk_hi : ctx - 1,
+                      tk_lo < t1};
+  };
+  // normalise and store (fully masked columns: l = 0, acc = 0 -> 0)
+  auto store = [&](int t, const float4_t (&acc)[NPV + 1], float, float lt, int ve,
+                   const ColumnInfo& c) __attribute__((always_inline)) {
+    if (!c.valid) return;
     const float inv = ldexpf(1.f, ve) / fmaxf(lt, FLT_MIN);  // the PV tiles carry 2^-ve
-    QT* op = static_cast<QT*>(a.out) + (int64_t)(q0 + ctok[t]) * a.o_tok +
-             (int64_t)chead[t] * a.o_head;
+    QT* op = static_cast<QT*>(a.out) + (int64_t)(q0 + c.tok) * a.o_tok + (int64_t)c.head * a.o_head;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v[VB];
 #pragma unroll
-      for (int k = 0; k < NPV; ++k) v[k] = acc[t][k][j] * inv;
+      for (int k = 0; k < NPV; ++k) v[k] = acc[k][j] * inv;
       store_run<QT, VB>(op + VB * (4 * qg + j), v);
     }
+  };
+  prefill_unit<QT, D, G>(a, L, kvh, span.b_lo, span.b_hi,
+                         a.block_tables + (int64_t)seq * a.bt_stride, q0, t0, column_of,
+                         bounds_of, store);
+}
+
+// Prefix tiles of a decode plan (decode_plan.cpp): the shared blocks of sequences whose
+// block tables begin with the same blocks, every key visible to each, read once per
+// tile of up to TQ member sequences (TQ * G columns: member j's head g is column
+// j G + g) and key range, as the chunked-prefill kernel reads a chunk's keys against
+// its query tokens, with no mask: each column's partial (m, l, acc) of the range goes to
+// the member row's chunk slot, for the chunk-merge kernel (decode_planned.hip) to merge
+// with the row's other ranges and its own blocks. Tiles reading the same blocks (one kv
+// head and range) are consecutive and run on one XCD, whose L2 then serves their keys.
+constexpr int kTileWords = 8, kMemberWords = 3;
+
+template <typename QT, int D, int G>
+__global__ __launch_bounds__(256) void prefix_tiles_kernel(PlanArgs p) {
+  static_assert(D == 64 || D == 128 || D == 256, "head_dim");
+  constexpr int TQ = PrefillShape<D>::kCols / G;
+  constexpr int NPV = D / 16;
+  constexpr int VB = D / 16;
+  static_assert(PrefillShape<D>::kCols % G == 0, "GQA group must divide the column tile");
+  const AttnArgs& a = p.a;
+
+  __shared__ PrefillLds<D> L;
+  __shared__ int s_row[TQ];      // member j's query token row
+  __shared__ int s_slot[TQ];     // its chunk slot for this tile's kv head and range
+  __shared__ int s_bad;
+
+  const int lane = threadIdx.x % kWave;
+  const int qg = lane >> 4;
+  const int hkv = a.cache.num_kv_heads;
+  const int64_t units = p.info.num_tiles;
+  const int64_t per_xcd = (units + kXcds - 1) / kXcds;
+  const int64_t slot = blockIdx.x / kXcds;
+  const int64_t unit = (int64_t)(blockIdx.x % kXcds) * per_xcd + slot;
+  if (slot >= per_xcd || unit >= units) return;
+
+  // ---- the tile and its members, every index checked (the plan is untrusted)
+  const int32_t* rec = p.plan + p.info.off_tiles + unit * kTileWords;
+  const int m0 = rec[0], n = rec[1], kvh = rec[2], range = rec[3];
+  const int blk0 = rec[4], nblk = rec[5], ids_off = rec[6], lead = rec[7];
+  if (threadIdx.x == 0) s_bad = 0;
+  __syncthreads();
+  bool bad = !(m0 >= 0 && n >= 1 && n <= TQ && n <= p.info.num_tile_members - m0 && kvh >= 0 &&
+               kvh < hkv && range >= 0 && range < p.info.tile_ranges && blk0 >= 0 && nblk >= 0 &&
+               ids_off >= 0 && nblk <= p.info.num_ids - ids_off && lead >= 0 && lead < a.num_seqs);
+  if (!bad && (int)threadIdx.x < n) {
+    const int32_t* mem = p.plan + p.info.off_tile_members + (int64_t)(m0 + threadIdx.x) * kMemberWords;
+    const int seq = mem[0], c0 = mem[1], span = mem[2];
+    bad = !(seq >= 0 && seq < a.num_seqs && c0 >= 0 && span > range &&
+            (int64_t)c0 + (int64_t)hkv * span <= p.info.num_chunks);
+    if (!bad) {
+      s_row[threadIdx.x] = seq;  // decode rows: sequence s's query token is row s
+      s_slot[threadIdx.x] = c0 + kvh * span + range;
+      // every key of the range must be visible to the member (its length as planned)
+      const RowSpan sp = row_span(a, a.context_lens[seq]);
+      if (sp.kv_begin > blk0 * kBlockTokens || (int64_t)sp.ctx < (int64_t)(blk0 + nblk) * kBlockTokens)
+        atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+    }
   }
+  if (bad) s_bad = 1;
+  __syncthreads();
+  if (s_bad) {
+    if (threadIdx.x == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+    return;  // the whole workgroup
+  }
+  const int row0 = s_row[0];  // the row invalid columns read
+
+  auto column_of = [&](int f) __attribute__((always_inline)) -> ColumnInfo {
+    const int j = f / G;
+    return ColumnInfo{j < n ? s_row[j] : row0, kvh * G + f % G, 0, INT_MAX, j < n};
+  };
+  // every key of the range is visible to every column: no step is bounded
+  auto bounds_of = [&](int wave) __attribute__((always_inline)) -> WaveBounds {
+    return WaveBounds{0, 0, INT_MAX, INT_MAX, (wave * PrefillShape<D>::NT * 16) / G < n};
+  };
+  // the partial of column (member j, head g): m, l and acc into the member's chunk
+  // slot, head g, with acc and l in the decode kernels' units (both times norm_scale,
+  // as the decode partials they merge with)
+  auto store = [&](int t, const float4_t (&acc)[NPV + 1], float m, float lt, int ve,
+                   const ColumnInfo& c) __attribute__((always_inline)) {
+    if (!c.valid) return;
+    const int f = (__builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * PrefillShape<D>::NT + t) * 16 +
+                  (lane & 15);
+    const int64_t col = plan_chunk_slot(p, s_slot[f / G], G) + f % G;
+    const float up = ldexpf(norm_scale<KF>(), ve);  // the PV tiles carry 2^-ve
+    float* dst = a.ws_o + col * D;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v[VB];
+#pragma unroll
+      for (int k = 0; k < NPV; ++k) v[k] = acc[k][j] * up;
+      store_run<float, VB>(dst + VB * (4 * qg + j), v);
+    }
+    if (qg == 0) {
+      a.ws_ml[col * 2] = m;
+      a.ws_ml[col * 2 + 1] = lt * norm_scale<KF>();
+    }
+  };
+  const int32_t* ids = p.plan + p.info.off_ids + ids_off - blk0;  // id of block b at ids[b]
+  prefill_unit<QT, D, G>(a, L, kvh, blk0, blk0 + nblk, ids, 0, row0, column_of, bounds_of, store);
 }
 
 template <typename QT, int D, int G>
@@ -981,7 +1132,50 @@ int dispatch_dim(const AttnArgs& a, int G, hipStream_t s) {
   }
 }
 
+template <typename QT, int D, int G>
+int launch_tiles(const PlanArgs& p, hipStream_t stream) {
+  const int64_t grid = ((int64_t)p.info.num_tiles + kXcds - 1) / kXcds * kXcds;
+  if (grid == 0) return 0;
+  if (grid > INT32_MAX) return fail(ASTR_EUNSUPPORTED, "prefix tile grid too large");
+  hipLaunchKernelGGL((prefix_tiles_kernel<QT, D, G>), dim3((uint32_t)grid), dim3(kWaves * kWave),
+                     0, stream, p);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "paged_attention (prefix tiles) launch");
+}
+
+template <typename QT, int D>
+int tiles_group(const PlanArgs& p, int G, hipStream_t s) {
+  switch (G) {
+    case 1: return launch_tiles<QT, D, 1>(p, s);
+    case 2: return launch_tiles<QT, D, 2>(p, s);
+    case 4: return launch_tiles<QT, D, 4>(p, s);
+    case 8: return launch_tiles<QT, D, 8>(p, s);
+    case 16: return launch_tiles<QT, D, 16>(p, s);
+    default: return fail(ASTR_EUNSUPPORTED, "GQA group size %d not supported", G);
+  }
+}
+
+template <typename QT>
+int tiles_dim(const PlanArgs& p, int G, hipStream_t s) {
+  switch (p.a.cache.head_dim) {
+    case 64: return tiles_group<QT, 64>(p, G, s);
+    case 128: return tiles_group<QT, 128>(p, G, s);
+    case 256: return tiles_group<QT, 256>(p, G, s);
+    default: return fail(ASTR_EUNSUPPORTED, "head_dim %d not in {64,128,256}", p.a.cache.head_dim);
+  }
+}
+
 }  // namespace
+
+template <>
+int launch_prefix_tiles_kf<KF>(const PlanArgs& p, int32_t q_dtype, hipStream_t stream) {
+  const int G = p.a.num_q_heads / p.a.cache.num_kv_heads;
+  switch (q_dtype) {
+    case ASTR_F32: return tiles_dim<float>(p, G, stream);
+    case ASTR_F16: return tiles_dim<_Float16>(p, G, stream);
+    default: return tiles_dim<bf16_t>(p, G, stream);
+  }
+}
 
 template <>
 int launch_prefill_kf<KF>(const AttnArgs& a, int32_t q_dtype, hipStream_t stream) {

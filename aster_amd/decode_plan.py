@@ -29,14 +29,22 @@ class DecodePlanInfo(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "num_workgroups", "waves_per_workgroup", "num_items", "num_blocks", "num_ids",
         "num_chunks", "num_chunked", "num_seqs", "num_kv_heads", "window", "tail_blocks",
-        "item_stride")] + \
+        "item_stride", "num_tiles", "tile_rows", "tile_ranges", "num_tile_members")] + \
         [(name, ctypes.c_int64) for name in (
-            "off_workgroups", "off_items", "off_ids", "off_chunked", "plan_words")]
+            "off_workgroups", "off_items", "off_ids", "off_chunked", "off_tiles",
+            "off_tile_members", "plan_words")]
 
 
 # Blocks at the end of each wave's range that it loads two at a time (the waves that
 # finish first leave memory bandwidth to the ones still streaming).
 DEFAULT_TAIL_BLOCKS = 0
+# Shared prefixes read in prefix tiles: the fewest shared blocks that make a tile.
+DEFAULT_MIN_SHARED_BLOCKS = 8
+
+
+def tile_columns(head_dim):
+    """Query columns of a prefix tile (the chunked-prefill kernel's per workgroup)."""
+    return 64 if head_dim == 256 else 128
 
 _lock = threading.Lock()
 _workgroups = {}
@@ -77,12 +85,16 @@ class DecodePlan:
 
 def plan_decode(block_tables, context_lens, *, num_q_heads, num_kv_heads, head_dim, q_dtype,
                 device, code_format=_native.ASTR_KV_INT8, window=None,
-                tail_blocks=DEFAULT_TAIL_BLOCKS, num_workgroups=None):
+                tail_blocks=DEFAULT_TAIL_BLOCKS, num_workgroups=None, shared_prefixes=True,
+                tile_rows=None, tile_ranges=0, min_shared_blocks=DEFAULT_MIN_SHARED_BLOCKS):
     """Plan the decode rows of one step from host ``block_tables`` (int ``[S, width]``)
     and ``context_lens`` (``[S]``, the lengths the device copy will hold) for the
     planned kernel on ``device``; the plan's words are uploaded asynchronously on the
     current stream. ``num_workgroups`` overrides the device's resident workgroups
-    (tests)."""
+    (tests). With ``shared_prefixes``, sequences whose tables begin with the same
+    ``min_shared_blocks`` blocks or more read them in prefix tiles of ``tile_rows``
+    sequences (default: as many as a tile's query columns hold) over ``tile_ranges``
+    key ranges (0: chosen by the planner)."""
     tables = np.ascontiguousarray(np.asarray(block_tables), dtype=np.int32)
     lens = np.ascontiguousarray(np.asarray(context_lens), dtype=np.int32)
     if tables.ndim != 2 or lens.ndim != 1 or tables.shape[0] != lens.shape[0]:
@@ -97,18 +109,26 @@ def plan_decode(block_tables, context_lens, *, num_q_heads, num_kv_heads, head_d
                              code_format, device)
     if num_workgroups is not None:
         wg = int(num_workgroups)
+    rows = 0
+    if shared_prefixes:
+        rows = tile_rows if tile_rows is not None else tile_columns(head_dim) // (
+            num_q_heads // num_kv_heads)
+        if type(rows) is not int or rows < 0:
+            raise ValueError("tile_rows must be a non-negative int")
+        rows = rows if rows >= 2 else 0
     lib = _native.lib()
     win = window or 0
     ctx = lens.astype(np.int64)
     first = np.where((win > 0) & (ctx > win), ctx - win, 0) // 16
     visible = int(np.maximum(-(-ctx // 16) - first, 0).sum())
-    bound = lib.astr_decode_plan_words_bound(lens.shape[0], num_kv_heads, visible, wg, nw)
+    bound = lib.astr_decode_plan_words_bound(lens.shape[0], num_kv_heads, visible, wg, nw, rows)
     host = torch.empty(max(int(bound), 1), dtype=torch.int32, pin_memory=True)
     info = DecodePlanInfo()
     i32p = ctypes.POINTER(ctypes.c_int32)
     rc = lib.astr_decode_plan(tables.ctypes.data_as(i32p), tables.shape[1],
                               lens.ctypes.data_as(i32p), lens.shape[0], num_kv_heads, win, wg,
-                              nw, ctypes.cast(host.data_ptr(), i32p), host.numel(),
+                              nw, rows, tile_ranges, min_shared_blocks,
+                              ctypes.cast(host.data_ptr(), i32p), host.numel(),
                               ctypes.byref(info))
     _native.check(rc, "decode plan")
     info.tail_blocks = tail_blocks

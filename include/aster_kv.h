@@ -289,7 +289,11 @@ typedef struct astr_decode_plan_info {
   int32_t tail_blocks;          /* blocks at the end of each wave's range that it loads
                                    two at a time (0: one at a time throughout) */
   int32_t item_stride;          /* item-table entries per workgroup */
-  int64_t off_workgroups, off_items, off_ids, off_chunked;
+  int32_t num_tiles;            /* prefix tiles: (shared prefix, kv head, key range) */
+  int32_t tile_rows;            /* sequences per prefix tile at most */
+  int32_t tile_ranges;          /* key ranges of each shared prefix */
+  int32_t num_tile_members;     /* sequences read through a prefix tile */
+  int64_t off_workgroups, off_items, off_ids, off_chunked, off_tiles, off_tile_members;
   int64_t plan_words;           /* int32 words of the plan */
 } astr_decode_plan_info;
 
@@ -303,10 +307,11 @@ int astr_decode_plan_workgroups(int32_t head_dim, int32_t num_q_heads, int32_t n
                                 int32_t q_dtype, int32_t code_format, int32_t* num_workgroups,
                                 int32_t* waves_per_workgroup);
 
-/* Upper bound of the int32 words of a plan (visible_blocks: sum over sequences). */
+/* Upper bound of the int32 words of a plan (visible_blocks: sum over sequences;
+ * tile_rows as passed to astr_decode_plan). */
 int64_t astr_decode_plan_words_bound(int32_t num_seqs, int32_t num_kv_heads,
                                      int64_t visible_blocks, int32_t num_workgroups,
-                                     int32_t waves_per_workgroup);
+                                     int32_t waves_per_workgroup, int32_t tile_rows);
 
 /*
  * Builds, on the host, the schedule of a decode batch: the same work as
@@ -320,10 +325,18 @@ int64_t astr_decode_plan_words_bound(int32_t num_seqs, int32_t num_kv_heads,
  * valid for these tables and lengths only (one plan per decode step serves every
  * layer). plan == NULL only sizes it (info->plan_words). Host memory only; nothing
  * is launched.
+ * Shared prefixes (the pages PrefixCache hands to several sequences, state.py:547-640,
+ * forked at state.py:210-216): with tile_rows >= 2, sequences whose tables begin with
+ * the same min_shared_blocks blocks or more, all of them visible, are read in prefix
+ * tiles of up to tile_rows sequences (tile_rows * G <= the prefix-tile kernel's
+ * columns: 128 at head dims up to 128, 64 at 256), each kv head's shared blocks cut
+ * into tile_ranges key ranges (0: chosen from the workgroup count); the rows' own
+ * blocks remain items. tile_rows = 0 plans no tiles.
  */
 int astr_decode_plan(const int32_t* block_tables, int32_t block_table_stride,
                      const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
                      int32_t window, int32_t num_workgroups, int32_t waves_per_workgroup,
+                     int32_t tile_rows, int32_t tile_ranges, int32_t min_shared_blocks,
                      int32_t* plan, int64_t plan_words, astr_decode_plan_info* info);
 
 /* Workspace bytes of astr_paged_attention_i8_planned for this plan. */

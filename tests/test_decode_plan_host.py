@@ -1,8 +1,10 @@
 """The host planner of the planned decode kernel (astr_decode_plan, C++): on random
 batches its plan covers every visible block of every (sequence, kv head) row exactly
-once with the row's physical ids, cuts only rows costing more than a workgroup's share,
-balances workgroups within one item of the mean (LPT) and waves within one block and
-one row start, and refuses what the kernel cannot take. No GPU: host memory only."""
+once with the row's physical ids (through a prefix tile for the shared blocks of
+sequences whose tables begin alike), cuts only rows costing more than a workgroup's
+share, balances workgroups within one item of the mean (LPT) and waves within one block
+and one row start, gives every partial its own chunk slot, and refuses what the kernel
+cannot take. No GPU: host memory only."""
 
 import ctypes
 
@@ -16,18 +18,19 @@ I32P = ctypes.POINTER(ctypes.c_int32)
 BLOCK_COST, ROW_COST = 50, 135
 
 
-def _plan(tables, lens, hkv, window, wg, nw=8):
+def _plan(tables, lens, hkv, window, wg, nw=8, tile_rows=0, tile_ranges=0, min_shared=8):
     lib = _native.lib()
     tables = np.ascontiguousarray(tables, np.int32)
     lens = np.ascontiguousarray(lens, np.int32)
     ctx = lens.astype(np.int64)
     first = np.where((window > 0) & (ctx > window), ctx - window, 0) // 16
     visible = int(np.maximum(-(-ctx // 16) - first, 0).sum())
-    bound = lib.astr_decode_plan_words_bound(len(lens), hkv, visible, wg, nw)
+    bound = lib.astr_decode_plan_words_bound(len(lens), hkv, visible, wg, nw, tile_rows)
     buf = np.zeros(max(bound, 1), np.int32)
     info = DecodePlanInfo()
     rc = lib.astr_decode_plan(tables.ctypes.data_as(I32P), tables.shape[1],
                               lens.ctypes.data_as(I32P), len(lens), hkv, window, wg, nw,
+                              tile_rows, tile_ranges, min_shared,
                               buf.ctypes.data_as(I32P), buf.size, ctypes.byref(info))
     return rc, info, buf
 
@@ -46,8 +49,8 @@ def _batch(rng, seqs, max_ctx, pool_extra=7):
     return tables, lens
 
 
-def _check(tables, lens, hkv, window, wg, nw=8):
-    rc, info, buf = _plan(tables, lens, hkv, window, wg, nw)
+def _check(tables, lens, hkv, window, wg, nw=8, tile_rows=0, tile_ranges=0, min_shared=8):
+    rc, info, buf = _plan(tables, lens, hkv, window, wg, nw, tile_rows, tile_ranges, min_shared)
     assert rc == 0, _native.last_error()
     n_items = info.num_items
     wgt = buf[info.off_workgroups:info.off_items].reshape(wg, nw + 3)
@@ -55,9 +58,26 @@ def _check(tables, lens, hkv, window, wg, nw=8):
     stride = info.item_stride
     assert n_items == wg * stride and 1 <= stride <= 64
     ids = buf[info.off_ids:info.off_chunked]
-    chunked = buf[info.off_chunked:info.plan_words].reshape(info.num_chunked, 4)
-    assert info.plan_words == info.off_chunked + 4 * info.num_chunked
+    chunked = buf[info.off_chunked:info.off_tiles].reshape(info.num_chunked, 4)
+    tiles = buf[info.off_tiles:info.off_tile_members].reshape(info.num_tiles, 8)
+    members = buf[info.off_tile_members:info.plan_words].reshape(info.num_tile_members, 3)
+    assert info.off_tiles == info.off_chunked + 4 * info.num_chunked
+    assert info.plan_words == info.off_tile_members + 3 * info.num_tile_members
     assert info.num_ids == ids.size
+    # prefix tiles: members share the tile's blocks (the lead's ids), see all of them,
+    # and write slot c0 + h * span + range of their own slots
+    tiled = {}  # (seq, kvh) -> list of (blk0, nblk, slot)
+    ranges = info.tile_ranges
+    if info.num_tiles:
+        assert 2 <= info.tile_rows <= max(tile_rows, 2) and 1 <= ranges <= 16
+    for m0, n, h, r, b0, nb, off, lead in tiles:
+        assert 2 <= n <= tile_rows and 0 <= h < hkv and 0 <= r < ranges and nb >= 1
+        assert (ids[off:off + nb] == tables[lead, b0:b0 + nb]).all()
+        for seq, c0, span in members[m0:m0 + n]:
+            assert (tables[seq, b0:b0 + nb] == tables[lead, b0:b0 + nb]).all()
+            assert lens[seq] >= (b0 + nb) * 16 and not (window and lens[seq] > window)
+            assert span > r
+            tiled.setdefault((int(seq), int(h)), []).append((int(b0), int(nb), int(c0 + h * span + r)))
     # workgroup g's items start at g * stride; each one's list starts at 0
     assert (wgt[:, 0] == np.arange(wg) * stride).all()
     assert (wgt[:, 1] - wgt[:, 0] <= stride).all() and (wgt[:, 1] >= wgt[:, 0]).all()
@@ -91,26 +111,32 @@ def _check(tables, lens, hkv, window, wg, nw=8):
             if hi > lo:
                 assert starts[lo] >= cost * w / nw - 1e-9
                 assert starts[hi - 1] < cost * (w + 1) / nw
-    # every row covered once; rows in several items are chunked, with consecutive slots
+    # every row covered once; rows in several items or with tiles are chunked, with
+    # consecutive slots (a member's tile ranges first)
     chunk_rows = {(int(s), int(h)): (int(c0), int(n)) for s, h, c0, n in chunked}
+    assert len(chunk_rows) == info.num_chunked
     slots = []
     total = 0
     for s, ctx in enumerate(lens.tolist()):
         kv0 = ctx - window if window and ctx > window else 0
         first, last = kv0 // 16, (ctx + 15) // 16
         for h in range(hkv):
-            parts = sorted(covered[(s, h)])
+            tparts = sorted(tiled.get((s, h), []))
+            own = sorted(covered.get((s, h), []))
+            parts = tparts + own
             assert parts[0][0] == first and sum(p[1] for p in parts) == last - first
             for (a0, an, _), (b0, _, _) in zip(parts, parts[1:]):
                 assert a0 + an == b0
-            if len(parts) == 1:
+            if len(parts) == 1 and not tparts:
                 assert parts[0][2] == -1 and (s, h) not in chunk_rows
             else:
                 c0, n = chunk_rows[(s, h)]
-                assert n == len(parts)
-                assert sorted(p[2] for p in parts) == list(range(c0, c0 + n))
+                assert n == len(parts) and len(tparts) in (0, ranges)
+                assert [p[2] for p in tparts] == list(range(c0, c0 + len(tparts)))
+                assert sorted(p[2] for p in own) == list(range(c0 + len(tparts), c0 + n))
                 slots += list(range(c0, c0 + n))
-            total += BLOCK_COST * (last - first) + (ROW_COST if last > first else 0)
+            nown = sum(p[1] for p in own)
+            total += BLOCK_COST * nown + (ROW_COST if nown else 0)
     assert sorted(slots) == list(range(info.num_chunks))
     # LPT: no workgroup beyond the mean plus one item (a chunk is at most a share)
     share = total / wg
@@ -171,5 +197,62 @@ def test_refusals():
     info = DecodePlanInfo()
     lens = np.array([33, 3], np.int32)
     rc = _native.lib().astr_decode_plan(tables.ctypes.data_as(I32P), 4, lens.ctypes.data_as(I32P),
-                                        2, 1, 0, 4, 8, None, 0, ctypes.byref(info))
+                                        2, 1, 0, 4, 8, 0, 0, 8, None, 0, ctypes.byref(info))
     assert rc == 0 and info.plan_words > 0
+    rc, _, _ = _plan(tables, np.array([3, 3], np.int32), 1, 0, 4, tile_rows=2, tile_ranges=17)
+    assert rc == _native.ASTR_EINVAL
+
+
+def _shared_batch(rng, groups, seqs_per_group, shared_blocks, own_max, hkv_pool_extra=5):
+    """Tables whose rows begin with their group's shared blocks, then blocks of their own."""
+    rows, lens = [], []
+    nxt = 0
+    for g in range(groups):
+        prefix = list(range(nxt, nxt + shared_blocks[g]))
+        nxt += shared_blocks[g]
+        for _ in range(seqs_per_group[g]):
+            own = int(rng.integers(0, own_max + 1))
+            ctx = shared_blocks[g] * 16 + own
+            nb = -(-ctx // 16)
+            row = prefix + list(range(nxt, nxt + nb - shared_blocks[g]))
+            nxt += nb - shared_blocks[g]
+            rows.append(row)
+            lens.append(ctx)
+    width = max(len(r) for r in rows)
+    tables = np.full((len(rows), width), 0, np.int32)
+    perm = rng.permutation(nxt + hkv_pool_extra).astype(np.int32)
+    for i, r in enumerate(rows):
+        tables[i, :len(r)] = perm[r]
+    order = rng.permutation(len(rows))  # groups interleaved in the batch
+    return tables[order], np.asarray(lens, np.int32)[order]
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_shared_prefixes_become_tiles(seed):
+    rng = np.random.default_rng(100 + seed)
+    groups = int(rng.integers(1, 4))
+    per = [int(rng.integers(2, 40)) for _ in range(groups)]
+    shared = [int(rng.integers(8, 40)) for _ in range(groups)]
+    tables, lens = _shared_batch(rng, groups, per, shared, int(rng.choice([0, 100, 700])))
+    hkv = int(rng.choice([1, 2, 8]))
+    rows = int(rng.choice([2, 4, 8, 32]))
+    wg = max(16, -(-len(lens) * hkv // 40))
+    info, _ = _check(tables, lens, hkv, 0, wg, tile_rows=rows,
+                     tile_ranges=int(rng.choice([0, 1, 3])))
+    # every group's sequences in tiles of `rows`, but for a last tile of one
+    assert info.num_tiles > 0
+    assert info.num_tile_members == sum(n - (n % rows == 1) for n in per)
+
+
+def test_config4_prefix_tiles():
+    from aster_amd import workloads as wl
+
+    w = wl.config4()
+    info, loads = _check(w.block_tables, w.context_lens, w.num_kv_heads, 0, 256, tile_rows=32)
+    assert info.num_tile_members == 256 and info.tile_ranges >= 1
+    assert info.num_tiles == 8 * (256 // 32) * info.tile_ranges
+    # the shared prefix is a windowed row's only when every key of it is visible
+    _check(w.block_tables[:40], w.context_lens[:40], w.num_kv_heads, 4096, 64, tile_rows=32)
+    info, _ = _check(w.block_tables[:40], w.context_lens[:40], w.num_kv_heads, 1000, 64,
+                     tile_rows=32)
+    assert info.num_tiles == 0

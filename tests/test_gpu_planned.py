@@ -99,6 +99,108 @@ def test_large_v_scales_and_extreme_scores(device):
     _assert_within_fp32_rounding(w, cache, q, out)
 
 
+def _shared_workload(dim, hq, hkv, qdtype, seed=0, groups=(40, 7, 2), shared=(20, 9, 33),
+                     own_max=300):
+    """Groups of sequences whose tables begin with their group's blocks (a forked
+    prefix), then blocks of their own (some none); groups interleaved in the batch,
+    and a few rows sharing nothing."""
+    rng = np.random.default_rng(seed + dim + hq)
+    rows, lens, nxt = [], [], 0
+    for g, n in enumerate(groups):
+        prefix = list(range(nxt, nxt + shared[g]))
+        nxt += shared[g]
+        for i in range(n):
+            own = 0 if i % 9 == 4 else int(rng.integers(1, own_max + 1))
+            ctx = shared[g] * 16 + own
+            nb = -(-ctx // 16)
+            rows.append(prefix + list(range(nxt, nxt + nb - shared[g])))
+            nxt += nb - shared[g]
+            lens.append(ctx)
+    for ctx in (5, 700, 0):
+        nb = -(-ctx // 16)
+        rows.append(list(range(nxt, nxt + nb)))
+        nxt += nb
+        lens.append(ctx)
+    perm = rng.permutation(nxt + 3).astype(np.int32)
+    tables = np.zeros((len(rows), max(len(r) for r in rows)), np.int32)
+    for i, r in enumerate(rows):
+        tables[i, :len(r)] = perm[r]
+    order = rng.permutation(len(rows))
+    return wl.DecodeWorkload("shared", hq, hkv, dim, np.asarray(lens, np.int32)[order],
+                             tables[order], nxt + 3, qdtype, seed, dim ** -0.5)
+
+
+@pytest.mark.parametrize("dim,hq,hkv", [(128, 32, 8), (128, 8, 8), (64, 32, 2), (256, 16, 4),
+                                        (128, 128, 8)])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("ranges", [0, 1, 3])
+def test_shared_prefixes_in_tiles(device, dim, hq, hkv, qdtype, ranges):
+    """Shared prefixes read in prefix tiles (the chunked-prefill kernel's column tiles,
+    no mask, one partial per member row and key range) and merged with the rows' own
+    blocks by the chunk kernel: the oracle's row-by-row result."""
+    w = _shared_workload(dim, hq, hkv, qdtype)
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    out, plan = _planned(cache, w, q, tables, lens, tile_ranges=ranges, num_workgroups=37)
+    assert plan.info.num_tiles > 0 and plan.info.num_tile_members >= 40
+    assert (out[torch.as_tensor(np.nonzero(w.context_lens == 0)[0], device=device)] == 0).all()
+    assert_attention_close(out, oracle_decode(w, cache, q))
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8_e4m3fn", "fp8_e5m2"])
+def test_shared_prefix_tiles_formats_and_padding(device, fmt):
+    w = _shared_workload(128, 32, 8, torch.bfloat16, seed=3)
+    cache, tables, lens = _build(w, device, fmt)
+    mark_padding(cache, w.block_tables, w.context_lens, 0.2, seed=5, whole_blocks=2)
+    cache.scales[::5, 0, 1] *= 2.0 ** 10  # V scales past the f16 weight range in some blocks
+    q = wl.queries(w, device)
+    out, plan = _planned(cache, w, q, tables, lens, fmt=fmt, tile_ranges=2)
+    assert plan.info.num_tiles > 0
+    assert_attention_close(out, oracle_decode(w, cache, q), atol=2e-3 * 2.0 ** 10)
+
+
+def test_shared_prefix_tiles_extreme_scores(device):
+    """q x100 and K scales x100: the tiles' scores take the third query term on every
+    step, and every output stays within the fp32 rounding of the exact result."""
+    from tests.test_gpu_hardening import _assert_within_fp32_rounding
+
+    w = _shared_workload(128, 32, 8, torch.bfloat16, seed=9)
+    cache, tables, lens = _build(w, device)
+    cache.scales[:, 0, 0] *= 100.0
+    q = (wl.queries(w, device).float() * 100.0).to(torch.bfloat16)
+    out, plan = _planned(cache, w, q, tables, lens, tile_ranges=2)
+    assert plan.info.num_tiles > 0
+    _assert_within_fp32_rounding(w, cache, q, out)
+
+
+def test_tile_plans_that_contradict_the_call_are_flagged(device):
+    w = _shared_workload(128, 32, 8, torch.bfloat16, seed=5)
+    cache, tables, lens = _build(w, device)
+    q = wl.queries(w, device)
+    plan = plan_decode(w.block_tables, w.context_lens, num_q_heads=32, num_kv_heads=8,
+                       head_dim=128, q_dtype=torch.bfloat16, device=device, tile_ranges=2)
+    assert plan.info.num_tiles > 0
+    kw = dict(max_context_len=w.max_context_len, scale=w.scale, decode_plan=plan, check=True)
+    info = plan.info
+    member = int(plan.words[info.off_tile_members].item())
+    # a member's device length shorter than its shared blocks
+    other = lens.clone()
+    other[member] = 3
+    with pytest.raises(ValueError):
+        cache.paged_attention(0, q, tables, other, **kw)
+    # a tile naming a kv head past the arena's, a member past the batch, a slot span
+    # beyond the chunk slots
+    for offset, value in ((info.off_tiles + 2, 8), (info.off_tile_members, 10 ** 6),
+                          (info.off_tile_members + 2, 10 ** 6)):
+        words = plan.words.clone()
+        plan.words[offset] = value
+        with pytest.raises(ValueError):
+            cache.paged_attention(0, q, tables, lens, **kw)
+        plan.words.copy_(words)
+    out = cache.paged_attention(0, q, tables, lens, **kw)
+    assert_attention_close(out, oracle_decode(w, cache, q))
+
+
 @pytest.mark.parametrize("builder", [wl.config2, wl.config4, wl.config5])
 def test_full_configs_match_the_unplanned_call(device, builder):
     """BASELINE configs 2, 4 and 5 at full size: the planned call equals the stream-K
@@ -111,6 +213,8 @@ def test_full_configs_match_the_unplanned_call(device, builder):
         assert plan.info.num_chunked == 0
     if builder is wl.config5:
         assert plan.info.num_chunked > 0
+    if builder is wl.config4:
+        assert plan.info.num_tile_members == w.num_seqs  # the prefix in tiles
     ref = cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
                                 scale=w.scale, check=True)
     assert_attention_close(out, ref)
