@@ -525,19 +525,25 @@ __device__ __forceinline__ float query_column_i8(const QueryColumn<QT, D>& raw, 
 // `dst` as [G][D] elements of QT (16 bytes per lane, D*sizeof(QT)/16 lanes per
 // head): ceil(G*D*sizeof(QT)/1024) vector-memory instructions.
 template <typename QT, int D, int G>
+constexpr int stage_query_loads() {
+  return (G + kWave / (D * (int)sizeof(QT) / 16) - 1) / (kWave / (D * (int)sizeof(QT) / 16));
+}
+template <typename QT, int D, int G>
 __device__ __forceinline__ void stage_query(const AttnArgs& a, int tok, int kvh, int lane,
                                             char* dst) {
   constexpr int kLanesPerHead = D * (int)sizeof(QT) / 16;
   constexpr int kHeadsPerLoad = kWave / kLanesPerHead;
   constexpr int kLoads = (G + kHeadsPerLoad - 1) / kHeadsPerLoad;
   const QT* q0 = static_cast<const QT*>(a.q) + (int64_t)tok * a.q_tok;
+  // the destination is wave-uniform: held in an SGPR before the lane-dependent branch
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(dst));
 #pragma unroll
   for (int k = 0; k < kLoads; ++k) {
     const int g = k * kHeadsPerLoad + lane / kLanesPerHead;
     if (g < G) {
       const char* src = reinterpret_cast<const char*>(q0 + (int64_t)(kvh * G + g) * a.q_head) +
                         (lane % kLanesPerHead) * 16;
-      lds_dma_x4(src, lds_addr(dst) + k * 1024);
+      lds_dma_x4(src, base + k * 1024);
     }
   }
 }

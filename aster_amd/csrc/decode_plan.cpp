@@ -26,6 +26,10 @@
 //   workgroups  [num_workgroups][waves + 3]: first item, end item, then waves + 1 bounds
 //               of the workgroup's block list: wave w streams its blocks [bound[w],
 //               bound[w + 1]) (positions counted from the workgroup's first block)
+//   waves       [num_workgroups * waves][6]: the wave's first piece (sequence, kv head),
+//               how many of its first blocks follow (up to 3, all of that piece) and
+//               their physical ids, so that the wave issues them before it reads its
+//               items
 //   items       [num_workgroups][item_stride][8] (workgroup g's items at g * item_stride,
 //               so a workgroup loads them without its record): sequence, kv head, first
 //               block within the sequence's
@@ -58,6 +62,7 @@ namespace plan {
 constexpr int kBlockTokens = 16;
 constexpr int64_t kBlockCost = 50, kRowCost = 135;
 constexpr int kItemWords = 8, kChunkedWords = 4, kTileWords = 8, kMemberWords = 3;
+constexpr int kWaveWords = 6, kPrefetchBlocks = 3;
 constexpr int kMaxItemsPerWorkgroup = 64;  // the kernel's LDS item table
 constexpr int kMaxBlocksPerWave = 1024;    // the kernel's block list windows
 constexpr int kMaxTileRanges = 16;
@@ -71,7 +76,8 @@ struct Unit {
 
 int64_t words_for(int64_t workgroups, int waves, int64_t items, int64_t ids, int64_t chunked,
                   int64_t tiles, int64_t members) {
-  return workgroups * (waves + 3) + items * kItemWords + ids + chunked * kChunkedWords +
+  return workgroups * (waves + 3) + workgroups * waves * kWaveWords + items * kItemWords + ids +
+         chunked * kChunkedWords +
          tiles * kTileWords + members * kMemberWords;
 }
 
@@ -293,7 +299,8 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
   info->num_kv_heads = num_kv_heads;
   info->window = window;
   info->off_workgroups = 0;
-  info->off_items = (int64_t)num_workgroups * (NW + 3);
+  info->off_waves = (int64_t)num_workgroups * (NW + 3);
+  info->off_items = info->off_waves + (int64_t)num_workgroups * NW * kWaveWords;
   info->off_ids = info->off_items + num_items * kItemWords;
   info->off_chunked = info->off_ids + visible;
   info->num_tiles = (int32_t)num_tiles;
@@ -368,6 +375,25 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
       bound[w] = (int32_t)b;
     }
     for (int w = 0; w < NW; ++w) most_per_wave = std::max<int64_t>(most_per_wave, bound[w + 1] - bound[w]);
+    // each wave's first piece and the ids of its first blocks
+    int32_t* went = plan + info->off_waves + (int64_t)g * NW * kWaveWords;
+    std::memset(went, 0, (size_t)NW * kWaveWords * sizeof(int32_t));
+    size_t m = 0;
+    int64_t m_pos = 0;  // position of member m's first block
+    for (int w = 0; w < NW; ++w, went += kWaveWords) {
+      const int64_t b0 = bound[w], b1 = bound[w + 1];
+      if (b1 <= b0) continue;
+      while (m < members[g].size() && m_pos + work[members[g][m]].nblk <= b0) {
+        m_pos += work[members[g][m]].nblk;
+        ++m;
+      }
+      const Unit& u = work[members[g][m]];
+      const int64_t c = std::min<int64_t>({kPrefetchBlocks, b1 - b0, m_pos + u.nblk - b0});
+      went[0] = u.seq;
+      went[1] = u.kvh;
+      went[2] = (int32_t)c;
+      for (int64_t j = 0; j < c; ++j) went[3 + j] = ids[u.ids_off + (b0 - m_pos) + j];
+    }
   }
   if (most_per_wave > kMaxBlocksPerWave)
     return fail(ASTR_EUNSUPPORTED, "plan: %lld blocks on one wave (at most %d): launch more "

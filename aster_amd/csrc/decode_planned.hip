@@ -29,6 +29,8 @@ constexpr int kMaxItems = 64;           // items per workgroup (the planner's li
 constexpr int kItemWords = 8;           // seq, kv head, first block, blocks, ctx, out, position, ids offset
 constexpr int kChunkedWords = 4;        // seq, kv head, first chunk slot, chunks
 constexpr int kIdsBytes = 256;          // per wave: the next window's block ids
+constexpr int kWaveWords = 6;           // first piece's sequence and kv head, prefetch count, ids
+constexpr int kPrefetchBlocks = 3;
 
 template <int D>
 constexpr int pl_stages() { return D == 256 ? 2 : 4; }
@@ -198,9 +200,8 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
   static_assert(!kLastInRing || NW * 2 * G * (D + 2) * sizeof(float) <= sizeof(lds),
                 "partials fit the ring");
   __shared__ __attribute__((aligned(16))) char id_slots[NW * kIdsBytes];   // [wave]
-  __shared__ int s_item[kMaxItems * kItemWords];
-  __shared__ int s_pos[kMaxItems];  // first block of each item in the workgroup's list
-  __shared__ int s_rec[NW + 3];     // first item, end item, wave bounds
+  __shared__ __attribute__((aligned(16))) int s_item[kMaxItems * kItemWords];
+  __shared__ __attribute__((aligned(16))) int s_rec[NW + 3];  // first item, end item, wave bounds
   __shared__ int s_bad;
   __shared__ bool s_first_ring[NW];  // the wave's slot 0 partial is in the ring
 
@@ -212,32 +213,75 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
   const int g = blockIdx.x;
   const int hkv = a.cache.num_kv_heads;
   const int32_t* const ids_tab = p.plan + p.info.off_ids;
+  const bool valid = r < G;
 
-  // ---- 1. the workgroup's record and items (at a fixed stride, loaded together) into
-  // LDS, every index checked
-  if (threadIdx.x == 0) s_bad = 0;
-  if (threadIdx.x < NW + 3)
-    s_rec[threadIdx.x] = p.plan[p.info.off_workgroups + (int64_t)g * (NW + 3) + threadIdx.x];
+  // ---- 0. in one round trip: this wave's entry (its first piece and the ids of its
+  // first blocks) with its bounds, and (wave 0) the workgroup's record and items (at a
+  // fixed stride) by direct-to-LDS loads; the query and the entry's blocks go out as
+  // soon as the entry is in, after the record and items (loads complete in issue
+  // order). The entry is checked against the items below.
+  int went = 0;
+  if (lane < kWaveWords)
+    went = p.plan[p.info.off_waves + ((int64_t)g * NW + wave) * kWaveWords + lane];
+  else if (lane < kWaveWords + 2)
+    went = p.plan[p.info.off_workgroups + (int64_t)g * (NW + 3) + 2 + wave + lane - kWaveWords];
   const int stride = p.info.item_stride;  // checked on the host: 1..kMaxItems
-  Item mine{};
-  if ((int)threadIdx.x < stride) {
-    const int32_t* src = p.plan + p.info.off_items + ((int64_t)g * stride + threadIdx.x) * kItemWords;
-    int v[kItemWords];
+  if (wave == 0) {
+    if (lane < NW + 3)
+      lds_dma_x1(p.plan + p.info.off_workgroups + (int64_t)g * (NW + 3) + lane,
+                 __builtin_amdgcn_readfirstlane(lds_addr(reinterpret_cast<const char*>(s_rec))));
+    const int32_t* src = p.plan + p.info.off_items + (int64_t)g * stride * kItemWords;
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_addr(reinterpret_cast<const char*>(s_item)));
+    for (int k = 0; k * kWave < stride * kItemWords; ++k)
+      if (k * kWave + lane < stride * kItemWords) lds_dma_x1(src + k * kWave + lane, dst + k * kWave * 4);
+  }
+  if (threadIdx.x == 0) s_bad = 0;
+  asm volatile("" : "+v"(went));  // the entry has landed
+  const int pseq = __builtin_amdgcn_readlane(went, 0), pkvh = __builtin_amdgcn_readlane(went, 1);
+  int pre = __builtin_amdgcn_readlane(went, 2);  // blocks issued here
+  const int pn = __builtin_amdgcn_readlane(went, kWaveWords + 1) - __builtin_amdgcn_readlane(went, kWaveWords);
+  int pid[kPrefetchBlocks];
 #pragma unroll
-    for (int k = 0; k < kItemWords; ++k) v[k] = src[k];
-    mine = Item{v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+  for (int j = 0; j < kPrefetchBlocks; ++j) pid[j] = __builtin_amdgcn_readlane(went, 3 + j);
+  bool pre_ok = pn > 0 && pre >= 1 && pre <= kPrefetchBlocks && pre <= pn && pseq >= 0 &&
+                pseq < a.num_seqs && pkvh >= 0 && pkvh < hkv;
 #pragma unroll
-    for (int k = 0; k < kItemWords; ++k) s_item[threadIdx.x * kItemWords + k] = v[k];
-    s_pos[threadIdx.x] = mine.pos;
+  for (int j = 0; j < kPrefetchBlocks; ++j)
+    pre_ok = pre_ok && (j >= pre || (unsigned)pid[j] < (unsigned)a.cache.num_blocks);
+  const bool bad_entry = pre != 0 && !pre_ok;  // raised with the wave's index flag below
+  // the wave starts after its items without a (valid) entry; it issues at most NS - 1
+  // blocks here (the last stage takes the query). fp32 queries (registers) start after
+  // the items: measured faster (their query loads would wait behind the blocks).
+  pre = pre_ok && sizeof(QT) == 2 ? min(pre, NS - 1) : 0;
+  QueryColumn<QT, D> qr;
+  if (pre > 0) {
+    if constexpr (sizeof(QT) == 2) {
+      stage_query<QT, D, G>(a, pseq, pkvh, lane, lds + ((NS - 1) * NW + wave) * S::kBytes);
+    } else {
+      load_query_column<QT, D>(query_col_ptr<QT>(a, pseq, pkvh * G + (valid ? r : 0), qg), qr);
+    }
+#pragma unroll
+    for (int j = 0; j < kPrefetchBlocks; ++j)
+      if (j < pre) stage_block<D>(a, pid[j], pkvh, lane, lds + (j * NW + wave) * S::kBytes);
+  }
+  if (wave == 0) {  // the record and items have landed (the loads issued after them may not)
+    constexpr int QL = sizeof(QT) == 2 ? stage_query_loads<QT, D, G>() : 0;
+    if (pre == 3) wait_vmcnt<QL + 3 * S::kLoads>();
+    else if (pre == 2) wait_vmcnt<QL + 2 * S::kLoads>();
+    else if (pre == 1) wait_vmcnt<QL + S::kLoads>();
+    else wait_vmcnt<0>();
   }
   __syncthreads();
+
+  // ---- 1. the record and items, every index checked
   const int ib = s_rec[0], ie = s_rec[1];
   const int total = s_rec[2 + NW];  // blocks of the workgroup's list
+  const int ni = ie - ib;
   bool bad = !(ib == g * stride && ib <= ie && ie - ib <= stride && s_rec[2] == 0 &&
                total <= p.info.num_blocks);
   if (threadIdx.x < NW)  // wave bounds: non-decreasing
     bad |= s_rec[3 + threadIdx.x] < s_rec[2 + threadIdx.x];
-  const int ni = ie - ib;
+  const Item mine = !bad && (int)threadIdx.x < ni ? item_at(s_item, threadIdx.x) : Item{};
   if (!bad && (int)threadIdx.x < ni)
     bad = !(mine.seq >= 0 && mine.seq < a.num_seqs && mine.kvh >= 0 && mine.kvh < hkv &&
             mine.nblk >= 0 && mine.blk0 >= 0 && mine.pos >= 0 &&
@@ -248,24 +292,16 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
   __syncthreads();
   if (s_bad) {
     if (threadIdx.x == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+    wait_vmcnt<0>();  // the blocks issued above land before the wave ends
     return;  // the whole workgroup: nothing below runs
   }
   if constexpr (kTrace) tm[1] = wall_clock64();
-  // The plan's lengths must be the device's and its blocks visible to them: checked
-  // beside the first block ids (a mismatch raises the index flag; the rows' outputs
-  // are then not to be used).
-  if ((int)threadIdx.x < ni) {
-    const int ctx = a.context_lens[mine.seq];
-    const RowSpan sp = row_span(a, ctx);
-    if (ctx != mine.ctx || mine.blk0 < sp.first_blk || mine.blk0 + mine.nblk > sp.last_blk)
-      atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
-  }
 
   // ---- 2. this wave's range of the workgroup's list and its first window of ids
   const int64_t gw = (int64_t)g * NW + wave;
   const int b0 = s_rec[2 + wave];
   int n = s_rec[3 + wave] - b0;
-  bool bad_index = n > kMaxBlocksPerWaveSK;
+  bool bad_index = n > kMaxBlocksPerWaveSK || bad_entry;
   if (bad_index) n = 0;
   // block b0 + j of the list: its item (the last whose first block is at or before it)
   // and the offset of its id; false when no item holds it
@@ -274,7 +310,7 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
     int lo = 0;
 #pragma unroll
     for (int step = kMaxItems / 2; step > 0; step >>= 1)
-      if (lo + step < ni && s_pos[lo + step] <= v) lo += step;
+      if (lo + step < ni && s_item[(lo + step) * kItemWords + 6] <= v) lo += step;
     k = lo;
     const int* it = s_item + lo * kItemWords;
     off = (int64_t)it[7] + (v - it[6]);
@@ -287,10 +323,28 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
     ok0 = locate(lane, rows, off);
     if (ok0) ids = ids_tab[off];
   }
-  bad_index |= __ballot(lane < n && (!ok0 || (unsigned)ids >= (unsigned)a.cache.num_blocks)) != 0;
-  asm volatile("" : "+v"(ids), "+v"(rows));  // landed (tested above): no pending load below
-  if constexpr (kTrace) tm[2] = wall_clock64();
+  bad_index |= __ballot(lane < n && !ok0) != 0;
   int nblk = bad_index ? 0 : n;
+  // The first window's ids, when first used (a wave with an entry first processes its
+  // query): every one in the arena; and the entry's piece and blocks the items'. Else
+  // the wave stops there, flagged.
+  auto check_ids = [&](const Item& it0) __attribute__((always_inline)) {
+    bool bad_ids = __ballot(lane < n && (unsigned)ids >= (unsigned)a.cache.num_blocks) != 0;
+    asm volatile("" : "+v"(ids));  // landed (tested here): no pending load below
+    if (pre > 0) {
+      bool same = it0.seq == pseq && it0.kvh == pkvh;
+#pragma unroll
+      for (int j = 0; j < kPrefetchBlocks; ++j)
+        same = same && (j >= pre || (__builtin_amdgcn_readlane(ids, j) == pid[j] &&
+                                     __builtin_amdgcn_readlane(rows, j) == __builtin_amdgcn_readlane(rows, 0)));
+      bad_ids |= !same;
+    }
+    if (bad_ids) {
+      bad_index = true;
+      nblk = 0;
+    }
+    if constexpr (kTrace) tm[2] = wall_clock64();
+  };
   int cw = 0;  // window of ids / rows; ids_nx / rows_nx hold window cw + 1
   char* const id_slot = id_slots + wave * kIdsBytes;
   bool ok_nx = true;
@@ -338,29 +392,35 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
   };
 
   // The first item's query rows go by direct-to-LDS loads into the last stage, issued
-  // before blocks 0 .. NS-2, so the block stream starts without waiting for them.
-  // fp32 queries (int8 codes) load into registers before the first blocks are issued.
-  QueryColumn<QT, D> qr;
+  // before blocks 0 .. NS-2, so the block stream starts without waiting for them (at
+  // the top, with the blocks of the wave's entry, when it has one). fp32 queries (int8
+  // codes) load into registers before the first blocks are issued.
   QkOperand<D, KF> qop;
   float cf = 0.f;
-  const bool valid = r < G;
   if (nblk > 0) {
     const Item it0 = item_at(s_item, __builtin_amdgcn_readfirstlane(rows));
+    if (pre == 0) check_ids(it0);
     if constexpr (sizeof(QT) == 2) {
-      stage_query<QT, D, G>(a, it0.seq, it0.kvh, lane, stage(NS - 1));
+      if (pre == 0 && nblk > 0) stage_query<QT, D, G>(a, it0.seq, it0.kvh, lane, stage(NS - 1));
       const int first = min(NS - 1, nblk);
-      for (int j = 0; j < first; ++j) issue(j);
-      if (first == 3) wait_vmcnt<3 * S::kLoads>();  // the query has landed
+      if (pre > 0 && pre < first) check_ids(it0);
+      for (int j = pre; j < first && j < nblk; ++j) issue(j);
+      // the query has landed: at least `first` stages' loads were issued after it
+      if (nblk == 0) wait_vmcnt<0>();  // stopped by check_ids: fewer loads
+      else if (first == 3) wait_vmcnt<3 * S::kLoads>();
       else if (first == 2) wait_vmcnt<2 * S::kLoads>();
-      else wait_vmcnt<S::kLoads>();
+      else if (first == 1) wait_vmcnt<S::kLoads>();
+      else wait_vmcnt<0>();
       lds_query<QT, D>(stage(NS - 1), r < G ? r : 0, qg, reinterpret_cast<QueryRaw<D>&>(qr));
       cf = qk_operand_column<QT, D, KF>(qr, valid, a.qk_scale_log2, qop);
+      if (pre > 0 && pre >= first) check_ids(it0);
       if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (values consumed)
     } else {
-      load_query_column<QT, D>(column_ptr(it0), qr);
+      if (pre == 0 && nblk > 0) load_query_column<QT, D>(column_ptr(it0), qr);
       cf = qk_operand_column<QT, D, KF>(qr, valid, a.qk_scale_log2, qop);
+      if (pre > 0) check_ids(it0);
       const int first = min(NS, nblk);
-      for (int j = 0; j < first; ++j) issue(j);
+      for (int j = pre; j < first; ++j) issue(j);
     }
     if (64 < nblk) request_ids(1);
   }
@@ -488,12 +548,21 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
   if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
   if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
   if constexpr (kTrace) tm[4] = wall_clock64();
+  // The plan's lengths must be the device's and its blocks visible to them (a mismatch
+  // raises the index flag; the rows' outputs are then not to be used).
+  if ((int)threadIdx.x < ni) {
+    const int ctx = a.context_lens[mine.seq];
+    const RowSpan sp = row_span(a, ctx);
+    if (ctx != mine.ctx || mine.blk0 < sp.first_blk || mine.blk0 + mine.nblk > sp.last_blk)
+      atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+  }
 
   // ---- 4. every wave is done streaming: the ring takes the workgroup's partials, then
   // the workgroup merges its rows that several of its waves hold (wave w takes items
   // w, w + NW, ...)
   float* const lo_ = reinterpret_cast<float*>(lds);            // [NW][2][G][D]
   float* const lml = lo_ + NW * 2 * G * D;                      // [NW][2][G][2]
+  wait_vmcnt<0>();  // no load into the ring is left (a wave stopped early may have some)
   __syncthreads();
   if constexpr (kTrace) tm[5] = wall_clock64();
   auto put = [&](int which, const float4_t (&v)[NPV + 1], float mv, float lv)

@@ -519,7 +519,9 @@ extern "C" int astr_paged_attention_i8_planned(
     return fail(ASTR_EINVAL, "plan info does not describe a plan for this arena");
   const int64_t wg_words = (int64_t)pi.num_workgroups * (pi.waves_per_workgroup + 3);
   const bool layout =
-      pi.off_workgroups == 0 && pi.off_items == wg_words && pi.num_ids >= 0 &&
+      pi.off_workgroups == 0 && pi.off_waves == wg_words &&
+      pi.off_items == wg_words + (int64_t)pi.num_workgroups * pi.waves_per_workgroup * 6 &&
+      pi.num_ids >= 0 &&
       pi.item_stride >= 1 && pi.item_stride <= 64 &&
       pi.num_items == (int64_t)pi.num_workgroups * pi.item_stride &&
       pi.off_ids == pi.off_items + (int64_t)pi.num_items * 8 &&

@@ -31,7 +31,7 @@ class DecodePlanInfo(ctypes.Structure):
         "num_chunks", "num_chunked", "num_seqs", "num_kv_heads", "window", "tail_blocks",
         "item_stride", "num_tiles", "tile_rows", "tile_ranges", "num_tile_members")] + \
         [(name, ctypes.c_int64) for name in (
-            "off_workgroups", "off_items", "off_ids", "off_chunked", "off_tiles",
+            "off_workgroups", "off_waves", "off_items", "off_ids", "off_chunked", "off_tiles",
             "off_tile_members", "plan_words")]
 
 

@@ -293,7 +293,8 @@ typedef struct astr_decode_plan_info {
   int32_t tile_rows;            /* sequences per prefix tile at most */
   int32_t tile_ranges;          /* key ranges of each shared prefix */
   int32_t num_tile_members;     /* sequences read through a prefix tile */
-  int64_t off_workgroups, off_items, off_ids, off_chunked, off_tiles, off_tile_members;
+  int64_t off_workgroups, off_waves, off_items, off_ids, off_chunked, off_tiles,
+      off_tile_members;
   int64_t plan_words;           /* int32 words of the plan */
 } astr_decode_plan_info;
 

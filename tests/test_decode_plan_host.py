@@ -53,7 +53,8 @@ def _check(tables, lens, hkv, window, wg, nw=8, tile_rows=0, tile_ranges=0, min_
     rc, info, buf = _plan(tables, lens, hkv, window, wg, nw, tile_rows, tile_ranges, min_shared)
     assert rc == 0, _native.last_error()
     n_items = info.num_items
-    wgt = buf[info.off_workgroups:info.off_items].reshape(wg, nw + 3)
+    wgt = buf[info.off_workgroups:info.off_waves].reshape(wg, nw + 3)
+    wents = buf[info.off_waves:info.off_items].reshape(wg, nw, 6)
     items = buf[info.off_items:info.off_ids].reshape(n_items, 8)
     stride = info.item_stride
     assert n_items == wg * stride and 1 <= stride <= 64
@@ -111,6 +112,17 @@ def _check(tables, lens, hkv, window, wg, nw=8, tile_rows=0, tile_ranges=0, min_
             if hi > lo:
                 assert starts[lo] >= cost * w / nw - 1e-9
                 assert starts[hi - 1] < cost * (w + 1) / nw
+            # the wave's entry: its first piece and the ids of up to 3 of its blocks
+            seq, kvh, count = wents[g, w, :3]
+            if hi <= lo:
+                assert count == 0
+                continue
+            k = next(k for k in range(wgt[g, 0], wgt[g, 1])
+                     if items[k, 6] <= lo < items[k, 6] + items[k, 3])
+            assert (seq, kvh) == (items[k, 0], items[k, 1])
+            assert count == min(3, hi - lo, items[k, 6] + items[k, 3] - lo)
+            first = items[k, 2] + lo - items[k, 6]
+            assert (wents[g, w, 3:3 + count] == tables[seq, first:first + count]).all()
     # every row covered once; rows in several items or with tiles are chunked, with
     # consecutive slots (a member's tile ranges first)
     chunk_rows = {(int(s), int(h)): (int(c0), int(n)) for s, h, c0, n in chunked}

@@ -238,9 +238,16 @@ def test_plans_that_contradict_the_call_are_flagged(device):
     other[4] += 1
     with pytest.raises(ValueError):
         cache.paged_attention(0, q, tables, other, **kw)
-    # a block id beyond the arena and an item naming a sequence past the batch
+    # a block id beyond the arena, an item naming a sequence past the batch, and wave
+    # entries whose first block or piece are not the items' (or out of range)
     info = plan.info
-    for offset, value in ((info.off_ids + 3, w.num_blocks + 5), (info.off_items, 10 ** 6)):
+    went = plan.words[info.off_waves:info.off_items].view(-1, 6)
+    w0 = int(torch.nonzero(went[:, 2] > 0)[0, 0])  # a wave that prefetches
+    e0 = info.off_waves + 6 * w0
+    other_id = int((went[w0, 3] + 1) % w.num_blocks)
+    for offset, value in ((info.off_ids + 3, w.num_blocks + 5), (info.off_items, 10 ** 6),
+                          (e0 + 3, other_id), (e0 + 1, (int(went[w0, 1]) + 1) % 8),
+                          (e0 + 0, 10 ** 6), (e0 + 2, 9)):
         words = plan.words.clone()
         plan.words[offset] = value
         with pytest.raises(ValueError):
