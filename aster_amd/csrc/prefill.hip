@@ -343,15 +343,15 @@ __device__ __forceinline__ int convert_v(const char* st, int lane, int half, uin
 
 // The PV MFMAs of one step: weights p = exp2(u * cfe - m) rounded to f16 for the 32 keys
 // of each block pair, against the slab of that pair, and the row sums from the same
-// rounded weights. vmix: the step's blocks were converted with different exponents; the
-// weights of block b then carry 2^(e_b - ve) (vf[b], at most 1, exact on f16) for the
+// rounded weights. The weights of block b carry 2^(e_b - ve) (vf[b], at most 1, exact
+// on f16; 1 unless the step's blocks were converted with different exponents) for the
 // numerator only (scaled in place after the row sums), so that every block's products
 // are in units of 2^-ve.
 template <int D, int NT>
 __device__ __forceinline__ void prefill_pv(const uint4* vt, const float (&u)[NT][16],
                                            const float (&cfe)[NT], const float (&m)[NT],
-                                           int lane, const half8_t& ones, bool vmix,
-                                           const half4_t& vf, float4_t (&acc)[NT][D / 16 + 1]) {
+                                           int lane, const half8_t& ones, const half4_t& vf,
+                                           float4_t (&acc)[NT][D / 16 + 1]) {
   constexpr int NPV = D / 16;
 #pragma unroll
   for (int pp = 0; pp < 2; ++pp) {
@@ -366,7 +366,9 @@ __device__ __forceinline__ void prefill_pv(const uint4* vt, const float (&u)[NT]
 #pragma unroll
     for (int t = 0; t < NT; ++t)
       acc[t][NPV] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop[t], acc[t][NPV], 0, 0, 0);
-    if (vmix) {
+    // (branch-free: vf is 1 but where the step mixes exponents, and a branch here would
+    // split the exponentials from the PV MFMAs they overlap with)
+    {
       const _Float16 f0 = vf[2 * pp], f1 = vf[2 * pp + 1];
 #pragma unroll
       for (int t = 0; t < NT; ++t) pop[t] = pop[t] * half8_t{f0, f0, f0, f0, f1, f1, f1, f1};
@@ -489,7 +491,7 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
                                              const QOp<D> (&qop)[NT],
                                              const float (&cf)[NT], const float (&cfe)[NT],
                                              const int (&lo)[NT], const int (&hi)[NT], int r,
-                                             int qg, const half8_t& ones, bool vmix,
+                                             int qg, const half8_t& ones,
                                              const half4_t& vf,
                                              float4_t (&acc)[NT][D / 16 + 1], float (&m)[NT],
                                              bool& bad_score, const AttnArgs& a,
@@ -639,7 +641,7 @@ __device__ __forceinline__ void prefill_step(const char* cur, const uint4* vt, u
   }
   static_assert(NBK == 4, "two block pairs per step");
   const int lane = qg * 16 + r;
-  prefill_pv<D, NT>(vt, u, cfe, m, lane, ones, vmix, vf, acc);
+  prefill_pv<D, NT>(vt, u, cfe, m, lane, ones, vf, acc);
 }
 
 // N consecutive outputs from fp32, with 16-byte (or 8-byte) stores.
@@ -879,7 +881,7 @@ __device__ __forceinline__ void prefill_unit(const AttnArgs& a, PrefillLds<D>& L
       }
       if (use != 0)
         prefill_step<QT, D, NT>(cur, L.vt[0], use, bounded & use, masks, kb0, qop, cf, cfe, lo, hi,
-                                r, qg, ones, vmix, vf, acc, m, bad_score, a, cols);
+                                r, qg, ones, vf, acc, m, bad_score, a, cols);
     }
     __syncthreads();  // step i's stage may be refilled
   }
