@@ -19,8 +19,11 @@
 // kernel (prefill.hip): a tile holds up to tile_rows such sequences (tile_rows * G
 // query columns, one MFMA column tile of the chunked-prefill kernel) and covers, per kv
 // head, one of tile_ranges equal ranges of their shared blocks. Each member row's
-// partials (one per range, then its own blocks' chunks) take consecutive chunk slots
-// and the chunk-merge kernel merges them; its own blocks are an item like any row's.
+// partials (one per range, then its own blocks' chunks) take consecutive chunk slots;
+// its own blocks are an item like any row's. Where they are one item, that item's
+// workgroup merges its partial (the slot after the ranges') with the ranges' (the tile
+// kernel runs first) into the row's output (out = -2 - the first range's slot); else
+// the chunk-merge kernel does.
 //
 // Plan layout (int32 words, offsets in astr_decode_plan_info):
 //   workgroups  [num_workgroups][waves + 3]: first item, end item, then waves + 1 bounds
@@ -33,9 +36,11 @@
 //   items       [num_workgroups][item_stride][8] (workgroup g's items at g * item_stride,
 //               so a workgroup loads them without its record): sequence, kv head, first
 //               block within the sequence's
-//               block table, blocks, context length, output (-1: the output row, else
-//               the chunk slot of its partial), position of its first block in the
-//               workgroup's list, offset of its first block id in `ids`
+//               block table, blocks, context length, output (-1: the output row; c >= 0:
+//               the chunk slot of its partial; -2 - c: the output row, through the
+//               tile_ranges + 1 chunk slots from c: the ranges' partials, then its own),
+//               position of its first block in the workgroup's list, offset of its first
+//               block id in `ids`
 //   ids         [num_ids]: the physical ids of every sequence's visible blocks, once per
 //               sequence (the items of its kv heads and chunks point into them)
 //   chunked     [num_chunked][4]: sequence, kv head, first chunk slot, chunks
@@ -238,6 +243,12 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
       }
       c0 = member_c0[u.seq] + (int64_t)u.kvh * member_span[u.seq];
       lead_slots = ranges;
+      if (k == 1) {  // merged by its workgroup: no chunk-merge record
+        Unit whole = u;
+        whole.out = (int)(-2 - c0);
+        work.push_back(whole);
+        continue;
+      }
     } else {
       chunk_slots += k;
     }

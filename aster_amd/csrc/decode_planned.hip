@@ -287,7 +287,9 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
             mine.nblk >= 0 && mine.blk0 >= 0 && mine.pos >= 0 &&
             (int64_t)mine.pos + mine.nblk <= total && mine.ids_off >= 0 &&
             (int64_t)mine.ids_off + mine.nblk <= p.info.num_ids && mine.ctx >= 0 &&
-            mine.out >= -1 && mine.out < p.info.num_chunks);
+            ((mine.out >= -1 && mine.out < p.info.num_chunks) ||
+             (mine.out <= -2 && p.info.tile_ranges >= 1 &&
+              -2 - (int64_t)mine.out + p.info.tile_ranges < p.info.num_chunks)));
   if (bad) s_bad = 1;
   __syncthreads();
   if (s_bad) {
@@ -506,7 +508,7 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
     lt += shfl_xor(lt, 32);
     lt *= norm_scale<KF>();  // the factor the PV weights carry
     const bool whole = b0 + pstart == it.pos && b0 + i == it.pos + it.nblk;
-    if (whole && it.out < 0) {
+    if (whole && it.out == -1) {
       if (valid) {
         const float inv = 1.f / fmaxf(lt, FLT_MIN);
         store_lane_out<QT, D>(static_cast<QT*>(a.out) + (int64_t)it.seq * a.o_tok +
@@ -514,8 +516,11 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
                               acc, inv);
       }
     } else if (whole) {
+      // a chunk's partial; or a row after shared-prefix ranges: its own partial, in the
+      // slot after theirs, for the workgroup's merge below
       if (valid) {
-        const int64_t slot = chunk_slot(p, it.out, G) + r;
+        const int own = it.out >= 0 ? it.out : -2 - it.out + p.info.tile_ranges;
+        const int64_t slot = chunk_slot(p, own, G) + r;
         store_lane_f32<D>(a.ws_o + slot * D + qg * (D / 4), acc);
         if (qg == 0) {
           a.ws_ml[slot * 2] = m;
@@ -587,7 +592,15 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
     QT* const orow = it.out < 0 ? static_cast<QT*>(a.out) + (int64_t)it.seq * a.o_tok +
                                       (int64_t)it.kvh * G * a.o_head
                                 : nullptr;
-    if (it.nblk == 0) {  // no visible key (online_attention.py:37): zero
+    // a row after shared-prefix ranges: their partials (chunk slots tb .. tb + R - 1)
+    // join its own pieces
+    const int tb = it.out <= -2 ? -2 - it.out : 0;
+    const int ranges = it.out <= -2 ? p.info.tile_ranges : 0;
+    auto range_src = [&](int j) __attribute__((always_inline)) -> Partial {
+      const int64_t slot = chunk_slot(p, tb + j, G);
+      return Partial{a.ws_o + slot * D, a.ws_ml + slot * 2};
+    };
+    if (it.nblk == 0 && ranges == 0) {  // no visible key (online_attention.py:37): zero
       if (orow != nullptr)
         for (int e = lane; e < G * D; e += kWave)
           orow[(int64_t)(e / D) * a.o_head + e % D] = from_float<QT>(0.f);
@@ -600,7 +613,11 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
       if (s_rec[2 + w] <= it.pos) w0 = w;
       if (s_rec[2 + w] <= it.pos + it.nblk - 1) w1 = w;
     }
-    if (w0 == w1) continue;  // whole in one wave: written there
+    if (w0 == w1) {  // whole in one wave: written there, or (after ranges) in its slot
+      if (ranges > 0)
+        merge_pieces<QT, D, G, merge_group<D, G>()>(a, range_src, ranges + 1, orow, 0, lane);
+      continue;
+    }
     // the piece of wave w0 + j: its last piece when the item begins inside w0's range
     // after another item, else its first; an empty range holds none
     auto src_of = [&](int j) __attribute__((always_inline)) -> Partial {
@@ -617,7 +634,11 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
       const int col = (w * 2 + which) * G;
       return Partial{lo_ + col * D, lml + col * 2};
     };
-    merge_pieces<QT, D, G, merge_group<D, G>()>(a, src_of, w1 - w0 + 1, orow,
+    const int nw = w1 - w0 + 1;
+    auto all_src = [&](int j) __attribute__((always_inline)) -> Partial {
+      return j < nw ? src_of(j) : range_src(j - nw);
+    };
+    merge_pieces<QT, D, G, merge_group<D, G>()>(a, all_src, nw + ranges, orow,
                                                 it.out < 0 ? 0 : chunk_slot(p, it.out, G), lane);
   }
 #if ASTR_TRACE

@@ -205,6 +205,14 @@ def planned_timeline(config="config2", calls=7, tail=None):
                                "mean_end": round(float(t[xcc == x, 4].mean()), 2),
                                "max_end": round(float(t[xcc == x, 4].max()), 2)}
                       for x in np.unique(xcc)}
+    # per number of pieces (rows the wave starts): end time and streaming time per block
+    rep["by_pieces"] = {}
+    for k in sorted(np.unique(np.minimum(pieces[streaming], 4))):
+        m = streaming & (np.minimum(pieces, 4) == k)
+        rep["by_pieces"][f"{k}{'+' if k == 4 else ''}"] = {
+            "waves": int(m.sum()), "mean_end": round(float(t[m, 4].mean()), 2),
+            "mean_blocks": round(float(nblk[m].mean()), 1),
+            "us_per_block": round(float(((t[m, 4] - t[m, 3]) / np.maximum(nblk[m], 1)).mean()), 3)}
     return rep
 
 

@@ -151,6 +151,14 @@ class PagedAttentionStep:
         cache = self.pool.cache
         cache.append(layer, key, value, self.slot_mapping)
         ws_work = self.work
+        plan = self._decode_plan(query, window) if self.partition_tokens == 0 else None
+        if plan is not None:
+            # decode rows on the host schedule (one per step and shape); rows aliasing
+            # shared prefix pages read them once per prefix tile
+            return cache.paged_attention(
+                layer, query, self.block_tables, self.context_lens,
+                max_context_len=self.max_context_len, scale=scale, window=window, out=out,
+                work=ws_work, decode_plan=plan)
         packs = (self._prefix_packs(query.shape[1])
                  if window is None and self.partition_tokens == 0 else None)
         if packs is not None:  # rows aliasing shared prefix pages read them once per pack
@@ -158,12 +166,6 @@ class PagedAttentionStep:
                 layer, query, self.block_tables, self.context_lens,
                 max_context_len=self.max_context_len, scale=scale, out=out, work=ws_work,
                 partition_tokens=0, prefix_packs=packs)
-        plan = self._decode_plan(query, window) if self.partition_tokens == 0 else None
-        if plan is not None:  # decode rows on the host schedule (one per step and shape)
-            return cache.paged_attention(
-                layer, query, self.block_tables, self.context_lens,
-                max_context_len=self.max_context_len, scale=scale, window=window, out=out,
-                work=ws_work, decode_plan=plan)
         return cache.paged_attention(
             layer, query, self.block_tables, self.context_lens,
             max_context_len=self.max_context_len, scale=scale, window=window,

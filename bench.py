@@ -257,19 +257,24 @@ def extra_measurements(device, partition, calls, planned=True, tail=None):
     del cache
     torch.cuda.empty_cache()
     # config 4: HBM fraction on the distinct K/V bytes, effective rate on the logical;
-    # with the prefix-pack plan (as the runner plans decode steps), and without it
+    # on the host schedule with prefix tiles (as the runner plans decode steps), with
+    # the stream-K kernel's prefix packs, and with neither
     w = wl.config4()
     cache, _ = build_arena(w, 2, device)
     q = wl.queries(w, device)
     call, _ = attention_caller(w, cache, q, device, partition)
     unplanned = time_calls(call, calls, 2)
     call, _ = attention_caller(w, cache, q, device, partition, packs=True)
-    avg, med = time_calls(call, calls, 2)
-    entry = hbm_entry(w, avg, med)
-    entry["without_plan_call_us"] = unplanned[0] * 1e3
-    if planned:  # the host schedule of the planned kernel, without prefix packs
+    packs = time_calls(call, calls, 2)
+    if planned:
         call, _ = attention_caller(w, cache, q, device, partition, planned=True, tail=tail)
-        entry["planned_call_us"] = time_calls(call, calls, 2)[0] * 1e3
+        avg, med = time_calls(call, calls, 2)
+    else:
+        avg, med = packs
+    entry = hbm_entry(w, avg, med)
+    entry["mode"] = "planned, prefix tiles" if planned else "stream-K, prefix packs"
+    entry["packs_call_us"] = packs[0] * 1e3
+    entry["without_plan_call_us"] = unplanned[0] * 1e3
     entry["logical_effective_gbs"] = entry.pop("achieved_gbs")
     entry["logical_frac"] = entry.pop("frac")
     unique = w.unique_kv_bytes() + (w.algorithmic_bytes() - w.attended_tokens * w.num_kv_heads

@@ -141,6 +141,13 @@ def _check(tables, lens, hkv, window, wg, nw=8, tile_rows=0, tile_ranges=0, min_
                 assert a0 + an == b0
             if len(parts) == 1 and not tparts:
                 assert parts[0][2] == -1 and (s, h) not in chunk_rows
+            elif len(own) == 1 and own[0][2] <= -2:
+                # a member row whose own blocks are one item: its workgroup merges the
+                # ranges' slots and its own (the next one)
+                tb = -2 - own[0][2]
+                assert (s, h) not in chunk_rows and len(tparts) == ranges
+                assert [p[2] for p in tparts] == list(range(tb, tb + ranges))
+                slots += list(range(tb, tb + ranges + 1))
             else:
                 c0, n = chunk_rows[(s, h)]
                 assert n == len(parts) and len(tparts) in (0, ranges)
