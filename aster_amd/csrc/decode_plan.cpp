@@ -30,7 +30,7 @@
 //               of the workgroup's block list: wave w streams its blocks [bound[w],
 //               bound[w + 1]) (positions counted from the workgroup's first block)
 //   waves       [num_workgroups * waves][6]: the wave's first piece (sequence, kv head),
-//               how many of its first blocks follow (up to 3, all of that piece) and
+//               how many of its first blocks follow (up to 2, all of that piece) and
 //               their physical ids, so that the wave issues them before it reads its
 //               items
 //   items       [num_workgroups][item_stride][8] (workgroup g's items at g * item_stride,
@@ -67,7 +67,11 @@ namespace plan {
 constexpr int kBlockTokens = 16;
 constexpr int64_t kBlockCost = 50, kRowCost = 135;
 constexpr int kItemWords = 8, kChunkedWords = 4, kTileWords = 8, kMemberWords = 3;
-constexpr int kWaveWords = 6, kPrefetchBlocks = 3;
+constexpr int kWaveWords = 6;
+// first blocks a wave issues from its entry (of the entry's 3 id slots): two measured
+// as fast as three on configs 2 and 5 (62.0-62.6 against 62.9 us on config 2), with a
+// smaller burst at the kernel's start
+constexpr int kPrefetchBlocks = 2;
 constexpr int kMaxItemsPerWorkgroup = 64;  // the kernel's LDS item table
 constexpr int kMaxBlocksPerWave = 1024;    // the kernel's block list windows
 constexpr int kMaxTileRanges = 16;

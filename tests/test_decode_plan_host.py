@@ -112,7 +112,7 @@ def _check(tables, lens, hkv, window, wg, nw=8, tile_rows=0, tile_ranges=0, min_
             if hi > lo:
                 assert starts[lo] >= cost * w / nw - 1e-9
                 assert starts[hi - 1] < cost * (w + 1) / nw
-            # the wave's entry: its first piece and the ids of up to 3 of its blocks
+            # the wave's entry: its first piece and the ids of up to 2 of its blocks
             seq, kvh, count = wents[g, w, :3]
             if hi <= lo:
                 assert count == 0
@@ -120,7 +120,7 @@ def _check(tables, lens, hkv, window, wg, nw=8, tile_rows=0, tile_ranges=0, min_
             k = next(k for k in range(wgt[g, 0], wgt[g, 1])
                      if items[k, 6] <= lo < items[k, 6] + items[k, 3])
             assert (seq, kvh) == (items[k, 0], items[k, 1])
-            assert count == min(3, hi - lo, items[k, 6] + items[k, 3] - lo)
+            assert count == min(2, hi - lo, items[k, 6] + items[k, 3] - lo)
             first = items[k, 2] + lo - items[k, 6]
             assert (wents[g, w, 3:3 + count] == tables[seq, first:first + count]).all()
     # every row covered once; rows in several items or with tiles are chunked, with
