@@ -11,7 +11,8 @@ PagedAttentionRunner) and a C-ABI library of hand-written HIP kernels
 from .attention_backend import BACKEND, AttentionWork, KernelWork, UnsupportedAttentionBackend
 from .kv_quantization import KVQuantization, QuantizedKV, quantize_kv
 from .offload import PagedStateArchive
-from .online_attention import AttentionBlock, SoftmaxState, merge_softmax, online_attention
+from .online_attention import (AttentionBlock, SoftmaxState, merge_softmax, online_attention,
+                               online_attention_statistics)
 from .paged_kv import DEFAULT_PARTITION_TOKENS, PagedKVCache
 from .paged_pool import (CacheCapacityError, KVStateCodec, PagedSequence, PagedStatePool, PageRef,
                          PageView, SlotReservation, StateError)
@@ -24,5 +25,5 @@ __all__ = [
     "KVStateCodec", "PagedStatePool", "PagedSequence", "PageRef", "PageView", "SlotReservation",
     "StateError", "CacheCapacityError", "PagedStateArchive", "PagedAttentionRunner",
     "PagedAttentionStep", "PrefixPacks", "plan_prefix_packs", "AttentionBlock", "SoftmaxState",
-    "merge_softmax", "online_attention",
+    "merge_softmax", "online_attention", "online_attention_statistics",
 ]

@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "astr_paged_attention_i8",
     "astr_paged_attention_varlen_i8",
     "astr_paged_attention_i8_noalloc",
+    "astr_paged_attention_i8_statistics",
     "astr_paged_attention_i8_shared",
     "astr_paged_attention_i8_workspace_bytes",
     "astr_paged_attention_i8_shared_workspace_bytes",
@@ -107,6 +108,11 @@ def lib():
             c_i32, c_i32, ctypes.c_float, c_i32, c_i32, c_vp, c_vp,
         ]
         handle.astr_paged_attention_i8_noalloc.restype = ctypes.c_int
+        handle.astr_paged_attention_i8_statistics.argtypes = [
+            desc_p, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_i32,
+            c_i32, c_i32, ctypes.c_float, c_i32, c_i32, c_vp, c_sz, c_vp, c_vp,
+        ]
+        handle.astr_paged_attention_i8_statistics.restype = ctypes.c_int
         handle.astr_paged_attention_i8_shared.argtypes = [
             desc_p, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i32, c_vp, c_i32,
             c_i32, c_i32, ctypes.c_float, c_i32, c_vp, c_i32, c_i32, c_vp, c_sz, c_vp, c_vp,

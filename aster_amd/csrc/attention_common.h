@@ -87,8 +87,20 @@ struct AttnArgs {
   int32_t* ws_pack;     // stream-K: per sequence, [pack column k * pack_rows + p or -1,
                         // the pack's first block, its end (the per-head order), the
                         // rows with blocks before the pack]
+  // statistics mode (fp32 queries, fixed partitions): per (token row, query head) the
+  // exact maximum score and the mass sum(exp(score - maximum)) at stats[(t * Hq + h) * 2
+  // + {0, 1}], and out holds the unnormalised numerator; nullptr: normalised rows
+  float* stats;
   int32_t* err_flag;
 };
+
+// Statistics of one row from its merged base-2 state (maximum m, mass l, numerator
+// acc): the maximum back in score units; a row that saw no key keeps (-inf, 0)
+// (online_attention.py:163-170 starts every row there).
+__device__ __forceinline__ void store_row_stats(float* stats, int64_t row, float m, float l) {
+  stats[row * 2] = l > 0.f ? m * (1.f / kLog2e) : -INFINITY;
+  stats[row * 2 + 1] = l;
+}
 
 // Query/output token rows [begin, begin + count) of sequence `seq` (count is
 // returned). A q_start entry that is negative, decreasing or beyond num_q_tokens

@@ -88,7 +88,12 @@ __device__ void finish_partition(const AttnArgs& a, Shared<G, D>& sh, const RowP
     const int h = head0 + g;
     if (!split) {
       QT* op = static_cast<QT*>(a.out) + (int64_t)tok * a.o_tok + (int64_t)h * a.o_head;
-      op[d] = from_float<QT>(O / fmaxf(L, FLT_MIN));
+      if (a.stats != nullptr) {  // the row's state itself
+        op[d] = from_float<QT>(O);
+        if (d == 0) store_row_stats(a.stats, (int64_t)tok * a.num_q_heads + h, M, L);
+      } else {
+        op[d] = from_float<QT>(O / fmaxf(L, FLT_MIN));
+      }
     } else {
       const int64_t base = ((int64_t)seq * a.num_q_heads + h) * a.max_parts + part;
       a.ws_o[base * D + d] = O;
@@ -298,6 +303,9 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
   const float* vsbase = a.cache.v_scales + (int64_t)kvh * a.cache.scale_head_stride + lrow;
   const bool masks = a.cache.key_valid != nullptr;  // key padding bytes of the token rows
   const uint8_t* kvbase = masks ? a.cache.key_valid + lrow : nullptr;
+  // statistics mode raises the reference on every larger score, so that it ends as the
+  // row's exact maximum
+  const float slack = a.stats != nullptr ? 0.f : kRescaleSlack;
   auto load = [&](int phys, ValuTile<NL>& t) __attribute__((always_inline)) {
     const int8_t* kp = kbase + (int64_t)phys * a.cache.code_block_stride;
     const int8_t* vp = vbase + (int64_t)phys * a.cache.code_block_stride;
@@ -349,7 +357,7 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(AttnArgs a) {
         const float v = s[j][g] * f;
         nonfinite |= valid && !__builtin_isfinite(v);
         s[j][g] = valid ? v : -INFINITY;
-        need |= s[j][g] > m[g] + kRescaleSlack;
+        need |= s[j][g] > m[g] + slack;
       }
     }
     if (__ballot(nonfinite) != 0) bad_score = true;
@@ -481,7 +489,10 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnArgs a) {
     }
   }
   QT* out = static_cast<QT*>(a.out) + (int64_t)tok * a.o_tok + (int64_t)h * a.o_head;
-  const float inv_l = 1.f / fmaxf(L, FLT_MIN);
+  // statistics mode: the merged state itself
+  const float inv_l = a.stats != nullptr ? 1.f : 1.f / fmaxf(L, FLT_MIN);
+  if (a.stats != nullptr && lane == 0)
+    store_row_stats(a.stats, (int64_t)tok * a.num_q_heads + h, M, L);
 #pragma unroll
   for (int e = 0; e < kPerLane; ++e) {
     const int d = lane + e * kWave;

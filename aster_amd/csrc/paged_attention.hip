@@ -199,7 +199,7 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
                     int32_t partition_tokens, void* workspace, size_t workspace_bytes,
                     int32_t* err_flag, void* stream, bool fixed_scratch = false,
                     const int32_t* packs = nullptr, int32_t num_packs = 0,
-                    int32_t pack_rows = 0) {
+                    int32_t pack_rows = 0, float* stats = nullptr) {
   using namespace astr;
   using namespace astr::attn;
   if (cache == nullptr || err_flag == nullptr)
@@ -231,7 +231,8 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
     return fail(ASTR_EINVAL, "partition_tokens %d must be 0 (auto) or a positive multiple of %d "
                 "up to %d", partition_tokens, kBlockTokens * kWaves,
                 kBlockTokens * kWaves * kMaxBlocksPerWave);
-  const bool streamk = use_streamk(q_dtype, partition_tokens, num_seqs);
+  // statistics come from the fixed-partition kernels (fp32 queries, exact VALU)
+  const bool streamk = stats == nullptr && use_streamk(q_dtype, partition_tokens, num_seqs);
   const int group = num_q_heads / cache->num_kv_heads;
   if (num_packs < 0) return fail(ASTR_EINVAL, "num_packs must be >= 0");
   if (num_packs > 0) {
@@ -336,6 +337,7 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
     a.ws_o = reinterpret_cast<float*>(base + ws.seq_bytes);
     a.ws_ml = reinterpret_cast<float*>(base + ws.seq_bytes + ws.o_bytes);
   }
+  a.stats = stats;
   a.err_flag = err_flag;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rc = streamk ? launch_streamk(a, q_dtype, s) : launch_partitioned(a, q_dtype, s);
@@ -393,6 +395,24 @@ extern "C" int astr_paged_attention_i8_shared(
                          block_table_stride, context_lens, num_seqs, num_q_heads, max_context_len,
                          scale, window, 0, workspace, workspace_bytes, err_flag, stream, false,
                          packs, num_packs, rows_per_pack);
+}
+
+extern "C" int astr_paged_attention_i8_statistics(
+    const astr_paged_kv* cache, const float* query, int64_t q_token_stride,
+    int64_t q_head_stride, float* weighted, int64_t w_token_stride, int64_t w_head_stride,
+    float* stats, const int32_t* block_tables, int32_t block_table_stride,
+    const int32_t* context_lens, int32_t num_seqs, int32_t num_q_heads, int32_t max_context_len,
+    float scale, int32_t window, int32_t partition_tokens, void* workspace,
+    size_t workspace_bytes, int32_t* err_flag, void* stream) {
+  astr::CallRange range("astr_paged_attention_i8_statistics");
+  if (stats == nullptr || (reinterpret_cast<uintptr_t>(stats) & 7u) != 0)
+    return astr::fail(ASTR_EINVAL, "an 8-byte aligned stats array [num_seqs, num_q_heads, 2] "
+                      "is required");
+  return paged_attention(cache, query, ASTR_F32, q_token_stride, q_head_stride, weighted,
+                         w_token_stride, w_head_stride, nullptr, num_seqs, 1, 1, block_tables,
+                         block_table_stride, context_lens, num_seqs, num_q_heads, max_context_len,
+                         scale, window, partition_tokens, workspace, workspace_bytes, err_flag,
+                         stream, false, nullptr, 0, 0, stats);
 }
 
 // ---- allocation-free decode entry point: split-K partials in a fixed device array

@@ -1,23 +1,24 @@
 """Op-level attention over explicit KV pages on the HIP path: the reference's
-``online_attention`` and ``merge_softmax`` (src/aster/optimization/online_attention.py)
-for callers that hold ``AttentionBlock`` pages rather than a paged arena.
+``online_attention``, ``online_attention_statistics`` and ``merge_softmax``
+(src/aster/optimization/online_attention.py) for callers that hold ``AttentionBlock``
+pages rather than a paged arena.
 
-``online_attention`` checks its arguments as the reference does (same exceptions and
-messages, online_attention.py:89-147), then lays the blocks' quantized codes and
+Both attention calls check their arguments as the reference does (same exceptions and
+messages, online_attention.py:89-147), then lay the blocks' quantized codes and
 scales into a transient single-layer arena. Each block's token ``t`` goes to
 absolute position ``offset + t``; positions no block covers, and key padding, become
 padding keys. Each query token then attends as one decode row of the library's
-paged kernels, its context ending at its own position. That gives the causal mask
-(``k <= p``) and the window (``k > p - window``) of online_attention.py:175-188.
-``merge_softmax`` runs a HIP kernel over fp32 states (``astr_merge_softmax_f32``).
+paged kernels, its context ending at its own position (causal) or at the last key.
+That gives the causal mask (``k <= p``) and the window (``k > p - window``) of
+online_attention.py:175-188. ``online_attention`` returns the rows' outputs;
+``online_attention_statistics`` the rows' unnormalised states from the exact fp32
+decode kernels (``astr_paged_attention_i8_statistics``). ``merge_softmax`` runs a
+HIP kernel over fp32 states (``astr_merge_softmax_f32``).
 
 Not served (``UnsupportedAttentionBackend``, never a silent downgrade):
   * plain tensor K/V, since the path attends to quantized pages;
   * blocks of different code formats, and value widths unlike the key width;
-  * windows without causality;
-  * fp64 queries or states;
-  * ``online_attention_statistics``, because the kernels return normalised rows,
-    not the unnormalised (maximum, mass, numerator) state.
+  * fp64 queries or states.
 """
 
 from __future__ import annotations
@@ -181,48 +182,39 @@ def _check(query, blocks, query_positions, causal, window, query_padding, scale,
     return query_padding, scale, heads, value_width
 
 
-@torch.no_grad()
-def online_attention(query, blocks, *, query_positions, causal=True, window=None,
-                     query_padding=None, scale=None, query_block_size=32, key_block_size=64,
-                     work=None):
-    """``online_attention`` (online_attention.py:217-219) on the HIP kernels:
-    ``query`` ``[B, Hq, Q, D]`` (fp32/fp16/bf16, device), ``blocks`` of
-    ``QuantizedKV`` pages, ``query_positions`` ``[B, Q]``; returns ``[B, Hq, Q, D]``
-    in the query dtype. The tile sizes are checked as the reference checks them; the
-    kernels' own tiles (16-token blocks, one decode row per query token) are what
-    ``work`` records."""
-    blocks = tuple(blocks)
-    query_padding, scale, heads, value_width = _check(
-        query, blocks, query_positions, causal, window, query_padding, scale,
-        query_block_size, key_block_size)
-    if query.device.type != "cuda":
-        raise UnsupportedAttentionBackend("hip_int8_paged attends to device pages")
-    if query.dtype not in (torch.float32, torch.float16, torch.bfloat16):
-        raise UnsupportedAttentionBackend("hip_int8_paged takes fp32/fp16/bf16 queries")
-    if not all(isinstance(b.key, QuantizedKV) and isinstance(b.value, QuantizedKV) for b in blocks):
-        raise UnsupportedAttentionBackend("hip_int8_paged attends to quantized KV pages")
-    formats = {_FORMAT_OF_DTYPE.get(v.values.dtype) for b in blocks for v in (b.key, b.value)}
-    if len(formats) != 1 or None in formats:
-        raise UnsupportedAttentionBackend("hip_int8_paged needs one KV code format per call")
-    batch, query_heads, queries, width = query.shape
-    if value_width != width:
-        raise UnsupportedAttentionBackend("hip_int8_paged needs equal key and value widths")
-    if window is not None and not causal:
-        raise UnsupportedAttentionBackend("hip_int8_paged windows are causal")
-    device = query.device
-    positions = query_positions.to(torch.int64)
+class _Rows:
+    """The transient arena of one call and its decode rows (one per query token)."""
 
-    # transient arena: row b owns blocks [b * nb, (b + 1) * nb) holding positions from
-    # `base` (the first page's offset rounded down to a block) on: causal and window
-    # masks are translation invariant, so memory and streamed blocks follow the span of
-    # keys, not their absolute offsets. Positions between pages are padding keys.
+    def __init__(self, cache, queries, tables, ctx, span, window):
+        self.cache, self.queries, self.tables, self.ctx = cache, queries, tables, ctx
+        self.span, self.window = span, window
+
+
+def _rows(query, blocks, positions, causal, window, query_padding, heads, width, fmt):
+    """Lay the blocks' codes and scales into a transient single-layer arena and give
+    every query token a decode row whose visible keys are the reference's
+    (online_attention.py:175-188).
+
+    Row ``b`` owns arena blocks ``[b * nb, (b + 1) * nb)`` holding positions from
+    ``base`` (the first page's offset rounded down to a block) on: causal and window
+    masks are translation invariant, so memory and streamed blocks follow the span of
+    keys, not their absolute offsets. Positions between pages are padding keys.
+
+    * causal: the row's context ends at its own position (``k <= p``), capped at the
+      last key unless a window counts back from the position (the kernels' window
+      keeps the ``window`` keys that end the context, ``k > p - window``);
+    * not causal: the context ends at the last key; with a window the first visible
+      key ``p - window + 1`` falls inside a block that the row reads through a copy of
+      its own, whose padding bytes hide the keys before it, and the row's table goes on
+      with the shared blocks after it.
+
+    A padded query, or one whose window or causal bound leaves no key, sees nothing
+    (context 0) and comes out as the empty state."""
+    batch, queries = positions.shape
+    device = positions.device
     base = min(b.offset for b in blocks) // BLOCK * BLOCK
     end = max(b.offset + _length(b.key) for b in blocks)  # one past the last key
-    # one decode row per query token, its context ending at its position (causal), or
-    # at the last key; keys past the last page are never visible, so a causal row's
-    # context stops there unless a window counts back from its own position (then a
-    # row whose window starts past the last key sees nothing); a padded query, or one
-    # before every key, sees nothing and comes out zero
+    first = None  # not causal, windowed: the first visible key of each row, from base
     if causal:
         ctx = positions + 1 - base
         if window is None:
@@ -230,17 +222,22 @@ def online_attention(query, blocks, *, query_positions, causal=True, window=None
         else:
             ctx = torch.where(positions + 1 - window >= end, torch.zeros_like(ctx), ctx)
         ctx = torch.clamp(ctx, min=0)
+        kernel_window = window
     else:
         ctx = torch.full_like(positions, end - base)
+        if window is not None:
+            first = torch.clamp(positions - window + 1 - base, min=0)
+            ctx = torch.where(first >= end - base, torch.zeros_like(ctx), ctx)
+        kernel_window = None
     if query_padding is not None:
         ctx = torch.where(query_padding, ctx, torch.zeros_like(ctx))
     span = max(int(ctx.max()), 1)
     if span >= 2**31:
         raise UnsupportedAttentionBackend("hip_int8_paged contexts are int32")
     nb = -(-span // BLOCK)
-    cache = PagedKVCache(num_blocks=batch * nb, num_layers=1, num_kv_heads=heads,
-                         head_dim=width, device=device,
-                         quantization=KVQuantization(formats.pop()))
+    own = batch * queries if first is not None else 0  # per-row first-block copies
+    cache = PagedKVCache(num_blocks=batch * nb + own, num_layers=1, num_kv_heads=heads,
+                         head_dim=width, device=device, quantization=KVQuantization(fmt))
     cache._enable_padding()
     cache.key_valid.zero_()
     rows = torch.arange(batch, device=device)[:, None]
@@ -258,17 +255,103 @@ def online_attention(query, blocks, *, query_positions, causal=True, window=None
                 else block.padding[:, keep].to(torch.uint8))
         cache.key_valid[blk, slot] = real
 
-    ctx = ctx.reshape(-1).to(torch.int32).contiguous()
-    tables = (rows * nb + torch.arange(nb, device=device)[None, :]).to(torch.int32)
-    tables = tables.repeat_interleave(queries, dim=0).contiguous()  # [B * Q, nb]
-    q_rows = query.permute(0, 2, 1, 3).reshape(batch * queries, query_heads, width).contiguous()
-    out = cache.paged_attention(0, q_rows, tables, ctx, max_context_len=nb * BLOCK, scale=scale,
-                                window=window if causal else None, check=True)
-    if work is not None:
-        visible = int(((ctx.to(torch.int64) + BLOCK - 1) // BLOCK).sum())
-        work.query_tiles += batch * queries
-        work.key_tiles += visible * heads
-        work.max_query_tile = max(work.max_query_tile, 1)
-        work.max_key_tile = max(work.max_key_tile, BLOCK)
-        work.max_score_elements = max(work.max_score_elements, query_heads * BLOCK)
+    ctx = ctx.reshape(-1)
+    seq_rows = torch.arange(batch * queries, device=device) // queries       # [B * Q]
+    cols = torch.arange(nb, device=device)[None, :]
+    if first is None:
+        tables = (seq_rows[:, None] * nb + cols).to(torch.int32)
+    else:
+        lead = torch.clamp(first.reshape(-1), max=nb * BLOCK - 1) // BLOCK   # [B * Q]
+        src = seq_rows * nb + lead
+        dst = batch * nb + torch.arange(batch * queries, device=device)
+        cache.codes[dst] = cache.codes[src]
+        cache.scales[dst] = cache.scales[src]
+        hide = torch.arange(BLOCK, device=device)[None, :] < (first.reshape(-1) - lead * BLOCK)[:, None]
+        cache.key_valid[dst] = torch.where(hide, torch.zeros_like(cache.key_valid[src]),
+                                           cache.key_valid[src])
+        shared = seq_rows[:, None] * nb + torch.clamp(lead[:, None] + cols, max=nb - 1)
+        tables = torch.where(cols == 0, dst[:, None], shared).to(torch.int32)
+        ctx = torch.where(ctx > 0, ctx - lead * BLOCK, ctx)
+    q_rows = query.permute(0, 2, 1, 3).reshape(batch * queries, query.shape[1], width)
+    return _Rows(cache, q_rows, tables.contiguous(), ctx.to(torch.int32).contiguous(), nb * BLOCK,
+                 kernel_window)
+
+
+def _prepare(query, blocks, query_positions, causal, window, query_padding, scale,
+             query_block_size, key_block_size):
+    """The reference's checks, then the HIP path's own gates (never a silent downgrade)."""
+    blocks = tuple(blocks)
+    query_padding, scale, heads, value_width = _check(
+        query, blocks, query_positions, causal, window, query_padding, scale,
+        query_block_size, key_block_size)
+    if query.device.type != "cuda":
+        raise UnsupportedAttentionBackend("hip_int8_paged attends to device pages")
+    if query.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise UnsupportedAttentionBackend("hip_int8_paged takes fp32/fp16/bf16 queries")
+    if not all(isinstance(b.key, QuantizedKV) and isinstance(b.value, QuantizedKV) for b in blocks):
+        raise UnsupportedAttentionBackend("hip_int8_paged attends to quantized KV pages")
+    formats = {_FORMAT_OF_DTYPE.get(v.values.dtype) for b in blocks for v in (b.key, b.value)}
+    if len(formats) != 1 or None in formats:
+        raise UnsupportedAttentionBackend("hip_int8_paged needs one KV code format per call")
+    if value_width != query.shape[-1]:
+        raise UnsupportedAttentionBackend("hip_int8_paged needs equal key and value widths")
+    rows = _rows(query, blocks, query_positions.to(torch.int64), causal, window, query_padding,
+                 heads, query.shape[-1], formats.pop())
+    return rows, scale, heads
+
+
+def _record(work, rows, heads, query_heads):
+    if work is None:
+        return
+    visible = int(((rows.ctx.to(torch.int64) + BLOCK - 1) // BLOCK).sum())
+    work.query_tiles += rows.ctx.numel()
+    work.key_tiles += visible * heads
+    work.max_query_tile = max(work.max_query_tile, 1)
+    work.max_key_tile = max(work.max_key_tile, BLOCK)
+    work.max_score_elements = max(work.max_score_elements, query_heads * BLOCK)
+
+
+@torch.no_grad()
+def online_attention_statistics(query, blocks, *, query_positions, causal=True, window=None,
+                                query_padding=None, scale=None, query_block_size=32,
+                                key_block_size=64, work=None):
+    """``online_attention_statistics`` (online_attention.py:74-214) on the HIP kernels:
+    the same arguments as :func:`online_attention`; returns the fp32
+    :class:`SoftmaxState` with ``maximum`` and ``mass`` ``[B, Hkv, G, Q]`` and
+    ``weighted`` ``[B, Hkv, G, Q, D]``. ``maximum`` is the largest visible score,
+    ``mass`` the sum of ``exp(score - maximum)`` and ``weighted`` the numerator; a row
+    that sees no key keeps the initial state ``(-inf, 0, 0)``. The query enters the
+    kernels in fp32 (the reference's accumulator dtype, :158-159), on the exact fp32
+    fixed-partition decode kernels."""
+    rows, scale, heads = _prepare(query, blocks, query_positions, causal, window, query_padding,
+                                  scale, query_block_size, key_block_size)
+    batch, query_heads, queries, width = query.shape
+    maximum, mass, weighted = rows.cache.paged_attention_statistics(
+        0, rows.queries.float().contiguous(), rows.tables, rows.ctx,
+        max_context_len=rows.span, scale=scale, window=rows.window, check=True)
+    _record(work, rows, heads, query_heads)
+    groups = query_heads // heads
+    shape = (batch, queries, heads, groups)
+    return SoftmaxState(maximum.reshape(shape).permute(0, 2, 3, 1).contiguous(),
+                        mass.reshape(shape).permute(0, 2, 3, 1).contiguous(),
+                        weighted.reshape(*shape, width).permute(0, 2, 3, 1, 4).contiguous())
+
+
+@torch.no_grad()
+def online_attention(query, blocks, *, query_positions, causal=True, window=None,
+                     query_padding=None, scale=None, query_block_size=32, key_block_size=64,
+                     work=None):
+    """``online_attention`` (online_attention.py:217-219) on the HIP kernels:
+    ``query`` ``[B, Hq, Q, D]`` (fp32/fp16/bf16, device), ``blocks`` of
+    ``QuantizedKV`` pages, ``query_positions`` ``[B, Q]``; returns ``[B, Hq, Q, D]``
+    in the query dtype. The tile sizes are checked as the reference checks them; the
+    kernels' own tiles (16-token blocks, one decode row per query token) are what
+    ``work`` records."""
+    rows, scale, heads = _prepare(query, blocks, query_positions, causal, window, query_padding,
+                                  scale, query_block_size, key_block_size)
+    batch, query_heads, queries, width = query.shape
+    out = rows.cache.paged_attention(0, rows.queries.contiguous(), rows.tables, rows.ctx,
+                                     max_context_len=rows.span, scale=scale, window=rows.window,
+                                     check=True)
+    _record(work, rows, heads, query_heads)
     return out.reshape(batch, queries, query_heads, width).permute(0, 2, 1, 3).contiguous()

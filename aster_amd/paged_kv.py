@@ -441,6 +441,50 @@ class PagedKVCache:
             self.raise_errors()
         return out
 
+    def paged_attention_statistics(self, layer, query, block_tables, context_lens, *,
+                                   max_context_len, scale=None, window=None,
+                                   partition_tokens=DEFAULT_PARTITION_TOKENS, check=False):
+        """Decode rows' softmax states instead of their outputs
+        (``online_attention_statistics``, online_attention.py:74-214): ``query`` fp32
+        ``[S, Hq, D]``, other arguments as :meth:`paged_attention`. Returns
+        ``(maximum, mass, weighted)``: ``[S, Hq]``, ``[S, Hq]`` and ``[S, Hq, D]`` fp32,
+        the largest visible score, ``sum(exp(score - maximum))`` and the numerator
+        ``sum(exp(score - maximum) * value)``; a row with no visible key gets
+        ``(-inf, 0, 0)``."""
+        if (query.ndim != 3 or query.shape[-1] != self.head_dim or query.device != self.device
+                or query.dtype != torch.float32 or query.stride(-1) != 1):
+            raise ValueError("query must be fp32 [tokens, num_q_heads, head_dim] on the cache "
+                             "device with contiguous rows")
+        num_seqs, num_q_heads = query.shape[0], query.shape[1]
+        if num_q_heads % self.num_kv_heads:
+            raise ValueError("Query heads must divide into KV groups")
+        _check_index(block_tables, "block_tables", 2, self.device)
+        _check_index(context_lens, "context_lens", 1, self.device)
+        if block_tables.shape[0] != num_seqs or context_lens.shape[0] != num_seqs:
+            raise ValueError("block_tables/context_lens must have one row per query row")
+        if max_context_len > block_tables.shape[1] * self.block_size:
+            raise ValueError("max_context_len exceeds the block table capacity")
+        scale = self.head_dim ** -0.5 if scale is None else float(scale)
+        if not math.isfinite(scale) or scale <= 0:
+            raise ValueError("Attention scale must be finite and positive")
+        if window is not None and (type(window) is not int or window < 1):
+            raise ValueError("Invalid causal/window semantics")
+        weighted = torch.empty_like(query)
+        stats = torch.empty((num_seqs, num_q_heads, 2), dtype=torch.float32, device=self.device)
+        need = self.workspace_bytes(num_seqs, num_q_heads, max_context_len, partition_tokens)
+        ws = self._scratch(need).data_ptr() if need else None
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        rc = _native.lib().astr_paged_attention_i8_statistics(
+            self._descs[layer], query.data_ptr(), query.stride(0), query.stride(1),
+            weighted.data_ptr(), weighted.stride(0), weighted.stride(1), stats.data_ptr(),
+            block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(), num_seqs,
+            num_q_heads, max_context_len, scale, window or 0, partition_tokens, ws, need,
+            self.err_flag.data_ptr(), stream)
+        _native.check(rc, "paged_attention_statistics")
+        if check:
+            self.raise_errors()
+        return stats[..., 0], stats[..., 1], weighted
+
 
 def _check_rows(tensor, name, heads, width, device):
     if (not isinstance(tensor, torch.Tensor) or tensor.ndim != 3 or tensor.shape[1] != heads

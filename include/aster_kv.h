@@ -159,6 +159,34 @@ int astr_paged_attention_i8(const astr_paged_kv* cache, const void* query, int32
                             int32_t* err_flag, void* stream);
 
 /*
+ * The unnormalised softmax state of each decode row instead of its output: replaces
+ * online_attention_statistics (src/aster/optimization/online_attention.py:74-214),
+ * whose SoftmaxState (:29-39) is (maximum, mass, weighted) per query row and head.
+ *   query: fp32 [num_seqs, num_q_heads, head_dim] (strides in elements).
+ *   weighted: fp32 [num_seqs, num_q_heads, head_dim], sum over visible keys of
+ *              exp(score - maximum) * value.
+ *   stats: fp32 [num_seqs, num_q_heads, 2], 8-byte aligned: (maximum, mass) with
+ *              maximum the largest visible score q.k * scale and mass the sum of
+ *              exp(score - maximum); a row with no visible key gets (-inf, 0) and
+ *              weighted 0 (the reference's initial state, online_attention.py:163-170).
+ *   Other arguments as astr_paged_attention_i8, whose fixed-partition kernels in exact
+ *   fp32 arithmetic serve this call (workspace sized by
+ *   astr_paged_attention_i8_workspace_bytes).
+ * weighted / max(mass, FLT_MIN) is the astr_paged_attention_i8 output up to the
+ * rounding of the division; maximum + log(mass) is the row's log-sum-exp.
+ */
+int astr_paged_attention_i8_statistics(const astr_paged_kv* cache, const float* query,
+                                       int64_t q_token_stride, int64_t q_head_stride,
+                                       float* weighted, int64_t w_token_stride,
+                                       int64_t w_head_stride, float* stats,
+                                       const int32_t* block_tables, int32_t block_table_stride,
+                                       const int32_t* context_lens, int32_t num_seqs,
+                                       int32_t num_q_heads, int32_t max_context_len,
+                                       float scale, int32_t window, int32_t partition_tokens,
+                                       void* workspace, size_t workspace_bytes,
+                                       int32_t* err_flag, void* stream);
+
+/*
  * astr_paged_attention_i8 without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid allocation): no counterpart in the reference. The split-K partials live

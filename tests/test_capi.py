@@ -122,6 +122,24 @@ def test_attention_argument_errors_need_no_device():
     del lib
 
 
+def test_statistics_argument_errors_need_no_device():
+    def stats_call(desc, stats=16, **kw):
+        args = dict(query=16, q_tok=128, q_head=128, w=16, w_tok=128, w_head=128, stats=stats,
+                    tables=16, bt_stride=4, lens=16, num_seqs=1, hq=1, max_ctx=64, scale=0.1,
+                    window=0, part=512, ws=None, ws_bytes=0, flag=16)
+        args.update(kw)
+        return _native.lib().astr_paged_attention_i8_statistics(
+            ctypes.byref(desc) if desc is not None else None, *args.values(), None)
+
+    assert stats_call(_desc(), stats=None) == _native.ASTR_EINVAL
+    assert "stats" in _native.last_error()
+    assert stats_call(_desc(), stats=20) == _native.ASTR_EINVAL  # not 8-byte aligned
+    assert stats_call(None) == _native.ASTR_EINVAL
+    assert stats_call(_desc(), scale=0.0) == _native.ASTR_EINVAL
+    assert stats_call(_desc(), q_tok=2) == _native.ASTR_EINVAL  # fp32 rows: 8 bytes apart
+    assert stats_call(_desc(), num_seqs=0) == 0
+
+
 def test_key_valid_argument_errors_need_no_device():
     f = _native.lib().astr_kv_write_key_valid
     flag = ctypes.c_int32(0)

@@ -1,7 +1,8 @@
 """The op-level API on the HIP kernels, against the oracle's restatement of
-online_attention / merge_softmax (online_attention.py:42-63, 74-219): explicit
-``AttentionBlock`` pages with gaps, offsets, key and query padding, causal and
-non-causal rows, windows, GQA, the three code formats and three query dtypes."""
+online_attention / online_attention_statistics / merge_softmax
+(online_attention.py:42-63, 74-219): explicit ``AttentionBlock`` pages with gaps,
+offsets, key and query padding, causal and non-causal rows, windows with and without
+causality, GQA, the three code formats and three query dtypes."""
 
 import numpy as np
 import pytest
@@ -85,6 +86,21 @@ def test_window_key_and_query_padding(device):
     _run(device, window=12, pad_fraction=0.25, query_pad=True, queries=9, seed=3)
 
 
+@pytest.mark.parametrize("window", [1, 5, 12, 40])
+def test_noncausal_windows(device, window):
+    """Windows without causality (online_attention.py:183-184): every key after
+    ``p - window`` is visible, later keys included. Rows read their first visible
+    block through a copy of their own; a window past the last key leaves no key."""
+    positions = [[0, 3, 17, 30, 45, 64, 66, 90], [8, 16, 24, 31, 56, 63, 70, 200]]
+    _run(device, causal=False, window=window, queries=8, positions=positions, seed=40 + window)
+
+
+def test_noncausal_window_padding_and_formats(device):
+    for k, fmt in enumerate(("int8", "fp8_e4m3fn", "fp8_e5m2")):
+        _run(device, causal=False, window=9, pad_fraction=0.25, query_pad=True, queries=7,
+             fmt=fmt, qdtype=(torch.bfloat16, torch.float16, torch.float32)[k], seed=50 + k)
+
+
 def test_gaps_offsets_and_queries_before_any_key(device):
     # keys only at [40, 56) and [70, 100); queries at 0 and 10 see nothing (zero rows)
     got = _run(device, spans=((40, 16), (70, 30)), positions=[[0, 10, 45, 69, 99]] * 2, seed=4)
@@ -104,8 +120,6 @@ def test_work_counters_and_unsupported_cases(device):
     work = aster_amd.AttentionWork()
     aster_amd.online_attention(q, dev_blocks, query_positions=pos, work=work)
     assert work.query_tiles == 2 and work.key_tiles == 2 * 2 and work.max_key_tile == 16
-    with pytest.raises(UnsupportedAttentionBackend):  # non-causal windows
-        aster_amd.online_attention(q, dev_blocks, query_positions=pos, causal=False, window=4)
     plain = AttentionBlock(torch.randn(1, 2, 16, 64, device=device, dtype=torch.bfloat16),
                            torch.randn(1, 2, 16, 64, device=device, dtype=torch.bfloat16), 0)
     with pytest.raises(UnsupportedAttentionBackend):  # unquantized pages
@@ -157,3 +171,95 @@ def test_pages_at_large_offsets(device, causal, window):
                  [99999, 100000, 100030, 100064, 104000, 104020, 104063, 104070]]
     _run(device, spans=spans, queries=8, positions=positions, causal=causal, window=window,
          seed=31)
+
+
+def _statistics(device, *, batch=2, hq=8, hkv=2, dim=128, queries=6,
+                spans=((0, 20), (24, 33), (57, 7)), fmt="int8", qdtype=torch.float32,
+                causal=True, window=None, pad_fraction=0.0, query_pad=False, positions=None,
+                seed=0, split=None):
+    """online_attention_statistics on the HIP kernels against the oracle's float64
+    statistics: the exact maximum and the mass and numerator relative to it, -inf/0
+    rows where nothing is visible. ``split`` also merges the statistics of the pages
+    before and after it with merge_softmax and checks the output against the whole."""
+    rng = np.random.default_rng(seed)
+    dev_blocks, ref_blocks = _pages(rng, batch, hkv, dim, spans, fmt, qdtype, device, pad_fraction)
+    query = torch.from_numpy(rng.standard_normal((batch, hq, queries, dim)).astype(np.float32))
+    query = query.to(device).to(qdtype)
+    last = max(o + n for o, n in spans)
+    if positions is None:
+        positions = np.stack([np.sort(rng.choice(last + 3, queries, replace=False))
+                              for _ in range(batch)])
+    positions = np.asarray(positions, np.int64)
+    qpad = (rng.random((batch, queries)) >= 0.3).astype(np.int32) if query_pad else None
+    kw = dict(causal=causal, window=window, scale=dim ** -0.5)
+    dev_kw = dict(kw, query_positions=torch.from_numpy(positions).to(device),
+                  query_padding=None if qpad is None else torch.from_numpy(qpad).to(device))
+    ref_kw = dict(kw, query_positions=positions, query_padding=qpad)
+    q64 = query.double().cpu().numpy()
+    got = aster_amd.online_attention_statistics(query, dev_blocks, **dev_kw)
+    want = ref.online_attention_statistics(q64, ref_blocks, **ref_kw)
+    groups = hq // hkv
+    assert got.maximum.shape == (batch, hkv, groups, queries) == want.maximum.shape
+    assert got.weighted.shape == (batch, hkv, groups, queries, dim)
+    assert all(t.dtype == torch.float32 for t in (got.maximum, got.mass, got.weighted))
+    m, l, w = (t.cpu().numpy() for t in (got.maximum, got.mass, got.weighted))
+    empty = ~np.isfinite(want.maximum)
+    np.testing.assert_array_equal(~np.isfinite(m), empty)
+    assert (m[empty] == -np.inf).all() and (l[empty] == 0).all() and (w[empty] == 0).all()
+    # scores of N(0, 1) rows are O(1): fp32 scores against float64 ones
+    np.testing.assert_allclose(m[~empty], want.maximum[~empty], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(l, want.mass, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(w, want.weighted, rtol=1e-4, atol=1e-4)
+    # the state normalises to online_attention's rows
+    out = aster_amd.online_attention(query, dev_blocks, **dev_kw)
+    assert_attention_close(got.output(dtype=qdtype).float().cpu().numpy(), out.float().cpu().numpy())
+    if split is not None:
+        left = aster_amd.online_attention_statistics(query, dev_blocks[:split], **dev_kw)
+        right = aster_amd.online_attention_statistics(query, dev_blocks[split:], **dev_kw)
+        merged = aster_amd.merge_softmax(left, right).output().cpu().numpy()
+        assert_attention_close(merged, want.output())
+    return got
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8_e4m3fn", "fp8_e5m2"])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_statistics_formats_and_query_dtypes(device, fmt, qdtype):
+    _statistics(device, fmt=fmt, qdtype=qdtype, split=1)
+
+
+@pytest.mark.parametrize("dim", [64, 128, 256])
+@pytest.mark.parametrize("causal,window", [(True, None), (True, 10), (False, None), (False, 7)])
+def test_statistics_masks_and_head_dims(device, dim, causal, window):
+    _statistics(device, dim=dim, causal=causal, window=window, pad_fraction=0.2, query_pad=True,
+                seed=dim + (window or 0), split=2)
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (16, 1)])
+def test_statistics_gqa_and_empty_rows(device, hq, hkv):
+    # keys only at [40, 56) and [70, 100): queries at 0 and 10 see nothing
+    got = _statistics(device, hq=hq, hkv=hkv, spans=((40, 16), (70, 30)), queries=5,
+                      positions=[[0, 10, 45, 69, 99]] * 2, seed=hq, split=1)
+    assert (got.maximum[..., :2] == -torch.inf).all()
+
+
+def test_statistics_long_rows_merge_partitions(device):
+    # 1500 keys: three 512-token partitions per row, merged with the exact maximum
+    _statistics(device, spans=((0, 700), (700, 800)), queries=4,
+                positions=[[100, 600, 1200, 1499], [511, 512, 1023, 1600]], seed=70, split=1)
+
+
+def test_statistics_extreme_scores(device):
+    """Scores far beyond the decode kernels' lazy-rescale slack (2^8): the statistics
+    keep the exact maximum, so the mass stays O(keys)."""
+    rng = np.random.default_rng(80)
+    dev_blocks, ref_blocks = _pages(rng, 1, 2, 64, ((0, 48),), "int8", torch.float32, device)
+    query = torch.from_numpy(rng.standard_normal((1, 4, 3, 64)).astype(np.float32) * 60)
+    query = query.to(device)
+    positions = np.array([[10, 30, 47]])
+    got = aster_amd.online_attention_statistics(
+        query, dev_blocks, query_positions=torch.from_numpy(positions).to(device))
+    want = ref.online_attention_statistics(query.double().cpu().numpy(), ref_blocks,
+                                           query_positions=positions)
+    np.testing.assert_allclose(got.maximum.cpu().numpy(), want.maximum, rtol=1e-5, atol=1e-4)
+    np.testing.assert_allclose(got.mass.cpu().numpy(), want.mass, rtol=1e-3, atol=1e-4)
+    np.testing.assert_allclose(got.weighted.cpu().numpy(), want.weighted, rtol=1e-3, atol=1e-3)
