@@ -29,6 +29,7 @@ ASTR_F32, ASTR_F16, ASTR_BF16 = 0, 1, 2
 # Every symbol include/aster_kv.h declares (checked by tests/test_capi.py).
 EXPORTED_SYMBOLS = (
     "astr_kv_quantize_append_i8",
+    "astr_kv_quantize_append_i8_reserved",
     "astr_kv_write_key_valid",
     "astr_paged_attention_i8",
     "astr_paged_attention_varlen_i8",
@@ -96,6 +97,10 @@ def lib():
             desc_p, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp,
         ]
         handle.astr_kv_quantize_append_i8.restype = ctypes.c_int
+        handle.astr_kv_quantize_append_i8_reserved.argtypes = [
+            desc_p, c_vp, c_vp, c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp,
+        ]
+        handle.astr_kv_quantize_append_i8_reserved.restype = ctypes.c_int
         handle.astr_kv_write_key_valid.argtypes = [desc_p, c_vp, c_vp, c_i64, c_vp, c_vp]
         handle.astr_kv_write_key_valid.restype = ctypes.c_int
         handle.astr_paged_attention_i8.argtypes = [

@@ -13,7 +13,9 @@
 // Two launches per call: a finiteness scan that sets ASTR_FLAG_NONFINITE_INPUT,
 // then the quantize/scatter kernel that does nothing when that bit is set, so a
 // bad suffix mutates no slot (kv_quantization.py:77-81, state.py:292 runs the
-// check before any copy).
+// check before any copy). For slots the caller has reserved and rolls back when
+// the flag is raised (the runner's step), one launch: the quantize/scatter kernel
+// checks its own row and leaves a non-finite row unwritten.
 #include <cfloat>
 
 #include "common.h"
@@ -117,11 +119,12 @@ __global__ __launch_bounds__(256) void finite_scan_kernel(AppendArgs a) {
   if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_INPUT);
 }
 
-template <typename T, int VEC, int KF>
+template <typename T, int VEC, int KF, bool kOwnCheck>
 __global__ __launch_bounds__(256) void quantize_append_kernel(AppendArgs a) {
   // All-or-nothing: the finite scan of this call (or an unacknowledged earlier
   // one) flagged the input, so leave every slot untouched. The flag, slot and
-  // row loads are independent and issue together.
+  // row loads are independent and issue together. kOwnCheck (reserved slots, no
+  // scan launch): the row's own check keeps a non-finite row out of its slot.
   RowRef rr;
   if (!row_of(a, rr)) return;
   const int lane = threadIdx.x & 63;
@@ -130,6 +133,16 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(AppendArgs a) {
   const int D = a.cache.head_dim;
   float x[kMaxPerLane];
   load_row<T, VEC>(row_src<T>(a, rr), D, lane, x);
+  constexpr int N = VEC > 0 ? VEC : kMaxPerLane;
+  if constexpr (kOwnCheck) {
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < N; ++i) bad |= !__builtin_isfinite(x[i]);
+    if (__ballot(bad) != 0) {
+      if (lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_INPUT);
+      return;
+    }
+  }
   if (flag & ASTR_FLAG_NONFINITE_INPUT) return;
   if (slot < 0) return;  // padding token: no slot
   const int64_t block = slot / a.cache.block_size, offset = slot - block * a.cache.block_size;
@@ -137,7 +150,6 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(AppendArgs a) {
     if (lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
     return;
   }
-  constexpr int N = VEC > 0 ? VEC : kMaxPerLane;
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(x[i]));
@@ -178,31 +190,41 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(AppendArgs a) {
   }
 }
 
-template <typename T, int VEC>
-int launch_append(const AppendArgs& a, hipStream_t stream) {
-  const int64_t rows = (a.value ? 2 : 1) * a.num_tokens * a.cache.num_kv_heads;
-  const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  hipLaunchKernelGGL((finite_scan_kernel<T, VEC>), dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+template <typename T, int VEC, bool kOwnCheck>
+void launch_quantize(const AppendArgs& a, uint32_t blocks, hipStream_t stream) {
   switch (a.cache.code_format) {
     case kInt8:
-      hipLaunchKernelGGL((quantize_append_kernel<T, VEC, kInt8>), dim3((uint32_t)blocks),
+      hipLaunchKernelGGL((quantize_append_kernel<T, VEC, kInt8, kOwnCheck>), dim3(blocks),
                          dim3(256), 0, stream, a);
       break;
     case kE4M3:
-      hipLaunchKernelGGL((quantize_append_kernel<T, VEC, kE4M3>), dim3((uint32_t)blocks),
+      hipLaunchKernelGGL((quantize_append_kernel<T, VEC, kE4M3, kOwnCheck>), dim3(blocks),
                          dim3(256), 0, stream, a);
       break;
     default:
-      hipLaunchKernelGGL((quantize_append_kernel<T, VEC, kE5M2>), dim3((uint32_t)blocks),
+      hipLaunchKernelGGL((quantize_append_kernel<T, VEC, kE5M2, kOwnCheck>), dim3(blocks),
                          dim3(256), 0, stream, a);
       break;
+  }
+}
+
+// reserved: the caller rolls the slots back on a flagged call, so no scan launch
+template <typename T, int VEC>
+int launch_append(const AppendArgs& a, bool reserved, hipStream_t stream) {
+  const int64_t rows = (a.value ? 2 : 1) * a.num_tokens * a.cache.num_kv_heads;
+  const uint32_t blocks = (uint32_t)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+  if (reserved) {
+    launch_quantize<T, VEC, true>(a, blocks, stream);
+  } else {
+    hipLaunchKernelGGL((finite_scan_kernel<T, VEC>), dim3(blocks), dim3(256), 0, stream, a);
+    launch_quantize<T, VEC, false>(a, blocks, stream);
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "quantize_append launch");
 }
 
 template <typename T>
-int launch_append_dim(const AppendArgs& a, hipStream_t stream) {
+int launch_append_dim(const AppendArgs& a, bool reserved, hipStream_t stream) {
   const int D = a.cache.head_dim;
   // The vector path needs every row start aligned to a whole vector.
   const int64_t vec = D >= 64 ? D / 64 : 1;
@@ -216,14 +238,14 @@ int launch_append_dim(const AppendArgs& a, hipStream_t stream) {
   if (aligned(a.key, a.key_token_stride, a.key_head_stride) &&
       aligned(a.value, a.value_token_stride, a.value_head_stride) && codes_ok) {
     switch (D) {
-      case 64: return launch_append<T, 1>(a, stream);
-      case 128: return launch_append<T, 2>(a, stream);
-      case 256: return launch_append<T, 4>(a, stream);
-      case 512: return launch_append<T, 8>(a, stream);
+      case 64: return launch_append<T, 1>(a, reserved, stream);
+      case 128: return launch_append<T, 2>(a, reserved, stream);
+      case 256: return launch_append<T, 4>(a, reserved, stream);
+      case 512: return launch_append<T, 8>(a, reserved, stream);
       default: break;
     }
   }
-  return launch_append<T, 0>(a, stream);
+  return launch_append<T, 0>(a, reserved, stream);
 }
 
 // One thread per token: the slot's key-padding byte (state.py:339-344 copies the
@@ -269,13 +291,13 @@ extern "C" int astr_kv_write_key_valid(const astr_paged_kv* cache, const int64_t
   return err == hipSuccess ? 0 : hip_fail(err, "write_key_valid launch");
 }
 
-extern "C" int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void* key,
-                                          const void* value, int32_t in_dtype, int64_t num_tokens,
-                                          int64_t key_token_stride, int64_t key_head_stride,
-                                          int64_t value_token_stride, int64_t value_head_stride,
-                                          const int64_t* slot_mapping, int32_t* err_flag,
-                                          void* stream) {
-  astr::CallRange range("astr_kv_quantize_append_i8");
+namespace {
+
+int quantize_append(const astr_paged_kv* cache, const void* key, const void* value,
+                    int32_t in_dtype, int64_t num_tokens, int64_t key_token_stride,
+                    int64_t key_head_stride, int64_t value_token_stride,
+                    int64_t value_head_stride, const int64_t* slot_mapping, int32_t* err_flag,
+                    void* stream, bool reserved) {
   using namespace astr;
   if (cache == nullptr || err_flag == nullptr)
     return fail(ASTR_EINVAL, "cache descriptor and err_flag are required");
@@ -301,9 +323,34 @@ extern "C" int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void
                value_head_stride, num_tokens, slot_mapping, *cache, err_flag};
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (in_dtype) {
-    case ASTR_F32: return launch_append_dim<float>(a, s);
-    case ASTR_F16: return launch_append_dim<_Float16>(a, s);
-    case ASTR_BF16: return launch_append_dim<bf16_t>(a, s);
+    case ASTR_F32: return launch_append_dim<float>(a, reserved, s);
+    case ASTR_F16: return launch_append_dim<_Float16>(a, reserved, s);
+    case ASTR_BF16: return launch_append_dim<bf16_t>(a, reserved, s);
     default: return fail(ASTR_EUNSUPPORTED, "input dtype %d is not f32/f16/bf16", in_dtype);
   }
+}
+
+}  // namespace
+
+extern "C" int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void* key,
+                                          const void* value, int32_t in_dtype, int64_t num_tokens,
+                                          int64_t key_token_stride, int64_t key_head_stride,
+                                          int64_t value_token_stride, int64_t value_head_stride,
+                                          const int64_t* slot_mapping, int32_t* err_flag,
+                                          void* stream) {
+  astr::CallRange range("astr_kv_quantize_append_i8");
+  return quantize_append(cache, key, value, in_dtype, num_tokens, key_token_stride,
+                         key_head_stride, value_token_stride, value_head_stride, slot_mapping,
+                         err_flag, stream, false);
+}
+
+extern "C" int astr_kv_quantize_append_i8_reserved(
+    const astr_paged_kv* cache, const void* key, const void* value, int32_t in_dtype,
+    int64_t num_tokens, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, const int64_t* slot_mapping,
+    int32_t* err_flag, void* stream) {
+  astr::CallRange range("astr_kv_quantize_append_i8_reserved");
+  return quantize_append(cache, key, value, in_dtype, num_tokens, key_token_stride,
+                         key_head_stride, value_token_stride, value_head_stride, slot_mapping,
+                         err_flag, stream, true);
 }

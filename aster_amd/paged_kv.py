@@ -132,12 +132,17 @@ class PagedKVCache:
             raise ValueError("Slot, block table or context length outside the KV arena")
 
     # ---- hot path -----------------------------------------------------------
-    def append(self, layer, key, value, slot_mapping, *, check=False):
+    def append(self, layer, key, value, slot_mapping, *, check=False, reserved=False):
         """Quantize ``key``/``value`` ``[T, Hkv, D]`` (fp32/fp16/bf16, device) into
         the slots ``slot_mapping`` (int64 ``[T]``; negative = skip). With
         ``check=True`` synchronise and raise ``ValueError`` on non-finite input, as
         quantize_kv does (kv_quantization.py:77-81); otherwise the error stays in
-        the sticky flag (and blocks further appends) until ``raise_errors``."""
+        the sticky flag (and blocks further appends) until ``raise_errors``.
+
+        A non-finite input leaves every slot as it was; with ``reserved=True`` (slots
+        the caller rolls back when the call is flagged, as the runner's step does) the
+        append takes one launch instead of two, and only the non-finite rows are
+        guaranteed to stay unwritten."""
         _check_rows(key, "key", self.num_kv_heads, self.head_dim, self.device)
         _check_rows(value, "value", self.num_kv_heads, self.head_dim, self.device)
         if key.shape != value.shape or key.dtype != value.dtype:
@@ -146,8 +151,10 @@ class PagedKVCache:
                 or slot_mapping.device != self.device or not slot_mapping.is_contiguous()):
             raise ValueError("slot_mapping must be a contiguous int64 device vector [T]")
         stream = torch.cuda.current_stream(self.device).cuda_stream
+        lib = _native.lib()
+        fn = lib.astr_kv_quantize_append_i8_reserved if reserved else lib.astr_kv_quantize_append_i8
         _native.check(
-            _native.lib().astr_kv_quantize_append_i8(
+            fn(
                 self._descs[layer], key.data_ptr(), value.data_ptr(), _DTYPE_CODES[key.dtype],
                 key.shape[0], key.stride(0), key.stride(1), value.stride(0), value.stride(1),
                 slot_mapping.data_ptr(), self.err_flag.data_ptr(), stream),

@@ -149,7 +149,8 @@ class PagedAttentionStep:
         if query.shape[0] != self.num_tokens or key.shape[0] != self.num_tokens:
             raise ValueError("query/key rows must match the step's tokens")
         cache = self.pool.cache
-        cache.append(layer, key, value, self.slot_mapping)
+        # the step's slots are reserved and rolled back if the step is flagged
+        cache.append(layer, key, value, self.slot_mapping, reserved=True)
         ws_work = self.work
         plan = self._decode_plan(query, window) if self.partition_tokens == 0 else None
         if plan is not None:

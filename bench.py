@@ -2,14 +2,15 @@
 
 A step is one decode-attention layer invocation of the hot path over the batch:
 quantize-and-append of the 64 new bf16 K/V tokens (one per sequence) via
-slot_mapping, then ragged paged attention of the 64 bf16 query rows (32 q heads,
-8 kv heads, D=128) over their INT8 pages (context U[128,4096]). Steps cycle over
-``--layers`` distinct layer arenas (default 4, ~1.1 GB) so each step reads its
-K/V from HBM, not from the 256 MB MALL, as a real multi-layer decode does.
+slot_mapping into their reserved slots (one launch, as the runner's step appends),
+then ragged paged attention of the 64 bf16 query rows (32 q heads, 8 kv heads,
+D=128) over their INT8 pages (context U[128,4096]) on the step's host plan. Steps
+cycle over ``--layers`` distinct layer arenas (default 4, ~1.1 GB) so each step reads
+its K/V from HBM, not from the 256 MB MALL, as a real multi-layer decode does.
 
 value = attended KV-tokens/s = sum(context_lens) / step time. The ``roofline``
-object is for the attention call (decode_streamk_kernel plus the split-K
-merge_streamk_kernel), timed with HIP events on the launch stream. ``extra`` measures
+object is for the attention call (decode_planned_kernel, or without a plan the
+stream-K kernel and its merge), timed with HIP events on the launch stream. ``extra`` measures
 configs 3, 4 and 5 in the same run the same way (their calls alone).
 ``cpu_baseline`` times the numpy restatement of the reference's CPU path (oracle/)
 on the whole config-2 step with one BLAS thread and with the host's CPU share.
@@ -342,7 +343,7 @@ def main():
 
     def step(i):
         layer = i % L
-        cache.append(layer, k_new, v_new, slots)
+        cache.append(layer, k_new, v_new, slots, reserved=True)
         call(layer)
 
     for i in range(args.warmup):
@@ -405,7 +406,7 @@ def main():
             "attended_kv_tokens": w.attended_tokens, "max_context_len": w.max_context_len,
             "append_tokens": int(k_new.shape[0]), "partition_tokens": args.partition,
             "layer_arenas": L,
-            "step": f"quantize_append({int(k_new.shape[0])} tok) + paged_attention",
+            "step": f"quantize_append_reserved({int(k_new.shape[0])} tok) + paged_attention",
         },
         "hbm_fraction_of_step": alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "roofline": {

@@ -112,6 +112,26 @@ int astr_kv_quantize_append_i8(const astr_paged_kv* cache, const void* key, cons
                                int32_t* err_flag, void* stream);
 
 /*
+ * astr_kv_quantize_append_i8 in one launch instead of two, for slots the caller has
+ * reserved and rolls back when the call is flagged: the same quantizer
+ * (kv_quantization.py:71-94) and slot placement (state.py:339-344), with the
+ * all-or-nothing rule of kv_quantization.py:77-81 / state.py:292 kept at the level
+ * of the caller's transaction instead of the slots. Each (token, head, K|V) row
+ * checks itself: a row holding a NaN/Inf sets ASTR_FLAG_NONFINITE_INPUT and is not
+ * written; the call's other rows may be written. A set input-flag bit at launch
+ * suppresses the rows that read it. The runner's step appends this way and aborts
+ * every reservation of a flagged step, so the pool's visible state is unchanged, as
+ * PagedStatePool.append_delta leaves it when quantize_kv raises.
+ */
+int astr_kv_quantize_append_i8_reserved(const astr_paged_kv* cache, const void* key,
+                                        const void* value, int32_t in_dtype,
+                                        int64_t num_tokens, int64_t key_token_stride,
+                                        int64_t key_head_stride, int64_t value_token_stride,
+                                        int64_t value_head_stride,
+                                        const int64_t* slot_mapping, int32_t* err_flag,
+                                        void* stream);
+
+/*
  * Write the key-padding bytes of new tokens: key_valid[slot_mapping[i]] =
  * token_valid[i] != 0 (1 for every token when token_valid is NULL); slots < 0
  * are skipped, slots outside the arena raise ASTR_FLAG_BAD_INDEX. The padding

@@ -199,3 +199,43 @@ def test_quantize_kv_api_fp8_matches_oracle(device, fmt):
     np.testing.assert_array_equal(packed.values.cpu().view(torch.uint8).numpy(), want.values)
     np.testing.assert_array_equal(packed.scales.cpu().numpy(), want.scales)
     np.testing.assert_array_equal(packed.dequantize().cpu().numpy(), want.dequantize())
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dim", [64, 128, 96])
+def test_reserved_append_matches_guarded_append(device, fmt, dtype, dim):
+    """The one-launch append for reserved slots writes the same codes and scales as
+    the two-launch append, bit for bit (vector and strided row loads)."""
+    rng = np.random.default_rng(dim)
+    x = np.concatenate([_edge_rows(dim, rng, fmt), rng.standard_normal((40, dim)) * 3])
+    x = x[: (len(x) // 4) * 4].astype(np.float32).reshape(-1, 2, 2, dim)  # [T, K|V, Hkv, D]
+    # edge rows beyond the input dtype's range become zeros, not infinities
+    k, v = (torch.from_numpy(np.ascontiguousarray(x[:, i])).to(device).to(dtype)
+            .nan_to_num(0.0, 0.0, 0.0) for i in (0, 1))
+    slots = torch.from_numpy(rng.permutation(64)[: k.shape[0]].astype(np.int64)).to(device)
+    slots[1] = -1  # a padding token keeps its slot
+    guarded, reserved = _cache(device, 4, 2, dim, fmt=fmt), _cache(device, 4, 2, dim, fmt=fmt)
+    guarded.append(0, k, v, slots, check=True)
+    reserved.append(0, k, v, slots, check=True, reserved=True)
+    assert torch.equal(guarded.codes, reserved.codes)
+    assert torch.equal(guarded.scales.view(torch.int32), reserved.scales.view(torch.int32))
+
+
+def test_reserved_append_leaves_nonfinite_rows_unwritten(device):
+    cache = _cache(device, 4, 2, 64)
+    k = torch.randn(5, 2, 64, device=device)
+    v = torch.randn(5, 2, 64, device=device)
+    v[3, 1, 17] = float("nan")
+    k[0, 0, 3] = float("-inf")
+    before = cache.codes.clone(), cache.scales.clone()
+    with pytest.raises(ValueError, match="finite"):
+        cache.append(0, k, v, torch.arange(5, device=device), check=True, reserved=True)
+    # the non-finite rows' slots: V of token 3 head 1, K of token 0 head 0 (block 0)
+    assert torch.equal(cache.codes[0, 0, 1, 1, 3], before[0][0, 0, 1, 1, 3])
+    assert torch.equal(cache.codes[0, 0, 0, 0, 0], before[0][0, 0, 0, 0, 0])
+    assert cache.scales[0, 0, 1, 1, 3] == before[1][0, 0, 1, 1, 3]
+    # the flag was acknowledged: a clean append now lands everywhere
+    cache.append(0, k.nan_to_num(0.0, 0.0, 0.0), v.nan_to_num(0.0), torch.arange(5, device=device),
+                 check=True, reserved=True)
+    assert (cache.codes[0, 0, :, :, :5] != 0).any(-1).all()

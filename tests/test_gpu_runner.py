@@ -1,6 +1,6 @@
 """Runner integration of the hip_int8_paged backend: a toy GQA decoder steps through
 PagedAttentionStep over the arena-backed pool (ragged prefill chunks, decode,
-fork + copy-on-write, a mixed step, an aborted step). At every layer the HIP
+fork + copy-on-write, a mixed step, an aborted step, a step with non-finite input). At every layer the HIP
 attention output is checked against the oracle's rendering of the reference's
 forward_batch row loop (paged_attention.py:168-215): the row's quantized history
 pages plus the chunk's own quantized K/V as one more block, causal positions,
@@ -87,6 +87,20 @@ def test_runner_steps_match_reference_row_loop(device):
         with PagedAttentionStep(pool, seqs, [16, 16, 16]) as step:
             raise RuntimeError("layer failed")
     assert pool.used_blocks == used and [s.length for s in seqs] == lengths
+    # 6. a chunk holding a non-finite key: the step appends in one launch into its
+    #    reserved slots, the flag raises the reference's error at commit and every
+    #    reservation is rolled back, so the pool is as before (kv_quantization.py:77-81
+    #    raises before PagedStatePool.append_delta changes anything)
+    with pytest.raises(ValueError, match="finite"):
+        with PagedAttentionStep(pool, seqs, [1, 4, 1]) as step:
+            key = torch.randn(6, model.hkv, model.d, device=device)
+            key[3, 0, 5] = float("nan")
+            q = torch.randn(6, model.hq, model.d, device=device)
+            step.attend(0, q, key, torch.randn_like(key), scale=model.scale)
+    assert pool.used_blocks == used and [s.length for s in seqs] == lengths
+    for s, k in zip(seqs + [fork], keys + ["d"]):
+        check_pool_matches_oracle(pool, oracle, s, k)
+    run_step(model, pool, oracle, seqs, keys, [tokens(1)] * 3, work)  # the flag was cleared
     for s in seqs + [fork]:
         pool.release(s)
     assert pool.used_blocks == 0
