@@ -201,6 +201,15 @@ def planned_timeline(config="config2", calls=7, tail=None):
            "items_per_workgroup": pct(items, [0, 50, 100]),
            "us_per_block": round(float(((t[streaming, 4] - t[streaming, 3]) /
                                         np.maximum(nblk[streaming], 1)).mean()), 3)}
+    # spread of the streaming ends: all waves, waves within their workgroup, and the
+    # workgroups' mean ends (what balancing inside a workgroup could and could not remove)
+    ends = t[:, 4]
+    groups = np.unique(wg)
+    rep["stream_end_sd_us"] = {
+        "waves": round(float(ends.std()), 2),
+        "within_workgroups": round(float(np.sqrt(np.mean([ends[wg == g].var()
+                                                          for g in groups]))), 2),
+        "workgroup_means": round(float(np.std([ends[wg == g].mean() for g in groups])), 2)}
     rep["per_xcc"] = {int(x): {"waves": int((xcc == x).sum()),
                                "mean_end": round(float(t[xcc == x, 4].mean()), 2),
                                "max_end": round(float(t[xcc == x, 4].max()), 2)}

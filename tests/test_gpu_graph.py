@@ -3,6 +3,7 @@ replays exactly what the eager calls produce: the path issues no memset and need
 host synchronisation inside a step. Replays are interleaved with eager work and
 synchronisations, and every replay is checked."""
 
+import numpy as np
 import pytest
 import torch
 
@@ -61,4 +62,59 @@ def test_decode_step_replays_in_a_graph(device):
         torch.cuda.synchronize()
         for o, r in zip(outs, ref):
             assert torch.equal(o, r)
+    cache.raise_errors()
+
+
+def test_mixed_step_replays_in_a_graph(device):
+    """A mixed step (chunk rows and decode rows in one varlen call): eagerly the chunk
+    rows run on a second stream beside the decode rows; under capture both go on the
+    captured stream. Replays equal the eager outputs bit for bit, and work the caller
+    enqueues after an eager call sees its outputs (the second stream is joined)."""
+    rng = np.random.default_rng(5)
+    q_lens = np.array([40, 1, 1, 17, 1, 64, 1, 0, 3], np.int32)
+    ctx = q_lens + rng.integers(0, 700, q_lens.size).astype(np.int32)
+    ctx[7] = 20
+    tables_h, pool = wl._tables_from_lengths(ctx, rng, spare_blocks=3)
+    w = wl.DecodeWorkload("mixed", 32, 8, 128, ctx, tables_h, pool, torch.bfloat16, 5,
+                          128 ** -0.5, query_lens=q_lens)
+    cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=1, num_kv_heads=w.num_kv_heads,
+                         head_dim=w.head_dim, device=device)
+    wl.materialize(w, cache, device=device)
+    tables, lens = wl.device_tables(w, device)
+    qsl = wl.device_query_start(w, device)
+    q = wl.queries(w, device)
+    ws_bytes = cache.workspace_bytes(w.num_seqs, w.num_q_heads, w.max_context_len, 0)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=device)
+    out = torch.empty_like(q)
+
+    def call():
+        cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                              scale=w.scale, query_start_loc=qsl, max_query_len=w.max_query_len,
+                              out=out, workspace=ws)
+
+    call()
+    copy = out.clone()  # enqueued after the call on the caller's stream
+    torch.cuda.synchronize()
+    cache.raise_errors()
+    ref = out.clone()
+    assert torch.equal(copy, ref)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for _ in range(3):
+        out.fill_(float("nan"))
+        call()  # eager, between the replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
     cache.raise_errors()
