@@ -74,7 +74,6 @@ struct AttnArgs {
   int32_t total_waves;
   int32_t min_waves;
   int32_t pref_waves;  // stream-K: waves the GPU holds at once (set by the launcher)
-  int32_t share_cus;   // stream-K: one workgroup per compute unit (a prefill kernel runs beside)
   float* ws_o;          // partial acc (layout depends on the split mode)
   float* ws_ml;         // partial (m, l)
   int32_t* ws_seq;      // stream-K: block prefix over its work rows [num_packs + num_seqs + 1]

@@ -903,7 +903,7 @@ int launch(AttnArgs a, hipStream_t stream) {
   // launch one wave per resident slot (whole workgroups) and at least min_waves (the
   // host-side bound), at most the workspace capacity passed in total_waves; the
   // kernels settle the waves they use from the actual block count
-  const int64_t resident = (int64_t)device_cus() * (a.share_cus ? 1 : per_cu) * NW;
+  const int64_t resident = (int64_t)device_cus() * per_cu * NW;
   int64_t waves = resident;
   if (waves < a.min_waves) waves = (a.min_waves + NW - 1) / NW * NW;
   if (waves > a.total_waves) waves = a.total_waves / NW * NW;

@@ -2,9 +2,8 @@
 // choice. Decode rows (one query token) run the stream-K kernel (bf16/fp16
 // queries, partition_tokens == 0, up to 512 sequences) or fixed-size split-K
 // partitions (every other case); rows with several query tokens (chunked
-// prefill, varlen entry point only) run the prefill kernel beside them on a second
-// stream (launch_mixed). Kernels: decode_streamk.hip, decode_partition.hip,
-// prefill.hip.
+// prefill, varlen entry point only) run the prefill kernel after them on the same
+// stream. Kernels: decode_streamk.hip, decode_partition.hip, prefill.hip.
 #include <mutex>
 
 #include "attention_common.h"
@@ -45,76 +44,6 @@ int device_cus() {
                    : 256;
   }
   return cus[dev];
-}
-
-// The chunk rows of a mixed step run on a second stream of the device, beside the
-// decode rows on the caller's stream: the prefill kernel is bound by VALU issue, the
-// decode kernels by HBM, and one workgroup of each fits a compute unit. The caller's
-// stream forks to the side stream through an event and joins it after the launches,
-// so everything the caller enqueues next waits for both. One side stream and event
-// pair per device, created at the first mixed call; calls fork under a lock.
-struct SideStream {
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-};
-
-std::mutex& side_mutex() {
-  static std::mutex mu;
-  return mu;
-}
-
-// The current device's side stream (side_mutex held). Returns 0, or an error code.
-int side_stream(SideStream** out) {
-  static SideStream tab[64];
-  int dev = 0;
-  hipError_t err = hipGetDevice(&dev);
-  if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
-  if (dev < 0 || dev >= 64) return fail(ASTR_EUNSUPPORTED, "device %d beyond 64", dev);
-  SideStream& t = tab[dev];
-  if (t.stream == nullptr) {
-    SideStream n;
-    if ((err = hipStreamCreateWithFlags(&n.stream, hipStreamNonBlocking)) != hipSuccess)
-      return hip_fail(err, "hipStreamCreateWithFlags");
-    if ((err = hipEventCreateWithFlags(&n.fork, hipEventDisableTiming)) != hipSuccess ||
-        (err = hipEventCreateWithFlags(&n.join, hipEventDisableTiming)) != hipSuccess)
-      return hip_fail(err, "hipEventCreateWithFlags");
-    t = n;
-  }
-  *out = &t;
-  return 0;
-}
-
-// Decode kernels on `s` and the prefill kernel beside them on the side stream, joined
-// back into `s`; under stream capture (a graph records no second stream here) both
-// go on `s`, the prefill after the decode kernels. The stream-K decode takes one
-// workgroup per compute unit either way (the same split, so the same results).
-int launch_mixed(const AttnArgs& a, int32_t q_dtype, bool streamk, hipStream_t s) {
-  AttnArgs d = a;
-  d.share_cus = 1;
-  auto decode = [&]() {
-    return streamk ? launch_streamk(d, q_dtype, s) : launch_partitioned(d, q_dtype, s);
-  };
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  hipError_t err = hipStreamIsCapturing(s, &cs);
-  if (err != hipSuccess) return hip_fail(err, "hipStreamIsCapturing");
-  if (cs != hipStreamCaptureStatusNone) {
-    const int rc = decode();
-    return rc != 0 ? rc : launch_prefill(a, q_dtype, s);
-  }
-  std::lock_guard<std::mutex> lock(side_mutex());
-  SideStream* side = nullptr;
-  int rc = side_stream(&side);
-  if (rc != 0) return rc;
-  if ((err = hipEventRecord(side->fork, s)) != hipSuccess ||
-      (err = hipStreamWaitEvent(side->stream, side->fork, 0)) != hipSuccess)
-    return hip_fail(err, "fork to the side stream");
-  rc = launch_prefill(a, q_dtype, side->stream);
-  const int rd = rc != 0 ? 0 : decode();
-  // join even after a failed launch, so that `s` never runs ahead of the side stream
-  if ((err = hipEventRecord(side->join, side->stream)) != hipSuccess ||
-      (err = hipStreamWaitEvent(s, side->join, 0)) != hipSuccess)
-    return hip_fail(err, "join from the side stream");
-  return rc != 0 ? rc : rd;
 }
 
 // Upper bound of the visible blocks of all rows of one launch.
@@ -411,8 +340,9 @@ int paged_attention(const astr_paged_kv* cache, const void* query, int32_t q_dty
   a.stats = stats;
   a.err_flag = err_flag;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (query_start_loc != nullptr && max_query_len >= 2) return launch_mixed(a, q_dtype, streamk, s);
-  return streamk ? launch_streamk(a, q_dtype, s) : launch_partitioned(a, q_dtype, s);
+  const int rc = streamk ? launch_streamk(a, q_dtype, s) : launch_partitioned(a, q_dtype, s);
+  if (rc != 0 || query_start_loc == nullptr || max_query_len < 2) return rc;
+  return launch_prefill(a, q_dtype, s);
 }
 
 }  // namespace

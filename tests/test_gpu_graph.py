@@ -66,10 +66,10 @@ def test_decode_step_replays_in_a_graph(device):
 
 
 def test_mixed_step_replays_in_a_graph(device):
-    """A mixed step (chunk rows and decode rows in one varlen call): eagerly the chunk
-    rows run on a second stream beside the decode rows; under capture both go on the
-    captured stream. Replays equal the eager outputs bit for bit, and work the caller
-    enqueues after an eager call sees its outputs (the second stream is joined)."""
+    """A mixed step (chunk rows and decode rows in one varlen call: the decode kernels,
+    then the prefill kernel) captured in a graph: replays equal the eager outputs bit
+    for bit, interleaved with eager calls, and work the caller enqueues after an eager
+    call sees its outputs."""
     rng = np.random.default_rng(5)
     q_lens = np.array([40, 1, 1, 17, 1, 64, 1, 0, 3], np.int32)
     ctx = q_lens + rng.integers(0, 700, q_lens.size).astype(np.int32)
