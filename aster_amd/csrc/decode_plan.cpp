@@ -54,7 +54,6 @@
 #include <cmath>
 #include <cstring>
 #include <functional>
-#include <queue>
 #include <vector>
 
 #include "aster_kv.h"
@@ -174,9 +173,7 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
         for (int s : group) {
           const int32_t* st = block_tables + (int64_t)s * block_table_stride;
           const int reach = std::min(context_lens[s] / kBlockTokens, lead_full);
-          int c = 0;
-          while (c < reach && st[c] == lt[c]) ++c;
-          common[s] = c;
+          common[s] = (int)(std::mismatch(st, st + reach, lt).first - st);
         }
         std::stable_sort(group.begin(), group.end(), [&](int x, int y) { return common[x] > common[y]; });
         for (size_t t0 = 0; t0 + 1 < group.size(); t0 += tile_rows) {
@@ -208,6 +205,7 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
   }
   // ---- items: every row's visible blocks after its shared prefix
   std::vector<Unit> units;
+  units.reserve((size_t)num_seqs * num_kv_heads);
   int64_t total_cost = 0;
   for (int s = 0; s < num_seqs; ++s) {
     const int b0 = first_blk[s] + shared_of[s], nb = last_blk[s] - b0;
@@ -223,6 +221,7 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
   // slots together, span per head)
   const double share = std::max(1.0, (double)total_cost / num_workgroups);
   std::vector<Unit> work;
+  work.reserve(units.size());
   std::vector<int32_t> chunked;  // [seq, kvh, first slot, chunks]
   std::vector<int> member_c0(num_seqs, -1), member_span(num_seqs, 0);
   int64_t chunk_slots = 0;
@@ -269,25 +268,42 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
     }
     if (chunk_slots > INT32_MAX / 2) return fail(ASTR_EUNSUPPORTED, "plan: batch too large");
   }
-  // ---- LPT: longest first onto the least loaded workgroup (ties: lowest index)
-  std::vector<int> order(work.size());
-  for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
-  std::stable_sort(order.begin(), order.end(),
-                   [&](int x, int y) { return work[x].cost > work[y].cost; });
-  typedef std::pair<int64_t, int> Load;  // (cost, workgroup)
-  std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
-  for (int g = 0; g < num_workgroups; ++g) heap.push(Load{0, g});
-  std::vector<std::vector<int>> members(num_workgroups);
-  for (int i : order) {
-    Load top = heap.top();
-    heap.pop();
-    members[top.second].push_back(i);
-    top.first += work[i].cost;
-    heap.push(top);
+  // ---- LPT: longest first onto the least loaded workgroup (ties: lowest index); the
+  // units then laid out per workgroup in that order (placed[off[g] .. off[g + 1]))
+  std::vector<std::pair<int64_t, int>> order(work.size());  // (-cost, index): stable
+  for (size_t i = 0; i < work.size(); ++i) order[i] = {-work[i].cost, (int)i};
+  std::sort(order.begin(), order.end());
+  // a binary min-heap of (cost, workgroup): the top takes the unit, then sinks
+  typedef std::pair<int64_t, int> Load;
+  std::vector<Load> heap(num_workgroups);
+  for (int g = 0; g < num_workgroups; ++g) heap[g] = Load{0, g};  // already a heap
+  std::vector<int> owner(work.size());
+  std::vector<int64_t> off(num_workgroups + 1, 0);
+  const size_t nh = heap.size();
+  for (const auto& o : order) {
+    owner[o.second] = heap[0].second;
+    ++off[heap[0].second + 1];
+    heap[0].first += work[o.second].cost;
+    for (size_t i = 0;;) {
+      const size_t l = 2 * i + 1;
+      if (l >= nh) break;
+      const size_t c = l + 1 < nh && heap[l + 1] < heap[l] ? l + 1 : l;
+      if (!(heap[c] < heap[i])) break;
+      std::swap(heap[c], heap[i]);
+      i = c;
+    }
+  }
+  int64_t stride = 1;  // items of the fullest workgroup
+  for (int g = 0; g < num_workgroups; ++g) {
+    stride = std::max(stride, off[g + 1]);
+    off[g + 1] += off[g];
+  }
+  std::vector<Unit> placed(work.size());
+  {
+    std::vector<int64_t> next(off.begin(), off.end() - 1);
+    for (const auto& o : order) placed[next[owner[o.second]]++] = work[o.second];
   }
   // ---- sizes and layout
-  int64_t stride = 1;  // items of the fullest workgroup
-  for (int g = 0; g < num_workgroups; ++g) stride = std::max<int64_t>(stride, (int64_t)members[g].size());
   const int64_t num_items = stride * num_workgroups;
   int64_t num_blocks = 0;
   for (const Unit& u : work) num_blocks += u.nblk;
@@ -298,10 +314,9 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
                                  num_members);
   if (num_items > INT32_MAX / kItemWords || num_blocks > INT32_MAX / 4)
     return fail(ASTR_EUNSUPPORTED, "plan: batch too large");
-  for (int g = 0; g < num_workgroups; ++g)
-    if ((int)members[g].size() > kMaxItemsPerWorkgroup)
-      return fail(ASTR_EUNSUPPORTED, "plan: %zu items on one workgroup (at most %d)",
-                  members[g].size(), kMaxItemsPerWorkgroup);
+  if (stride > kMaxItemsPerWorkgroup)
+    return fail(ASTR_EUNSUPPORTED, "plan: %lld items on one workgroup (at most %d)",
+                (long long)stride, kMaxItemsPerWorkgroup);
   info->num_workgroups = num_workgroups;
   info->waves_per_workgroup = NW;
   info->num_items = (int32_t)num_items;
@@ -347,8 +362,10 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
     int64_t item = g * stride;
     rec[0] = (int32_t)item;
     int64_t pos = 0, g_cost = 0;
-    for (int i : members[g]) {
-      const Unit& u = work[i];
+    const Unit* const mine = placed.data() + off[g];
+    const size_t cnt = (size_t)(off[g + 1] - off[g]);
+    for (size_t q = 0; q < cnt; ++q) {
+      const Unit& u = mine[q];
       int32_t* it = items + item * kItemWords;
       it[0] = u.seq;
       it[1] = u.kvh;
@@ -375,15 +392,15 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
     for (int w = 1; w < NW; ++w) {
       const int64_t target = (g_cost * w + NW - 1) / NW;
       // skip members whose last block starts before the target
-      while (k < members[g].size()) {
-        const Unit& u = work[members[g][k]];
+      while (k < cnt) {
+        const Unit& u = mine[k];
         if (u.nblk > 0 && k_cost + kRowCost + kBlockCost * (u.nblk - 1) >= target) break;
         k_cost += u.cost;
         k_pos += u.nblk;
         ++k;
       }
       int64_t b = k_pos;
-      if (k < members[g].size()) {
+      if (k < cnt) {
         const int64_t over = target - k_cost - kRowCost;
         b += over <= 0 ? 0 : (over + kBlockCost - 1) / kBlockCost;
       }
@@ -398,11 +415,11 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
     for (int w = 0; w < NW; ++w, went += kWaveWords) {
       const int64_t b0 = bound[w], b1 = bound[w + 1];
       if (b1 <= b0) continue;
-      while (m < members[g].size() && m_pos + work[members[g][m]].nblk <= b0) {
-        m_pos += work[members[g][m]].nblk;
+      while (m < cnt && m_pos + mine[m].nblk <= b0) {
+        m_pos += mine[m].nblk;
         ++m;
       }
-      const Unit& u = work[members[g][m]];
+      const Unit& u = mine[m];
       const int64_t c = std::min<int64_t>({kPrefetchBlocks, b1 - b0, m_pos + u.nblk - b0});
       went[0] = u.seq;
       went[1] = u.kvh;
