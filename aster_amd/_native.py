@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "astr_decode_plan",
     "astr_paged_attention_i8_planned_workspace_bytes",
     "astr_paged_attention_i8_planned",
+    "astr_paged_attention_i8_planned_append",
     "astr_last_error",
     "astr_version",
 )
@@ -154,6 +155,11 @@ def lib():
             c_vp, c_vp, c_vp, c_sz, c_vp, c_vp,
         ]
         handle.astr_paged_attention_i8_planned.restype = ctypes.c_int
+        handle.astr_paged_attention_i8_planned_append.argtypes = [
+            desc_p, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64,
+            c_i64, c_i64, c_vp, c_vp, c_i32, ctypes.c_float, c_vp, c_vp, c_vp, c_sz, c_vp, c_vp,
+        ]
+        handle.astr_paged_attention_i8_planned_append.restype = ctypes.c_int
         handle.astr_last_error.argtypes = []
         handle.astr_last_error.restype = ctypes.c_char_p
         handle.astr_version.argtypes = []

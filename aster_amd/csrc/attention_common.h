@@ -91,6 +91,14 @@ struct AttnArgs {
   // exact maximum score and the mass sum(exp(score - maximum)) at stats[(t * Hq + h) * 2
   // + {0, 1}], and out holds the unnormalised numerator; nullptr: normalised rows
   float* stats;
+  // planned decode with the step's append: each decode row's newest token (position
+  // ctx - 1) as key and value rows of the query dtype ([num_seqs, Hkv, D], strides in
+  // elements) with its cache slot, quantized and written by the wave that streams the
+  // block holding it; nullptr: the token was appended beforehand
+  const void* new_k;
+  const void* new_v;
+  int64_t nk_tok, nk_head, nv_tok, nv_head;
+  const int64_t* new_slots;
   int32_t* err_flag;
 };
 

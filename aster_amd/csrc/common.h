@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <cfloat>
 #include <stdint.h>
 
 #include "aster_kv.h"
@@ -149,6 +150,45 @@ constexpr int kE5M2 = ASTR_KV_FP8_E5M2;
 template <int KF>
 __device__ __forceinline__ constexpr float format_max() {
   return KF == kInt8 ? 127.f : KF == kE4M3 ? 448.f : 57344.f;
+}
+
+// Finite c with |c| <= format_max -> FP8 bits, round to nearest even. With M mantissa
+// bits and exponent bias B: below the smallest normal 2^(1-B) the value counts
+// subnormal steps of 2^(1-B-M), rint(|c| * 2^(B-1+M)) in 0..2^M (scaling by a power of
+// two is exact; 2^M is the smallest normal's code); above it the fp32 mantissa is
+// rounded to M bits at bit 23-M (half to even, a carry steps the exponent) and the
+// exponent rebiased from 127 to B. The sign is kept (-0 for a negative underflow).
+template <int KF>
+__device__ __forceinline__ uint8_t fp8_round(float c) {
+  constexpr int M = KF == kE4M3 ? 3 : 2;
+  constexpr int B = KF == kE4M3 ? 7 : 15;
+  const uint32_t bits = __builtin_bit_cast(uint32_t, c);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  const uint32_t mag = bits & 0x7fffffffu;
+  uint32_t code;
+  if (mag < ((uint32_t)(128 - B) << 23)) {
+    code = (uint32_t)__builtin_rintf(__builtin_bit_cast(float, mag) * (float)(1 << (B - 1 + M)));
+  } else {
+    const uint32_t r = mag + ((1u << (22 - M)) - 1u) + ((mag >> (23 - M)) & 1u);
+    code = (r >> (23 - M)) - ((uint32_t)(127 - B) << M);
+  }
+  return (uint8_t)(code | sign);
+}
+// The row's scale from its largest magnitude (kv_quantization.py:86-90): true
+// division, then the FLT_MIN clamp; an all-zero row gets scale 1.
+template <int KF>
+__device__ __forceinline__ float quant_scale(float amax) {
+  return amax == 0.f ? 1.f : fmaxf(amax / format_max<KF>(), FLT_MIN);
+}
+
+// One code (kv_quantization.py:91-94): divide by the scale, clamp to the format's
+// range, round half to even (int8) or to the nearest-even FP8 value; as a byte.
+template <int KF>
+__device__ __forceinline__ int8_t quant_code(float x, float scale) {
+  constexpr float kMax = format_max<KF>();
+  const float n = fminf(fmaxf(x / scale, -kMax), kMax);
+  if constexpr (KF == kInt8) return (int8_t)__builtin_rintf(n);
+  else return (int8_t)fp8_round<KF>(n);
 }
 
 // The f16 conversions below give a code's value times 2^-8 for E4M3FN (its bits

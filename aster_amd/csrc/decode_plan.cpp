@@ -172,7 +172,9 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
         std::vector<int> group(cand.begin() + g0, cand.begin() + g1);
         for (int s : group) {
           const int32_t* st = block_tables + (int64_t)s * block_table_stride;
-          const int reach = std::min(context_lens[s] / kBlockTokens, lead_full);
+          // whole blocks before the one of the newest token (position ctx - 1), which
+          // stays the row's own (an appending decode writes it in that row's block)
+          const int reach = std::min((context_lens[s] - 1) / kBlockTokens, lead_full);
           common[s] = (int)(std::mismatch(st, st + reach, lt).first - st);
         }
         std::stable_sort(group.begin(), group.end(), [&](int x, int y) { return common[x] > common[y]; });
@@ -420,7 +422,11 @@ extern "C" int astr_decode_plan(const int32_t* block_tables, int32_t block_table
         ++m;
       }
       const Unit& u = mine[m];
-      const int64_t c = std::min<int64_t>({kPrefetchBlocks, b1 - b0, m_pos + u.nblk - b0});
+      int64_t c = std::min<int64_t>({kPrefetchBlocks, b1 - b0, m_pos + u.nblk - b0});
+      // not the block of the row's newest token: an appending decode stages the token
+      // with that block, after the wave has its items
+      const int64_t newest = u.ctx > 0 ? (u.ctx - 1) / kBlockTokens - (u.blk_begin + b0 - m_pos) : -1;
+      if (newest >= 0) c = std::min(c, newest);
       went[0] = u.seq;
       went[1] = u.kvh;
       went[2] = (int32_t)c;

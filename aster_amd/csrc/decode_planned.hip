@@ -13,6 +13,8 @@
 // of its waves hold (the merge_softmax rule, online_attention.py:42-63, and
 // SoftmaxState.output, :35-39) and writes the row; rows the plan cut across
 // workgroups leave one partial per chunk for merge_chunks_kernel.
+#include <type_traits>
+
 #include "attention_common.h"
 
 namespace astr {
@@ -182,7 +184,109 @@ __device__ __forceinline__ void merge_pieces(const AttnArgs& a, SrcOf src_of, in
   }
 }
 
-template <typename QT, int D, int G>
+// The step's append inside the decode (AttnArgs::new_k): the newest token of a row sits
+// at position ctx - 1, in the row's last visible block, which one wave of the plan
+// streams. That wave stages the token's key and value rows and the slot the caller
+// reserved for it right before the block (so they have landed once the block has),
+// quantizes them as quantize_kv does (kv_quantization.py:71-94, the same arithmetic as
+// quantize_append_kernel), writes the codes and scales into the block's LDS stage before
+// the attention reads it, and into the arena. Bytes per stage and wave: both rows, then
+// the slot.
+template <typename QT, int D>
+constexpr int new_token_bytes() { return 2 * D * (int)sizeof(QT) + 16; }
+
+template <typename QT, int D>
+__device__ __forceinline__ void stage_new_token(const AttnArgs& a, int seq, int kvh, int lane,
+                                                char* dst) {
+  constexpr int kRow = D * (int)sizeof(QT);
+  static_assert(kRow % 128 == 0, "rows of whole 4-byte lanes");
+  const char* k = static_cast<const char*>(a.new_k) +
+                  ((int64_t)seq * a.nk_tok + (int64_t)kvh * a.nk_head) * (int64_t)sizeof(QT);
+  const char* v = static_cast<const char*>(a.new_v) +
+                  ((int64_t)seq * a.nv_tok + (int64_t)kvh * a.nv_head) * (int64_t)sizeof(QT);
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(dst));
+#pragma unroll
+  for (int j = 0; j * 256 < kRow; ++j)
+    if (j * 256 + lane * 4 < kRow) lds_dma_x1(k + j * 256 + lane * 4, base + j * 256);
+#pragma unroll
+  for (int j = 0; j * 256 < kRow; ++j)
+    if (j * 256 + lane * 4 < kRow) lds_dma_x1(v + j * 256 + lane * 4, base + kRow + j * 256);
+  if (lane < 2)
+    lds_dma_x1(reinterpret_cast<const char*>(a.new_slots + seq) + lane * 4, base + 2 * kRow);
+}
+
+// Quantizes the staged token of row (seq, kvh) whose position ctx - 1 lies in block
+// `phys` (staged at `st`; its rows and slot at `nb`) and writes it into the stage and
+// into the arena. The caller's slot must be the plan's position of the token (else the
+// index flag is raised and only the arena copy is written, at the caller's slot); a
+// token holding a non-finite value raises the input flag and is written nowhere.
+template <typename QT, int D, int KF>
+__device__ __forceinline__ void append_token(const AttnArgs& a, int kvh, int ctx, int phys,
+                                             char* st, const char* nb, int lane) {
+  using S = Stage<D>;
+  constexpr int E = D / kWave;  // elements per lane
+  constexpr int kRow = D * (int)sizeof(QT);
+  struct alignas(E * sizeof(QT)) Elems {
+    QT e[E];
+  };
+  const Elems wk = *reinterpret_cast<const Elems*>(nb + lane * E * (int)sizeof(QT));
+  const Elems wv = *reinterpret_cast<const Elems*>(nb + kRow + lane * E * (int)sizeof(QT));
+  const int64_t slot = *reinterpret_cast<const int64_t*>(nb + 2 * kRow);
+  bool bad = false;
+  float ak = 0.f, av = 0.f;
+  float xk[E], xv[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    xk[e] = to_float<QT>(wk.e[e]);
+    xv[e] = to_float<QT>(wv.e[e]);
+    bad |= !__builtin_isfinite(xk[e]) || !__builtin_isfinite(xv[e]);
+    ak = fmaxf(ak, fabsf(xk[e]));
+    av = fmaxf(av, fabsf(xv[e]));
+  }
+  if (__ballot(bad) != 0) {
+    if (lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_INPUT);
+    return;
+  }
+  const float sk = quant_scale<KF>(wave_max(ak)), sv = quant_scale<KF>(wave_max(av));
+  typedef typename std::conditional<E == 1, uint8_t,
+                                    typename std::conditional<E == 2, uint16_t, uint32_t>::type>::type
+      Codes;
+  Codes ck = 0, cv = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    ck |= (Codes)((uint32_t)(uint8_t)quant_code<KF>(xk[e], sk) << (8 * e));
+    cv |= (Codes)((uint32_t)(uint8_t)quant_code<KF>(xv[e], sv) << (8 * e));
+  }
+  const int t = (ctx - 1) % kBlockTokens;
+  const int d = lane * E;
+  if (slot == (int64_t)phys * kBlockTokens + t) {
+    *reinterpret_cast<Codes*>(st + S::kK + k_chunk<D>(t, d / 16) + d % 16) = ck;
+    *reinterpret_cast<Codes*>(st + S::kV + t * D + d) = cv;
+    if (lane == 0) {
+      *reinterpret_cast<float*>(st + S::kS + 4 * t) = sk;
+      *reinterpret_cast<float*>(st + S::kS + 64 + 4 * t) = sv;
+    }
+  } else if (lane == 0) {
+    atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+  }
+  if (slot >= 0 && slot < (int64_t)a.cache.num_blocks * kBlockTokens) {
+    const int64_t blk = slot / kBlockTokens, off = slot % kBlockTokens;
+    const int64_t co = blk * a.cache.code_block_stride + (int64_t)kvh * a.cache.code_head_stride +
+                       off * D + d;
+    *reinterpret_cast<Codes*>(a.cache.k_codes + co) = ck;
+    *reinterpret_cast<Codes*>(a.cache.v_codes + co) = cv;
+    if (lane == 0) {
+      const int64_t so = blk * a.cache.scale_block_stride +
+                         (int64_t)kvh * a.cache.scale_head_stride + off;
+      a.cache.k_scales[so] = sk;
+      a.cache.v_scales[so] = sv;
+    }
+  } else if (lane == 0) {
+    atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+  }
+}
+
+template <typename QT, int D, int G, bool kAppend>
 __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(PlanArgs p) {
   static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   static_assert(G >= 1 && G <= 16, "GQA group");
@@ -204,6 +308,10 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
   __shared__ __attribute__((aligned(16))) int s_rec[NW + 3];  // first item, end item, wave bounds
   __shared__ int s_bad;
   __shared__ bool s_first_ring[NW];  // the wave's slot 0 partial is in the ring
+  // the step's append: per stage and wave, the newest token staged with its block
+  static_assert(!kAppend || sizeof(QT) == 2, "appends of 2-byte rows");
+  constexpr int kNewBytes = new_token_bytes<QT, D>();
+  __shared__ __attribute__((aligned(16))) char s_new[kAppend ? NS * NW * kNewBytes : 16];
 
   long long tm[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // trace marks (kTrace)
   if constexpr (kTrace) tm[0] = wall_clock64();
@@ -307,7 +415,8 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
   if (bad_index) n = 0;
   // block b0 + j of the list: its item (the last whose first block is at or before it)
   // and the offset of its id; false when no item holds it
-  auto locate = [&](int j, int& k, int64_t& off) __attribute__((always_inline)) -> bool {
+  // (appends: whether it holds its row's newest token, position ctx - 1)
+  auto locate = [&](int j, int& k, int64_t& off, bool& fin) __attribute__((always_inline)) -> bool {
     const int v = b0 + j;
     int lo = 0;
 #pragma unroll
@@ -316,16 +425,19 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
     k = lo;
     const int* it = s_item + lo * kItemWords;
     off = (int64_t)it[7] + (v - it[6]);
+    fin = kAppend && it[4] > 0 && it[2] + (v - it[6]) == (it[4] - 1) / kBlockTokens;
     return ni > 0 && v >= it[6] && v < it[6] + it[3];
   };
   int ids = 0, rows = 0, ids_nx = 0, rows_nx = 0;
-  bool ok0 = true;
+  uint64_t fmask = 0, fmask_nx = 0;  // appends: the windows' blocks that hold a newest token
+  bool ok0 = true, fin0 = false;
   if (lane < n) {
     int64_t off;
-    ok0 = locate(lane, rows, off);
+    ok0 = locate(lane, rows, off, fin0);
     if (ok0) ids = ids_tab[off];
   }
   bad_index |= __ballot(lane < n && !ok0) != 0;
+  if constexpr (kAppend) fmask = __ballot(lane < n && ok0 && fin0);
   int nblk = bad_index ? 0 : n;
   // The first window's ids, when first used (a wave with an entry first processes its
   // query): every one in the arena; and the entry's piece and blocks the items'. Else
@@ -340,6 +452,9 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
         same = same && (j >= pre || (__builtin_amdgcn_readlane(ids, j) == pid[j] &&
                                      __builtin_amdgcn_readlane(rows, j) == __builtin_amdgcn_readlane(rows, 0)));
       bad_ids |= !same;
+      // appends: the entry's blocks never hold a newest token (its rows are staged with
+      // the block, once the wave has its items)
+      if constexpr (kAppend) bad_ids |= (fmask & ((1ull << pre) - 1)) != 0;
     }
     if (bad_ids) {
       bad_index = true;
@@ -357,11 +472,13 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of the slot are done
     const int j = 64 * w + lane;
     ok_nx = true;
+    bool fin = false;
     if (j < n) {
       int64_t off;
-      ok_nx = locate(j, rows_nx, off);
+      ok_nx = locate(j, rows_nx, off, fin);
       if (ok_nx) lds_dma_x1(ids_tab + off, lds_addr(id_slot));
     }
+    if constexpr (kAppend) fmask_nx = __ballot(j < n && ok_nx && fin);
   };
 
   auto stage = [&](int j) __attribute__((always_inline)) -> char* {
@@ -372,11 +489,19 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
     return __builtin_amdgcn_readfirstlane(cur ? __builtin_amdgcn_readlane(rows, j & 63)
                                               : __builtin_amdgcn_readlane(rows_nx, j & 63));
   };
+  auto new_token = [&](int j) __attribute__((always_inline)) -> char* {
+    return s_new + ((j % NS) * NW + wave) * kNewBytes;
+  };
   auto issue = [&](int j) __attribute__((always_inline)) {
     const bool cur = (j >> 6) == cw;
     const int id = cur ? __builtin_amdgcn_readlane(ids, j & 63)
                        : __builtin_amdgcn_readlane(ids_nx, j & 63);
     const int k = row_at(j);
+    if constexpr (kAppend) {  // the token goes out right before its block
+      if (((cur ? fmask : fmask_nx) >> (j & 63)) & 1)
+        stage_new_token<QT, D>(a, s_item[k * kItemWords], s_item[k * kItemWords + 1], lane,
+                               new_token(j));
+    }
     stage_block<D>(a, __builtin_amdgcn_readfirstlane(id), s_item[k * kItemWords + 1], lane,
                    stage(j));
   };
@@ -470,6 +595,12 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
         if constexpr (kTrace) {
           if (i == 0) tm[3] = wall_clock64();
         }
+        if constexpr (kAppend) {
+          if ((fmask >> (i & 63)) & 1)
+            append_token<QT, D, KF>(a, it.kvh, it.ctx,
+                                    __builtin_amdgcn_readlane(ids, i & 63), stage(i),
+                                    new_token(i), lane);
+        }
         mfma_block<QT, D, KF>(stage(i), qop, cf, pos0 + (i - pstart) * kBlockTokens,
                               psp.kv_begin, psp.ctx, valid, r, qg, acc, m, l, vr, bad_score,
                               masks);
@@ -495,6 +626,7 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
       if (i == wend && i < nblk) {  // into the next window of the block list
         ids = ids_nx;
         rows = rows_nx;
+        fmask = fmask_nx;
         ++cw;
         if (64 * (cw + 1) < nblk) request_ids(cw + 1);
         if (__builtin_amdgcn_readlane(rows, 0) == crid) continue;  // the item goes on
@@ -684,11 +816,24 @@ int query_resident_per_cu(Kernel kernel, int threads) {
 
 template <typename QT, int D, int G>
 int launch(const PlanArgs& p, hipStream_t stream, int* resident) {
-  auto kernel = decode_planned_kernel<QT, D, G>;
+  auto kernel = decode_planned_kernel<QT, D, G, false>;
+  static const int per_cu = query_resident_per_cu(kernel, kPlanWaves * kWave);
   if (resident != nullptr) {
-    static const int per_cu = query_resident_per_cu(kernel, kPlanWaves * kWave);
     *resident = per_cu;
     return 0;
+  }
+  if (p.a.new_k != nullptr) {  // the step's append in the decode (2-byte rows)
+    // at head dim 64 the token rows would take the LDS of the second workgroup per CU
+    if constexpr (sizeof(QT) == 2 && D >= 128) {
+      auto append = decode_planned_kernel<QT, D, G, true>;
+      static const int append_per_cu = query_resident_per_cu(append, kPlanWaves * kWave);
+      if (append_per_cu < per_cu)  // the plan counts on the plain kernel's residency
+        return fail(ASTR_EUNSUPPORTED, "the appending decode holds fewer workgroups per CU");
+      kernel = append;
+    } else {
+      return fail(ASTR_EUNSUPPORTED, "the decode appends bf16/fp16 rows at head dims 128 and "
+                  "256 only");
+    }
   }
   hipLaunchKernelGGL(kernel, dim3(p.info.num_workgroups), dim3(kPlanWaves * kWave), 0, stream, p);
   if (p.info.num_chunked > 0)

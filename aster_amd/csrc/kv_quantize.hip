@@ -25,28 +25,6 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;  // one wave per (token, head, K|V) row
 
-// Finite c with |c| <= format_max -> FP8 bits, round to nearest even. With M mantissa
-// bits and exponent bias B: below the smallest normal 2^(1-B) the value counts
-// subnormal steps of 2^(1-B-M), rint(|c| * 2^(B-1+M)) in 0..2^M (scaling by a power of
-// two is exact; 2^M is the smallest normal's code); above it the fp32 mantissa is
-// rounded to M bits at bit 23-M (half to even, a carry steps the exponent) and the
-// exponent rebiased from 127 to B. The sign is kept (-0 for a negative underflow).
-template <int KF>
-__device__ __forceinline__ uint8_t fp8_round(float c) {
-  constexpr int M = KF == kE4M3 ? 3 : 2;
-  constexpr int B = KF == kE4M3 ? 7 : 15;
-  const uint32_t bits = __builtin_bit_cast(uint32_t, c);
-  const uint32_t sign = (bits >> 24) & 0x80u;
-  const uint32_t mag = bits & 0x7fffffffu;
-  uint32_t code;
-  if (mag < ((uint32_t)(128 - B) << 23)) {
-    code = (uint32_t)__builtin_rintf(__builtin_bit_cast(float, mag) * (float)(1 << (B - 1 + M)));
-  } else {
-    const uint32_t r = mag + ((1u << (22 - M)) - 1u) + ((mag >> (23 - M)) & 1u);
-    code = (r >> (23 - M)) - ((uint32_t)(127 - B) << M);
-  }
-  return (uint8_t)(code | sign);
-}
 constexpr int kMaxPerLane = 8;    // head_dim <= 512
 
 struct AppendArgs {
@@ -154,20 +132,12 @@ __global__ __launch_bounds__(256) void quantize_append_kernel(AppendArgs a) {
 #pragma unroll
   for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(x[i]));
   amax = wave_max(amax);
-  // kv_quantization.py:86-90 -- true division, then the FLT_MIN clamp.
-  constexpr float kMax = format_max<KF>();
-  const float scale = amax == 0.f ? 1.f : fmaxf(amax / kMax, FLT_MIN);
+  const float scale = quant_scale<KF>(amax);
   int8_t* codes = (rr.is_v ? a.cache.v_codes : a.cache.k_codes) +
                   block * a.cache.code_block_stride + rr.h * a.cache.code_head_stride + offset * D;
   int8_t q[N];
 #pragma unroll
-  for (int i = 0; i < N; ++i) {
-    // kv_quantization.py:91-94 -- divide, clamp, round half to even (int8) or to
-    // the nearest-even FP8 value
-    const float n = fminf(fmaxf(x[i] / scale, -kMax), kMax);
-    if constexpr (KF == kInt8) q[i] = (int8_t)__builtin_rintf(n);
-    else q[i] = (int8_t)fp8_round<KF>(n);
-  }
+  for (int i = 0; i < N; ++i) q[i] = quant_code<KF>(x[i], scale);
   if constexpr (VEC > 0) {
     struct alignas(VEC) Pack {
       int8_t e[VEC];

@@ -520,13 +520,23 @@ extern "C" size_t astr_paged_attention_i8_planned_workspace_bytes(
   return planned_workspace(*info, num_q_heads, head_dim);
 }
 
-extern "C" int astr_paged_attention_i8_planned(
-    const astr_paged_kv* cache, const void* query, int32_t q_dtype, int64_t q_token_stride,
-    int64_t q_head_stride, void* out, int64_t out_token_stride, int64_t out_head_stride,
-    const int32_t* context_lens, int32_t num_q_heads, float scale, const int32_t* plan,
-    const astr_decode_plan_info* info, void* workspace, size_t workspace_bytes,
-    int32_t* err_flag, void* stream) {
-  astr::CallRange range("astr_paged_attention_i8_planned");
+namespace {
+
+// The step's newest tokens for the appending decode (AttnArgs::new_k), or none.
+struct NewTokens {
+  const void* key = nullptr;
+  const void* value = nullptr;
+  int64_t k_tok = 0, k_head = 0, v_tok = 0, v_head = 0;
+  const int64_t* slots = nullptr;
+};
+
+int planned_attention(const astr_paged_kv* cache, const void* query, int32_t q_dtype,
+                      int64_t q_token_stride, int64_t q_head_stride, void* out,
+                      int64_t out_token_stride, int64_t out_head_stride,
+                      const int32_t* context_lens, int32_t num_q_heads, float scale,
+                      const int32_t* plan, const astr_decode_plan_info* info, void* workspace,
+                      size_t workspace_bytes, int32_t* err_flag, void* stream,
+                      const NewTokens& nt) {
   using namespace astr;
   using namespace astr::attn;
   if (cache == nullptr || err_flag == nullptr || info == nullptr)
@@ -620,6 +630,13 @@ extern "C" int astr_paged_attention_i8_planned(
   a.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                      align256(slots * cache->head_dim * sizeof(float)));
   a.err_flag = err_flag;
+  a.new_k = nt.key;
+  a.new_v = nt.value;
+  a.nk_tok = nt.k_tok;
+  a.nk_head = nt.k_head;
+  a.nv_tok = nt.v_tok;
+  a.nv_head = nt.v_head;
+  a.new_slots = nt.slots;
   p.plan = plan;
   p.info = pi;
   // the prefix tiles' partials, then the decode kernel and the chunk merge that reads them
@@ -628,4 +645,54 @@ extern "C" int astr_paged_attention_i8_planned(
     if (rc != 0) return rc;
   }
   return launch_planned(p, q_dtype, static_cast<hipStream_t>(stream), nullptr);
+}
+
+}  // namespace
+
+extern "C" int astr_paged_attention_i8_planned(
+    const astr_paged_kv* cache, const void* query, int32_t q_dtype, int64_t q_token_stride,
+    int64_t q_head_stride, void* out, int64_t out_token_stride, int64_t out_head_stride,
+    const int32_t* context_lens, int32_t num_q_heads, float scale, const int32_t* plan,
+    const astr_decode_plan_info* info, void* workspace, size_t workspace_bytes,
+    int32_t* err_flag, void* stream) {
+  astr::CallRange range("astr_paged_attention_i8_planned");
+  return planned_attention(cache, query, q_dtype, q_token_stride, q_head_stride, out,
+                           out_token_stride, out_head_stride, context_lens, num_q_heads, scale,
+                           plan, info, workspace, workspace_bytes, err_flag, stream,
+                           NewTokens{});
+}
+
+extern "C" int astr_paged_attention_i8_planned_append(
+    const astr_paged_kv* cache, const void* query, int32_t q_dtype, int64_t q_token_stride,
+    int64_t q_head_stride, void* out, int64_t out_token_stride, int64_t out_head_stride,
+    const void* key, const void* value, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, const int64_t* slot_mapping,
+    const int32_t* context_lens, int32_t num_q_heads, float scale, const int32_t* plan,
+    const astr_decode_plan_info* info, void* workspace, size_t workspace_bytes,
+    int32_t* err_flag, void* stream) {
+  astr::CallRange range("astr_paged_attention_i8_planned_append");
+  using astr::fail;
+  if (info != nullptr && info->num_seqs > 0) {
+    if (key == nullptr || value == nullptr || slot_mapping == nullptr)
+      return fail(ASTR_EINVAL, "key, value and slot_mapping are required");
+    if (q_dtype != ASTR_BF16 && q_dtype != ASTR_F16)
+      return fail(ASTR_EUNSUPPORTED, "the appending decode takes bf16/fp16 queries and rows");
+    // 4-byte lanes of each row (the rows' direct-to-LDS loads), 8-byte slots
+    if ((reinterpret_cast<uintptr_t>(key) | reinterpret_cast<uintptr_t>(value)) & 3u ||
+        (key_token_stride | key_head_stride | value_token_stride | value_head_stride) & 1 ||
+        (reinterpret_cast<uintptr_t>(slot_mapping) & 7u))
+      return fail(ASTR_EINVAL, "key/value rows must be 4-byte aligned and slot_mapping 8-byte "
+                  "aligned");
+  }
+  NewTokens nt;
+  nt.key = key;
+  nt.value = value;
+  nt.k_tok = key_token_stride;
+  nt.k_head = key_head_stride;
+  nt.v_tok = value_token_stride;
+  nt.v_head = value_head_stride;
+  nt.slots = slot_mapping;
+  return planned_attention(cache, query, q_dtype, q_token_stride, q_head_stride, out,
+                           out_token_stride, out_head_stride, context_lens, num_q_heads, scale,
+                           plan, info, workspace, workspace_bytes, err_flag, stream, nt);
 }

@@ -308,7 +308,7 @@ class PagedKVCache:
                         scale=None, window=None, partition_tokens=DEFAULT_PARTITION_TOKENS,
                         query_start_loc=None, max_query_len=None, causal=True,
                         out=None, workspace=None, work=None, check=False, prefix_packs=None,
-                        decode_plan=None):
+                        decode_plan=None, append=None):
         """Paged attention of this layer's arena for every row of a step.
 
         Decode (``query_start_loc=None``): one query token per sequence, ``query``
@@ -337,7 +337,13 @@ class PagedKVCache:
         ``decode_plan`` (decode, bf16/fp16 queries): a ``decode_plan.plan_decode``
         schedule of the same block tables and lengths (and window); the planned kernel
         streams the blocks the plan names and does not read ``block_tables``. Same
-        outputs as without it."""
+        outputs as without it.
+
+        ``append`` (with ``decode_plan``, bf16/fp16): ``(key, value, slot_mapping)`` of the
+        step's newest tokens, key/value ``[S, Hkv, D]`` in the query dtype and int64 slots
+        ``[S]`` the caller reserved. The decode quantizes and writes each token into the
+        arena and attends to it in the same launch: the outputs and the arena equal
+        ``append(..., reserved=True)`` followed by the call without it."""
         if query.ndim != 3 or query.shape[-1] != self.head_dim or query.device != self.device:
             raise ValueError("query must be [tokens, num_q_heads, head_dim] on the cache device")
         if query.dtype not in _DTYPE_CODES:
@@ -386,6 +392,23 @@ class PagedKVCache:
                     or decode_plan.info.num_kv_heads != self.num_kv_heads
                     or decode_plan.words.device != self.device):
                 raise ValueError("the decode plan was built for another batch")
+        if append is not None:
+            if decode_plan is None:
+                raise ValueError("an appending decode runs on a decode plan")
+            key, value, slots = append
+            _check_rows(key, "key", self.num_kv_heads, self.head_dim, self.device)
+            _check_rows(value, "value", self.num_kv_heads, self.head_dim, self.device)
+            if (key.dtype != query.dtype or value.dtype != query.dtype
+                    or query.dtype not in (torch.bfloat16, torch.float16)
+                    or key.shape[0] != num_tokens or value.shape[0] != num_tokens):
+                raise ValueError("an appending decode takes bf16/fp16 key/value rows "
+                                 "[S, Hkv, D] in the query dtype")
+            if not self.decode_appends(query.dtype):
+                raise UnsupportedAttentionBackend(
+                    "hip_int8_paged decodes append at head dims 128 and 256")
+            if (slots.dtype != torch.int64 or slots.shape != (num_tokens,)
+                    or slots.device != self.device or not slots.is_contiguous()):
+                raise ValueError("slot_mapping must be a contiguous int64 device vector [S]")
         if out is None:
             out = torch.empty_like(query)
         elif (not isinstance(out, torch.Tensor) or out.shape != query.shape
@@ -406,7 +429,16 @@ class PagedKVCache:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         ws = workspace.data_ptr() if need else None
         lib = _native.lib()
-        if decode_plan is not None:
+        if append is not None:
+            key, value, slots = append
+            rc = lib.astr_paged_attention_i8_planned_append(
+                self._descs[layer], query.data_ptr(), _DTYPE_CODES[query.dtype], query.stride(0),
+                query.stride(1), out.data_ptr(), out.stride(0), out.stride(1), key.data_ptr(),
+                value.data_ptr(), key.stride(0), key.stride(1), value.stride(0), value.stride(1),
+                slots.data_ptr(), context_lens.data_ptr(), num_q_heads, scale,
+                decode_plan.words.data_ptr(), ctypes.byref(decode_plan.info), ws, need,
+                self.err_flag.data_ptr(), stream)
+        elif decode_plan is not None:
             rc = lib.astr_paged_attention_i8_planned(
                 self._descs[layer], query.data_ptr(), _DTYPE_CODES[query.dtype], query.stride(0),
                 query.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
@@ -447,6 +479,12 @@ class PagedKVCache:
         if check:
             self.raise_errors()
         return out
+
+    def decode_appends(self, dtype):
+        """Whether a planned decode of this arena appends the step's ``dtype`` rows itself
+        (``paged_attention(append=...)``): bf16/fp16 at head dims 128 and 256 (at 64 the
+        token rows would cost the kernel its second workgroup per CU)."""
+        return dtype in (torch.bfloat16, torch.float16) and self.head_dim in (128, 256)
 
     def paged_attention_statistics(self, layer, query, block_tables, context_lens, *,
                                    max_context_len, scale=None, window=None,

@@ -13,6 +13,8 @@ that row loop:
     slots in one launch and runs one ragged attention launch (decode rows on the
     decode kernels, chunk rows on the prefill kernel) over history + chunk,
     causal within the chunk, exactly the keys the reference's per-row call sees;
+    a planned decode step with bf16/fp16 rows (head dims 128, 256) appends inside
+    the attention launch;
   * on exit it checks the device error flag and commits every reservation, or
     rolls all of them back if the step raised.
 
@@ -149,17 +151,23 @@ class PagedAttentionStep:
         if query.shape[0] != self.num_tokens or key.shape[0] != self.num_tokens:
             raise ValueError("query/key rows must match the step's tokens")
         cache = self.pool.cache
-        # the step's slots are reserved and rolled back if the step is flagged
-        cache.append(layer, key, value, self.slot_mapping, reserved=True)
         ws_work = self.work
         plan = self._decode_plan(query, window) if self.partition_tokens == 0 else None
         if plan is not None:
             # decode rows on the host schedule (one per step and shape); rows aliasing
-            # shared prefix pages read them once per prefix tile
+            # shared prefix pages read them once per prefix tile. bf16/fp16 rows are
+            # appended by the decode itself (one launch), into the step's reserved slots
+            fused = (cache.decode_appends(query.dtype) and key.dtype == query.dtype
+                     and value.dtype == query.dtype)
+            if not fused:
+                cache.append(layer, key, value, self.slot_mapping, reserved=True)
             return cache.paged_attention(
                 layer, query, self.block_tables, self.context_lens,
                 max_context_len=self.max_context_len, scale=scale, window=window, out=out,
-                work=ws_work, decode_plan=plan)
+                work=ws_work, decode_plan=plan,
+                append=(key, value, self.slot_mapping) if fused else None)
+        # the step's slots are reserved and rolled back if the step is flagged
+        cache.append(layer, key, value, self.slot_mapping, reserved=True)
         packs = (self._prefix_packs(query.shape[1])
                  if window is None and self.partition_tokens == 0 else None)
         if packs is not None:  # rows aliasing shared prefix pages read them once per pack

@@ -2,9 +2,10 @@
 
 A step is one decode-attention layer invocation of the hot path over the batch:
 quantize-and-append of the 64 new bf16 K/V tokens (one per sequence) via
-slot_mapping into their reserved slots (one launch, as the runner's step appends),
-then ragged paged attention of the 64 bf16 query rows (32 q heads, 8 kv heads,
-D=128) over their INT8 pages (context U[128,4096]) on the step's host plan. Steps
+slot_mapping into their reserved slots, and ragged paged attention of the 64 bf16 query
+rows (32 q heads, 8 kv heads, D=128) over their INT8 pages (context U[128,4096]) on the
+step's host plan, in one launch as the runner's decode step runs them (the decode
+quantizes each new token in the wave that streams its block). Steps
 cycle over ``--layers`` distinct layer arenas (default 4, ~1.1 GB) so each step reads
 its K/V from HBM, not from the 256 MB MALL, as a real multi-layer decode does.
 
@@ -204,12 +205,12 @@ def attention_caller(w, cache, q, device, partition, rows=None, packs=False, pla
                                       prefix_packs=plan))
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=device)
 
-    def call(layer):
+    def call(layer, append=None):
         cache.paged_attention(layer, q, tables, lens, max_context_len=w.max_context_len,
                               scale=w.scale, partition_tokens=partition, out=out, workspace=ws,
                               query_start_loc=qsl,
                               max_query_len=w.max_query_len if varlen else None,
-                              prefix_packs=plan, decode_plan=decode_plan)
+                              prefix_packs=plan, decode_plan=decode_plan, append=append)
 
     call.plan_us = plan_us
     call.planned = decode_plan is not None
@@ -341,10 +342,17 @@ def main():
     k_new, v_new, slots = step_batch
     varlen = w.query_lens is not None
 
+    # the runner's step: a planned bf16/fp16 decode appends the new tokens inside the
+    # attention launch; otherwise one append launch into the reserved slots, then the call
+    fused = call.planned and k_new.dtype == q.dtype and cache.decode_appends(q.dtype)
+
     def step(i):
         layer = i % L
-        cache.append(layer, k_new, v_new, slots, reserved=True)
-        call(layer)
+        if fused:
+            call(layer, append=(k_new, v_new, slots))
+        else:
+            cache.append(layer, k_new, v_new, slots, reserved=True)
+            call(layer)
 
     for i in range(args.warmup):
         step(i)
@@ -406,7 +414,9 @@ def main():
             "attended_kv_tokens": w.attended_tokens, "max_context_len": w.max_context_len,
             "append_tokens": int(k_new.shape[0]), "partition_tokens": args.partition,
             "layer_arenas": L,
-            "step": f"quantize_append_reserved({int(k_new.shape[0])} tok) + paged_attention",
+            "step": (f"paged_attention with the append of {int(k_new.shape[0])} tokens (one launch)"
+                     if fused else
+                     f"quantize_append_reserved({int(k_new.shape[0])} tok) + paged_attention"),
         },
         "hbm_fraction_of_step": alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "roofline": {

@@ -17,7 +17,9 @@
  *
  * Device error flag (int32, caller-zeroed, sticky until the caller clears it):
  *   bit 0 ASTR_FLAG_NONFINITE_INPUT  a K/V input value was NaN/Inf: the
- *                                    append wrote NO slot (all-or-nothing)
+ *                                    append wrote NO slot (all-or-nothing; the
+ *                                    reserved-slot appends: none of the
+ *                                    non-finite rows)
  *   bit 1 ASTR_FLAG_NONFINITE_SCORE  an attention score was NaN/Inf
  *   bit 2 ASTR_FLAG_BAD_INDEX        a slot / block-table entry / context
  *                                    length pointed outside the arena or
@@ -416,6 +418,39 @@ int astr_paged_attention_i8_planned(const astr_paged_kv* cache, const void* quer
                                     int32_t num_q_heads, float scale, const int32_t* plan,
                                     const astr_decode_plan_info* info, void* workspace,
                                     size_t workspace_bytes, int32_t* err_flag, void* stream);
+
+/*
+ * astr_kv_quantize_append_i8_reserved and astr_paged_attention_i8_planned in one
+ * launch: the decode step of PagedAttentionRunner.forward_batch with its chunk's
+ * quantize-then-append (paged_attention.py:185-192, 226-229; quantize_kv,
+ * kv_quantization.py:71-94) folded into the attention. Each sequence's newest token
+ * (position ctx - 1, one per decode row) comes as key/value rows of the query dtype
+ * (bf16/fp16): [num_seqs, num_kv_heads, head_dim], strides in elements (even), rows
+ * 4-byte aligned; slot_mapping: int64 [num_seqs] device slots the caller reserved
+ * (8-byte aligned). The wave that streams the block holding the token quantizes it
+ * (the quantizer's arithmetic, bit for bit), writes the codes and scales into the
+ * arena at slot_mapping[s] and into its copy of the block, so the call's outputs and
+ * the arena after it equal the two calls'. A slot that is not the plan's position of
+ * the token (block id of position ctx - 1 times 16 plus (ctx - 1) mod 16) raises
+ * ASTR_FLAG_BAD_INDEX (the token is still written at slot_mapping[s] when that lies in
+ * the arena); a token holding a NaN/Inf raises ASTR_FLAG_NONFINITE_INPUT and is not
+ * written, the call's other tokens may be: the caller rolls back reserved slots on a
+ * flagged call, as for astr_kv_quantize_append_i8_reserved. Plans from
+ * astr_decode_plan keep each newest token's block out of prefix tiles and out of the
+ * blocks a wave issues from its entry. Each newest token's block must be its own
+ * sequence's (no other row's table holds it), as the runner's copy-on-write
+ * reservations make it (state.py:306-310, 330-337): another row reading that block
+ * would see it as it was before the call. Other arguments as
+ * astr_paged_attention_i8_planned.
+ */
+int astr_paged_attention_i8_planned_append(
+    const astr_paged_kv* cache, const void* query, int32_t q_dtype, int64_t q_token_stride,
+    int64_t q_head_stride, void* out, int64_t out_token_stride, int64_t out_head_stride,
+    const void* key, const void* value, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, const int64_t* slot_mapping,
+    const int32_t* context_lens, int32_t num_q_heads, float scale, const int32_t* plan,
+    const astr_decode_plan_info* info, void* workspace, size_t workspace_bytes,
+    int32_t* err_flag, void* stream);
 
 /*
  * Bit-exact copy of whole blocks: block i of `num_blocks` goes from

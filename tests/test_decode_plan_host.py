@@ -76,7 +76,9 @@ def _check(tables, lens, hkv, window, wg, nw=8, tile_rows=0, tile_ranges=0, min_
         assert (ids[off:off + nb] == tables[lead, b0:b0 + nb]).all()
         for seq, c0, span in members[m0:m0 + n]:
             assert (tables[seq, b0:b0 + nb] == tables[lead, b0:b0 + nb]).all()
-            assert lens[seq] >= (b0 + nb) * 16 and not (window and lens[seq] > window)
+            # whole blocks before the newest token's (position ctx - 1), which stays
+            # the row's own (an appending decode writes it in the row's own block)
+            assert (lens[seq] - 1) // 16 >= b0 + nb and not (window and lens[seq] > window)
             assert span > r
             tiled.setdefault((int(seq), int(h)), []).append((int(b0), int(nb), int(c0 + h * span + r)))
     # workgroup g's items start at g * stride; each one's list starts at 0
@@ -120,8 +122,12 @@ def _check(tables, lens, hkv, window, wg, nw=8, tile_rows=0, tile_ranges=0, min_
             k = next(k for k in range(wgt[g, 0], wgt[g, 1])
                      if items[k, 6] <= lo < items[k, 6] + items[k, 3])
             assert (seq, kvh) == (items[k, 0], items[k, 1])
-            assert count == min(2, hi - lo, items[k, 6] + items[k, 3] - lo)
             first = items[k, 2] + lo - items[k, 6]
+            # never the block of the row's newest token (an appending decode stages the
+            # token with it, once the wave has its items)
+            newest = (items[k, 4] - 1) // 16 - first if items[k, 4] > 0 else -1
+            assert count == min(2, hi - lo, items[k, 6] + items[k, 3] - lo,
+                                newest if newest >= 0 else 2)
             assert (wents[g, w, 3:3 + count] == tables[seq, first:first + count]).all()
     # every row covered once; rows in several items or with tiles are chunked, with
     # consecutive slots (a member's tile ranges first)

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from aster_amd import KVQuantization, PagedKVCache
+from aster_amd import KVQuantization, PagedKVCache, UnsupportedAttentionBackend
 from aster_amd import _native
 from aster_amd import workloads as wl
 from aster_amd.decode_plan import plan_decode
@@ -100,7 +100,7 @@ def test_large_v_scales_and_extreme_scores(device):
 
 
 def _shared_workload(dim, hq, hkv, qdtype, seed=0, groups=(40, 7, 2), shared=(20, 9, 33),
-                     own_max=300):
+                     own_max=300, empty_own=True):
     """Groups of sequences whose tables begin with their group's blocks (a forked
     prefix), then blocks of their own (some none); groups interleaved in the batch,
     and a few rows sharing nothing."""
@@ -110,7 +110,7 @@ def _shared_workload(dim, hq, hkv, qdtype, seed=0, groups=(40, 7, 2), shared=(20
         prefix = list(range(nxt, nxt + shared[g]))
         nxt += shared[g]
         for i in range(n):
-            own = 0 if i % 9 == 4 else int(rng.integers(1, own_max + 1))
+            own = 0 if i % 9 == 4 and empty_own else int(rng.integers(1, own_max + 1))
             ctx = shared[g] * 16 + own
             nb = -(-ctx // 16)
             rows.append(prefix + list(range(nxt, nxt + nb - shared[g])))
@@ -292,3 +292,157 @@ def test_fp32_queries_on_the_full_config2_and_config1(device):
         plan_decode(w.block_tables, w.context_lens, num_q_heads=32, num_kv_heads=8,
                     head_dim=128, q_dtype=torch.float32, device=device,
                     code_format=FORMAT_CODES["fp8_e4m3fn"])
+
+
+# ---- the step's append inside the planned decode (astr_paged_attention_i8_planned_append)
+
+def _held_batch(w, cache, device):
+    """Fills `cache` with every token but each row's newest (position ctx - 1) and
+    returns those as per-sequence rows in the query dtype, with their slots (a zero row
+    and slot -1 where a row has no token)."""
+    _, (k, v, slots) = wl.materialize(w, cache, device=device, hold_last=True)
+    has = torch.from_numpy(w.context_lens > 0).to(device)
+    shape = (w.num_seqs,) + tuple(k.shape[1:])
+    key = torch.zeros(shape, dtype=w.q_dtype, device=device)
+    value = torch.zeros(shape, dtype=w.q_dtype, device=device)
+    slot = torch.full((w.num_seqs,), -1, dtype=torch.int64, device=device)
+    key[has], value[has], slot[has] = k.to(w.q_dtype), v.to(w.q_dtype), slots
+    return key, value, slot
+
+
+def _append_pair(w, device, fmt="int8", window=None, padding=False, scale_v=False,
+                 **plan_kw):
+    """The same step twice: the reserved-slot append then the planned decode, and the
+    planned decode that appends; returns both outputs and both arenas."""
+    caches = []
+    for _ in range(2):
+        cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=1,
+                             num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, device=device,
+                             quantization=KVQuantization(fmt))
+        held = _held_batch(w, cache, device)
+        if padding:
+            mark_padding(cache, w.block_tables, w.context_lens, 0.2, seed=5, whole_blocks=2)
+        if scale_v:
+            cache.scales[::5, 0, 1] *= 2.0 ** 10  # V scales past the f16 weight range
+        caches.append(cache)
+    tables, lens = wl.device_tables(w, device)
+    q = wl.queries(w, device)
+    plan = plan_decode(w.block_tables, w.context_lens, num_q_heads=w.num_q_heads,
+                       num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, q_dtype=w.q_dtype,
+                       device=device, code_format=FORMAT_CODES[fmt], window=window, **plan_kw)
+    key, value, slot = held
+    kw = dict(max_context_len=w.max_context_len, scale=w.scale, window=window,
+              decode_plan=plan, check=True)
+    caches[0].append(0, key, value, slot, reserved=True, check=True)
+    two = caches[0].paged_attention(0, q, tables, lens, **kw)
+    one = caches[1].paged_attention(0, q, tables, lens, append=(key, value, slot), **kw)
+    return two, one, caches, q, plan
+
+
+def _assert_same_step(two, one, caches):
+    assert torch.equal(two, one)
+    assert torch.equal(caches[0].codes, caches[1].codes)
+    assert torch.equal(caches[0].scales.view(torch.int32), caches[1].scales.view(torch.int32))
+
+
+@pytest.mark.parametrize("dim,hq,hkv", [(128, 8, 8), (128, 32, 8), (128, 128, 8), (256, 8, 2),
+                                        (256, 32, 4), (256, 16, 2)])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16])
+def test_append_in_decode_equals_append_then_decode(device, dim, hq, hkv, qdtype):
+    """Rows of 1..2048 tokens (and an empty one), newest tokens at every block offset:
+    outputs and arena bit for bit as the append launch followed by the decode, and the
+    oracle's result."""
+    w = _edge_workload(dim, hq, hkv, qdtype, seed=11)
+    two, one, caches, q, _ = _append_pair(w, device)
+    _assert_same_step(two, one, caches)
+    assert_attention_close(one, oracle_decode(w, caches[1], q))
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8_e4m3fn", "fp8_e5m2"])
+@pytest.mark.parametrize("window", [None, 100])
+def test_append_in_decode_formats_windows_padding(device, fmt, window):
+    w = _edge_workload(128, 16, 4, torch.bfloat16, seed=13)
+    two, one, caches, q, _ = _append_pair(w, device, fmt=fmt, window=window, padding=True,
+                                          scale_v=True)
+    _assert_same_step(two, one, caches)
+
+
+@pytest.mark.parametrize("workgroups", [40, 150])
+def test_append_in_decode_with_chunks_and_tiles(device, workgroups):
+    """Rows cut across workgroups (the newest token in one chunk) and rows sharing
+    prefixes (tiles end before any newest token's block)."""
+    w = _edge_workload(128, 32, 8, torch.bfloat16, seed=workgroups)
+    two, one, caches, _, plan = _append_pair(w, device, num_workgroups=workgroups)
+    assert plan.info.num_chunked > 0
+    _assert_same_step(two, one, caches)
+    # every row's newest token in a block of its own, as the runner's copy-on-write
+    # reservations keep it (a row with no block of its own would append into the pages
+    # its group shares)
+    w = _shared_workload(128, 32, 8, torch.bfloat16, seed=5, empty_own=False)
+    two, one, caches, _, plan = _append_pair(w, device, num_workgroups=workgroups,
+                                             tile_ranges=2)
+    assert plan.info.num_tiles > 0
+    _assert_same_step(two, one, caches)
+
+
+def test_append_in_decode_full_configs(device):
+    for w in (wl.config2(), wl.config4()):
+        two, one, caches, _, _ = _append_pair(w, device)
+        _assert_same_step(two, one, caches)
+
+
+def test_append_in_decode_nonfinite_and_wrong_slots_are_flagged(device):
+    w = _edge_workload(128, 32, 8, torch.bfloat16, seed=17)
+    cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=1, num_kv_heads=w.num_kv_heads,
+                         head_dim=w.head_dim, device=device)
+    key, value, slot = _held_batch(w, cache, device)
+    tables, lens = wl.device_tables(w, device)
+    q = wl.queries(w, device)
+    plan = plan_decode(w.block_tables, w.context_lens, num_q_heads=w.num_q_heads,
+                       num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, q_dtype=w.q_dtype,
+                       device=device)
+    kw = dict(max_context_len=w.max_context_len, scale=w.scale, decode_plan=plan)
+    # a non-finite value in one row: the input flag, and that token written nowhere
+    bad = value.clone()
+    bad[3, 2, 7] = float("nan")
+    before = cache.codes.clone()
+    cache.paged_attention(0, q, tables, lens, append=(key, bad, slot), **kw)
+    with pytest.raises(ValueError, match="finite"):
+        cache.raise_errors()
+    s3 = int(slot[3])
+    assert torch.equal(cache.codes[s3 // 16, 0, :, 2, s3 % 16], before[s3 // 16, 0, :, 2, s3 % 16])
+    # a slot that is not the plan's position of the token: the index flag; the token goes
+    # to the caller's slot (a spare block)
+    used = {int(b) for r, n in enumerate(-(-w.context_lens // 16)) for b in w.block_tables[r, :n]}
+    blk = min(set(range(w.num_blocks)) - used)
+    wrong = slot.clone()
+    wrong[5] = blk * 16 + 3
+    cache.paged_attention(0, q, tables, lens, append=(key, value, wrong), **kw)
+    with pytest.raises(ValueError, match="outside"):
+        cache.raise_errors()
+    probe = PagedKVCache(num_blocks=w.num_blocks, num_layers=1, num_kv_heads=w.num_kv_heads,
+                         head_dim=w.head_dim, device=device)
+    probe.append(0, key[5:6], value[5:6], wrong[5:6], check=True)
+    assert torch.equal(cache.codes[blk, 0, :, :, 3], probe.codes[blk, 0, :, :, 3])
+    with pytest.raises(ValueError, match="decode plan"):
+        cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                              append=(key, value, slot))
+
+
+def test_append_in_decode_head_dim_64_is_refused(device):
+    """At head dim 64 the decode does not append (its token rows would cost the kernel
+    its second workgroup per CU): refused, never run at half occupancy; the runner
+    appends in a launch of its own there."""
+    w = _edge_workload(64, 16, 2, torch.bfloat16, seed=19)
+    cache = PagedKVCache(num_blocks=w.num_blocks, num_layers=1, num_kv_heads=w.num_kv_heads,
+                         head_dim=w.head_dim, device=device)
+    key, value, slot = _held_batch(w, cache, device)
+    tables, lens = wl.device_tables(w, device)
+    q = wl.queries(w, device)
+    plan = plan_decode(w.block_tables, w.context_lens, num_q_heads=w.num_q_heads,
+                       num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, q_dtype=w.q_dtype,
+                       device=device)
+    assert not cache.decode_appends(torch.bfloat16)
+    with pytest.raises(UnsupportedAttentionBackend):
+        cache.paged_attention(0, q, tables, lens, max_context_len=w.max_context_len,
+                              scale=w.scale, decode_plan=plan, append=(key, value, slot))
