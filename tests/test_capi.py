@@ -241,3 +241,33 @@ def test_merge_softmax_rejects_overlapping_outputs_without_launching():
     assert f(*ins, om, ol, ln + wide_b - 4, rows, width, None) == _native.ASTR_EINVAL  # partial
     assert f(*ins, om, om + row_b - 4, on, rows, width, None) == _native.ASTR_EINVAL  # out/out
     assert f(*ins, om, ol, on, 0, width, None) == 0  # no rows: nothing to launch
+
+
+def test_planned_append_argument_errors_need_no_device():
+    """astr_paged_attention_i8_planned_append checks its token rows before anything
+    else: key/value/slot_mapping are required, bf16/fp16 only, rows 4-byte aligned and
+    slots 8-byte aligned; a plan without sequences launches nothing."""
+    from aster_amd.decode_plan import DecodePlanInfo
+
+    info = DecodePlanInfo()
+    info.num_seqs = 4
+
+    def call(**kw):
+        args = dict(query=16, q_dtype=2, q_tok=128, q_head=128, out=16, o_tok=128, o_head=128,
+                    key=16, value=16, k_tok=1024, k_head=128, v_tok=1024, v_head=128,
+                    slots=16, lens=16, hq=32, scale=0.1, plan=16, info=ctypes.byref(info),
+                    ws=None, ws_bytes=0, flag=16)
+        args.update(kw)
+        return _native.lib().astr_paged_attention_i8_planned_append(
+            ctypes.byref(_desc(num_kv_heads=8)), *args.values(), None)
+
+    assert call(key=None) == _native.ASTR_EINVAL
+    assert "key, value and slot_mapping" in _native.last_error()
+    assert call(slots=None) == _native.ASTR_EINVAL
+    assert call(q_dtype=0) == _native.ASTR_EUNSUPPORTED  # fp32 rows: appended separately
+    assert call(key=18) == _native.ASTR_EINVAL            # rows not 4-byte aligned
+    assert call(k_head=127) == _native.ASTR_EINVAL        # odd element stride
+    assert call(slots=20) == _native.ASTR_EINVAL          # slots not 8-byte aligned
+    assert "aligned" in _native.last_error()
+    info.num_seqs = 0
+    assert call(key=None) == 0                            # nothing to do
