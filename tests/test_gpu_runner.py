@@ -115,3 +115,36 @@ def test_pack_unpack_reference_layout(device):
     for b, n in enumerate(counts):
         assert torch.equal(back[b, :, :n], x[b, :, :n])
         assert (back[b, :, n:] == 0).all()
+
+
+def test_bf16_decode_step_with_nonfinite_key_rolls_back(device):
+    """A bf16 decode step appends inside the planned attention launch; a non-finite
+    key raises the reference's error at commit and rolls every reservation back: the
+    pool's pages equal those before the step, token for token."""
+    pool = PagedStatePool(PagedKVCache(num_blocks=64, num_layers=1, num_kv_heads=2,
+                                       head_dim=128, device=device))
+    seqs = [pool.create("tenant") for _ in range(3)]
+    gen = torch.Generator(device=device).manual_seed(7)
+
+    def rows(n, heads):
+        return torch.randn(n, heads, 128, generator=gen, device=device).to(torch.bfloat16)
+
+    with PagedAttentionStep(pool, seqs, [37, 5, 20]) as step:  # a prefill step
+        step.attend(0, rows(62, 8), rows(62, 2), rows(62, 2), scale=128 ** -0.5)
+    before = [pool.materialize(s) for s in seqs]
+    used = pool.used_blocks
+    key = rows(3, 2)
+    key[1, 1, 9] = float("nan")
+    with pytest.raises(ValueError, match="finite"):
+        with PagedAttentionStep(pool, seqs, [1, 1, 1]) as step:
+            assert step.attend(0, rows(3, 8), key, rows(3, 2),
+                               scale=128 ** -0.5).shape == (3, 8, 128)
+    assert pool.used_blocks == used and [s.length for s in seqs] == [37, 5, 20]
+    for s, old in zip(seqs, before):
+        for a, b in zip(pool.materialize(s), old):
+            for x, y in zip(a, b):
+                assert torch.equal(x, y)
+    # a clean decode step then commits (the flag was cleared)
+    with PagedAttentionStep(pool, seqs, [1, 1, 1]) as step:
+        step.attend(0, rows(3, 8), rows(3, 2), rows(3, 2), scale=128 ** -0.5)
+    assert [s.length for s in seqs] == [38, 6, 21]
