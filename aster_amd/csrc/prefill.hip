@@ -41,6 +41,22 @@ constexpr int KF = ASTR_KF;  // this translation unit's code format
 constexpr int kXcds = 8;
 constexpr int kPrefillBuffers = 3;
 
+// Per-wave timeline of the prefix-tile kernel (trace builds only, -DASTR_TRACE=1, built
+// apart from the product library by `python -m aster_amd.build --trace`): wall-clock
+// marks (100 MHz s_memrealtime) of each wave of the last launch, read back with
+// astr_trace_read_tiles. Marks: 0 entry, 1 tile and members checked, 2 query columns
+// quantized (the first steps' loads in flight), 3 first key step done, 4 key steps done,
+// 5 partials stored. Info: key steps, XCC id, kv head, key range.
+#ifndef ASTR_TRACE
+#define ASTR_TRACE 0
+#endif
+constexpr bool kTrace = ASTR_TRACE != 0;
+#if ASTR_TRACE
+constexpr int kTileTraceWaves = 8192;
+static __device__ long long g_ttrace[kTileTraceWaves][8];
+static __device__ int g_ttrace_info[kTileTraceWaves][4];
+#endif
+
 template <int D>
 struct PrefillShape {
   static constexpr int NT = D == 256 ? 1 : 2;     // 16-column MFMA tiles per wave
@@ -707,11 +723,13 @@ struct WaveBounds {
 // workgroup's query columns (column_of(f), bounds_of(wave)), through the key steps
 // described at the top of this file; store(t, acc, m, lt, ve, col) then takes column
 // tile t of each wave (acc in units of 2^-ve, lt the row sums of lane (0, r)'s column).
-template <typename QT, int D, int G, typename ColumnOf, typename BoundsOf, typename Store>
+// mark(k) is called at the unit's timeline marks 2-5 (the tile kernel's trace builds).
+template <typename QT, int D, int G, typename ColumnOf, typename BoundsOf, typename Store,
+          typename Mark>
 __device__ __forceinline__ void prefill_unit(const AttnArgs& a, PrefillLds<D>& L, int kvh,
                                              int b_lo, int b_hi, const int32_t* blocks, int q0,
                                              int t0, ColumnOf column_of, BoundsOf bounds_of,
-                                             Store store) {
+                                             Store store, Mark mark) {
   using S = Stage<D>;
   constexpr int NT = PrefillShape<D>::NT;
   constexpr int NPV = D / 16;
@@ -801,6 +819,7 @@ __device__ __forceinline__ void prefill_unit(const AttnArgs& a, PrefillLds<D>& L
     cfe[t] = cf[t] > 0.f ? cf[t] : FLT_MIN;  // cf >= 0 or NaN (scale > 0)
   }
   const WaveBounds wb = bounds_of(wave);
+  mark(2);
 
   const ColumnRefs<NT> cols{q0, t0, ctok, chead, cvalid};
   float4_t acc[NT][NPV + 1];  // [NPV]: row sums in row 0 (lanes qg = 0)
@@ -884,7 +903,9 @@ __device__ __forceinline__ void prefill_unit(const AttnArgs& a, PrefillLds<D>& L
                                 r, qg, ones, vf, acc, m, bad_score, a, cols);
     }
     __syncthreads();  // step i's stage may be refilled
+    if (i == 0) mark(3);
   }
+  mark(4);
   if (bad_index && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
   if (bad_score && lane == 0) atomicOr(a.err_flag, ASTR_FLAG_NONFINITE_SCORE);
 
@@ -893,6 +914,7 @@ __device__ __forceinline__ void prefill_unit(const AttnArgs& a, PrefillLds<D>& L
     const float lt = __shfl(acc[t][NPV][0], r, kWave);  // row 0 of the sum tile: lane (0, r)
     store(t, acc[t], m[t], lt, ve, ColumnInfo{ctok[t], chead[t], lo[t], hi[t], cvalid[t]});
   }
+  mark(5);
 }
 
 template <typename QT, int D, int G>
@@ -993,7 +1015,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   };
   prefill_unit<QT, D, G>(a, L, kvh, span.b_lo, span.b_hi,
                          a.block_tables + (int64_t)seq * a.bt_stride, q0, t0, column_of,
-                         bounds_of, store);
+                         bounds_of, store, [](int) {});
 }
 
 // Prefix tiles of a decode plan (decode_plan.cpp): the shared blocks of sequences whose
@@ -1023,6 +1045,8 @@ __global__ __launch_bounds__(256) void prefix_tiles_kernel(PlanArgs p) {
   const int lane = threadIdx.x % kWave;
   const int qg = lane >> 4;
   const int hkv = a.cache.num_kv_heads;
+  long long tm[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // trace marks (kTrace)
+  if constexpr (kTrace) tm[0] = wall_clock64();
   const int64_t units = p.info.num_tiles;
   const int64_t per_xcd = (units + kXcds - 1) / kXcds;
   const int64_t slot = blockIdx.x / kXcds;
@@ -1059,6 +1083,7 @@ __global__ __launch_bounds__(256) void prefix_tiles_kernel(PlanArgs p) {
     return;  // the whole workgroup
   }
   const int row0 = s_row[0];  // the row invalid columns read
+  if constexpr (kTrace) tm[1] = wall_clock64();
 
   auto column_of = [&](int f) __attribute__((always_inline)) -> ColumnInfo {
     const int j = f / G;
@@ -1070,29 +1095,66 @@ __global__ __launch_bounds__(256) void prefix_tiles_kernel(PlanArgs p) {
   };
   // the partial of column (member j, head g): m, l and acc into the member's chunk
   // slot, head g, with acc and l in the decode kernels' units (both times norm_scale,
-  // as the decode partials they merge with)
+  // as the decode partials they merge with). Lane (qg, r) holds elements
+  // [D/4 qg, D/4 (qg + 1)) of column r: written as they are, every store instruction
+  // would touch 64 cache lines. The tile goes through the wave's share of the stage
+  // buffers (free after the last key step's barrier) instead, and each store
+  // instruction then writes 1 KB of whole columns (4 to 16 cache lines).
+  constexpr int kRow = D + 4;  // floats per staged column (padded against bank conflicts)
+  static_assert(kWaves * 16 * kRow * (int)sizeof(float) <= (int)sizeof(L.stages),
+                "a wave's column tile fits its share of the stages");
   auto store = [&](int t, const float4_t (&acc)[NPV + 1], float m, float lt, int ve,
                    const ColumnInfo& c) __attribute__((always_inline)) {
-    if (!c.valid) return;
-    const int f = (__builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * PrefillShape<D>::NT + t) * 16 +
-                  (lane & 15);
-    const int64_t col = plan_chunk_slot(p, s_slot[f / G], G) + f % G;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int f0 = (wave * PrefillShape<D>::NT + t) * 16;  // the tile's first column
+    float* const tile = reinterpret_cast<float*>(L.stages) + wave * 16 * kRow;
     const float up = ldexpf(norm_scale<KF>(), ve);  // the PV tiles carry 2^-ve
-    float* dst = a.ws_o + col * D;
+    __builtin_amdgcn_wave_barrier();  // after the previous tile's reads of this share
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v[VB];
 #pragma unroll
       for (int k = 0; k < NPV; ++k) v[k] = acc[k][j] * up;
-      store_run<float, VB>(dst + VB * (4 * qg + j), v);
+#pragma unroll
+      for (int k = 0; k < VB / 4; ++k)
+        *reinterpret_cast<float4_t*>(tile + (lane & 15) * kRow + VB * (4 * qg + j) + 4 * k) =
+            float4_t{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
     }
-    if (qg == 0) {
+    __builtin_amdgcn_wave_barrier();  // a wave's LDS accesses complete in issue order
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) {
+      const int e = i * kWave + lane;  // float4 e of the tile: column e / (D/4)
+      const int cc = e / (D / 4), q = e % (D / 4);
+      const int f = f0 + cc;
+      const float4_t v = *reinterpret_cast<const float4_t*>(tile + cc * kRow + 4 * q);
+      if (f / G < n) {
+        const int64_t col = plan_chunk_slot(p, s_slot[f / G], G) + f % G;
+        *reinterpret_cast<float4_t*>(a.ws_o + col * D + 4 * q) = v;
+      }
+    }
+    if (c.valid && qg == 0) {
+      const int f = f0 + (lane & 15);
+      const int64_t col = plan_chunk_slot(p, s_slot[f / G], G) + f % G;
       a.ws_ml[col * 2] = m;
       a.ws_ml[col * 2 + 1] = lt * norm_scale<KF>();
     }
   };
   const int32_t* ids = p.plan + p.info.off_ids + ids_off - blk0;  // id of block b at ids[b]
-  prefill_unit<QT, D, G>(a, L, kvh, blk0, blk0 + nblk, ids, 0, row0, column_of, bounds_of, store);
+  auto mark = [&](int k) __attribute__((always_inline)) {
+    if constexpr (kTrace) tm[k] = wall_clock64();
+  };
+  prefill_unit<QT, D, G>(a, L, kvh, blk0, blk0 + nblk, ids, 0, row0, column_of, bounds_of, store,
+                         mark);
+#if ASTR_TRACE
+  const int64_t tw = unit * kWaves + threadIdx.x / kWave;
+  if (lane == 0 && tw < kTileTraceWaves) {
+    for (int k = 0; k < 8; ++k) g_ttrace[tw][k] = tm[k];
+    g_ttrace_info[tw][0] = (nblk + kWaves - 1) / kWaves;
+    g_ttrace_info[tw][1] = (int)__builtin_amdgcn_s_getreg((20 << 0) | (0 << 6) | (3 << 11));  // XCC_ID
+    g_ttrace_info[tw][2] = kvh;
+    g_ttrace_info[tw][3] = range;
+  }
+#endif
 }
 
 template <typename QT, int D, int G>
@@ -1168,6 +1230,18 @@ int tiles_dim(const PlanArgs& p, int G, hipStream_t s) {
 }
 
 }  // namespace
+
+#if ASTR_TRACE && ASTR_KF == 0
+// Trace builds: copies the marks and info of the first `waves` waves of the last
+// prefix-tile launch of the int8 format (8 int64 + 4 int32 per wave; wave w of tile
+// unit u at u * 4 + w) to host memory.
+extern "C" int astr_trace_read_tiles(void* marks, void* info, int waves) {
+  if (waves < 0 || waves > kTileTraceWaves) return ASTR_EINVAL;
+  hipError_t e = hipMemcpyFromSymbol(marks, HIP_SYMBOL(g_ttrace), (size_t)waves * 64);
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(info, HIP_SYMBOL(g_ttrace_info), (size_t)waves * 16);
+  return e == hipSuccess ? 0 : (int)e;
+}
+#endif
 
 template <>
 int launch_prefix_tiles_kf<KF>(const PlanArgs& p, int32_t q_dtype, hipStream_t stream) {

@@ -12,13 +12,15 @@
       launches of one kernel, e.g. bench.py's prefill-only calls in a mixed step).
   python -m aster_amd.profiling durations <rocprof_dir> [kernel_substring]
       The same statistics of kernel durations (us) from ``*_kernel_trace.csv``.
-  python -m aster_amd.profiling timeline [config2|config4|config5] [--packs | --planned [--tail N]]
+  python -m aster_amd.profiling timeline [config2|config4|config5] [--packs | --planned [--tail N] [--tile-ranges R]]
       Per-wave timeline of the stream-K (or, --planned, the planned) decode kernel on a
       BASELINE workload, from
       the trace build (``python -m aster_amd.build --trace``, which records wall-clock
       marks per wave): when waves start, have their block ids and first block, and
       end, per XCC and by the number of pieces (rows) a wave streams, and what a row
-      start inside a wave costs. Runs a few calls and reads the last one.
+      start inside a wave costs; with --planned on a plan with prefix tiles (config4),
+      also the prefix-tile kernel's waves: members checked, queries quantized, first
+      and later key steps, partials stored. Runs a few calls and reads the last one.
   python -m aster_amd.profiling traffic <fetch_dir> <write_dir> <cal_fetch_dir> <cal_write_dir> [kernel_substring]
       HBM bytes per launch per kernel (median dispatch) from a FETCH_SIZE and a
       WRITE_SIZE run, each scaled by what the counter reads for ``copy`` (the
@@ -110,11 +112,12 @@ def traffic(fetch_dir, write_dir, cal_fetch_dir, cal_write_dir, pattern="astr", 
             "calibration": {"fetch_scale": round(fs, 7), "write_scale": round(ws, 7)}}
 
 
-def _decode_calls(config, packs, q_dtype, calls, planned=False, tail=None):
+def _decode_calls(config, packs, q_dtype, calls, planned=False, tail=None, tile_ranges=0):
     """Run ``calls`` paged_attention calls of a BASELINE decode workload over four layer
     arenas, cycled, so that a call does not find the previous call's K/V in the
     memory-side cache (as bench.py does). ``q_dtype`` overrides the workload's query
-    type ("float32" routes to the exact fp32 kernel)."""
+    type ("float32" routes to the exact fp32 kernel). Returns the decode plan of
+    ``planned`` calls (else None)."""
     import torch
 
     from . import workloads as wl
@@ -143,7 +146,8 @@ def _decode_calls(config, packs, q_dtype, calls, planned=False, tail=None):
         schedule = plan_decode(w.block_tables, w.context_lens, num_q_heads=w.num_q_heads,
                                num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
                                q_dtype=q.dtype, device=dev,
-                               tail_blocks=DEFAULT_TAIL_BLOCKS if tail is None else tail)
+                               tail_blocks=DEFAULT_TAIL_BLOCKS if tail is None else tail,
+                               tile_ranges=tile_ranges)
         plan = None
     for i in range(calls):
         cache.paged_attention(i % layers, q, tables, lens, max_context_len=w.max_context_len,
@@ -151,14 +155,59 @@ def _decode_calls(config, packs, q_dtype, calls, planned=False, tail=None):
     torch.cuda.synchronize()
     print(f"{calls} calls of {config} (packs={bool(packs)}, planned={bool(planned)}, "
           f"queries {q.dtype})", flush=True)
+    return schedule
 
 
-def planned_timeline(config="config2", calls=7, tail=None):
+def _trace_marks(lib, reader, n):
+    """(marks, info) of the first ``n`` waves from a trace build's reader entry."""
+    import ctypes
+
+    import numpy as np
+
+    fn = getattr(lib, reader)
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+    marks = np.zeros((n, 8), np.int64)
+    info = np.zeros((n, 4), np.int32)
+    rc = fn(marks.ctypes.data, info.ctypes.data, n)
+    if rc != 0:
+        raise RuntimeError(f"{reader} failed ({rc})")
+    return marks, info
+
+
+def _tiles_report(marks, info, decode_start):
+    """Timeline of the prefix-tile kernel's waves (us from the first tile wave's start)
+    and the gap to the planned decode kernel's first wave (``decode_start``, raw clock)."""
+    import numpy as np
+
+    live = marks[:, 0] != 0
+    marks, info = marks[live], info[live]
+    origin = marks[:, 0].min()
+    t = (marks - origin) / 100.0
+    steps, xcc = info[:, 0], info[:, 1]
+    pct = lambda x, p: [round(float(v), 2) for v in np.percentile(x, p)]
+    multi = steps > 1
+    return {"waves": int(live.sum()), "steps_per_unit": pct(steps, [0, 50, 100]),
+            "start_us": pct(t[:, 0], [0, 50, 100]),
+            "checked_us": pct(t[:, 1] - t[:, 0], [50, 90]),
+            "queries_us": pct(t[:, 2] - t[:, 1], [50, 90]),
+            "first_step_us": pct(t[:, 3] - t[:, 2], [50, 90]),
+            "later_step_us": (round(float(((t[multi, 4] - t[multi, 3]) /
+                                           (steps[multi] - 1)).mean()), 3)
+                              if multi.any() else None),
+            "store_us": pct(t[:, 5] - t[:, 4], [50, 90]),
+            "exit_pct_50_90_100_us": pct(t[:, 5], [50, 90, 100]),
+            "per_xcc_max_exit": {int(x): round(float(t[xcc == x, 5].max()), 2)
+                                 for x in np.unique(xcc)},
+            "decode_first_wave_after_last_tile_us": round(
+                float((decode_start - marks[:, 5].max()) / 100.0), 2)}
+
+
+def planned_timeline(config="config2", calls=7, tail=None, tile_ranges=0):
     """The trace build's per-wave marks of the planned decode kernel (the last of
     ``calls`` planned calls over ``config``), as a report dict (us from the first wave's
     start): startup to items checked, block ids, first block; streaming end; the
-    workgroup barrier; exit after the workgroup's merges."""
-    import ctypes
+    workgroup barrier; exit after the workgroup's merges. Where the plan has prefix
+    tiles, ``tiles`` gives the tile kernel's timeline in the same call."""
     import contextlib
     import io
 
@@ -169,15 +218,14 @@ def planned_timeline(config="config2", calls=7, tail=None):
     _native.LIB_PATH = build.TRACE_OUT
     _native._lib = None
     lib = _native.lib()
-    lib.astr_trace_read_planned.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
     with contextlib.redirect_stdout(io.StringIO()):
-        _decode_calls(config, False, None, calls, planned=True, tail=tail)
-    n = 16384
-    marks = np.zeros((n, 8), np.int64)
-    info = np.zeros((n, 4), np.int32)
-    rc = lib.astr_trace_read_planned(marks.ctypes.data, info.ctypes.data, n)
-    if rc != 0:
-        raise RuntimeError(f"astr_trace_read_planned failed ({rc})")
+        plan = _decode_calls(config, False, None, calls, planned=True, tail=tail,
+                             tile_ranges=tile_ranges)
+    marks, info = _trace_marks(lib, "astr_trace_read_planned", 16384)
+    tiles = None
+    if plan is not None and plan.info.num_tiles > 0:
+        tm, ti = _trace_marks(lib, "astr_trace_read_tiles", 8192)
+        tiles = _tiles_report(tm, ti, marks[marks[:, 0] != 0, 0].min())
     live = marks[:, 0] != 0
     wave_ids = np.nonzero(live)[0]
     marks, info = marks[live], info[live]
@@ -214,6 +262,8 @@ def planned_timeline(config="config2", calls=7, tail=None):
                                "mean_end": round(float(t[xcc == x, 4].mean()), 2),
                                "max_end": round(float(t[xcc == x, 4].max()), 2)}
                       for x in np.unique(xcc)}
+    if tiles is not None:
+        rep["tiles"] = tiles
     # per number of pieces (rows the wave starts): end time and streaming time per block
     rep["by_pieces"] = {}
     for k in sorted(np.unique(np.minimum(pieces[streaming], 4))):
@@ -304,6 +354,7 @@ def main():
     t.add_argument("--packs", action="store_true")
     t.add_argument("--planned", action="store_true")
     t.add_argument("--tail", type=int, default=None)
+    t.add_argument("--tile-ranges", type=int, default=0)
     d = sub.add_parser("calls")
     d.add_argument("config", nargs="?", default="config2")
     d.add_argument("--packs", action="store_true")
@@ -331,7 +382,8 @@ def main():
     if args.cmd == "timeline":
         import json
 
-        rep = (planned_timeline(args.config, tail=args.tail) if args.planned else
+        rep = (planned_timeline(args.config, tail=args.tail, tile_ranges=args.tile_ranges)
+               if args.planned else
                timeline(args.config, args.packs))
         print(json.dumps(rep, indent=1))
         return
