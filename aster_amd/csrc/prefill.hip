@@ -723,13 +723,16 @@ struct WaveBounds {
 // workgroup's query columns (column_of(f), bounds_of(wave)), through the key steps
 // described at the top of this file; store(t, acc, m, lt, ve, col) then takes column
 // tile t of each wave (acc in units of 2^-ve, lt the row sums of lane (0, r)'s column).
-// mark(k) is called at the unit's timeline marks 2-5 (the tile kernel's trace builds).
+// prologue() runs (in uniform control flow) once the stages are cleared and the first
+// block ids are on their way, before any column is read: it returns false (uniformly)
+// to end the unit there, with nothing stored. mark(k) is called at the unit's timeline
+// marks 2-5 (the tile kernel's trace builds).
 template <typename QT, int D, int G, typename ColumnOf, typename BoundsOf, typename Store,
-          typename Mark>
+          typename Prologue, typename Mark>
 __device__ __forceinline__ void prefill_unit(const AttnArgs& a, PrefillLds<D>& L, int kvh,
                                              int b_lo, int b_hi, const int32_t* blocks, int q0,
                                              int t0, ColumnOf column_of, BoundsOf bounds_of,
-                                             Store store, Mark mark) {
+                                             Store store, Prologue prologue, Mark mark) {
   using S = Stage<D>;
   constexpr int NT = PrefillShape<D>::NT;
   constexpr int NPV = D / 16;
@@ -739,6 +742,23 @@ __device__ __forceinline__ void prefill_unit(const AttnArgs& a, PrefillLds<D>& L
   const int r = lane & 15, qg = lane >> 4;
   char* const lds = L.stages;
   const int nsteps = (b_hi - b_lo + kWaves - 1) / kWaves;
+
+  // The block ids of the first 64 steps go out first, so that their load overlaps the
+  // clearing of the stages and the prologue. After each load the ids pass through an
+  // empty asm that redefines them: the one wait for their load happens there (once per
+  // 64 steps), and the compiler's wait tracking no longer treats them as a pending load
+  // at every issue below (where it would wait for every stage in flight, vmcnt(0), each
+  // step).
+  int ids = 0;
+  auto fetch_ids = [&](int s0) __attribute__((always_inline)) {
+    const int blk = b_lo + (s0 + lane) * kWaves + wave;
+    ids = (s0 + lane < nsteps && blk < b_hi) ? blocks[blk] : 0;
+  };
+  auto load_ids = [&](int s0) __attribute__((always_inline)) {
+    fetch_ids(s0);
+    asm volatile("" : "+v"(ids));
+  };
+  if (nsteps > 0) fetch_ids(0);
 
   // zero scales in every stage, once every wave is past its last read of what the
   // stages held before (the dispatch plan): a stage that no step writes (a block past
@@ -755,23 +775,16 @@ __device__ __forceinline__ void prefill_unit(const AttnArgs& a, PrefillLds<D>& L
                                S::kK)[j % (2 * D)] = uint4{0u, 0u, 0u, 0u};
   }
   __syncthreads();
+  if (!prologue()) {
+    wait_vmcnt<0>();
+    return;
+  }
 
-  // ---- this wave's columns. The block ids and the query go out together; the first
-  // steps' loads are issued before the query is quantized.
+  // ---- this wave's columns: the query goes out, then the first steps' loads, before
+  // the query is quantized.
   int lo[NT], hi[NT], ctok[NT], chead[NT];
   bool cvalid[NT];
   QueryColumn<QT, D> qraw[NT];
-  int ids = 0;
-  // After each load the ids pass through an empty asm that redefines them: the one wait
-  // for their load happens there (once per 64 steps), and the compiler's wait tracking
-  // no longer treats them as a pending load at every issue below (where it would wait
-  // for every stage in flight, vmcnt(0), each step).
-  auto load_ids = [&](int s0) __attribute__((always_inline)) {
-    const int blk = b_lo + (s0 + lane) * kWaves + wave;
-    ids = (s0 + lane < nsteps && blk < b_hi) ? blocks[blk] : 0;
-    asm volatile("" : "+v"(ids));
-  };
-  if (nsteps > 0) load_ids(0);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const ColumnInfo c = column_of((wave * NT + t) * 16 + r);
@@ -803,6 +816,7 @@ __device__ __forceinline__ void prefill_unit(const AttnArgs& a, PrefillLds<D>& L
   auto buffer = [&](int step) __attribute__((always_inline)) -> char* {
     return lds + (step % NB) * kWaves * S::kBytes;
   };
+  asm volatile("" : "+v"(ids));  // the first ids have landed
   // bit (step % NB): this wave issued loads for that step (uniform over the wave)
   uint32_t inflight = 0;
   for (int j = 0; j < NB - 1 && j < nsteps; ++j)
@@ -1015,7 +1029,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(AttnArgs a) {
   };
   prefill_unit<QT, D, G>(a, L, kvh, span.b_lo, span.b_hi,
                          a.block_tables + (int64_t)seq * a.bt_stride, q0, t0, column_of,
-                         bounds_of, store, [](int) {});
+                         bounds_of, store, []() { return true; }, [](int) {});
 }
 
 // Prefix tiles of a decode plan (decode_plan.cpp): the shared blocks of sequences whose
@@ -1053,41 +1067,41 @@ __global__ __launch_bounds__(256) void prefix_tiles_kernel(PlanArgs p) {
   const int64_t unit = (int64_t)(blockIdx.x % kXcds) * per_xcd + slot;
   if (slot >= per_xcd || unit >= units) return;
 
-  // ---- the tile and its members, every index checked (the plan is untrusted)
+  // ---- the tile, every index checked (the plan is untrusted); its members are read and
+  // checked in the unit's prologue, while the first block ids load
   const int32_t* rec = p.plan + p.info.off_tiles + unit * kTileWords;
   const int m0 = rec[0], n = rec[1], kvh = rec[2], range = rec[3];
   const int blk0 = rec[4], nblk = rec[5], ids_off = rec[6], lead = rec[7];
-  if (threadIdx.x == 0) s_bad = 0;
-  __syncthreads();
-  bool bad = !(m0 >= 0 && n >= 1 && n <= TQ && n <= p.info.num_tile_members - m0 && kvh >= 0 &&
-               kvh < hkv && range >= 0 && range < p.info.tile_ranges && blk0 >= 0 && nblk >= 0 &&
-               ids_off >= 0 && nblk <= p.info.num_ids - ids_off && lead >= 0 && lead < a.num_seqs);
-  if (!bad && (int)threadIdx.x < n) {
-    const int32_t* mem = p.plan + p.info.off_tile_members + (int64_t)(m0 + threadIdx.x) * kMemberWords;
-    const int seq = mem[0], c0 = mem[1], span = mem[2];
-    bad = !(seq >= 0 && seq < a.num_seqs && c0 >= 0 && span > range &&
-            (int64_t)c0 + (int64_t)hkv * span <= p.info.num_chunks);
-    if (!bad) {
-      s_row[threadIdx.x] = seq;  // decode rows: sequence s's query token is row s
-      s_slot[threadIdx.x] = c0 + kvh * span + range;
-      // every key of the range must be visible to the member (its length as planned)
-      const RowSpan sp = row_span(a, a.context_lens[seq]);
-      if (sp.kv_begin > blk0 * kBlockTokens || (int64_t)sp.ctx < (int64_t)(blk0 + nblk) * kBlockTokens)
-        atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
-    }
-  }
-  if (bad) s_bad = 1;
-  __syncthreads();
-  if (s_bad) {
+  if (!(m0 >= 0 && n >= 1 && n <= TQ && n <= p.info.num_tile_members - m0 && kvh >= 0 &&
+        kvh < hkv && range >= 0 && range < p.info.tile_ranges && blk0 >= 0 && nblk >= 0 &&
+        ids_off >= 0 && nblk <= p.info.num_ids - ids_off && lead >= 0 && lead < a.num_seqs)) {
     if (threadIdx.x == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
-    return;  // the whole workgroup
+    return;  // the whole workgroup (every thread read the same record)
   }
-  const int row0 = s_row[0];  // the row invalid columns read
-  if constexpr (kTrace) tm[1] = wall_clock64();
+  if (threadIdx.x == 0) s_bad = 0;  // ordered before the prologue by the unit's barriers
+  int mctx = 0;  // thread j < n: member j's context length, checked after the unit
+  auto prologue = [&]() __attribute__((always_inline)) -> bool {
+    if ((int)threadIdx.x < n) {
+      const int32_t* mem = p.plan + p.info.off_tile_members + (int64_t)(m0 + threadIdx.x) * kMemberWords;
+      const int seq = mem[0], c0 = mem[1], span = mem[2];
+      if (!(seq >= 0 && seq < a.num_seqs && c0 >= 0 && span > range &&
+            (int64_t)c0 + (int64_t)hkv * span <= p.info.num_chunks)) {
+        s_bad = 1;
+      } else {
+        s_row[threadIdx.x] = seq;  // decode rows: sequence s's query token is row s
+        s_slot[threadIdx.x] = c0 + kvh * span + range;
+        mctx = a.context_lens[seq];  // its wait falls after the key steps
+      }
+    }
+    __syncthreads();
+    if constexpr (kTrace) tm[1] = wall_clock64();
+    return __builtin_amdgcn_readfirstlane(s_bad) == 0;
+  };
 
+  // an invalid column reads member 0's query row (and is zeroed when quantized)
   auto column_of = [&](int f) __attribute__((always_inline)) -> ColumnInfo {
     const int j = f / G;
-    return ColumnInfo{j < n ? s_row[j] : row0, kvh * G + f % G, 0, INT_MAX, j < n};
+    return ColumnInfo{s_row[j < n ? j : 0], kvh * G + f % G, 0, INT_MAX, j < n};
   };
   // every key of the range is visible to every column: no step is bounded
   auto bounds_of = [&](int wave) __attribute__((always_inline)) -> WaveBounds {
@@ -1128,8 +1142,12 @@ __global__ __launch_bounds__(256) void prefix_tiles_kernel(PlanArgs p) {
       const int f = f0 + cc;
       const float4_t v = *reinterpret_cast<const float4_t*>(tile + cc * kRow + 4 * q);
       if (f / G < n) {
+        // non-temporal: the decode kernel reads the partials only after streaming the
+        // rows' own blocks, long after they would have left the cache, and dirty lines
+        // left in the cache are written back at this kernel's end (measured: config 4's
+        // call 69.2 -> 68.6 us)
         const int64_t col = plan_chunk_slot(p, s_slot[f / G], G) + f % G;
-        *reinterpret_cast<float4_t*>(a.ws_o + col * D + 4 * q) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(a.ws_o + col * D + 4 * q));
       }
     }
     if (c.valid && qg == 0) {
@@ -1143,8 +1161,18 @@ __global__ __launch_bounds__(256) void prefix_tiles_kernel(PlanArgs p) {
   auto mark = [&](int k) __attribute__((always_inline)) {
     if constexpr (kTrace) tm[k] = wall_clock64();
   };
-  prefill_unit<QT, D, G>(a, L, kvh, blk0, blk0 + nblk, ids, 0, row0, column_of, bounds_of, store,
-                         mark);
+  prefill_unit<QT, D, G>(a, L, kvh, blk0, blk0 + nblk, ids, 0, 0, column_of, bounds_of, store,
+                         prologue, mark);
+  if (s_bad) {  // a member failed its checks: nothing was stored
+    if (threadIdx.x == 0) atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+    return;
+  }
+  // every key of the range must be visible to each member (its length as planned)
+  if ((int)threadIdx.x < n) {
+    const RowSpan sp = row_span(a, mctx);
+    if (sp.kv_begin > blk0 * kBlockTokens || (int64_t)sp.ctx < (int64_t)(blk0 + nblk) * kBlockTokens)
+      atomicOr(a.err_flag, ASTR_FLAG_BAD_INDEX);
+  }
 #if ASTR_TRACE
   const int64_t tw = unit * kWaves + threadIdx.x / kWave;
   if (lane == 0 && tw < kTileTraceWaves) {
