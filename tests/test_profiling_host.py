@@ -1,4 +1,5 @@
-"""The rocprofv3 CSV readers of aster_amd.profiling, on hand-made counter files."""
+"""The rocprofv3 CSV readers and the tile-timeline report of aster_amd.profiling, on
+hand-made counter files and trace marks."""
 
 import csv
 import os
@@ -44,3 +45,25 @@ def test_traffic_scales_by_the_copy_calibration(tmp_path):
     assert rep["kernels"] == {"decode_streamk_kernel": (200 + 7) * 1024,
                               "merge_streamk_kernel": (6 + 1) * 1024}
     assert rep["bytes_per_launch"] == 214 * 1024
+
+
+def test_tile_timeline_report_from_marks():
+    np = pytest.importorskip("numpy")
+    # two tile units of four waves (marks in 100 MHz ticks, info: steps, XCC, kv head,
+    # range); unused trace slots stay zero and are dropped
+    marks = np.zeros((12, 8), np.int64)
+    info = np.zeros((12, 4), np.int32)
+    for w in range(8):
+        t0 = 1000 + 10 * w  # wave w starts 0.1 w us after the first
+        # checked +2 us, queries +1 us, first step +3 us, 7 later steps of 2 us, store 1 us
+        marks[w, :6] = [t0, t0 + 200, t0 + 300, t0 + 600, t0 + 2000, t0 + 2100]
+        info[w] = [8, w // 4, w // 4, 0]
+    rep = profiling._tiles_report(marks, info, decode_start=1000 + 70 + 2100 + 350)
+    assert rep["waves"] == 8 and rep["steps_per_unit"] == [8.0, 8.0, 8.0]
+    assert rep["start_us"] == [0.0, 0.35, 0.7]
+    assert rep["checked_us"] == [2.0, 2.0] and rep["queries_us"] == [1.0, 1.0]
+    assert rep["first_step_us"] == [3.0, 3.0] and rep["later_step_us"] == 2.0
+    assert rep["store_us"] == [1.0, 1.0]
+    assert rep["exit_pct_50_90_100_us"][2] == 21.7
+    assert rep["per_xcc_max_exit"] == {0: 21.3, 1: 21.7}
+    assert rep["decode_first_wave_after_last_tile_us"] == 3.5
