@@ -11,8 +11,10 @@
 //     range per wave. Pieces of an item that two or more of the workgroup's waves hold
 //     are merged in that workgroup after its waves finish; chunks of an item that two
 //     or more workgroups hold are merged by the chunk-merge kernel.
-// The cost model is the stream-K kernel's: 50 per block and 135 per row start (a
-// row's query load and the partial it writes when it ends).
+// The cost model: 50 per block and 200 per row start (a row's query load, the partial
+// it writes when it ends and, in a step that appends, its newest token; measured on the
+// planned kernel, config 2 and config 4 steps ran 0.5 and 0.9 us faster at 200 than at
+// the stream-K kernel's 135, with the attention-only calls unchanged, and 260 slower).
 //
 // Shared prefixes (tile_rows >= 2): sequences whose block tables begin with the same
 // blocks, every key of them visible to each, are read together by the prefix-tile
@@ -64,7 +66,7 @@ int fail(int code, const char* fmt, ...);
 namespace plan {
 
 constexpr int kBlockTokens = 16;
-constexpr int64_t kBlockCost = 50, kRowCost = 135;
+constexpr int64_t kBlockCost = 50, kRowCost = 200;
 constexpr int kItemWords = 8, kChunkedWords = 4, kTileWords = 8, kMemberWords = 3;
 constexpr int kWaveWords = 6;
 // first blocks a wave issues from its entry (of the entry's 3 id slots): two measured

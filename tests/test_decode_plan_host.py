@@ -15,7 +15,7 @@ from aster_amd import _native
 from aster_amd.decode_plan import DecodePlanInfo
 
 I32P = ctypes.POINTER(ctypes.c_int32)
-BLOCK_COST, ROW_COST = 50, 135
+BLOCK_COST, ROW_COST = 50, 200  # the planner's cost model (decode_plan.cpp)
 
 
 def _plan(tables, lens, hkv, window, wg, nw=8, tile_rows=0, tile_ranges=0, min_shared=8):
