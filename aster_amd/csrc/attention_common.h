@@ -568,6 +568,19 @@ __device__ __forceinline__ void stage_query(const AttnArgs& a, int tok, int kvh,
   }
 }
 
+// Query row g of a stage_query buffer as the lane's column (the QueryColumn layout
+// load_query_column gives; any query type).
+template <typename QT, int D>
+__device__ __forceinline__ void lds_query_column(const char* buf, int g, int qg,
+                                                 QueryColumn<QT, D>& q) {
+  const char* row = buf + (g * D + 16 * qg) * (int)sizeof(QT);
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int c = 0; c < (int)(16 * sizeof(QT) / 16); ++c)
+      q.w[h][c] = *reinterpret_cast<const uint4*>(row + 64 * h * (int)sizeof(QT) + 16 * c);
+}
+
 // Query row g of a stage_query buffer in the QueryRaw lane layout.
 template <typename QT, int D>
 __device__ __forceinline__ void lds_query(const char* buf, int g, int qg, QueryRaw<D>& q) {

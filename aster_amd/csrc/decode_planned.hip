@@ -296,6 +296,8 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
   constexpr int NPV = D / 16;
   constexpr bool kFirstInRegs = first_in_registers<D>();
   constexpr bool kLastInRing = last_in_ring<D>();
+  // the G query rows of a piece travel by direct-to-LDS load into a ring stage
+  constexpr bool kStagedQuery = G * D * (int)sizeof(QT) <= S::kBytes;
   const AttnArgs& a = p.a;
 
   // the block ring; once every wave is done streaming, the workgroup's partials
@@ -358,22 +360,20 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
     pre_ok = pre_ok && (j >= pre || (unsigned)pid[j] < (unsigned)a.cache.num_blocks);
   const bool bad_entry = pre != 0 && !pre_ok;  // raised with the wave's index flag below
   // the wave starts after its items without a (valid) entry; it issues at most NS - 1
-  // blocks here (the last stage takes the query). fp32 queries (registers) start after
-  // the items: measured faster (their query loads would wait behind the blocks).
-  pre = pre_ok && sizeof(QT) == 2 ? min(pre, NS - 1) : 0;
+  // blocks here (the last stage takes the query). Queries whose G rows do not fit a stage
+  // (fp32 at G D > 1024 for D = 128) load into registers and start after the items: their
+  // register loads would wait behind the blocks (measured slower).
+  pre = pre_ok && kStagedQuery ? min(pre, NS - 1) : 0;
   QueryColumn<QT, D> qr;
   if (pre > 0) {
-    if constexpr (sizeof(QT) == 2) {
+    if constexpr (kStagedQuery)
       stage_query<QT, D, G>(a, pseq, pkvh, lane, lds + ((NS - 1) * NW + wave) * S::kBytes);
-    } else {
-      load_query_column<QT, D>(query_col_ptr<QT>(a, pseq, pkvh * G + (valid ? r : 0), qg), qr);
-    }
 #pragma unroll
     for (int j = 0; j < kPrefetchBlocks; ++j)
       if (j < pre) stage_block<D>(a, pid[j], pkvh, lane, lds + (j * NW + wave) * S::kBytes);
   }
   if (wave == 0) {  // the record and items have landed (the loads issued after them may not)
-    constexpr int QL = sizeof(QT) == 2 ? stage_query_loads<QT, D, G>() : 0;
+    constexpr int QL = kStagedQuery ? stage_query_loads<QT, D, G>() : 0;
     if (pre == 3) wait_vmcnt<QL + 3 * S::kLoads>();
     else if (pre == 2) wait_vmcnt<QL + 2 * S::kLoads>();
     else if (pre == 1) wait_vmcnt<QL + S::kLoads>();
@@ -520,14 +520,14 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
 
   // The first item's query rows go by direct-to-LDS loads into the last stage, issued
   // before blocks 0 .. NS-2, so the block stream starts without waiting for them (at
-  // the top, with the blocks of the wave's entry, when it has one). fp32 queries (int8
-  // codes) load into registers before the first blocks are issued.
+  // the top, with the blocks of the wave's entry, when it has one). Queries whose rows
+  // do not fit a stage load into registers before the first blocks are issued.
   QkOperand<D, KF> qop;
   float cf = 0.f;
   if (nblk > 0) {
     const Item it0 = item_at(s_item, __builtin_amdgcn_readfirstlane(rows));
     if (pre == 0) check_ids(it0);
-    if constexpr (sizeof(QT) == 2) {
+    if constexpr (kStagedQuery) {
       if (pre == 0 && nblk > 0) stage_query<QT, D, G>(a, it0.seq, it0.kvh, lane, stage(NS - 1));
       const int first = min(NS - 1, nblk);
       if (pre > 0 && pre < first) check_ids(it0);
@@ -538,7 +538,7 @@ __global__ __launch_bounds__(kPlanWaves * kWave) void decode_planned_kernel(Plan
       else if (first == 2) wait_vmcnt<2 * S::kLoads>();
       else if (first == 1) wait_vmcnt<S::kLoads>();
       else wait_vmcnt<0>();
-      lds_query<QT, D>(stage(NS - 1), r < G ? r : 0, qg, reinterpret_cast<QueryRaw<D>&>(qr));
+      lds_query_column<QT, D>(stage(NS - 1), r < G ? r : 0, qg, qr);
       cf = qk_operand_column<QT, D, KF>(qr, valid, a.qk_scale_log2, qop);
       if (pre > 0 && pre >= first) check_ids(it0);
       if (NS - 1 < nblk) issue(NS - 1);  // after the query reads above (values consumed)
