@@ -1,4 +1,5 @@
-"""INTEGRATION.md's snippets name only symbols this repository has: every
+"""The integration guide at the repository root (the reference-side bindings a
+maintainer adds) names only symbols this repository has in its code snippets: every
 ``aster_amd`` import resolves, every name the reference-side stub module re-exports
 (``aster.optimization.hip_int8_paged``) is one of that stub's imports, the calls the
 snippets make pass keyword arguments the functions accept, and every C entry point
